@@ -1,0 +1,334 @@
+#!/usr/bin/env python3
+"""Benchmark of ferrograd's fused training path on one MI355X.
+
+Headline ("c5"): one full training step of the
+8-layer MLP -- batch 2048, fp32, 1024 -> 4096 x7 -> 1000, GELU (tanh) after
+layers 1-7, softmax cross-entropy, Adam (lr 1e-3) -- with inputs and
+parameters resident in HBM.  value = training steps per second.
+
+Also measured in the same run (HIP events on the stream the kernels run on):
+  * the dominant kernel of the step, the hidden-layer forward GEMM
+    (2048 x 4096 x 4096, bias + GELU epilogue) -> roofline vs fp32 MFMA peak;
+  * c2: 4096^3 GEMM forward (bias + ReLU) and its dA / dB backward;
+  * c3: fused softmax + CE forward/backward over [8192, 32000];
+  * c4: multi-tensor Adam over 64 x 4 Mi parameters;
+and the CPU restatement (oracle/) timed on the host cores on a bounded
+sample of the same workload (one full c5 step on the same inputs), which
+also gives a parity check of the step's loss and gradients.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "MLP train steps/sec on 1 MI355X; GEMM TFLOP/s; softmax/Adam HBM GB/s"
+PEAK_FP32_MFMA_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def event_time_ms(fn, reps: int) -> float:
+    """Average duration of fn() over reps launches, timed with HIP events on
+    torch's current stream (the stream the library context enqueues on)."""
+    import torch
+
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    fn()
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(reps):
+        fn()
+    stop.record()
+    stop.synchronize()
+    return start.elapsed_time(stop) / reps
+
+
+def init_c5(trainer, ctx) -> None:
+    """Config c5 data: X ~ N(0,1), labels U{0..999}, W Kaiming-uniform
+    U(-sqrt(6/fan_in), +sqrt(6/fan_in)), b = 0; seed 4 (device generator)."""
+    seed = 4
+    B = trainer.B
+    ctx.rng_normal(seed, 0, 0.0, 1.0, trainer.X, trainer.X.numel())
+    ctx.rng_int(seed, 1, trainer.dims[-1], trainer.labels, B)
+    for l, w in enumerate(trainer.W):
+        bound = math.sqrt(6.0 / trainer.dims[l])
+        ctx.rng_uniform(seed, 10 + l, -bound, bound, w, w.numel())
+    for b in trainer.b:
+        b.zero_()
+
+
+def gemm_components(ctx, reps: int):
+    """c2 (4096^3) forward + dA + dB, and the c5 hidden-layer forward GEMM."""
+    import torch
+
+    import ferrograd_amd as fa
+
+    out = {}
+    n = 4096
+    g = torch.Generator(device="cuda").manual_seed(1)
+    A = torch.randn((n, n), device="cuda", generator=g)
+    Bm = torch.randn((n, n), device="cuda", generator=g)
+    bias = 0.1 * torch.randn((n,), device="cuda", generator=g)
+    dC = torch.randn((n, n), device="cuda", generator=g)
+    C, Z, dA, dB = (torch.empty((n, n), device="cuda") for _ in range(4))
+    flops = 2.0 * n * n * n
+    t_f = event_time_ms(lambda: ctx.gemm(fa.NN, n, n, n, A, n, Bm, n, C, n, bias=bias,
+                                         act=fa.ACT_RELU, Z=Z, ldz=n), reps)
+    t_a = event_time_ms(lambda: ctx.gemm_bwd(fa.NT, n, n, n, dC, n, Bm, n, dA, n,
+                                             act=fa.ACT_RELU, Zs=Z, ldzs=n), reps)
+    t_b = event_time_ms(lambda: ctx.gemm(fa.TN, n, n, n, A, n, dC, n, dB, n), reps)
+    out["c2_gemm_4096"] = {
+        "fwd_ms": t_f, "dA_ms": t_a, "dB_ms": t_b,
+        "fwd_tflops": flops / t_f / 1e9, "dA_tflops": flops / t_a / 1e9,
+        "dB_tflops": flops / t_b / 1e9,
+        "fwd_bwd_tflops": 3 * flops / (t_f + t_a + t_b) / 1e9,
+    }
+    del A, Bm, bias, dC, C, Z, dA, dB
+    # c5 hidden layer forward: [2048,4096] x [4096,4096] + bias, GELU.
+    M, N, K = 2048, 4096, 4096
+    X = torch.randn((M, K), device="cuda", generator=g)
+    W = torch.randn((K, N), device="cuda", generator=g)
+    b = torch.randn((N,), device="cuda", generator=g)
+    H, Zh = torch.empty((M, N), device="cuda"), torch.empty((M, N), device="cuda")
+    t = event_time_ms(lambda: ctx.gemm(fa.NN, M, N, K, X, K, W, N, H, N, bias=b,
+                                       act=fa.ACT_GELU, Z=Zh, ldz=N), reps)
+    out["c5_hidden_fwd_gemm"] = {"ms": t, "flops_per_launch": 2 * M * N * K,
+                                 "tflops": 2.0 * M * N * K / t / 1e9}
+    return out
+
+
+def softmax_component(ctx, reps: int):
+    import torch
+
+    R, C = 8192, 32000
+    x = torch.empty((R, C), device="cuda")
+    lab = torch.empty((R,), device="cuda", dtype=torch.int32)
+    ctx.rng_normal(2, 0, 0.0, 2.0, x, R * C)
+    ctx.rng_int(2, 1, C, lab, R)
+    d = torch.empty_like(x)
+    loss, mean = torch.empty(R, device="cuda"), torch.empty(1, device="cuda")
+    am = torch.empty(R, device="cuda", dtype=torch.int32)
+    t = event_time_ms(lambda: ctx.softmax_ce(x, C, lab, R, C, 1.0, row_loss=loss,
+                                             mean_loss=mean, dlogits=d, ldd=C, argmax=am), reps)
+    nbytes = 2 * R * C * 4 + R * 4 * 3  # logits in, dlogits out, labels/loss/argmax
+    return {"c3_softmax_ce_8192x32000": {"ms": t, "bytes": nbytes, "gbs": nbytes / t / 1e6,
+                                         "frac_hbm": nbytes / t / 1e6 / PEAK_HBM_GBS}}
+
+
+def adam_component(ctx, reps: int):
+    import torch
+
+    import ferrograd_amd as fa
+
+    nt, n = 64, 4 * 1024 * 1024
+    P = [torch.empty(n, device="cuda") for _ in range(nt)]
+    G = [torch.empty(n, device="cuda") for _ in range(nt)]
+    M = [torch.zeros(n, device="cuda") for _ in range(nt)]
+    V = [torch.zeros(n, device="cuda") for _ in range(nt)]
+    for i in range(nt):
+        ctx.rng_normal(3, i, 0.0, 0.02, P[i], n)
+        ctx.rng_normal(3, 1000 + i, 0.0, 1e-3, G[i], n)
+    mt = fa.MultiTensor(ctx, P, G, M, V)
+    step = [0]
+
+    def one():
+        step[0] += 1
+        mt.adam(1e-3, 0.9, 0.999, 1e-8, step[0])
+
+    t = event_time_ms(one, reps)
+    mt.close()
+    nbytes = 28 * nt * n
+    return {"c4_adam_64x4Mi": {"ms": t, "bytes": nbytes, "gbs": nbytes / t / 1e6,
+                               "frac_hbm": nbytes / t / 1e6 / PEAK_HBM_GBS}}
+
+
+def cpu_baseline_c5(host, dims, batch, threads):
+    """One full c5 training step (forward, CE, backward incl. dX, Adam) with
+    the CPU restatement, on the same initial inputs as the GPU run."""
+    import numpy as np
+
+    import oracle as O
+
+    O.set_num_threads(threads)
+    X, y, W = host["X"], host["y"], host["W"]
+    L = len(W)
+    b = [np.zeros(dims[l + 1], np.float32) for l in range(L)]
+    t0 = time.perf_counter()
+    Zs, Hs = [], []
+    inp = X
+    for l in range(L):
+        last = l == L - 1
+        Z, H = O.bias_act(O.gemm(O.NN, inp, W[l]), b[l], O.ACT_NONE if last else O.ACT_GELU)
+        Zs.append(Z)
+        Hs.append(H)
+        inp = H
+    row_loss, dZ, _, mean = O.softmax_ce(Zs[-1], y)
+    dW, db = [None] * L, [None] * L
+    for l in range(L - 1, -1, -1):
+        prev = Hs[l - 1] if l > 0 else X
+        dW[l] = O.gemm(O.TN, prev, dZ)
+        db[l] = O.bias_grad(dZ)
+        up = O.gemm(O.NT, dZ, W[l])
+        dZ = O.act_bwd(O.ACT_GELU, up, Zs[l - 1]) if l > 0 else up
+    s, r = O.adam_scalars(np.float32(1e-3), np.float32(0.9), np.float32(0.999), 1)
+    Wn = []
+    for l in range(L):
+        for p, g in ((W[l].copy(), dW[l]), (b[l].copy(), db[l])):
+            m, v = np.zeros_like(p), np.zeros_like(p)
+            O.adam_(p, g, m, v, np.float32(0.9), np.float32(0.999), np.float32(1e-8), s, r)
+            Wn.append(p)
+    dt = time.perf_counter() - t0
+    return dt, {"mean_loss": mean, "dW": dW, "db": db, "params": Wn}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-components", action="store_true",
+                    help="skip the c2/c3/c4 component measurements")
+    ap.add_argument("--reps", type=int, default=20, help="launches per kernel timing")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one MI355X only: this build has no multi-GPU path "
+              f"(--gpus {args.gpus} requested).", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    import ferrograd_amd as fa
+    from ferrograd_amd.mlp import MLPTrainStep
+
+    torch.cuda.init()
+    ctx = fa.Context(0, torch.cuda.current_stream().cuda_stream)
+    log(f"device {ctx.arch}, {ctx.cu_count} CUs")
+    dims = [1024] + [4096] * 7 + [1000]
+    batch = 2048
+    tr = MLPTrainStep(ctx, dims, batch, fa.ACT_GELU, optim="adam", lr=1e-3, data_grad=True)
+    init_c5(tr, ctx)
+    torch.cuda.synchronize()
+    host = None
+    if not args.no_cpu:
+        host = {"X": tr.X.cpu().numpy(), "y": tr.labels.cpu().numpy().view(np.uint32),
+                "W": [w.cpu().numpy() for w in tr.W]}
+    # First step (from the initial state) doubles as the parity sample.
+    tr.step()
+    torch.cuda.synchronize()
+    first = {"mean_loss": float(tr.loss.cpu()[0]), "dW": [w.cpu().numpy() for w in tr.dW],
+             "db": [b.cpu().numpy() for b in tr.db], "W": [w.cpu().numpy() for w in tr.W]}
+    for _ in range(max(0, args.warmup - 1)):
+        tr.step()
+    torch.cuda.synchronize()
+    log(f"warmup done ({args.warmup} steps); timing {args.steps} steps")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        tr.step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = 1000.0 * elapsed / args.steps
+    steps_per_s = args.steps / elapsed
+    log(f"c5 step: {ms_per_step:.3f} ms ({steps_per_s:.2f} steps/s)")
+
+    # Per-phase breakdown (events).
+    phases = {
+        "forward_ms": event_time_ms(tr.forward, 5),
+        "loss_ms": event_time_ms(tr.loss_and_grad, 5),
+        "backward_ms": event_time_ms(tr.backward, 5),
+    }
+    step_flops = tr.gemm_flops()
+
+    comps = gemm_components(ctx, args.reps)
+    hid = comps["c5_hidden_fwd_gemm"]
+    roofline = {
+        "bound": "mfma",
+        "kernel": "gemm_f32_mfma NN 2048x4096x4096 + bias + GELU (c5 hidden-layer forward)",
+        "achieved": hid["tflops"],
+        "peak": PEAK_FP32_MFMA_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": hid["tflops"] / PEAK_FP32_MFMA_TFLOPS,
+        "traffic": None,
+    }
+    if not args.no_components:
+        comps.update(softmax_component(ctx, args.reps))
+        comps.update(adam_component(ctx, 10))
+    log("components: " + json.dumps(comps))
+
+    cpu = None
+    parity = None
+    if host is not None:
+        threads = min(16, os.cpu_count() or 1)
+        log(f"CPU baseline: one c5 step on {threads} threads")
+        dt, ref = cpu_baseline_c5(host, dims, batch, threads)
+        cpu = {"value": 1.0 / dt, "unit": "steps/s", "cores": threads, "kind": "port",
+               "sample": "one full c5 training step (forward, CE, backward incl. dX, Adam) "
+                         "on the same inputs, oracle/ C restatement with OpenMP"}
+
+        def rel(a, b):
+            b = np.asarray(b, np.float64)
+            return float(np.max(np.abs(np.asarray(a, np.float64) - b)) /
+                         max(float(np.max(np.abs(b))), 1e-30))
+
+        parity = {
+            "loss_rel": abs(first["mean_loss"] - ref["mean_loss"]) / max(1.0, abs(ref["mean_loss"])),
+            "dW_max_rel": max(rel(a, b) for a, b in zip(first["dW"], ref["dW"])),
+            "db_max_rel": max(rel(a, b) for a, b in zip(first["db"], ref["db"])),
+            "W_after_adam_max_rel": max(rel(a, b) for a, b in zip(first["W"], ref["params"][0::2])),
+            "tolerance_gemm": 1e-5 * math.sqrt(4096),
+        }
+        log("parity vs CPU: " + json.dumps(parity))
+
+    result = {
+        "metric": METRIC,
+        "value": steps_per_s,
+        "unit": "steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (counter-based SplitMix64 generator, seed 4; random-init weights)",
+        "config": {
+            "workload": "c5: 8-layer MLP training step, batch 2048, 1024->4096x7->1000, "
+                        "GELU-tanh, softmax-CE, Adam lr 1e-3 (dX of the data input computed, "
+                        "as ferrograd trains every Input)",
+            "global_batch": batch,
+            "dims": dims,
+            "parallelism": "single GPU",
+            "gemm_flops_per_step": step_flops,
+            "params": tr.num_params(),
+        },
+        "step_effective_tflops": step_flops / (ms_per_step * 1e-3) / 1e12,
+        "phases_ms": phases,
+        "roofline": roofline,
+        "components": comps,
+        "cpu_baseline": cpu,
+        "parity": parity,
+    }
+    tr.close()
+    ctx.close()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

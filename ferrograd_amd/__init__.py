@@ -1,0 +1,197 @@
+"""ferrograd_amd -- MI355X (gfx950) backend for ferrograd's fused training path.
+
+The product is the C-ABI library ``libferrograd_hip.so`` (declared in
+``include/ferrograd_hip.h``): hand-written HIP kernels for gfx950 and the C++
+host runtime around them.  This package is the thin Python face of that ABI:
+
+* ``Context`` / direct-kernel helpers below take device pointers (``int``) or
+  any object with ``data_ptr()`` (e.g. a torch tensor used purely as device
+  memory);
+* ``graph`` mirrors ferrograd's Graph / GpuContext API (build, lower,
+  schedule, dispatch_forward / loss / backward / optim) on top of the
+  library's planner.
+
+Nothing here computes on the CPU: every call goes to the library, and the
+import fails loudly when the library has not been built.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Sequence
+
+import numpy as np
+
+from . import _lib
+from ._lib import FgError, call, load
+
+NN, NT, TN = 0, 1, 2
+ACT_NONE, ACT_RELU, ACT_GELU = 0, 1, 2
+
+__all__ = [
+    "NN", "NT", "TN", "ACT_NONE", "ACT_RELU", "ACT_GELU", "FgError", "Context",
+    "MultiTensor", "load", "rng_uniform", "rng_normal", "rng_int",
+]
+
+
+def _ptr(x) -> Optional[int]:
+    """Device address of x: None, an int address, or an object with data_ptr()."""
+    if x is None:
+        return None
+    if isinstance(x, int):
+        return x
+    return int(x.data_ptr())
+
+
+class Context:
+    """An fg_ctx bound to ``device`` and a HIP stream.
+
+    ``stream`` is a raw hipStream_t address (e.g. ``torch.cuda.current_stream()
+    .cuda_stream``) or None for a private stream."""
+
+    def __init__(self, device: int = 0, stream: Optional[int] = None):
+        h = ctypes.c_void_p()
+        call("fg_ctx_create", device, stream, ctypes.byref(h))
+        self.handle = h
+        arch = ctypes.create_string_buffer(64)
+        flags = ctypes.c_uint32()
+        cus = ctypes.c_int()
+        call("fg_ctx_target", h, arch, 64, ctypes.byref(flags), ctypes.byref(cus))
+        self.arch = arch.value.decode()
+        self.flags = flags.value
+        self.cu_count = cus.value
+
+    @property
+    def stream(self) -> int:
+        s = ctypes.c_void_p()
+        call("fg_ctx_stream", self.handle, ctypes.byref(s))
+        return int(s.value or 0)
+
+    def sync(self) -> None:
+        call("fg_sync", self.handle)
+
+    def is_ready(self) -> bool:
+        r = ctypes.c_int()
+        call("fg_is_ready", self.handle, ctypes.byref(r))
+        return bool(r.value)
+
+    def reserve_workspace(self, nbytes: int) -> None:
+        call("fg_ctx_reserve_workspace", self.handle, nbytes)
+
+    def close(self) -> None:
+        if self.handle:
+            call("fg_ctx_destroy", self.handle)
+            self.handle = None
+
+    def __del__(self):  # pragma: no cover - best effort
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ------------------------------------------------------ direct kernels
+    def gemm(self, layout: int, M: int, N: int, K: int, A, lda: int, B, ldb: int, C, ldc: int,
+             bias=None, act: int = ACT_NONE, Z=None, ldz: int = 0,
+             accumulate: bool = False) -> None:
+        call("fg_gemm_f32", self.handle, layout, M, N, K, _ptr(A), lda, _ptr(B), ldb, _ptr(bias),
+             act, _ptr(C), ldc, _ptr(Z), ldz, int(accumulate))
+
+    def gemm_bwd(self, layout: int, M: int, N: int, K: int, A, lda: int, B, ldb: int, C,
+                 ldc: int, act: int = ACT_NONE, Zs=None, ldzs: int = 0,
+                 accumulate: bool = False) -> None:
+        call("fg_gemm_bwd_f32", self.handle, layout, M, N, K, _ptr(A), lda, _ptr(B), ldb, act,
+             _ptr(Zs), ldzs, _ptr(C), ldc, int(accumulate))
+
+    def bias_grad(self, M: int, N: int, dZ, ld: int, dbias, accumulate: bool = False) -> None:
+        call("fg_bias_grad_f32", self.handle, M, N, _ptr(dZ), ld, _ptr(dbias), int(accumulate))
+
+    def act_bwd(self, act: int, n: int, dH, Z, dZ) -> None:
+        call("fg_act_bwd_f32", self.handle, act, n, _ptr(dH), _ptr(Z), _ptr(dZ))
+
+    def softmax_ce(self, logits, ldx: int, labels, R: int, C: int, grad_scale: float = 1.0,
+                   row_loss=None, mean_loss=None, dlogits=None, ldd: int = 0,
+                   argmax=None) -> None:
+        call("fg_softmax_ce_f32", self.handle, _ptr(logits), ldx, _ptr(labels), R, C,
+             grad_scale, _ptr(row_loss), _ptr(mean_loss), _ptr(dlogits), ldd or C, _ptr(argmax))
+
+    def softmax(self, x, R: int, C: int, y) -> None:
+        call("fg_softmax_f32", self.handle, _ptr(x), R, C, _ptr(y))
+
+    def softmax_bwd(self, y, dy, R: int, C: int, dx, accumulate: bool = False) -> None:
+        call("fg_softmax_bwd_f32", self.handle, _ptr(y), _ptr(dy), R, C, _ptr(dx),
+             int(accumulate))
+
+    def fill_u32(self, dst, value: int, count: int) -> None:
+        call("fg_fill_u32", self.handle, _ptr(dst), value, count)
+
+    def rng_uniform(self, seed, tensor_id, lo, hi, dst, n) -> None:
+        call("fg_rng_uniform_dev", self.handle, seed, tensor_id, lo, hi, _ptr(dst), n)
+
+    def rng_normal(self, seed, tensor_id, mean, std, dst, n) -> None:
+        call("fg_rng_normal_dev", self.handle, seed, tensor_id, mean, std, _ptr(dst), n)
+
+    def rng_int(self, seed, tensor_id, bound, dst, n) -> None:
+        call("fg_rng_int_dev", self.handle, seed, tensor_id, bound, _ptr(dst), n)
+
+
+class MultiTensor:
+    """A device-resident tensor list for the one-launch SGD / Adam updates."""
+
+    def __init__(self, ctx: Context, params: Sequence, grads: Sequence,
+                 m: Optional[Sequence] = None, v: Optional[Sequence] = None,
+                 sizes: Optional[Sequence[int]] = None):
+        n = len(params)
+        if sizes is None:
+            sizes = [int(p.numel()) for p in params]
+        arr = ctypes.c_void_p * n
+        P = arr(*[_ptr(p) for p in params])
+        G = arr(*[_ptr(g) for g in grads])
+        Mv = arr(*[_ptr(x) for x in m]) if m is not None else None
+        Vv = arr(*[_ptr(x) for x in v]) if v is not None else None
+        S = (ctypes.c_uint64 * n)(*sizes)
+        h = ctypes.c_void_p()
+        call("fg_mt_create", ctx.handle, n, P, G, Mv, Vv, S, ctypes.byref(h))
+        self.ctx = ctx
+        self.handle = h
+
+    def sgd(self, lr: float, zero_grad: bool = True) -> None:
+        call("fg_sgd_step", self.ctx.handle, self.handle, lr, int(zero_grad))
+
+    def adam(self, lr: float, b1: float, b2: float, eps: float, step: int,
+             zero_grad: bool = False) -> None:
+        call("fg_adam_step", self.ctx.handle, self.handle, lr, b1, b2, eps, step, int(zero_grad))
+
+    def adam_scalars(self, b1: float, b2: float, eps: float, step_size: float,
+                     inv_sqrt_bc2: float, zero_grad: bool = False) -> None:
+        call("fg_adam_step_scalars", self.ctx.handle, self.handle, b1, b2, eps, step_size,
+             inv_sqrt_bc2, int(zero_grad))
+
+    def close(self) -> None:
+        if self.handle:
+            call("fg_mt_destroy", self.handle)
+            self.handle = None
+
+    def __del__(self):  # pragma: no cover - best effort
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ------------------------------------------------------------ synthetic data
+def rng_uniform(seed: int, tensor_id: int, shape, lo: float = 0.0, hi: float = 1.0) -> np.ndarray:
+    out = np.empty(shape, dtype=np.float32)
+    call("fg_rng_uniform_host", seed, tensor_id, lo, hi, out.ctypes.data, out.size)
+    return out
+
+
+def rng_normal(seed: int, tensor_id: int, shape, mean: float = 0.0,
+               std: float = 1.0) -> np.ndarray:
+    out = np.empty(shape, dtype=np.float32)
+    call("fg_rng_normal_host", seed, tensor_id, mean, std, out.ctypes.data, out.size)
+    return out
+
+
+def rng_int(seed: int, tensor_id: int, shape, bound: int) -> np.ndarray:
+    out = np.empty(shape, dtype=np.uint32)
+    call("fg_rng_int_host", seed, tensor_id, bound, out.ctypes.data, out.size)
+    return out

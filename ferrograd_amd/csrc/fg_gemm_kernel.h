@@ -1,0 +1,349 @@
+// fg_gemm_kernel.h -- fp32 GEMM on CDNA4 matrix cores
+// (v_mfma_f32_32x32x2_f32) with fused epilogues.  Included by the
+// per-layout instantiation units k_gemm_{nn,nt,tn}.hip.
+//
+// Replaces the reference's matmul kernels: a 16x16 LDS tile per 256-thread
+// block with one scalar fmaf per LDS pair (crates/ferrograd-nn/src/op/matmul/
+// generic.rs:98-319), forward plus the dA / dB backward forms
+// (op/matmul/mod.rs:75-125), and the elementwise producers/consumers the
+// lowering inlines around them (kernel/forward.rs:298-464).
+//
+// Design (gfx950, 256 CUs, 64-wide waves, 160 KiB LDS per CU):
+//  * 256 threads = 4 waves per workgroup; each wave owns a (TM*32)x(TN*32)
+//    block of C held in TM*TN 16-register MFMA accumulators (up to 256
+//    registers, which the compiler places in AGPRs).
+//  * K is consumed in BK=16 tiles staged through LDS, double-buffered: the
+//    global loads of tile t+1 are issued before the MFMAs of tile t and
+//    written to the other LDS buffer afterwards -- one barrier per tile.
+//  * No operand is transposed on its way to LDS.  A k-contiguous operand is
+//    kept [row][k] (row stride BK+4 floats, conflict-free 16-byte reads) and
+//    a row-contiguous one [k][row] (stride rows+4).  The MFMA's k index is
+//    permuted consistently for both operands so that a lane of a
+//    k-contiguous operand reads 4 consecutive k with one ds_read_b128: in a
+//    16-k tile, lane half h (lanes 32h..32h+31) feeds k = 8h + 4q + s to the
+//    s-th MFMA of quad q.  Summation order inside the MFMA is hardware
+//    defined; results match the CPU restatement within the 1e-5*sqrt(K)
+//    tolerance, not bit for bit.
+//  * The epilogue stages each wave's accumulators through LDS one 32-row
+//    slice at a time and applies bias / activation / activation-derivative
+//    on float4 groups, so global stores (and the reads of bias, Z) are
+//    16-byte and coalesced.
+//  * Workgroup ids are remapped so that the 8 XCDs (each with its own L2)
+//    get contiguous groups of output tiles.
+//  * Edge tiles are zero-filled on load and masked on store, so any M, N, K
+//    work (the reference requires multiples of 16; N = 10 and N = 1000 of
+//    the target configurations are not).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "fg_act.h"
+
+namespace fg {
+namespace gemm {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kThreads = 256;
+
+struct GemmArgs {
+    const float *A;
+    const float *B;
+    float *C;
+    float *Z;           // forward: pre-activation output (optional)
+    const float *bias;  // forward: row-broadcast bias (optional)
+    const float *Zs;    // backward: saved pre-activation for act'(.)
+    int M, N, K;
+    int lda, ldb, ldc, ldz, ldzs;
+    int act;
+    int mode;  // 0 forward epilogue, 1 backward (act-derivative) epilogue
+    int accumulate;
+    int tiles_m, tiles_n;
+    int vec_out;  // C (and Z / Zs) rows 16-byte aligned: float4 epilogue I/O
+};
+
+// LDS footprint in floats.
+template <int BM, int BN, int BK, bool AK, bool BNC, int WTN>
+struct Lds {
+    static constexpr int a_ld = AK ? (BK + 4) : (BM + 4);
+    static constexpr int a_sz = AK ? BM * a_ld : BK * a_ld;
+    static constexpr int b_ld = BNC ? (BN + 4) : (BK + 4);
+    static constexpr int b_sz = BNC ? BK * b_ld : BN * b_ld;
+    static constexpr int buf = a_sz + b_sz;
+    static constexpr int stage_ld = WTN + 4;
+    static constexpr int stage = 4 * 32 * stage_ld;
+    static constexpr int total = (2 * buf > stage) ? 2 * buf : stage;
+};
+
+// Loads one operand tile into registers.  Operand rows are M (for A) or N
+// (for B); "KC" = k-contiguous in global memory.
+template <int R, int BK, bool KC, bool VEC>
+struct TileLoader {
+    static constexpr int kElems = R * BK;
+    static constexpr int kPer = VEC ? kElems / 4 / kThreads : kElems / kThreads;
+    static_assert(kPer >= 1, "tile too small for the thread count");
+    static_assert((VEC ? kElems / 4 : kElems) % kThreads == 0, "tile not divisible");
+    f32x4 v4[VEC ? kPer : 1];
+    float v1[VEC ? 1 : kPer];
+
+    __device__ __forceinline__ void load(const float *__restrict__ base, int ld, int row0, int rmax,
+                                         int k0, int K) {
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) {
+            const int idx = threadIdx.x + q * kThreads;
+            if constexpr (VEC) {
+                int row, kk;
+                if constexpr (KC) {
+                    row = idx / (BK / 4);
+                    kk = (idx % (BK / 4)) * 4;
+                } else {
+                    kk = idx / (R / 4);
+                    row = (idx % (R / 4)) * 4;
+                }
+                const int gr = row0 + row, gk = k0 + kk;
+                const bool ok = (gr < rmax) && (gk < K);
+                const float *p = KC ? base + (size_t)gr * ld + gk : base + (size_t)gk * ld + gr;
+                v4[q] = ok ? *reinterpret_cast<const f32x4 *>(p) : f32x4{0.f, 0.f, 0.f, 0.f};
+            } else {
+                int row, kk;
+                if constexpr (KC) {
+                    row = idx / BK;
+                    kk = idx % BK;
+                } else {
+                    kk = idx / R;
+                    row = idx % R;
+                }
+                const int gr = row0 + row, gk = k0 + kk;
+                const bool ok = (gr < rmax) && (gk < K);
+                v1[q] = ok ? (KC ? base[(size_t)gr * ld + gk] : base[(size_t)gk * ld + gr]) : 0.0f;
+            }
+        }
+    }
+
+    __device__ __forceinline__ void store(float *lds) const {
+        constexpr int ld = KC ? (BK + 4) : (R + 4);
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) {
+            const int idx = threadIdx.x + q * kThreads;
+            if constexpr (VEC) {
+                if constexpr (KC) {
+                    const int row = idx / (BK / 4), kk = (idx % (BK / 4)) * 4;
+                    *reinterpret_cast<f32x4 *>(lds + row * ld + kk) = v4[q];
+                } else {
+                    const int kk = idx / (R / 4), row = (idx % (R / 4)) * 4;
+                    *reinterpret_cast<f32x4 *>(lds + kk * ld + row) = v4[q];
+                }
+            } else {
+                if constexpr (KC) {
+                    const int row = idx / BK, kk = idx % BK;
+                    lds[row * ld + kk] = v1[q];
+                } else {
+                    const int kk = idx / R, row = idx % R;
+                    lds[kk * ld + row] = v1[q];
+                }
+            }
+        }
+    }
+};
+
+// Map the linear workgroup id to an output tile.  Consecutive ids go to
+// different XCDs (round-robin dispatch), so first regroup ids per XCD, then
+// walk tiles in groups of kGroupM tile-rows, column by column, which keeps
+// the A row-panels and B column-panels a group touches small.
+__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int &tm, int &tn) {
+    const int nt = tiles_m * tiles_n;
+    if ((nt & 7) == 0) bid = (bid & 7) * (nt >> 3) + (bid >> 3);
+    constexpr int kGroupM = 4;
+    const int per_group = kGroupM * tiles_n;
+    const int g = bid / per_group;
+    const int first = g * kGroupM;
+    const int gsize = min(tiles_m - first, kGroupM);
+    const int in = bid - g * per_group;
+    tm = first + in % gsize;
+    tn = in / gsize;
+}
+
+// One output element of the epilogue.
+__device__ __forceinline__ float epi_value(const GemmArgs &p, float v, float bv, int row, int col,
+                                           float *zout) {
+    if (p.mode == 0) {
+        v += bv;
+        *zout = v;
+        return act_fwd(p.act, v);
+    }
+    if (p.act != kActNone) v *= act_grad(p.act, p.Zs[(size_t)row * p.ldzs + col]);
+    return v;
+}
+
+template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC, bool VEC>
+__global__ __launch_bounds__(kThreads) void gemm_f32_mfma(GemmArgs p) {
+    static_assert(WGM * WGN == 4, "4 waves per workgroup");
+    constexpr int WTM = BM / WGM, WTN = BN / WGN;
+    constexpr int TM = WTM / 32, TN = WTN / 32;
+    static_assert(TM >= 1 && TN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "wave tile");
+    static_assert(BK % 16 == 0, "BK must be a multiple of 16");
+    using L = Lds<BM, BN, BK, AK, BNC, WTN>;
+    __shared__ __attribute__((aligned(16))) float lds[L::total];
+
+    int tile_m, tile_n;
+    tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tile_m, tile_n);
+    const int m0 = tile_m * BM, n0 = tile_n * BN;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int l32 = lane & 31, h = lane >> 5;
+    const int wm0 = (wave / WGN) * WTM, wn0 = (wave % WGN) * WTN;
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    TileLoader<BM, BK, AK, VEC> la;
+    TileLoader<BN, BK, !BNC, VEC> lb;
+    const int nk = (p.K + BK - 1) / BK;
+
+    la.load(p.A, p.lda, m0, p.M, 0, p.K);
+    lb.load(p.B, p.ldb, n0, p.N, 0, p.K);
+    la.store(lds);
+    lb.store(lds + L::a_sz);
+    __syncthreads();
+
+    for (int kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        const bool more = kt + 1 < nk;
+        if (more) {
+            la.load(p.A, p.lda, m0, p.M, (kt + 1) * BK, p.K);
+            lb.load(p.B, p.ldb, n0, p.N, (kt + 1) * BK, p.K);
+        }
+        const float *As = lds + cur * L::buf;
+        const float *Bs = As + L::a_sz;
+#pragma unroll
+        for (int u = 0; u < BK / 16; ++u) {
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const int kb = u * 16 + 8 * h + 4 * q;
+                f32x4 a[TM], b[TN];
+#pragma unroll
+                for (int i = 0; i < TM; ++i) {
+                    const int row = wm0 + i * 32 + l32;
+                    if constexpr (AK) {
+                        a[i] = *reinterpret_cast<const f32x4 *>(As + row * L::a_ld + kb);
+                    } else {
+#pragma unroll
+                        for (int s = 0; s < 4; ++s) a[i][s] = As[(kb + s) * L::a_ld + row];
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    const int col = wn0 + j * 32 + l32;
+                    if constexpr (BNC) {
+#pragma unroll
+                        for (int s = 0; s < 4; ++s) b[j][s] = Bs[(kb + s) * L::b_ld + col];
+                    } else {
+                        b[j] = *reinterpret_cast<const f32x4 *>(Bs + col * L::b_ld + kb);
+                    }
+                }
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+#pragma unroll
+                    for (int i = 0; i < TM; ++i)
+#pragma unroll
+                        for (int j = 0; j < TN; ++j)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], b[j][s],
+                                                                             acc[i][j], 0, 0, 0);
+            }
+        }
+        if (more) {
+            float *nxt = lds + (cur ^ 1) * L::buf;
+            la.store(nxt);
+            lb.store(nxt + L::a_sz);
+        }
+        __syncthreads();
+    }
+
+    // Epilogue.  Accumulator register r of lane (h, l32) in block (i, j)
+    // holds C[wm0 + 32i + 8(r/4) + 4h + r%4][wn0 + 32j + l32].  Each wave
+    // writes one 32 x WTN slice to its LDS stage, then reads it back as
+    // float4 rows.
+    float *stage = lds + wave * (32 * L::stage_ld);
+    constexpr int F4 = WTN / 4;  // float4 per slice row
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                stage[((r >> 2) * 8 + h * 4 + (r & 3)) * L::stage_ld + j * 32 + l32] = acc[i][j][r];
+        __syncthreads();
+        for (int e = lane; e < 32 * F4; e += 64) {
+            const int rr = e / F4, c4 = (e % F4) * 4;
+            const int row = m0 + wm0 + i * 32 + rr;
+            const int col = n0 + wn0 + c4;
+            if (row >= p.M || col >= p.N) continue;
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(stage + rr * L::stage_ld + c4);
+            float *crow = p.C + (size_t)row * p.ldc;
+            if (p.vec_out && col + 4 <= p.N) {
+                f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+                if (p.mode == 0 && p.bias) bv = *reinterpret_cast<const f32x4 *>(p.bias + col);
+                f32x4 o, z;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    float zt;
+                    o[t] = epi_value(p, v[t], bv[t], row, col + t, &zt);
+                    z[t] = zt;
+                }
+                if (p.mode == 0 && p.Z)
+                    *reinterpret_cast<f32x4 *>(p.Z + (size_t)row * p.ldz + col) = z;
+                if (p.accumulate) o += *reinterpret_cast<const f32x4 *>(crow + col);
+                *reinterpret_cast<f32x4 *>(crow + col) = o;
+            } else {
+                for (int t = 0; t < 4 && col + t < p.N; ++t) {
+                    const float bv = (p.mode == 0 && p.bias) ? p.bias[col + t] : 0.0f;
+                    float z;
+                    float o = epi_value(p, v[t], bv, row, col + t, &z);
+                    if (p.mode == 0 && p.Z) p.Z[(size_t)row * p.ldz + col + t] = z;
+                    if (p.accumulate) o += crow[col + t];
+                    crow[col + t] = o;
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
+template <int BM, int BN, int WGM, int WGN, bool AK, bool BNC, bool VEC>
+void launch_one(const GemmArgs &a0, hipStream_t st) {
+    GemmArgs a = a0;
+    a.tiles_m = (a.M + BM - 1) / BM;
+    a.tiles_n = (a.N + BN - 1) / BN;
+    gemm_f32_mfma<BM, BN, 16, WGM, WGN, AK, BNC, VEC>
+        <<<a.tiles_m * a.tiles_n, kThreads, 0, st>>>(a);
+}
+
+// Tile configurations: 0: 256x256, 1: 256x128, 2: 128x256, 3: 128x128,
+// 4: 64x64 (also the only scalar-load variant, for unaligned operands).
+template <bool AK, bool BNC>
+void launch_layout(const GemmArgs &a, bool vec, int cfg, hipStream_t st) {
+    if (!vec) {
+        launch_one<64, 64, 2, 2, AK, BNC, false>(a, st);
+        return;
+    }
+    switch (cfg) {
+        case 0: launch_one<256, 256, 2, 2, AK, BNC, true>(a, st); break;
+        case 1: launch_one<256, 128, 2, 2, AK, BNC, true>(a, st); break;
+        case 2: launch_one<128, 256, 2, 2, AK, BNC, true>(a, st); break;
+        case 3: launch_one<128, 128, 2, 2, AK, BNC, true>(a, st); break;
+        default: launch_one<64, 64, 2, 2, AK, BNC, true>(a, st); break;
+    }
+}
+
+// Defined in k_gemm_{nn,nt,tn}.hip.
+void launch_nn(const GemmArgs &a, bool vec, int cfg, hipStream_t st);
+void launch_nt(const GemmArgs &a, bool vec, int cfg, hipStream_t st);
+void launch_tn(const GemmArgs &a, bool vec, int cfg, hipStream_t st);
+
+}  // namespace gemm
+}  // namespace fg

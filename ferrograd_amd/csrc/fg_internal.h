@@ -1,0 +1,67 @@
+// fg_internal.h -- shared internals of the gfx950 backend (not part of the ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/ferrograd_hip.h"
+
+namespace fg {
+
+// Thread-local last error (fg_last_error_msg).
+void set_error(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
+void clear_error();
+
+// Map a HIP status to an fg_status and record the message.  Mirrors the
+// HipError -> ErrorKind mapping of rocm/mod.rs:468-545.
+int hip_fail(hipError_t e, const char *what, const char *file, int line);
+
+}  // namespace fg
+
+struct fg_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    bool own_stream = false;
+    int cu_count = 0;
+    char arch[64] = {0};
+    // Scratch workspace for kernels that need partial results.  Grown by
+    // fg::workspace(); plans reserve it before stream capture.
+    void *ws = nullptr;
+    uint64_t ws_bytes = 0;
+};
+
+struct fg_buf {
+    int device = 0;
+    void *ptr = nullptr;
+    uint64_t bytes = 0;
+};
+
+namespace fg {
+// Returns a workspace pointer of at least `bytes` (grows the context's
+// workspace with a synchronizing reallocation if needed), or nullptr with
+// the error set.
+void *workspace(fg_ctx *ctx, uint64_t bytes);
+}  // namespace fg
+
+#define FG_HIP(call)                                                     \
+    do {                                                                 \
+        hipError_t fg_e_ = (call);                                       \
+        if (fg_e_ != hipSuccess)                                         \
+            return fg::hip_fail(fg_e_, #call, __FILE__, __LINE__);       \
+    } while (0)
+
+#define FG_REQUIRE(cond, code, ...)                                      \
+    do {                                                                 \
+        if (!(cond)) {                                                   \
+            fg::set_error(__VA_ARGS__);                                  \
+            return (code);                                               \
+        }                                                                \
+    } while (0)
+
+// Check the launch that was just enqueued.
+#define FG_LAUNCH_CHECK(name) FG_HIP(hipGetLastError())
+
+#define FG_API extern "C" __attribute__((visibility("default")))

@@ -1,0 +1,226 @@
+// k_gemm.hip -- host dispatch of the MFMA GEMM (tile-configuration choice,
+// argument checks) and the bias-gradient column reduction.  The kernel
+// itself is in fg_gemm_kernel.h, instantiated per layout in k_gemm_*.hip.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+
+#include "fg_gemm_kernel.h"
+#include "fg_internal.h"
+
+namespace {
+
+using fg::gemm::GemmArgs;
+using fg::gemm::kThreads;
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// ------------------------------------------------------------ dispatch
+struct Cfg {
+    int bm, bn;
+    int conc;   // workgroups resident per CU (registers / LDS bound)
+    float eff;  // relative per-CU efficiency (model, tuned by measurement)
+};
+
+constexpr Cfg kCfgs[] = {
+    {256, 256, 1, 0.90f},
+    {256, 128, 1, 0.85f},
+    {128, 256, 1, 0.85f},
+    {128, 128, 2, 0.70f},
+    {64, 64, 4, 0.40f},
+};
+
+int pick_cfg(int M, int N, int cus) {
+    int best = 0;
+    double best_t = 1e300;
+    for (int c = 0; c < (int)(sizeof kCfgs / sizeof kCfgs[0]); ++c) {
+        const Cfg &g = kCfgs[c];
+        const double tiles = (double)((M + g.bm - 1) / g.bm) * (double)((N + g.bn - 1) / g.bn);
+        const double rounds = std::ceil(tiles / ((double)cus * g.conc));
+        const double t = rounds * g.conc * (double)g.bm * g.bn / g.eff;
+        if (t < best_t - 1e-9) {
+            best_t = t;
+            best = c;
+        }
+    }
+    return best;
+}
+
+int gemm_common(fg_ctx *ctx, int layout, GemmArgs &a, const char *who) {
+    FG_REQUIRE(ctx, FG_ERR_INVALID_ARGUMENT, "%s: ctx is NULL", who);
+    FG_REQUIRE(layout >= FG_NN && layout <= FG_TN, FG_ERR_INVALID_ARGUMENT, "%s: bad layout %d",
+               who, layout);
+    FG_REQUIRE(a.M >= 0 && a.N >= 0 && a.K >= 0, FG_ERR_SHAPE, "%s: negative dimension", who);
+    FG_REQUIRE(a.act >= 0 && a.act <= 2, FG_ERR_INVALID_ARGUMENT, "%s: bad act %d", who, a.act);
+    if (a.M == 0 || a.N == 0) return FG_OK;
+    FG_REQUIRE(a.A && a.B && a.C, FG_ERR_INVALID_ARGUMENT, "%s: NULL operand", who);
+    // Leading dimensions: A is [M][K] (NN/NT) or [K][M] (TN); B is [K][N]
+    // (NN/TN) or [N][K] (NT); C is [M][N].
+    const int a_cols = layout == FG_TN ? a.M : a.K;
+    const int b_cols = layout == FG_NT ? a.K : a.N;
+    FG_REQUIRE(a.lda >= std::max(a_cols, 1) && a.ldb >= std::max(b_cols, 1) && a.ldc >= a.N,
+               FG_ERR_SHAPE, "%s: leading dimension too small (lda=%d ldb=%d ldc=%d)", who, a.lda,
+               a.ldb, a.ldc);
+    FG_HIP(hipSetDevice(ctx->device));
+    if (a.K == 0) a.A = a.B;  // loads are all masked; K=0 yields the epilogue of zero
+    // The 16-byte path needs 16-byte aligned bases and every row start
+    // aligned, i.e. leading dimensions and the contiguous extents that the
+    // bounds checks split on (K for k-contiguous operands, M / N otherwise)
+    // divisible by 4.
+    const bool aligned_ptrs = ((((uintptr_t)a.A) | ((uintptr_t)a.B)) & 15u) == 0;
+    bool vec = aligned_ptrs && a.lda % 4 == 0 && a.ldb % 4 == 0;
+    if (layout == FG_NN) vec = vec && a.K % 4 == 0 && a.N % 4 == 0;
+    if (layout == FG_NT) vec = vec && a.K % 4 == 0;
+    if (layout == FG_TN) vec = vec && a.M % 4 == 0 && a.N % 4 == 0;
+    const int cfg = pick_cfg(a.M, a.N, ctx->cu_count > 0 ? ctx->cu_count : 256);
+    auto al16 = [](const void *q) { return (((uintptr_t)q) & 15u) == 0; };
+    a.vec_out = al16(a.C) && a.ldc % 4 == 0 && (!a.Z || (al16(a.Z) && a.ldz % 4 == 0)) &&
+                (!a.bias || al16(a.bias));
+    switch (layout) {
+        case FG_NN: fg::gemm::launch_nn(a, vec, cfg, ctx->stream); break;
+        case FG_NT: fg::gemm::launch_nt(a, vec, cfg, ctx->stream); break;
+        default: fg::gemm::launch_tn(a, vec, cfg, ctx->stream); break;
+    }
+    FG_LAUNCH_CHECK(who);
+    return FG_OK;
+}
+
+// ----------------------------------------------------------- bias grad
+// Column sums of dZ[M][N]: phase 1 -- grid (column strips of 256 columns,
+// row splits); each thread sums 4 columns (float4) over its rows; partial
+// results per split go to workspace.  Phase 2 -- one thread per column adds
+// the splits in order.  Deterministic.
+constexpr int kBgCols = 256;  // columns per strip (64 lanes x float4)
+constexpr int kBgRowsPerThreadGroup = kThreads / (kBgCols / 4);  // 4 row groups
+
+__global__ __launch_bounds__(kThreads) void bias_grad_partial(const float *__restrict__ dZ, int M,
+                                                              int N, int ld, int rows_per_split,
+                                                              float *__restrict__ partial,
+                                                              int vec) {
+    __shared__ f32x4 sh[kThreads];
+    const int strip = blockIdx.x, split = blockIdx.y;
+    const int cq = threadIdx.x % (kBgCols / 4);
+    const int rg = threadIdx.x / (kBgCols / 4);
+    const int col = strip * kBgCols + cq * 4;
+    const int r0 = split * rows_per_split;
+    const int r1 = min(M, r0 + rows_per_split);
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    if (col < N) {
+        for (int r = r0 + rg; r < r1; r += kBgRowsPerThreadGroup) {
+            const float *row = dZ + (size_t)r * ld;
+            if (vec && col + 4 <= N) {
+                s += *reinterpret_cast<const f32x4 *>(row + col);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (col + e < N) s[e] += row[col + e];
+            }
+        }
+    }
+    sh[threadIdx.x] = s;
+    __syncthreads();
+    if (rg == 0 && col < N) {
+        f32x4 t = sh[cq];
+#pragma unroll
+        for (int g = 1; g < kBgRowsPerThreadGroup; ++g) t += sh[g * (kBgCols / 4) + cq];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (col + e < N) partial[(size_t)split * N + col + e] = t[e];
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void bias_grad_final(const float *__restrict__ partial,
+                                                            int splits, int N,
+                                                            float *__restrict__ dbias,
+                                                            int accumulate) {
+    const int col = blockIdx.x * kThreads + threadIdx.x;
+    if (col >= N) return;
+    float s = 0.0f;
+    for (int k = 0; k < splits; ++k) s += partial[(size_t)k * N + col];
+    dbias[col] = accumulate ? dbias[col] + s : s;
+}
+
+}  // namespace
+
+FG_API int fg_gemm_f32(fg_ctx *ctx, int layout, int M, int N, int K, const float *d_A, int lda,
+                       const float *d_B, int ldb, const float *d_bias, int act, float *d_C,
+                       int ldc, float *d_Z, int ldz, int accumulate) {
+    GemmArgs a{};
+    a.A = d_A;
+    a.B = d_B;
+    a.C = d_C;
+    a.Z = d_Z;
+    a.bias = d_bias;
+    a.Zs = nullptr;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.lda = lda;
+    a.ldb = ldb;
+    a.ldc = ldc;
+    a.ldz = d_Z ? ldz : 0;
+    a.ldzs = 0;
+    a.act = act;
+    a.mode = 0;
+    a.accumulate = accumulate ? 1 : 0;
+    FG_REQUIRE(!d_Z || ldz >= N, FG_ERR_SHAPE, "fg_gemm_f32: ldz=%d < N=%d", ldz, N);
+    FG_REQUIRE(!(accumulate && act != FG_ACT_NONE), FG_ERR_INVALID_ARGUMENT,
+               "fg_gemm_f32: accumulate requires act NONE");
+    return gemm_common(ctx, layout, a, "fg_gemm_f32");
+}
+
+FG_API int fg_gemm_bwd_f32(fg_ctx *ctx, int layout, int M, int N, int K, const float *d_A, int lda,
+                           const float *d_B, int ldb, int act, const float *d_Zs, int ldzs,
+                           float *d_C, int ldc, int accumulate) {
+    GemmArgs a{};
+    a.A = d_A;
+    a.B = d_B;
+    a.C = d_C;
+    a.Z = nullptr;
+    a.bias = nullptr;
+    a.Zs = d_Zs;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.lda = lda;
+    a.ldb = ldb;
+    a.ldc = ldc;
+    a.ldz = 0;
+    a.ldzs = ldzs;
+    a.act = act;
+    a.mode = 1;
+    a.accumulate = accumulate ? 1 : 0;
+    FG_REQUIRE(act == FG_ACT_NONE || (d_Zs && ldzs >= N), FG_ERR_INVALID_ARGUMENT,
+               "fg_gemm_bwd_f32: act %d needs Zs with ldzs >= N", act);
+    return gemm_common(ctx, layout, a, "fg_gemm_bwd_f32");
+}
+
+FG_API int fg_bias_grad_f32(fg_ctx *ctx, int M, int N, const float *d_dZ, int ld, float *d_dbias,
+                            int accumulate) {
+    FG_REQUIRE(ctx, FG_ERR_INVALID_ARGUMENT, "fg_bias_grad_f32: ctx is NULL");
+    FG_REQUIRE(M >= 0 && N >= 0 && ld >= N, FG_ERR_SHAPE,
+               "fg_bias_grad_f32: bad shape M=%d N=%d ld=%d", M, N, ld);
+    if (N == 0) return FG_OK;
+    FG_REQUIRE(d_dZ && d_dbias, FG_ERR_INVALID_ARGUMENT, "fg_bias_grad_f32: NULL pointer");
+    FG_HIP(hipSetDevice(ctx->device));
+    const int strips = (N + kBgCols - 1) / kBgCols;
+    const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    // Enough splits for ~4 workgroups per CU, each covering >= 16 rows.
+    int splits = std::max(1, std::min((4 * cus + strips - 1) / strips, (M + 15) / 16));
+    const int rows_per_split = M > 0 ? (M + splits - 1) / splits : 0;
+    splits = M > 0 ? (M + rows_per_split - 1) / rows_per_split : 1;
+    float *partial = (float *)fg::workspace(ctx, (uint64_t)splits * N * sizeof(float));
+    if (!partial) return FG_ERR_OUT_OF_MEMORY;
+    const int vec = ((((uintptr_t)d_dZ) & 15u) == 0) && (ld % 4 == 0);
+    if (M > 0) {
+        bias_grad_partial<<<dim3(strips, splits), kThreads, 0, ctx->stream>>>(
+            d_dZ, M, N, ld, rows_per_split, partial, vec);
+        FG_LAUNCH_CHECK("bias_grad_partial");
+    } else {
+        splits = 0;
+    }
+    bias_grad_final<<<(N + kThreads - 1) / kThreads, kThreads, 0, ctx->stream>>>(
+        partial, splits, N, d_dbias, accumulate);
+    FG_LAUNCH_CHECK("bias_grad_final");
+    return FG_OK;
+}

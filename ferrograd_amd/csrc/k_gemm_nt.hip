@@ -1,0 +1,13 @@
+// k_gemm_nt.hip -- instantiates the MFMA GEMM for layout NT: dA = dC.B^T (A[M][K], B stored [N][K]).
+// Kept in its own translation unit so the three layouts compile in parallel.
+#include "fg_gemm_kernel.h"
+
+namespace fg {
+namespace gemm {
+
+void launch_nt(const GemmArgs &a, bool vec, int cfg, hipStream_t st) {
+    launch_layout<true, false>(a, vec, cfg, st);
+}
+
+}  // namespace gemm
+}  // namespace fg

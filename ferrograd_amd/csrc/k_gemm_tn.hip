@@ -1,0 +1,13 @@
+// k_gemm_tn.hip -- instantiates the MFMA GEMM for layout TN: dB = A^T.dC (A stored [K][M], B[K][N]).
+// Kept in its own translation unit so the three layouts compile in parallel.
+#include "fg_gemm_kernel.h"
+
+namespace fg {
+namespace gemm {
+
+void launch_tn(const GemmArgs &a, bool vec, int cfg, hipStream_t st) {
+    launch_layout<false, true>(a, vec, cfg, st);
+}
+
+}  // namespace gemm
+}  // namespace fg

@@ -1,0 +1,322 @@
+// k_softmax.hip -- row softmax, fused softmax + cross-entropy (forward and
+// backward), softmax backward, for gfx950.
+//
+// Reference: the softmax node (crates/ferrograd-nn/src/op/softmax.rs:112-446)
+// makes three passes over each row with 256-thread LDS tree reductions
+// (read x twice, write e, read-modify-write e), the CE loss kernel
+// (crates/fused_gpu/src/dispatch/backend/kernel/loss.rs:12-165 with
+// basic_loss.rs:91-133) is a separate launch writing a full [R,C] loss
+// buffer, and its gradient is then pushed through the softmax Jacobian a
+// second time (defect).
+//
+// Here one workgroup owns one row.  The fast path keeps the whole row in
+// registers (NV float4 per thread, 256 threads: up to 32768 columns), so the
+// logits are read from HBM exactly once and dlogits written exactly once:
+// 8*C bytes per row, the minimum.  Reductions are wavefront shuffles (64
+// lanes) followed by one LDS exchange across the 4 waves.  Rows too long for
+// registers, or not 16-byte aligned, use a two-pass streaming kernel with an
+// online max/sum.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "fg_internal.h"
+
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kNT = 256;
+constexpr int kWaves = kNT / 64;
+
+__device__ __forceinline__ void argmax_combine(float &m, int &i, float m2, int i2) {
+    if (m2 > m || (m2 == m && i2 < i)) {
+        m = m2;
+        i = i2;
+    }
+}
+
+// Block-wide (max, lowest index of max); every thread receives the result.
+__device__ __forceinline__ void block_argmax(float &m, int &idx, float *sm, int *si) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float m2 = __shfl_xor(m, o);
+        const int i2 = __shfl_xor(idx, o);
+        argmax_combine(m, idx, m2, i2);
+    }
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        sm[w] = m;
+        si[w] = idx;
+    }
+    __syncthreads();
+    m = sm[0];
+    idx = si[0];
+#pragma unroll
+    for (int k = 1; k < kWaves; ++k) argmax_combine(m, idx, sm[k], si[k]);
+    __syncthreads();
+}
+
+__device__ __forceinline__ float block_sum(float s, float *sm) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) sm[w] = s;
+    __syncthreads();
+    float t = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kWaves; ++k) t += sm[k];
+    __syncthreads();
+    return t;
+}
+
+// (max, sum of exp(x - max)) pairs for the streaming kernel.
+__device__ __forceinline__ void ms_combine(float &m, float &s, float m2, float s2) {
+    const float mn = fmaxf(m, m2);
+    if (mn == -INFINITY) return;
+    s = s * expf(m - mn) + s2 * expf(m2 - mn);
+    m = mn;
+}
+
+__device__ __forceinline__ void block_ms(float &m, float &s, float *sm, float *ss) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float m2 = __shfl_xor(m, o);
+        const float s2 = __shfl_xor(s, o);
+        ms_combine(m, s, m2, s2);
+    }
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        sm[w] = m;
+        ss[w] = s;
+    }
+    __syncthreads();
+    m = sm[0];
+    s = ss[0];
+#pragma unroll
+    for (int k = 1; k < kWaves; ++k) ms_combine(m, s, sm[k], ss[k]);
+    __syncthreads();
+}
+
+// Row epilogue shared by both kernels: loss and argmax from thread 0.
+__device__ __forceinline__ void row_outputs(const float *xr, int C, const uint32_t *labels, int r,
+                                            float m, float s, int am, float *row_loss,
+                                            uint32_t *argmax) {
+    if (threadIdx.x != 0) return;
+    if (argmax) argmax[r] = (uint32_t)am;
+    if (row_loss) {
+        const uint32_t t = labels ? labels[r] : 0u;
+        // A label outside [0, C) has no logit; report NaN rather than read.
+        row_loss[r] = (t < (uint32_t)C) ? (m + logf(s)) - xr[t] : __builtin_nanf("");
+    }
+}
+
+// Register-resident fast path.  out (may be NULL) receives
+//   labels ? scale*(p - onehot) : scale*p.
+template <int NV>
+__global__ __launch_bounds__(kNT) void softmax_rows_v4(const float *__restrict__ x, int ldx,
+                                                       const uint32_t *__restrict__ labels, int C,
+                                                       float scale, float *__restrict__ row_loss,
+                                                       float *__restrict__ out, int ldo,
+                                                       uint32_t *__restrict__ argmax) {
+    __shared__ float sm[kWaves];
+    __shared__ int si[kWaves];
+    const int r = blockIdx.x;
+    const float *xr = x + (size_t)r * ldx;
+    const int C4 = C >> 2;
+    f32x4 v[NV];
+    float m = -INFINITY;
+    int am = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int j = threadIdx.x + i * kNT;
+        if (j < C4)
+            v[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(xr) + j);
+        else
+            v[i] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    }
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c0 = 4 * (threadIdx.x + i * kNT);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (v[i][e] > m) {
+                m = v[i][e];
+                am = c0 + e;
+            }
+    }
+    block_argmax(m, am, sm, si);
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[i][e] = expf(v[i][e] - m);
+            s += v[i][e];
+        }
+    }
+    s = block_sum(s, sm);
+    row_outputs(xr, C, labels, r, m, s, am, row_loss, argmax);
+    if (out) {
+        const float inv = 1.0f / s;
+        const int t = labels ? (int)labels[r] : -1;
+        float *orow = out + (size_t)r * ldo;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int j = threadIdx.x + i * kNT;
+            if (j < C4) {
+                f32x4 d;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float p = v[i][e] * inv;
+                    d[e] = scale * (4 * j + e == t ? p - 1.0f : p);
+                }
+                __builtin_nontemporal_store(d, reinterpret_cast<f32x4 *>(orow) + j);
+            }
+        }
+    }
+}
+
+// Streaming path for any C and alignment: pass 1 online (max, sum, argmax),
+// pass 2 recomputes exp and writes.
+__global__ __launch_bounds__(kNT) void softmax_rows_stream(const float *__restrict__ x, int ldx,
+                                                           const uint32_t *__restrict__ labels,
+                                                           int C, float scale,
+                                                           float *__restrict__ row_loss,
+                                                           float *__restrict__ out, int ldo,
+                                                           uint32_t *__restrict__ argmax) {
+    __shared__ float sm[kWaves], ss[kWaves];
+    __shared__ int si[kWaves];
+    const int r = blockIdx.x;
+    const float *xr = x + (size_t)r * ldx;
+    float m = -INFINITY, s = 0.0f, am_m = -INFINITY;
+    int am = 0x7fffffff;
+    for (int c = threadIdx.x; c < C; c += kNT) {
+        const float xv = xr[c];
+        if (xv > am_m) {
+            am_m = xv;
+            am = c;
+        }
+        ms_combine(m, s, xv, 1.0f);
+    }
+    block_argmax(am_m, am, sm, si);
+    block_ms(m, s, sm, ss);
+    row_outputs(xr, C, labels, r, m, s, am, row_loss, argmax);
+    if (out) {
+        const float inv = 1.0f / s;
+        const int t = labels ? (int)labels[r] : -1;
+        float *orow = out + (size_t)r * ldo;
+        for (int c = threadIdx.x; c < C; c += kNT) {
+            const float p = expf(xr[c] - m) * inv;
+            orow[c] = scale * (c == t ? p - 1.0f : p);
+        }
+    }
+}
+
+// mean[0] = sum(vals[0..n)) / n in a fixed order (one block).
+__global__ __launch_bounds__(1024) void mean_kernel(const float *__restrict__ vals, int n,
+                                                    float *__restrict__ mean) {
+    __shared__ double sh[1024];
+    double acc = 0.0;
+    for (int i = threadIdx.x; i < n; i += 1024) acc += (double)vals[i];
+    sh[threadIdx.x] = acc;
+    __syncthreads();
+    for (int o = 512; o > 0; o >>= 1) {
+        if ((int)threadIdx.x < o) sh[threadIdx.x] += sh[threadIdx.x + o];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) mean[0] = n > 0 ? (float)(sh[0] / (double)n) : 0.0f;
+}
+
+// dx (=|+=) y * (dy - sum(dy*y)) per row (softmax.rs:448-688, all columns).
+__global__ __launch_bounds__(kNT) void softmax_bwd_rows(const float *__restrict__ y,
+                                                        const float *__restrict__ dy, int C,
+                                                        float *__restrict__ dx, int accumulate) {
+    __shared__ float sm[kWaves];
+    const size_t base = (size_t)blockIdx.x * C;
+    float dot = 0.0f;
+    for (int c = threadIdx.x; c < C; c += kNT) dot += dy[base + c] * y[base + c];
+    dot = block_sum(dot, sm);
+    for (int c = threadIdx.x; c < C; c += kNT) {
+        const float g = y[base + c] * (dy[base + c] - dot);
+        dx[base + c] = accumulate ? dx[base + c] + g : g;
+    }
+}
+
+int launch_rows(fg_ctx *ctx, const float *x, int ldx, const uint32_t *labels, int R, int C,
+                float scale, float *row_loss, float *out, int ldo, uint32_t *argmax) {
+    const bool aligned = ((((uintptr_t)x) | ((uintptr_t)out)) & 15u) == 0 && (C % 4 == 0) &&
+                         (ldx % 4 == 0) && (!out || ldo % 4 == 0);
+    const int C4 = C / 4;
+    dim3 grid(R), block(kNT);
+    hipStream_t st = ctx->stream;
+#define FG_SM_LAUNCH(NV)                                                                    \
+    softmax_rows_v4<NV><<<grid, block, 0, st>>>(x, ldx, labels, C, scale, row_loss, out, ldo, \
+                                                argmax)
+    if (aligned && C4 <= kNT * 1)
+        FG_SM_LAUNCH(1);
+    else if (aligned && C4 <= kNT * 2)
+        FG_SM_LAUNCH(2);
+    else if (aligned && C4 <= kNT * 4)
+        FG_SM_LAUNCH(4);
+    else if (aligned && C4 <= kNT * 8)
+        FG_SM_LAUNCH(8);
+    else if (aligned && C4 <= kNT * 16)
+        FG_SM_LAUNCH(16);
+    else if (aligned && C4 <= kNT * 32)
+        FG_SM_LAUNCH(32);
+    else
+        softmax_rows_stream<<<grid, block, 0, st>>>(x, ldx, labels, C, scale, row_loss, out, ldo,
+                                                    argmax);
+#undef FG_SM_LAUNCH
+    FG_LAUNCH_CHECK("softmax_rows");
+    return FG_OK;
+}
+
+}  // namespace
+
+FG_API int fg_softmax_ce_f32(fg_ctx *ctx, const float *d_logits, int ldx, const uint32_t *d_labels,
+                             int R, int C, float grad_scale, float *d_row_loss, float *d_mean_loss,
+                             float *d_dlogits, int ldd, uint32_t *d_argmax) {
+    FG_REQUIRE(ctx, FG_ERR_INVALID_ARGUMENT, "fg_softmax_ce_f32: ctx is NULL");
+    FG_REQUIRE(R >= 0 && C > 0 && ldx >= C, FG_ERR_SHAPE,
+               "fg_softmax_ce_f32: bad shape R=%d C=%d ldx=%d", R, C, ldx);
+    FG_REQUIRE(!d_dlogits || ldd >= C, FG_ERR_SHAPE, "fg_softmax_ce_f32: ldd=%d < C=%d", ldd, C);
+    FG_REQUIRE(d_logits && d_labels, FG_ERR_INVALID_ARGUMENT,
+               "fg_softmax_ce_f32: logits and labels are required");
+    if (R == 0) return FG_OK;
+    FG_HIP(hipSetDevice(ctx->device));
+    float *row_loss = d_row_loss;
+    if (!row_loss && d_mean_loss) {
+        row_loss = (float *)fg::workspace(ctx, (uint64_t)R * sizeof(float));
+        if (!row_loss) return FG_ERR_OUT_OF_MEMORY;
+    }
+    int rc = launch_rows(ctx, d_logits, ldx, d_labels, R, C, grad_scale, row_loss, d_dlogits, ldd,
+                         d_argmax);
+    if (rc) return rc;
+    if (d_mean_loss) {
+        mean_kernel<<<1, 1024, 0, ctx->stream>>>(row_loss, R, d_mean_loss);
+        FG_LAUNCH_CHECK("mean_kernel");
+    }
+    return FG_OK;
+}
+
+FG_API int fg_softmax_f32(fg_ctx *ctx, const float *d_x, int R, int C, float *d_y) {
+    FG_REQUIRE(ctx && d_x && d_y, FG_ERR_INVALID_ARGUMENT, "fg_softmax_f32: NULL argument");
+    FG_REQUIRE(R >= 0 && C > 0, FG_ERR_SHAPE, "fg_softmax_f32: bad shape R=%d C=%d", R, C);
+    if (R == 0) return FG_OK;
+    FG_HIP(hipSetDevice(ctx->device));
+    return launch_rows(ctx, d_x, C, nullptr, R, C, 1.0f, nullptr, d_y, C, nullptr);
+}
+
+FG_API int fg_softmax_bwd_f32(fg_ctx *ctx, const float *d_y, const float *d_dy, int R, int C,
+                              float *d_dx, int accumulate) {
+    FG_REQUIRE(ctx && d_y && d_dy && d_dx, FG_ERR_INVALID_ARGUMENT,
+               "fg_softmax_bwd_f32: NULL argument");
+    FG_REQUIRE(R >= 0 && C > 0, FG_ERR_SHAPE, "fg_softmax_bwd_f32: bad shape R=%d C=%d", R, C);
+    if (R == 0) return FG_OK;
+    FG_HIP(hipSetDevice(ctx->device));
+    softmax_bwd_rows<<<R, kNT, 0, ctx->stream>>>(d_y, d_dy, C, d_dx, accumulate);
+    FG_LAUNCH_CHECK("softmax_bwd_rows");
+    return FG_OK;
+}

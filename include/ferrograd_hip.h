@@ -1,0 +1,210 @@
+/*
+ * ferrograd_hip.h -- C ABI of the MI355X (gfx950) backend for ferrograd's
+ * fused training path.
+ *
+ * The reference's seam for this path is the Rust trait `GpuBackend`
+ * (crates/fused_gpu/src/dispatch/mod.rs:161-261) implemented by
+ * `rocm::GpuContext` (crates/fused_gpu/src/dispatch/backend/rocm/mod.rs:81-429)
+ * plus the graph/plug-in types of crates/fused_gpu/src/dispatch/backend/mod.rs.
+ * Each entry point below names the reference interface it replaces.
+ *
+ * Conventions
+ *  - Every function returns an fg_status (0 = success).  On failure the
+ *    message is available from fg_last_error_msg() on the same thread.
+ *  - Sizes are in bytes unless named otherwise; tensors are row-major fp32
+ *    with the last dimension contiguous; leading dimensions are in elements.
+ *  - Pointers named `d_*` or typed as device tensors are device addresses;
+ *    all device work is enqueued on the context's stream, asynchronously,
+ *    in call order.  fg_sync() waits for it.
+ *  - No call allocates device memory except the fg_buf_*, fg_mt_create,
+ *    fg_ctx_reserve_workspace and fg_graph_lower entry points (and the
+ *    first call of a direct kernel that needs more workspace than the
+ *    context holds).
+ */
+#ifndef FERROGRAD_HIP_H
+#define FERROGRAD_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes: a subset of fused_gpu::errors::ErrorKind
+ * (crates/fused_gpu/src/errors.rs:102-140), one code per kind this backend
+ * can raise. */
+typedef enum fg_status {
+    FG_OK = 0,
+    FG_ERR_INVALID_ARGUMENT = 1, /* ErrorKind::InvalidArgument           */
+    FG_ERR_OUT_OF_MEMORY = 2,    /* ErrorKind::OutOfMemory               */
+    FG_ERR_UNSUPPORTED = 3,      /* ErrorKind::UnsupportedFeature        */
+    FG_ERR_DEVICE = 4,           /* ErrorKind::DeviceError (HIP status)  */
+    FG_ERR_SHAPE = 5,            /* ErrorKind::ShapeMismatch             */
+    FG_ERR_GRAPH = 6,            /* ErrorKind::ComputeGraphError         */
+    FG_ERR_INTERNAL = 7,         /* ErrorKind::InternalError             */
+    FG_ERR_NO_DEVICE = 8,        /* ErrorKind::NoDevice                  */
+    FG_ERR_OUT_OF_BOUNDS = 9     /* ErrorKind::OutOfBounds               */
+} fg_status;
+
+/* Message of the last failing call on this thread ("" if none).  Replaces
+ * the `msg`/`ctx` fields of fused_gpu::errors::Error (errors.rs:13-19). */
+const char *fg_last_error_msg(void);
+/* Library ABI version (major*10000 + minor*100 + patch). */
+int fg_version(void);
+
+/* ------------------------------------------------------------- context */
+typedef struct fg_ctx fg_ctx;
+
+/* Target flags reported by fg_ctx_target (TargetFlags, dispatch/mod.rs:32-60). */
+#define FG_TARGET_LIN_ACC 0x1u /* matrix cores present (MFMA)           */
+
+/* Open `device` and bind a stream.  `stream` is an existing hipStream_t to
+ * enqueue on, or NULL to create a private default-priority stream.
+ * Replaces rocm::GpuContext::new (rocm/mod.rs:57-79). */
+int fg_ctx_create(int device, void *stream, fg_ctx **out);
+int fg_ctx_destroy(fg_ctx *ctx);
+/* Architecture name (e.g. "gfx950"), FG_TARGET_* flags and CU count.
+ * Replaces GpuBackend::target_spec (dispatch/mod.rs:161-170). */
+int fg_ctx_target(fg_ctx *ctx, char *arch, size_t arch_len, uint32_t *flags,
+                  int *cu_count);
+/* The hipStream_t work is enqueued on. */
+int fg_ctx_stream(fg_ctx *ctx, void **stream);
+/* Pre-size the context's scratch workspace so later direct-kernel calls
+ * (and graph capture) never allocate. */
+int fg_ctx_reserve_workspace(fg_ctx *ctx, uint64_t bytes);
+/* GpuBackend::sync / is_ready (rocm/mod.rs:398-400). */
+int fg_sync(fg_ctx *ctx);
+int fg_is_ready(fg_ctx *ctx, int *ready);
+
+/* ------------------------------------------------------------- buffers */
+typedef struct fg_buf fg_buf;
+
+/* GpuBackend::alloc / alloc_zeroed / alloc_init (dispatch/mod.rs:161-200).
+ * Sizes are u64 bytes (the reference's are u32). */
+int fg_buf_alloc(fg_ctx *ctx, uint64_t bytes, fg_buf **out);
+int fg_buf_alloc_zeroed(fg_ctx *ctx, uint64_t bytes, fg_buf **out);
+int fg_buf_alloc_init(fg_ctx *ctx, const void *src, uint64_t bytes, fg_buf **out);
+int fg_buf_free(fg_buf *buf);
+/* Buffer::size_bytes (tensor.rs:125-198). */
+uint64_t fg_buf_size_bytes(const fg_buf *buf);
+/* Device address of the buffer's first byte. */
+void *fg_buf_device_ptr(const fg_buf *buf);
+/* GpuBackend::upload / download / copy (rocm/mod.rs:184-205, 402-421):
+ * synchronous with respect to the host buffer. */
+int fg_upload(fg_ctx *ctx, fg_buf *dst, const void *src, uint64_t bytes,
+              uint64_t dst_off);
+int fg_download(fg_ctx *ctx, const fg_buf *src, void *dst, uint64_t bytes,
+                uint64_t src_off);
+int fg_copy(fg_ctx *ctx, const fg_buf *src, fg_buf *dst);
+/* Fill `count` u32 words of a buffer with `value` (a small fill kernel,
+ * safe under stream capture). */
+int fg_fill_u32(fg_ctx *ctx, void *d_dst, uint32_t value, uint64_t count);
+
+/* ------------------------------------------------- direct kernel calls */
+/* Operand layouts of the matmul lowering (ferrograd-nn op/matmul/mod.rs:17-188):
+ *   NN: C = A.B     A[M][K], B[K][N]   forward          (generic.rs:98-149)
+ *   NT: C = A.B^T   A[M][K], B[N][K]   dA = dC.B^T      (mod.rs:75-84)
+ *   TN: C = A^T.B   A[K][M], B[K][N]   dB = A^T.dC      (mod.rs:85-94)   */
+typedef enum fg_layout { FG_NN = 0, FG_NT = 1, FG_TN = 2 } fg_layout;
+/* Activations fused in GEMM epilogues (relu: unary.rs:436-490,
+ * gelu tanh form: unary.rs:492-733). */
+typedef enum fg_act { FG_ACT_NONE = 0, FG_ACT_RELU = 1, FG_ACT_GELU = 2 } fg_act;
+
+/* Forward GEMM with fused epilogue:
+ *   Zv = op(A).op(B) (+ bias[col] if d_bias) ;  C = act(Zv)
+ *   if d_Z: Z = Zv (pre-activation saved for backward)
+ *   if accumulate: C += act(Zv) instead of C = act(Zv) (requires act NONE)
+ * Replaces the matmul-rooted fused kernel (forward.rs:298-464 with
+ * generic.rs:13-325) plus the bias/activation consumers inlined after it. */
+int fg_gemm_f32(fg_ctx *ctx, int layout, int M, int N, int K,
+                const float *d_A, int lda, const float *d_B, int ldb,
+                const float *d_bias, int act, float *d_C, int ldc,
+                float *d_Z, int ldz, int accumulate);
+
+/* Backward GEMM with the activation derivative fused in the epilogue:
+ *   C = (op(A).op(B)) * act'(Zs)        (elementwise, Zs[M][N] ld ldzs)
+ * or C += ... when accumulate.  With act NONE, Zs is ignored.  Used for
+ * dZ_prev = (dZ . W^T) * act'(Z_prev): matmul dA (mod.rs:75-84) with the
+ * upstream activation's backward (unary.rs) inlined. */
+int fg_gemm_bwd_f32(fg_ctx *ctx, int layout, int M, int N, int K,
+                    const float *d_A, int lda, const float *d_B, int ldb,
+                    int act, const float *d_Zs, int ldzs, float *d_C, int ldc,
+                    int accumulate);
+
+/* dbias[j] (=|+=) sum_i dZ[i][j]: the bias-add's backward (new broadcast
+ * op; reference binary.rs:53-63 has none). Deterministic order. */
+int fg_bias_grad_f32(fg_ctx *ctx, int M, int N, const float *d_dZ, int ld,
+                     float *d_dbias, int accumulate);
+
+/* dZ[i] = dH[i] * act'(Z[i]) over n elements (unary backward, unary.rs). */
+int fg_act_bwd_f32(fg_ctx *ctx, int act, uint64_t n, const float *d_dH,
+                   const float *d_Z, float *d_dZ);
+
+/* Fused row softmax + cross-entropy, forward and backward, one HBM read of
+ * the logits (softmax.rs:112-446 + basic_loss.rs:91-133 + loss.rs:12-165):
+ *   row_loss[r] = logsumexp(x_r) - x_r[label_r]
+ *   mean_loss[0] = mean_r row_loss[r]
+ *   dlogits[r][c] = grad_scale * (softmax(x_r)[c] - [c == label_r])
+ *   argmax[r] = lowest c attaining max_c x_r[c]
+ * Any output pointer may be NULL to skip it. labels[r] must be < C. */
+int fg_softmax_ce_f32(fg_ctx *ctx, const float *d_logits, int ldx,
+                      const uint32_t *d_labels, int R, int C, float grad_scale,
+                      float *d_row_loss, float *d_mean_loss, float *d_dlogits,
+                      int ldd, uint32_t *d_argmax);
+
+/* Plain row softmax y = softmax(x) and its backward
+ * dx (=|+=) y * (dy - sum(dy*y)) (softmax.rs:112-446, 448-688). */
+int fg_softmax_f32(fg_ctx *ctx, const float *d_x, int R, int C, float *d_y);
+int fg_softmax_bwd_f32(fg_ctx *ctx, const float *d_y, const float *d_dy, int R,
+                       int C, float *d_dx, int accumulate);
+
+/* ----------------------------------------- multi-tensor optimiser lists */
+/* One launch updates every tensor of the list.  Replaces the per-tensor
+ * optimiser kernels captured one launch per input tensor
+ * (kernel/optim.rs:12-158, rocm/mod.rs:268-322), with per-tensor sizes
+ * (the reference derives every size from the root node's shape). */
+typedef struct fg_mt fg_mt;
+/* params/grads: n device pointers each; m/v: n device pointers each for Adam
+ * state, or NULL for SGD; sizes: elements per tensor. */
+int fg_mt_create(fg_ctx *ctx, int n, float *const *d_params,
+                 float *const *d_grads, float *const *d_m, float *const *d_v,
+                 const uint64_t *sizes, fg_mt **out);
+int fg_mt_destroy(fg_mt *mt);
+/* SGD (basic_optim.rs:3-31): w -= fl(g*lr); g = 0 when zero_grad. */
+int fg_sgd_step(fg_ctx *ctx, fg_mt *mt, float lr, int zero_grad);
+/* Adam (PyTorch formula, bias-corrected; absent in the reference):
+ *   m = b1 m + (1-b1) g ; v = b2 v + (1-b2) g^2
+ *   p -= (lr/(1-b1^t)) m / (sqrt(v)/sqrt(1-b2^t) + eps)
+ * `step` is t >= 1; bias corrections are computed in double on the host. */
+int fg_adam_step(fg_ctx *ctx, fg_mt *mt, float lr, float b1, float b2,
+                 float eps, int step, int zero_grad);
+/* Same update with precomputed fp32 step_size = lr/(1-b1^t) and
+ * inv_sqrt_bc2 = 1/sqrt(1-b2^t) (what fg_adam_step derives). */
+int fg_adam_step_scalars(fg_ctx *ctx, fg_mt *mt, float b1, float b2, float eps,
+                         float step_size, float inv_sqrt_bc2, int zero_grad);
+
+/* ----------------------------------------------------- synthetic data */
+/* Counter-based SplitMix64 generator keyed by (seed, tensor_id): element i
+ * depends only on (seed, tensor_id, i), so host and device fills of the same
+ * key produce the same values.  Used to build identical CPU/GPU inputs.
+ *   uniform: [lo, hi) from the top 24 bits of the 64-bit draw
+ *   normal : mean + std * Box-Muller(draws 2i, 2i+1), computed in double
+ *   int    : floor(u32 * n / 2^32) in [0, n)                               */
+int fg_rng_uniform_host(uint64_t seed, uint64_t tensor_id, float lo, float hi,
+                        float *dst, uint64_t n);
+int fg_rng_normal_host(uint64_t seed, uint64_t tensor_id, float mean, float std,
+                       float *dst, uint64_t n);
+int fg_rng_int_host(uint64_t seed, uint64_t tensor_id, uint32_t bound,
+                    uint32_t *dst, uint64_t n);
+int fg_rng_uniform_dev(fg_ctx *ctx, uint64_t seed, uint64_t tensor_id, float lo,
+                       float hi, float *d_dst, uint64_t n);
+int fg_rng_normal_dev(fg_ctx *ctx, uint64_t seed, uint64_t tensor_id, float mean,
+                      float std, float *d_dst, uint64_t n);
+int fg_rng_int_dev(fg_ctx *ctx, uint64_t seed, uint64_t tensor_id, uint32_t bound,
+                   uint32_t *d_dst, uint64_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FERROGRAD_HIP_H */

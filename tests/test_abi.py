@@ -1,0 +1,81 @@
+"""CPU checks of the C-ABI library: it loads, exports exactly what
+include/ferrograd_hip.h declares, and its host-only code paths (argument
+validation, the synthetic-data generator) behave.  No GPU work is issued."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import ferrograd_amd as fa
+from ferrograd_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    names = set()
+    for fn in os.listdir(os.path.join(ROOT, "include")):
+        if not fn.endswith(".h"):
+            continue
+        text = open(os.path.join(ROOT, "include", fn)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"\b(fg_[a-z0-9_]+)\s*\(", text):
+            names.add(m.group(1))
+    return names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    declared = header_functions()
+    assert declared, "no declarations parsed"
+    missing = [n for n in sorted(declared) if not hasattr(lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+    # The Python binding covers exactly the declared surface.
+    assert declared == set(_lib.SIGNATURES), (
+        declared ^ set(_lib.SIGNATURES))
+
+
+def test_version_and_error_message():
+    lib = _lib.load()
+    assert lib.fg_version() >= 100
+    rc = lib.fg_sync(None)
+    assert rc == 1  # FG_ERR_INVALID_ARGUMENT
+    assert b"ctx is NULL" in lib.fg_last_error_msg()
+    with pytest.raises(fa.FgError) as e:
+        _lib.call("fg_upload", None, None, None, 4, 0)
+    assert e.value.code == 1
+
+
+def test_host_rng_is_deterministic_and_keyed():
+    a = fa.rng_normal(4, 7, (1000,))
+    b = fa.rng_normal(4, 7, (1000,))
+    c = fa.rng_normal(4, 8, (1000,))
+    assert np.array_equal(a, b) and not np.array_equal(a, c)
+    # Counter-based: a prefix of a longer fill is the shorter fill.
+    assert np.array_equal(fa.rng_normal(4, 7, (300000,))[:1000], a)
+
+
+def test_host_rng_distributions():
+    u = fa.rng_uniform(0, 1, (1 << 20,))
+    assert u.min() >= 0.0 and u.max() < 1.0
+    assert abs(u.mean() - 0.5) < 2e-3 and abs(u.var() - 1 / 12) < 2e-3
+    n = fa.rng_normal(1, 2, (1 << 20,), 0.0, 2.0).astype(np.float64)
+    assert abs(n.mean()) < 1e-2 and abs(n.std() - 2.0) < 1e-2
+    k = fa.rng_int(2, 3, (1 << 20,), 1000)
+    assert k.min() == 0 and k.max() == 999
+    counts = np.bincount(k, minlength=1000)
+    assert counts.min() > 800 and counts.max() < 1300
+    # Uniform lo/hi mapping (Kaiming-uniform bounds).
+    w = fa.rng_uniform(0, 5, (4096,), -0.5, 0.5)
+    assert w.min() >= -0.5 and w.max() < 0.5
+
+
+def test_context_without_gpu_reports_no_device():
+    torch = pytest.importorskip("torch")
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    with pytest.raises(fa.FgError) as e:
+        fa.Context(0)
+    assert e.value.code in (8, 4)

@@ -1,0 +1,399 @@
+"""GPU parity of every direct kernel entry point against the CPU oracle.
+
+Inputs are seeded; the HIP path runs through the C ABI (ferrograd_amd);
+torch tensors serve only as device memory.  Tolerances (BASELINE.json
+north_star): GEMM outputs max normwise relative error 1e-5*sqrt(K);
+elementwise / softmax / optimiser 1e-5; argmax and integer outputs
+bit-exact; SGD and Adam are held to bit-exactness, which their kernels are
+written to give.
+"""
+import math
+import sys
+
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import golden, normwise_rel
+
+pytestmark = pytest.mark.gpu
+
+f32 = np.float32
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def dev(a):
+    torch = _torch()
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    _torch().cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def note(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def empty(shape, dtype=None):
+    torch = _torch()
+    return torch.empty(shape, dtype=dtype or torch.float32, device="cuda")
+
+
+# ------------------------------------------------------------------ GEMM
+SHAPES = [(17, 33, 29), (64, 256, 784), (64, 10, 256), (300, 260, 100), (128, 1000, 512),
+          (512, 512, 512), (256, 2048, 64), (1, 1, 1)]
+
+
+def storage(layout, A, B):
+    """(A_stored, B_stored) for a logical C = A.B in the given layout."""
+    if layout == O.NN:
+        return A, B
+    if layout == O.NT:
+        return A, np.ascontiguousarray(B.T)
+    return np.ascontiguousarray(A.T), B
+
+
+def run_gemm(ctx, layout, A, B, bias=None, act=0, want_z=True):
+    M, K = A.shape
+    N = B.shape[1]
+    As, Bs = storage(layout, A, B)
+    dA, dB = dev(As), dev(Bs)
+    dC = empty((M, N))
+    dZ = empty((M, N)) if want_z else None
+    db = dev(bias) if bias is not None else None
+    ctx.gemm(layout, M, N, K, dA, As.shape[1], dB, Bs.shape[1], dC, N, bias=db, act=act,
+             Z=dZ, ldz=N)
+    return host(dC), (host(dZ) if want_z else None)
+
+
+@pytest.mark.parametrize("layout", [O.NN, O.NT, O.TN], ids=["NN", "NT", "TN"])
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("act", [O.ACT_NONE, O.ACT_RELU, O.ACT_GELU], ids=["none", "relu", "gelu"])
+def test_gemm_forward_parity(gpu_ctx, layout, shape, act):
+    M, N, K = shape
+    note(f"gemm fwd layout={layout} M={M} N={N} K={K} act={act}")
+    rng = np.random.default_rng(M * 7 + N * 13 + K + layout)
+    A = rng.standard_normal((M, K)).astype(f32)
+    B = rng.standard_normal((K, N)).astype(f32)
+    bias = (0.1 * rng.standard_normal(N)).astype(f32)
+    C, Z = run_gemm(gpu_ctx, layout, A, B, bias, act)
+    Zr, Hr = O.bias_act(O.gemm(O.NN, A, B), bias, act)
+    tol = 1e-5 * math.sqrt(K)
+    assert normwise_rel(Z, Zr) < tol
+    assert normwise_rel(C, Hr) < tol
+
+
+@pytest.mark.parametrize("layout", [O.NN, O.NT, O.TN], ids=["NN", "NT", "TN"])
+def test_gemm_bias_and_activation_exact_on_zero_product(gpu_ctx, layout):
+    """A = 0: the output is act(bias) per column, so a bias indexing slip
+    cannot hide under the GEMM tolerance."""
+    M, N, K = 70, 130, 36
+    note(f"gemm zero-product bias layout={layout}")
+    A = np.zeros((M, K), f32)
+    B = np.random.default_rng(1).standard_normal((K, N)).astype(f32)
+    bias = np.linspace(-2, 2, N).astype(f32)
+    for act in (O.ACT_NONE, O.ACT_RELU):
+        C, Z = run_gemm(gpu_ctx, layout, A, B, bias, act)
+        assert np.array_equal(Z, np.tile(bias, (M, 1)))
+        assert np.array_equal(C, np.tile(O.act(act, bias), (M, 1)))
+    C, _ = run_gemm(gpu_ctx, layout, A, B, bias, O.ACT_GELU)
+    assert np.max(np.abs(C - np.tile(O.act(O.ACT_GELU, bias), (M, 1)))) < 1e-6
+
+
+def test_gemm_k_zero_and_accumulate(gpu_ctx):
+    torch = _torch()
+    note("gemm K=0 and accumulate")
+    M, N = 40, 24
+    bias = np.arange(N, dtype=f32)
+    dC = empty((M, N))
+    dummy = empty((4,))
+    gpu_ctx.gemm(O.NN, M, N, 0, dummy, 1, dummy, N, dC, N, bias=dev(bias), act=O.ACT_RELU)
+    assert np.array_equal(host(dC), np.tile(bias, (M, 1)))
+    rng = np.random.default_rng(3)
+    A = rng.standard_normal((M, 50)).astype(f32)
+    B = rng.standard_normal((50, N)).astype(f32)
+    C0 = rng.standard_normal((M, N)).astype(f32)
+    dC = dev(C0)
+    gpu_ctx.gemm(O.NN, M, N, 50, dev(A), 50, dev(B), N, dC, N, accumulate=True)
+    assert normwise_rel(host(dC), C0 + O.gemm(O.NN, A, B)) < 1e-5 * math.sqrt(50)
+    del torch
+
+
+@pytest.mark.parametrize("layout", [O.NN, O.NT, O.TN], ids=["NN", "NT", "TN"])
+@pytest.mark.parametrize("act", [O.ACT_NONE, O.ACT_RELU, O.ACT_GELU], ids=["none", "relu", "gelu"])
+def test_gemm_backward_epilogue_parity(gpu_ctx, layout, act):
+    """C = (op(A).op(B)) * act'(Zs): the dA GEMM with the upstream activation
+    derivative fused in."""
+    M, N, K = 200, 136, 300
+    note(f"gemm bwd layout={layout} act={act}")
+    rng = np.random.default_rng(11 + layout * 3 + act)
+    A = rng.standard_normal((M, K)).astype(f32)
+    B = rng.standard_normal((K, N)).astype(f32)
+    Zs = rng.standard_normal((M, N)).astype(f32)
+    As, Bs = storage(layout, A, B)
+    dC = empty((M, N))
+    gpu_ctx.gemm_bwd(layout, M, N, K, dev(As), As.shape[1], dev(Bs), Bs.shape[1], dC, N, act=act,
+                     Zs=dev(Zs), ldzs=N)
+    ref = O.act_bwd(act, O.gemm(O.NN, A, B), Zs)
+    assert normwise_rel(host(dC), ref) < 1e-5 * math.sqrt(K)
+
+
+def test_gemm_c2_full_size_sampled(gpu_ctx):
+    """Config 2 at its real shape, 4096^3: forward NN + bias + ReLU, dA (NT
+    with the ReLU mask) and dB (TN), checked on 48 sampled rows against
+    float64 dot products."""
+    torch = _torch()
+    n = 4096
+    note("gemm c2 4096^3 sampled")
+    g = torch.Generator(device="cuda").manual_seed(1)
+    dA = torch.randn((n, n), device="cuda", generator=g)
+    dB = torch.randn((n, n), device="cuda", generator=g)
+    dbias = 0.1 * torch.randn((n,), device="cuda", generator=g)
+    dG = torch.randn((n, n), device="cuda", generator=g)
+    dC, dZ, dX, dW = (empty((n, n)) for _ in range(4))
+    gpu_ctx.gemm(O.NN, n, n, n, dA, n, dB, n, dC, n, bias=dbias, act=O.ACT_RELU, Z=dZ, ldz=n)
+    gpu_ctx.gemm_bwd(O.NT, n, n, n, dG, n, dB, n, dX, n, act=O.ACT_RELU, Zs=dZ, ldzs=n)
+    gpu_ctx.gemm_bwd(O.TN, n, n, n, dA, n, dG, n, dW, n)
+    rows = np.random.default_rng(5).choice(n, 48, replace=False)
+    A, B, bias, G = host(dA), host(dB), host(dbias), host(dG)
+    A64, B64, G64 = A.astype(np.float64), B.astype(np.float64), G.astype(np.float64)
+    tol = 1e-5 * math.sqrt(n)
+    Zr = A64[rows] @ B64 + bias
+    Z = host(dZ)[rows]
+    assert normwise_rel(Z, Zr) < tol
+    assert normwise_rel(host(dC)[rows], np.maximum(Zr, 0)) < tol
+    mask = host(dZ)[rows] > 0
+    Xr = (G64[rows] @ B64.T) * mask
+    assert normwise_rel(host(dX)[rows], Xr) < tol
+    Wr = A64[:, rows].T @ G64      # rows of dW = A^T . G
+    assert normwise_rel(host(dW)[rows], Wr) < tol
+
+
+# ----------------------------------------------------- bias grad, act bwd
+@pytest.mark.parametrize("shape", [(2048, 4096), (64, 10), (1, 5), (1000, 1000), (3, 4097),
+                                   (4096, 1000)], ids=lambda s: "x".join(map(str, s)))
+def test_bias_grad_parity(gpu_ctx, shape):
+    M, N = shape
+    note(f"bias_grad M={M} N={N}")
+    dZ = np.random.default_rng(M + N).standard_normal((M, N)).astype(f32)
+    out = empty((N,))
+    gpu_ctx.bias_grad(M, N, dev(dZ), N, out)
+    ref = O.bias_grad(dZ)
+    assert normwise_rel(host(out), ref) < 1e-5
+    # accumulate
+    gpu_ctx.bias_grad(M, N, dev(dZ), N, out, accumulate=True)
+    assert normwise_rel(host(out), 2 * ref.astype(np.float64)) < 1e-5
+
+
+@pytest.mark.parametrize("n", [1, 7, 4096, 1000003])
+def test_act_bwd_parity(gpu_ctx, n):
+    note(f"act_bwd n={n}")
+    rng = np.random.default_rng(n)
+    dH = rng.standard_normal(n).astype(f32)
+    Z = (3 * rng.standard_normal(n)).astype(f32)
+    out = empty((n,))
+    gpu_ctx.act_bwd(O.ACT_RELU, n, dev(dH), dev(Z), out)
+    assert np.array_equal(host(out), O.act_bwd(O.ACT_RELU, dH, Z))
+    gpu_ctx.act_bwd(O.ACT_GELU, n, dev(dH), dev(Z), out)
+    ref = O.act_bwd(O.ACT_GELU, dH, Z)
+    assert np.max(np.abs(host(out) - ref) / np.maximum(np.abs(ref), 1.0)) < 1e-5
+
+
+# --------------------------------------------------------- softmax + CE
+def check_softmax_ce(ctx, x, labels, scale=1.0):
+    torch = _torch()
+    R, C = x.shape
+    dx, dl = dev(x), dev(labels.astype(np.uint32).view(np.int32))
+    loss, mean, dlog = empty((R,)), empty((1,)), empty((R, C))
+    am = empty((R,), torch.int32)
+    ctx.softmax_ce(dx, C, dl, R, C, scale, row_loss=loss, mean_loss=mean, dlogits=dlog, ldd=C,
+                   argmax=am)
+    rl, d, a, m = O.softmax_ce(x, labels.astype(np.uint32), scale)
+    assert np.array_equal(host(am).view(np.uint32), a)
+    got = host(loss)
+    assert np.max(np.abs(got - rl) / np.maximum(np.abs(rl), 1.0)) < 1e-5
+    assert normwise_rel(host(dlog), d) < 1e-5
+    assert abs(float(host(mean)[0]) - m) <= 1e-5 * max(1.0, abs(m))
+
+
+def test_softmax_ce_fixture(gpu_ctx):
+    note("softmax_ce fixture 9x37")
+    g = golden("softmax_ce_9x37.npz")
+    check_softmax_ce(gpu_ctx, g["x"], g["labels"])
+
+
+@pytest.mark.parametrize("shape", [(64, 10), (7, 1024), (2048, 1000), (256, 32000), (16, 40000),
+                                   (33, 4100), (5, 8192)], ids=lambda s: "x".join(map(str, s)))
+def test_softmax_ce_parity(gpu_ctx, shape):
+    R, C = shape
+    note(f"softmax_ce R={R} C={C}")
+    rng = np.random.default_rng(R * C)
+    x = (2 * rng.standard_normal((R, C))).astype(f32)
+    x[0, C // 3] = x[0, C // 2] = 50.0   # tie: argmax must be the first
+    labels = rng.integers(0, C, R)
+    check_softmax_ce(gpu_ctx, x, labels, scale=1.0)
+    check_softmax_ce(gpu_ctx, x, labels, scale=1.0 / R)
+
+
+def test_softmax_ce_c3_full_size(gpu_ctx):
+    """Config 3 at its real shape: logits [8192, 32000] ~ N(0, 2^2), seed 2."""
+    torch = _torch()
+    R, C = 8192, 32000
+    note("softmax_ce c3 8192x32000")
+    x = empty((R, C))
+    lab = empty((R,), torch.int32)
+    gpu_ctx.rng_normal(2, 0, 0.0, 2.0, x, R * C)
+    gpu_ctx.rng_int(2, 1, C, lab, R)
+    check_softmax_ce(gpu_ctx, host(x), host(lab).view(np.uint32))
+
+
+def test_softmax_and_backward(gpu_ctx):
+    note("softmax / softmax_bwd")
+    # std_wgsl.rs:97-187 closed form: uniform rows of 64 -> 1/64, backward 0.
+    x = np.full((16, 64), 5.0, f32)
+    y = empty((16, 64))
+    gpu_ctx.softmax(dev(x), 16, 64, y)
+    yh = host(y)
+    assert np.all(yh == f32(1 / 64))
+    dx = empty((16, 64))
+    gpu_ctx.softmax_bwd(y, dev(np.ones((16, 64), f32)), 16, 64, dx)
+    assert np.all(host(dx) == 0.0)
+    rng = np.random.default_rng(4)
+    for (R, C) in [(33, 1000), (3, 37), (2, 40000)]:
+        x = rng.standard_normal((R, C)).astype(f32)
+        dy = rng.standard_normal((R, C)).astype(f32)
+        y = empty((R, C))
+        gpu_ctx.softmax(dev(x), R, C, y)
+        assert normwise_rel(host(y), O.softmax(x)) < 1e-5
+        dx = empty((R, C))
+        gpu_ctx.softmax_bwd(y, dev(dy), R, C, dx)
+        assert normwise_rel(host(dx), O.softmax_bwd(host(y), dy)) < 1e-5
+
+
+# ------------------------------------------------------------ optimisers
+SIZES = [1, 3, 4096, 4097, 100003, 262144]
+
+
+def make_list(rng, sizes, misalign):
+    """Host arrays plus device tensors; misalign shifts every device tensor
+    by one float so the 16-byte path is not taken."""
+    torch = _torch()
+    hs, ds = [], []
+    for n in sizes:
+        h = rng.standard_normal(n).astype(f32)
+        base = torch.empty(n + 1, dtype=torch.float32, device="cuda")
+        d = base[1:] if misalign else base[:n]
+        d.copy_(torch.from_numpy(h))
+        hs.append(h)
+        ds.append(d)
+    return hs, ds
+
+
+@pytest.mark.parametrize("misalign", [False, True], ids=["aligned", "misaligned"])
+def test_sgd_multi_tensor_bit_exact(gpu_ctx, misalign):
+    import ferrograd_amd as fa
+    note(f"sgd multi-tensor misalign={misalign}")
+    rng = np.random.default_rng(21)
+    W, dW = make_list(rng, SIZES, misalign)
+    G, dG = make_list(rng, SIZES, misalign)
+    mt = fa.MultiTensor(gpu_ctx, dW, dG)
+    lr = f32(0.01)
+    mt.sgd(float(lr), zero_grad=True)
+    for w, g, dw, dg in zip(W, G, dW, dG):
+        O.sgd_(w, g, lr, True)
+        assert np.array_equal(host(dw), w)
+        assert np.all(host(dg) == 0)
+    mt.close()
+
+
+@pytest.mark.parametrize("misalign", [False, True], ids=["aligned", "misaligned"])
+def test_adam_multi_tensor_bit_exact_10_steps(gpu_ctx, misalign):
+    import ferrograd_amd as fa
+    torch = _torch()
+    note(f"adam multi-tensor misalign={misalign}")
+    rng = np.random.default_rng(22)
+    P, dP = make_list(rng, SIZES, misalign)
+    G, dG = make_list(rng, SIZES, misalign)
+    Mh = [np.zeros_like(p) for p in P]
+    Vh = [np.zeros_like(p) for p in P]
+    dM = [torch.zeros_like(d) for d in dP]
+    dV = [torch.zeros_like(d) for d in dP]
+    if misalign:
+        dM = [torch.zeros(d.numel() + 1, device="cuda")[1:] for d in dP]
+        dV = [torch.zeros(d.numel() + 1, device="cuda")[1:] for d in dP]
+    mt = fa.MultiTensor(gpu_ctx, dP, dG, dM, dV)
+    b1, b2, eps, lr = f32(0.9), f32(0.999), f32(1e-8), f32(1e-3)
+    for step in range(1, 11):
+        for h, d in zip(G, dG):
+            h[:] = (1e-3 * rng.standard_normal(h.size)).astype(f32)
+            d.copy_(torch.from_numpy(h))
+        mt.adam(float(lr), float(b1), float(b2), float(eps), step)
+        s, r = O.adam_scalars(lr, b1, b2, step)
+        for p, g, m, v in zip(P, G, Mh, Vh):
+            O.adam_(p, g, m, v, b1, b2, eps, s, r)
+    for p, m, v, dp, dm, dv in zip(P, Mh, Vh, dP, dM, dV):
+        assert np.array_equal(host(dp), p)
+        assert np.array_equal(host(dm), m)
+        assert np.array_equal(host(dv), v)
+    mt.close()
+
+
+def test_adam_c4_full_size_sampled(gpu_ctx):
+    """Config 4 at its real shape: 64 tensors x 4 Mi parameters, 10 steps
+    with fresh N(0, 1e-3^2) grads (device generator), bit-exact against the
+    oracle on a sample of 4 tensors."""
+    import ferrograd_amd as fa
+    torch = _torch()
+    note("adam c4 64x4Mi 10 steps (sampled)")
+    nt, n = 64, 4 * 1024 * 1024
+    P = [empty((n,)) for _ in range(nt)]
+    G = [empty((n,)) for _ in range(nt)]
+    M = [torch.zeros(n, device="cuda") for _ in range(nt)]
+    V = [torch.zeros(n, device="cuda") for _ in range(nt)]
+    for i, p in enumerate(P):
+        gpu_ctx.rng_normal(3, i, 0.0, 0.02, p, n)
+    sample = [0, 21, 42, 63]
+    hp = {i: host(P[i]).copy() for i in sample}
+    hm = {i: np.zeros(n, f32) for i in sample}
+    hv = {i: np.zeros(n, f32) for i in sample}
+    mt = fa.MultiTensor(gpu_ctx, P, G, M, V)
+    b1, b2, eps, lr = f32(0.9), f32(0.999), f32(1e-8), f32(1e-3)
+    for step in range(1, 11):
+        for i, g in enumerate(G):
+            gpu_ctx.rng_normal(3, 1000 * step + i, 0.0, 1e-3, g, n)
+        hg = {i: host(G[i]) for i in sample}
+        mt.adam(float(lr), float(b1), float(b2), float(eps), step)
+        s, r = O.adam_scalars(lr, b1, b2, step)
+        for i in sample:
+            O.adam_(hp[i], hg[i], hm[i], hv[i], b1, b2, eps, s, r)
+    for i in sample:
+        assert np.array_equal(host(P[i]), hp[i]), i
+        assert np.array_equal(host(M[i]), hm[i]), i
+        assert np.array_equal(host(V[i]), hv[i]), i
+    mt.close()
+
+
+def test_device_rng_matches_host(gpu_ctx):
+    import ferrograd_amd as fa
+    torch = _torch()
+    note("device rng vs host rng")
+    n = 100000
+    x = empty((n,))
+    gpu_ctx.rng_uniform(9, 4, -1.0, 1.0, x, n)
+    assert np.array_equal(host(x), fa.rng_uniform(9, 4, (n,), -1.0, 1.0))
+    k = empty((n,), torch.int32)
+    gpu_ctx.rng_int(9, 5, 1000, k, n)
+    assert np.array_equal(host(k).view(np.uint32), fa.rng_int(9, 5, (n,), 1000))
+    gpu_ctx.rng_normal(9, 6, 0.0, 1.0, x, n)
+    # Box-Muller in double: device and host libm may differ in the last
+    # double ulp, which almost never survives rounding to fp32.
+    hx = fa.rng_normal(9, 6, (n,))
+    assert np.mean(host(x) == hx) > 0.999
+    assert np.max(np.abs(host(x) - hx)) < 1e-5
