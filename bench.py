@@ -216,8 +216,7 @@ def main() -> int:
     import ferrograd_amd as fa
     from ferrograd_amd.mlp import MLPTrainStep
 
-    torch.cuda.init()
-    ctx = fa.Context(0, torch.cuda.current_stream().cuda_stream)
+    ctx, _stream = fa.torch_context(0)
     log(f"device {ctx.arch}, {ctx.cu_count} CUs")
     dims = [1024] + [4096] * 7 + [1000]
     batch = 2048
@@ -289,7 +288,13 @@ def main() -> int:
             "loss_rel": abs(first["mean_loss"] - ref["mean_loss"]) / max(1.0, abs(ref["mean_loss"])),
             "dW_max_rel": max(rel(a, b) for a, b in zip(first["dW"], ref["dW"])),
             "db_max_rel": max(rel(a, b) for a, b in zip(first["db"], ref["db"])),
-            "W_after_adam_max_rel": max(rel(a, b) for a, b in zip(first["W"], ref["params"][0::2])),
+            # Adam's first step is p - lr*g/(|g|+eps), i.e. nearly -lr*sign(g):
+            # where a gradient entry is within rounding noise of zero its sign
+            # (and so a 2*lr step) can differ, so report the fraction of
+            # parameters off by more than 1e-5 relative.
+            "W_after_adam_mismatch_frac": float(np.mean(np.concatenate([
+                (np.abs(a.astype(np.float64) - b) > 1e-5 * np.max(np.abs(b))).ravel()
+                for a, b in zip(first["W"], ref["params"][0::2])]))),
             "tolerance_gemm": 1e-5 * math.sqrt(4096),
         }
         log("parity vs CPU: " + json.dumps(parity))

@@ -29,7 +29,7 @@ ACT_NONE, ACT_RELU, ACT_GELU = 0, 1, 2
 
 __all__ = [
     "NN", "NT", "TN", "ACT_NONE", "ACT_RELU", "ACT_GELU", "FgError", "Context",
-    "MultiTensor", "load", "rng_uniform", "rng_normal", "rng_int",
+    "MultiTensor", "load", "rng_uniform", "rng_normal", "rng_int", "torch_context",
 ]
 
 
@@ -131,6 +131,21 @@ class Context:
 
     def rng_int(self, seed, tensor_id, bound, dst, n) -> None:
         call("fg_rng_int_dev", self.handle, seed, tensor_id, bound, _ptr(dst), n)
+
+
+def torch_context(device: int = 0):
+    """A Context sharing a fresh default-priority torch stream, made current.
+
+    torch's default stream has the handle 0, which fg_ctx_create reads as
+    "create a private stream"; binding an explicit stream instead keeps
+    torch ops (allocation, copies, events) and library launches in one
+    ordered queue.  Returns (context, torch stream)."""
+    import torch
+
+    torch.cuda.init()
+    s = torch.cuda.Stream(device)
+    torch.cuda.set_stream(s)
+    return Context(device, s.cuda_stream), s
 
 
 class MultiTensor:

@@ -15,10 +15,9 @@
 // written per parameter; SGD: 8 B read + 4-8 B written), with 16-byte
 // non-temporal accesses -- the kernels are HBM-bound.
 //
-// Arithmetic is written with explicit round-to-nearest intrinsics and this
-// unit is compiled with -ffp-contract=off, so each element goes through
-// exactly the fp32 operation sequence of the CPU restatement (bit-exact
-// parity).
+// This unit is compiled with -ffp-contract=off and uses only correctly
+// rounded operations, so each element goes through exactly the fp32
+// operation sequence of the CPU restatement (bit-exact parity).
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -57,13 +56,16 @@ __device__ inline void st_nt(float *p, f32x4 v) {
 
 // m = b1*m + (1-b1)*g ; v = b2*v + (1-b2)*(g*g) ;
 // p = p - (step_size*m) / (sqrt(v)*inv_sqrt_bc2 + eps)
+// Plain operators: this unit is compiled without contraction, and HIP's
+// sqrtf and '/' are correctly rounded (the __fsqrt_rn intrinsic is not: it
+// maps to the hardware approximation).
 __device__ inline void adam_elem(float &p, float g, float &m, float &v, float b1,
                                  float omb1, float b2, float omb2, float eps,
                                  float step_size, float inv_sqrt_bc2) {
-    const float mi = __fadd_rn(__fmul_rn(b1, m), __fmul_rn(omb1, g));
-    const float vi = __fadd_rn(__fmul_rn(b2, v), __fmul_rn(omb2, __fmul_rn(g, g)));
-    const float denom = __fadd_rn(__fmul_rn(__fsqrt_rn(vi), inv_sqrt_bc2), eps);
-    p = __fsub_rn(p, __fdiv_rn(__fmul_rn(step_size, mi), denom));
+    const float mi = b1 * m + omb1 * g;
+    const float vi = b2 * v + omb2 * (g * g);
+    const float denom = sqrtf(vi) * inv_sqrt_bc2 + eps;
+    p = p - (step_size * mi) / denom;
     m = mi;
     v = vi;
 }
@@ -74,7 +76,7 @@ __global__ __launch_bounds__(kThreads) void adam_mt_kernel(
     const MTChunk c = chunks[blockIdx.x];
     const MTTensor t = tensors[c.tensor];
     const uint64_t end = (c.start + kChunk < t.n) ? c.start + kChunk : t.n;
-    const float omb1 = __fsub_rn(1.0f, b1), omb2 = __fsub_rn(1.0f, b2);
+    const float omb1 = 1.0f - b1, omb2 = 1.0f - b2;
     if (vec) {
         f32x4 P[kUnroll], G[kUnroll], M[kUnroll], V[kUnroll];
         uint64_t idx[kUnroll];
@@ -150,19 +152,19 @@ __global__ __launch_bounds__(kThreads) void sgd_mt_kernel(const MTTensor *__rest
         for (int u = 0; u < kUnroll; ++u) {
             if (idx[u] + 4 <= end) {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) W[u][e] = __fsub_rn(W[u][e], __fmul_rn(G[u][e], lr));
+                for (int e = 0; e < 4; ++e) W[u][e] = W[u][e] - G[u][e] * lr;
                 st_nt(t.p + idx[u], W[u]);
                 if (zero_grad) st_nt(t.g + idx[u], f32x4{0.f, 0.f, 0.f, 0.f});
             } else {
                 for (uint64_t i = idx[u]; i < end && i < idx[u] + 4; ++i) {
-                    t.p[i] = __fsub_rn(t.p[i], __fmul_rn(t.g[i], lr));
+                    t.p[i] = t.p[i] - t.g[i] * lr;
                     if (zero_grad) t.g[i] = 0.0f;
                 }
             }
         }
     } else {
         for (uint64_t i = c.start + threadIdx.x; i < end; i += kThreads) {
-            t.p[i] = __fsub_rn(t.p[i], __fmul_rn(t.g[i], lr));
+            t.p[i] = t.p[i] - t.g[i] * lr;
             if (zero_grad) t.g[i] = 0.0f;
         }
     }

@@ -42,8 +42,7 @@ def gpu_ctx():
         pytest.skip("no GPU")
     import ferrograd_amd as fa
 
-    torch.cuda.init()
-    ctx = fa.Context(0, torch.cuda.current_stream().cuda_stream)
+    ctx, _stream = fa.torch_context(0)
     yield ctx
     ctx.sync()
     ctx.close()
