@@ -27,6 +27,8 @@ SOURCES = [
     "k_gemm_nn.hip",
     "k_gemm_nt.hip",
     "k_gemm_tn.hip",
+    "k_eltwise_prog.hip",
+    "fg_graph.cpp",
 ]
 
 # Packed-fp32 VALU instructions are disabled for all device code: some of

@@ -56,6 +56,33 @@ SIGNATURES = {
     "fg_sgd_step": (i32, [vp, vp, f32, i32]),
     "fg_adam_step": (i32, [vp, vp, f32, f32, f32, f32, i32, i32]),
     "fg_adam_step_scalars": (i32, [vp, vp, f32, f32, f32, f32, f32, i32]),
+    "fg_memcpy_h2d": (i32, [vp, vp, vp, u64]),
+    "fg_memcpy_d2h": (i32, [vp, vp, vp, u64]),
+    "fg_graph_create": (i32, [i32, i32, pvp]),
+    "fg_graph_destroy": (i32, [vp]),
+    "fg_graph_new_field": (i32, [vp, ctypes.POINTER(u32)]),
+    "fg_graph_input": (i32, [vp, vp, i32, ctypes.POINTER(u32)]),
+    "fg_graph_constant_f32": (i32, [vp, f32, ctypes.POINTER(u32)]),
+    "fg_graph_op": (i32, [vp, i32, vp, i32, ctypes.POINTER(u32)]),
+    "fg_graph_set_input_flags": (i32, [vp, u32, u32]),
+    "fg_graph_num_nodes": (i32, [vp, ctypes.POINTER(u32)]),
+    "fg_graph_validate": (i32, [vp, vp, i32]),
+    "fg_plan_create": (i32, [vp, vp, vp, i32, pvp]),
+    "fg_plan_destroy": (i32, [vp]),
+    "fg_plan_count": (i32, [vp, i32, ctypes.POINTER(i32)]),
+    "fg_plan_tensor": (i32, [vp, i32, i32, pvp, ctypes.POINTER(u64), ctypes.POINTER(u32)]),
+    "fg_plan_bind_input": (i32, [vp, i32, vp, u64]),
+    "fg_plan_bind_target": (i32, [vp, vp, u64]),
+    "fg_plan_set_lr": (i32, [vp, f32]),
+    "fg_plan_set_adam": (i32, [vp, f32, f32, f32]),
+    "fg_plan_forward": (i32, [vp]),
+    "fg_plan_loss": (i32, [vp]),
+    "fg_plan_backward": (i32, [vp]),
+    "fg_plan_optim": (i32, [vp]),
+    "fg_plan_single_optim": (i32, [vp, i32]),
+    "fg_plan_capture_step": (i32, [vp]),
+    "fg_plan_launch_step": (i32, [vp]),
+    "fg_plan_describe": (i32, [vp, cp, sz, ctypes.POINTER(sz)]),
     "fg_rng_uniform_host": (i32, [u64, u64, f32, f32, vp, u64]),
     "fg_rng_normal_host": (i32, [u64, u64, f32, f32, vp, u64]),
     "fg_rng_int_host": (i32, [u64, u64, u32, vp, u64]),

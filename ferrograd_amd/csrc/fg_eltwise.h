@@ -1,0 +1,68 @@
+// fg_eltwise.h -- elementwise program: a tiny register machine evaluated per
+// element by one kernel launch.  The planner compiles fused chains of
+// ferrograd-nn elementwise ops (forward and backward) and the MSE / BCE /
+// CE-on-probabilities losses into these programs, so arbitrary chains run
+// as single launches from ahead-of-time code (the reference instead emits a
+// new HIP source per fused kernel and compiles it with hipRTC,
+// rocm/generate.rs:17-70).
+#pragma once
+
+#include <cstdint>
+
+namespace fg {
+
+enum EltOp : uint8_t {
+    kEltLoad = 0,   // r[dst] = src[a] at the element (mode of src a)
+    kEltImm,        // r[dst] = imm
+    kEltStore,      // dsts[a][i] = r[b]
+    kEltAccum,      // dsts[a][i] += r[b]
+    kEltAdd,        // r[dst] = r[a] + r[b]
+    kEltSub,
+    kEltMul,
+    kEltDiv,
+    kEltNeg,        // r[dst] = -r[a]
+    kEltRelu,
+    kEltGelu,
+    kEltElu,        // x >= 0 ? x : exp(x) - 1   (unary.rs:329-434)
+    kEltTanh,
+    kEltExp,
+    kEltLog,
+    kEltAbs,
+    kEltReluD,      // [x > 0]
+    kEltGeluD,      // d gelu / dx
+    kEltEluD,       // x >= 0 ? 1 : exp(x)
+    kEltSign,       // x > 0 ? 1 : (x < 0 ? -1 : 0)
+    kEltLabelEq,    // r[dst] = (col == labels[row]) ? 1 : 0
+    kEltSelect,     // r[dst] = r[a] != 0 ? r[b] : r[c]
+    kEltMax,        // r[dst] = max(r[a], r[b])
+};
+
+// Source addressing modes.
+enum EltMode : uint8_t {
+    kModeFull = 0,  // src[i]
+    kModeRow = 1,   // src[i % cols]   (row-broadcast bias vector)
+    kModeScalar = 2 // src[0]
+};
+
+constexpr int kEltMaxInstr = 64;
+constexpr int kEltMaxSrc = 12;
+constexpr int kEltMaxDst = 8;
+constexpr int kEltRegs = 16;
+
+struct EltInstr {
+    uint8_t op, dst, a, b, c, pad[3];
+    float imm;
+};
+
+struct EltProgram {
+    const float *src[kEltMaxSrc];
+    float *dst[kEltMaxDst];
+    const uint32_t *labels;
+    uint64_t n;     // elements
+    uint32_t cols;  // row length (for row-broadcast and labels)
+    uint8_t src_mode[kEltMaxSrc];
+    int32_t n_instr;
+    EltInstr ins[kEltMaxInstr];
+};
+
+}  // namespace fg

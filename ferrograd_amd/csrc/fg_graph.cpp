@@ -1,0 +1,1532 @@
+// fg_graph.cpp -- graph IR, lowering / fusion planner and plan executor.
+//
+// Replaces, behind the C ABI, the reference's graph compiler and runtime
+// for the fused training path:
+//   * graph IR and SaveIndicators: crates/fused_gpu/src/dispatch/backend/
+//     mod.rs:499-1316 (Node, GraphOp, validate, compute_saved_nodes);
+//   * lowering: kernel/{forward,backward,loss,optim}.rs driven by
+//     kernel/mod.rs:107-152 -- which emits one generated kernel per root and
+//     re-inlines elementwise chains into every consumer;
+//   * buffers and scheduling: dispatch/mod.rs:509-845 and the hipGraph
+//     capture of rocm/mod.rs:268-389.
+//
+// Lowering here pattern-matches the graph onto the hand-written gfx950
+// kernels instead of generating code:
+//   * matmul [-> bias add] [-> relu|gelu] becomes ONE GEMM launch whose
+//     epilogue adds the bias, applies the activation and also stores the
+//     pre-activation (kept for backward);
+//   * runs of elementwise nodes of one shape become ONE elementwise-program
+//     launch (fg_eltwise.h) that reads each external input once and writes
+//     every node value;
+//   * softmax followed by the CE loss becomes ONE fused softmax+CE launch
+//     writing dlogits = p - onehot directly;
+//   * backward is planned statically in reverse node order; the activation
+//     derivative of a layer is fused into the epilogue of the dA GEMM of the
+//     layer above (dZ_prev = (dZ W^T) * act'(Z_prev)), bias gradients are
+//     column reductions, and every optimiser update is one multi-tensor
+//     launch.
+// All plan-owned tensors live in one 256-byte-aligned device arena.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "fg_eltwise.h"
+#include "fg_internal.h"
+
+namespace {
+
+constexpr int kNone = -1;
+
+bool is_unary(int op) {
+    switch (op) {
+        case FG_OP_RELU: case FG_OP_GELU: case FG_OP_ELU: case FG_OP_TANH:
+        case FG_OP_EXP: case FG_OP_LOG: case FG_OP_ABS: case FG_OP_NEG:
+            return true;
+        default:
+            return false;
+    }
+}
+bool is_binary_elt(int op) {
+    return op == FG_OP_ADD || op == FG_OP_SUB || op == FG_OP_MUL || op == FG_OP_DIV ||
+           op == FG_OP_BIAS_ADD;
+}
+bool is_elementwise(int op) { return is_unary(op) || is_binary_elt(op); }
+int arity(int op) {
+    if (op == FG_OP_INPUT || op == FG_OP_CONST) return 0;
+    if (is_unary(op) || op == FG_OP_SOFTMAX) return 1;
+    return 2;
+}
+
+const char *op_name(int op) {
+    static const char *names[] = {"input", "const", "add",  "sub", "mul",  "div",
+                                  "matmul", "relu", "gelu", "elu", "tanh", "exp",
+                                  "log",   "abs",   "neg",  "softmax", "bias_add"};
+    return (op >= 0 && op <= FG_OP_BIAS_ADD) ? names[op] : "?";
+}
+
+// SaveIndicator flags (kernel/mod.rs:41-93).
+constexpr uint32_t kDefFwd = 1u, kDefBwd = 2u;
+
+struct GNode {
+    int op = FG_OP_INPUT;
+    std::vector<uint32_t> in;
+    std::vector<uint32_t> fields;  // Input: meta field per dim
+    float value = 0.0f;            // Const
+    uint32_t flags = 0;            // Input flags
+};
+
+struct Shape {
+    bool scalar = false;
+    bool vector = false;  // rank 1
+    int64_t rows = 1, cols = 1;
+    int64_t numel() const { return scalar ? 1 : rows * cols; }
+};
+
+}  // namespace
+
+struct fg_graph {
+    int loss = FG_LOSS_MSE;
+    int optim = FG_OPTIM_SGD;
+    uint32_t nfields = 0;
+    std::vector<GNode> nodes;
+};
+
+namespace {
+
+// --------------------------------------------------------- shape checks
+int infer_shapes(const fg_graph &g, const uint32_t *meta, int n_meta, std::vector<Shape> &sh) {
+    const size_t n = g.nodes.size();
+    FG_REQUIRE(n > 0, FG_ERR_GRAPH, "graph has no nodes");
+    FG_REQUIRE(n_meta >= (int)g.nfields + 1, FG_ERR_GRAPH,
+               "metadata has %d fields, graph declares %u dims (+1 for lr)", n_meta, g.nfields);
+    sh.assign(n, Shape{});
+    for (size_t i = 0; i < n; ++i) {
+        const GNode &nd = g.nodes[i];
+        Shape s;
+        switch (nd.op) {
+            case FG_OP_INPUT: {
+                FG_REQUIRE(!nd.fields.empty(), FG_ERR_GRAPH, "input %zu has rank 0", i);
+                int64_t rows = 1;
+                for (size_t d = 0; d < nd.fields.size(); ++d) {
+                    const uint32_t f = nd.fields[d];
+                    FG_REQUIRE(f >= 1 && f < (uint32_t)n_meta, FG_ERR_GRAPH,
+                               "input %zu: missing metadata field %u", i, f);
+                    FG_REQUIRE(meta[f] > 0, FG_ERR_SHAPE, "input %zu: dim %zu is 0", i, d);
+                    if (d + 1 < nd.fields.size()) rows *= meta[f];
+                }
+                s.rows = rows;
+                s.cols = meta[nd.fields.back()];
+                s.vector = nd.fields.size() == 1;
+                break;
+            }
+            case FG_OP_CONST:
+                s.scalar = true;
+                break;
+            case FG_OP_MATMUL: {
+                const Shape &a = sh[nd.in[0]], &b = sh[nd.in[1]];
+                FG_REQUIRE(!a.scalar && !b.scalar && !a.vector && !b.vector, FG_ERR_SHAPE,
+                           "matmul %zu: operands must be matrices", i);
+                FG_REQUIRE(a.cols == b.rows, FG_ERR_SHAPE,
+                           "matmul %zu: inner dims differ (%lld vs %lld)", i,
+                           (long long)a.cols, (long long)b.rows);
+                s.rows = a.rows;
+                s.cols = b.cols;
+                break;
+            }
+            case FG_OP_SOFTMAX: {
+                const Shape &a = sh[nd.in[0]];
+                FG_REQUIRE(!a.scalar, FG_ERR_SHAPE, "softmax %zu of a scalar", i);
+                s = a;
+                break;
+            }
+            default: {
+                if (is_unary(nd.op)) {
+                    FG_REQUIRE(!sh[nd.in[0]].scalar, FG_ERR_SHAPE, "%s %zu of a scalar",
+                               op_name(nd.op), i);
+                    s = sh[nd.in[0]];
+                    break;
+                }
+                const Shape &a = sh[nd.in[0]], &b = sh[nd.in[1]];
+                FG_REQUIRE(!(a.scalar && b.scalar), FG_ERR_SHAPE,
+                           "%s %zu: both operands are constants", op_name(nd.op), i);
+                if (nd.op == FG_OP_BIAS_ADD) {
+                    FG_REQUIRE(!a.scalar && b.vector && b.cols == a.cols, FG_ERR_SHAPE,
+                               "bias_add %zu: needs x[..., N] + b[N]", i);
+                    s = a;
+                } else if (a.scalar) {
+                    s = b;
+                } else if (b.scalar) {
+                    s = a;
+                } else if (a.rows == b.rows && a.cols == b.cols && a.vector == b.vector) {
+                    s = a;
+                } else if (b.vector && b.cols == a.cols) {
+                    s = a;  // row broadcast of b
+                } else if (a.vector && a.cols == b.cols) {
+                    s = b;  // row broadcast of a
+                } else {
+                    fg::set_error("%s %zu: shapes [%lld,%lld] and [%lld,%lld] do not match",
+                                  op_name(nd.op), i, (long long)a.rows, (long long)a.cols,
+                                  (long long)b.rows, (long long)b.cols);
+                    return FG_ERR_SHAPE;
+                }
+            }
+        }
+        sh[i] = s;
+    }
+    const int last_op = g.nodes.back().op;
+    FG_REQUIRE(last_op != FG_OP_INPUT && last_op != FG_OP_CONST, FG_ERR_GRAPH,
+               "the last node must be an operation");
+    return FG_OK;
+}
+
+// ---------------------------------------------------------------- plan
+enum LaunchKind {
+    LK_GEMM,
+    LK_GEMM_BWD,
+    LK_BIAS_GRAD,
+    LK_SOFTMAX,
+    LK_SOFTMAX_BWD,
+    LK_ELT,
+    LK_SMCE,
+    LK_FILL0,
+};
+
+struct Launch {
+    int kind = LK_GEMM;
+    int layout = FG_NN, M = 0, N = 0, K = 0, lda = 0, ldb = 0, ldc = 0, ldz = 0;
+    int act = FG_ACT_NONE, accumulate = 0;
+    int sA = kNone, sB = kNone, sC = kNone, sZ = kNone, sBias = kNone, sExtra = kNone;
+    fg::EltProgram prog{};
+    int src_slot[fg::kEltMaxSrc];
+    int dst_slot[fg::kEltMaxDst];
+    int label_slot = kNone;
+    uint64_t count = 0;
+    std::string desc;
+    Launch() {
+        std::fill(src_slot, src_slot + fg::kEltMaxSrc, kNone);
+        std::fill(dst_slot, dst_slot + fg::kEltMaxDst, kNone);
+    }
+};
+
+struct Slot {
+    uint64_t offset = 0;
+    uint64_t bytes = 0;
+    bool external = false;
+    void *ext = nullptr;
+};
+
+struct Group {
+    int mm = kNone, bias_node = kNone, bias_src = kNone, act_node = kNone;
+    int pre = kNone;  // node holding the pre-activation value
+    int fin = kNone;  // last node of the group
+};
+
+}  // namespace
+
+struct fg_plan {
+    fg_ctx *ctx = nullptr;
+    fg_graph g;
+    std::vector<uint32_t> meta;
+    std::vector<Shape> shape;
+    std::vector<std::vector<uint32_t>> users;
+    std::vector<uint32_t> save;
+    std::vector<char> needs_grad;
+    std::vector<int> val_slot, grad_slot, group_of;
+    std::vector<Group> groups;
+    std::vector<Slot> slots;
+    char *arena = nullptr;
+    uint64_t arena_bytes = 0;
+    std::vector<uint32_t> inputs;  // input node ids in order
+    std::vector<int> input_slot;
+    int target_slot = kNone, loss_slot = kNone, mean_slot = kNone, adam_slot = kNone;
+    uint64_t target_bytes = 0;
+    int last = 0;
+    bool ce_fused_possible = false;
+    bool ce_fused_pending = false;
+    std::vector<Launch> fwd, loss, bwd_seed, bwd_fused;
+    std::vector<int> m_slot, v_slot;
+    std::vector<uint32_t> opt_inputs;  // indices into inputs that the optimiser updates
+    fg_mt *mt_all = nullptr;
+    std::vector<fg_mt *> mt_single;
+    bool mt_dirty = true;
+    float lr = 1e-3f, b1 = 0.9f, b2 = 0.999f, eps = 1e-8f;
+    uint64_t ws_bytes = 0;
+    std::vector<uint32_t> saved_nodes, grad_nodes;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+
+    void *ptr(int slot) const {
+        if (slot == kNone) return nullptr;
+        const Slot &s = slots[slot];
+        return s.external ? s.ext : (void *)(arena + s.offset);
+    }
+    int new_slot(uint64_t bytes) {
+        Slot s;
+        s.bytes = bytes;
+        slots.push_back(s);
+        return (int)slots.size() - 1;
+    }
+    int new_external(uint64_t bytes) {
+        Slot s;
+        s.bytes = bytes;
+        s.external = true;
+        slots.push_back(s);
+        return (int)slots.size() - 1;
+    }
+    int vslot(uint32_t n) const { return val_slot[n]; }
+    ~fg_plan();
+};
+
+fg_plan::~fg_plan() {
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+    if (mt_all) fg_mt_destroy(mt_all);
+    for (fg_mt *m : mt_single)
+        if (m) fg_mt_destroy(m);
+    if (arena && ctx) {
+        (void)hipSetDevice(ctx->device);
+        (void)hipFree(arena);
+    }
+}
+
+namespace {
+
+// ------------------------------------------------ SaveIndicator rules
+// matmul/mod.rs:191-202, softmax.rs:699-718, unary.rs:15-21,
+// binary.rs:66-72 (mul/div), backend/mod.rs:1189-1208 (inputs).
+void compute_saved(const fg_graph &g, const std::vector<std::vector<uint32_t>> &users,
+                   std::vector<uint32_t> &save) {
+    const size_t n = g.nodes.size();
+    save.assign(n, 0);
+    auto nonleaf = [&](uint32_t i) { return !g.nodes[i].in.empty(); };
+    for (size_t i = 0; i < n; ++i) {
+        const GNode &nd = g.nodes[i];
+        switch (nd.op) {
+            case FG_OP_INPUT: save[i] |= kDefBwd; break;
+            case FG_OP_MATMUL:
+                save[i] |= kDefFwd | kDefBwd;
+                for (uint32_t x : nd.in)
+                    if (nonleaf(x)) save[x] |= kDefFwd;
+                break;
+            case FG_OP_SOFTMAX:
+                save[i] |= kDefFwd | kDefBwd;
+                for (uint32_t x : nd.in) {
+                    const int op = g.nodes[x].op;
+                    if (op == FG_OP_MATMUL || op == FG_OP_GELU || op == FG_OP_SOFTMAX)
+                        save[x] |= kDefFwd | kDefBwd;
+                }
+                for (uint32_t u : users[i]) save[u] |= kDefBwd;
+                break;
+            case FG_OP_MUL:
+            case FG_OP_DIV:
+                for (uint32_t x : nd.in)
+                    if (nonleaf(x)) save[x] |= kDefFwd;
+                break;
+            default:
+                if (is_unary(nd.op) && nonleaf(nd.in[0])) save[nd.in[0]] |= kDefFwd;
+                break;
+        }
+    }
+}
+
+// -------------------------------------------------- elementwise batches
+struct EltBuilder {
+    fg_plan &P;
+    Launch L;
+    int nregs = 0, nsrc = 0, ndst = 0;
+    int64_t numel = -1, cols = -1;
+    std::vector<std::pair<uint32_t, int>> reg_of;  // node -> register in this batch
+    std::vector<std::string> names;
+    explicit EltBuilder(fg_plan &p) : P(p) { reset(); }
+    void reset() {
+        L = Launch();
+        L.kind = LK_ELT;
+        nregs = nsrc = ndst = 0;
+        numel = cols = -1;
+        reg_of.clear();
+        names.clear();
+    }
+    bool empty() const { return L.prog.n_instr == 0; }
+    int reg() { return nregs++; }
+    void ins(uint8_t op, int dst, int a = 0, int b = 0, int c = 0, float imm = 0.0f) {
+        fg::EltInstr &e = L.prog.ins[L.prog.n_instr++];
+        e.op = op;
+        e.dst = (uint8_t)dst;
+        e.a = (uint8_t)a;
+        e.b = (uint8_t)b;
+        e.c = (uint8_t)c;
+        e.imm = imm;
+    }
+    int find_reg(uint32_t n) const {
+        for (auto &p : reg_of)
+            if (p.first == n) return p.second;
+        return kNone;
+    }
+    // Load value of node x (slot s, shape xs) into a register for an output
+    // of numel/cols.
+    int load(int slot, const Shape &xs) {
+        for (int k = 0; k < nsrc; ++k)
+            if (L.src_slot[k] == slot) {
+                const int r = reg();
+                ins(fg::kEltLoad, r, k);
+                return r;
+            }
+        const int k = nsrc++;
+        L.src_slot[k] = slot;
+        L.prog.src_mode[k] = xs.scalar ? fg::kModeScalar
+                             : (xs.vector && xs.numel() != numel) ? fg::kModeRow
+                                                                    : fg::kModeFull;
+        const int r = reg();
+        ins(fg::kEltLoad, r, k);
+        return r;
+    }
+    int operand(uint32_t x) {
+        const GNode &nd = P.g.nodes[x];
+        if (nd.op == FG_OP_CONST) {
+            const int r = reg();
+            ins(fg::kEltImm, r, 0, 0, 0, nd.value);
+            return r;
+        }
+        const int r = find_reg(x);
+        if (r != kNone) return r;
+        return load(P.vslot(x), P.shape[x]);
+    }
+    void store(int slot, int r, bool accum) {
+        int k = kNone;
+        for (int j = 0; j < ndst; ++j)
+            if (L.dst_slot[j] == slot) k = j;
+        if (k == kNone) {
+            k = ndst++;
+            L.dst_slot[k] = slot;
+        }
+        ins(accum ? fg::kEltAccum : fg::kEltStore, 0, k, r);
+    }
+    bool fits(int more_instr, int more_regs, int more_src, int more_dst) const {
+        return L.prog.n_instr + more_instr <= fg::kEltMaxInstr &&
+               nregs + more_regs <= fg::kEltRegs && nsrc + more_src <= fg::kEltMaxSrc &&
+               ndst + more_dst <= fg::kEltMaxDst;
+    }
+    void begin(int64_t n, int64_t c) {
+        numel = n;
+        cols = c;
+        L.prog.n = (uint64_t)n;
+        L.prog.cols = (uint32_t)c;
+    }
+    void flush(std::vector<Launch> &out, const char *phase) {
+        if (empty() || ndst == 0) {  // nothing stored: no launch
+            reset();
+            return;
+        }
+        std::string d = std::string(phase) + " eltwise[";
+        for (size_t i = 0; i < names.size(); ++i) d += (i ? "," : "") + names[i];
+        d += "] n=" + std::to_string(numel);
+        L.desc = d;
+        out.push_back(L);
+        reset();
+    }
+};
+
+uint8_t unary_code(int op) {
+    switch (op) {
+        case FG_OP_RELU: return fg::kEltRelu;
+        case FG_OP_GELU: return fg::kEltGelu;
+        case FG_OP_ELU: return fg::kEltElu;
+        case FG_OP_TANH: return fg::kEltTanh;
+        case FG_OP_EXP: return fg::kEltExp;
+        case FG_OP_LOG: return fg::kEltLog;
+        case FG_OP_ABS: return fg::kEltAbs;
+        default: return fg::kEltNeg;
+    }
+}
+
+std::string dims_str(int M, int N, int K) {
+    return std::to_string(M) + "x" + std::to_string(N) + "x" + std::to_string(K);
+}
+
+// ------------------------------------------------------------ lowering
+int lower_forward(fg_plan &P) {
+    const fg_graph &g = P.g;
+    EltBuilder eb(P);
+    for (uint32_t n = 0; n < g.nodes.size(); ++n) {
+        const GNode &nd = g.nodes[n];
+        if (nd.op == FG_OP_INPUT || nd.op == FG_OP_CONST) continue;
+        const int gi = P.group_of[n];
+        if (gi != kNone) {
+            const Group &G = P.groups[gi];
+            if ((int)n != G.fin) continue;
+            eb.flush(P.fwd, "forward");
+            const uint32_t a = g.nodes[G.mm].in[0], b = g.nodes[G.mm].in[1];
+            Launch L;
+            L.kind = LK_GEMM;
+            L.layout = FG_NN;
+            L.M = (int)P.shape[a].rows;
+            L.K = (int)P.shape[a].cols;
+            L.N = (int)P.shape[b].cols;
+            L.lda = L.K;
+            L.ldb = L.N;
+            L.ldc = L.N;
+            L.sA = P.vslot(a);
+            L.sB = P.vslot(b);
+            L.sBias = G.bias_src != kNone ? P.vslot(G.bias_src) : kNone;
+            L.act = G.act_node == kNone ? FG_ACT_NONE
+                    : g.nodes[G.act_node].op == FG_OP_RELU ? FG_ACT_RELU
+                                                            : FG_ACT_GELU;
+            L.sC = P.vslot(G.fin);
+            L.sZ = G.act_node != kNone ? P.vslot(G.pre) : kNone;
+            L.ldz = L.N;
+            L.desc = "forward gemm NN " + dims_str(L.M, L.N, L.K) +
+                     (L.sBias != kNone ? " +bias" : "") +
+                     (L.act == FG_ACT_RELU ? " +relu" : L.act == FG_ACT_GELU ? " +gelu" : "") +
+                     " -> node " + std::to_string(G.fin);
+            P.fwd.push_back(L);
+            continue;
+        }
+        if (nd.op == FG_OP_SOFTMAX) {
+            eb.flush(P.fwd, "forward");
+            Launch L;
+            L.kind = LK_SOFTMAX;
+            L.M = (int)P.shape[n].rows;
+            L.N = (int)P.shape[n].cols;
+            L.sA = P.vslot(nd.in[0]);
+            L.sC = P.vslot(n);
+            L.desc = "forward softmax " + std::to_string(L.M) + "x" + std::to_string(L.N) +
+                     " -> node " + std::to_string(n);
+            P.fwd.push_back(L);
+            continue;
+        }
+        // elementwise node
+        const Shape &s = P.shape[n];
+        if (!eb.empty() && (eb.numel != s.numel() || eb.cols != s.cols || !eb.fits(6, 4, 2, 1)))
+            eb.flush(P.fwd, "forward");
+        if (eb.empty()) eb.begin(s.numel(), s.cols);
+        int r;
+        if (is_unary(nd.op)) {
+            const int x = eb.operand(nd.in[0]);
+            r = eb.reg();
+            eb.ins(unary_code(nd.op), r, x);
+        } else {
+            const int x = eb.operand(nd.in[0]);
+            const int y = eb.operand(nd.in[1]);
+            r = eb.reg();
+            const uint8_t code = (nd.op == FG_OP_ADD || nd.op == FG_OP_BIAS_ADD) ? fg::kEltAdd
+                                 : nd.op == FG_OP_SUB                          ? fg::kEltSub
+                                 : nd.op == FG_OP_MUL                          ? fg::kEltMul
+                                                                               : fg::kEltDiv;
+            eb.ins(code, r, x, y);
+        }
+        eb.reg_of.push_back({n, r});
+        eb.store(P.vslot(n), r, false);
+        eb.names.push_back(std::string(op_name(nd.op)) + "#" + std::to_string(n));
+    }
+    eb.flush(P.fwd, "forward");
+    return FG_OK;
+}
+
+int lower_loss(fg_plan &P) {
+    const fg_graph &g = P.g;
+    const uint32_t last = (uint32_t)P.last;
+    const Shape &s = P.shape[last];
+    if (P.ce_fused_possible) {
+        const uint32_t x = g.nodes[last].in[0];
+        Launch L;
+        L.kind = LK_SMCE;
+        L.M = (int)s.rows;
+        L.N = (int)s.cols;
+        L.sA = P.vslot(x);
+        L.sZ = P.target_slot;  // labels
+        L.sB = P.loss_slot;    // row loss
+        L.sBias = P.mean_slot;
+        L.sC = P.needs_grad[x] ? P.grad_slot[x] : kNone;
+        L.desc = "loss softmax+ce " + std::to_string(L.M) + "x" + std::to_string(L.N) +
+                 " (dlogits -> grad of node " + std::to_string(x) + ")";
+        P.loss.push_back(L);
+        return FG_OK;
+    }
+    EltBuilder eb(P);
+    eb.begin(s.numel(), s.cols);
+    const int p = eb.load(P.vslot(last), s);
+    const int seed = P.grad_slot[last];
+    if (g.loss == FG_LOSS_CE) {
+        // basic_loss.rs:91-133: grad = p - [col == label]; loss = -log p at
+        // the label column, 0 elsewhere.
+        eb.L.label_slot = P.target_slot;
+        const int oh = eb.reg();
+        eb.ins(fg::kEltLabelEq, oh);
+        const int gr = eb.reg();
+        eb.ins(fg::kEltSub, gr, p, oh);
+        eb.store(seed, gr, false);
+        const int lp = eb.reg();
+        eb.ins(fg::kEltLog, lp, p);
+        const int nl = eb.reg();
+        eb.ins(fg::kEltNeg, nl, lp);
+        const int z = eb.reg();
+        eb.ins(fg::kEltImm, z, 0, 0, 0, 0.0f);
+        const int lo = eb.reg();
+        eb.ins(fg::kEltSelect, lo, oh, nl, z);
+        eb.store(P.loss_slot, lo, false);
+        eb.names.push_back("ce");
+    } else {
+        Shape ts = s;
+        const int t = eb.load(P.target_slot, ts);
+        const int d = eb.reg();
+        eb.ins(fg::kEltSub, d, p, t);
+        if (g.loss == FG_LOSS_MSE) {
+            // basic_loss.rs:3-27: loss = (p-t)^2, grad = 2(p-t)
+            const int l = eb.reg();
+            eb.ins(fg::kEltMul, l, d, d);
+            eb.store(P.loss_slot, l, false);
+            const int two = eb.reg();
+            eb.ins(fg::kEltImm, two, 0, 0, 0, 2.0f);
+            const int gr = eb.reg();
+            eb.ins(fg::kEltMul, gr, two, d);
+            eb.store(seed, gr, false);
+            eb.names.push_back("mse");
+        } else {
+            // basic_loss.rs:29-89: loss = -(t log p + (1-t) log(1-p)) (the
+            // reference takes 1-t for 1-p -- corrected), grad = p - t.
+            const int one = eb.reg();
+            eb.ins(fg::kEltImm, one, 0, 0, 0, 1.0f);
+            const int lp = eb.reg();
+            eb.ins(fg::kEltLog, lp, p);
+            const int omp = eb.reg();
+            eb.ins(fg::kEltSub, omp, one, p);
+            const int lomp = eb.reg();
+            eb.ins(fg::kEltLog, lomp, omp);
+            const int omt = eb.reg();
+            eb.ins(fg::kEltSub, omt, one, t);
+            const int t1 = eb.reg();
+            eb.ins(fg::kEltMul, t1, t, lp);
+            const int t2 = eb.reg();
+            eb.ins(fg::kEltMul, t2, omt, lomp);
+            eb.ins(fg::kEltAdd, t1, t1, t2);
+            eb.ins(fg::kEltNeg, t1, t1);
+            eb.store(P.loss_slot, t1, false);
+            eb.store(seed, d, false);
+            eb.names.push_back("bce");
+        }
+    }
+    eb.flush(P.loss, "loss");
+    return FG_OK;
+}
+
+// Backward for one mode.  fused: the loss kernel already wrote the CE
+// gradient of the final softmax's input; otherwise start from the seed.
+int lower_backward(fg_plan &P, bool fused, std::vector<Launch> &out) {
+    const fg_graph &g = P.g;
+    const size_t nn = g.nodes.size();
+    std::vector<char> ginit(nn, 0), gskip(nn, 0);
+    const uint32_t last = (uint32_t)P.last;
+    if (fused)
+        ginit[g.nodes[last].in[0]] = 1;
+    else
+        ginit[last] = 1;
+    auto gs = [&](uint32_t n) { return P.grad_slot[n]; };
+    EltBuilder eb(P);
+    auto elt_contrib = [&](uint32_t n) {
+        // One program per elementwise node: contributions to its inputs.
+        const GNode &nd = g.nodes[n];
+        const Shape &s = P.shape[n];
+        eb.begin(s.numel(), s.cols);
+        const int gr = eb.load(gs(n), s);
+        auto emit = [&](uint32_t x, int r) {
+            if (!P.needs_grad[x]) return;
+            eb.store(gs(x), r, ginit[x] != 0);
+            ginit[x] = 1;
+        };
+        const int op = nd.op;
+        if (is_unary(op)) {
+            const uint32_t x = nd.in[0];
+            if (!P.needs_grad[x]) {
+                eb.reset();
+                return;
+            }
+            int d;
+            switch (op) {
+                case FG_OP_NEG: d = eb.reg(); eb.ins(fg::kEltNeg, d, gr); break;
+                case FG_OP_TANH: {  // 1 - y^2 (y = output)
+                    const int y = eb.load(P.vslot(n), s);
+                    const int y2 = eb.reg(); eb.ins(fg::kEltMul, y2, y, y);
+                    const int one = eb.reg(); eb.ins(fg::kEltImm, one, 0, 0, 0, 1.0f);
+                    const int dd = eb.reg(); eb.ins(fg::kEltSub, dd, one, y2);
+                    d = eb.reg(); eb.ins(fg::kEltMul, d, gr, dd);
+                    break;
+                }
+                case FG_OP_EXP: {  // y
+                    const int y = eb.load(P.vslot(n), s);
+                    d = eb.reg(); eb.ins(fg::kEltMul, d, gr, y);
+                    break;
+                }
+                case FG_OP_LOG: {  // 1/x (the reference divides by its output, unary.rs:241-249)
+                    const int xv = eb.operand(x);
+                    d = eb.reg(); eb.ins(fg::kEltDiv, d, gr, xv);
+                    break;
+                }
+                default: {  // relu, gelu, elu, abs: g * f'(x)
+                    const int xv = eb.operand(x);
+                    const uint8_t code = op == FG_OP_RELU ? fg::kEltReluD
+                                         : op == FG_OP_GELU ? fg::kEltGeluD
+                                         : op == FG_OP_ELU ? fg::kEltEluD
+                                                           : fg::kEltSign;
+                    const int dd = eb.reg(); eb.ins(code, dd, xv);
+                    d = eb.reg(); eb.ins(fg::kEltMul, d, gr, dd);
+                    break;
+                }
+            }
+            emit(x, d);
+        } else {
+            const uint32_t a = nd.in[0], b = nd.in[1];
+            const Shape &sa = P.shape[a], &sb = P.shape[b];
+            const bool bcast_a = !sa.scalar && sa.numel() != s.numel();
+            const bool bcast_b = !sb.scalar && sb.numel() != s.numel();
+            // Row-broadcast operands reduce over rows: handled by bias_grad
+            // for add/sub; products with a broadcast vector are rejected at
+            // plan creation.
+            if (op == FG_OP_ADD || op == FG_OP_BIAS_ADD || op == FG_OP_SUB) {
+                if (P.needs_grad[a] && !bcast_a) emit(a, gr);
+                if (P.needs_grad[b] && !bcast_b) {
+                    if (op == FG_OP_SUB) {
+                        const int d = eb.reg(); eb.ins(fg::kEltNeg, d, gr);
+                        emit(b, d);
+                    } else {
+                        emit(b, gr);
+                    }
+                }
+            } else if (op == FG_OP_MUL) {
+                if (P.needs_grad[a]) {
+                    const int bv = eb.operand(b);
+                    const int d = eb.reg(); eb.ins(fg::kEltMul, d, gr, bv);
+                    emit(a, d);
+                }
+                if (P.needs_grad[b]) {
+                    const int av = eb.operand(a);
+                    const int d = eb.reg(); eb.ins(fg::kEltMul, d, gr, av);
+                    emit(b, d);
+                }
+            } else {  // DIV: d/da = g / b ; d/db = -g a / b^2
+                const int bv = eb.operand(b);
+                if (P.needs_grad[a]) {
+                    const int d = eb.reg(); eb.ins(fg::kEltDiv, d, gr, bv);
+                    emit(a, d);
+                }
+                if (P.needs_grad[b]) {
+                    const int av = eb.operand(a);
+                    const int q = eb.reg(); eb.ins(fg::kEltDiv, q, av, bv);
+                    const int q2 = eb.reg(); eb.ins(fg::kEltDiv, q2, q, bv);
+                    const int d0 = eb.reg(); eb.ins(fg::kEltMul, d0, gr, q2);
+                    const int d = eb.reg(); eb.ins(fg::kEltNeg, d, d0);
+                    emit(b, d);
+                }
+            }
+            eb.names.push_back(std::string("d") + op_name(op) + "#" + std::to_string(n));
+            eb.flush(out, "backward");
+            // Column reductions for broadcast operands.
+            auto reduce = [&](uint32_t x, bool neg) {
+                if (!P.needs_grad[x]) return;
+                Launch L;
+                L.kind = LK_BIAS_GRAD;
+                L.M = (int)s.rows;
+                L.N = (int)s.cols;
+                L.sA = gs(n);
+                L.desc = "backward bias_grad " + std::to_string(L.M) + "x" + std::to_string(L.N);
+                if (!neg) {
+                    L.sC = gs(x);
+                    L.accumulate = ginit[x];
+                    L.desc += " -> grad of node " + std::to_string(x);
+                    ginit[x] = 1;
+                    out.push_back(L);
+                    return;
+                }
+                // sub's broadcast operand: reduce into a temporary, then
+                // grad (=|+=) -temporary.
+                const int tmp = P.new_slot((uint64_t)L.N * 4);
+                L.sC = tmp;
+                L.desc += " -> temporary";
+                out.push_back(L);
+                Shape vs;
+                vs.vector = true;
+                vs.cols = L.N;
+                eb.begin(L.N, L.N);
+                const int t = eb.load(tmp, vs);
+                const int d = eb.reg();
+                eb.ins(fg::kEltNeg, d, t);
+                eb.store(gs(x), d, ginit[x] != 0);
+                ginit[x] = 1;
+                eb.names.push_back("neg-reduce#" + std::to_string(x));
+                eb.flush(out, "backward");
+            };
+            if (bcast_a) reduce(a, false);
+            if (bcast_b) reduce(b, op == FG_OP_SUB);
+            return;
+        }
+        eb.names.push_back(std::string("d") + op_name(op) + "#" + std::to_string(n));
+        eb.flush(out, "backward");
+    };
+
+    for (int64_t ni = (int64_t)nn - 1; ni >= 0; --ni) {
+        const uint32_t n = (uint32_t)ni;
+        const GNode &nd = g.nodes[n];
+        if (nd.op == FG_OP_INPUT || nd.op == FG_OP_CONST || !P.needs_grad[n]) continue;
+        if (fused && n == last) continue;
+        const int gi = P.group_of[n];
+        if (gi != kNone) {
+            const Group &G = P.groups[gi];
+            if ((int)n != G.fin) continue;
+            const int pre = G.pre;
+            if (G.act_node != kNone && !gskip[G.act_node]) {
+                if (!ginit[G.act_node]) continue;
+                // dZ = dH * act'(Z) as a program (no downstream GEMM took it).
+                const Shape &s = P.shape[pre];
+                eb.begin(s.numel(), s.cols);
+                const int gh = eb.load(gs(G.act_node), s);
+                const int z = eb.load(P.vslot(pre), s);
+                const int dd = eb.reg();
+                eb.ins(g.nodes[G.act_node].op == FG_OP_RELU ? fg::kEltReluD : fg::kEltGeluD, dd, z);
+                const int d = eb.reg();
+                eb.ins(fg::kEltMul, d, gh, dd);
+                eb.store(gs(pre), d, ginit[pre] != 0);
+                ginit[pre] = 1;
+                eb.names.push_back("dact#" + std::to_string(G.act_node));
+                eb.flush(out, "backward");
+            } else if (G.act_node == kNone && !ginit[pre]) {
+                continue;
+            }
+            const uint32_t a = g.nodes[G.mm].in[0], b = g.nodes[G.mm].in[1];
+            const int M = (int)P.shape[a].rows, K = (int)P.shape[a].cols, N = (int)P.shape[b].cols;
+            if (G.bias_src != kNone && P.needs_grad[G.bias_src]) {
+                Launch L;
+                L.kind = LK_BIAS_GRAD;
+                L.M = M;
+                L.N = N;
+                L.sA = gs(pre);
+                L.sC = gs(G.bias_src);
+                L.accumulate = ginit[G.bias_src];
+                L.desc = "backward bias_grad " + std::to_string(M) + "x" + std::to_string(N) +
+                         " -> grad of node " + std::to_string(G.bias_src);
+                ginit[G.bias_src] = 1;
+                out.push_back(L);
+            }
+            if (P.needs_grad[b]) {  // dB = A^T dZ
+                Launch L;
+                L.kind = LK_GEMM;
+                L.layout = FG_TN;
+                L.M = K;
+                L.N = N;
+                L.K = M;
+                L.sA = P.vslot(a);
+                L.lda = K;
+                L.sB = gs(pre);
+                L.ldb = N;
+                L.sC = gs(b);
+                L.ldc = N;
+                L.accumulate = ginit[b];
+                L.desc = "backward gemm TN " + dims_str(K, N, M) + " -> grad of node " +
+                         std::to_string(b);
+                ginit[b] = 1;
+                out.push_back(L);
+            }
+            if (P.needs_grad[a]) {  // dA = dZ B^T  (with act' of the layer below fused)
+                Launch L;
+                L.kind = LK_GEMM_BWD;
+                L.layout = FG_NT;
+                L.M = M;
+                L.N = K;
+                L.K = N;
+                L.sA = gs(pre);
+                L.lda = N;
+                L.sB = P.vslot(b);
+                L.ldb = N;
+                L.ldc = K;
+                const int ga = P.group_of[a];
+                const bool fuse = ga != kNone && P.groups[ga].act_node == (int)a &&
+                                  P.users[a].size() == 1 && !ginit[a];
+                if (fuse) {
+                    const Group &G2 = P.groups[ga];
+                    L.act = g.nodes[a].op == FG_OP_RELU ? FG_ACT_RELU : FG_ACT_GELU;
+                    L.sZ = P.vslot(G2.pre);
+                    L.ldz = K;
+                    L.sC = gs(G2.pre);
+                    L.accumulate = ginit[G2.pre];
+                    ginit[G2.pre] = 1;
+                    gskip[a] = 1;
+                    L.desc = "backward gemm NT " + dims_str(M, K, N) + " *" +
+                             (L.act == FG_ACT_RELU ? "relu'" : "gelu'") + " -> grad of node " +
+                             std::to_string(G2.pre);
+                } else {
+                    L.sC = gs(a);
+                    L.accumulate = ginit[a];
+                    ginit[a] = 1;
+                    L.desc = "backward gemm NT " + dims_str(M, K, N) + " -> grad of node " +
+                             std::to_string(a);
+                }
+                out.push_back(L);
+            }
+            continue;
+        }
+        if (!ginit[n]) continue;  // no gradient reaches this node
+        if (nd.op == FG_OP_SOFTMAX) {
+            const uint32_t x = nd.in[0];
+            if (!P.needs_grad[x]) continue;
+            Launch L;
+            L.kind = LK_SOFTMAX_BWD;
+            L.M = (int)P.shape[n].rows;
+            L.N = (int)P.shape[n].cols;
+            L.sA = P.vslot(n);
+            L.sB = gs(n);
+            L.sC = gs(x);
+            L.accumulate = ginit[x];
+            ginit[x] = 1;
+            L.desc = "backward softmax " + std::to_string(L.M) + "x" + std::to_string(L.N) +
+                     " -> grad of node " + std::to_string(x);
+            out.push_back(L);
+            continue;
+        }
+        elt_contrib(n);
+    }
+    // Inputs no gradient reached get zeros.
+    for (uint32_t n : P.inputs) {
+        if (!P.needs_grad[n] || ginit[n]) continue;
+        Launch L;
+        L.kind = LK_FILL0;
+        L.sC = gs(n);
+        L.count = (uint64_t)P.shape[n].numel();
+        L.desc = "backward zero grad of node " + std::to_string(n);
+        out.push_back(L);
+    }
+    return FG_OK;
+}
+
+// ------------------------------------------------------------ execute
+int run(fg_plan &P, const std::vector<Launch> &list) {
+    fg_ctx *ctx = P.ctx;
+    for (const Launch &L : list) {
+        int rc = FG_OK;
+        switch (L.kind) {
+            case LK_GEMM:
+                rc = fg_gemm_f32(ctx, L.layout, L.M, L.N, L.K, (const float *)P.ptr(L.sA), L.lda,
+                                 (const float *)P.ptr(L.sB), L.ldb, (const float *)P.ptr(L.sBias),
+                                 L.act, (float *)P.ptr(L.sC), L.ldc, (float *)P.ptr(L.sZ), L.ldz,
+                                 L.accumulate);
+                break;
+            case LK_GEMM_BWD:
+                rc = fg_gemm_bwd_f32(ctx, L.layout, L.M, L.N, L.K, (const float *)P.ptr(L.sA),
+                                     L.lda, (const float *)P.ptr(L.sB), L.ldb, L.act,
+                                     (const float *)P.ptr(L.sZ), L.ldz, (float *)P.ptr(L.sC),
+                                     L.ldc, L.accumulate);
+                break;
+            case LK_BIAS_GRAD:
+                rc = fg_bias_grad_f32(ctx, L.M, L.N, (const float *)P.ptr(L.sA), L.N,
+                                      (float *)P.ptr(L.sC), L.accumulate);
+                break;
+            case LK_SOFTMAX:
+                rc = fg_softmax_f32(ctx, (const float *)P.ptr(L.sA), L.M, L.N,
+                                    (float *)P.ptr(L.sC));
+                break;
+            case LK_SOFTMAX_BWD:
+                rc = fg_softmax_bwd_f32(ctx, (const float *)P.ptr(L.sA),
+                                        (const float *)P.ptr(L.sB), L.M, L.N,
+                                        (float *)P.ptr(L.sC), L.accumulate);
+                break;
+            case LK_SMCE:
+                FG_REQUIRE(P.ptr(L.sZ), FG_ERR_INVALID_ARGUMENT,
+                           "dispatch_loss: no target bound (fg_plan_bind_target)");
+                rc = fg_softmax_ce_f32(ctx, (const float *)P.ptr(L.sA), L.N,
+                                       (const uint32_t *)P.ptr(L.sZ), L.M, L.N, 1.0f,
+                                       (float *)P.ptr(L.sB), (float *)P.ptr(L.sBias),
+                                       (float *)P.ptr(L.sC), L.N, nullptr);
+                break;
+            case LK_ELT: {
+                fg::EltProgram p = L.prog;
+                for (int k = 0; k < fg::kEltMaxSrc; ++k)
+                    if (L.src_slot[k] != kNone) {
+                        p.src[k] = (const float *)P.ptr(L.src_slot[k]);
+                        FG_REQUIRE(p.src[k], FG_ERR_INVALID_ARGUMENT,
+                                   "plan: unbound input or target (%s)", L.desc.c_str());
+                    }
+                for (int k = 0; k < fg::kEltMaxDst; ++k)
+                    if (L.dst_slot[k] != kNone) p.dst[k] = (float *)P.ptr(L.dst_slot[k]);
+                if (L.label_slot != kNone) {
+                    p.labels = (const uint32_t *)P.ptr(L.label_slot);
+                    FG_REQUIRE(p.labels, FG_ERR_INVALID_ARGUMENT,
+                               "dispatch_loss: no target bound (fg_plan_bind_target)");
+                }
+                rc = fg::launch_eltwise(ctx, p);
+                break;
+            }
+            case LK_FILL0:
+                rc = fg_fill_u32(ctx, P.ptr(L.sC), 0u, L.count);
+                break;
+            default:
+                fg::set_error("plan: unknown launch kind %d", L.kind);
+                return FG_ERR_INTERNAL;
+        }
+        if (rc != FG_OK) return rc;
+    }
+    return FG_OK;
+}
+
+int ensure_mt(fg_plan &P) {
+    if (!P.mt_dirty) return FG_OK;
+    for (uint32_t idx : P.opt_inputs)
+        FG_REQUIRE(P.ptr(P.input_slot[idx]), FG_ERR_INVALID_ARGUMENT,
+                   "dispatch_optim: input %u is not bound", idx);
+    if (P.mt_all) fg_mt_destroy(P.mt_all);
+    P.mt_all = nullptr;
+    for (fg_mt *m : P.mt_single)
+        if (m) fg_mt_destroy(m);
+    P.mt_single.assign(P.inputs.size(), nullptr);
+    if (P.opt_inputs.empty()) {
+        P.mt_dirty = false;
+        return FG_OK;
+    }
+    const bool adam = P.g.optim == FG_OPTIM_ADAM;
+    std::vector<float *> pp, gg, mm, vv;
+    std::vector<uint64_t> sz;
+    for (uint32_t idx : P.opt_inputs) {
+        const uint32_t n = P.inputs[idx];
+        pp.push_back((float *)P.ptr(P.input_slot[idx]));
+        gg.push_back((float *)P.ptr(P.grad_slot[n]));
+        if (adam) {
+            mm.push_back((float *)P.ptr(P.m_slot[idx]));
+            vv.push_back((float *)P.ptr(P.v_slot[idx]));
+        }
+        sz.push_back((uint64_t)P.shape[n].numel());
+    }
+    int rc = fg_mt_create(P.ctx, (int)pp.size(), pp.data(), gg.data(), adam ? mm.data() : nullptr,
+                          adam ? vv.data() : nullptr, sz.data(), &P.mt_all);
+    if (rc) return rc;
+    for (size_t k = 0; k < P.opt_inputs.size(); ++k) {
+        rc = fg_mt_create(P.ctx, 1, &pp[k], &gg[k], adam ? &mm[k] : nullptr,
+                          adam ? &vv[k] : nullptr, &sz[k], &P.mt_single[P.opt_inputs[k]]);
+        if (rc) return rc;
+    }
+    P.mt_dirty = false;
+    return FG_OK;
+}
+
+int run_optim(fg_plan &P, fg_mt *mt) {
+    if (!mt) return FG_OK;
+    if (P.g.optim == FG_OPTIM_ADAM)
+        return fg::mt_adam_dev(P.ctx, mt, P.lr, P.b1, P.b2, P.eps, P.ptr(P.adam_slot), 0);
+    // SGD zeroes the gradient after the update (basic_optim.rs:27-28).
+    return fg_sgd_step(P.ctx, mt, P.lr, 1);
+}
+
+void drop_graph(fg_plan &P) {
+    if (P.exec) (void)hipGraphExecDestroy(P.exec);
+    if (P.graph) (void)hipGraphDestroy(P.graph);
+    P.exec = nullptr;
+    P.graph = nullptr;
+}
+
+}  // namespace
+
+// ====================================================================== ABI
+FG_API int fg_memcpy_h2d(fg_ctx *ctx, void *d_dst, const void *src, uint64_t bytes) {
+    FG_REQUIRE(ctx && (bytes == 0 || (d_dst && src)), FG_ERR_INVALID_ARGUMENT,
+               "fg_memcpy_h2d: NULL argument");
+    if (!bytes) return FG_OK;
+    FG_HIP(hipMemcpyAsync(d_dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+    FG_HIP(hipStreamSynchronize(ctx->stream));
+    return FG_OK;
+}
+
+FG_API int fg_memcpy_d2h(fg_ctx *ctx, void *dst, const void *d_src, uint64_t bytes) {
+    FG_REQUIRE(ctx && (bytes == 0 || (dst && d_src)), FG_ERR_INVALID_ARGUMENT,
+               "fg_memcpy_d2h: NULL argument");
+    if (!bytes) return FG_OK;
+    FG_HIP(hipMemcpyAsync(dst, d_src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    FG_HIP(hipStreamSynchronize(ctx->stream));
+    return FG_OK;
+}
+
+FG_API int fg_graph_create(int loss, int optim, fg_graph **out) {
+    FG_REQUIRE(out, FG_ERR_INVALID_ARGUMENT, "fg_graph_create: out is NULL");
+    FG_REQUIRE(loss >= FG_LOSS_MSE && loss <= FG_LOSS_CE, FG_ERR_INVALID_ARGUMENT,
+               "fg_graph_create: unknown loss %d", loss);
+    FG_REQUIRE(optim == FG_OPTIM_SGD || optim == FG_OPTIM_ADAM, FG_ERR_INVALID_ARGUMENT,
+               "fg_graph_create: unknown optimiser %d", optim);
+    fg_graph *g = new fg_graph;
+    g->loss = loss;
+    g->optim = optim;
+    *out = g;
+    return FG_OK;
+}
+
+FG_API int fg_graph_destroy(fg_graph *g) {
+    delete g;
+    return FG_OK;
+}
+
+FG_API int fg_graph_new_field(fg_graph *g, uint32_t *field) {
+    FG_REQUIRE(g && field, FG_ERR_INVALID_ARGUMENT, "fg_graph_new_field: NULL argument");
+    *field = ++g->nfields;
+    return FG_OK;
+}
+
+FG_API int fg_graph_input(fg_graph *g, const uint32_t *fields, int rank, uint32_t *node) {
+    FG_REQUIRE(g && node && (fields || rank == 0), FG_ERR_INVALID_ARGUMENT,
+               "fg_graph_input: NULL argument");
+    FG_REQUIRE(rank >= 1 && rank <= 8, FG_ERR_GRAPH, "fg_graph_input: rank %d not in [1, 8]",
+               rank);
+    for (int d = 0; d < rank; ++d)
+        FG_REQUIRE(fields[d] >= 1 && fields[d] <= g->nfields, FG_ERR_GRAPH,
+                   "fg_graph_input: field %u was not declared", fields[d]);
+    GNode nd;
+    nd.op = FG_OP_INPUT;
+    nd.fields.assign(fields, fields + rank);
+    g->nodes.push_back(nd);
+    *node = (uint32_t)g->nodes.size() - 1;
+    return FG_OK;
+}
+
+FG_API int fg_graph_constant_f32(fg_graph *g, float value, uint32_t *node) {
+    FG_REQUIRE(g && node, FG_ERR_INVALID_ARGUMENT, "fg_graph_constant_f32: NULL argument");
+    GNode nd;
+    nd.op = FG_OP_CONST;
+    nd.value = value;
+    g->nodes.push_back(nd);
+    *node = (uint32_t)g->nodes.size() - 1;
+    return FG_OK;
+}
+
+FG_API int fg_graph_op(fg_graph *g, int op, const uint32_t *inputs, int n_inputs, uint32_t *node) {
+    FG_REQUIRE(g && node && (inputs || n_inputs == 0), FG_ERR_INVALID_ARGUMENT,
+               "fg_graph_op: NULL argument");
+    FG_REQUIRE(op >= FG_OP_ADD && op <= FG_OP_BIAS_ADD, FG_ERR_INVALID_ARGUMENT,
+               "fg_graph_op: op %d is not an operation (use fg_graph_input/constant)", op);
+    FG_REQUIRE(n_inputs == arity(op), FG_ERR_GRAPH, "fg_graph_op: %s takes %d inputs, got %d",
+               op_name(op), arity(op), n_inputs);
+    for (int k = 0; k < n_inputs; ++k)
+        FG_REQUIRE(inputs[k] < g->nodes.size(), FG_ERR_GRAPH,
+                   "fg_graph_op: input node %u does not exist", inputs[k]);
+    GNode nd;
+    nd.op = op;
+    nd.in.assign(inputs, inputs + n_inputs);
+    g->nodes.push_back(nd);
+    *node = (uint32_t)g->nodes.size() - 1;
+    return FG_OK;
+}
+
+FG_API int fg_graph_set_input_flags(fg_graph *g, uint32_t node, uint32_t flags) {
+    FG_REQUIRE(g && node < g->nodes.size() && g->nodes[node].op == FG_OP_INPUT,
+               FG_ERR_INVALID_ARGUMENT, "fg_graph_set_input_flags: node %u is not an input", node);
+    g->nodes[node].flags = flags;
+    return FG_OK;
+}
+
+FG_API int fg_graph_num_nodes(const fg_graph *g, uint32_t *n) {
+    FG_REQUIRE(g && n, FG_ERR_INVALID_ARGUMENT, "fg_graph_num_nodes: NULL argument");
+    *n = (uint32_t)g->nodes.size();
+    return FG_OK;
+}
+
+FG_API int fg_graph_validate(const fg_graph *g, const uint32_t *meta, int n_meta) {
+    FG_REQUIRE(g && (meta || n_meta == 0), FG_ERR_INVALID_ARGUMENT,
+               "fg_graph_validate: NULL argument");
+    std::vector<Shape> sh;
+    return infer_shapes(*g, meta, n_meta, sh);
+}
+
+FG_API int fg_plan_create(fg_ctx *ctx, const fg_graph *g, const uint32_t *meta, int n_meta,
+                          fg_plan **out) {
+    FG_REQUIRE(g && out && meta, FG_ERR_INVALID_ARGUMENT, "fg_plan_create: NULL argument");
+    std::unique_ptr<fg_plan> P(new fg_plan);
+    P->ctx = ctx;
+    P->g = *g;
+    P->meta.assign(meta, meta + n_meta);
+    int rc = infer_shapes(P->g, meta, n_meta, P->shape);
+    if (rc) return rc;
+    const fg_graph &G = P->g;
+    const size_t nn = G.nodes.size();
+    P->last = (int)nn - 1;
+    float lr;
+    std::memcpy(&lr, &meta[0], 4);
+    P->lr = lr;
+    P->users.assign(nn, {});
+    for (uint32_t i = 0; i < nn; ++i)
+        for (uint32_t x : G.nodes[i].in) P->users[x].push_back(i);
+    compute_saved(G, P->users, P->save);
+    // needs_grad: depends on an input that takes a gradient.
+    P->needs_grad.assign(nn, 0);
+    for (uint32_t i = 0; i < nn; ++i) {
+        const GNode &nd = G.nodes[i];
+        if (nd.op == FG_OP_INPUT) {
+            P->needs_grad[i] = !(nd.flags & FG_INPUT_NO_GRAD);
+            P->inputs.push_back(i);
+        } else if (nd.op != FG_OP_CONST) {
+            for (uint32_t x : nd.in) P->needs_grad[i] |= P->needs_grad[x];
+        }
+    }
+    // Products with a row-broadcast vector that needs a gradient would need
+    // a reduction of a product: not supported.
+    for (uint32_t i = 0; i < nn; ++i) {
+        const GNode &nd = G.nodes[i];
+        if (nd.op != FG_OP_MUL && nd.op != FG_OP_DIV) continue;
+        for (uint32_t x : nd.in) {
+            const Shape &sx = P->shape[x];
+            FG_REQUIRE(sx.scalar || sx.numel() == P->shape[i].numel() || !P->needs_grad[x],
+                       FG_ERR_UNSUPPORTED,
+                       "%s %u: gradient of a row-broadcast operand is not supported",
+                       op_name(nd.op), i);
+        }
+    }
+    P->ce_fused_possible = G.loss == FG_LOSS_CE && G.nodes.back().op == FG_OP_SOFTMAX;
+
+    // GEMM groups.
+    P->group_of.assign(nn, kNone);
+    for (uint32_t i = 0; i < nn; ++i) {
+        if (G.nodes[i].op != FG_OP_MATMUL) continue;
+        Group gr;
+        gr.mm = (int)i;
+        int cur = (int)i;
+        if (P->users[i].size() == 1) {
+            const uint32_t u = P->users[i][0];
+            const GNode &un = G.nodes[u];
+            if ((un.op == FG_OP_BIAS_ADD || un.op == FG_OP_ADD) && un.in[0] == i &&
+                un.in[1] != i) {
+                const Shape &sb = P->shape[un.in[1]];
+                if (sb.vector && sb.cols == P->shape[i].cols && G.nodes[un.in[1]].op != FG_OP_CONST) {
+                    gr.bias_node = (int)u;
+                    gr.bias_src = (int)un.in[1];
+                    cur = (int)u;
+                }
+            }
+        }
+        gr.pre = cur;
+        if (P->users[cur].size() == 1) {
+            const uint32_t u = P->users[cur][0];
+            const int op = G.nodes[u].op;
+            if ((op == FG_OP_RELU || op == FG_OP_GELU) && G.nodes[u].in[0] == (uint32_t)cur)
+                gr.act_node = (int)u;
+        }
+        gr.fin = gr.act_node != kNone ? gr.act_node : cur;
+        const int gi = (int)P->groups.size();
+        P->groups.push_back(gr);
+        P->group_of[gr.mm] = gi;
+        if (gr.bias_node != kNone) P->group_of[gr.bias_node] = gi;
+        if (gr.act_node != kNone) P->group_of[gr.act_node] = gi;
+    }
+
+    // Slots.
+    P->val_slot.assign(nn, kNone);
+    P->grad_slot.assign(nn, kNone);
+    P->input_slot.assign(P->inputs.size(), kNone);
+    for (size_t k = 0; k < P->inputs.size(); ++k) {
+        const uint32_t n = P->inputs[k];
+        P->input_slot[k] = P->new_external((uint64_t)P->shape[n].numel() * 4);
+        P->val_slot[n] = P->input_slot[k];
+    }
+    for (uint32_t i = 0; i < nn; ++i) {
+        const int op = G.nodes[i].op;
+        if (op == FG_OP_INPUT || op == FG_OP_CONST) continue;
+        P->val_slot[i] = P->new_slot((uint64_t)P->shape[i].numel() * 4);
+    }
+    for (const Group &gr : P->groups)  // the pre-bias product is not materialised
+        if (gr.bias_node != kNone) P->val_slot[gr.mm] = P->val_slot[gr.bias_node];
+    for (uint32_t i = 0; i < nn; ++i) {
+        if (G.nodes[i].op == FG_OP_CONST) continue;
+        if (P->needs_grad[i] || (int)i == P->last)
+            P->grad_slot[i] = P->new_slot((uint64_t)P->shape[i].numel() * 4);
+    }
+    for (const Group &gr : P->groups)  // d(matmul) == d(bias add)
+        if (gr.bias_node != kNone && P->grad_slot[gr.bias_node] != kNone)
+            P->grad_slot[gr.mm] = P->grad_slot[gr.bias_node];
+    const Shape &ls = P->shape[P->last];
+    if (G.loss == FG_LOSS_CE) {
+        P->target_bytes = (uint64_t)ls.rows * 4;
+        P->loss_slot = P->new_slot((uint64_t)(P->ce_fused_possible ? ls.rows : ls.numel()) * 4);
+    } else {
+        P->target_bytes = (uint64_t)ls.numel() * 4;
+        P->loss_slot = P->new_slot((uint64_t)ls.numel() * 4);
+    }
+    P->target_slot = P->new_external(P->target_bytes);
+    P->mean_slot = P->new_slot(4);
+    // Optimiser.
+    for (size_t k = 0; k < P->inputs.size(); ++k) {
+        const GNode &nd = G.nodes[P->inputs[k]];
+        if (!(nd.flags & (FG_INPUT_NO_GRAD | FG_INPUT_FROZEN))) P->opt_inputs.push_back((uint32_t)k);
+    }
+    P->m_slot.assign(P->inputs.size(), kNone);
+    P->v_slot.assign(P->inputs.size(), kNone);
+    if (G.optim == FG_OPTIM_ADAM) {
+        for (uint32_t k : P->opt_inputs) {
+            const uint64_t b = (uint64_t)P->shape[P->inputs[k]].numel() * 4;
+            P->m_slot[k] = P->new_slot(b);
+            P->v_slot[k] = P->new_slot(b);
+        }
+        P->adam_slot = P->new_slot(fg::adam_dev_state_bytes());
+    }
+    // Exposed lists in SaveIndicator order.
+    for (uint32_t i = 0; i < nn; ++i) {
+        if (P->save[i] & kDefFwd) P->saved_nodes.push_back(i);
+        if ((P->save[i] & kDefBwd) && P->grad_slot[i] != kNone) P->grad_nodes.push_back(i);
+    }
+
+    // Lowering (launches refer to slots; lowering may add temporaries).
+    if ((rc = lower_forward(*P))) return rc;
+    if ((rc = lower_loss(*P))) return rc;
+    if ((rc = lower_backward(*P, false, P->bwd_seed))) return rc;
+    if (P->ce_fused_possible && (rc = lower_backward(*P, true, P->bwd_fused))) return rc;
+
+    // Arena: every plan-owned tensor, 256-byte aligned, one allocation.
+    uint64_t off = 0;
+    for (Slot &s : P->slots) {
+        if (s.external) continue;
+        s.offset = off;
+        off += (s.bytes + 255) & ~uint64_t(255);
+    }
+    P->arena_bytes = off;
+    if (!ctx) {  // dry plan: lowering only (describe), nothing allocated
+        *out = P.release();
+        return FG_OK;
+    }
+    FG_HIP(hipSetDevice(ctx->device));
+    if (off) {
+        hipError_t e = hipMalloc((void **)&P->arena, off);
+        if (e != hipSuccess)
+            return fg::hip_fail(e, "fg_plan_create: arena hipMalloc", __FILE__, __LINE__);
+        // Zero the arena once (grads of unreached inputs, optimiser state,
+        // the Adam step counter) with a fill kernel.
+        rc = fg_fill_u32(ctx, P->arena, 0u, off / 4);
+        if (rc) return rc;
+    }
+    // Workspace for bias-gradient partials (the largest column reduction),
+    // reserved now so dispatch and capture never allocate.
+    uint64_t ws = 1u << 20;
+    for (auto *list : {&P->bwd_seed, &P->bwd_fused})
+        for (const Launch &L : *list)
+            if (L.kind == LK_BIAS_GRAD) ws = std::max<uint64_t>(ws, (uint64_t)L.N * 4 * 1024);
+    if (!fg::workspace(ctx, ws)) return FG_ERR_OUT_OF_MEMORY;
+    FG_HIP(hipStreamSynchronize(ctx->stream));
+    *out = P.release();
+    return FG_OK;
+}
+
+FG_API int fg_plan_destroy(fg_plan *p) {
+    if (!p) return FG_OK;
+    if (p->ctx) {
+        (void)hipSetDevice(p->ctx->device);
+        (void)hipStreamSynchronize(p->ctx->stream);
+    }
+    delete p;
+    return FG_OK;
+}
+
+FG_API int fg_plan_count(const fg_plan *p, int role, int *count) {
+    FG_REQUIRE(p && count, FG_ERR_INVALID_ARGUMENT, "fg_plan_count: NULL argument");
+    switch (role) {
+        case FG_ROLE_FORWARD_OUT: case FG_ROLE_SEED: case FG_ROLE_LOSS: case FG_ROLE_TARGET:
+            *count = 1;
+            break;
+        case FG_ROLE_MEAN_LOSS: *count = p->ce_fused_possible ? 1 : 0; break;
+        case FG_ROLE_FORWARD_SAVED: *count = (int)p->saved_nodes.size(); break;
+        case FG_ROLE_GRAD: *count = (int)p->grad_nodes.size(); break;
+        case FG_ROLE_INPUT: *count = (int)p->inputs.size(); break;
+        case FG_ROLE_STATE:
+            *count = p->g.optim == FG_OPTIM_ADAM ? 2 * (int)p->opt_inputs.size() : 0;
+            break;
+        default:
+            fg::set_error("fg_plan_count: unknown role %d", role);
+            return FG_ERR_INVALID_ARGUMENT;
+    }
+    return FG_OK;
+}
+
+FG_API int fg_plan_tensor(const fg_plan *p, int role, int index, void **d_ptr, uint64_t *bytes,
+                          uint32_t *node) {
+    FG_REQUIRE(p, FG_ERR_INVALID_ARGUMENT, "fg_plan_tensor: plan is NULL");
+    int cnt = 0;
+    int rc = fg_plan_count(p, role, &cnt);
+    if (rc) return rc;
+    FG_REQUIRE(index >= 0 && index < cnt, FG_ERR_OUT_OF_BOUNDS,
+               "fg_plan_tensor: index %d out of range for role %d (%d tensors)", index, role, cnt);
+    int slot = kNone;
+    uint32_t nd = 0;
+    switch (role) {
+        case FG_ROLE_FORWARD_OUT: nd = p->last; slot = p->val_slot[nd]; break;
+        case FG_ROLE_SEED: nd = p->last; slot = p->grad_slot[nd]; break;
+        case FG_ROLE_LOSS: nd = p->last; slot = p->loss_slot; break;
+        case FG_ROLE_MEAN_LOSS: nd = p->last; slot = p->mean_slot; break;
+        case FG_ROLE_TARGET: nd = p->last; slot = p->target_slot; break;
+        case FG_ROLE_FORWARD_SAVED: nd = p->saved_nodes[index]; slot = p->val_slot[nd]; break;
+        case FG_ROLE_GRAD: nd = p->grad_nodes[index]; slot = p->grad_slot[nd]; break;
+        case FG_ROLE_INPUT: nd = p->inputs[index]; slot = p->input_slot[index]; break;
+        case FG_ROLE_STATE: {
+            const uint32_t k = p->opt_inputs[index / 2];
+            nd = p->inputs[k];
+            slot = (index % 2) ? p->v_slot[k] : p->m_slot[k];
+            break;
+        }
+    }
+    if (d_ptr) *d_ptr = p->ptr(slot);
+    if (bytes) *bytes = p->slots[slot].bytes;
+    if (node) *node = nd;
+    return FG_OK;
+}
+
+FG_API int fg_plan_bind_input(fg_plan *p, int index, void *d_ptr, uint64_t bytes) {
+    FG_REQUIRE(p && d_ptr, FG_ERR_INVALID_ARGUMENT, "fg_plan_bind_input: NULL argument");
+    FG_REQUIRE(index >= 0 && index < (int)p->inputs.size(), FG_ERR_OUT_OF_BOUNDS,
+               "fg_plan_bind_input: input %d out of range (%zu inputs)", index, p->inputs.size());
+    Slot &s = p->slots[p->input_slot[index]];
+    FG_REQUIRE(bytes >= s.bytes, FG_ERR_SHAPE,
+               "fg_plan_bind_input: input %d needs %llu bytes, got %llu", index,
+               (unsigned long long)s.bytes, (unsigned long long)bytes);
+    if (s.ext != d_ptr) {
+        s.ext = d_ptr;
+        p->mt_dirty = true;
+        drop_graph(*p);
+    }
+    return FG_OK;
+}
+
+FG_API int fg_plan_bind_target(fg_plan *p, const void *d_ptr, uint64_t bytes) {
+    FG_REQUIRE(p && d_ptr, FG_ERR_INVALID_ARGUMENT, "fg_plan_bind_target: NULL argument");
+    Slot &s = p->slots[p->target_slot];
+    FG_REQUIRE(bytes >= s.bytes, FG_ERR_SHAPE,
+               "fg_plan_bind_target: target needs %llu bytes, got %llu",
+               (unsigned long long)s.bytes, (unsigned long long)bytes);
+    if (s.ext != d_ptr) {
+        s.ext = const_cast<void *>(d_ptr);
+        drop_graph(*p);
+    }
+    return FG_OK;
+}
+
+FG_API int fg_plan_set_lr(fg_plan *p, float lr) {
+    FG_REQUIRE(p, FG_ERR_INVALID_ARGUMENT, "fg_plan_set_lr: plan is NULL");
+    if (p->lr != lr) drop_graph(*p);
+    p->lr = lr;
+    return FG_OK;
+}
+
+FG_API int fg_plan_set_adam(fg_plan *p, float b1, float b2, float eps) {
+    FG_REQUIRE(p, FG_ERR_INVALID_ARGUMENT, "fg_plan_set_adam: plan is NULL");
+    FG_REQUIRE(b1 >= 0.f && b1 < 1.f && b2 >= 0.f && b2 < 1.f && eps >= 0.f,
+               FG_ERR_INVALID_ARGUMENT, "fg_plan_set_adam: bad hyper-parameters");
+    drop_graph(*p);
+    p->b1 = b1;
+    p->b2 = b2;
+    p->eps = eps;
+    return FG_OK;
+}
+
+FG_API int fg_plan_forward(fg_plan *p) {
+    FG_REQUIRE(p && p->ctx, FG_ERR_INVALID_ARGUMENT, "fg_plan_forward: plan is NULL or has no device (dry plan)");
+    FG_HIP(hipSetDevice(p->ctx->device));
+    for (size_t k = 0; k < p->inputs.size(); ++k)
+        FG_REQUIRE(p->ptr(p->input_slot[k]), FG_ERR_INVALID_ARGUMENT,
+                   "dispatch_forward: input %zu is not bound", k);
+    return run(*p, p->fwd);
+}
+
+FG_API int fg_plan_loss(fg_plan *p) {
+    FG_REQUIRE(p && p->ctx, FG_ERR_INVALID_ARGUMENT, "fg_plan_loss: plan is NULL or has no device (dry plan)");
+    FG_REQUIRE(p->ptr(p->target_slot), FG_ERR_INVALID_ARGUMENT,
+               "dispatch_loss: no target bound (fg_plan_bind_target)");
+    FG_HIP(hipSetDevice(p->ctx->device));
+    int rc = run(*p, p->loss);
+    if (rc == FG_OK && p->ce_fused_possible) p->ce_fused_pending = true;
+    return rc;
+}
+
+FG_API int fg_plan_backward(fg_plan *p) {
+    FG_REQUIRE(p && p->ctx, FG_ERR_INVALID_ARGUMENT, "fg_plan_backward: plan is NULL or has no device (dry plan)");
+    FG_HIP(hipSetDevice(p->ctx->device));
+    const bool fused = p->ce_fused_pending;
+    p->ce_fused_pending = false;
+    return run(*p, fused ? p->bwd_fused : p->bwd_seed);
+}
+
+FG_API int fg_plan_optim(fg_plan *p) {
+    FG_REQUIRE(p && p->ctx, FG_ERR_INVALID_ARGUMENT, "fg_plan_optim: plan is NULL or has no device (dry plan)");
+    FG_HIP(hipSetDevice(p->ctx->device));
+    int rc = ensure_mt(*p);
+    if (rc) return rc;
+    return run_optim(*p, p->mt_all);
+}
+
+FG_API int fg_plan_single_optim(fg_plan *p, int input_index) {
+    FG_REQUIRE(p && p->ctx, FG_ERR_INVALID_ARGUMENT, "fg_plan_single_optim: plan is NULL or has no device (dry plan)");
+    FG_REQUIRE(input_index >= 0 && input_index < (int)p->inputs.size(), FG_ERR_OUT_OF_BOUNDS,
+               "fg_plan_single_optim: input %d out of range", input_index);
+    FG_HIP(hipSetDevice(p->ctx->device));
+    int rc = ensure_mt(*p);
+    if (rc) return rc;
+    FG_REQUIRE(p->g.optim != FG_OPTIM_ADAM, FG_ERR_UNSUPPORTED,
+               "fg_plan_single_optim: Adam keeps one step counter per plan; use fg_plan_optim");
+    return run_optim(*p, p->mt_single[input_index]);
+}
+
+FG_API int fg_plan_capture_step(fg_plan *p) {
+    FG_REQUIRE(p && p->ctx, FG_ERR_INVALID_ARGUMENT, "fg_plan_capture_step: plan is NULL or has no device (dry plan)");
+    FG_HIP(hipSetDevice(p->ctx->device));
+    for (size_t k = 0; k < p->inputs.size(); ++k)
+        FG_REQUIRE(p->ptr(p->input_slot[k]), FG_ERR_INVALID_ARGUMENT,
+                   "fg_plan_capture_step: input %zu is not bound", k);
+    FG_REQUIRE(p->ptr(p->target_slot), FG_ERR_INVALID_ARGUMENT,
+               "fg_plan_capture_step: no target bound");
+    int rc = ensure_mt(*p);  // allocates: must precede capture
+    if (rc) return rc;
+    drop_graph(*p);
+    FG_HIP(hipStreamSynchronize(p->ctx->stream));
+    FG_HIP(hipStreamBeginCapture(p->ctx->stream, hipStreamCaptureModeThreadLocal));
+    rc = run(*p, p->fwd);
+    if (rc == FG_OK) rc = run(*p, p->loss);
+    if (rc == FG_OK) rc = run(*p, p->ce_fused_possible ? p->bwd_fused : p->bwd_seed);
+    if (rc == FG_OK) rc = run_optim(*p, p->mt_all);
+    hipGraph_t graph = nullptr;
+    hipError_t e = hipStreamEndCapture(p->ctx->stream, &graph);
+    if (rc != FG_OK) {
+        if (graph) (void)hipGraphDestroy(graph);
+        return rc;
+    }
+    if (e != hipSuccess) return fg::hip_fail(e, "hipStreamEndCapture", __FILE__, __LINE__);
+    hipGraphExec_t exec = nullptr;
+    e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(graph);
+        return fg::hip_fail(e, "hipGraphInstantiate", __FILE__, __LINE__);
+    }
+    p->graph = graph;
+    p->exec = exec;
+    return FG_OK;
+}
+
+FG_API int fg_plan_launch_step(fg_plan *p) {
+    FG_REQUIRE(p && p->ctx, FG_ERR_INVALID_ARGUMENT, "fg_plan_launch_step: plan is NULL or has no device (dry plan)");
+    FG_REQUIRE(p->exec, FG_ERR_INVALID_ARGUMENT,
+               "fg_plan_launch_step: no captured step (call fg_plan_capture_step; rebinding "
+               "inputs, target or hyper-parameters drops the capture)");
+    FG_HIP(hipSetDevice(p->ctx->device));
+    FG_HIP(hipGraphLaunch(p->exec, p->ctx->stream));
+    return FG_OK;
+}
+
+FG_API int fg_plan_describe(const fg_plan *p, char *buf, size_t len, size_t *needed) {
+    FG_REQUIRE(p, FG_ERR_INVALID_ARGUMENT, "fg_plan_describe: plan is NULL");
+    std::string s;
+    auto add = [&](const char *title, const std::vector<Launch> &v) {
+        s += std::string(title) + ": " + std::to_string(v.size()) + " launches\n";
+        for (const Launch &L : v) s += "  " + L.desc + "\n";
+    };
+    add("forward", p->fwd);
+    add("loss", p->loss);
+    add("backward(seed)", p->bwd_seed);
+    if (p->ce_fused_possible) add("backward(ce-fused)", p->bwd_fused);
+    s += "optim: " + std::string(p->g.optim == FG_OPTIM_ADAM ? "adam" : "sgd") + " over " +
+         std::to_string(p->opt_inputs.size()) + " inputs, 1 multi-tensor launch\n";
+    s += "arena: " + std::to_string(p->arena_bytes) + " bytes\n";
+    if (needed) *needed = s.size() + 1;
+    if (buf && len) {
+        const size_t n = std::min(len - 1, s.size());
+        std::memcpy(buf, s.data(), n);
+        buf[n] = 0;
+    }
+    return FG_OK;
+}

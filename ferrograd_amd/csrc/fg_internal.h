@@ -44,6 +44,16 @@ namespace fg {
 // workspace with a synchronizing reallocation if needed), or nullptr with
 // the error set.
 void *workspace(fg_ctx *ctx, uint64_t bytes);
+
+// Adam with device-resident step counter / bias-correction scalars
+// (k_optim.hip).  d_state points at adam_dev_state_bytes() zeroed bytes.
+uint64_t adam_dev_state_bytes();
+int mt_adam_dev(fg_ctx *ctx, fg_mt *mt, float lr, float b1, float b2, float eps, void *d_state,
+                int zero_grad);
+
+// Elementwise program launch (k_eltwise_prog.hip).
+struct EltProgram;
+int launch_eltwise(fg_ctx *ctx, const EltProgram &p);
 }  // namespace fg
 
 #define FG_HIP(call)                                                     \

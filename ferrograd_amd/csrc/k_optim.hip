@@ -130,6 +130,88 @@ __global__ __launch_bounds__(kThreads) void adam_mt_kernel(
     }
 }
 
+// Adam with its per-step scalars in device memory: a one-thread kernel
+// advances the step counter and derives step_size / inv_sqrt_bc2 (in
+// double, rounded once to fp32) so that a captured hipGraph replays correct
+// bias corrections on every step without host involvement.
+struct AdamDevState {
+    uint32_t step;
+    float step_size;
+    float inv_sqrt_bc2;
+    float pad;
+};
+
+__global__ void adam_advance_kernel(AdamDevState *st, double lr, double b1, double b2) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    const uint32_t t = st->step + 1;
+    st->step = t;
+    const double bc1 = 1.0 - pow(b1, (double)t);
+    const double bc2 = 1.0 - pow(b2, (double)t);
+    st->step_size = (float)(lr / bc1);
+    st->inv_sqrt_bc2 = (float)(1.0 / sqrt(bc2));
+}
+
+__global__ __launch_bounds__(kThreads) void adam_mt_dev_kernel(
+    const MTTensor *__restrict__ tensors, const MTChunk *__restrict__ chunks, float b1,
+    float b2, float eps, const AdamDevState *__restrict__ st, int zero_grad, int vec) {
+    const float step_size = st->step_size, inv_sqrt_bc2 = st->inv_sqrt_bc2;
+    const MTChunk c = chunks[blockIdx.x];
+    const MTTensor t = tensors[c.tensor];
+    const uint64_t end = (c.start + kChunk < t.n) ? c.start + kChunk : t.n;
+    const float omb1 = 1.0f - b1, omb2 = 1.0f - b2;
+    if (vec) {
+        f32x4 P[kUnroll], G[kUnroll], M[kUnroll], V[kUnroll];
+        uint64_t idx[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            idx[u] = c.start + (uint64_t)(u * kThreads + threadIdx.x) * 4;
+            if (idx[u] + 4 <= end) {
+                P[u] = ld_nt(t.p + idx[u]);
+                G[u] = ld_nt(t.g + idx[u]);
+                M[u] = ld_nt(t.m + idx[u]);
+                V[u] = ld_nt(t.v + idx[u]);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            if (idx[u] + 4 <= end) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float pe = P[u][e], me = M[u][e], ve = V[u][e];
+                    adam_elem(pe, G[u][e], me, ve, b1, omb1, b2, omb2, eps, step_size,
+                              inv_sqrt_bc2);
+                    P[u][e] = pe;
+                    M[u][e] = me;
+                    V[u][e] = ve;
+                }
+                st_nt(t.p + idx[u], P[u]);
+                st_nt(t.m + idx[u], M[u]);
+                st_nt(t.v + idx[u], V[u]);
+                if (zero_grad) st_nt(t.g + idx[u], f32x4{0.f, 0.f, 0.f, 0.f});
+            } else {
+                for (uint64_t i = idx[u]; i < end && i < idx[u] + 4; ++i) {
+                    float p = t.p[i], m = t.m[i], v = t.v[i];
+                    adam_elem(p, t.g[i], m, v, b1, omb1, b2, omb2, eps, step_size,
+                              inv_sqrt_bc2);
+                    t.p[i] = p;
+                    t.m[i] = m;
+                    t.v[i] = v;
+                    if (zero_grad) t.g[i] = 0.0f;
+                }
+            }
+        }
+    } else {
+        for (uint64_t i = c.start + threadIdx.x; i < end; i += kThreads) {
+            float p = t.p[i], m = t.m[i], v = t.v[i];
+            adam_elem(p, t.g[i], m, v, b1, omb1, b2, omb2, eps, step_size, inv_sqrt_bc2);
+            t.p[i] = p;
+            t.m[i] = m;
+            t.v[i] = v;
+            if (zero_grad) t.g[i] = 0.0f;
+        }
+    }
+}
+
 // basic_optim.rs:3-31: scaled = g*lr ; w = w - scaled ; g = 0
 __global__ __launch_bounds__(kThreads) void sgd_mt_kernel(const MTTensor *__restrict__ tensors,
                                                           const MTChunk *__restrict__ chunks,
@@ -266,6 +348,28 @@ FG_API int fg_adam_step_scalars(fg_ctx *ctx, fg_mt *mt, float b1, float b2, floa
     FG_LAUNCH_CHECK("adam_mt_kernel");
     return FG_OK;
 }
+
+namespace fg {
+
+uint64_t adam_dev_state_bytes() { return sizeof(AdamDevState); }
+
+// Advance the device step counter at d_state (zero-initialised
+// AdamDevState) and apply one Adam update with the derived scalars.
+int mt_adam_dev(fg_ctx *ctx, fg_mt *mt, float lr, float b1, float b2, float eps, void *d_state,
+                int zero_grad) {
+    FG_REQUIRE(ctx && mt && d_state, FG_ERR_INVALID_ARGUMENT, "mt_adam_dev: NULL argument");
+    FG_REQUIRE(mt->has_state, FG_ERR_INVALID_ARGUMENT,
+               "mt_adam_dev: tensor list was created without m/v state");
+    AdamDevState *st = reinterpret_cast<AdamDevState *>(d_state);
+    adam_advance_kernel<<<1, 64, 0, ctx->stream>>>(st, (double)lr, (double)b1, (double)b2);
+    FG_LAUNCH_CHECK("adam_advance_kernel");
+    adam_mt_dev_kernel<<<mt->nchunks, kThreads, 0, ctx->stream>>>(
+        mt->d_tensors, mt->d_chunks, b1, b2, eps, st, zero_grad, mt->vec);
+    FG_LAUNCH_CHECK("adam_mt_dev_kernel");
+    return FG_OK;
+}
+
+}  // namespace fg
 
 FG_API int fg_adam_step(fg_ctx *ctx, fg_mt *mt, float lr, float b1, float b2, float eps,
                         int step, int zero_grad) {

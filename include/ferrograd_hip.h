@@ -17,9 +17,10 @@
  *    all device work is enqueued on the context's stream, asynchronously,
  *    in call order.  fg_sync() waits for it.
  *  - No call allocates device memory except the fg_buf_*, fg_mt_create,
- *    fg_ctx_reserve_workspace and fg_graph_lower entry points (and the
- *    first call of a direct kernel that needs more workspace than the
- *    context holds).
+ *    fg_ctx_reserve_workspace and fg_plan_create entry points, the first
+ *    fg_plan_optim / fg_plan_capture_step after inputs are (re)bound (they
+ *    build the optimiser's tensor list), and the first call of a direct
+ *    kernel that needs more workspace than the context holds.
  */
 #ifndef FERROGRAD_HIP_H
 #define FERROGRAD_HIP_H
@@ -183,6 +184,137 @@ int fg_adam_step(fg_ctx *ctx, fg_mt *mt, float lr, float b1, float b2,
  * inv_sqrt_bc2 = 1/sqrt(1-b2^t) (what fg_adam_step derives). */
 int fg_adam_step_scalars(fg_ctx *ctx, fg_mt *mt, float b1, float b2, float eps,
                          float step_size, float inv_sqrt_bc2, int zero_grad);
+
+/* Raw host <-> device copies on the context's stream, synchronous with
+ * respect to the host buffer (GpuBackend::upload / download for buffers
+ * the plan owns, dispatch/mod.rs:161-261). */
+int fg_memcpy_h2d(fg_ctx *ctx, void *d_dst, const void *src, uint64_t bytes);
+int fg_memcpy_d2h(fg_ctx *ctx, void *dst, const void *d_src, uint64_t bytes);
+
+/* --------------------------------------------------------------- graph */
+/* Graph IR: the mirror of fused_gpu's Graph / Node / GraphOp
+ * (crates/fused_gpu/src/dispatch/backend/mod.rs:499-1316) with the
+ * ferrograd-nn builders as a fixed operation enum.  Node ids are creation
+ * order (mod.rs:1224-1235); the last node is the forward output. */
+typedef struct fg_graph fg_graph;
+
+/* LossType constants (crates/ferrograd-nn/src/loss/basic_loss.rs). */
+typedef enum fg_loss {
+    FG_LOSS_MSE = 0, /* MEAN_SQUARED_ERROR   (basic_loss.rs:3-27)   */
+    FG_LOSS_BCE = 1, /* BINARY_CROSS_ENTROPY (basic_loss.rs:29-89)  */
+    FG_LOSS_CE = 2   /* CROSS_ENTROPY        (basic_loss.rs:91-133) */
+} fg_loss;
+
+/* OptimType constants: SGD (ferrograd-nn optim/basic_optim.rs:3-31) and
+ * Adam (new; absent in the reference). */
+typedef enum fg_optim { FG_OPTIM_SGD = 0, FG_OPTIM_ADAM = 1 } fg_optim;
+
+/* Operations of the ferrograd-nn builders (crates/ferrograd-nn/src/op/,
+ * re-exported by crates/ferrograd/src/graph.rs:106-159).  BIAS_ADD is new:
+ * x[..., N] + b[N] broadcast over rows (the reference's add has no
+ * broadcast, binary.rs:53-63); ADD / SUB also accept that broadcast. */
+typedef enum fg_op {
+    FG_OP_INPUT = 0,
+    FG_OP_CONST = 1,
+    FG_OP_ADD = 2,
+    FG_OP_SUB = 3,
+    FG_OP_MUL = 4,
+    FG_OP_DIV = 5,
+    FG_OP_MATMUL = 6,
+    FG_OP_RELU = 7,
+    FG_OP_GELU = 8,
+    FG_OP_ELU = 9,
+    FG_OP_TANH = 10,
+    FG_OP_EXP = 11,
+    FG_OP_LOG = 12,
+    FG_OP_ABS = 13,
+    FG_OP_NEG = 14,
+    FG_OP_SOFTMAX = 15,
+    FG_OP_BIAS_ADD = 16
+} fg_op;
+
+/* Input flags (extension): every Input is trainable in ferrograd
+ * (kernel/backward.rs:95-106, dispatch/mod.rs:735-744). */
+#define FG_INPUT_NO_GRAD 0x1u /* compute no gradient for this input      */
+#define FG_INPUT_FROZEN 0x2u  /* compute its gradient, never update it    */
+
+/* Graph::new(loss, optim) (crates/ferrograd/src/graph.rs:34). */
+int fg_graph_create(int loss, int optim, fg_graph **out);
+int fg_graph_destroy(fg_graph *g);
+/* Metadata::new_field (backend/mod.rs:576-620): returns the meta index of a
+ * new dimension field (1, 2, ...; index 0 holds the learning rate). */
+int fg_graph_new_field(fg_graph *g, uint32_t *field);
+/* DefineOps::input(&[fields]) (graph.rs:111): an fp32 input whose dims are
+ * meta fields. */
+int fg_graph_input(fg_graph *g, const uint32_t *fields, int rank, uint32_t *node);
+/* DefineOps::constant_f32 (graph.rs:106-159): a scalar constant. */
+int fg_graph_constant_f32(fg_graph *g, float value, uint32_t *node);
+/* DefineOps::{add,sub,mul,div,matmul,relu,...,softmax}: node from op and
+ * inputs (ids must exist already). */
+int fg_graph_op(fg_graph *g, int op, const uint32_t *inputs, int n_inputs, uint32_t *node);
+int fg_graph_set_input_flags(fg_graph *g, uint32_t node, uint32_t flags);
+int fg_graph_num_nodes(const fg_graph *g, uint32_t *n);
+/* Graph::validate (backend/mod.rs:853-975, 1172-1185) against a meta
+ * binding [lr_bits, dim1, dim2, ...]; any positive dims are accepted (the
+ * reference requires multiples of 16, mod.rs:617-619). */
+int fg_graph_validate(const fg_graph *g, const uint32_t *meta, int n_meta);
+
+/* ---------------------------------------------------------------- plan */
+/* A lowered, allocated and scheduled graph: replaces Graph::lower +
+ * GpuContext::compile + alloc_tensors + schedule (kernel/mod.rs:107-152,
+ * dispatch/mod.rs:369-455, 509-575, 664-764).  All plan-owned tensors live
+ * in one device arena. */
+typedef struct fg_plan fg_plan;
+
+/* Buffer roles (AllocTensors, dispatch/mod.rs:835-845). */
+typedef enum fg_role {
+    FG_ROLE_FORWARD_OUT = 0,   /* value of the last node                     */
+    FG_ROLE_SEED = 1,          /* dL/d(last node)                            */
+    FG_ROLE_LOSS = 2,          /* loss_t: per element (MSE/BCE, CE on probs), */
+                               /* per row (CE fused with a final softmax)     */
+    FG_ROLE_FORWARD_SAVED = 3, /* saved forward values, SaveIndicator order  */
+    FG_ROLE_GRAD = 4,          /* grad_tensors, SaveIndicator order          */
+    FG_ROLE_INPUT = 5,         /* bound input tensors, input order           */
+    FG_ROLE_STATE = 6,         /* optimiser state (Adam m, v per input)      */
+    FG_ROLE_MEAN_LOSS = 7,     /* scalar mean loss (CE fused)                */
+    FG_ROLE_TARGET = 8         /* bound loss target                          */
+} fg_role;
+
+/* ctx may be NULL for a dry plan: lowering only (fg_plan_describe and
+ * fg_plan_count work; nothing is allocated and dispatch fails). */
+int fg_plan_create(fg_ctx *ctx, const fg_graph *g, const uint32_t *meta, int n_meta,
+                   fg_plan **out);
+int fg_plan_destroy(fg_plan *p);
+int fg_plan_count(const fg_plan *p, int role, int *count);
+/* Device address, byte size and node id of a role's index-th tensor. */
+int fg_plan_tensor(const fg_plan *p, int role, int index, void **d_ptr, uint64_t *bytes,
+                   uint32_t *node);
+/* Bind the index-th input (input order) / the loss target to caller-owned
+ * device memory (the reference passes in_tensors and the target to
+ * schedule / dispatch_loss, dispatch/mod.rs:664-788).  CE targets are u32
+ * labels, one per row of the last node; MSE / BCE targets match its shape. */
+int fg_plan_bind_input(fg_plan *p, int index, void *d_ptr, uint64_t bytes);
+int fg_plan_bind_target(fg_plan *p, const void *d_ptr, uint64_t bytes);
+/* Learning rate (meta field 0, kernel/optim.rs:119-131) and Adam betas/eps. */
+int fg_plan_set_lr(fg_plan *p, float lr);
+int fg_plan_set_adam(fg_plan *p, float b1, float b2, float eps);
+/* dispatch_forward / dispatch_loss / dispatch_backward / dispatch_optim /
+ * dispatch_single_optim (dispatch/mod.rs:766-814), enqueued on the stream.
+ * After fg_plan_loss with CE on a final softmax, the next fg_plan_backward
+ * starts from dlogits = p - onehot (the CE gradient is not pushed through
+ * the softmax Jacobian again); otherwise it starts from the seed buffer. */
+int fg_plan_forward(fg_plan *p);
+int fg_plan_loss(fg_plan *p);
+int fg_plan_backward(fg_plan *p);
+int fg_plan_optim(fg_plan *p);
+int fg_plan_single_optim(fg_plan *p, int input_index);
+/* Capture forward + loss + backward + optim into one hipGraph (replayed by
+ * fg_plan_launch_step); re-capture after rebinding inputs or target. */
+int fg_plan_capture_step(fg_plan *p);
+int fg_plan_launch_step(fg_plan *p);
+/* Human-readable launch list ("forward: gemm NN 64x256x784 bias+relu ...")
+ * written to buf (truncated to len); *needed receives the full length. */
+int fg_plan_describe(const fg_plan *p, char *buf, size_t len, size_t *needed);
 
 /* ----------------------------------------------------- synthetic data */
 /* Counter-based SplitMix64 generator keyed by (seed, tensor_id): element i

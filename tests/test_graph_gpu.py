@@ -1,0 +1,565 @@
+"""GPU tests of the graph path (planner + executor) through the ferrograd
+API mirror.
+
+The first block re-hosts the reference's own integration tests
+(crates/ferrograd/tests/std_wgsl.rs, tests/optim.rs) with their exact
+closed-form expectations; the rest compare whole training steps with the CPU
+oracle (BASELINE configs c1 and a reduced c5), the three losses and every
+elementwise op's backward with float64 numpy, and check that a captured
+hipGraph step replays like the eager step.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import normwise_rel
+
+pytestmark = pytest.mark.gpu
+
+f32 = np.float32
+
+
+def api():
+    from ferrograd_amd import graph as G
+    return G
+
+
+@pytest.fixture(scope="module")
+def ctx(gpu_ctx):
+    from ferrograd_amd.graph import GpuContext
+    return GpuContext(gpu_ctx)
+
+
+def new_graph(loss, optim=None):
+    G = api()
+    return G.Graph(loss, (optim or G.Optim.sgd()).lower), G.Metadata.new()
+
+
+# ------------------------------------------------ reference tests, re-hosted
+def test_mul_add_forward_backward(ctx):
+    """std_wgsl.rs:10-94."""
+    G = api()
+    graph, meta = new_graph(G.MEAN_SQUARED_ERROR)
+    m, n = meta.new_field(), meta.new_field()
+    with graph.define_ops() as ops:
+        a = ops.input([m, n], G.SimpleDType.F32)
+        b = ops.input([m, n], G.SimpleDType.F32)
+        c = ops.input([m, n], G.SimpleDType.F32)
+        x = ops.mul(a, b)
+        ops.add(c, x)
+    saved = graph.compute_saved_nodes()
+    graph.validate(meta)
+    mb = [G.f32_bits(1e-3), 32, 32]
+    assert meta.validate_meta(mb)
+    mb = ctx.alloc_meta(mb)
+    st = ctx.alloc_tensors(graph, saved, mb, G.Optim.sgd().state)
+    kernels = ctx.compile(graph.lower(meta, None, saved))
+    ins = [ctx.init_tensor_f32([32, 32], [3.0] * 1024), ctx.init_tensor_f32([32, 32], [2.0] * 1024),
+           ctx.init_tensor_f32([32, 32], [1.0] * 1024)]
+    ctx.upload(st.seed, [1.0] * 1024, 0)
+    sch = ctx.schedule(kernels, mb, ins, st, [], G.Optim.sgd().state)
+    ctx.dispatch_forward(sch)
+    ctx.dispatch_backward(sch)
+    ctx.sync()
+    assert np.all(ctx.download(st.forward_out) == 7.0)
+    assert np.all(ctx.download(st.grad_tensors[0]) == 2.0)
+    assert np.all(ctx.download(st.grad_tensors[1]) == 3.0)
+    assert np.all(ctx.download(st.grad_tensors[2]) == 1.0)
+
+
+def test_matmul_sub_softmax_forward_backward(ctx):
+    """std_wgsl.rs:97-187: softmax(c - a@b), seed 1 -> every grad 0."""
+    G = api()
+    graph, meta = new_graph(G.CROSS_ENTROPY)
+    m, n, k = meta.new_field(), meta.new_field(), meta.new_field()
+    with graph.define_ops() as ops:
+        a = ops.input([m, k])
+        b = ops.input([k, n])
+        c = ops.input([m, n])
+        ops.softmax(ops.sub(c, ops.matmul(a, b)))
+    mb = [G.f32_bits(1e-3), 16, 64, 32]
+    st = ctx.alloc_tensors(graph, graph.compute_saved_nodes(), mb)
+    ins = [ctx.init_tensor_f32([16, 32], [3.0] * 512), ctx.init_tensor_f32([32, 64], [2.0] * 2048),
+           ctx.init_tensor_f32([16, 64], [1.0] * 1024)]
+    ctx.upload(st.seed, [1.0] * 1024, 0)
+    sch = ctx.schedule(graph.lower(meta), mb, ins, st)
+    ctx.dispatch_forward(sch)
+    ctx.dispatch_backward(sch)
+    ctx.sync()
+    assert np.all(ctx.download(st.forward_out) == f32(1 / 64))
+    assert np.all(ctx.download(st.grad_tensors[0])[:512] == 0.0)
+    assert np.all(ctx.download(st.grad_tensors[1]) == 0.0)
+    assert np.all(ctx.download(st.grad_tensors[2])[:1024] == 0.0)
+
+
+def test_div_const_softmax_forward_backward(ctx):
+    """std_wgsl.rs:190-265: softmax(2/x) + 2 -> 2 + 1/32, grad 0."""
+    G = api()
+    graph, meta = new_graph(G.CROSS_ENTROPY)
+    m, n = meta.new_field(), meta.new_field()
+    with graph.define_ops() as ops:
+        x = ops.input([m, n])
+        two = ops.constant_f32(2.0)
+        ops.add(ops.softmax(ops.div(two, x)), two)
+    mb = [G.f32_bits(1e-3), 16, 32]
+    st = ctx.alloc_tensors(graph, graph.compute_saved_nodes(), mb)
+    ins = [ctx.init_tensor_f32([16, 32], [3.0] * 512)]
+    ctx.upload(st.seed, [1.0] * 512, 0)
+    sch = ctx.schedule(graph.lower(meta), mb, ins, st)
+    ctx.dispatch_forward(sch)
+    ctx.dispatch_backward(sch)
+    ctx.sync()
+    assert np.all(ctx.download(st.forward_out) == f32(2.0 + 1.0 / 32.0))
+    assert np.all(ctx.download(st.grad_tensors[0]) == 0.0)
+
+
+def test_matmul_add_forward_backward(ctx):
+    """std_wgsl.rs:268-373: a@b + c -> 97; dA 128, dB 96, dC 1."""
+    G = api()
+    M, N, K = 32, 64, 16
+    graph, meta = new_graph(G.MEAN_SQUARED_ERROR)
+    m, n, k = meta.new_field(), meta.new_field(), meta.new_field()
+    with graph.define_ops() as ops:
+        a = ops.input([m, k])
+        b = ops.input([k, n])
+        c = ops.input([m, n])
+        ops.add(ops.matmul(a, b), c)
+    mb = [G.f32_bits(1e-3), M, N, K]
+    st = ctx.alloc_tensors(graph, graph.compute_saved_nodes(), mb)
+    ins = [ctx.init_tensor_f32([M, K], [3.0] * (M * K)), ctx.init_tensor_f32([K, N], [2.0] * (K * N)),
+           ctx.init_tensor_f32([M, N], [1.0] * (M * N))]
+    ctx.upload(st.seed, [1.0] * (M * N), 0)
+    sch = ctx.schedule(graph.lower(meta), mb, ins, st)
+    ctx.dispatch_forward(sch)
+    ctx.dispatch_backward(sch)
+    ctx.sync()
+    assert np.all(ctx.download(st.forward_out) == 97.0)
+    assert np.all(ctx.download(st.grad_tensors[0]) == 128.0)
+    assert np.all(ctx.download(st.grad_tensors[1]) == 96.0)
+    assert np.all(ctx.download(st.grad_tensors[2]) == 1.0)
+
+
+def test_matmul_chain3_forward_backward(ctx):
+    """std_wgsl.rs:376-520."""
+    G = api()
+    M, N, K, H = 32, 64, 128, 256
+    A_VAL, B_VAL, C_VAL, D_VAL, E_VAL = 3.0, 2.0, 1.0, 0.5, 1.0
+    X_VAL = A_VAL * B_VAL * K
+    Y_VAL = C_VAL * X_VAL * M
+    Z_VAL = Y_VAL * D_VAL * N
+    Y_GRAD = D_VAL * H
+    X_GRAD = Y_GRAD * C_VAL * H
+    D_GRAD = Y_VAL * H
+    C_GRAD = Y_GRAD * X_VAL * N
+    B_GRAD = A_VAL * X_GRAD * M
+    A_GRAD = X_GRAD * B_VAL * N
+    graph, meta = new_graph(G.MEAN_SQUARED_ERROR)
+    m, n, k, h = (meta.new_field() for _ in range(4))
+    with graph.define_ops() as ops:
+        a = ops.input([m, k])
+        b = ops.input([k, n])
+        c = ops.input([h, m])
+        d = ops.input([n, h])
+        e = ops.input([h, h])
+        x = ops.matmul(a, b)
+        y = ops.matmul(c, x)
+        z = ops.matmul(y, d)
+        ops.add(z, e)
+    mb = [G.f32_bits(1e-3), M, N, K, H]
+    st = ctx.alloc_tensors(graph, graph.compute_saved_nodes(), mb)
+    ins = [ctx.init_tensor_f32([M, K], [A_VAL] * (M * K)),
+           ctx.init_tensor_f32([K, N], [B_VAL] * (K * N)),
+           ctx.init_tensor_f32([H, M], [C_VAL] * (H * M)),
+           ctx.init_tensor_f32([N, H], [D_VAL] * (N * H)),
+           ctx.init_tensor_f32([H, H], [E_VAL] * (H * H))]
+    ctx.upload(st.seed, [1.0] * (H * H), 0)
+    sch = ctx.schedule(graph.lower(meta), mb, ins, st)
+    ctx.dispatch_forward(sch)
+    ctx.dispatch_backward(sch)
+    ctx.sync()
+    fs = st.forward_saved
+    assert np.all(ctx.download(fs[0]) == X_VAL)
+    assert np.all(ctx.download(fs[1]) == Y_VAL)
+    assert np.all(ctx.download(fs[2]) == Z_VAL)
+    assert np.all(ctx.download(st.forward_out) == Z_VAL + E_VAL)
+    gt = st.grad_tensors
+    assert np.all(ctx.download(gt[0]) == A_GRAD)
+    assert np.all(ctx.download(gt[1]) == B_GRAD)
+    assert np.all(ctx.download(gt[2]) == C_GRAD)
+    assert np.all(ctx.download(gt[3]) == D_GRAD)
+    assert np.all(ctx.download(gt[4]) == 1.0)
+
+
+def test_matmul_sub_forward_backward(ctx):
+    """std_wgsl.rs:523-653."""
+    G = api()
+    M, N, K = 32, 64, 128
+    graph, meta = new_graph(G.MEAN_SQUARED_ERROR)
+    m, n, k = meta.new_field(), meta.new_field(), meta.new_field()
+    with graph.define_ops() as ops:
+        a = ops.input([m, k])
+        b = ops.input([k, n])
+        c = ops.input([m, k])
+        d = ops.input([k, n])
+        ops.sub(ops.matmul(a, b), ops.matmul(c, d))
+    mb = [G.f32_bits(1e-3), M, N, K]
+    st = ctx.alloc_tensors(graph, graph.compute_saved_nodes(), mb)
+    ins = [ctx.init_tensor_f32([M, K], [3.0] * (M * K)), ctx.init_tensor_f32([K, N], [2.0] * (K * N)),
+           ctx.init_tensor_f32([M, K], [1.0] * (M * K)), ctx.init_tensor_f32([K, N], [0.5] * (K * N))]
+    ctx.upload(st.seed, [1.0] * (M * N), 0)
+    sch = ctx.schedule(graph.lower(meta), mb, ins, st)
+    ctx.dispatch_forward(sch)
+    ctx.dispatch_backward(sch)
+    ctx.sync()
+    assert np.all(ctx.download(st.forward_saved[0]) == 768.0)
+    assert np.all(ctx.download(st.forward_saved[1]) == 64.0)
+    assert np.all(ctx.download(st.forward_out) == 704.0)
+    gt = st.grad_tensors
+    assert np.all(ctx.download(gt[0]) == 128.0)
+    assert np.all(ctx.download(gt[1]) == 96.0)
+    assert np.all(ctx.download(gt[2]) == -32.0)
+    assert np.all(ctx.download(gt[3]) == -32.0)
+
+
+def _mul_add_optim(ctx, separate):
+    G = api()
+    graph, meta = new_graph(G.MEAN_SQUARED_ERROR)
+    m, n = meta.new_field(), meta.new_field()
+    with graph.define_ops() as ops:
+        a = ops.input([m, n])
+        b = ops.input([m, n])
+        c = ops.input([m, n])
+        ops.add(c, ops.mul(a, b))
+    mb = [G.f32_bits(1e-3), 32, 32]
+    st = ctx.alloc_tensors(graph, graph.compute_saved_nodes(), mb)
+    ins = [ctx.init_tensor_f32([32, 32], [3.0] * 1024), ctx.init_tensor_f32([32, 32], [2.0] * 1024),
+           ctx.init_tensor_f32([32, 32], [1.0] * 1024)]
+    ctx.upload(st.seed, [1.0] * 1024, 0)
+    sch = ctx.schedule(graph.lower(meta), mb, ins, st)
+    ctx.dispatch_forward(sch)
+    ctx.dispatch_backward(sch)
+    if separate:
+        for i, t in enumerate(ins):
+            ctx.dispatch_single_optim(sch, t, i, st)
+    else:
+        ctx.dispatch_optim(sch)
+    ctx.sync()
+    assert np.all(ctx.download(st.forward_out) == 7.0)
+    for gt in st.grad_tensors[:3]:
+        assert np.all(ctx.download(gt) == 0.0)
+    assert np.all(ctx.download(ins[0]) == f32(3.0) - f32(2e-3))
+    assert np.all(ctx.download(ins[1]) == f32(2.0) - f32(3e-3))
+    assert np.all(ctx.download(ins[2]) == f32(1.0) - f32(1e-3))
+
+
+def test_mul_add_optim(ctx):
+    """tests/optim.rs:10-104."""
+    _mul_add_optim(ctx, False)
+
+
+def test_mul_add_separate_optim(ctx):
+    """tests/optim.rs:107-207."""
+    _mul_add_optim(ctx, True)
+
+
+# --------------------------------------------------------- MLP steps
+def build_mlp(ctx, dims, batch, act, optim, trainable_x=False):
+    G = api()
+    graph, meta = new_graph(G.CROSS_ENTROPY, optim)
+    B = meta.new_field()
+    d = [meta.new_field() for _ in dims]
+    with graph.define_ops() as ops:
+        x = ops.input([B, d[0]], trainable=trainable_x)
+        h = x
+        for l in range(len(dims) - 1):
+            W = ops.input([d[l], d[l + 1]])
+            b = ops.input([d[l + 1]])
+            z = ops.bias_add(ops.matmul(h, W), b)
+            h = getattr(ops, act)(z) if l < len(dims) - 2 else z
+        ops.softmax(h)
+    mb = [G.f32_bits(1e-3), batch] + list(dims)
+    st = ctx.alloc_tensors(graph, graph.compute_saved_nodes(), mb)
+    return graph, meta, mb, st
+
+
+def oracle_mlp_step(X, Ws, bs, y, act):
+    L = len(Ws)
+    Zs, Hs = [], []
+    inp = X
+    for l in range(L):
+        a = O.ACT_NONE if l == L - 1 else act
+        Z, H = O.bias_act(O.gemm(O.NN, inp, Ws[l]), bs[l], a)
+        Zs.append(Z)
+        Hs.append(H)
+        inp = H
+    rl, dZ, _, mean = O.softmax_ce(Zs[-1], y)
+    dW, db = [None] * L, [None] * L
+    for l in range(L - 1, -1, -1):
+        prev = Hs[l - 1] if l > 0 else X
+        dW[l] = O.gemm(O.TN, prev, dZ)
+        db[l] = O.bias_grad(dZ)
+        up = O.gemm(O.NT, dZ, Ws[l])
+        dZ = O.act_bwd(act, up, Zs[l - 1]) if l > 0 else up
+    return mean, rl, dW, db, dZ, O.softmax(Zs[-1])
+
+
+def test_c1_two_layer_mlp_sgd_step(ctx):
+    """BASELINE config c1: batch 64, 784 -> 256 -> ReLU -> 10, CE, SGD lr 0.01;
+    Kaiming-uniform weights and zero biases from seed 0, inputs U[0,1),
+    labels U{0..9}.  Loss and every parameter gradient vs the oracle, then
+    the SGD update bit for bit."""
+    import ferrograd_amd as fa
+    G = api()
+    dims, B = [784, 256, 10], 64
+    graph, meta, mb, st = build_mlp(ctx, dims, B, "relu", G.Optim.sgd())
+    X = fa.rng_uniform(0, 0, (B, 784))
+    y = fa.rng_int(0, 1, (B,), 10)
+    Ws = [fa.rng_uniform(0, 10 + l, (dims[l], dims[l + 1]), -math.sqrt(6 / dims[l]),
+                         math.sqrt(6 / dims[l])) for l in range(2)]
+    bs = [np.zeros(d, f32) for d in dims[1:]]
+    ins = [ctx.init_tensor_f32(X.shape, X)]
+    for W, b in zip(Ws, bs):
+        ins += [ctx.init_tensor_f32(W.shape, W), ctx.init_tensor_f32(b.shape, b)]
+    tgt = ctx.new_onehot_init(y)
+    sch = ctx.schedule(graph.lower(meta), [G.f32_bits(0.01)] + mb[1:], ins, st)
+    ctx.dispatch_forward(sch)
+    ctx.dispatch_loss(sch, tgt)
+    ctx.dispatch_backward(sch)
+    ctx.sync()
+    mean, rl, dW, db, dX, probs = oracle_mlp_step(X, Ws, bs, y, O.ACT_RELU)
+    assert abs(float(ctx.download(st.mean_loss)[0]) - mean) < 1e-5 * max(1, abs(mean))
+    assert normwise_rel(ctx.download(st.loss_t), rl) < 1e-5
+    assert normwise_rel(ctx.download(st.forward_out).reshape(B, 10), probs) < 1e-5
+    tol = 1e-5 * math.sqrt(784)
+    grads = {t.node: ctx.download(t) for t in st.grad_tensors}
+    in_nodes = [i for i, nd in enumerate(graph.nodes) if nd.op == 0]
+    exp = [dX] + [v for pair in zip(dW, db) for v in pair]
+    for node, ref in zip(in_nodes, exp):
+        assert normwise_rel(grads[node].reshape(ref.shape), ref) < tol, node
+    # SGD: w - fl(g*lr), bit for bit against the oracle on the GPU's grads.
+    ctx.dispatch_optim(sch)
+    ctx.sync()
+    host_params = [Ws[0], bs[0], Ws[1], bs[1]]
+    for k, t in enumerate(ins[1:]):
+        w = host_params[k].copy().reshape(-1)
+        g = grads[in_nodes[k + 1]].copy()
+        O.sgd_(w, g, f32(0.01), True)
+        assert np.array_equal(ctx.download(t), w)
+    assert np.array_equal(ctx.download(ins[0]), X.reshape(-1))  # data input is frozen
+
+
+def test_mlp_gelu_adam_steps_match_oracle(ctx):
+    """A reduced c5 (GELU hidden layers, CE, Adam) for 3 steps: loss,
+    gradients and parameters against the oracle run on the same inputs."""
+    import ferrograd_amd as fa
+    G = api()
+    dims, B = [96, 128, 128, 40], 64
+    graph, meta, mb, st = build_mlp(ctx, dims, B, "gelu", G.Optim.adam())
+    X = fa.rng_normal(4, 0, (B, dims[0]))
+    y = fa.rng_int(4, 1, (B,), dims[-1])
+    Ws = [fa.rng_uniform(4, 10 + l, (dims[l], dims[l + 1]), -math.sqrt(6 / dims[l]),
+                         math.sqrt(6 / dims[l])) for l in range(3)]
+    bs = [np.zeros(d, f32) for d in dims[1:]]
+    ins = [ctx.init_tensor_f32(X.shape, X)]
+    for W, b in zip(Ws, bs):
+        ins += [ctx.init_tensor_f32(W.shape, W), ctx.init_tensor_f32(b.shape, b)]
+    tgt = ctx.new_onehot_init(y)
+    sch = ctx.schedule(graph.lower(meta), mb, ins, st)
+    P = [w.copy() for pair in zip(Ws, bs) for w in pair]
+    Mh = [np.zeros_like(p) for p in P]
+    Vh = [np.zeros_like(p) for p in P]
+    in_nodes = [i for i, nd in enumerate(graph.nodes) if nd.op == 0]
+    for step in range(1, 4):
+        ctx.dispatch_forward(sch)
+        ctx.dispatch_loss(sch, tgt)
+        ctx.dispatch_backward(sch)
+        ctx.sync()
+        grads = {t.node: ctx.download(t) for t in st.grad_tensors}
+        mean, rl, dW, db, dX, probs = oracle_mlp_step(X, P[0::2], P[1::2], y, O.ACT_GELU)
+        assert abs(float(ctx.download(st.mean_loss)[0]) - mean) < 1e-5 * max(1, abs(mean))
+        exp = [v for pair in zip(dW, db) for v in pair]
+        for node, ref in zip(in_nodes[1:], exp):
+            assert normwise_rel(grads[node].reshape(ref.shape), ref) < 1e-5 * math.sqrt(128)
+        ctx.dispatch_optim(sch)
+        ctx.sync()
+        # Oracle Adam on the GPU's own gradients: any difference is the
+        # update, not the gradient.
+        s, r = O.adam_scalars(f32(1e-3), f32(0.9), f32(0.999), step)
+        for k in range(len(P)):
+            g = grads[in_nodes[k + 1]].reshape(P[k].shape).copy()
+            O.adam_(P[k], g, Mh[k], Vh[k], f32(0.9), f32(0.999), f32(1e-8), s, r)
+            got = ctx.download(ins[k + 1]).reshape(P[k].shape)
+            assert normwise_rel(got, P[k]) < 1e-5, (step, k)
+            P[k] = got.copy()  # continue from the device state
+
+
+def test_captured_step_replays_like_eager(ctx):
+    """fg_plan_capture_step: 4 graph replays, each followed by eager work and
+    a sync, match 4 eager steps of an identical plan."""
+    import ferrograd_amd as fa
+    from ferrograd_amd._lib import call
+    G = api()
+    dims, B = [64, 96, 10], 32
+    runs = []
+    for captured in (False, True):
+        graph, meta, mb, st = build_mlp(ctx, dims, B, "gelu", G.Optim.adam())
+        X = fa.rng_normal(7, 0, (B, dims[0]))
+        y = fa.rng_int(7, 1, (B,), dims[-1])
+        ins = [ctx.init_tensor_f32(X.shape, X)]
+        for l in range(2):
+            W = fa.rng_uniform(7, 10 + l, (dims[l], dims[l + 1]), -0.3, 0.3)
+            ins += [ctx.init_tensor_f32(W.shape, W), ctx.init_tensor_f32((dims[l + 1],),
+                                                                         np.zeros(dims[l + 1]))]
+        tgt = ctx.new_onehot_init(y)
+        sch = ctx.schedule(graph.lower(meta), mb, ins, st)
+        hist = []
+        if captured:
+            call("fg_plan_bind_target", sch.plan.handle, tgt.data_ptr(), tgt.nbytes)
+            call("fg_plan_capture_step", sch.plan.handle)
+        for _ in range(4):
+            if captured:
+                call("fg_plan_launch_step", sch.plan.handle)
+                ctx.download(st.forward_out)  # eager work between replays
+            else:
+                ctx.dispatch_forward(sch)
+                ctx.dispatch_loss(sch, tgt)
+                ctx.dispatch_backward(sch)
+                ctx.dispatch_optim(sch)
+            ctx.sync()
+            hist.append([ctx.download(t).copy() for t in ins[1:]] +
+                        [ctx.download(st.mean_loss).copy()])
+        runs.append(hist)
+    for a, b in zip(*runs):
+        for x, y2 in zip(a, b):
+            assert np.array_equal(x, y2)
+
+
+# --------------------------------------------------- losses and elementwise
+@pytest.mark.parametrize("loss", ["MEAN_SQUARED_ERROR", "BINARY_CROSS_ENTROPY", "CROSS_ENTROPY"])
+def test_losses_on_tanh_output(ctx, loss):
+    """MSE / BCE / CE (no softmax) on pred = 0.5 + 0.4 tanh(x): loss_t and
+    backward against float64 numpy (basic_loss.rs:3-133; BCE's 1-pred is
+    taken from pred)."""
+    G = api()
+    R, C = 12, 10
+    graph, meta = new_graph(getattr(G, loss))
+    r, c = meta.new_field(), meta.new_field()
+    with graph.define_ops() as ops:
+        x = ops.input([r, c])
+        half, scale = ops.constant_f32(0.5), ops.constant_f32(0.4)
+        ops.add(ops.mul(ops.tanh(x), scale), half)
+    mb = [G.f32_bits(1e-3), R, C]
+    st = ctx.alloc_tensors(graph, graph.compute_saved_nodes(), mb)
+    rng = np.random.default_rng(5)
+    X = rng.standard_normal((R, C)).astype(f32)
+    ins = [ctx.init_tensor_f32([R, C], X)]
+    sch = ctx.schedule(graph.lower(meta), mb, ins, st)
+    p = 0.5 + 0.4 * np.tanh(X.astype(np.float64))
+    if loss == "CROSS_ENTROPY":
+        lab = rng.integers(0, C, R)
+        tgt = ctx.new_onehot_init(lab)
+        oh = np.eye(C)[lab]
+        exp_loss = np.where(oh > 0, -np.log(p), 0.0)
+        seed = p - oh
+    else:
+        T = rng.uniform(0, 1, (R, C)).astype(f32)
+        tgt = ctx.init_tensor_f32([R, C], T)
+        t = T.astype(np.float64)
+        if loss == "MEAN_SQUARED_ERROR":
+            exp_loss, seed = (p - t) ** 2, 2 * (p - t)
+        else:
+            exp_loss = -(t * np.log(p) + (1 - t) * np.log(1 - p))
+            seed = p - t
+    ctx.dispatch_forward(sch)
+    ctx.dispatch_loss(sch, tgt)
+    ctx.dispatch_backward(sch)
+    ctx.sync()
+    assert normwise_rel(ctx.download(st.forward_out).reshape(R, C), p) < 1e-6
+    assert normwise_rel(ctx.download(st.loss_t).reshape(R, C), exp_loss) < 1e-5
+    assert normwise_rel(ctx.download(st.seed).reshape(R, C), seed) < 1e-5
+    gx = seed * 0.4 * (1 - np.tanh(X.astype(np.float64)) ** 2)
+    assert normwise_rel(ctx.download(st.grad_tensors[0]).reshape(R, C), gx) < 1e-5
+
+
+UNARY = {
+    "relu": (lambda x: np.maximum(x, 0), lambda x: (x > 0).astype(float)),
+    "elu": (lambda x: np.where(x >= 0, x, np.expm1(x)), lambda x: np.where(x >= 0, 1.0, np.exp(x))),
+    "tanh": (np.tanh, lambda x: 1 - np.tanh(x) ** 2),
+    "exp": (np.exp, np.exp),
+    "abs": (np.abs, np.sign),
+    "neg": (lambda x: -x, lambda x: -np.ones_like(x)),
+    "log": (lambda x: np.log(np.abs(x) + 0.5), None),
+}
+
+
+@pytest.mark.parametrize("op", list(UNARY))
+def test_unary_forward_backward(ctx, op):
+    """Each unary op on a [17, 23] input, seed = random upstream gradient."""
+    G = api()
+    R, C = 17, 23
+    graph, meta = new_graph(G.MEAN_SQUARED_ERROR)
+    r, c = meta.new_field(), meta.new_field()
+    rng = np.random.default_rng(len(op))
+    X = rng.standard_normal((R, C)).astype(f32)
+    X[np.abs(X) < 1e-3] = 0.5  # keep away from relu / abs kinks
+    with graph.define_ops() as ops:
+        x = ops.input([r, c])
+        if op == "log":  # log(|x| + 0.5): the reference's log backward divides by its output
+            ops.log(ops.add(ops.abs(x), ops.constant_f32(0.5)))
+        else:
+            getattr(ops, op)(x)
+    mb = [G.f32_bits(1e-3), R, C]
+    st = ctx.alloc_tensors(graph, graph.compute_saved_nodes(), mb)
+    sch = ctx.schedule(graph.lower(meta), mb, [ctx.init_tensor_f32([R, C], X)], st)
+    seed = rng.standard_normal((R, C)).astype(f32)
+    ctx.upload(st.seed, seed)
+    ctx.dispatch_forward(sch)
+    ctx.dispatch_backward(sch)
+    ctx.sync()
+    x64 = X.astype(np.float64)
+    fwd, d = UNARY[op]
+    assert normwise_rel(ctx.download(st.forward_out).reshape(R, C), fwd(x64)) < 1e-6
+    if op == "log":
+        exp = seed / (np.abs(x64) + 0.5) * np.sign(x64)
+    else:
+        exp = seed * d(x64)
+    assert normwise_rel(ctx.download(st.grad_tensors[0]).reshape(R, C), exp) < 1e-5
+
+
+def test_binary_broadcast_and_div_backward(ctx):
+    """(a / b) * c - bias (row-broadcast sub): forward and every gradient
+    against float64 numpy, including the negated column reduction."""
+    G = api()
+    R, C = 9, 300
+    graph, meta = new_graph(G.MEAN_SQUARED_ERROR)
+    r, c = meta.new_field(), meta.new_field()
+    with graph.define_ops() as ops:
+        a = ops.input([r, c])
+        b = ops.input([r, c])
+        cc = ops.input([r, c])
+        bias = ops.input([c])
+        ops.sub(ops.mul(ops.div(a, b), cc), bias)
+    mb = [G.f32_bits(1e-3), R, C]
+    st = ctx.alloc_tensors(graph, graph.compute_saved_nodes(), mb)
+    rng = np.random.default_rng(3)
+    A = rng.standard_normal((R, C)).astype(f32)
+    Bv = (rng.uniform(0.5, 2.0, (R, C)) * rng.choice([-1, 1], (R, C))).astype(f32)
+    Cc = rng.standard_normal((R, C)).astype(f32)
+    bias = rng.standard_normal(C).astype(f32)
+    ins = [ctx.init_tensor_f32([R, C], A), ctx.init_tensor_f32([R, C], Bv),
+           ctx.init_tensor_f32([R, C], Cc), ctx.init_tensor_f32([C], bias)]
+    sch = ctx.schedule(graph.lower(meta), mb, ins, st)
+    seed = rng.standard_normal((R, C)).astype(f32)
+    ctx.upload(st.seed, seed)
+    ctx.dispatch_forward(sch)
+    ctx.dispatch_backward(sch)
+    ctx.sync()
+    a, b, c2, s = (v.astype(np.float64) for v in (A, Bv, Cc, seed))
+    assert normwise_rel(ctx.download(st.forward_out).reshape(R, C), a / b * c2 - bias) < 1e-6
+    g = {t.node: ctx.download(t) for t in st.grad_tensors}
+    assert normwise_rel(g[0].reshape(R, C), s * c2 / b) < 1e-5
+    assert normwise_rel(g[1].reshape(R, C), -s * c2 * a / b ** 2) < 1e-5
+    assert normwise_rel(g[2].reshape(R, C), s * a / b) < 1e-5
+    assert normwise_rel(g[3], -s.sum(0)) < 1e-5
