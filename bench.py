@@ -57,18 +57,92 @@ def event_time_ms(fn, reps: int) -> float:
     return start.elapsed_time(stop) / reps
 
 
-def init_c5(trainer, ctx) -> None:
-    """Config c5 data: X ~ N(0,1), labels U{0..999}, W Kaiming-uniform
-    U(-sqrt(6/fan_in), +sqrt(6/fan_in)), b = 0; seed 4 (device generator)."""
-    seed = 4
-    B = trainer.B
-    ctx.rng_normal(seed, 0, 0.0, 1.0, trainer.X, trainer.X.numel())
-    ctx.rng_int(seed, 1, trainer.dims[-1], trainer.labels, B)
-    for l, w in enumerate(trainer.W):
-        bound = math.sqrt(6.0 / trainer.dims[l])
-        ctx.rng_uniform(seed, 10 + l, -bound, bound, w, w.numel())
-    for b in trainer.b:
-        b.zero_()
+class C5Step:
+    """Config c5 built as a ferrograd graph and run through the planner:
+    X [2048,1024] ~ N(0,1), labels U{0..999}, W_l Kaiming-uniform
+    U(-sqrt(6/fan_in), +sqrt(6/fan_in)), b_l = 0 (seed 4, device generator);
+    matmul -> bias_add -> gelu per hidden layer, softmax + CROSS_ENTROPY,
+    Adam lr 1e-3.  X is an Input whose gradient is computed (ferrograd trains
+    every Input) but which the optimiser does not update."""
+
+    def __init__(self, ctx, dims, batch):
+        import torch
+
+        from ferrograd_amd import graph as G
+
+        self.G, self.ctx, self.dims, self.B = G, ctx, dims, batch
+        self.gctx = G.GpuContext(ctx)
+        graph, meta = G.Graph(G.CROSS_ENTROPY, G.Optim.adam().lower), G.Metadata.new()
+        fb = meta.new_field()
+        fd = [meta.new_field() for _ in dims]
+        L = len(dims) - 1
+        with graph.define_ops() as ops:
+            h = ops.input([fb, fd[0]], trainable=False)
+            self.w_nodes, self.b_nodes = [], []
+            for l in range(L):
+                W = ops.input([fd[l], fd[l + 1]])
+                b = ops.input([fd[l + 1]])
+                self.w_nodes.append(W)
+                self.b_nodes.append(b)
+                z = ops.bias_add(ops.matmul(h, W), b)
+                h = ops.gelu(z) if l < L - 1 else z
+            ops.softmax(h)
+        mb = [G.f32_bits(1e-3), batch] + list(dims)
+        self.st = self.gctx.alloc_tensors(graph, graph.compute_saved_nodes(), mb)
+        seed = 4
+        self.X = torch.empty((batch, dims[0]), device="cuda")
+        self.labels = torch.empty((batch,), device="cuda", dtype=torch.int32)
+        ctx.rng_normal(seed, 0, 0.0, 1.0, self.X, self.X.numel())
+        ctx.rng_int(seed, 1, dims[-1], self.labels, batch)
+        self.W = [torch.empty((dims[l], dims[l + 1]), device="cuda") for l in range(L)]
+        self.b = [torch.zeros((dims[l + 1],), device="cuda") for l in range(L)]
+        for l, w in enumerate(self.W):
+            bound = math.sqrt(6.0 / dims[l])
+            ctx.rng_uniform(seed, 10 + l, -bound, bound, w, w.numel())
+        ins = [self.X]
+        for w, b in zip(self.W, self.b):
+            ins += [w, b]
+        self.sch = self.gctx.schedule(graph.lower(meta), mb, ins, self.st)
+        gmap = {t.node: t for t in self.st.grad_tensors}
+        self.dW = [gmap[n] for n in self.w_nodes]
+        self.db = [gmap[n] for n in self.b_nodes]
+        self.describe = self.sch.plan.describe()
+
+    def forward(self):
+        self.gctx.dispatch_forward(self.sch)
+
+    def loss(self):
+        self.gctx.dispatch_loss(self.sch, self.labels)
+
+    def backward(self):
+        self.gctx.dispatch_backward(self.sch)
+
+    def step_eager(self):
+        self.forward()
+        self.loss()
+        self.backward()
+        self.gctx.dispatch_optim(self.sch)
+
+    def capture(self):
+        self.gctx.capture_step(self.sch, self.labels)
+
+    def step_graph(self):
+        self.gctx.launch_step(self.sch)
+
+    def mean_loss(self) -> float:
+        return float(self.gctx.download(self.st.mean_loss)[0])
+
+    def download(self, t):
+        return self.gctx.download(t)
+
+    def gemm_flops(self) -> int:
+        """Algorithmic GEMM flops of one step: forward, dW, and dX for every
+        layer including the data input (2*M*N*K per GEMM)."""
+        return 2 * self.B * sum(self.dims[l] * self.dims[l + 1]
+                                for l in range(len(self.dims) - 1)) * 3
+
+    def num_params(self) -> int:
+        return sum(w.numel() for w in self.W) + sum(b.numel() for b in self.b)
 
 
 def gemm_components(ctx, reps: int):
@@ -214,42 +288,53 @@ def main() -> int:
     import torch
 
     import ferrograd_amd as fa
-    from ferrograd_amd.mlp import MLPTrainStep
 
     ctx, _stream = fa.torch_context(0)
     log(f"device {ctx.arch}, {ctx.cu_count} CUs")
     dims = [1024] + [4096] * 7 + [1000]
     batch = 2048
-    tr = MLPTrainStep(ctx, dims, batch, fa.ACT_GELU, optim="adam", lr=1e-3, data_grad=True)
-    init_c5(tr, ctx)
+    tr = C5Step(ctx, dims, batch)
+    log("plan:\n" + tr.describe)
     torch.cuda.synchronize()
     host = None
     if not args.no_cpu:
         host = {"X": tr.X.cpu().numpy(), "y": tr.labels.cpu().numpy().view(np.uint32),
                 "W": [w.cpu().numpy() for w in tr.W]}
     # First step (from the initial state) doubles as the parity sample.
-    tr.step()
+    tr.step_eager()
     torch.cuda.synchronize()
-    first = {"mean_loss": float(tr.loss.cpu()[0]), "dW": [w.cpu().numpy() for w in tr.dW],
-             "db": [b.cpu().numpy() for b in tr.db], "W": [w.cpu().numpy() for w in tr.W]}
+    first = {"mean_loss": tr.mean_loss(),
+             "dW": [tr.download(t).reshape(w.shape) for t, w in zip(tr.dW, tr.W)],
+             "db": [tr.download(t) for t in tr.db], "W": [w.cpu().numpy() for w in tr.W]}
     for _ in range(max(0, args.warmup - 1)):
-        tr.step()
+        tr.step_eager()
     torch.cuda.synchronize()
-    log(f"warmup done ({args.warmup} steps); timing {args.steps} steps")
+    # Eager launches (host-driven, one call per kernel).
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        tr.step()
+        tr.step_eager()
+    torch.cuda.synchronize()
+    eager_ms = 1000.0 * (time.perf_counter() - t0) / args.steps
+    # The whole step captured once into a hipGraph and replayed.
+    tr.capture()
+    tr.step_graph()
+    torch.cuda.synchronize()
+    log(f"warmup done ({args.warmup} eager steps, eager {eager_ms:.3f} ms/step); "
+        f"timing {args.steps} captured steps")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        tr.step_graph()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms_per_step = 1000.0 * elapsed / args.steps
     steps_per_s = args.steps / elapsed
-    log(f"c5 step: {ms_per_step:.3f} ms ({steps_per_s:.2f} steps/s)")
+    log(f"c5 step: {ms_per_step:.3f} ms ({steps_per_s:.2f} steps/s); loss {tr.mean_loss():.4f}")
 
     # Per-phase breakdown (events).
     phases = {
+        "eager_step_ms": eager_ms,
         "forward_ms": event_time_ms(tr.forward, 5),
-        "loss_ms": event_time_ms(tr.loss_and_grad, 5),
-        "backward_ms": event_time_ms(tr.backward, 5),
+        "loss_backward_ms": event_time_ms(lambda: (tr.loss(), tr.backward()), 5),
     }
     step_flops = tr.gemm_flops()
 
@@ -329,8 +414,6 @@ def main() -> int:
         "cpu_baseline": cpu,
         "parity": parity,
     }
-    tr.close()
-    ctx.close()
     print(json.dumps(result), flush=True)
     return 0
 

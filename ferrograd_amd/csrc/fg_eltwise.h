@@ -12,7 +12,7 @@
 namespace fg {
 
 enum EltOp : uint8_t {
-    kEltLoad = 0,   // r[dst] = src[a] at the element (mode of src a)
+    kEltLoad = 0,   // r[dst] = src[a] at the element, addressing mode c
     kEltImm,        // r[dst] = imm
     kEltStore,      // dsts[a][i] = r[b]
     kEltAccum,      // dsts[a][i] += r[b]
@@ -54,13 +54,19 @@ struct EltInstr {
     float imm;
 };
 
+// Passed by value as the kernel argument.  Every field the kernel indexes
+// with a run-time value (src, dst, ins) has elements of at least 4 bytes:
+// the compiler may reuse a computed element address as the base of a scalar
+// (SMEM) load, and SMEM ignores the low two address bits, so an array of
+// bytes indexed next to the pointer array once produced misaligned pointer
+// reads.  The addressing mode of a load therefore travels in the
+// instruction (field c), not in a byte array.
 struct EltProgram {
     const float *src[kEltMaxSrc];
     float *dst[kEltMaxDst];
     const uint32_t *labels;
     uint64_t n;     // elements
     uint32_t cols;  // row length (for row-broadcast and labels)
-    uint8_t src_mode[kEltMaxSrc];
     int32_t n_instr;
     EltInstr ins[kEltMaxInstr];
 };

@@ -370,19 +370,18 @@ struct EltBuilder {
     // Load value of node x (slot s, shape xs) into a register for an output
     // of numel/cols.
     int load(int slot, const Shape &xs) {
-        for (int k = 0; k < nsrc; ++k)
-            if (L.src_slot[k] == slot) {
-                const int r = reg();
-                ins(fg::kEltLoad, r, k);
-                return r;
-            }
-        const int k = nsrc++;
-        L.src_slot[k] = slot;
-        L.prog.src_mode[k] = xs.scalar ? fg::kModeScalar
-                             : (xs.vector && xs.numel() != numel) ? fg::kModeRow
-                                                                    : fg::kModeFull;
+        const int mode = xs.scalar ? fg::kModeScalar
+                         : (xs.vector && xs.numel() != numel) ? fg::kModeRow
+                                                                : fg::kModeFull;
+        int k = kNone;
+        for (int j = 0; j < nsrc; ++j)
+            if (L.src_slot[j] == slot) k = j;
+        if (k == kNone) {
+            k = nsrc++;
+            L.src_slot[k] = slot;
+        }
         const int r = reg();
-        ins(fg::kEltLoad, r, k);
+        ins(fg::kEltLoad, r, k, 0, mode);
         return r;
     }
     int operand(uint32_t x) {
@@ -900,6 +899,91 @@ int lower_backward(fg_plan &P, bool fused, std::vector<Launch> &out) {
     return FG_OK;
 }
 
+// ------------------------------------------------------- static checks
+int check_slot(const fg_plan &P, const Launch &L, int slot, uint64_t need, const char *what) {
+    if (slot == kNone) return FG_OK;
+    FG_REQUIRE(slot >= 0 && slot < (int)P.slots.size(), FG_ERR_INTERNAL,
+               "plan: %s of '%s' refers to slot %d of %zu", what, L.desc.c_str(), slot,
+               P.slots.size());
+    FG_REQUIRE(P.slots[slot].bytes >= need, FG_ERR_INTERNAL,
+               "plan: %s of '%s' needs %llu bytes, slot %d has %llu", what, L.desc.c_str(),
+               (unsigned long long)need, slot, (unsigned long long)P.slots[slot].bytes);
+    return FG_OK;
+}
+
+int check_launch(const fg_plan &P, const Launch &L) {
+    const uint64_t M = (uint64_t)L.M, N = (uint64_t)L.N, K = (uint64_t)L.K;
+    int rc = FG_OK;
+    auto chk = [&](int slot, uint64_t floats, const char *what) {
+        if (rc == FG_OK) rc = check_slot(P, L, slot, floats * 4, what);
+    };
+    switch (L.kind) {
+        case LK_GEMM:
+        case LK_GEMM_BWD:
+            chk(L.sA, M * K, "A");
+            chk(L.sB, K * N, "B");
+            chk(L.sC, M * N, "C");
+            chk(L.sZ, M * N, "Z");
+            chk(L.sBias, N, "bias");
+            break;
+        case LK_BIAS_GRAD:
+            chk(L.sA, M * N, "dZ");
+            chk(L.sC, N, "dbias");
+            break;
+        case LK_SOFTMAX:
+        case LK_SOFTMAX_BWD:
+            chk(L.sA, M * N, "x");
+            chk(L.sB, M * N, "dy");
+            chk(L.sC, M * N, "out");
+            break;
+        case LK_SMCE:
+            chk(L.sA, M * N, "logits");
+            chk(L.sZ, M, "labels");
+            chk(L.sB, M, "row loss");
+            chk(L.sBias, 1, "mean loss");
+            chk(L.sC, M * N, "dlogits");
+            break;
+        case LK_FILL0:
+            chk(L.sC, L.count, "fill");
+            break;
+        case LK_ELT: {
+            const fg::EltProgram &p = L.prog;
+            FG_REQUIRE(p.n_instr > 0 && p.n_instr <= fg::kEltMaxInstr, FG_ERR_INTERNAL,
+                       "plan: '%s' has %d instructions", L.desc.c_str(), p.n_instr);
+            for (int k = 0; k < p.n_instr && rc == FG_OK; ++k) {
+                const fg::EltInstr &in = p.ins[k];
+                FG_REQUIRE(in.dst < fg::kEltRegs && in.a < 16 && in.b < 16 && in.c < 16,
+                           FG_ERR_INTERNAL, "plan: '%s' instruction %d out of range",
+                           L.desc.c_str(), k);
+                if (in.op == fg::kEltLoad) {
+                    FG_REQUIRE(in.a < fg::kEltMaxSrc && L.src_slot[in.a] != kNone,
+                               FG_ERR_INTERNAL, "plan: '%s' loads unset source %d",
+                               L.desc.c_str(), in.a);
+                    const uint8_t mode = in.c;
+                    FG_REQUIRE(mode <= fg::kModeScalar, FG_ERR_INTERNAL,
+                               "plan: '%s' load with mode %d", L.desc.c_str(), mode);
+                    chk(L.src_slot[in.a],
+                        mode == fg::kModeScalar ? 1 : mode == fg::kModeRow ? p.cols : p.n,
+                        "source");
+                } else if (in.op == fg::kEltStore || in.op == fg::kEltAccum) {
+                    FG_REQUIRE(in.a < fg::kEltMaxDst && L.dst_slot[in.a] != kNone,
+                               FG_ERR_INTERNAL, "plan: '%s' stores to unset destination %d",
+                               L.desc.c_str(), in.a);
+                    chk(L.dst_slot[in.a], p.n, "destination");
+                } else if (in.op == fg::kEltLabelEq) {
+                    FG_REQUIRE(p.cols > 0 && L.label_slot != kNone, FG_ERR_INTERNAL,
+                               "plan: '%s' compares labels without labels", L.desc.c_str());
+                    chk(L.label_slot, p.n / p.cols, "labels");
+                }
+            }
+            break;
+        }
+        default:
+            break;
+    }
+    return rc;
+}
+
 // ------------------------------------------------------------ execute
 int run(fg_plan &P, const std::vector<Launch> &list) {
     fg_ctx *ctx = P.ctx;
@@ -1272,6 +1356,12 @@ FG_API int fg_plan_create(fg_ctx *ctx, const fg_graph *g, const uint32_t *meta, 
     if ((rc = lower_loss(*P))) return rc;
     if ((rc = lower_backward(*P, false, P->bwd_seed))) return rc;
     if (P->ce_fused_possible && (rc = lower_backward(*P, true, P->bwd_fused))) return rc;
+
+    // Static bounds check of every launch against the sizes of the slots it
+    // touches, so a planner slip is an error here rather than a device fault.
+    for (auto *list : {&P->fwd, &P->loss, &P->bwd_seed, &P->bwd_fused})
+        for (const Launch &L : *list)
+            if ((rc = check_launch(*P, L))) return rc;
 
     // Arena: every plan-owned tensor, 256-byte aligned, one allocation.
     uint64_t off = 0;

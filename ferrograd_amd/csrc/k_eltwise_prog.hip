@@ -14,8 +14,7 @@ namespace {
 
 constexpr int kThreads = 256;
 
-__device__ __forceinline__ float elt_load(const EltProgram &p, int s, uint64_t i) {
-    const uint8_t mode = p.src_mode[s];
+__device__ __forceinline__ float elt_load(const EltProgram &p, int s, int mode, uint64_t i) {
     if (mode == kModeScalar) return p.src[s][0];
     if (mode == kModeRow) return p.src[s][i % p.cols];
     return p.src[s][i];
@@ -30,7 +29,7 @@ __global__ __launch_bounds__(kThreads) void eltwise_prog_kernel(const EltProgram
         for (int k = 0; k < p.n_instr; ++k) {
             const EltInstr in = p.ins[k];
             switch (in.op) {
-                case kEltLoad: r[in.dst & 15] = elt_load(p, in.a, i); break;
+                case kEltLoad: r[in.dst & 15] = elt_load(p, in.a, in.c, i); break;
                 case kEltImm: r[in.dst & 15] = in.imm; break;
                 case kEltStore: p.dst[in.a][i] = r[in.b & 15]; break;
                 case kEltAccum: p.dst[in.a][i] += r[in.b & 15]; break;
@@ -91,7 +90,9 @@ int launch_eltwise(fg_ctx *ctx, const EltProgram &p) {
         if (in.op == kEltLoad) {
             FG_REQUIRE(in.a < kEltMaxSrc && p.src[in.a], FG_ERR_INTERNAL,
                        "eltwise program: load of missing source %d", in.a);
-            if (p.src_mode[in.a] == kModeRow) needs_cols = true;
+            FG_REQUIRE(in.c <= kModeScalar, FG_ERR_INTERNAL,
+                       "eltwise program: bad addressing mode %d", in.c);
+            if (in.c == kModeRow) needs_cols = true;
         }
         if (in.op == kEltStore || in.op == kEltAccum)
             FG_REQUIRE(in.a < kEltMaxDst && p.dst[in.a], FG_ERR_INTERNAL,

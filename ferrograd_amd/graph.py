@@ -500,6 +500,16 @@ class GpuContext:
     def sync(self) -> None:
         self.ctx.sync()
 
+    # ---------------------------------------------------- extensions
+    def capture_step(self, s: Schedule, target: Tensor) -> None:
+        """Capture forward + loss + backward + optim into one hipGraph."""
+        call("fg_plan_bind_target", s.plan.handle, target.data_ptr(), tensor_nbytes(target))
+        call("fg_plan_capture_step", s.plan.handle)
+
+    def launch_step(self, s: Schedule) -> None:
+        """Replay the captured training step."""
+        call("fg_plan_launch_step", s.plan.handle)
+
 
 def call_ptr(buf_handle) -> int:
     from ._lib import load
