@@ -56,10 +56,10 @@ EXTRA = {
 }
 
 
-def _compile(src: str) -> str:
+def _compile(src: str, obj_dir: str = OBJ, defines=()) -> str:
     path = os.path.join(CSRC, src)
-    obj = os.path.join(OBJ, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *COMMON, *DEVICE, *EXTRA.get(src, [])]
+    obj = os.path.join(obj_dir, os.path.splitext(src)[0] + ".o")
+    cmd = [HIPCC, *COMMON, *DEVICE, *EXTRA.get(src, []), *[f"-D{d}" for d in defines]]
     if src.endswith(".hip"):
         cmd += ["-x", "hip"]
     cmd += ["-c", path, "-o", obj]
@@ -75,21 +75,22 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(verbose: bool = True) -> str:
-    """Compile all sources and link the shared library; returns its path."""
-    os.makedirs(OBJ, exist_ok=True)
+def build(verbose: bool = True, lib: str = LIB, obj_dir: str = OBJ, defines=()) -> str:
+    """Compile all sources and link the shared library; returns its path.
+    `defines` (e.g. ["FG_GEMM_BK=32"]) builds a tuning variant into `lib`."""
+    os.makedirs(obj_dir, exist_ok=True)
     jobs = min(len(SOURCES), int(os.environ.get("MAX_JOBS", "8")))
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
-        objs = list(ex.map(_compile, SOURCES))
-    tmp = LIB + ".tmp"
+        objs = list(ex.map(lambda s: _compile(s, obj_dir, defines), SOURCES))
+    tmp = lib + ".tmp"
     cmd = [HIPCC, "-shared", f"--offload-arch={ARCH}", "-fPIC", "-o", tmp, *objs, "-lpthread"]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib)
     if verbose:
-        print(f"built {LIB}")
-    return LIB
+        print(f"built {lib}")
+    return lib
 
 
 if __name__ == "__main__":

@@ -47,6 +47,13 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kThreads = 256;
 
+// K-tile depth (a multiple of 16).  A compile-time tuning knob: builds may
+// override it with -DFG_GEMM_BK=32.
+#ifndef FG_GEMM_BK
+#define FG_GEMM_BK 16
+#endif
+constexpr int kBK = FG_GEMM_BK;
+
 struct GemmArgs {
     const float *A;
     const float *B;
@@ -63,8 +70,9 @@ struct GemmArgs {
     int vec_out;  // C (and Z / Zs) rows 16-byte aligned: float4 epilogue I/O
 };
 
-// LDS footprint in floats.
-template <int BM, int BN, int BK, bool AK, bool BNC, int WTN>
+// LDS footprint in floats (NW waves, each staging a 32 x WTN slice in the
+// epilogue).
+template <int BM, int BN, int BK, bool AK, bool BNC, int WTN, int NW>
 struct Lds {
     static constexpr int a_ld = AK ? (BK + 4) : (BM + 4);
     static constexpr int a_sz = AK ? BM * a_ld : BK * a_ld;
@@ -72,18 +80,18 @@ struct Lds {
     static constexpr int b_sz = BNC ? BK * b_ld : BN * b_ld;
     static constexpr int buf = a_sz + b_sz;
     static constexpr int stage_ld = WTN + 4;
-    static constexpr int stage = 4 * 32 * stage_ld;
+    static constexpr int stage = NW * 32 * stage_ld;
     static constexpr int total = (2 * buf > stage) ? 2 * buf : stage;
 };
 
-// Loads one operand tile into registers.  Operand rows are M (for A) or N
-// (for B); "KC" = k-contiguous in global memory.
-template <int R, int BK, bool KC, bool VEC>
+// Loads one operand tile into registers with NT threads.  Operand rows are
+// M (for A) or N (for B); "KC" = k-contiguous in global memory.
+template <int R, int BK, bool KC, bool VEC, int NT>
 struct TileLoader {
     static constexpr int kElems = R * BK;
-    static constexpr int kPer = VEC ? kElems / 4 / kThreads : kElems / kThreads;
+    static constexpr int kPer = VEC ? kElems / 4 / NT : kElems / NT;
     static_assert(kPer >= 1, "tile too small for the thread count");
-    static_assert((VEC ? kElems / 4 : kElems) % kThreads == 0, "tile not divisible");
+    static_assert((VEC ? kElems / 4 : kElems) % NT == 0, "tile not divisible");
     f32x4 v4[VEC ? kPer : 1];
     float v1[VEC ? 1 : kPer];
 
@@ -91,7 +99,7 @@ struct TileLoader {
                                          int k0, int K) {
 #pragma unroll
         for (int q = 0; q < kPer; ++q) {
-            const int idx = threadIdx.x + q * kThreads;
+            const int idx = threadIdx.x + q * NT;
             if constexpr (VEC) {
                 int row, kk;
                 if constexpr (KC) {
@@ -125,7 +133,7 @@ struct TileLoader {
         constexpr int ld = KC ? (BK + 4) : (R + 4);
 #pragma unroll
         for (int q = 0; q < kPer; ++q) {
-            const int idx = threadIdx.x + q * kThreads;
+            const int idx = threadIdx.x + q * NT;
             if constexpr (VEC) {
                 if constexpr (KC) {
                     const int row = idx / (BK / 4), kk = (idx % (BK / 4)) * 4;
@@ -177,13 +185,14 @@ __device__ __forceinline__ float epi_value(const GemmArgs &p, float v, float bv,
 }
 
 template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC, bool VEC>
-__global__ __launch_bounds__(kThreads) void gemm_f32_mfma(GemmArgs p) {
-    static_assert(WGM * WGN == 4, "4 waves per workgroup");
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_mfma(GemmArgs p) {
+    constexpr int NT = 64 * WGM * WGN;
+    static_assert(WGM * WGN == 4 || WGM * WGN == 8, "4 or 8 waves per workgroup");
     constexpr int WTM = BM / WGM, WTN = BN / WGN;
     constexpr int TM = WTM / 32, TN = WTN / 32;
     static_assert(TM >= 1 && TN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "wave tile");
     static_assert(BK % 16 == 0, "BK must be a multiple of 16");
-    using L = Lds<BM, BN, BK, AK, BNC, WTN>;
+    using L = Lds<BM, BN, BK, AK, BNC, WTN, WGM * WGN>;
     __shared__ __attribute__((aligned(16))) float lds[L::total];
 
     int tile_m, tile_n;
@@ -201,8 +210,8 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_mfma(GemmArgs p) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    TileLoader<BM, BK, AK, VEC> la;
-    TileLoader<BN, BK, !BNC, VEC> lb;
+    TileLoader<BM, BK, AK, VEC, NT> la;
+    TileLoader<BN, BK, !BNC, VEC, NT> lb;
     const int nk = (p.K + BK - 1) / BK;
 
     la.load(p.A, p.lda, m0, p.M, 0, p.K);
@@ -314,29 +323,38 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_mfma(GemmArgs p) {
     }
 }
 
-template <int BM, int BN, int WGM, int WGN, bool AK, bool BNC, bool VEC>
+template <int BM, int BN, int WGM, int WGN, int BK, bool AK, bool BNC, bool VEC>
 void launch_one(const GemmArgs &a0, hipStream_t st) {
     GemmArgs a = a0;
     a.tiles_m = (a.M + BM - 1) / BM;
     a.tiles_n = (a.N + BN - 1) / BN;
-    gemm_f32_mfma<BM, BN, 16, WGM, WGN, AK, BNC, VEC>
-        <<<a.tiles_m * a.tiles_n, kThreads, 0, st>>>(a);
+    gemm_f32_mfma<BM, BN, BK, WGM, WGN, AK, BNC, VEC>
+        <<<a.tiles_m * a.tiles_n, 64 * WGM * WGN, 0, st>>>(a);
 }
 
-// Tile configurations: 0: 256x256, 1: 256x128, 2: 128x256, 3: 128x128,
-// 4: 64x64 (also the only scalar-load variant, for unaligned operands).
+// Tile configurations (index: BM x BN, waves, K depth):
+//   0: 256x256, 4 waves, BK 16      1: 256x128, 4 waves, BK 16
+//   2: 128x256, 4 waves, BK 16      3: 128x128, 4 waves, BK 32
+//   4:  64x64,  4 waves, BK 16      5: 128x64,  4 waves, BK 32
+//   6: 256x256, 8 waves, BK 16      7: 256x128, 8 waves, BK 16
+// 64x64 is also the only scalar-load variant, for unaligned operands.
+constexpr int kNumCfgs = 8;
+
 template <bool AK, bool BNC>
 void launch_layout(const GemmArgs &a, bool vec, int cfg, hipStream_t st) {
     if (!vec) {
-        launch_one<64, 64, 2, 2, AK, BNC, false>(a, st);
+        launch_one<64, 64, 2, 2, 16, AK, BNC, false>(a, st);
         return;
     }
     switch (cfg) {
-        case 0: launch_one<256, 256, 2, 2, AK, BNC, true>(a, st); break;
-        case 1: launch_one<256, 128, 2, 2, AK, BNC, true>(a, st); break;
-        case 2: launch_one<128, 256, 2, 2, AK, BNC, true>(a, st); break;
-        case 3: launch_one<128, 128, 2, 2, AK, BNC, true>(a, st); break;
-        default: launch_one<64, 64, 2, 2, AK, BNC, true>(a, st); break;
+        case 0: launch_one<256, 256, 2, 2, kBK, AK, BNC, true>(a, st); break;
+        case 1: launch_one<256, 128, 2, 2, kBK, AK, BNC, true>(a, st); break;
+        case 2: launch_one<128, 256, 2, 2, kBK, AK, BNC, true>(a, st); break;
+        case 3: launch_one<128, 128, 2, 2, 32, AK, BNC, true>(a, st); break;
+        case 5: launch_one<128, 64, 2, 2, 32, AK, BNC, true>(a, st); break;
+        case 6: launch_one<256, 256, 2, 4, kBK, AK, BNC, true>(a, st); break;
+        case 7: launch_one<256, 128, 4, 2, kBK, AK, BNC, true>(a, st); break;
+        default: launch_one<64, 64, 2, 2, 16, AK, BNC, true>(a, st); break;
     }
 }
 

@@ -16,34 +16,27 @@ using fg::gemm::kThreads;
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // ------------------------------------------------------------ dispatch
-struct Cfg {
-    int bm, bn;
-    int conc;   // workgroups resident per CU (registers / LDS bound)
-    float eff;  // relative per-CU efficiency (model, tuned by measurement)
-};
+// Tile configuration per call (indices as in fg_gemm_kernel.h), from a
+// measured sweep on MI355X (256 CUs) over the BASELINE shapes:
+//  * NN (forward): 256x128 with 8 waves when it yields >= one tile per CU
+//    (105 TFLOP/s at 2048x4096x4096, 128 at 4096^3); else 128x64.
+//  * NT / TN (dA, dW): 256x256 with 8 waves for large-K squares that fill
+//    the chip (130-133 at 4096^3); 128x128 (BK 32) with >= two tiles per CU
+//    (120 at 2048x4096x4096 and 4096x4096x2048); else 128x64 with >= one
+//    tile per CU (104-108 for the 1024- and 1000-wide layers).
+//  * 64x64 for anything smaller.
+int tiles(int M, int N, int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); }
 
-constexpr Cfg kCfgs[] = {
-    {256, 256, 1, 0.90f},
-    {256, 128, 1, 0.85f},
-    {128, 256, 1, 0.85f},
-    {128, 128, 2, 0.70f},
-    {64, 64, 4, 0.40f},
-};
-
-int pick_cfg(int M, int N, int cus) {
-    int best = 0;
-    double best_t = 1e300;
-    for (int c = 0; c < (int)(sizeof kCfgs / sizeof kCfgs[0]); ++c) {
-        const Cfg &g = kCfgs[c];
-        const double tiles = (double)((M + g.bm - 1) / g.bm) * (double)((N + g.bn - 1) / g.bn);
-        const double rounds = std::ceil(tiles / ((double)cus * g.conc));
-        const double t = rounds * g.conc * (double)g.bm * g.bn / g.eff;
-        if (t < best_t - 1e-9) {
-            best_t = t;
-            best = c;
-        }
+int pick_cfg(int layout, int M, int N, int K, int cus) {
+    if (layout == FG_NN) {
+        if (tiles(M, N, 256, 128) >= cus) return 7;
+        if (tiles(M, N, 128, 64) >= cus) return 5;
+        return 4;
     }
-    return best;
+    if (K >= 4096 && tiles(M, N, 256, 256) >= cus) return 6;
+    if (tiles(M, N, 128, 128) >= 2 * cus) return 3;
+    if (tiles(M, N, 128, 64) >= cus) return 5;
+    return 4;
 }
 
 int gemm_common(fg_ctx *ctx, int layout, GemmArgs &a, const char *who) {
@@ -72,7 +65,11 @@ int gemm_common(fg_ctx *ctx, int layout, GemmArgs &a, const char *who) {
     if (layout == FG_NN) vec = vec && a.K % 4 == 0 && a.N % 4 == 0;
     if (layout == FG_NT) vec = vec && a.K % 4 == 0;
     if (layout == FG_TN) vec = vec && a.M % 4 == 0 && a.N % 4 == 0;
-    const int cfg = pick_cfg(a.M, a.N, ctx->cu_count > 0 ? ctx->cu_count : 256);
+#ifdef FG_GEMM_FORCE_CFG  // tuning builds: one tile configuration for every shape
+    const int cfg = FG_GEMM_FORCE_CFG;
+#else
+    const int cfg = pick_cfg(layout, a.M, a.N, a.K, ctx->cu_count > 0 ? ctx->cu_count : 256);
+#endif
     auto al16 = [](const void *q) { return (((uintptr_t)q) & 15u) == 0; };
     a.vec_out = al16(a.C) && a.ldc % 4 == 0 && (!a.Z || (al16(a.Z) && a.ldz % 4 == 0)) &&
                 (!a.bias || al16(a.bias));
