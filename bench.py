@@ -181,7 +181,9 @@ def gemm_components(ctx, reps: int):
     t = event_time_ms(lambda: ctx.gemm(fa.NN, M, N, K, X, K, W, N, H, N, bias=b,
                                        act=fa.ACT_GELU, Z=Zh, ldz=N), reps)
     out["c5_hidden_fwd_gemm"] = {"ms": t, "flops_per_launch": 2 * M * N * K,
-                                 "tflops": 2.0 * M * N * K / t / 1e9}
+                                 "tflops": 2.0 * M * N * K / t / 1e9,
+                                 # X, W, bias read once; H and Z written once.
+                                 "bytes": 4 * (M * K + K * N + N + 2 * M * N)}
     return out
 
 
@@ -228,6 +230,85 @@ def adam_component(ctx, reps: int):
     nbytes = 28 * nt * n
     return {"c4_adam_64x4Mi": {"ms": t, "bytes": nbytes, "gbs": nbytes / t / 1e6,
                                "frac_hbm": nbytes / t / 1e6 / PEAK_HBM_GBS}}
+
+
+def only_gemm_c5_hidden(ctx, reps):
+    """The c5 hidden-layer forward GEMM, 2048x4096x4096 + bias + GELU."""
+    import torch
+
+    import ferrograd_amd as fa
+
+    M, N, K = 2048, 4096, 4096
+    X, W = torch.randn((M, K), device="cuda"), torch.randn((K, N), device="cuda")
+    b = torch.randn((N,), device="cuda")
+    H, Z = torch.empty((M, N), device="cuda"), torch.empty((M, N), device="cuda")
+    for _ in range(reps):
+        ctx.gemm(fa.NN, M, N, K, X, K, W, N, H, N, bias=b, act=fa.ACT_GELU, Z=Z, ldz=N)
+
+
+def only_softmax_ce_c3(ctx, reps):
+    """The c3 fused softmax + CE over [8192, 32000]."""
+    import torch
+
+    R, C = 8192, 32000
+    x = torch.empty((R, C), device="cuda")
+    lab = torch.empty((R,), device="cuda", dtype=torch.int32)
+    ctx.rng_normal(2, 0, 0.0, 2.0, x, R * C)
+    ctx.rng_int(2, 1, C, lab, R)
+    d = torch.empty_like(x)
+    loss = torch.empty(R, device="cuda")
+    for _ in range(reps):
+        ctx.softmax_ce(x, C, lab, R, C, 1.0, row_loss=loss, dlogits=d, ldd=C)
+
+
+def only_adam_c4(ctx, reps):
+    """The c4 multi-tensor Adam over 64 x 4 Mi parameters."""
+    import torch
+
+    import ferrograd_amd as fa
+
+    nt, n = 64, 4 * 1024 * 1024
+    P = [torch.zeros(n, device="cuda") for _ in range(nt)]
+    G = [torch.full((n,), 1e-3, device="cuda") for _ in range(nt)]
+    M = [torch.zeros(n, device="cuda") for _ in range(nt)]
+    V = [torch.zeros(n, device="cuda") for _ in range(nt)]
+    mt = fa.MultiTensor(ctx, P, G, M, V)
+    for step in range(1, reps + 1):
+        mt.adam(1e-3, 0.9, 0.999, 1e-8, step)
+    torch.cuda.synchronize()
+    mt.close()
+
+
+def only_copy_256mib(ctx, reps):
+    """Calibration for the HBM counters: a plain device copy of 256 MiB
+    (reads 256 MiB, writes 256 MiB per launch)."""
+    import torch
+
+    a = torch.ones(64 * 1024 * 1024, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(reps):
+        b.copy_(a)
+
+
+ONLY = {
+    "gemm_c5_hidden": only_gemm_c5_hidden,
+    "softmax_ce_c3": only_softmax_ce_c3,
+    "adam_c4": only_adam_c4,
+    "copy_256mib": only_copy_256mib,
+}
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed counter summary
+    (profiles/traffic.json, produced from two rocprofv3 --pmc passes,
+    FETCH_SIZE and WRITE_SIZE, scaled by what the same counters read for a
+    plain 256 MiB copy); None when the summary is absent."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)[kernel]["traffic_bytes"]
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def cpu_baseline_c5(host, dims, batch, threads):
@@ -278,6 +359,8 @@ def main() -> int:
     ap.add_argument("--no-components", action="store_true",
                     help="skip the c2/c3/c4 component measurements")
     ap.add_argument("--reps", type=int, default=20, help="launches per kernel timing")
+    ap.add_argument("--only", choices=sorted(ONLY), default=None,
+                    help="run only this kernel --reps times (for rocprofv3 counter passes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X only: this build has no multi-GPU path "
@@ -288,6 +371,13 @@ def main() -> int:
     import torch
 
     import ferrograd_amd as fa
+
+    if args.only:
+        ctx, _stream = fa.torch_context(0)
+        ONLY[args.only](ctx, args.reps)
+        torch.cuda.synchronize()
+        log(f"ran {args.only} x{args.reps}")
+        return 0
 
     ctx, _stream = fa.torch_context(0)
     log(f"device {ctx.arch}, {ctx.cu_count} CUs")
@@ -347,7 +437,9 @@ def main() -> int:
         "peak": PEAK_FP32_MFMA_TFLOPS,
         "unit": "TFLOP/s",
         "frac": hid["tflops"] / PEAK_FP32_MFMA_TFLOPS,
-        "traffic": None,
+        "traffic": measured_traffic("gemm_c5_hidden"),
+        "traffic_unit": "HBM bytes per launch (rocprofv3 FETCH_SIZE/WRITE_SIZE, copy-calibrated)",
+        "algorithmic_bytes": hid["bytes"],
     }
     if not args.no_components:
         comps.update(softmax_component(ctx, args.reps))
