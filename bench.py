@@ -12,6 +12,7 @@ Also measured in the same run (HIP events on the stream the kernels run on):
   * c2: 4096^3 GEMM forward (bias + ReLU) and its dA / dB backward;
   * c3: fused softmax + CE forward/backward over [8192, 32000];
   * c4: multi-tensor Adam over 64 x 4 Mi parameters;
+  * c1: the 2-layer MLP step (latency bound: steps/s, launches, us/launch);
 and the CPU restatement (oracle/) timed on the host cores on a bounded
 sample of the same workload (one full c5 step on the same inputs), which
 also gives a parity check of the step's loss and gradients.
@@ -57,22 +58,28 @@ def event_time_ms(fn, reps: int) -> float:
     return start.elapsed_time(stop) / reps
 
 
-class C5Step:
-    """Config c5 built as a ferrograd graph and run through the planner:
-    X [2048,1024] ~ N(0,1), labels U{0..999}, W_l Kaiming-uniform
-    U(-sqrt(6/fan_in), +sqrt(6/fan_in)), b_l = 0 (seed 4, device generator);
-    matmul -> bias_add -> gelu per hidden layer, softmax + CROSS_ENTROPY,
-    Adam lr 1e-3.  X is an Input whose gradient is computed (ferrograd trains
-    every Input) but which the optimiser does not update."""
+class MLPStep:
+    """An MLP training step built as a ferrograd graph and run through the
+    planner: matmul -> bias_add -> act per hidden layer, softmax +
+    CROSS_ENTROPY, then the optimiser.  Weights Kaiming-uniform
+    U(-sqrt(6/fan_in), +sqrt(6/fan_in)), biases 0, labels U{0..classes-1},
+    all from the device generator keyed by `seed`.  X is an Input whose
+    gradient is computed (ferrograd trains every Input) but which the
+    optimiser does not update.
 
-    def __init__(self, ctx, dims, batch):
+    c5: X ~ N(0,1), 1024 -> 4096 x7 -> 1000, GELU, Adam lr 1e-3, seed 4.
+    c1: X ~ U[0,1), 784 -> 256 -> 10, ReLU, SGD lr 0.01, seed 0."""
+
+    def __init__(self, ctx, dims, batch, act="gelu", optim="adam", lr=1e-3, seed=4,
+                 x_dist="normal"):
         import torch
 
         from ferrograd_amd import graph as G
 
         self.G, self.ctx, self.dims, self.B = G, ctx, dims, batch
         self.gctx = G.GpuContext(ctx)
-        graph, meta = G.Graph(G.CROSS_ENTROPY, G.Optim.adam().lower), G.Metadata.new()
+        opt = G.Optim.adam() if optim == "adam" else G.Optim.sgd()
+        graph, meta = G.Graph(G.CROSS_ENTROPY, opt.lower), G.Metadata.new()
         fb = meta.new_field()
         fd = [meta.new_field() for _ in dims]
         L = len(dims) - 1
@@ -85,14 +92,16 @@ class C5Step:
                 self.w_nodes.append(W)
                 self.b_nodes.append(b)
                 z = ops.bias_add(ops.matmul(h, W), b)
-                h = ops.gelu(z) if l < L - 1 else z
+                h = (ops.gelu(z) if act == "gelu" else ops.relu(z)) if l < L - 1 else z
             ops.softmax(h)
-        mb = [G.f32_bits(1e-3), batch] + list(dims)
+        mb = [G.f32_bits(lr), batch] + list(dims)
         self.st = self.gctx.alloc_tensors(graph, graph.compute_saved_nodes(), mb)
-        seed = 4
         self.X = torch.empty((batch, dims[0]), device="cuda")
         self.labels = torch.empty((batch,), device="cuda", dtype=torch.int32)
-        ctx.rng_normal(seed, 0, 0.0, 1.0, self.X, self.X.numel())
+        if x_dist == "normal":
+            ctx.rng_normal(seed, 0, 0.0, 1.0, self.X, self.X.numel())
+        else:
+            ctx.rng_uniform(seed, 0, 0.0, 1.0, self.X, self.X.numel())
         ctx.rng_int(seed, 1, dims[-1], self.labels, batch)
         self.W = [torch.empty((dims[l], dims[l + 1]), device="cuda") for l in range(L)]
         self.b = [torch.zeros((dims[l + 1],), device="cuda") for l in range(L)]
@@ -107,6 +116,14 @@ class C5Step:
         self.dW = [gmap[n] for n in self.w_nodes]
         self.db = [gmap[n] for n in self.b_nodes]
         self.describe = self.sch.plan.describe()
+
+    def launches_per_step(self) -> int:
+        """Kernel dispatches of one step as planned (forward, loss, backward
+        from the fused CE seed, optimiser)."""
+        for line in self.describe.splitlines():
+            if line.startswith("kernels per step: "):
+                return int(line.split()[3])
+        raise RuntimeError("plan description has no kernel count")
 
     def forward(self):
         self.gctx.dispatch_forward(self.sch)
@@ -230,6 +247,51 @@ def adam_component(ctx, reps: int):
     nbytes = 28 * nt * n
     return {"c4_adam_64x4Mi": {"ms": t, "bytes": nbytes, "gbs": nbytes / t / 1e6,
                                "frac_hbm": nbytes / t / 1e6 / PEAK_HBM_GBS}}
+
+
+def copy_component(reps: int):
+    """Context for the HBM-bound kernels: a plain device copy of 1 GiB
+    (torch's copy kernel), read + write bytes per second."""
+    import torch
+
+    a = torch.ones(256 * 1024 * 1024, device="cuda")
+    b = torch.empty_like(a)
+    t = event_time_ms(lambda: b.copy_(a), reps)
+    nbytes = 2 * a.numel() * 4
+    del a, b
+    return {"hbm_copy_1gib": {"ms": t, "bytes": nbytes, "gbs": nbytes / t / 1e6,
+                              "frac_hbm": nbytes / t / 1e6 / PEAK_HBM_GBS}}
+
+
+def c1_component(ctx, steps: int = 2000):
+    """c1: the 2-layer MLP step (batch 64, 784 -> 256 -> 10, ReLU, softmax-CE,
+    SGD lr 0.01), latency bound: steps/s of the captured step, launches per
+    step and the average time per launch."""
+    import torch
+
+    tr = MLPStep(ctx, [784, 256, 10], 64, act="relu", optim="sgd", lr=0.01, seed=0,
+                 x_dist="uniform")
+    for _ in range(3):
+        tr.step_eager()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        tr.step_eager()
+    torch.cuda.synchronize()
+    eager_ms = 1000.0 * (time.perf_counter() - t0) / steps
+    tr.capture()
+    tr.step_graph()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        tr.step_graph()
+    torch.cuda.synchronize()
+    ms = 1000.0 * (time.perf_counter() - t0) / steps
+    n = tr.launches_per_step()
+    return {"c1_mlp_step": {"steps_per_s": 1000.0 / ms, "ms_per_step": ms,
+                            "eager_ms_per_step": eager_ms, "launches_per_step": n,
+                            "us_per_launch": 1000.0 * ms / n, "loss": tr.mean_loss(),
+                            "steps_timed": steps}}
 
 
 def only_gemm_c5_hidden(ctx, reps):
@@ -383,7 +445,7 @@ def main() -> int:
     log(f"device {ctx.arch}, {ctx.cu_count} CUs")
     dims = [1024] + [4096] * 7 + [1000]
     batch = 2048
-    tr = C5Step(ctx, dims, batch)
+    tr = MLPStep(ctx, dims, batch)
     log("plan:\n" + tr.describe)
     torch.cuda.synchronize()
     host = None
@@ -444,6 +506,8 @@ def main() -> int:
     if not args.no_components:
         comps.update(softmax_component(ctx, args.reps))
         comps.update(adam_component(ctx, 10))
+        comps.update(c1_component(ctx))
+        comps.update(copy_component(args.reps))
     log("components: " + json.dumps(comps))
 
     cpu = None

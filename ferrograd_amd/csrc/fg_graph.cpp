@@ -1605,12 +1605,29 @@ FG_API int fg_plan_describe(const fg_plan *p, char *buf, size_t len, size_t *nee
         s += std::string(title) + ": " + std::to_string(v.size()) + " launches\n";
         for (const Launch &L : v) s += "  " + L.desc + "\n";
     };
+    // Kernel dispatches per planned launch: the bias-gradient reduction is a
+    // partial and a final pass, the fused softmax + CE adds the mean-loss
+    // reduction, the Adam update is preceded by its step-counter advance.
+    auto kernels = [&](const std::vector<Launch> &v) {
+        int n = 0;
+        for (const Launch &L : v)
+            n += (L.kind == LK_BIAS_GRAD || (L.kind == LK_SMCE && L.sBias != kNone)) ? 2 : 1;
+        return n;
+    };
     add("forward", p->fwd);
     add("loss", p->loss);
     add("backward(seed)", p->bwd_seed);
     if (p->ce_fused_possible) add("backward(ce-fused)", p->bwd_fused);
-    s += "optim: " + std::string(p->g.optim == FG_OPTIM_ADAM ? "adam" : "sgd") + " over " +
+    const bool adam = p->g.optim == FG_OPTIM_ADAM;
+    s += "optim: " + std::string(adam ? "adam" : "sgd") + " over " +
          std::to_string(p->opt_inputs.size()) + " inputs, 1 multi-tensor launch\n";
+    const int k_opt = p->opt_inputs.empty() ? 0 : (adam ? 2 : 1);
+    const int k_bwd = kernels(p->ce_fused_possible ? p->bwd_fused : p->bwd_seed);
+    s += "kernels per step: " +
+         std::to_string(kernels(p->fwd) + kernels(p->loss) + k_bwd + k_opt) +
+         " (forward " + std::to_string(kernels(p->fwd)) + ", loss " +
+         std::to_string(kernels(p->loss)) + ", backward " + std::to_string(k_bwd) +
+         ", optim " + std::to_string(k_opt) + ")\n";
     s += "arena: " + std::to_string(p->arena_bytes) + " bytes\n";
     if (needed) *needed = s.size() + 1;
     if (buf && len) {
