@@ -26,6 +26,7 @@ from ._lib import FgError, call, load
 
 NN, NT, TN = 0, 1, 2
 ACT_NONE, ACT_RELU, ACT_GELU = 0, 1, 2
+DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 
 __all__ = [
     "NN", "NT", "TN", "ACT_NONE", "ACT_RELU", "ACT_GELU", "FgError", "Context",
@@ -101,23 +102,39 @@ class Context:
         call("fg_gemm_bwd_f32", self.handle, layout, M, N, K, _ptr(A), lda, _ptr(B), ldb, act,
              _ptr(Zs), ldzs, _ptr(C), ldc, int(accumulate))
 
-    def bias_grad(self, M: int, N: int, dZ, ld: int, dbias, accumulate: bool = False) -> None:
-        call("fg_bias_grad_f32", self.handle, M, N, _ptr(dZ), ld, _ptr(dbias), int(accumulate))
+    def gemm_x16(self, dtype: int, layout: int, M: int, N: int, K: int, A, lda: int, B,
+                 ldb: int, C, ldc: int, bias=None, act: int = ACT_NONE, Z=None, ldz: int = 0,
+                 accumulate: bool = False) -> None:
+        """16-bit GEMM (dtype DTYPE_F16 / DTYPE_BF16 for every operand)."""
+        call("fg_gemm_x16", self.handle, dtype, layout, M, N, K, _ptr(A), lda, _ptr(B), ldb,
+             _ptr(bias), act, _ptr(C), ldc, _ptr(Z), ldz, int(accumulate))
+
+    def gemm_bwd_x16(self, dtype: int, layout: int, M: int, N: int, K: int, A, lda: int, B,
+                     ldb: int, C, ldc: int, act: int = ACT_NONE, Zs=None, ldzs: int = 0,
+                     accumulate: bool = False) -> None:
+        call("fg_gemm_bwd_x16", self.handle, dtype, layout, M, N, K, _ptr(A), lda, _ptr(B),
+             ldb, act, _ptr(Zs), ldzs, _ptr(C), ldc, int(accumulate))
+
+    def bias_grad(self, M: int, N: int, dZ, ld: int, dbias, accumulate: bool = False,
+                  dtype: int = DTYPE_F32) -> None:
+        call("fg_bias_grad", self.handle, dtype, M, N, _ptr(dZ), ld, _ptr(dbias),
+             int(accumulate))
 
     def act_bwd(self, act: int, n: int, dH, Z, dZ) -> None:
         call("fg_act_bwd_f32", self.handle, act, n, _ptr(dH), _ptr(Z), _ptr(dZ))
 
     def softmax_ce(self, logits, ldx: int, labels, R: int, C: int, grad_scale: float = 1.0,
                    row_loss=None, mean_loss=None, dlogits=None, ldd: int = 0,
-                   argmax=None) -> None:
-        call("fg_softmax_ce_f32", self.handle, _ptr(logits), ldx, _ptr(labels), R, C,
+                   argmax=None, dtype: int = DTYPE_F32) -> None:
+        call("fg_softmax_ce", self.handle, dtype, _ptr(logits), ldx, _ptr(labels), R, C,
              grad_scale, _ptr(row_loss), _ptr(mean_loss), _ptr(dlogits), ldd or C, _ptr(argmax))
 
-    def softmax(self, x, R: int, C: int, y) -> None:
-        call("fg_softmax_f32", self.handle, _ptr(x), R, C, _ptr(y))
+    def softmax(self, x, R: int, C: int, y, dtype: int = DTYPE_F32) -> None:
+        call("fg_softmax", self.handle, dtype, _ptr(x), R, C, _ptr(y))
 
-    def softmax_bwd(self, y, dy, R: int, C: int, dx, accumulate: bool = False) -> None:
-        call("fg_softmax_bwd_f32", self.handle, _ptr(y), _ptr(dy), R, C, _ptr(dx),
+    def softmax_bwd(self, y, dy, R: int, C: int, dx, accumulate: bool = False,
+                    dtype: int = DTYPE_F32) -> None:
+        call("fg_softmax_bwd", self.handle, dtype, _ptr(y), _ptr(dy), R, C, _ptr(dx),
              int(accumulate))
 
     def fill_u32(self, dst, value: int, count: int) -> None:
@@ -153,7 +170,9 @@ class MultiTensor:
 
     def __init__(self, ctx: Context, params: Sequence, grads: Sequence,
                  m: Optional[Sequence] = None, v: Optional[Sequence] = None,
-                 sizes: Optional[Sequence[int]] = None):
+                 sizes: Optional[Sequence[int]] = None, dtypes: Optional[Sequence[int]] = None):
+        """dtypes: element type per tensor (DTYPE_*) of params / grads; m and
+        v are always fp32."""
         n = len(params)
         if sizes is None:
             sizes = [int(p.numel()) for p in params]
@@ -164,7 +183,8 @@ class MultiTensor:
         Vv = arr(*[_ptr(x) for x in v]) if v is not None else None
         S = (ctypes.c_uint64 * n)(*sizes)
         h = ctypes.c_void_p()
-        call("fg_mt_create", ctx.handle, n, P, G, Mv, Vv, S, ctypes.byref(h))
+        D = (ctypes.c_int * n)(*dtypes) if dtypes is not None else None
+        call("fg_mt_create_x", ctx.handle, n, D, P, G, Mv, Vv, S, ctypes.byref(h))
         self.ctx = ctx
         self.handle = h
 

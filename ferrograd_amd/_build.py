@@ -27,8 +27,12 @@ SOURCES = [
     "k_gemm_nn.hip",
     "k_gemm_nt.hip",
     "k_gemm_tn.hip",
+    "k_gemm16.hip",
+    "k_gemm16_bf16.hip",
+    "k_gemm16_f16.hip",
     "k_eltwise_prog.hip",
     "fg_graph.cpp",
+    "fg_bpat.cpp",
 ]
 
 # Packed-fp32 VALU instructions are disabled for all device code: some of

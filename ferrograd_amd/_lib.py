@@ -47,6 +47,28 @@ SIGNATURES = {
     "fg_gemm_bwd_f32": (i32, [vp, i32, i32, i32, i32, vp, i32, vp, i32, i32, vp, i32, vp, i32,
                               i32]),
     "fg_bias_grad_f32": (i32, [vp, i32, i32, vp, i32, vp, i32]),
+    "fg_bias_grad": (i32, [vp, i32, i32, i32, vp, i32, vp, i32]),
+    "fg_softmax_ce": (i32, [vp, i32, vp, i32, vp, i32, i32, f32, vp, vp, vp, i32, vp]),
+    "fg_softmax": (i32, [vp, i32, vp, i32, i32, vp]),
+    "fg_softmax_bwd": (i32, [vp, i32, vp, vp, i32, i32, vp, i32]),
+    "fg_mt_create_x": (i32, [vp, i32, vp, vp, vp, vp, vp, vp, vp]),
+    "fg_graph_input_x": (i32, [vp, vp, i32, i32, vp]),
+    "fg_graph_constant": (i32, [vp, i32, f32, vp]),
+    "fg_plan_tensor_dtype": (i32, [vp, i32, i32, vp]),
+    "fg_plan_save": (i32, [vp, ctypes.c_char_p, i32]),
+    "fg_plan_load": (i32, [vp, ctypes.c_char_p]),
+    "fg_bpat_save": (i32, [vp, ctypes.c_char_p, i32, i32, vp]),
+    "fg_bpat_save_host": (i32, [ctypes.c_char_p, i32, i32, vp]),
+    "fg_bpat_open": (i32, [ctypes.c_char_p, vp]),
+    "fg_bpat_close": (i32, [vp]),
+    "fg_bpat_info": (i32, [vp, vp, vp]),
+    "fg_bpat_tensor_info": (i32, [vp, i32, vp, vp, vp]),
+    "fg_bpat_read_f32": (i32, [vp, i32, vp]),
+    "fg_bpat_upload": (i32, [vp, vp, i32, vp, i32]),
+    "fg_gemm_x16": (i32, [vp, i32, i32, i32, i32, i32, vp, i32, vp, i32, vp, i32, vp, i32, vp,
+                          i32, i32]),
+    "fg_gemm_bwd_x16": (i32, [vp, i32, i32, i32, i32, i32, vp, i32, vp, i32, i32, vp, i32, vp,
+                              i32, i32]),
     "fg_act_bwd_f32": (i32, [vp, i32, u64, vp, vp, vp]),
     "fg_softmax_ce_f32": (i32, [vp, vp, i32, vp, i32, i32, f32, vp, vp, vp, i32, vp]),
     "fg_softmax_f32": (i32, [vp, vp, i32, i32, vp]),
@@ -94,6 +116,7 @@ SIGNATURES = {
 STATUS_NAMES = {
     0: "OK", 1: "INVALID_ARGUMENT", 2: "OUT_OF_MEMORY", 3: "UNSUPPORTED", 4: "DEVICE",
     5: "SHAPE", 6: "GRAPH", 7: "INTERNAL", 8: "NO_DEVICE", 9: "OUT_OF_BOUNDS",
+    10: "SERIALIZATION", 11: "FILE_NOT_FOUND",
 }
 
 

@@ -12,10 +12,10 @@
 namespace fg {
 
 enum EltOp : uint8_t {
-    kEltLoad = 0,   // r[dst] = src[a] at the element, addressing mode c
+    kEltLoad = 0,   // r[dst] = src[a] at the element, addressing mode c, element type b
     kEltImm,        // r[dst] = imm
-    kEltStore,      // dsts[a][i] = r[b]
-    kEltAccum,      // dsts[a][i] += r[b]
+    kEltStore,      // dsts[a][i] = r[b]              (element type c, rounded to it)
+    kEltAccum,      // dsts[a][i] = dsts[a][i] + r[b]  (element type c, rounded to it)
     kEltAdd,        // r[dst] = r[a] + r[b]
     kEltSub,
     kEltMul,
@@ -35,6 +35,7 @@ enum EltOp : uint8_t {
     kEltLabelEq,    // r[dst] = (col == labels[row]) ? 1 : 0
     kEltSelect,     // r[dst] = r[a] != 0 ? r[b] : r[c]
     kEltMax,        // r[dst] = max(r[a], r[b])
+    kEltRound,      // r[dst] = r[a] rounded to element type c (a 16-bit node value)
 };
 
 // Source addressing modes.
@@ -53,6 +54,10 @@ struct EltInstr {
     uint8_t op, dst, a, b, c, pad[3];
     float imm;
 };
+
+// Element types (b of a load, c of a store / accumulate / round) are the
+// fg_half.h codes: 0 fp32, 1 fp16, 2 bf16.  16-bit sources and destinations
+// are addressed as 16-bit words through the same pointer arrays.
 
 // Passed by value as the kernel argument.  Every field the kernel indexes
 // with a run-time value (src, dst, ins) has elements of at least 4 bytes:

@@ -1,0 +1,363 @@
+// fg_gemm16_kernel.h -- 16-bit (bf16 / fp16) GEMM on CDNA4 matrix cores
+// (v_mfma_f32_32x32x16_bf16 / _f16) with fp32 accumulation and the same
+// fused epilogues as the fp32 kernel.  Included by k_gemm16_{bf16,f16}.hip.
+//
+// The reference evaluates a 16-bit matmul with its accumulator declared in
+// the node's type (crates/ferrograd-nn/src/op/matmul/mod.rs:150-161,
+// generic.rs:251-314), i.e. a 16-bit running sum over K.  Here products are
+// summed in fp32 and the result is rounded once to the storage type; then,
+// as the reference's node values are, the bias-add node and the activation
+// node are each rounded to the storage type.
+//
+// Design (gfx950):
+//  * Each MFMA consumes, per lane, 8 consecutive k of one row of A and of
+//    one column of B (16 bytes each).  Both operands are therefore kept in
+//    LDS k-contiguous, [row][k] with a row stride of BK+8 elements (16-byte
+//    aligned rows, conflict-free 16-byte reads).  An operand that is
+//    row-contiguous in memory (B of NN, both operands of TN) is transposed
+//    on its way to LDS: a thread loads a 4(k) x 8(row) block with four
+//    16-byte loads and writes eight 8-byte k-runs, built with v_perm_b32.
+//  * K advances in BK-deep tiles through double-buffered LDS (one barrier
+//    per tile); the global loads of tile t+1 are in flight during the MFMAs
+//    of tile t.
+//  * Accumulators (TM x TN blocks of 16 fp32 per lane) are staged through
+//    LDS one 32-row slice at a time for the epilogue, which reads bias / Z
+//    and writes C / Z four elements (8 bytes) per lane.
+//  * Workgroup ids are remapped per XCD as in the fp32 kernel.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "fg_act.h"
+#include "fg_half.h"
+
+namespace fg {
+namespace gemm16 {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+struct Args {
+    const uint16_t *A;
+    const uint16_t *B;
+    uint16_t *C;
+    uint16_t *Z;           // forward: pre-activation output (optional)
+    const uint16_t *bias;  // forward: row-broadcast bias (optional)
+    const uint16_t *Zs;    // backward: saved pre-activation for act'(.)
+    int M, N, K;
+    int lda, ldb, ldc, ldz, ldzs;
+    int act;
+    int mode;  // 0 forward epilogue, 1 backward (act-derivative) epilogue
+    int accumulate;
+    int tiles_m, tiles_n;
+    int vec_out;  // C / Z / Zs rows and bias 8-byte aligned: 4-element epilogue I/O
+};
+
+// Element conversion and the MFMA of one storage type.
+template <bool BF>
+struct T16;
+template <>
+struct T16<true> {
+    static __device__ __forceinline__ float to_f(uint16_t h) { return bf16_to_f(h); }
+    static __device__ __forceinline__ uint16_t from_f(float f) { return f_to_bf16(f); }
+    static __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                      __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    }
+};
+template <>
+struct T16<false> {
+    static __device__ __forceinline__ float to_f(uint16_t h) { return f16_to_f(h); }
+    static __device__ __forceinline__ uint16_t from_f(float f) { return f_to_f16(f); }
+    static __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                     __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+    }
+};
+
+__device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) {
+    return (uint32_t)lo | ((uint32_t)hi << 16);
+}
+
+// Loads one operand tile (R rows x BK k) into registers and writes it to
+// LDS as [row][k] with row stride BK+8.  KC: k-contiguous in memory.
+template <int R, int BK, bool KC, bool VEC, int NT>
+struct Loader {
+    static constexpr int kLd = BK + 8;
+    static constexpr int kUnits = KC ? R * BK / 8 : (BK / 4) * (R / 8);
+    // Units per thread; when the tile has fewer units than threads, the
+    // threads past the last unit load and store nothing.
+    static constexpr int kPer = (kUnits + NT - 1) / NT;
+    static_assert(kUnits % NT == 0 || kUnits < NT, "tile not divisible by the thread count");
+    static __device__ __forceinline__ bool active(int idx) { return kUnits >= NT || idx < kUnits; }
+    u32x4 v[KC ? kPer : 4 * kPer];
+
+    __device__ __forceinline__ void load(const uint16_t *__restrict__ base, int ld, int row0,
+                                         int rmax, int k0, int K) {
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) {
+            const int idx = threadIdx.x + q * NT;
+            if (!active(idx)) continue;
+            if constexpr (KC) {
+                const int row = idx / (BK / 8), kk = (idx % (BK / 8)) * 8;
+                const int gr = row0 + row, gk = k0 + kk;
+                const uint16_t *p = base + (size_t)gr * ld + gk;
+                if (VEC && gr < rmax && gk + 8 <= K) {
+                    v[q] = *reinterpret_cast<const u32x4 *>(p);
+                } else {
+                    uint16_t e[8];
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) e[t] = (gr < rmax && gk + t < K) ? p[t] : 0;
+                    v[q] = u32x4{pack2(e[0], e[1]), pack2(e[2], e[3]), pack2(e[4], e[5]),
+                                 pack2(e[6], e[7])};
+                }
+            } else {
+                const int kq = idx / (R / 8), r8 = idx % (R / 8);
+                const int gr = row0 + r8 * 8;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int gk = k0 + kq * 4 + t;
+                    const uint16_t *p = base + (size_t)gk * ld + gr;
+                    if (VEC && gk < K && gr + 8 <= rmax) {
+                        v[q * 4 + t] = *reinterpret_cast<const u32x4 *>(p);
+                    } else {
+                        uint16_t e[8];
+#pragma unroll
+                        for (int s = 0; s < 8; ++s) e[s] = (gk < K && gr + s < rmax) ? p[s] : 0;
+                        v[q * 4 + t] = u32x4{pack2(e[0], e[1]), pack2(e[2], e[3]),
+                                             pack2(e[4], e[5]), pack2(e[6], e[7])};
+                    }
+                }
+            }
+        }
+    }
+
+    __device__ __forceinline__ void store(uint16_t *lds) const {
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) {
+            const int idx = threadIdx.x + q * NT;
+            if (!active(idx)) continue;
+            if constexpr (KC) {
+                const int row = idx / (BK / 8), kk = (idx % (BK / 8)) * 8;
+                *reinterpret_cast<u32x4 *>(lds + row * kLd + kk) = v[q];
+            } else {
+                const int kq = idx / (R / 8), r8 = idx % (R / 8);
+                // v[q*4+t] holds k = 4kq+t for rows 8r8..8r8+7 (two rows per
+                // dword, the lower row in the low half).  Row e gets the
+                // four k as two dwords (k, k+1) and (k+2, k+3).
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int w = e >> 1;
+                    const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+                    const uint32_t d0 =
+                        __builtin_amdgcn_perm(v[q * 4 + 1][w], v[q * 4 + 0][w], sel);
+                    const uint32_t d1 =
+                        __builtin_amdgcn_perm(v[q * 4 + 3][w], v[q * 4 + 2][w], sel);
+                    *reinterpret_cast<u32x2 *>(lds + (r8 * 8 + e) * kLd + kq * 4) =
+                        u32x2{d0, d1};
+                }
+            }
+        }
+    }
+};
+
+__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int &tm, int &tn) {
+    const int nt = tiles_m * tiles_n;
+    if ((nt & 7) == 0) bid = (bid & 7) * (nt >> 3) + (bid >> 3);
+    constexpr int kGroupM = 4;
+    const int per_group = kGroupM * tiles_n;
+    const int g = bid / per_group;
+    const int first = g * kGroupM;
+    const int gsize = min(tiles_m - first, kGroupM);
+    const int in = bid - g * per_group;
+    tm = first + in % gsize;
+    tn = in / gsize;
+}
+
+// Epilogue of one element: v is the fp32 sum; node values are rounded to
+// the storage type as the reference's matmul, bias-add and activation nodes
+// each are.
+template <bool BF>
+__device__ __forceinline__ float epi16(const Args &p, float v, const uint16_t *bias, int row,
+                                       int col, float *zout) {
+    using E = T16<BF>;
+    v = E::to_f(E::from_f(v));
+    if (p.mode == 0) {
+        if (bias) v = E::to_f(E::from_f(v + E::to_f(bias[col])));
+        *zout = v;
+        return p.act == kActNone ? v : E::to_f(E::from_f(act_fwd(p.act, v)));
+    }
+    if (p.act != kActNone) {
+        const float z = E::to_f(p.Zs[(size_t)row * p.ldzs + col]);
+        // ReLU' masks (a select: +0 where z <= 0); GELU' scales.
+        v = p.act == kActRelu ? (z > 0.0f ? v : 0.0f)
+                              : E::to_f(E::from_f(v * act_grad(p.act, z)));
+    }
+    return v;
+}
+
+template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC, bool VEC, bool BF>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm16_mfma(Args p) {
+    using E = T16<BF>;
+    constexpr int NT = 64 * WGM * WGN;
+    constexpr int WTM = BM / WGM, WTN = BN / WGN;
+    constexpr int TM = WTM / 32, TN = WTN / 32;
+    static_assert(TM >= 1 && TN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "wave tile");
+    static_assert(BK % 16 == 0, "BK must be a multiple of 16");
+    constexpr int kLd = BK + 8;
+    constexpr int kASz = BM * kLd, kBSz = BN * kLd;  // elements
+    constexpr int kBuf = kASz + kBSz;
+    constexpr int kStageLd = WTN + 4;                 // floats
+    constexpr int kStageBytes = WGM * WGN * 32 * kStageLd * 4;
+    constexpr int kBytes = (4 * kBuf > kStageBytes) ? 4 * kBuf : kStageBytes;
+    __shared__ __attribute__((aligned(16))) uint16_t lds[kBytes / 2];
+
+    int tile_m, tile_n;
+    tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tile_m, tile_n);
+    const int m0 = tile_m * BM, n0 = tile_n * BN;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int l32 = lane & 31, h = lane >> 5;
+    const int wm0 = (wave / WGN) * WTM, wn0 = (wave % WGN) * WTN;
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    // A is k-contiguous unless TN; B is k-contiguous only for NT.
+    Loader<BM, BK, AK, VEC, NT> la;
+    Loader<BN, BK, !BNC, VEC, NT> lb;
+    const int nk = (p.K + BK - 1) / BK;
+
+    la.load(p.A, p.lda, m0, p.M, 0, p.K);
+    lb.load(p.B, p.ldb, n0, p.N, 0, p.K);
+    la.store(lds);
+    lb.store(lds + kASz);
+    __syncthreads();
+
+    for (int kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        const bool more = kt + 1 < nk;
+        if (more) {
+            la.load(p.A, p.lda, m0, p.M, (kt + 1) * BK, p.K);
+            lb.load(p.B, p.ldb, n0, p.N, (kt + 1) * BK, p.K);
+        }
+        const uint16_t *As = lds + cur * kBuf;
+        const uint16_t *Bs = As + kASz;
+#pragma unroll
+        for (int u = 0; u < BK / 16; ++u) {
+            const int kb = u * 16 + 8 * h;
+            u32x4 a[TM], b[TN];
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+                a[i] = *reinterpret_cast<const u32x4 *>(As + (wm0 + i * 32 + l32) * kLd + kb);
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                b[j] = *reinterpret_cast<const u32x4 *>(Bs + (wn0 + j * 32 + l32) * kLd + kb);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) acc[i][j] = E::mfma(a[i], b[j], acc[i][j]);
+        }
+        if (more) {
+            uint16_t *nxt = lds + (cur ^ 1) * kBuf;
+            la.store(nxt);
+            lb.store(nxt + kASz);
+        }
+        __syncthreads();
+    }
+
+    // Epilogue.  Accumulator register r of lane (h, l32) in block (i, j)
+    // holds C[wm0 + 32i + 8(r/4) + 4h + r%4][wn0 + 32j + l32].
+    float *stage = reinterpret_cast<float *>(lds) + wave * (32 * kStageLd);
+    constexpr int G4 = WTN / 4;  // groups of 4 columns per slice row
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                stage[((r >> 2) * 8 + h * 4 + (r & 3)) * kStageLd + j * 32 + l32] = acc[i][j][r];
+        __syncthreads();
+        for (int e = lane; e < 32 * G4; e += 64) {
+            const int rr = e / G4, c4 = (e % G4) * 4;
+            const int row = m0 + wm0 + i * 32 + rr;
+            const int col = n0 + wn0 + c4;
+            if (row >= p.M || col >= p.N) continue;
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(stage + rr * kStageLd + c4);
+            uint16_t *crow = p.C + (size_t)row * p.ldc;
+            const uint16_t *bias = p.mode == 0 ? p.bias : nullptr;
+            if (p.vec_out && col + 4 <= p.N) {
+                uint16_t o[4], z[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    float zt;
+                    float ot = epi16<BF>(p, v[t], bias, row, col + t, &zt);
+                    z[t] = E::from_f(zt);
+                    if (p.accumulate) ot += E::to_f(crow[col + t]);
+                    o[t] = E::from_f(ot);
+                }
+                if (p.mode == 0 && p.Z)
+                    *reinterpret_cast<u32x2 *>(p.Z + (size_t)row * p.ldz + col) =
+                        u32x2{pack2(z[0], z[1]), pack2(z[2], z[3])};
+                *reinterpret_cast<u32x2 *>(crow + col) =
+                    u32x2{pack2(o[0], o[1]), pack2(o[2], o[3])};
+            } else {
+                for (int t = 0; t < 4 && col + t < p.N; ++t) {
+                    float zt;
+                    float ot = epi16<BF>(p, v[t], bias, row, col + t, &zt);
+                    if (p.mode == 0 && p.Z) p.Z[(size_t)row * p.ldz + col + t] = E::from_f(zt);
+                    if (p.accumulate) ot += E::to_f(crow[col + t]);
+                    crow[col + t] = E::from_f(ot);
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
+template <int BM, int BN, int WGM, int WGN, int BK, bool AK, bool BNC, bool VEC, bool BF>
+void launch_one(const Args &a0, hipStream_t st) {
+    Args a = a0;
+    a.tiles_m = (a.M + BM - 1) / BM;
+    a.tiles_n = (a.N + BN - 1) / BN;
+    gemm16_mfma<BM, BN, BK, WGM, WGN, AK, BNC, VEC, BF>
+        <<<a.tiles_m * a.tiles_n, 64 * WGM * WGN, 0, st>>>(a);
+}
+
+// Tile configurations (BM x BN, waves, K depth):
+//   0: 256x256, 4 waves, BK 32     1: 256x256, 8 waves, BK 32
+//   2: 128x128, 4 waves, BK 32     3:  64x64,  4 waves, BK 32
+//   4: 256x128, 4 waves, BK 32     5: 256x256, 4 waves, BK 64
+// 64x64 is also the only element-load variant, for unaligned operands.
+constexpr int kNumCfgs = 6;
+
+template <bool AK, bool BNC, bool BF>
+void launch_layout(const Args &a, bool vec, int cfg, hipStream_t st) {
+    if (!vec) {
+        launch_one<64, 64, 2, 2, 32, AK, BNC, false, BF>(a, st);
+        return;
+    }
+    switch (cfg) {
+        case 0: launch_one<256, 256, 2, 2, 32, AK, BNC, true, BF>(a, st); break;
+        case 1: launch_one<256, 256, 2, 4, 32, AK, BNC, true, BF>(a, st); break;
+        case 2: launch_one<128, 128, 2, 2, 32, AK, BNC, true, BF>(a, st); break;
+        case 4: launch_one<256, 128, 2, 2, 32, AK, BNC, true, BF>(a, st); break;
+        case 5: launch_one<256, 256, 2, 2, 64, AK, BNC, true, BF>(a, st); break;
+        default: launch_one<64, 64, 2, 2, 32, AK, BNC, true, BF>(a, st); break;
+    }
+}
+
+// Defined in k_gemm16_{bf16,f16}.hip.  layout: FG_NN / FG_NT / FG_TN.
+void launch_bf16(int layout, const Args &a, bool vec, int cfg, hipStream_t st);
+void launch_f16(int layout, const Args &a, bool vec, int cfg, hipStream_t st);
+
+}  // namespace gemm16
+}  // namespace fg

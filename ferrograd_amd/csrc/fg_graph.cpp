@@ -76,9 +76,38 @@ struct GNode {
     int op = FG_OP_INPUT;
     std::vector<uint32_t> in;
     std::vector<uint32_t> fields;  // Input: meta field per dim
-    float value = 0.0f;            // Const
+    float value = 0.0f;            // Const (already rounded to dtype)
     uint32_t flags = 0;            // Input flags
+    int dtype = FG_DTYPE_F32;      // Input / Const: declared; operations: of their first input
 };
+
+int esize(int dt) { return dt == FG_DTYPE_F32 ? 4 : 2; }
+const char *dtype_name(int dt) {
+    return dt == FG_DTYPE_F16 ? "f16" : dt == FG_DTYPE_BF16 ? "bf16" : "f32";
+}
+
+// Host rounding of an fp32 value to a 16-bit type and back (graph constants
+// of F16 / BF16 type hold values of that type): nearest, ties to even.
+float round_host(int dt, float x) {
+    uint32_t u;
+    std::memcpy(&u, &x, 4);
+    if (dt == FG_DTYPE_BF16) {
+        if ((u & 0x7fffffffu) <= 0x7f800000u) u = (u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u;
+    } else if (dt == FG_DTYPE_F16) {
+        const float a = std::fabs(x);
+        if (!(a < 65520.0f)) return a == a ? std::copysign(INFINITY, x) : x;
+        // Scale so the f16 unit in the last place becomes an integer step of
+        // the fp32 value, round with nearbyint (ties to even), scale back.
+        int e;
+        std::frexp(a, &e);
+        const int ulp_exp = std::max(e - 11, -24);  // f16: 11-bit significand, min 2^-24
+        const float r = std::ldexp(std::nearbyint(std::ldexp(x, -ulp_exp)), ulp_exp);
+        std::memcpy(&u, &r, 4);
+    }
+    float r;
+    std::memcpy(&r, &u, 4);
+    return r;
+}
 
 struct Shape {
     bool scalar = false;
@@ -198,6 +227,7 @@ enum LaunchKind {
 
 struct Launch {
     int kind = LK_GEMM;
+    int dtype = FG_DTYPE_F32;  // element type of the launch's tensors
     int layout = FG_NN, M = 0, N = 0, K = 0, lda = 0, ldb = 0, ldc = 0, ldz = 0;
     int act = FG_ACT_NONE, accumulate = 0;
     int sA = kNone, sB = kNone, sC = kNone, sZ = kNone, sBias = kNone, sExtra = kNone;
@@ -215,9 +245,11 @@ struct Launch {
 
 struct Slot {
     uint64_t offset = 0;
-    uint64_t bytes = 0;
+    uint64_t bytes = 0;        // allocated (whole words)
+    uint64_t used = 0;         // elements x element size
     bool external = false;
     void *ext = nullptr;
+    int dtype = FG_DTYPE_F32;  // element type (u32 labels count as 4-byte elements)
 };
 
 struct Group {
@@ -241,6 +273,7 @@ struct fg_plan {
     std::vector<Slot> slots;
     char *arena = nullptr;
     uint64_t arena_bytes = 0;
+    std::vector<int> dtype;        // element type per node
     std::vector<uint32_t> inputs;  // input node ids in order
     std::vector<int> input_slot;
     int target_slot = kNone, loss_slot = kNone, mean_slot = kNone, adam_slot = kNone;
@@ -265,19 +298,25 @@ struct fg_plan {
         const Slot &s = slots[slot];
         return s.external ? s.ext : (void *)(arena + s.offset);
     }
-    int new_slot(uint64_t bytes) {
+    // Slot of `elems` elements of type dt (bytes rounded up to whole words
+    // so word fills cover it).
+    int new_slot(uint64_t elems, int dt = FG_DTYPE_F32) {
         Slot s;
-        s.bytes = bytes;
+        s.used = elems * esize(dt);
+        s.bytes = (s.used + 3) & ~uint64_t(3);
+        s.dtype = dt;
         slots.push_back(s);
         return (int)slots.size() - 1;
     }
-    int new_external(uint64_t bytes) {
+    int new_external(uint64_t elems, int dt = FG_DTYPE_F32) {
         Slot s;
-        s.bytes = bytes;
+        s.bytes = s.used = elems * esize(dt);
+        s.dtype = dt;
         s.external = true;
         slots.push_back(s);
         return (int)slots.size() - 1;
     }
+    int sdt(int slot) const { return slot == kNone ? FG_DTYPE_F32 : slots[slot].dtype; }
     int vslot(uint32_t n) const { return val_slot[n]; }
     ~fg_plan();
 };
@@ -381,8 +420,12 @@ struct EltBuilder {
             L.src_slot[k] = slot;
         }
         const int r = reg();
-        ins(fg::kEltLoad, r, k, 0, mode);
+        ins(fg::kEltLoad, r, k, P.sdt(slot), mode);
         return r;
+    }
+    // Round register r to a 16-bit node type (a node value of that type).
+    void round(int r, int dt) {
+        if (dt != FG_DTYPE_F32) ins(fg::kEltRound, r, r, 0, dt);
     }
     int operand(uint32_t x) {
         const GNode &nd = P.g.nodes[x];
@@ -403,7 +446,7 @@ struct EltBuilder {
             k = ndst++;
             L.dst_slot[k] = slot;
         }
-        ins(accum ? fg::kEltAccum : fg::kEltStore, 0, k, r);
+        ins(accum ? fg::kEltAccum : fg::kEltStore, 0, k, r, P.sdt(slot));
     }
     bool fits(int more_instr, int more_regs, int more_src, int more_dst) const {
         return L.prog.n_instr + more_instr <= fg::kEltMaxInstr &&
@@ -443,6 +486,10 @@ uint8_t unary_code(int op) {
     }
 }
 
+std::string dt_suffix(int dt) {
+    return dt == FG_DTYPE_F32 ? std::string() : std::string(" ") + dtype_name(dt);
+}
+
 std::string dims_str(int M, int N, int K) {
     return std::to_string(M) + "x" + std::to_string(N) + "x" + std::to_string(K);
 }
@@ -462,6 +509,7 @@ int lower_forward(fg_plan &P) {
             const uint32_t a = g.nodes[G.mm].in[0], b = g.nodes[G.mm].in[1];
             Launch L;
             L.kind = LK_GEMM;
+            L.dtype = P.dtype[G.mm];
             L.layout = FG_NN;
             L.M = (int)P.shape[a].rows;
             L.K = (int)P.shape[a].cols;
@@ -478,7 +526,7 @@ int lower_forward(fg_plan &P) {
             L.sC = P.vslot(G.fin);
             L.sZ = G.act_node != kNone ? P.vslot(G.pre) : kNone;
             L.ldz = L.N;
-            L.desc = "forward gemm NN " + dims_str(L.M, L.N, L.K) +
+            L.desc = "forward gemm NN " + dims_str(L.M, L.N, L.K) + dt_suffix(L.dtype) +
                      (L.sBias != kNone ? " +bias" : "") +
                      (L.act == FG_ACT_RELU ? " +relu" : L.act == FG_ACT_GELU ? " +gelu" : "") +
                      " -> node " + std::to_string(G.fin);
@@ -489,6 +537,7 @@ int lower_forward(fg_plan &P) {
             eb.flush(P.fwd, "forward");
             Launch L;
             L.kind = LK_SOFTMAX;
+            L.dtype = P.dtype[n];
             L.M = (int)P.shape[n].rows;
             L.N = (int)P.shape[n].cols;
             L.sA = P.vslot(nd.in[0]);
@@ -500,7 +549,7 @@ int lower_forward(fg_plan &P) {
         }
         // elementwise node
         const Shape &s = P.shape[n];
-        if (!eb.empty() && (eb.numel != s.numel() || eb.cols != s.cols || !eb.fits(6, 4, 2, 1)))
+        if (!eb.empty() && (eb.numel != s.numel() || eb.cols != s.cols || !eb.fits(7, 4, 2, 1)))
             eb.flush(P.fwd, "forward");
         if (eb.empty()) eb.begin(s.numel(), s.cols);
         int r;
@@ -518,6 +567,7 @@ int lower_forward(fg_plan &P) {
                                                                                : fg::kEltDiv;
             eb.ins(code, r, x, y);
         }
+        eb.round(r, P.dtype[n]);
         eb.reg_of.push_back({n, r});
         eb.store(P.vslot(n), r, false);
         eb.names.push_back(std::string(op_name(nd.op)) + "#" + std::to_string(n));
@@ -534,6 +584,7 @@ int lower_loss(fg_plan &P) {
         const uint32_t x = g.nodes[last].in[0];
         Launch L;
         L.kind = LK_SMCE;
+        L.dtype = P.dtype[x];
         L.M = (int)s.rows;
         L.N = (int)s.cols;
         L.sA = P.vslot(x);
@@ -728,6 +779,7 @@ int lower_backward(fg_plan &P, bool fused, std::vector<Launch> &out) {
                 if (!P.needs_grad[x]) return;
                 Launch L;
                 L.kind = LK_BIAS_GRAD;
+                L.dtype = P.sdt(gs(n));
                 L.M = (int)s.rows;
                 L.N = (int)s.cols;
                 L.sA = gs(n);
@@ -742,7 +794,7 @@ int lower_backward(fg_plan &P, bool fused, std::vector<Launch> &out) {
                 }
                 // sub's broadcast operand: reduce into a temporary, then
                 // grad (=|+=) -temporary.
-                const int tmp = P.new_slot((uint64_t)L.N * 4);
+                const int tmp = P.new_slot((uint64_t)L.N, L.dtype);
                 L.sC = tmp;
                 L.desc += " -> temporary";
                 out.push_back(L);
@@ -799,6 +851,7 @@ int lower_backward(fg_plan &P, bool fused, std::vector<Launch> &out) {
             if (G.bias_src != kNone && P.needs_grad[G.bias_src]) {
                 Launch L;
                 L.kind = LK_BIAS_GRAD;
+                L.dtype = P.sdt(gs(pre));
                 L.M = M;
                 L.N = N;
                 L.sA = gs(pre);
@@ -812,6 +865,7 @@ int lower_backward(fg_plan &P, bool fused, std::vector<Launch> &out) {
             if (P.needs_grad[b]) {  // dB = A^T dZ
                 Launch L;
                 L.kind = LK_GEMM;
+                L.dtype = P.dtype[G.mm];
                 L.layout = FG_TN;
                 L.M = K;
                 L.N = N;
@@ -831,6 +885,7 @@ int lower_backward(fg_plan &P, bool fused, std::vector<Launch> &out) {
             if (P.needs_grad[a]) {  // dA = dZ B^T  (with act' of the layer below fused)
                 Launch L;
                 L.kind = LK_GEMM_BWD;
+                L.dtype = P.dtype[G.mm];
                 L.layout = FG_NT;
                 L.M = M;
                 L.N = K;
@@ -872,6 +927,7 @@ int lower_backward(fg_plan &P, bool fused, std::vector<Launch> &out) {
             if (!P.needs_grad[x]) continue;
             Launch L;
             L.kind = LK_SOFTMAX_BWD;
+            L.dtype = P.dtype[n];
             L.M = (int)P.shape[n].rows;
             L.N = (int)P.shape[n].cols;
             L.sA = P.vslot(n);
@@ -892,7 +948,7 @@ int lower_backward(fg_plan &P, bool fused, std::vector<Launch> &out) {
         Launch L;
         L.kind = LK_FILL0;
         L.sC = gs(n);
-        L.count = (uint64_t)P.shape[n].numel();
+        L.count = P.slots[gs(n)].bytes / 4;  // words (slot sizes are whole words)
         L.desc = "backward zero grad of node " + std::to_string(n);
         out.push_back(L);
     }
@@ -914,8 +970,11 @@ int check_slot(const fg_plan &P, const Launch &L, int slot, uint64_t need, const
 int check_launch(const fg_plan &P, const Launch &L) {
     const uint64_t M = (uint64_t)L.M, N = (uint64_t)L.N, K = (uint64_t)L.K;
     int rc = FG_OK;
-    auto chk = [&](int slot, uint64_t floats, const char *what) {
-        if (rc == FG_OK) rc = check_slot(P, L, slot, floats * 4, what);
+    // elems of the slot's own element type (fill counts are words).
+    auto chk = [&](int slot, uint64_t elems, const char *what) {
+        if (rc == FG_OK && slot != kNone)
+            rc = check_slot(P, L, slot,
+                            elems * (L.kind == LK_FILL0 ? 4 : esize(P.slots[slot].dtype)), what);
     };
     switch (L.kind) {
         case LK_GEMM:
@@ -991,37 +1050,45 @@ int run(fg_plan &P, const std::vector<Launch> &list) {
         int rc = FG_OK;
         switch (L.kind) {
             case LK_GEMM:
-                rc = fg_gemm_f32(ctx, L.layout, L.M, L.N, L.K, (const float *)P.ptr(L.sA), L.lda,
-                                 (const float *)P.ptr(L.sB), L.ldb, (const float *)P.ptr(L.sBias),
-                                 L.act, (float *)P.ptr(L.sC), L.ldc, (float *)P.ptr(L.sZ), L.ldz,
-                                 L.accumulate);
+                if (L.dtype == FG_DTYPE_F32)
+                    rc = fg_gemm_f32(ctx, L.layout, L.M, L.N, L.K, (const float *)P.ptr(L.sA),
+                                     L.lda, (const float *)P.ptr(L.sB), L.ldb,
+                                     (const float *)P.ptr(L.sBias), L.act, (float *)P.ptr(L.sC),
+                                     L.ldc, (float *)P.ptr(L.sZ), L.ldz, L.accumulate);
+                else
+                    rc = fg_gemm_x16(ctx, L.dtype, L.layout, L.M, L.N, L.K, P.ptr(L.sA), L.lda,
+                                     P.ptr(L.sB), L.ldb, P.ptr(L.sBias), L.act, P.ptr(L.sC),
+                                     L.ldc, P.ptr(L.sZ), L.ldz, L.accumulate);
                 break;
             case LK_GEMM_BWD:
-                rc = fg_gemm_bwd_f32(ctx, L.layout, L.M, L.N, L.K, (const float *)P.ptr(L.sA),
-                                     L.lda, (const float *)P.ptr(L.sB), L.ldb, L.act,
-                                     (const float *)P.ptr(L.sZ), L.ldz, (float *)P.ptr(L.sC),
-                                     L.ldc, L.accumulate);
+                if (L.dtype == FG_DTYPE_F32)
+                    rc = fg_gemm_bwd_f32(ctx, L.layout, L.M, L.N, L.K,
+                                         (const float *)P.ptr(L.sA), L.lda,
+                                         (const float *)P.ptr(L.sB), L.ldb, L.act,
+                                         (const float *)P.ptr(L.sZ), L.ldz,
+                                         (float *)P.ptr(L.sC), L.ldc, L.accumulate);
+                else
+                    rc = fg_gemm_bwd_x16(ctx, L.dtype, L.layout, L.M, L.N, L.K, P.ptr(L.sA),
+                                         L.lda, P.ptr(L.sB), L.ldb, L.act, P.ptr(L.sZ), L.ldz,
+                                         P.ptr(L.sC), L.ldc, L.accumulate);
                 break;
             case LK_BIAS_GRAD:
-                rc = fg_bias_grad_f32(ctx, L.M, L.N, (const float *)P.ptr(L.sA), L.N,
-                                      (float *)P.ptr(L.sC), L.accumulate);
+                rc = fg_bias_grad(ctx, L.dtype, L.M, L.N, P.ptr(L.sA), L.N, P.ptr(L.sC),
+                                  L.accumulate);
                 break;
             case LK_SOFTMAX:
-                rc = fg_softmax_f32(ctx, (const float *)P.ptr(L.sA), L.M, L.N,
-                                    (float *)P.ptr(L.sC));
+                rc = fg_softmax(ctx, L.dtype, P.ptr(L.sA), L.M, L.N, P.ptr(L.sC));
                 break;
             case LK_SOFTMAX_BWD:
-                rc = fg_softmax_bwd_f32(ctx, (const float *)P.ptr(L.sA),
-                                        (const float *)P.ptr(L.sB), L.M, L.N,
-                                        (float *)P.ptr(L.sC), L.accumulate);
+                rc = fg_softmax_bwd(ctx, L.dtype, P.ptr(L.sA), P.ptr(L.sB), L.M, L.N, P.ptr(L.sC),
+                                    L.accumulate);
                 break;
             case LK_SMCE:
                 FG_REQUIRE(P.ptr(L.sZ), FG_ERR_INVALID_ARGUMENT,
                            "dispatch_loss: no target bound (fg_plan_bind_target)");
-                rc = fg_softmax_ce_f32(ctx, (const float *)P.ptr(L.sA), L.N,
-                                       (const uint32_t *)P.ptr(L.sZ), L.M, L.N, 1.0f,
-                                       (float *)P.ptr(L.sB), (float *)P.ptr(L.sBias),
-                                       (float *)P.ptr(L.sC), L.N, nullptr);
+                rc = fg_softmax_ce(ctx, L.dtype, P.ptr(L.sA), L.N, (const uint32_t *)P.ptr(L.sZ),
+                                   L.M, L.N, 1.0f, (float *)P.ptr(L.sB), (float *)P.ptr(L.sBias),
+                                   P.ptr(L.sC), L.N, nullptr);
                 break;
             case LK_ELT: {
                 fg::EltProgram p = L.prog;
@@ -1068,24 +1135,28 @@ int ensure_mt(fg_plan &P) {
         return FG_OK;
     }
     const bool adam = P.g.optim == FG_OPTIM_ADAM;
-    std::vector<float *> pp, gg, mm, vv;
+    std::vector<void *> pp, gg;
+    std::vector<float *> mm, vv;
     std::vector<uint64_t> sz;
+    std::vector<int> dts;
     for (uint32_t idx : P.opt_inputs) {
         const uint32_t n = P.inputs[idx];
-        pp.push_back((float *)P.ptr(P.input_slot[idx]));
-        gg.push_back((float *)P.ptr(P.grad_slot[n]));
+        pp.push_back(P.ptr(P.input_slot[idx]));
+        gg.push_back(P.ptr(P.grad_slot[n]));
+        dts.push_back(P.dtype[n]);
         if (adam) {
             mm.push_back((float *)P.ptr(P.m_slot[idx]));
             vv.push_back((float *)P.ptr(P.v_slot[idx]));
         }
         sz.push_back((uint64_t)P.shape[n].numel());
     }
-    int rc = fg_mt_create(P.ctx, (int)pp.size(), pp.data(), gg.data(), adam ? mm.data() : nullptr,
-                          adam ? vv.data() : nullptr, sz.data(), &P.mt_all);
+    int rc = fg_mt_create_x(P.ctx, (int)pp.size(), dts.data(), pp.data(), gg.data(),
+                            adam ? mm.data() : nullptr, adam ? vv.data() : nullptr, sz.data(),
+                            &P.mt_all);
     if (rc) return rc;
     for (size_t k = 0; k < P.opt_inputs.size(); ++k) {
-        rc = fg_mt_create(P.ctx, 1, &pp[k], &gg[k], adam ? &mm[k] : nullptr,
-                          adam ? &vv[k] : nullptr, &sz[k], &P.mt_single[P.opt_inputs[k]]);
+        rc = fg_mt_create_x(P.ctx, 1, &dts[k], &pp[k], &gg[k], adam ? &mm[k] : nullptr,
+                            adam ? &vv[k] : nullptr, &sz[k], &P.mt_single[P.opt_inputs[k]]);
         if (rc) return rc;
     }
     P.mt_dirty = false;
@@ -1168,6 +1239,23 @@ FG_API int fg_graph_input(fg_graph *g, const uint32_t *fields, int rank, uint32_
     return FG_OK;
 }
 
+FG_API int fg_graph_input_x(fg_graph *g, const uint32_t *fields, int rank, int dtype,
+                           uint32_t *node) {
+    FG_REQUIRE(dtype >= FG_DTYPE_F32 && dtype <= FG_DTYPE_BF16, FG_ERR_UNSUPPORTED,
+               "fg_graph_input_x: element type %d is not F32 / F16 / BF16", dtype);
+    int rc = fg_graph_input(g, fields, rank, node);
+    if (rc == FG_OK) g->nodes[*node].dtype = dtype;
+    return rc;
+}
+
+FG_API int fg_graph_constant(fg_graph *g, int dtype, float value, uint32_t *node) {
+    FG_REQUIRE(dtype >= FG_DTYPE_F32 && dtype <= FG_DTYPE_BF16, FG_ERR_UNSUPPORTED,
+               "fg_graph_constant: element type %d is not F32 / F16 / BF16", dtype);
+    int rc = fg_graph_constant_f32(g, round_host(dtype, value), node);
+    if (rc == FG_OK) g->nodes[*node].dtype = dtype;
+    return rc;
+}
+
 FG_API int fg_graph_constant_f32(fg_graph *g, float value, uint32_t *node) {
     FG_REQUIRE(g && node, FG_ERR_INVALID_ARGUMENT, "fg_graph_constant_f32: NULL argument");
     GNode nd;
@@ -1228,6 +1316,13 @@ FG_API int fg_plan_create(fg_ctx *ctx, const fg_graph *g, const uint32_t *meta, 
     const fg_graph &G = P->g;
     const size_t nn = G.nodes.size();
     P->last = (int)nn - 1;
+    // Element types: an operation takes its first input's type
+    // (op/binary.rs:232, unary.rs, matmul/mod.rs:294).
+    P->dtype.assign(nn, FG_DTYPE_F32);
+    for (uint32_t i = 0; i < nn; ++i) {
+        const GNode &nd = G.nodes[i];
+        P->dtype[i] = nd.in.empty() ? nd.dtype : P->dtype[nd.in[0]];
+    }
     float lr;
     std::memcpy(&lr, &meta[0], 4);
     P->lr = lr;
@@ -1265,6 +1360,9 @@ FG_API int fg_plan_create(fg_ctx *ctx, const fg_graph *g, const uint32_t *meta, 
     P->group_of.assign(nn, kNone);
     for (uint32_t i = 0; i < nn; ++i) {
         if (G.nodes[i].op != FG_OP_MATMUL) continue;
+        FG_REQUIRE(P->dtype[G.nodes[i].in[0]] == P->dtype[G.nodes[i].in[1]], FG_ERR_UNSUPPORTED,
+                   "matmul %u: operands of different element types (%s, %s)", i,
+                   dtype_name(P->dtype[G.nodes[i].in[0]]), dtype_name(P->dtype[G.nodes[i].in[1]]));
         Group gr;
         gr.mm = (int)i;
         int cur = (int)i;
@@ -1274,7 +1372,8 @@ FG_API int fg_plan_create(fg_ctx *ctx, const fg_graph *g, const uint32_t *meta, 
             if ((un.op == FG_OP_BIAS_ADD || un.op == FG_OP_ADD) && un.in[0] == i &&
                 un.in[1] != i) {
                 const Shape &sb = P->shape[un.in[1]];
-                if (sb.vector && sb.cols == P->shape[i].cols && G.nodes[un.in[1]].op != FG_OP_CONST) {
+                if (sb.vector && sb.cols == P->shape[i].cols &&
+                    G.nodes[un.in[1]].op != FG_OP_CONST && P->dtype[un.in[1]] == P->dtype[i]) {
                     gr.bias_node = (int)u;
                     gr.bias_src = (int)un.in[1];
                     cur = (int)u;
@@ -1302,34 +1401,40 @@ FG_API int fg_plan_create(fg_ctx *ctx, const fg_graph *g, const uint32_t *meta, 
     P->input_slot.assign(P->inputs.size(), kNone);
     for (size_t k = 0; k < P->inputs.size(); ++k) {
         const uint32_t n = P->inputs[k];
-        P->input_slot[k] = P->new_external((uint64_t)P->shape[n].numel() * 4);
+        P->input_slot[k] = P->new_external((uint64_t)P->shape[n].numel(), P->dtype[n]);
         P->val_slot[n] = P->input_slot[k];
     }
     for (uint32_t i = 0; i < nn; ++i) {
         const int op = G.nodes[i].op;
         if (op == FG_OP_INPUT || op == FG_OP_CONST) continue;
-        P->val_slot[i] = P->new_slot((uint64_t)P->shape[i].numel() * 4);
+        P->val_slot[i] = P->new_slot((uint64_t)P->shape[i].numel(), P->dtype[i]);
     }
     for (const Group &gr : P->groups)  // the pre-bias product is not materialised
         if (gr.bias_node != kNone) P->val_slot[gr.mm] = P->val_slot[gr.bias_node];
     for (uint32_t i = 0; i < nn; ++i) {
         if (G.nodes[i].op == FG_OP_CONST) continue;
         if (P->needs_grad[i] || (int)i == P->last)
-            P->grad_slot[i] = P->new_slot((uint64_t)P->shape[i].numel() * 4);
+            P->grad_slot[i] = P->new_slot((uint64_t)P->shape[i].numel(), P->dtype[i]);
     }
     for (const Group &gr : P->groups)  // d(matmul) == d(bias add)
         if (gr.bias_node != kNone && P->grad_slot[gr.bias_node] != kNone)
             P->grad_slot[gr.mm] = P->grad_slot[gr.bias_node];
     const Shape &ls = P->shape[P->last];
+    // Loss and target: CE on a final softmax keeps fp32 per-row losses and
+    // u32 labels; otherwise both are of the output's type (dispatch/mod.rs:
+    // 551-562 sizes loss_t by the last node's type).
+    const int ldt = P->dtype[P->last];
     if (G.loss == FG_LOSS_CE) {
         P->target_bytes = (uint64_t)ls.rows * 4;
-        P->loss_slot = P->new_slot((uint64_t)(P->ce_fused_possible ? ls.rows : ls.numel()) * 4);
+        P->target_slot = P->new_external((uint64_t)ls.rows);
+        P->loss_slot = P->ce_fused_possible ? P->new_slot((uint64_t)ls.rows)
+                                            : P->new_slot((uint64_t)ls.numel(), ldt);
     } else {
-        P->target_bytes = (uint64_t)ls.numel() * 4;
-        P->loss_slot = P->new_slot((uint64_t)ls.numel() * 4);
+        P->target_bytes = (uint64_t)ls.numel() * esize(ldt);
+        P->target_slot = P->new_external((uint64_t)ls.numel(), ldt);
+        P->loss_slot = P->new_slot((uint64_t)ls.numel(), ldt);
     }
-    P->target_slot = P->new_external(P->target_bytes);
-    P->mean_slot = P->new_slot(4);
+    P->mean_slot = P->new_slot(1);
     // Optimiser.
     for (size_t k = 0; k < P->inputs.size(); ++k) {
         const GNode &nd = G.nodes[P->inputs[k]];
@@ -1339,11 +1444,11 @@ FG_API int fg_plan_create(fg_ctx *ctx, const fg_graph *g, const uint32_t *meta, 
     P->v_slot.assign(P->inputs.size(), kNone);
     if (G.optim == FG_OPTIM_ADAM) {
         for (uint32_t k : P->opt_inputs) {
-            const uint64_t b = (uint64_t)P->shape[P->inputs[k]].numel() * 4;
-            P->m_slot[k] = P->new_slot(b);
-            P->v_slot[k] = P->new_slot(b);
+            const uint64_t e = (uint64_t)P->shape[P->inputs[k]].numel();
+            P->m_slot[k] = P->new_slot(e);  // fp32 state whatever the parameter type
+            P->v_slot[k] = P->new_slot(e);
         }
-        P->adam_slot = P->new_slot(fg::adam_dev_state_bytes());
+        P->adam_slot = P->new_slot((fg::adam_dev_state_bytes() + 3) / 4);
     }
     // Exposed lists in SaveIndicator order.
     for (uint32_t i = 0; i < nn; ++i) {
@@ -1427,8 +1532,34 @@ FG_API int fg_plan_count(const fg_plan *p, int role, int *count) {
     return FG_OK;
 }
 
+namespace {
+int plan_slot_of(const fg_plan *p, int role, int index, int *slot_out, uint32_t *node_out);
+}
+
 FG_API int fg_plan_tensor(const fg_plan *p, int role, int index, void **d_ptr, uint64_t *bytes,
                           uint32_t *node) {
+    int slot = kNone;
+    uint32_t nd = 0;
+    int rc = plan_slot_of(p, role, index, &slot, &nd);
+    if (rc) return rc;
+    if (d_ptr) *d_ptr = p->ptr(slot);
+    if (bytes) *bytes = p->slots[slot].used;
+    if (node) *node = nd;
+    return FG_OK;
+}
+
+FG_API int fg_plan_tensor_dtype(const fg_plan *p, int role, int index, int *dtype) {
+    FG_REQUIRE(dtype, FG_ERR_INVALID_ARGUMENT, "fg_plan_tensor_dtype: dtype is NULL");
+    int slot = kNone;
+    uint32_t nd = 0;
+    int rc = plan_slot_of(p, role, index, &slot, &nd);
+    if (rc) return rc;
+    *dtype = p->slots[slot].dtype;
+    return FG_OK;
+}
+
+namespace {
+int plan_slot_of(const fg_plan *p, int role, int index, int *slot_out, uint32_t *node_out) {
     FG_REQUIRE(p, FG_ERR_INVALID_ARGUMENT, "fg_plan_tensor: plan is NULL");
     int cnt = 0;
     int rc = fg_plan_count(p, role, &cnt);
@@ -1453,18 +1584,18 @@ FG_API int fg_plan_tensor(const fg_plan *p, int role, int index, void **d_ptr, u
             break;
         }
     }
-    if (d_ptr) *d_ptr = p->ptr(slot);
-    if (bytes) *bytes = p->slots[slot].bytes;
-    if (node) *node = nd;
+    *slot_out = slot;
+    *node_out = nd;
     return FG_OK;
 }
+}  // namespace
 
 FG_API int fg_plan_bind_input(fg_plan *p, int index, void *d_ptr, uint64_t bytes) {
     FG_REQUIRE(p && d_ptr, FG_ERR_INVALID_ARGUMENT, "fg_plan_bind_input: NULL argument");
     FG_REQUIRE(index >= 0 && index < (int)p->inputs.size(), FG_ERR_OUT_OF_BOUNDS,
                "fg_plan_bind_input: input %d out of range (%zu inputs)", index, p->inputs.size());
     Slot &s = p->slots[p->input_slot[index]];
-    FG_REQUIRE(bytes >= s.bytes, FG_ERR_SHAPE,
+    FG_REQUIRE(bytes >= s.used, FG_ERR_SHAPE,
                "fg_plan_bind_input: input %d needs %llu bytes, got %llu", index,
                (unsigned long long)s.bytes, (unsigned long long)bytes);
     if (s.ext != d_ptr) {
@@ -1595,6 +1726,127 @@ FG_API int fg_plan_launch_step(fg_plan *p) {
                "inputs, target or hyper-parameters drops the capture)");
     FG_HIP(hipSetDevice(p->ctx->device));
     FG_HIP(hipGraphLaunch(p->exec, p->ctx->stream));
+    return FG_OK;
+}
+
+// ------------------------------------------------------------ checkpoints
+// A checkpoint is a bpat file holding every Input in input order, then for
+// Adam the m and v state of each updated input and a one-element tensor
+// with the step count (the reference's io::save_tensors covers the tensors
+// a caller passes; optimiser state has no counterpart there).
+namespace {
+int plan_ckpt_tensors(const fg_plan *p, std::vector<fg_bpat_tensor> &ts) {
+    auto add = [&](int slot, uint32_t node) -> int {
+        fg_bpat_tensor t{};
+        t.d_ptr = p->ptr(slot);
+        FG_REQUIRE(t.d_ptr, FG_ERR_INVALID_ARGUMENT,
+                   "checkpoint: input node %u is not bound", node);
+        t.dtype = p->slots[slot].dtype;
+        const Shape &sh = p->shape[node];
+        if (sh.vector) {
+            t.rank = 1;
+            t.shape[0] = (uint32_t)sh.cols;
+        } else {
+            t.rank = 2;
+            t.shape[0] = (uint32_t)sh.rows;
+            t.shape[1] = (uint32_t)sh.cols;
+        }
+        ts.push_back(t);
+        return FG_OK;
+    };
+    for (size_t k = 0; k < p->inputs.size(); ++k)
+        if (int rc = add(p->input_slot[k], p->inputs[k])) return rc;
+    if (p->g.optim == FG_OPTIM_ADAM) {
+        for (uint32_t k : p->opt_inputs) {
+            if (int rc = add(p->m_slot[k], p->inputs[k])) return rc;
+            ts.back().dtype = FG_DTYPE_F32;
+            if (int rc = add(p->v_slot[k], p->inputs[k])) return rc;
+            ts.back().dtype = FG_DTYPE_F32;
+        }
+    }
+    return FG_OK;
+}
+}  // namespace
+
+FG_API int fg_plan_save(fg_plan *p, const char *path, int header) {
+    FG_REQUIRE(p && p->ctx && path, FG_ERR_INVALID_ARGUMENT, "fg_plan_save: NULL argument");
+    std::vector<fg_bpat_tensor> ts;
+    if (int rc = plan_ckpt_tensors(p, ts)) return rc;
+    float step = 0.0f;
+    if (p->g.optim == FG_OPTIM_ADAM) {
+        uint32_t st[4];
+        FG_HIP(hipSetDevice(p->ctx->device));
+        FG_HIP(hipMemcpyAsync(st, p->ptr(p->adam_slot), sizeof st, hipMemcpyDeviceToHost,
+                              p->ctx->stream));
+        FG_HIP(hipStreamSynchronize(p->ctx->stream));
+        step = (float)st[0];
+    }
+    // Host copies of every tensor, then one write (with the step count last).
+    std::vector<fg_bpat_tensor> all;
+    std::vector<std::vector<uint8_t>> host(ts.size());
+    FG_HIP(hipSetDevice(p->ctx->device));
+    for (size_t i = 0; i < ts.size(); ++i) {
+        uint64_t n = 1;
+        for (int d = 0; d < ts[i].rank; ++d) n *= ts[i].shape[d];
+        host[i].resize(n * esize(ts[i].dtype));
+        if (n)
+            FG_HIP(hipMemcpyAsync(host[i].data(), ts[i].d_ptr, host[i].size(),
+                                  hipMemcpyDeviceToHost, p->ctx->stream));
+        fg_bpat_tensor h = ts[i];
+        h.d_ptr = host[i].data();
+        all.push_back(h);
+    }
+    FG_HIP(hipStreamSynchronize(p->ctx->stream));
+    if (p->g.optim == FG_OPTIM_ADAM) {
+        fg_bpat_tensor s{};
+        s.d_ptr = &step;
+        s.dtype = FG_DTYPE_F32;
+        s.rank = 1;
+        s.shape[0] = 1;
+        all.push_back(s);
+    }
+    return fg_bpat_save_host(path, header, (int)all.size(), all.data());
+}
+
+FG_API int fg_plan_load(fg_plan *p, const char *path) {
+    FG_REQUIRE(p && p->ctx && path, FG_ERR_INVALID_ARGUMENT, "fg_plan_load: NULL argument");
+    std::vector<fg_bpat_tensor> ts;
+    if (int rc = plan_ckpt_tensors(p, ts)) return rc;
+    fg_bpat *f = nullptr;
+    if (int rc = fg_bpat_open(path, &f)) return rc;
+    std::unique_ptr<fg_bpat, int (*)(fg_bpat *)> guard(f, fg_bpat_close);
+    int count = 0;
+    fg_bpat_info(f, nullptr, &count);
+    const bool adam = p->g.optim == FG_OPTIM_ADAM;
+    FG_REQUIRE(count == (int)ts.size() + (adam ? 1 : 0), FG_ERR_SHAPE,
+               "fg_plan_load: %s holds %d tensors, the plan expects %zu", path, count,
+               ts.size() + (adam ? 1 : 0));
+    for (size_t i = 0; i < ts.size(); ++i) {
+        uint64_t n = 0, want = 1;
+        fg_bpat_tensor_info(f, (int)i, nullptr, nullptr, &n);
+        for (int d = 0; d < ts[i].rank; ++d) want *= ts[i].shape[d];
+        FG_REQUIRE(n == want, FG_ERR_SHAPE, "fg_plan_load: tensor %zu has %llu elements, not %llu",
+                   i, (unsigned long long)n, (unsigned long long)want);
+    }
+    for (size_t i = 0; i < ts.size(); ++i)
+        if (int rc = fg_bpat_upload(p->ctx, f, (int)i, const_cast<void *>(ts[i].d_ptr),
+                                    ts[i].dtype))
+            return rc;
+    if (adam) {
+        uint64_t n = 0;
+        fg_bpat_tensor_info(f, (int)ts.size(), nullptr, nullptr, &n);
+        FG_REQUIRE(n == 1, FG_ERR_SHAPE, "fg_plan_load: the step-count tensor has %llu elements",
+                   (unsigned long long)n);
+        float step = 0.0f;
+        fg_bpat_read_f32(f, (int)ts.size(), &step);
+        FG_REQUIRE(step >= 0.0f && step < 4294967296.0f && step == std::floor(step),
+                   FG_ERR_SERIALIZATION, "fg_plan_load: step count %g is not a count", step);
+        const uint32_t st[4] = {(uint32_t)step, 0u, 0u, 0u};
+        FG_HIP(hipSetDevice(p->ctx->device));
+        FG_HIP(hipMemcpyAsync(p->ptr(p->adam_slot), st, sizeof st, hipMemcpyHostToDevice,
+                              p->ctx->stream));
+        FG_HIP(hipStreamSynchronize(p->ctx->stream));
+    }
     return FG_OK;
 }
 

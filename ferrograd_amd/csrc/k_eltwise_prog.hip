@@ -6,6 +6,7 @@
 
 #include "fg_act.h"
 #include "fg_eltwise.h"
+#include "fg_half.h"
 #include "fg_internal.h"
 
 namespace fg {
@@ -14,10 +15,10 @@ namespace {
 
 constexpr int kThreads = 256;
 
-__device__ __forceinline__ float elt_load(const EltProgram &p, int s, int mode, uint64_t i) {
-    if (mode == kModeScalar) return p.src[s][0];
-    if (mode == kModeRow) return p.src[s][i % p.cols];
-    return p.src[s][i];
+__device__ __forceinline__ float elt_load(const EltProgram &p, int s, int mode, int dt,
+                                          uint64_t i) {
+    const uint64_t j = mode == kModeScalar ? 0 : mode == kModeRow ? i % p.cols : i;
+    return load_as_f(p.src[s], dt, j);
 }
 
 __global__ __launch_bounds__(kThreads) void eltwise_prog_kernel(const EltProgram p) {
@@ -29,10 +30,14 @@ __global__ __launch_bounds__(kThreads) void eltwise_prog_kernel(const EltProgram
         for (int k = 0; k < p.n_instr; ++k) {
             const EltInstr in = p.ins[k];
             switch (in.op) {
-                case kEltLoad: r[in.dst & 15] = elt_load(p, in.a, in.c, i); break;
+                case kEltLoad: r[in.dst & 15] = elt_load(p, in.a, in.c, in.b, i); break;
                 case kEltImm: r[in.dst & 15] = in.imm; break;
-                case kEltStore: p.dst[in.a][i] = r[in.b & 15]; break;
-                case kEltAccum: p.dst[in.a][i] += r[in.b & 15]; break;
+                case kEltStore: store_from_f(p.dst[in.a], in.c, i, r[in.b & 15]); break;
+                case kEltAccum:
+                    store_from_f(p.dst[in.a], in.c, i,
+                                 load_as_f(p.dst[in.a], in.c, i) + r[in.b & 15]);
+                    break;
+                case kEltRound: r[in.dst & 15] = round_to(in.c, r[in.a & 15]); break;
                 case kEltAdd: r[in.dst & 15] = r[in.a & 15] + r[in.b & 15]; break;
                 case kEltSub: r[in.dst & 15] = r[in.a & 15] - r[in.b & 15]; break;
                 case kEltMul: r[in.dst & 15] = r[in.a & 15] * r[in.b & 15]; break;
@@ -92,11 +97,19 @@ int launch_eltwise(fg_ctx *ctx, const EltProgram &p) {
                        "eltwise program: load of missing source %d", in.a);
             FG_REQUIRE(in.c <= kModeScalar, FG_ERR_INTERNAL,
                        "eltwise program: bad addressing mode %d", in.c);
+            FG_REQUIRE(in.b <= kBF16, FG_ERR_INTERNAL, "eltwise program: bad load type %d",
+                       in.b);
             if (in.c == kModeRow) needs_cols = true;
         }
-        if (in.op == kEltStore || in.op == kEltAccum)
+        if (in.op == kEltStore || in.op == kEltAccum) {
             FG_REQUIRE(in.a < kEltMaxDst && p.dst[in.a], FG_ERR_INTERNAL,
                        "eltwise program: store to missing destination %d", in.a);
+            FG_REQUIRE(in.c <= kBF16, FG_ERR_INTERNAL, "eltwise program: bad store type %d",
+                       in.c);
+        }
+        if (in.op == kEltRound)
+            FG_REQUIRE(in.c <= kBF16, FG_ERR_INTERNAL, "eltwise program: bad round type %d",
+                       in.c);
         if (in.op == kEltLabelEq) {
             FG_REQUIRE(p.labels, FG_ERR_INTERNAL, "eltwise program: labels missing");
             needs_cols = true;

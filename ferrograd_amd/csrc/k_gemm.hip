@@ -7,6 +7,7 @@
 #include <cmath>
 
 #include "fg_gemm_kernel.h"
+#include "fg_half.h"
 #include "fg_internal.h"
 
 namespace {
@@ -90,10 +91,14 @@ int gemm_common(fg_ctx *ctx, int layout, GemmArgs &a, const char *who) {
 constexpr int kBgCols = 256;  // columns per strip (64 lanes x float4)
 constexpr int kBgRowsPerThreadGroup = kThreads / (kBgCols / 4);  // 4 row groups
 
-__global__ __launch_bounds__(kThreads) void bias_grad_partial(const float *__restrict__ dZ, int M,
+// DT: element type of dZ (fg_half.h codes); 16-bit rows are read 4
+// elements (8 bytes) at a time when aligned.
+template <int DT>
+__global__ __launch_bounds__(kThreads) void bias_grad_partial(const void *__restrict__ dZ, int M,
                                                               int N, int ld, int rows_per_split,
                                                               float *__restrict__ partial,
                                                               int vec) {
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
     __shared__ f32x4 sh[kThreads];
     const int strip = blockIdx.x, split = blockIdx.y;
     const int cq = threadIdx.x % (kBgCols / 4);
@@ -104,13 +109,22 @@ __global__ __launch_bounds__(kThreads) void bias_grad_partial(const float *__res
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
     if (col < N) {
         for (int r = r0 + rg; r < r1; r += kBgRowsPerThreadGroup) {
-            const float *row = dZ + (size_t)r * ld;
+            const uint64_t row = (uint64_t)r * ld;
             if (vec && col + 4 <= N) {
-                s += *reinterpret_cast<const f32x4 *>(row + col);
+                if constexpr (DT == fg::kF32) {
+                    s += *reinterpret_cast<const f32x4 *>(static_cast<const float *>(dZ) + row +
+                                                          col);
+                } else {
+                    const u32x2 w = *reinterpret_cast<const u32x2 *>(
+                        static_cast<const uint16_t *>(dZ) + row + col);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        s[e] += fg::h16_to_f(DT, (uint16_t)(w[e >> 1] >> (16 * (e & 1))));
+                }
             } else {
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    if (col + e < N) s[e] += row[col + e];
+                    if (col + e < N) s[e] += fg::load_as_f(dZ, DT, row + col + e);
             }
         }
     }
@@ -126,15 +140,17 @@ __global__ __launch_bounds__(kThreads) void bias_grad_partial(const float *__res
     }
 }
 
+// Adds the splits of each column in order; the sum is rounded to the
+// element type dt once (with accumulate: round(dbias + sum)).
 __global__ __launch_bounds__(kThreads) void bias_grad_final(const float *__restrict__ partial,
                                                             int splits, int N,
-                                                            float *__restrict__ dbias,
-                                                            int accumulate) {
+                                                            void *__restrict__ dbias,
+                                                            int accumulate, int dt) {
     const int col = blockIdx.x * kThreads + threadIdx.x;
     if (col >= N) return;
     float s = 0.0f;
     for (int k = 0; k < splits; ++k) s += partial[(size_t)k * N + col];
-    dbias[col] = accumulate ? dbias[col] + s : s;
+    fg::store_from_f(dbias, dt, col, accumulate ? fg::load_as_f(dbias, dt, col) + s : s);
 }
 
 }  // namespace
@@ -192,13 +208,15 @@ FG_API int fg_gemm_bwd_f32(fg_ctx *ctx, int layout, int M, int N, int K, const f
     return gemm_common(ctx, layout, a, "fg_gemm_bwd_f32");
 }
 
-FG_API int fg_bias_grad_f32(fg_ctx *ctx, int M, int N, const float *d_dZ, int ld, float *d_dbias,
-                            int accumulate) {
-    FG_REQUIRE(ctx, FG_ERR_INVALID_ARGUMENT, "fg_bias_grad_f32: ctx is NULL");
+FG_API int fg_bias_grad(fg_ctx *ctx, int dtype, int M, int N, const void *d_dZ, int ld,
+                        void *d_dbias, int accumulate) {
+    FG_REQUIRE(ctx, FG_ERR_INVALID_ARGUMENT, "fg_bias_grad: ctx is NULL");
+    FG_REQUIRE(dtype >= FG_DTYPE_F32 && dtype <= FG_DTYPE_BF16, FG_ERR_INVALID_ARGUMENT,
+               "fg_bias_grad: bad dtype %d", dtype);
     FG_REQUIRE(M >= 0 && N >= 0 && ld >= N, FG_ERR_SHAPE,
-               "fg_bias_grad_f32: bad shape M=%d N=%d ld=%d", M, N, ld);
+               "fg_bias_grad: bad shape M=%d N=%d ld=%d", M, N, ld);
     if (N == 0) return FG_OK;
-    FG_REQUIRE(d_dZ && d_dbias, FG_ERR_INVALID_ARGUMENT, "fg_bias_grad_f32: NULL pointer");
+    FG_REQUIRE(d_dZ && d_dbias, FG_ERR_INVALID_ARGUMENT, "fg_bias_grad: NULL pointer");
     FG_HIP(hipSetDevice(ctx->device));
     const int strips = (N + kBgCols - 1) / kBgCols;
     const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
@@ -208,16 +226,33 @@ FG_API int fg_bias_grad_f32(fg_ctx *ctx, int M, int N, const float *d_dZ, int ld
     splits = M > 0 ? (M + rows_per_split - 1) / rows_per_split : 1;
     float *partial = (float *)fg::workspace(ctx, (uint64_t)splits * N * sizeof(float));
     if (!partial) return FG_ERR_OUT_OF_MEMORY;
-    const int vec = ((((uintptr_t)d_dZ) & 15u) == 0) && (ld % 4 == 0);
+    const unsigned align = dtype == FG_DTYPE_F32 ? 16u : 8u;
+    const int vec = ((((uintptr_t)d_dZ) & (align - 1)) == 0) && (ld % 4 == 0);
     if (M > 0) {
-        bias_grad_partial<<<dim3(strips, splits), kThreads, 0, ctx->stream>>>(
-            d_dZ, M, N, ld, rows_per_split, partial, vec);
+        const dim3 grid(strips, splits);
+        if (dtype == FG_DTYPE_F32)
+            bias_grad_partial<fg::kF32><<<grid, kThreads, 0, ctx->stream>>>(d_dZ, M, N, ld,
+                                                                            rows_per_split,
+                                                                            partial, vec);
+        else if (dtype == FG_DTYPE_F16)
+            bias_grad_partial<fg::kF16><<<grid, kThreads, 0, ctx->stream>>>(d_dZ, M, N, ld,
+                                                                            rows_per_split,
+                                                                            partial, vec);
+        else
+            bias_grad_partial<fg::kBF16><<<grid, kThreads, 0, ctx->stream>>>(d_dZ, M, N, ld,
+                                                                             rows_per_split,
+                                                                             partial, vec);
         FG_LAUNCH_CHECK("bias_grad_partial");
     } else {
         splits = 0;
     }
     bias_grad_final<<<(N + kThreads - 1) / kThreads, kThreads, 0, ctx->stream>>>(
-        partial, splits, N, d_dbias, accumulate);
+        partial, splits, N, d_dbias, accumulate, dtype);
     FG_LAUNCH_CHECK("bias_grad_final");
     return FG_OK;
+}
+
+FG_API int fg_bias_grad_f32(fg_ctx *ctx, int M, int N, const float *d_dZ, int ld, float *d_dbias,
+                            int accumulate) {
+    return fg_bias_grad(ctx, FG_DTYPE_F32, M, N, d_dZ, ld, d_dbias, accumulate);
 }

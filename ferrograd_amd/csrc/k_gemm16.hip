@@ -1,0 +1,128 @@
+// k_gemm16.hip -- host dispatch of the 16-bit (bf16 / fp16) MFMA GEMM:
+// argument checks, alignment decisions and the tile-configuration choice.
+// The kernel is in fg_gemm16_kernel.h, instantiated in k_gemm16_{bf16,f16}.hip.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "fg_gemm16_kernel.h"
+#include "fg_internal.h"
+
+namespace {
+
+using fg::gemm16::Args;
+
+int tiles(int M, int N, int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); }
+
+// Tile configuration (indices as in fg_gemm16_kernel.h), from a measured
+// sweep on MI355X over the configurations' shapes (TFLOP/s, bf16):
+//  * NN: 256x128 when it gives >= one tile per CU (506 at 4096^3, 330 at
+//    2048x4096x4096), else 128x128 with >= one tile per CU, else 64x64
+//    (85 for the 1000-wide head, where larger tiles leave CUs idle);
+//  * NT: 256x256 with 8 waves when it fills the chip (783 at 4096^3), else
+//    128x128 (569 at 2048x4096x4096), else 64x64;
+//  * TN: 256x256 with 8 waves when it gives >= half a tile per CU (336-367
+//    for the 4096-wide weight gradients), else 128x128, else 64x64.
+int pick_cfg16(int layout, int M, int N, int cus) {
+    if (layout == FG_NN) {
+        if (tiles(M, N, 256, 128) >= cus) return 4;
+        if (tiles(M, N, 128, 128) >= cus) return 2;
+        return 3;
+    }
+    if (layout == FG_NT) {
+        if (tiles(M, N, 256, 256) >= cus) return 1;
+        if (tiles(M, N, 128, 128) >= cus) return 2;
+        return 3;
+    }
+    if (tiles(M, N, 256, 256) >= cus / 2) return 1;
+    if (tiles(M, N, 128, 128) >= cus) return 2;
+    return 3;
+}
+
+int gemm16_common(fg_ctx *ctx, int dtype, int layout, Args &a, const char *who) {
+    FG_REQUIRE(ctx, FG_ERR_INVALID_ARGUMENT, "%s: ctx is NULL", who);
+    FG_REQUIRE(dtype == FG_DTYPE_F16 || dtype == FG_DTYPE_BF16, FG_ERR_UNSUPPORTED,
+               "%s: dtype %d is not a 16-bit type (use fg_gemm_f32 for fp32)", who, dtype);
+    FG_REQUIRE(layout >= FG_NN && layout <= FG_TN, FG_ERR_INVALID_ARGUMENT, "%s: bad layout %d",
+               who, layout);
+    FG_REQUIRE(a.M >= 0 && a.N >= 0 && a.K >= 0, FG_ERR_SHAPE, "%s: negative dimension", who);
+    FG_REQUIRE(a.act >= 0 && a.act <= 2, FG_ERR_INVALID_ARGUMENT, "%s: bad act %d", who, a.act);
+    if (a.M == 0 || a.N == 0) return FG_OK;
+    FG_REQUIRE(a.A && a.B && a.C, FG_ERR_INVALID_ARGUMENT, "%s: NULL operand", who);
+    const int a_cols = layout == FG_TN ? a.M : a.K;
+    const int b_cols = layout == FG_NT ? a.K : a.N;
+    FG_REQUIRE(a.lda >= std::max(a_cols, 1) && a.ldb >= std::max(b_cols, 1) && a.ldc >= a.N,
+               FG_ERR_SHAPE, "%s: leading dimension too small (lda=%d ldb=%d ldc=%d)", who, a.lda,
+               a.ldb, a.ldc);
+    FG_HIP(hipSetDevice(ctx->device));
+    if (a.K == 0) a.A = a.B;  // loads are all masked; K=0 yields the epilogue of zero
+    // 16-byte operand loads need 16-byte aligned bases and leading
+    // dimensions that keep every row start aligned (multiples of 8
+    // elements); the bounds checks split per 8-element vector, so the
+    // extents themselves are free.
+    auto al = [](const void *q, unsigned m) { return (((uintptr_t)q) & (m - 1)) == 0; };
+    const bool vec = al(a.A, 16) && al(a.B, 16) && a.lda % 8 == 0 && a.ldb % 8 == 0;
+    a.vec_out = al(a.C, 8) && a.ldc % 4 == 0 && (!a.Z || (al(a.Z, 8) && a.ldz % 4 == 0)) &&
+                (!a.bias || al(a.bias, 8));
+#ifdef FG_GEMM16_FORCE_CFG  // tuning builds: one tile configuration for every shape
+    const int cfg = FG_GEMM16_FORCE_CFG;
+#else
+    const int cfg = pick_cfg16(layout, a.M, a.N, ctx->cu_count > 0 ? ctx->cu_count : 256);
+#endif
+    if (dtype == FG_DTYPE_BF16)
+        fg::gemm16::launch_bf16(layout, a, vec, cfg, ctx->stream);
+    else
+        fg::gemm16::launch_f16(layout, a, vec, cfg, ctx->stream);
+    FG_LAUNCH_CHECK(who);
+    return FG_OK;
+}
+
+}  // namespace
+
+FG_API int fg_gemm_x16(fg_ctx *ctx, int dtype, int layout, int M, int N, int K, const void *d_A,
+                       int lda, const void *d_B, int ldb, const void *d_bias, int act, void *d_C,
+                       int ldc, void *d_Z, int ldz, int accumulate) {
+    Args a{};
+    a.A = static_cast<const uint16_t *>(d_A);
+    a.B = static_cast<const uint16_t *>(d_B);
+    a.C = static_cast<uint16_t *>(d_C);
+    a.Z = static_cast<uint16_t *>(d_Z);
+    a.bias = static_cast<const uint16_t *>(d_bias);
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.lda = lda;
+    a.ldb = ldb;
+    a.ldc = ldc;
+    a.ldz = d_Z ? ldz : 0;
+    a.act = act;
+    a.mode = 0;
+    a.accumulate = accumulate ? 1 : 0;
+    FG_REQUIRE(!d_Z || ldz >= N, FG_ERR_SHAPE, "fg_gemm_x16: ldz=%d < N=%d", ldz, N);
+    FG_REQUIRE(!(accumulate && act != FG_ACT_NONE), FG_ERR_INVALID_ARGUMENT,
+               "fg_gemm_x16: accumulate requires act NONE");
+    return gemm16_common(ctx, dtype, layout, a, "fg_gemm_x16");
+}
+
+FG_API int fg_gemm_bwd_x16(fg_ctx *ctx, int dtype, int layout, int M, int N, int K,
+                           const void *d_A, int lda, const void *d_B, int ldb, int act,
+                           const void *d_Zs, int ldzs, void *d_C, int ldc, int accumulate) {
+    Args a{};
+    a.A = static_cast<const uint16_t *>(d_A);
+    a.B = static_cast<const uint16_t *>(d_B);
+    a.C = static_cast<uint16_t *>(d_C);
+    a.Zs = static_cast<const uint16_t *>(d_Zs);
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.lda = lda;
+    a.ldb = ldb;
+    a.ldc = ldc;
+    a.ldzs = ldzs;
+    a.act = act;
+    a.mode = 1;
+    a.accumulate = accumulate ? 1 : 0;
+    FG_REQUIRE(act == FG_ACT_NONE || (d_Zs && ldzs >= N), FG_ERR_INVALID_ARGUMENT,
+               "fg_gemm_bwd_x16: act %d needs Zs with ldzs >= N", act);
+    return gemm16_common(ctx, dtype, layout, a, "fg_gemm_bwd_x16");
+}

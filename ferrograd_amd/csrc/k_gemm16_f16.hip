@@ -1,0 +1,19 @@
+// k_gemm16_f16.hip -- instantiates the 16-bit MFMA GEMM for f16 storage, all
+// three layouts (NN forward, NT dA, TN dB).  One translation unit per type
+// so the two compile in parallel.
+#include "fg_gemm16_kernel.h"
+#include "fg_internal.h"
+
+namespace fg {
+namespace gemm16 {
+
+void launch_f16(int layout, const Args &a, bool vec, int cfg, hipStream_t st) {
+    switch (layout) {
+        case FG_NN: launch_layout<true, true, false>(a, vec, cfg, st); break;
+        case FG_NT: launch_layout<true, false, false>(a, vec, cfg, st); break;
+        default: launch_layout<false, true, false>(a, vec, cfg, st); break;
+    }
+}
+
+}  // namespace gemm16
+}  // namespace fg

@@ -23,6 +23,7 @@
 #include <cmath>
 #include <vector>
 
+#include "fg_half.h"
 #include "fg_internal.h"
 
 namespace {
@@ -31,12 +32,16 @@ constexpr int kThreads = 256;
 constexpr int kUnroll = 4;                               // float4 per thread per stream
 constexpr int kChunk = kThreads * 4 * kUnroll;           // 4096 elements per block
 
+// p and g are of element type dtype (fg_half.h codes; 16-bit tensors are
+// addressed as 16-bit words through the same pointers); m and v are fp32.
 struct MTTensor {
     float *p;
     float *g;
     float *m;
     float *v;
     uint64_t n;
+    uint32_t dtype;
+    uint32_t pad;
 };
 
 struct MTChunk {
@@ -70,12 +75,35 @@ __device__ inline void adam_elem(float &p, float g, float &m, float &v, float b1
     v = vi;
 }
 
+// One chunk of a 16-bit tensor: the update in fp32 (m, v stay fp32), the
+// parameter rounded once to its type; the gradient read as stored.
+__device__ void adam_chunk_h16(const MTTensor &t, uint64_t start, uint64_t end, float b1,
+                               float b2, float eps, float step_size, float inv_sqrt_bc2,
+                               int zero_grad) {
+    uint16_t *p16 = reinterpret_cast<uint16_t *>(t.p);
+    uint16_t *g16 = reinterpret_cast<uint16_t *>(t.g);
+    const float omb1 = 1.0f - b1, omb2 = 1.0f - b2;
+    for (uint64_t i = start + threadIdx.x; i < end; i += kThreads) {
+        float p = fg::h16_to_f(t.dtype, p16[i]), m = t.m[i], v = t.v[i];
+        adam_elem(p, fg::h16_to_f(t.dtype, g16[i]), m, v, b1, omb1, b2, omb2, eps, step_size,
+                  inv_sqrt_bc2);
+        p16[i] = fg::f_to_h16(t.dtype, p);
+        t.m[i] = m;
+        t.v[i] = v;
+        if (zero_grad) g16[i] = 0;
+    }
+}
+
 __global__ __launch_bounds__(kThreads) void adam_mt_kernel(
     const MTTensor *__restrict__ tensors, const MTChunk *__restrict__ chunks, float b1,
     float b2, float eps, float step_size, float inv_sqrt_bc2, int zero_grad, int vec) {
     const MTChunk c = chunks[blockIdx.x];
     const MTTensor t = tensors[c.tensor];
     const uint64_t end = (c.start + kChunk < t.n) ? c.start + kChunk : t.n;
+    if (t.dtype != fg::kF32) {
+        adam_chunk_h16(t, c.start, end, b1, b2, eps, step_size, inv_sqrt_bc2, zero_grad);
+        return;
+    }
     const float omb1 = 1.0f - b1, omb2 = 1.0f - b2;
     if (vec) {
         f32x4 P[kUnroll], G[kUnroll], M[kUnroll], V[kUnroll];
@@ -158,6 +186,10 @@ __global__ __launch_bounds__(kThreads) void adam_mt_dev_kernel(
     const MTChunk c = chunks[blockIdx.x];
     const MTTensor t = tensors[c.tensor];
     const uint64_t end = (c.start + kChunk < t.n) ? c.start + kChunk : t.n;
+    if (t.dtype != fg::kF32) {
+        adam_chunk_h16(t, c.start, end, b1, b2, eps, step_size, inv_sqrt_bc2, zero_grad);
+        return;
+    }
     const float omb1 = 1.0f - b1, omb2 = 1.0f - b2;
     if (vec) {
         f32x4 P[kUnroll], G[kUnroll], M[kUnroll], V[kUnroll];
@@ -219,6 +251,16 @@ __global__ __launch_bounds__(kThreads) void sgd_mt_kernel(const MTTensor *__rest
     const MTChunk c = chunks[blockIdx.x];
     const MTTensor t = tensors[c.tensor];
     const uint64_t end = (c.start + kChunk < t.n) ? c.start + kChunk : t.n;
+    if (t.dtype != fg::kF32) {  // 16-bit: w = round(w - g*lr)
+        uint16_t *w16 = reinterpret_cast<uint16_t *>(t.p);
+        uint16_t *g16 = reinterpret_cast<uint16_t *>(t.g);
+        for (uint64_t i = c.start + threadIdx.x; i < end; i += kThreads) {
+            const float w = fg::h16_to_f(t.dtype, w16[i]), g = fg::h16_to_f(t.dtype, g16[i]);
+            w16[i] = fg::f_to_h16(t.dtype, w - g * lr);
+            if (zero_grad) g16[i] = 0;
+        }
+        return;
+    }
     if (vec) {
         f32x4 W[kUnroll], G[kUnroll];
         uint64_t idx[kUnroll];
@@ -264,9 +306,9 @@ struct fg_mt {
     MTChunk *d_chunks = nullptr;
 };
 
-FG_API int fg_mt_create(fg_ctx *ctx, int n, float *const *d_params, float *const *d_grads,
-                        float *const *d_m, float *const *d_v, const uint64_t *sizes,
-                        fg_mt **out) {
+FG_API int fg_mt_create_x(fg_ctx *ctx, int n, const int *dtypes, void *const *d_params,
+                          void *const *d_grads, float *const *d_m, float *const *d_v,
+                          const uint64_t *sizes, fg_mt **out) {
     FG_REQUIRE(ctx && out && n > 0 && d_params && d_grads && sizes, FG_ERR_INVALID_ARGUMENT,
                "fg_mt_create: NULL argument or empty list");
     FG_REQUIRE((d_m == nullptr) == (d_v == nullptr), FG_ERR_INVALID_ARGUMENT,
@@ -278,10 +320,15 @@ FG_API int fg_mt_create(fg_ctx *ctx, int n, float *const *d_params, float *const
     for (int i = 0; i < n; ++i) {
         FG_REQUIRE(d_params[i] && d_grads[i], FG_ERR_INVALID_ARGUMENT,
                    "fg_mt_create: tensor %d has a NULL param or grad", i);
-        tens[i].p = d_params[i];
-        tens[i].g = d_grads[i];
+        const int dt = dtypes ? dtypes[i] : FG_DTYPE_F32;
+        FG_REQUIRE(dt >= FG_DTYPE_F32 && dt <= FG_DTYPE_BF16, FG_ERR_INVALID_ARGUMENT,
+                   "fg_mt_create: tensor %d has unknown dtype %d", i, dt);
+        tens[i].p = static_cast<float *>(d_params[i]);
+        tens[i].g = static_cast<float *>(d_grads[i]);
         tens[i].m = d_m ? d_m[i] : nullptr;
         tens[i].v = d_v ? d_v[i] : nullptr;
+        tens[i].dtype = (uint32_t)dt;
+        tens[i].pad = 0;
         if (d_m) {
             FG_REQUIRE(d_m[i] && d_v[i], FG_ERR_INVALID_ARGUMENT,
                        "fg_mt_create: tensor %d has a NULL optimiser state", i);
@@ -315,6 +362,13 @@ FG_API int fg_mt_create(fg_ctx *ctx, int n, float *const *d_params, float *const
     }
     *out = mt;
     return FG_OK;
+}
+
+FG_API int fg_mt_create(fg_ctx *ctx, int n, float *const *d_params, float *const *d_grads,
+                        float *const *d_m, float *const *d_v, const uint64_t *sizes,
+                        fg_mt **out) {
+    return fg_mt_create_x(ctx, n, nullptr, reinterpret_cast<void *const *>(d_params),
+                          reinterpret_cast<void *const *>(d_grads), d_m, d_v, sizes, out);
 }
 
 FG_API int fg_mt_destroy(fg_mt *mt) {

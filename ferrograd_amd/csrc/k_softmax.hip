@@ -20,6 +20,7 @@
 
 #include <cmath>
 
+#include "fg_half.h"
 #include "fg_internal.h"
 
 namespace {
@@ -98,16 +99,18 @@ __device__ __forceinline__ void block_ms(float &m, float &s, float *sm, float *s
     __syncthreads();
 }
 
-// Row epilogue shared by both kernels: loss and argmax from thread 0.
-__device__ __forceinline__ void row_outputs(const float *xr, int C, const uint32_t *labels, int r,
-                                            float m, float s, int am, float *row_loss,
+// Row epilogue shared by the kernels: loss and argmax from thread 0.  xr
+// is the row of logits of element type dt.
+__device__ __forceinline__ void row_outputs(const void *xr, int dt, int C, const uint32_t *labels,
+                                            int r, float m, float s, int am, float *row_loss,
                                             uint32_t *argmax) {
     if (threadIdx.x != 0) return;
     if (argmax) argmax[r] = (uint32_t)am;
     if (row_loss) {
         const uint32_t t = labels ? labels[r] : 0u;
         // A label outside [0, C) has no logit; report NaN rather than read.
-        row_loss[r] = (t < (uint32_t)C) ? (m + logf(s)) - xr[t] : __builtin_nanf("");
+        row_loss[r] =
+            (t < (uint32_t)C) ? (m + logf(s)) - fg::load_as_f(xr, dt, t) : __builtin_nanf("");
     }
 }
 
@@ -156,7 +159,7 @@ __global__ __launch_bounds__(kNT) void softmax_rows_v4(const float *__restrict__
         }
     }
     s = block_sum(s, sm);
-    row_outputs(xr, C, labels, r, m, s, am, row_loss, argmax);
+    row_outputs(xr, fg::kF32, C, labels, r, m, s, am, row_loss, argmax);
     if (out) {
         const float inv = 1.0f / s;
         const int t = labels ? (int)labels[r] : -1;
@@ -177,22 +180,23 @@ __global__ __launch_bounds__(kNT) void softmax_rows_v4(const float *__restrict__
     }
 }
 
-// Streaming path for any C and alignment: pass 1 online (max, sum, argmax),
-// pass 2 recomputes exp and writes.
-__global__ __launch_bounds__(kNT) void softmax_rows_stream(const float *__restrict__ x, int ldx,
+// Streaming path for any C, alignment and element type dt (x and out share
+// it): pass 1 online (max, sum, argmax), pass 2 recomputes exp and writes,
+// rounding to dt.
+__global__ __launch_bounds__(kNT) void softmax_rows_stream(const void *__restrict__ x, int ldx,
                                                            const uint32_t *__restrict__ labels,
                                                            int C, float scale,
                                                            float *__restrict__ row_loss,
-                                                           float *__restrict__ out, int ldo,
-                                                           uint32_t *__restrict__ argmax) {
+                                                           void *__restrict__ out, int ldo,
+                                                           uint32_t *__restrict__ argmax, int dt) {
     __shared__ float sm[kWaves], ss[kWaves];
     __shared__ int si[kWaves];
     const int r = blockIdx.x;
-    const float *xr = x + (size_t)r * ldx;
+    const uint64_t xb = (uint64_t)r * ldx;
     float m = -INFINITY, s = 0.0f, am_m = -INFINITY;
     int am = 0x7fffffff;
     for (int c = threadIdx.x; c < C; c += kNT) {
-        const float xv = xr[c];
+        const float xv = fg::load_as_f(x, dt, xb + c);
         if (xv > am_m) {
             am_m = xv;
             am = c;
@@ -201,14 +205,89 @@ __global__ __launch_bounds__(kNT) void softmax_rows_stream(const float *__restri
     }
     block_argmax(am_m, am, sm, si);
     block_ms(m, s, sm, ss);
-    row_outputs(xr, C, labels, r, m, s, am, row_loss, argmax);
+    const size_t esz = dt == fg::kF32 ? 4 : 2;
+    row_outputs(static_cast<const char *>(x) + xb * esz, dt, C, labels, r, m, s, am, row_loss,
+                argmax);
     if (out) {
         const float inv = 1.0f / s;
         const int t = labels ? (int)labels[r] : -1;
-        float *orow = out + (size_t)r * ldo;
+        const uint64_t ob = (uint64_t)r * ldo;
         for (int c = threadIdx.x; c < C; c += kNT) {
-            const float p = expf(xr[c] - m) * inv;
-            orow[c] = scale * (c == t ? p - 1.0f : p);
+            const float p = expf(fg::load_as_f(x, dt, xb + c) - m) * inv;
+            fg::store_from_f(out, dt, ob + c, scale * (c == t ? p - 1.0f : p));
+        }
+    }
+}
+
+// Register-resident path for 16-bit rows (fp16 / bf16, 8-byte aligned,
+// C % 4 == 0): NV groups of 4 elements per thread, read once, written once.
+template <int NV>
+__global__ __launch_bounds__(kNT) void softmax_rows_h4(const uint16_t *__restrict__ x, int ldx,
+                                                       const uint32_t *__restrict__ labels, int C,
+                                                       float scale, float *__restrict__ row_loss,
+                                                       uint16_t *__restrict__ out, int ldo,
+                                                       uint32_t *__restrict__ argmax, int dt) {
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    __shared__ float sm[kWaves];
+    __shared__ int si[kWaves];
+    const int r = blockIdx.x;
+    const uint16_t *xr = x + (size_t)r * ldx;
+    const int C4 = C >> 2;
+    f32x4 v[NV];
+    float m = -INFINITY;
+    int am = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int j = threadIdx.x + i * kNT;
+        if (j < C4) {
+            const u32x2 w = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(xr) + j);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                v[i][e] = fg::h16_to_f(dt, (uint16_t)(w[e >> 1] >> (16 * (e & 1))));
+        } else {
+            v[i] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c0 = 4 * (threadIdx.x + i * kNT);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (v[i][e] > m) {
+                m = v[i][e];
+                am = c0 + e;
+            }
+    }
+    block_argmax(m, am, sm, si);
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[i][e] = expf(v[i][e] - m);
+            s += v[i][e];
+        }
+    }
+    s = block_sum(s, sm);
+    row_outputs(xr, dt, C, labels, r, m, s, am, row_loss, argmax);
+    if (out) {
+        const float inv = 1.0f / s;
+        const int t = labels ? (int)labels[r] : -1;
+        uint16_t *orow = out + (size_t)r * ldo;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int j = threadIdx.x + i * kNT;
+            if (j < C4) {
+                uint16_t d[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float p = v[i][e] * inv;
+                    d[e] = fg::f_to_h16(dt, scale * (4 * j + e == t ? p - 1.0f : p));
+                }
+                const u32x2 w = {(uint32_t)d[0] | ((uint32_t)d[1] << 16),
+                                 (uint32_t)d[2] | ((uint32_t)d[3] << 16)};
+                __builtin_nontemporal_store(w, reinterpret_cast<u32x2 *>(orow) + j);
+            }
         }
     }
 }
@@ -228,62 +307,90 @@ __global__ __launch_bounds__(1024) void mean_kernel(const float *__restrict__ va
     if (threadIdx.x == 0) mean[0] = n > 0 ? (float)(sh[0] / (double)n) : 0.0f;
 }
 
-// dx (=|+=) y * (dy - sum(dy*y)) per row (softmax.rs:448-688, all columns).
-__global__ __launch_bounds__(kNT) void softmax_bwd_rows(const float *__restrict__ y,
-                                                        const float *__restrict__ dy, int C,
-                                                        float *__restrict__ dx, int accumulate) {
+// dx (=|+=) y * (dy - sum(dy*y)) per row (softmax.rs:448-688, all columns);
+// y, dy, dx of element type dt, the result rounded to it once.
+__global__ __launch_bounds__(kNT) void softmax_bwd_rows(const void *__restrict__ y,
+                                                        const void *__restrict__ dy, int C,
+                                                        void *__restrict__ dx, int accumulate,
+                                                        int dt) {
     __shared__ float sm[kWaves];
-    const size_t base = (size_t)blockIdx.x * C;
+    const uint64_t base = (uint64_t)blockIdx.x * C;
     float dot = 0.0f;
-    for (int c = threadIdx.x; c < C; c += kNT) dot += dy[base + c] * y[base + c];
+    for (int c = threadIdx.x; c < C; c += kNT)
+        dot += fg::load_as_f(dy, dt, base + c) * fg::load_as_f(y, dt, base + c);
     dot = block_sum(dot, sm);
     for (int c = threadIdx.x; c < C; c += kNT) {
-        const float g = y[base + c] * (dy[base + c] - dot);
-        dx[base + c] = accumulate ? dx[base + c] + g : g;
+        const float g = fg::load_as_f(y, dt, base + c) * (fg::load_as_f(dy, dt, base + c) - dot);
+        fg::store_from_f(dx, dt, base + c, accumulate ? fg::load_as_f(dx, dt, base + c) + g : g);
     }
 }
 
-int launch_rows(fg_ctx *ctx, const float *x, int ldx, const uint32_t *labels, int R, int C,
-                float scale, float *row_loss, float *out, int ldo, uint32_t *argmax) {
-    const bool aligned = ((((uintptr_t)x) | ((uintptr_t)out)) & 15u) == 0 && (C % 4 == 0) &&
-                         (ldx % 4 == 0) && (!out || ldo % 4 == 0);
+int launch_rows(fg_ctx *ctx, int dt, const void *x, int ldx, const uint32_t *labels, int R, int C,
+                float scale, float *row_loss, void *out, int ldo, uint32_t *argmax) {
+    const unsigned align = dt == fg::kF32 ? 16u : 8u;
+    const bool aligned = ((((uintptr_t)x) | ((uintptr_t)out)) & (align - 1)) == 0 &&
+                         (C % 4 == 0) && (ldx % 4 == 0) && (!out || ldo % 4 == 0);
     const int C4 = C / 4;
     dim3 grid(R), block(kNT);
     hipStream_t st = ctx->stream;
-#define FG_SM_LAUNCH(NV)                                                                    \
-    softmax_rows_v4<NV><<<grid, block, 0, st>>>(x, ldx, labels, C, scale, row_loss, out, ldo, \
-                                                argmax)
-    if (aligned && C4 <= kNT * 1)
-        FG_SM_LAUNCH(1);
-    else if (aligned && C4 <= kNT * 2)
-        FG_SM_LAUNCH(2);
-    else if (aligned && C4 <= kNT * 4)
-        FG_SM_LAUNCH(4);
-    else if (aligned && C4 <= kNT * 8)
-        FG_SM_LAUNCH(8);
-    else if (aligned && C4 <= kNT * 16)
-        FG_SM_LAUNCH(16);
-    else if (aligned && C4 <= kNT * 32)
-        FG_SM_LAUNCH(32);
-    else
-        softmax_rows_stream<<<grid, block, 0, st>>>(x, ldx, labels, C, scale, row_loss, out, ldo,
-                                                    argmax);
+    if (dt == fg::kF32) {
+        const float *xf = static_cast<const float *>(x);
+        float *of = static_cast<float *>(out);
+#define FG_SM_LAUNCH(NV) \
+    softmax_rows_v4<NV><<<grid, block, 0, st>>>(xf, ldx, labels, C, scale, row_loss, of, ldo, argmax)
+        if (aligned && C4 <= kNT * 1)
+            FG_SM_LAUNCH(1);
+        else if (aligned && C4 <= kNT * 2)
+            FG_SM_LAUNCH(2);
+        else if (aligned && C4 <= kNT * 4)
+            FG_SM_LAUNCH(4);
+        else if (aligned && C4 <= kNT * 8)
+            FG_SM_LAUNCH(8);
+        else if (aligned && C4 <= kNT * 16)
+            FG_SM_LAUNCH(16);
+        else if (aligned && C4 <= kNT * 32)
+            FG_SM_LAUNCH(32);
+        else
+            softmax_rows_stream<<<grid, block, 0, st>>>(x, ldx, labels, C, scale, row_loss, out,
+                                                        ldo, argmax, dt);
 #undef FG_SM_LAUNCH
+    } else {
+        const uint16_t *xh = static_cast<const uint16_t *>(x);
+        uint16_t *oh = static_cast<uint16_t *>(out);
+#define FG_SM_LAUNCH(NV)                                                                        \
+    softmax_rows_h4<NV><<<grid, block, 0, st>>>(xh, ldx, labels, C, scale, row_loss, oh, ldo, \
+                                                argmax, dt)
+        if (aligned && C4 <= kNT * 1)
+            FG_SM_LAUNCH(1);
+        else if (aligned && C4 <= kNT * 4)
+            FG_SM_LAUNCH(4);
+        else if (aligned && C4 <= kNT * 16)
+            FG_SM_LAUNCH(16);
+        else if (aligned && C4 <= kNT * 32)
+            FG_SM_LAUNCH(32);
+        else
+            softmax_rows_stream<<<grid, block, 0, st>>>(x, ldx, labels, C, scale, row_loss, out,
+                                                        ldo, argmax, dt);
+#undef FG_SM_LAUNCH
+    }
     FG_LAUNCH_CHECK("softmax_rows");
     return FG_OK;
 }
 
 }  // namespace
 
-FG_API int fg_softmax_ce_f32(fg_ctx *ctx, const float *d_logits, int ldx, const uint32_t *d_labels,
-                             int R, int C, float grad_scale, float *d_row_loss, float *d_mean_loss,
-                             float *d_dlogits, int ldd, uint32_t *d_argmax) {
-    FG_REQUIRE(ctx, FG_ERR_INVALID_ARGUMENT, "fg_softmax_ce_f32: ctx is NULL");
+FG_API int fg_softmax_ce(fg_ctx *ctx, int dtype, const void *d_logits, int ldx,
+                         const uint32_t *d_labels, int R, int C, float grad_scale,
+                         float *d_row_loss, float *d_mean_loss, void *d_dlogits, int ldd,
+                         uint32_t *d_argmax) {
+    FG_REQUIRE(ctx, FG_ERR_INVALID_ARGUMENT, "fg_softmax_ce: ctx is NULL");
+    FG_REQUIRE(dtype >= FG_DTYPE_F32 && dtype <= FG_DTYPE_BF16, FG_ERR_INVALID_ARGUMENT,
+               "fg_softmax_ce: bad dtype %d", dtype);
     FG_REQUIRE(R >= 0 && C > 0 && ldx >= C, FG_ERR_SHAPE,
-               "fg_softmax_ce_f32: bad shape R=%d C=%d ldx=%d", R, C, ldx);
-    FG_REQUIRE(!d_dlogits || ldd >= C, FG_ERR_SHAPE, "fg_softmax_ce_f32: ldd=%d < C=%d", ldd, C);
+               "fg_softmax_ce: bad shape R=%d C=%d ldx=%d", R, C, ldx);
+    FG_REQUIRE(!d_dlogits || ldd >= C, FG_ERR_SHAPE, "fg_softmax_ce: ldd=%d < C=%d", ldd, C);
     FG_REQUIRE(d_logits && d_labels, FG_ERR_INVALID_ARGUMENT,
-               "fg_softmax_ce_f32: logits and labels are required");
+               "fg_softmax_ce: logits and labels are required");
     if (R == 0) return FG_OK;
     FG_HIP(hipSetDevice(ctx->device));
     float *row_loss = d_row_loss;
@@ -291,8 +398,8 @@ FG_API int fg_softmax_ce_f32(fg_ctx *ctx, const float *d_logits, int ldx, const 
         row_loss = (float *)fg::workspace(ctx, (uint64_t)R * sizeof(float));
         if (!row_loss) return FG_ERR_OUT_OF_MEMORY;
     }
-    int rc = launch_rows(ctx, d_logits, ldx, d_labels, R, C, grad_scale, row_loss, d_dlogits, ldd,
-                         d_argmax);
+    int rc = launch_rows(ctx, dtype, d_logits, ldx, d_labels, R, C, grad_scale, row_loss,
+                         d_dlogits, ldd, d_argmax);
     if (rc) return rc;
     if (d_mean_loss) {
         mean_kernel<<<1, 1024, 0, ctx->stream>>>(row_loss, R, d_mean_loss);
@@ -301,22 +408,42 @@ FG_API int fg_softmax_ce_f32(fg_ctx *ctx, const float *d_logits, int ldx, const 
     return FG_OK;
 }
 
-FG_API int fg_softmax_f32(fg_ctx *ctx, const float *d_x, int R, int C, float *d_y) {
-    FG_REQUIRE(ctx && d_x && d_y, FG_ERR_INVALID_ARGUMENT, "fg_softmax_f32: NULL argument");
-    FG_REQUIRE(R >= 0 && C > 0, FG_ERR_SHAPE, "fg_softmax_f32: bad shape R=%d C=%d", R, C);
+FG_API int fg_softmax_ce_f32(fg_ctx *ctx, const float *d_logits, int ldx, const uint32_t *d_labels,
+                             int R, int C, float grad_scale, float *d_row_loss, float *d_mean_loss,
+                             float *d_dlogits, int ldd, uint32_t *d_argmax) {
+    return fg_softmax_ce(ctx, FG_DTYPE_F32, d_logits, ldx, d_labels, R, C, grad_scale, d_row_loss,
+                         d_mean_loss, d_dlogits, ldd, d_argmax);
+}
+
+FG_API int fg_softmax(fg_ctx *ctx, int dtype, const void *d_x, int R, int C, void *d_y) {
+    FG_REQUIRE(ctx && d_x && d_y, FG_ERR_INVALID_ARGUMENT, "fg_softmax: NULL argument");
+    FG_REQUIRE(dtype >= FG_DTYPE_F32 && dtype <= FG_DTYPE_BF16, FG_ERR_INVALID_ARGUMENT,
+               "fg_softmax: bad dtype %d", dtype);
+    FG_REQUIRE(R >= 0 && C > 0, FG_ERR_SHAPE, "fg_softmax: bad shape R=%d C=%d", R, C);
     if (R == 0) return FG_OK;
     FG_HIP(hipSetDevice(ctx->device));
-    return launch_rows(ctx, d_x, C, nullptr, R, C, 1.0f, nullptr, d_y, C, nullptr);
+    return launch_rows(ctx, dtype, d_x, C, nullptr, R, C, 1.0f, nullptr, d_y, C, nullptr);
+}
+
+FG_API int fg_softmax_f32(fg_ctx *ctx, const float *d_x, int R, int C, float *d_y) {
+    return fg_softmax(ctx, FG_DTYPE_F32, d_x, R, C, d_y);
+}
+
+FG_API int fg_softmax_bwd(fg_ctx *ctx, int dtype, const void *d_y, const void *d_dy, int R, int C,
+                          void *d_dx, int accumulate) {
+    FG_REQUIRE(ctx && d_y && d_dy && d_dx, FG_ERR_INVALID_ARGUMENT,
+               "fg_softmax_bwd: NULL argument");
+    FG_REQUIRE(dtype >= FG_DTYPE_F32 && dtype <= FG_DTYPE_BF16, FG_ERR_INVALID_ARGUMENT,
+               "fg_softmax_bwd: bad dtype %d", dtype);
+    FG_REQUIRE(R >= 0 && C > 0, FG_ERR_SHAPE, "fg_softmax_bwd: bad shape R=%d C=%d", R, C);
+    if (R == 0) return FG_OK;
+    FG_HIP(hipSetDevice(ctx->device));
+    softmax_bwd_rows<<<R, kNT, 0, ctx->stream>>>(d_y, d_dy, C, d_dx, accumulate, dtype);
+    FG_LAUNCH_CHECK("softmax_bwd_rows");
+    return FG_OK;
 }
 
 FG_API int fg_softmax_bwd_f32(fg_ctx *ctx, const float *d_y, const float *d_dy, int R, int C,
                               float *d_dx, int accumulate) {
-    FG_REQUIRE(ctx && d_y && d_dy && d_dx, FG_ERR_INVALID_ARGUMENT,
-               "fg_softmax_bwd_f32: NULL argument");
-    FG_REQUIRE(R >= 0 && C > 0, FG_ERR_SHAPE, "fg_softmax_bwd_f32: bad shape R=%d C=%d", R, C);
-    if (R == 0) return FG_OK;
-    FG_HIP(hipSetDevice(ctx->device));
-    softmax_bwd_rows<<<R, kNT, 0, ctx->stream>>>(d_y, d_dy, C, d_dx, accumulate);
-    FG_LAUNCH_CHECK("softmax_bwd_rows");
-    return FG_OK;
+    return fg_softmax_bwd(ctx, FG_DTYPE_F32, d_y, d_dy, R, C, d_dx, accumulate);
 }

@@ -68,7 +68,30 @@ CROSS_ENTROPY = LossType("CROSS_ENTROPY", 2)
 
 
 class SimpleDType:
+    """Element types of tensors (backend/mod.rs:335-427).  F16 tensors are
+    numpy float16 on the host; BF16 tensors are raw 16-bit words (numpy has
+    no bfloat16; see bf16_from_f32 / bf16_to_f32)."""
     F32 = "f32"
+    F16 = "f16"
+    BF16 = "bf16"
+
+
+DTYPE_CODE = {SimpleDType.F32: 0, SimpleDType.F16: 1, SimpleDType.BF16: 2}
+_CODE_NP = {0: np.float32, 1: np.float16, 2: np.uint16}
+
+
+def bf16_from_f32(x) -> np.ndarray:
+    """Round float32 values to bfloat16 words (nearest, ties to even; NaN
+    stays NaN)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + np.uint32(0x7FFF) + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), r)
+
+
+def bf16_to_f32(bits) -> np.ndarray:
+    """Widen bfloat16 words to float32 (exact)."""
+    return (np.ascontiguousarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
 
 
 @dataclass(frozen=True)
@@ -131,6 +154,7 @@ class _Node:
     fields: List[int] = field(default_factory=list)
     value: float = 0.0
     flags: int = 0
+    dtype: int = 0  # DTYPE_CODE of an input / constant
 
 
 class _DefineOps:
@@ -154,13 +178,20 @@ class _DefineOps:
 
     def input(self, shape: Sequence[Field], dtype: str = SimpleDType.F32,
               trainable: bool = True, requires_grad: bool = True) -> int:
-        if dtype != SimpleDType.F32:
-            raise FgError(3, "only f32 inputs are supported on this path")
+        if dtype not in DTYPE_CODE:
+            raise FgError(3, f"element type {dtype!r} is not supported on this path")
         flags = (0 if requires_grad else INPUT_NO_GRAD) | (0 if trainable else INPUT_FROZEN)
-        return self._push(_Node(OP_INPUT, fields=[f.index for f in shape], flags=flags))
+        return self._push(_Node(OP_INPUT, fields=[f.index for f in shape], flags=flags,
+                                dtype=DTYPE_CODE[dtype]))
 
     def constant_f32(self, value: float) -> int:
         return self._push(_Node(OP_CONST, value=float(value)))
+
+    def constant_f16(self, value: float) -> int:
+        return self._push(_Node(OP_CONST, value=float(value), dtype=1))
+
+    def constant_bf16(self, value: float) -> int:
+        return self._push(_Node(OP_CONST, value=float(value), dtype=2))
 
     def _op(self, op: int, *xs: int) -> int:
         return self._push(_Node(op, inputs=list(xs)))
@@ -238,11 +269,11 @@ class Graph:
             for nd in self.nodes:
                 if nd.op == OP_INPUT:
                     arr = (ctypes.c_uint32 * len(nd.fields))(*nd.fields)
-                    call("fg_graph_input", h, arr, len(nd.fields), ctypes.byref(out))
+                    call("fg_graph_input_x", h, arr, len(nd.fields), nd.dtype, ctypes.byref(out))
                     if nd.flags:
                         call("fg_graph_set_input_flags", h, out.value, nd.flags)
                 elif nd.op == OP_CONST:
-                    call("fg_graph_constant_f32", h, nd.value, ctypes.byref(out))
+                    call("fg_graph_constant", h, nd.dtype, nd.value, ctypes.byref(out))
                 else:
                     arr = (ctypes.c_uint32 * len(nd.inputs))(*nd.inputs)
                     call("fg_graph_op", h, nd.op, arr, len(nd.inputs), ctypes.byref(out))
@@ -356,12 +387,19 @@ class Plan:
         call("fg_plan_count", self.handle, role, ctypes.byref(c))
         return c.value
 
-    def tensor(self, role: int, index: int = 0, dtype=np.float32) -> Tensor:
+    def tensor(self, role: int, index: int = 0, dtype=None) -> Tensor:
+        """A role's index-th tensor; its host dtype follows the plan's element
+        type (float32, float16, or uint16 words for bfloat16) unless given
+        (labels are u32: pass np.uint32)."""
         ptr = ctypes.c_void_p()
         nb = ctypes.c_uint64()
         node = ctypes.c_uint32()
         call("fg_plan_tensor", self.handle, role, index, ctypes.byref(ptr), ctypes.byref(nb),
              ctypes.byref(node))
+        if dtype is None:
+            code = ctypes.c_int()
+            call("fg_plan_tensor_dtype", self.handle, role, index, ctypes.byref(code))
+            dtype = _CODE_NP[code.value]
         t = Tensor(ptr.value or 0, nb.value, (nb.value // np.dtype(dtype).itemsize,), dtype,
                    owner=self)
         t.node = node.value
@@ -447,13 +485,34 @@ class GpuContext:
             raise FgError(5, f"init_tensor_f32: {a.size} values for shape {tuple(shape)}")
         return self._alloc(a, shape)
 
+    def init_tensor_f16(self, shape: Sequence[int], data) -> Tensor:
+        """GpuContext::init_tensor_f16 (dispatch/mod.rs:614-628)."""
+        a = np.asarray(data, dtype=np.float16).reshape(-1)
+        if a.size != int(np.prod(shape)):
+            raise FgError(5, f"init_tensor_f16: {a.size} values for shape {tuple(shape)}")
+        return self._alloc(a, shape)
+
+    def init_tensor_bf16(self, shape: Sequence[int], data) -> Tensor:
+        """GpuContext::init_tensor_bf16 (dispatch/mod.rs:630-645): float
+        values are rounded to bfloat16; uint16 arrays are taken as words."""
+        a = np.asarray(data)
+        a = (a.astype(np.uint16) if a.dtype == np.uint16 else bf16_from_f32(a)).reshape(-1)
+        if a.size != int(np.prod(shape)):
+            raise FgError(5, f"init_tensor_bf16: {a.size} values for shape {tuple(shape)}")
+        return self._alloc(a, shape)
+
     def new_onehot_init(self, labels: Sequence[int]) -> Tensor:
         """u32 class labels, one per row (dispatch/mod.rs:647-662)."""
         a = np.asarray(labels, dtype=np.uint32).reshape(-1)
         return self._alloc(a, (a.size,))
 
     def upload(self, t: Tensor, data, offset: int = 0) -> None:
-        a = np.ascontiguousarray(np.asarray(data, dtype=t.dtype).reshape(-1))
+        """Copy host data into t (converted to t's element type; float data
+        for a bfloat16 tensor is rounded to it)."""
+        d = np.asarray(data)
+        if t.dtype == np.uint16 and d.dtype != np.uint16:
+            d = bf16_from_f32(d)
+        a = np.ascontiguousarray(np.asarray(d, dtype=t.dtype).reshape(-1))
         off = int(offset) * t.dtype.itemsize
         if off + a.nbytes > t.nbytes:
             raise FgError(9, f"upload: {a.nbytes} bytes at {off} exceed {t.nbytes}")

@@ -45,7 +45,9 @@ typedef enum fg_status {
     FG_ERR_GRAPH = 6,            /* ErrorKind::ComputeGraphError         */
     FG_ERR_INTERNAL = 7,         /* ErrorKind::InternalError             */
     FG_ERR_NO_DEVICE = 8,        /* ErrorKind::NoDevice                  */
-    FG_ERR_OUT_OF_BOUNDS = 9     /* ErrorKind::OutOfBounds               */
+    FG_ERR_OUT_OF_BOUNDS = 9,    /* ErrorKind::OutOfBounds               */
+    FG_ERR_SERIALIZATION = 10,   /* ErrorKind::SerializationError        */
+    FG_ERR_FILE_NOT_FOUND = 11   /* ErrorKind::FileNotFound              */
 } fg_status;
 
 /* Message of the last failing call on this thread ("" if none).  Replaces
@@ -133,10 +135,37 @@ int fg_gemm_bwd_f32(fg_ctx *ctx, int layout, int M, int N, int K,
                     int act, const float *d_Zs, int ldzs, float *d_C, int ldc,
                     int accumulate);
 
+/* Element types of tensors: SimpleDType F32 / F16 / BF16
+ * (crates/fused_gpu/src/dispatch/backend/mod.rs:335-427). 16-bit tensors are
+ * stored as 16-bit words; kernels compute in fp32 and round to the storage
+ * type (nearest even) wherever a node value is stored. */
+typedef enum fg_dtype { FG_DTYPE_F32 = 0, FG_DTYPE_F16 = 1, FG_DTYPE_BF16 = 2 } fg_dtype;
+
+/* 16-bit GEMMs (dtype FG_DTYPE_F16 or FG_DTYPE_BF16 for every operand and
+ * output): the same contract as fg_gemm_f32 / fg_gemm_bwd_f32, with the
+ * products summed in fp32 on the MFMA units and each node value -- the
+ * matmul, the bias add, the activation, C += -- rounded to the storage
+ * type.  Replaces the 16-bit instances of the matmul lowering
+ * (op/matmul/mod.rs:150-161, generic.rs:13-325), whose running sum is
+ * itself 16-bit. Leading dimensions are in elements. */
+int fg_gemm_x16(fg_ctx *ctx, int dtype, int layout, int M, int N, int K,
+                const void *d_A, int lda, const void *d_B, int ldb,
+                const void *d_bias, int act, void *d_C, int ldc,
+                void *d_Z, int ldz, int accumulate);
+int fg_gemm_bwd_x16(fg_ctx *ctx, int dtype, int layout, int M, int N, int K,
+                    const void *d_A, int lda, const void *d_B, int ldb,
+                    int act, const void *d_Zs, int ldzs, void *d_C, int ldc,
+                    int accumulate);
+
 /* dbias[j] (=|+=) sum_i dZ[i][j]: the bias-add's backward (new broadcast
  * op; reference binary.rs:53-63 has none). Deterministic order. */
 int fg_bias_grad_f32(fg_ctx *ctx, int M, int N, const float *d_dZ, int ld,
                      float *d_dbias, int accumulate);
+
+/* Same reduction over dZ of element type dtype (fp32 sums, the result
+ * rounded to dtype once). */
+int fg_bias_grad(fg_ctx *ctx, int dtype, int M, int N, const void *d_dZ, int ld,
+                 void *d_dbias, int accumulate);
 
 /* dZ[i] = dH[i] * act'(Z[i]) over n elements (unary backward, unary.rs). */
 int fg_act_bwd_f32(fg_ctx *ctx, int act, uint64_t n, const float *d_dH,
@@ -154,11 +183,22 @@ int fg_softmax_ce_f32(fg_ctx *ctx, const float *d_logits, int ldx,
                       float *d_row_loss, float *d_mean_loss, float *d_dlogits,
                       int ldd, uint32_t *d_argmax);
 
+/* Same, with logits and dlogits of element type dtype (FG_DTYPE_*): fp32
+ * arithmetic, dlogits rounded to dtype once; row_loss / mean_loss stay fp32. */
+int fg_softmax_ce(fg_ctx *ctx, int dtype, const void *d_logits, int ldx,
+                  const uint32_t *d_labels, int R, int C, float grad_scale,
+                  float *d_row_loss, float *d_mean_loss, void *d_dlogits, int ldd,
+                  uint32_t *d_argmax);
+
 /* Plain row softmax y = softmax(x) and its backward
  * dx (=|+=) y * (dy - sum(dy*y)) (softmax.rs:112-446, 448-688). */
 int fg_softmax_f32(fg_ctx *ctx, const float *d_x, int R, int C, float *d_y);
 int fg_softmax_bwd_f32(fg_ctx *ctx, const float *d_y, const float *d_dy, int R,
                        int C, float *d_dx, int accumulate);
+/* The same two over tensors of element type dtype (fp32 arithmetic). */
+int fg_softmax(fg_ctx *ctx, int dtype, const void *d_x, int R, int C, void *d_y);
+int fg_softmax_bwd(fg_ctx *ctx, int dtype, const void *d_y, const void *d_dy, int R,
+                   int C, void *d_dx, int accumulate);
 
 /* ----------------------------------------- multi-tensor optimiser lists */
 /* One launch updates every tensor of the list.  Replaces the per-tensor
@@ -171,6 +211,12 @@ typedef struct fg_mt fg_mt;
 int fg_mt_create(fg_ctx *ctx, int n, float *const *d_params,
                  float *const *d_grads, float *const *d_m, float *const *d_v,
                  const uint64_t *sizes, fg_mt **out);
+/* Same, with an element type per tensor (dtypes[i], FG_DTYPE_*; NULL = all
+ * fp32) for its parameter and gradient; m / v stay fp32.  A 16-bit
+ * parameter is updated in fp32 and rounded to its type once per step. */
+int fg_mt_create_x(fg_ctx *ctx, int n, const int *dtypes, void *const *d_params,
+                   void *const *d_grads, float *const *d_m, float *const *d_v,
+                   const uint64_t *sizes, fg_mt **out);
 int fg_mt_destroy(fg_mt *mt);
 /* SGD (basic_optim.rs:3-31): w -= fl(g*lr); g = 0 when zero_grad. */
 int fg_sgd_step(fg_ctx *ctx, fg_mt *mt, float lr, int zero_grad);
@@ -190,6 +236,46 @@ int fg_adam_step_scalars(fg_ctx *ctx, fg_mt *mt, float b1, float b2, float eps,
  * the plan owns, dispatch/mod.rs:161-261). */
 int fg_memcpy_h2d(fg_ctx *ctx, void *d_dst, const void *src, uint64_t bytes);
 int fg_memcpy_d2h(fg_ctx *ctx, void *dst, const void *d_src, uint64_t bytes);
+
+/* ------------------------------------------------------- bpat tensor files */
+/* fused_gpu::io (crates/fused_gpu/src/io/mod.rs:20-196; layouts in
+ * io/headers.rs:1-117): BpatHeader variants in declaration order. */
+typedef enum fg_bpat_header {
+    FG_BPAT_V0 = 0,      /* "bpat":       u64 rank and dims, f64 data            */
+    FG_BPAT_V1 = 1,      /* "BPATv1\0\0": as V0 + CRC-32 per tensor and per file */
+    FG_BPAT_V1M = 2,     /* "BPATv1m\0":  u32 rank and dims, f32 data, CRCs      */
+    FG_BPAT_V2_F16 = 3,  /* "BPAT\0f16":  u32 rank and dims, f16 data            */
+    FG_BPAT_V2_BF16 = 4, /* "BPATbf16":   u32 rank and dims, bf16 data           */
+    FG_BPAT_V2_F32 = 5   /* "BPAT\0f32":  u32 rank and dims, f32 data            */
+} fg_bpat_header;
+
+/* One device tensor to save: d_ptr holds prod(shape) elements of dtype. */
+typedef struct fg_bpat_tensor {
+    const void *d_ptr;
+    int dtype;          /* FG_DTYPE_* */
+    int rank;           /* 0..8 */
+    uint32_t shape[8];
+} fg_bpat_tensor;
+
+/* save_tensors (io/mod.rs:95-123): writes n <= 255 tensors, converting each
+ * to the header's element type (nearest even when narrowing). */
+int fg_bpat_save(fg_ctx *ctx, const char *path, int header, int n,
+                 const fg_bpat_tensor *tensors);
+/* The same from host memory (d_ptr read as a host pointer): for tools and
+ * for writing files without a device. */
+int fg_bpat_save_host(const char *path, int header, int n, const fg_bpat_tensor *tensors);
+/* load_tensors (io/mod.rs:125-160) split in two steps: parse (and verify
+ * the CRCs of V1 / V1M) a file into host memory, then upload any of its
+ * tensors into caller-owned device memory of a chosen element type. */
+typedef struct fg_bpat fg_bpat;
+int fg_bpat_open(const char *path, fg_bpat **out);
+int fg_bpat_close(fg_bpat *f);
+int fg_bpat_info(const fg_bpat *f, int *header, int *count);
+/* shape receives up to 8 dims. */
+int fg_bpat_tensor_info(const fg_bpat *f, int index, int *rank, uint32_t *shape,
+                        uint64_t *numel);
+int fg_bpat_read_f32(const fg_bpat *f, int index, float *dst);
+int fg_bpat_upload(fg_ctx *ctx, const fg_bpat *f, int index, void *d_dst, int dtype);
 
 /* --------------------------------------------------------------- graph */
 /* Graph IR: the mirror of fused_gpu's Graph / Node / GraphOp
@@ -247,8 +333,16 @@ int fg_graph_new_field(fg_graph *g, uint32_t *field);
 /* DefineOps::input(&[fields]) (graph.rs:111): an fp32 input whose dims are
  * meta fields. */
 int fg_graph_input(fg_graph *g, const uint32_t *fields, int rank, uint32_t *node);
+/* DefineOps::input(&[fields], SimpleDType) (graph.rs:111, backend/mod.rs:
+ * 335-427): an input of element type dtype (FG_DTYPE_F32 / F16 / BF16).
+ * Operations take the type of their first input. */
+int fg_graph_input_x(fg_graph *g, const uint32_t *fields, int rank, int dtype,
+                     uint32_t *node);
 /* DefineOps::constant_f32 (graph.rs:106-159): a scalar constant. */
 int fg_graph_constant_f32(fg_graph *g, float value, uint32_t *node);
+/* constant_f16 / constant_bf16 (backend/mod.rs:1293-1310): value rounded to
+ * dtype (nearest, ties to even). */
+int fg_graph_constant(fg_graph *g, int dtype, float value, uint32_t *node);
 /* DefineOps::{add,sub,mul,div,matmul,relu,...,softmax}: node from op and
  * inputs (ids must exist already). */
 int fg_graph_op(fg_graph *g, int op, const uint32_t *inputs, int n_inputs, uint32_t *node);
@@ -289,6 +383,9 @@ int fg_plan_count(const fg_plan *p, int role, int *count);
 /* Device address, byte size and node id of a role's index-th tensor. */
 int fg_plan_tensor(const fg_plan *p, int role, int index, void **d_ptr, uint64_t *bytes,
                    uint32_t *node);
+/* Element type (FG_DTYPE_*) of that tensor: the node's type, except fp32
+ * Adam state, fp32 per-row CE losses and u32 labels (reported as F32). */
+int fg_plan_tensor_dtype(const fg_plan *p, int role, int index, int *dtype);
 /* Bind the index-th input (input order) / the loss target to caller-owned
  * device memory (the reference passes in_tensors and the target to
  * schedule / dispatch_loss, dispatch/mod.rs:664-788).  CE targets are u32
@@ -312,6 +409,14 @@ int fg_plan_single_optim(fg_plan *p, int input_index);
  * fg_plan_launch_step); re-capture after rebinding inputs or target. */
 int fg_plan_capture_step(fg_plan *p);
 int fg_plan_launch_step(fg_plan *p);
+/* Checkpoint of a plan to / from a bpat file (format header as for
+ * fg_bpat_save): every Input in input order, then for Adam the m and v of
+ * each updated input and a one-element tensor holding the step count.
+ * Loading checks the tensor count and sizes and restores all of them into
+ * the plan's bound inputs and state.  (The reference saves only the tensors
+ * a caller passes, io/mod.rs:95-123; optimiser state is new.) */
+int fg_plan_save(fg_plan *p, const char *path, int header);
+int fg_plan_load(fg_plan *p, const char *path);
 /* Human-readable launch list ("forward: gemm NN 64x256x784 bias+relu ...")
  * written to buf (truncated to len); *needed receives the full length. */
 int fg_plan_describe(const fg_plan *p, char *buf, size_t len, size_t *needed);

@@ -20,6 +20,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libfg_oracle.so")
 
 NN, NT, TN = 0, 1, 2
+F32, F16, BF16 = 0, 1, 2
 ACT_NONE, ACT_RELU, ACT_GELU = 0, 1, 2
 
 _lib = None
@@ -68,6 +69,24 @@ def _load():
     lib.fgo_adam_scalars.restype = None
     lib.fgo_adam.argtypes = [c_i64, vp, vp, vp, vp, c_float, c_float, c_float, c_float, c_float]
     lib.fgo_adam.restype = None
+    lib.fgo_f32_to_f16.argtypes = [c_float]
+    lib.fgo_f32_to_f16.restype = ctypes.c_uint16
+    lib.fgo_f16_to_f32.argtypes = [ctypes.c_uint16]
+    lib.fgo_f16_to_f32.restype = c_float
+    lib.fgo_f32_to_bf16.argtypes = [c_float]
+    lib.fgo_f32_to_bf16.restype = ctypes.c_uint16
+    lib.fgo_bf16_to_f32.argtypes = [ctypes.c_uint16]
+    lib.fgo_bf16_to_f32.restype = c_float
+    lib.fgo_to_f32.argtypes = [c_int, c_i64, vp, vp]
+    lib.fgo_to_f32.restype = None
+    lib.fgo_from_f32.argtypes = [c_int, c_i64, vp, vp]
+    lib.fgo_from_f32.restype = None
+    lib.fgo_gemm_x16.argtypes = [c_int, c_int, c_int, c_int, c_int, vp, c_int, vp, c_int, vp,
+                                 c_int, vp, c_int, vp, c_int, c_int]
+    lib.fgo_gemm_x16.restype = None
+    lib.fgo_gemm_bwd_x16.argtypes = [c_int, c_int, c_int, c_int, c_int, vp, c_int, vp, c_int,
+                                     c_int, vp, c_int, vp, c_int, c_int]
+    lib.fgo_gemm_bwd_x16.restype = None
     lib.fgo_num_threads.argtypes = []
     lib.fgo_num_threads.restype = c_int
     lib.fgo_set_num_threads.argtypes = [c_int]
@@ -201,3 +220,61 @@ def adam_(p, g, m, v, b1, b2, eps, step_size, inv_sqrt_bc2) -> None:
         assert a.dtype == np.float32 and a.flags.c_contiguous and a.size == p.size
     _load().fgo_adam(p.size, _p(p), _p(g), _p(m), _p(v), float(b1), float(b2), float(eps),
                      float(step_size), float(inv_sqrt_bc2))
+
+
+# ------------------------------------------------------ 16-bit storage types
+def _u16(a):
+    return np.ascontiguousarray(a, dtype=np.uint16)
+
+
+def to_f32(dtype: int, bits) -> np.ndarray:
+    """Widen 16-bit words (F16 or BF16) to float32."""
+    bits = _u16(bits)
+    out = np.empty(bits.shape, dtype=np.float32)
+    _load().fgo_to_f32(dtype, bits.size, _p(bits), _p(out))
+    return out
+
+
+def from_f32(dtype: int, x) -> np.ndarray:
+    """Round float32 values to 16-bit words (F16 or BF16), nearest even."""
+    x = _c32(x)
+    out = np.empty(x.shape, dtype=np.uint16)
+    _load().fgo_from_f32(dtype, x.size, _p(x), _p(out))
+    return out
+
+
+def _x16_dims(layout, A, B):
+    if layout == NN:
+        (M, K), N = A.shape, B.shape[1]
+    elif layout == NT:
+        (M, K), N = A.shape, B.shape[0]
+    else:
+        (K, M), N = A.shape, B.shape[1]
+    return M, N, K
+
+
+def gemm_x16(dtype: int, layout: int, A, B, bias=None, act: int = ACT_NONE, C=None,
+             want_z: bool = False):
+    """16-bit GEMM (16-bit word arrays in and out): returns C, or (C, Z).
+    With C given, accumulates into a copy of it (act must be NONE)."""
+    A, B = _u16(A), _u16(B)
+    M, N, K = _x16_dims(layout, A, B)
+    acc = C is not None
+    out = _u16(C).copy() if acc else np.zeros((M, N), dtype=np.uint16)
+    Z = np.zeros((M, N), dtype=np.uint16) if want_z else None
+    b = None if bias is None else _u16(bias)
+    _load().fgo_gemm_x16(dtype, layout, M, N, K, _p(A), A.shape[1], _p(B), B.shape[1], _p(b),
+                         act, _p(out), N, _p(Z), N, int(acc))
+    return (out, Z) if want_z else out
+
+
+def gemm_bwd_x16(dtype: int, layout: int, A, B, act: int = ACT_NONE, Zs=None, C=None):
+    """C (=|+=) round(round(op(A).op(B)) * act'(Zs)) on 16-bit words."""
+    A, B = _u16(A), _u16(B)
+    M, N, K = _x16_dims(layout, A, B)
+    acc = C is not None
+    out = _u16(C).copy() if acc else np.zeros((M, N), dtype=np.uint16)
+    zs = None if Zs is None else _u16(Zs)
+    _load().fgo_gemm_bwd_x16(dtype, layout, M, N, K, _p(A), A.shape[1], _p(B), B.shape[1], act,
+                             _p(zs), N, _p(out), N, int(acc))
+    return out

@@ -244,3 +244,147 @@ void fgo_adam(int64_t n, float *p, const float *g, float *m, float *v,
         v[i] = vi;
     }
 }
+
+/* ------------------------------------------------ 16-bit storage types */
+uint16_t fgo_f32_to_f16(float x) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    const uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+    const uint32_t a = u & 0x7fffffffu;
+    if (a >= 0x7f800000u) /* infinity, or NaN (quieted, top payload bits kept) */
+        return (uint16_t)(sign | 0x7c00u | (a > 0x7f800000u ? 0x200u | ((a >> 13) & 0x3ffu) : 0u));
+    if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* >= 65520 rounds to infinity */
+    if (a < 0x38800000u) {                                   /* below 2^-14: subnormal or zero */
+        if (a < 0x33000000u) return sign;                    /* <= 2^-25 rounds to zero */
+        const uint32_t e = a >> 23;
+        const uint32_t m = (a & 0x7fffffu) | 0x800000u;
+        const uint32_t shift = 126u - e; /* value = m * 2^(e-150) = (m >> shift) units of 2^-24 */
+        uint32_t q = m >> shift;
+        const uint32_t rem = m & ((1u << shift) - 1u), half = 1u << (shift - 1u);
+        if (rem > half || (rem == half && (q & 1u))) ++q;
+        return (uint16_t)(sign | q);
+    }
+    const uint32_t e = (a >> 23) - 127u + 15u;
+    const uint32_t m = a & 0x7fffffu;
+    uint32_t q = (e << 10) | (m >> 13);
+    const uint32_t rem = m & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) ++q; /* carry may reach infinity */
+    return (uint16_t)(sign | q);
+}
+
+float fgo_f16_to_f32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    const uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+    uint32_t u;
+    if (e == 0) {
+        float f = ldexpf((float)m, -24); /* exact: m < 2^10 */
+        memcpy(&u, &f, 4);
+        u |= sign;
+    } else if (e == 31) {
+        u = sign | 0x7f800000u | (m << 13);
+    } else {
+        u = sign | ((e - 15u + 127u) << 23) | (m << 13);
+    }
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+uint16_t fgo_f32_to_bf16(float x) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u); /* quiet NaN */
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+float fgo_bf16_to_f32(uint16_t h) {
+    const uint32_t u = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+static inline float to_f(int dt, uint16_t h) {
+    return dt == FGO_BF16 ? fgo_bf16_to_f32(h) : fgo_f16_to_f32(h);
+}
+static inline uint16_t from_f(int dt, float f) {
+    return dt == FGO_BF16 ? fgo_f32_to_bf16(f) : fgo_f32_to_f16(f);
+}
+static inline float rnd(int dt, float f) { return to_f(dt, from_f(dt, f)); }
+
+void fgo_to_f32(int dtype, int64_t n, const uint16_t *src, float *dst) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) dst[i] = to_f(dtype, src[i]);
+}
+
+void fgo_from_f32(int dtype, int64_t n, const float *src, uint16_t *dst) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) dst[i] = from_f(dtype, src[i]);
+}
+
+/* Widen a rows x cols operand with leading dimension ld into a dense array. */
+static float *widen(int dt, int rows, int cols, const uint16_t *src, int ld) {
+    float *d = (float *)malloc((size_t)(rows > 0 ? rows : 1) * (size_t)(cols > 0 ? cols : 1) * 4);
+    if (!d) abort();
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < rows; ++i)
+        for (int j = 0; j < cols; ++j) d[(size_t)i * cols + j] = to_f(dt, src[(size_t)i * ld + j]);
+    return d;
+}
+
+static float *gemm_x16_sum(int dt, int layout, int M, int N, int K, const uint16_t *A, int lda,
+                           const uint16_t *B, int ldb) {
+    const int ar = layout == FGO_TN ? K : M, ac = layout == FGO_TN ? M : K;
+    const int br = layout == FGO_NT ? N : K, bc = layout == FGO_NT ? K : N;
+    float *a = widen(dt, ar, ac, A, lda);
+    float *b = widen(dt, br, bc, B, ldb);
+    float *s = (float *)malloc((size_t)(M > 0 ? M : 1) * (size_t)(N > 0 ? N : 1) * 4);
+    if (!s) abort();
+    fgo_gemm(layout, M, N, K, a, ac, b, bc, s, N);
+    free(a);
+    free(b);
+    return s;
+}
+
+void fgo_gemm_x16(int dtype, int layout, int M, int N, int K,
+                  const uint16_t *A, int lda, const uint16_t *B, int ldb,
+                  const uint16_t *bias, int act, uint16_t *C, int ldc,
+                  uint16_t *Z, int ldz, int accumulate) {
+    float *s = gemm_x16_sum(dtype, layout, M, N, K, A, lda, B, ldb);
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < M; ++i) {
+        for (int j = 0; j < N; ++j) {
+            float v = rnd(dtype, s[(size_t)i * N + j]);
+            if (bias) v = rnd(dtype, v + to_f(dtype, bias[j]));
+            if (Z) Z[(size_t)i * ldz + j] = from_f(dtype, v);
+            float o = act == FGO_ACT_NONE ? v : rnd(dtype, (float)act_d(act, (double)v));
+            if (accumulate) o = o + to_f(dtype, C[(size_t)i * ldc + j]);
+            C[(size_t)i * ldc + j] = from_f(dtype, o);
+        }
+    }
+    free(s);
+}
+
+void fgo_gemm_bwd_x16(int dtype, int layout, int M, int N, int K,
+                      const uint16_t *A, int lda, const uint16_t *B, int ldb,
+                      int act, const uint16_t *Zs, int ldzs, uint16_t *C,
+                      int ldc, int accumulate) {
+    float *s = gemm_x16_sum(dtype, layout, M, N, K, A, lda, B, ldb);
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < M; ++i) {
+        for (int j = 0; j < N; ++j) {
+            float v = rnd(dtype, s[(size_t)i * N + j]);
+            if (act != FGO_ACT_NONE) {
+                const float z = to_f(dtype, Zs[(size_t)i * ldzs + j]);
+                /* ReLU' masks the gradient (0 where z <= 0, as the reference's
+                 * conditional add leaves it); GELU' scales it. */
+                v = act == FGO_ACT_RELU ? (z > 0.0f ? v : 0.0f)
+                                        : rnd(dtype, v * (float)act_grad_d(act, (double)z));
+            }
+            if (accumulate) v = v + to_f(dtype, C[(size_t)i * ldc + j]);
+            C[(size_t)i * ldc + j] = from_f(dtype, v);
+        }
+    }
+    free(s);
+}

@@ -97,6 +97,40 @@ void fgo_adam(int64_t n, float *p, const float *g, float *m, float *v,
               float b1, float b2, float eps, float step_size,
               float inv_sqrt_bc2);
 
+/* ------------------------------------------------ 16-bit storage types */
+/* SimpleDType F16 / BF16 (crates/fused_gpu/src/dispatch/backend/mod.rs:
+ * 335-427; conversions by the `half` crate, version 2, at the reference's
+ * upload / download boundary: dispatch/mod.rs:614-645).  Restated from the
+ * IEEE 754 binary16 definition and the bfloat16 layout (upper 16 bits of a
+ * binary32): round to nearest, ties to even; overflow to infinity; NaN stays
+ * NaN (quiet). */
+enum { FGO_F32 = 0, FGO_F16 = 1, FGO_BF16 = 2 };
+uint16_t fgo_f32_to_f16(float x);
+float fgo_f16_to_f32(uint16_t h);
+uint16_t fgo_f32_to_bf16(float x);
+float fgo_bf16_to_f32(uint16_t h);
+/* Element-wise conversions of n values (dtype FGO_F16 or FGO_BF16). */
+void fgo_to_f32(int dtype, int64_t n, const uint16_t *src, float *dst);
+void fgo_from_f32(int dtype, int64_t n, const float *src, uint16_t *dst);
+
+/* 16-bit GEMM with fp32 accumulation (fgo_gemm on the widened operands);
+ * then each node value is rounded to the storage type, in the order the
+ * reference's nodes produce them: the matmul, the bias add (bias may be
+ * NULL), the activation; with accumulate, C = round(C + value).  Z (may be
+ * NULL) receives the rounded pre-activation.  The reference's own 16-bit
+ * matmul keeps a 16-bit running sum (op/matmul/mod.rs:150-161) -- replaced
+ * by the fp32 sum. */
+void fgo_gemm_x16(int dtype, int layout, int M, int N, int K,
+                  const uint16_t *A, int lda, const uint16_t *B, int ldb,
+                  const uint16_t *bias, int act, uint16_t *C, int ldc,
+                  uint16_t *Z, int ldz, int accumulate);
+/* Backward form: C (=|+=) round(round(sum) * act'(Zs)); the ReLU mask is a
+ * select (+0 where Zs <= 0). */
+void fgo_gemm_bwd_x16(int dtype, int layout, int M, int N, int K,
+                      const uint16_t *A, int lda, const uint16_t *B, int ldb,
+                      int act, const uint16_t *Zs, int ldzs, uint16_t *C,
+                      int ldc, int accumulate);
+
 /* Number of OpenMP threads the oracle uses. */
 int fgo_num_threads(void);
 void fgo_set_num_threads(int n);
