@@ -13,6 +13,7 @@ Also measured in the same run (HIP events on the stream the kernels run on):
   * c3: fused softmax + CE forward/backward over [8192, 32000];
   * c4: multi-tensor Adam over 64 x 4 Mi parameters;
   * c1: the 2-layer MLP step (latency bound: steps/s, launches, us/launch);
+  * the same c2 GEMMs and c5 step with bfloat16 tensors;
 and the CPU restatement (oracle/) timed on the host cores on a bounded
 sample of the same workload (one full c5 step on the same inputs), which
 also gives a parity check of the step's loss and gradients.
@@ -35,6 +36,7 @@ if ROOT not in sys.path:
 METRIC = "MLP train steps/sec on 1 MI355X; GEMM TFLOP/s; softmax/Adam HBM GB/s"
 PEAK_FP32_MFMA_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
+PEAK_BF16_MFMA_TFLOPS = 2500.0
 
 
 def log(msg: str) -> None:
@@ -71,7 +73,7 @@ class MLPStep:
     c1: X ~ U[0,1), 784 -> 256 -> 10, ReLU, SGD lr 0.01, seed 0."""
 
     def __init__(self, ctx, dims, batch, act="gelu", optim="adam", lr=1e-3, seed=4,
-                 x_dist="normal"):
+                 x_dist="normal", dtype="f32"):
         import torch
 
         from ferrograd_amd import graph as G
@@ -84,11 +86,11 @@ class MLPStep:
         fd = [meta.new_field() for _ in dims]
         L = len(dims) - 1
         with graph.define_ops() as ops:
-            h = ops.input([fb, fd[0]], trainable=False)
+            h = ops.input([fb, fd[0]], dtype, trainable=False)
             self.w_nodes, self.b_nodes = [], []
             for l in range(L):
-                W = ops.input([fd[l], fd[l + 1]])
-                b = ops.input([fd[l + 1]])
+                W = ops.input([fd[l], fd[l + 1]], dtype)
+                b = ops.input([fd[l + 1]], dtype)
                 self.w_nodes.append(W)
                 self.b_nodes.append(b)
                 z = ops.bias_add(ops.matmul(h, W), b)
@@ -108,6 +110,11 @@ class MLPStep:
         for l, w in enumerate(self.W):
             bound = math.sqrt(6.0 / dims[l])
             ctx.rng_uniform(seed, 10 + l, -bound, bound, w, w.numel())
+        if dtype != "f32":  # same draws, rounded to the 16-bit type
+            tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+            self.X = self.X.to(tdt)
+            self.W = [w.to(tdt) for w in self.W]
+            self.b = [b.to(tdt) for b in self.b]
         ins = [self.X]
         for w, b in zip(self.W, self.b):
             ins += [w, b]
@@ -261,6 +268,52 @@ def copy_component(reps: int):
     del a, b
     return {"hbm_copy_1gib": {"ms": t, "bytes": nbytes, "gbs": nbytes / t / 1e6,
                               "frac_hbm": nbytes / t / 1e6 / PEAK_HBM_GBS}}
+
+
+def c5_bf16_component(ctx, steps: int = 10):
+    """The c5 step with every tensor in bfloat16 (16-bit MFMA GEMMs, fp32
+    sums and optimiser state): captured steps/s and effective TFLOP/s."""
+    import torch
+
+    dims = [1024] + [4096] * 7 + [1000]
+    tr = MLPStep(ctx, dims, 2048, dtype="bf16")
+    tr.step_eager()
+    tr.capture()
+    tr.step_graph()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        tr.step_graph()
+    torch.cuda.synchronize()
+    ms = 1000.0 * (time.perf_counter() - t0) / steps
+    return {"c5_bf16_step": {"steps_per_s": 1000.0 / ms, "ms_per_step": ms,
+                             "effective_tflops": tr.gemm_flops() / (ms * 1e-3) / 1e12,
+                             "loss": tr.mean_loss(), "steps_timed": steps}}
+
+
+def gemm_bf16_component(ctx, reps: int):
+    """c2-shaped 4096^3 GEMMs in bfloat16: forward (bias + ReLU), dA, dB."""
+    import torch
+
+    import ferrograd_amd as fa
+
+    n = 4096
+    g = torch.Generator(device="cuda").manual_seed(1)
+    A, Bm, dC = (torch.randn((n, n), device="cuda", generator=g).to(torch.bfloat16)
+                 for _ in range(3))
+    bias = (0.1 * torch.randn((n,), device="cuda", generator=g)).to(torch.bfloat16)
+    C, Z, dA, dB = (torch.empty((n, n), device="cuda", dtype=torch.bfloat16) for _ in range(4))
+    bf = fa.DTYPE_BF16
+    flops = 2.0 * n * n * n
+    t_f = event_time_ms(lambda: ctx.gemm_x16(bf, fa.NN, n, n, n, A, n, Bm, n, C, n, bias=bias,
+                                             act=fa.ACT_RELU, Z=Z, ldz=n), reps)
+    t_a = event_time_ms(lambda: ctx.gemm_bwd_x16(bf, fa.NT, n, n, n, dC, n, Bm, n, dA, n,
+                                                 act=fa.ACT_RELU, Zs=Z, ldzs=n), reps)
+    t_b = event_time_ms(lambda: ctx.gemm_x16(bf, fa.TN, n, n, n, A, n, dC, n, dB, n), reps)
+    tf = lambda t: flops / t / 1e9
+    return {"c2_gemm_4096_bf16": {"fwd_tflops": tf(t_f), "dA_tflops": tf(t_a),
+                                  "dB_tflops": tf(t_b), "peak_tflops": PEAK_BF16_MFMA_TFLOPS,
+                                  "fwd_ms": t_f, "dA_ms": t_a, "dB_ms": t_b}}
 
 
 def c1_component(ctx, steps: int = 2000):
@@ -507,6 +560,8 @@ def main() -> int:
         comps.update(softmax_component(ctx, args.reps))
         comps.update(adam_component(ctx, 10))
         comps.update(c1_component(ctx))
+        comps.update(gemm_bf16_component(ctx, args.reps))
+        comps.update(c5_bf16_component(ctx))
         comps.update(copy_component(args.reps))
     log("components: " + json.dumps(comps))
 

@@ -33,6 +33,7 @@ SOURCES = [
     "k_eltwise_prog.hip",
     "fg_graph.cpp",
     "fg_bpat.cpp",
+    "fg_telemetry.cpp",
 ]
 
 # Packed-fp32 VALU instructions are disabled for all device code: some of

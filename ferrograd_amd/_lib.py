@@ -55,6 +55,10 @@ SIGNATURES = {
     "fg_graph_input_x": (i32, [vp, vp, i32, i32, vp]),
     "fg_graph_constant": (i32, [vp, i32, f32, vp]),
     "fg_plan_tensor_dtype": (i32, [vp, i32, i32, vp]),
+    "fg_monitor_start": (i32, [vp, i32, vp]),
+    "fg_monitor_stop": (i32, [vp, vp]),
+    "fg_monitor_sample": (i32, [vp, i32, vp, vp, vp]),
+    "fg_monitor_destroy": (i32, [vp]),
     "fg_plan_save": (i32, [vp, ctypes.c_char_p, i32]),
     "fg_plan_load": (i32, [vp, ctypes.c_char_p]),
     "fg_bpat_save": (i32, [vp, ctypes.c_char_p, i32, i32, vp]),

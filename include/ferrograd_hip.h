@@ -237,6 +237,19 @@ int fg_adam_step_scalars(fg_ctx *ctx, fg_mt *mt, float b1, float b2, float eps,
 int fg_memcpy_h2d(fg_ctx *ctx, void *d_dst, const void *src, uint64_t bytes);
 int fg_memcpy_d2h(fg_ctx *ctx, void *dst, const void *d_src, uint64_t bytes);
 
+/* ------------------------------------------------------------ telemetry */
+/* Device memory monitor: the gpu_telemetry 0.2 GpuMonitor the reference's
+ * example harness uses (crates/ferrograd/examples/matmul_chain3.rs:145-171:
+ * start(interval), stop(), samples of heap usage / budget).  A background
+ * thread samples hipMemGetInfo on the context's device every interval_us
+ * (>= 100): used = total - free, budget = total. */
+typedef struct fg_monitor fg_monitor;
+int fg_monitor_start(fg_ctx *ctx, int interval_us, fg_monitor **out);
+int fg_monitor_stop(fg_monitor *m, int *n_samples);
+int fg_monitor_sample(const fg_monitor *m, int index, double *t_s, uint64_t *used,
+                      uint64_t *budget);
+int fg_monitor_destroy(fg_monitor *m);
+
 /* ------------------------------------------------------- bpat tensor files */
 /* fused_gpu::io (crates/fused_gpu/src/io/mod.rs:20-196; layouts in
  * io/headers.rs:1-117): BpatHeader variants in declaration order. */
