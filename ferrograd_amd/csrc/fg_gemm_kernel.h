@@ -9,12 +9,15 @@
 // lowering inlines around them (kernel/forward.rs:298-464).
 //
 // Design (gfx950, 256 CUs, 64-wide waves, 160 KiB LDS per CU):
-//  * 256 threads = 4 waves per workgroup; each wave owns a (TM*32)x(TN*32)
-//    block of C held in TM*TN 16-register MFMA accumulators (up to 256
-//    registers, which the compiler places in AGPRs).
-//  * K is consumed in BK=16 tiles staged through LDS, double-buffered: the
-//    global loads of tile t+1 are issued before the MFMAs of tile t and
-//    written to the other LDS buffer afterwards -- one barrier per tile.
+//  * 4 or 8 waves per workgroup; each wave owns a (TM*32)x(TN*32) block of
+//    C held in TM*TN 16-register MFMA accumulators (up to 256 registers,
+//    which the compiler places in AGPRs).
+//  * K is consumed in BK-deep tiles (16 or 32) staged through LDS.  Where
+//    whole K tiles and 16-byte alignment allow, gemm_f32_dma moves them
+//    straight from global memory into a three-stage LDS ring (two tiles in
+//    flight, swizzled unpadded layout); otherwise gemm_f32_mfma stages them
+//    through registers into double-buffered LDS (the loads of tile t+1 in
+//    flight during the MFMAs of tile t).  One barrier per tile either way.
 //  * No operand is transposed on its way to LDS.  A k-contiguous operand is
 //    kept [row][k] (row stride BK+4 floats, conflict-free 16-byte reads) and
 //    a row-contiguous one [k][row] (stride rows+4).  The MFMA's k index is
@@ -54,6 +57,15 @@ constexpr int kThreads = 256;
 #endif
 constexpr int kBK = FG_GEMM_BK;
 
+// Direct-to-LDS operand loads (gemm_f32_dma) where the shapes allow; 0
+// keeps every call on the register-staged kernel.  A compile-time knob for
+// measurement builds.
+#ifndef FG_GEMM_DMA
+#define FG_GEMM_DMA 1
+#endif
+constexpr bool kDma = FG_GEMM_DMA != 0;
+
+
 struct GemmArgs {
     const float *A;
     const float *B;
@@ -74,10 +86,12 @@ struct GemmArgs {
 // epilogue).
 template <int BM, int BN, int BK, bool AK, bool BNC, int WTN, int NW>
 struct Lds {
-    static constexpr int a_ld = AK ? (BK + 4) : (BM + 4);
-    static constexpr int a_sz = AK ? BM * a_ld : BK * a_ld;
-    static constexpr int b_ld = BNC ? (BN + 4) : (BK + 4);
-    static constexpr int b_sz = BNC ? BK * b_ld : BN * b_ld;
+    static constexpr bool a_rowk = AK;    // A stored [row][k] (else [k][row])
+    static constexpr bool b_rowk = !BNC;  // B stored [col][k] (else [k][col])
+    static constexpr int a_ld = a_rowk ? (BK + 4) : (BM + 4);
+    static constexpr int a_sz = a_rowk ? BM * a_ld : BK * a_ld;
+    static constexpr int b_ld = b_rowk ? (BK + 4) : (BN + 4);
+    static constexpr int b_sz = b_rowk ? BN * b_ld : BK * b_ld;
     static constexpr int buf = a_sz + b_sz;
     static constexpr int stage_ld = WTN + 4;
     static constexpr int stage = NW * 32 * stage_ld;
@@ -184,6 +198,64 @@ __device__ __forceinline__ float epi_value(const GemmArgs &p, float v, float bv,
     return v;
 }
 
+// Epilogue shared by the GEMM kernels.  Accumulator register r of lane
+// (h, l32) in block (i, j) holds C[r0 + 32i + 8(r/4) + 4h + r%4][c0 + 32j + l32]
+// (r0, c0: the wave's first row and column).  Each wave writes one
+// 32 x WTN slice to its LDS stage (stride WTN+4 floats), then reads it back
+// as float4 rows and applies bias / activation / activation-derivative with
+// 16-byte global accesses.  lds must hold NW * 32 * (WTN + 4) floats and be
+// free (every wave past its last read of the operand tiles).
+template <int TM, int TN, int WTN, int NW>
+__device__ __forceinline__ void store_tile(const GemmArgs &p, const f32x16 (&acc)[TM][TN],
+                                           float *lds, int r0, int c0, int wave, int lane) {
+    constexpr int kStageLd = WTN + 4;
+    const int l32 = lane & 31, h = lane >> 5;
+    float *stage = lds + wave * (32 * kStageLd);
+    constexpr int F4 = WTN / 4;  // float4 per slice row
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                stage[((r >> 2) * 8 + h * 4 + (r & 3)) * kStageLd + j * 32 + l32] = acc[i][j][r];
+        __syncthreads();
+        for (int e = lane; e < 32 * F4; e += 64) {
+            const int rr = e / F4, c4 = (e % F4) * 4;
+            const int row = r0 + i * 32 + rr;
+            const int col = c0 + c4;
+            if (row >= p.M || col >= p.N) continue;
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(stage + rr * kStageLd + c4);
+            float *crow = p.C + (size_t)row * p.ldc;
+            if (p.vec_out && col + 4 <= p.N) {
+                f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+                if (p.mode == 0 && p.bias) bv = *reinterpret_cast<const f32x4 *>(p.bias + col);
+                f32x4 o, z;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    float zt;
+                    o[t] = epi_value(p, v[t], bv[t], row, col + t, &zt);
+                    z[t] = zt;
+                }
+                if (p.mode == 0 && p.Z)
+                    *reinterpret_cast<f32x4 *>(p.Z + (size_t)row * p.ldz + col) = z;
+                if (p.accumulate) o += *reinterpret_cast<const f32x4 *>(crow + col);
+                *reinterpret_cast<f32x4 *>(crow + col) = o;
+            } else {
+                for (int t = 0; t < 4 && col + t < p.N; ++t) {
+                    const float bv = (p.mode == 0 && p.bias) ? p.bias[col + t] : 0.0f;
+                    float z;
+                    float o = epi_value(p, v[t], bv, row, col + t, &z);
+                    if (p.mode == 0 && p.Z) p.Z[(size_t)row * p.ldz + col + t] = z;
+                    if (p.accumulate) o += crow[col + t];
+                    crow[col + t] = o;
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
 template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC, bool VEC>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_mfma(GemmArgs p) {
     constexpr int NT = 64 * WGM * WGN;
@@ -229,41 +301,47 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_mfma(GemmArgs p) {
         }
         const float *As = lds + cur * L::buf;
         const float *Bs = As + L::a_sz;
+        // Group g of the tile (4 consecutive k per lane half): lane half h
+        // feeds k = 16*(g/2) + 8h + 4*(g%2) + s to the s-th MFMA.
+        auto load_frag = [&](int g, f32x4 *a, f32x4 *b) {
+            const int kb = (g >> 1) * 16 + 8 * h + 4 * (g & 1);
 #pragma unroll
-        for (int u = 0; u < BK / 16; ++u) {
+            for (int i = 0; i < TM; ++i) {
+                const int row = wm0 + i * 32 + l32;
+                if constexpr (L::a_rowk) {
+                    a[i] = *reinterpret_cast<const f32x4 *>(As + row * L::a_ld + kb);
+                } else {
 #pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                const int kb = u * 16 + 8 * h + 4 * q;
-                f32x4 a[TM], b[TN];
-#pragma unroll
-                for (int i = 0; i < TM; ++i) {
-                    const int row = wm0 + i * 32 + l32;
-                    if constexpr (AK) {
-                        a[i] = *reinterpret_cast<const f32x4 *>(As + row * L::a_ld + kb);
-                    } else {
-#pragma unroll
-                        for (int s = 0; s < 4; ++s) a[i][s] = As[(kb + s) * L::a_ld + row];
-                    }
+                    for (int s = 0; s < 4; ++s) a[i][s] = As[(kb + s) * L::a_ld + row];
                 }
-#pragma unroll
-                for (int j = 0; j < TN; ++j) {
-                    const int col = wn0 + j * 32 + l32;
-                    if constexpr (BNC) {
-#pragma unroll
-                        for (int s = 0; s < 4; ++s) b[j][s] = Bs[(kb + s) * L::b_ld + col];
-                    } else {
-                        b[j] = *reinterpret_cast<const f32x4 *>(Bs + col * L::b_ld + kb);
-                    }
-                }
-#pragma unroll
-                for (int s = 0; s < 4; ++s)
-#pragma unroll
-                    for (int i = 0; i < TM; ++i)
-#pragma unroll
-                        for (int j = 0; j < TN; ++j)
-                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], b[j][s],
-                                                                             acc[i][j], 0, 0, 0);
             }
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int col = wn0 + j * 32 + l32;
+                if constexpr (!L::b_rowk) {
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) b[j][s] = Bs[(kb + s) * L::b_ld + col];
+                } else {
+                    b[j] = *reinterpret_cast<const f32x4 *>(Bs + col * L::b_ld + kb);
+                }
+            }
+        };
+        auto mfma_group = [&](const f32x4 *a, const f32x4 *b) {
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], b[j][s],
+                                                                         acc[i][j], 0, 0, 0);
+        };
+        constexpr int NG = BK / 8;  // 4-k groups per tile and lane half
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+            f32x4 a[TM], b[TN];
+            load_frag(g, a, b);
+            mfma_group(a, b);
         }
         if (more) {
             float *nxt = lds + (cur ^ 1) * L::buf;
@@ -273,54 +351,180 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_mfma(GemmArgs p) {
         __syncthreads();
     }
 
-    // Epilogue.  Accumulator register r of lane (h, l32) in block (i, j)
-    // holds C[wm0 + 32i + 8(r/4) + 4h + r%4][wn0 + 32j + l32].  Each wave
-    // writes one 32 x WTN slice to its LDS stage, then reads it back as
-    // float4 rows.
-    float *stage = lds + wave * (32 * L::stage_ld);
-    constexpr int F4 = WTN / 4;  // float4 per slice row
+    store_tile<TM, TN, WTN, WGM * WGN>(p, acc, lds, m0 + wm0, n0 + wn0, wave, lane);
+}
+
+// ------------------------------------------------ direct-to-LDS variant
+// The same GEMM with the operand tiles moved from global memory straight
+// into LDS (global_load_lds_dwordx4: each lane's 16 bytes land at the wave's
+// LDS base + 16 * lane), a three-stage LDS ring with the loads of tile t+2
+// in flight while tile t is multiplied (two stages and tile t+1 where three
+// do not fit), and one barrier per tile.  Used when
+// every 16-byte chunk of a tile is either in bounds or belongs only to
+// outputs that are masked: K % BK == 0 and the VEC alignment conditions.
+// Rows (or columns) past the matrix edge are clamped to the last valid one,
+// so every load reads mapped memory; the values they bring only reach
+// masked outputs.
+//
+// LDS layout per stage (no padding -- DMA writes whole 1 KiB runs per wave):
+//  * a k-contiguous operand [rows][BK], 16-byte chunk c of row r stored at
+//    chunk c ^ ((r / (64 / BK)) % (BK / 4)): the 8 rows read together by a
+//    16-byte LDS read then hit distinct banks;
+//  * a row-contiguous operand [BK][R] (R = BM or BN), chunk c of k-row k
+//    stored at chunk c ^ (8 * ((k / 8) % 2)): the two lane halves, which read
+//    k-rows 8 apart, hit opposite halves of the banks.
+template <int BK>
+__device__ __forceinline__ int swz_k(int row) {
+    return (row / (64 / BK)) % (BK / 4);
+}
+__device__ __forceinline__ int swz_r(int k) { return ((k >> 3) & 1) * 8; }
+
+// s_waitcnt with vmcnt <= N and no wait on the other counters.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_dma(GemmArgs p) {
+    constexpr int NW = WGM * WGN;
+    constexpr int WTM = BM / WGM, WTN = BN / WGN;
+    constexpr int TM = WTM / 32, TN = WTN / 32;
+    static_assert(TM >= 1 && TN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "wave tile");
+    static_assert(BK == 16 || BK == 32, "BK 16 or 32");
+    constexpr int kInstA = BM * BK / 4 / 64, kInstB = BN * BK / 4 / 64;  // wave loads per tile
+    static_assert(kInstA % NW == 0 && kInstB % NW == 0, "loads divide among the waves");
+    constexpr int kPerA = kInstA / NW, kPerB = kInstB / NW, kLoads = kPerA + kPerB;
+    constexpr int kASz = BM * BK, kBSz = BN * BK, kStageSz = kASz + kBSz;
+    // Three stages (two tiles in flight) when they fit in the 160 KiB of
+    // LDS, else two.
+    constexpr int kStages = 3 * kStageSz * 4 <= 160 * 1024 ? 3 : 2;
+    constexpr int kAhead = kStages - 1;
+    constexpr int kEpi = NW * 32 * (WTN + 4);
+    constexpr int kLds = (kStages * kStageSz > kEpi) ? kStages * kStageSz : kEpi;
+    __shared__ __attribute__((aligned(16))) float lds[kLds];
+
+    int tile_m, tile_n;
+    tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tile_m, tile_n);
+    const int m0 = tile_m * BM, n0 = tile_n * BN;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int l32 = lane & 31, h = lane >> 5;
+    const int wm0 = (wave / WGN) * WTM, wn0 = (wave % WGN) * WTN;
+
+    f32x16 acc[TM][TN];
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
-                stage[((r >> 2) * 8 + h * 4 + (r & 3)) * L::stage_ld + j * 32 + l32] = acc[i][j][r];
-        __syncthreads();
-        for (int e = lane; e < 32 * F4; e += 64) {
-            const int rr = e / F4, c4 = (e % F4) * 4;
-            const int row = m0 + wm0 + i * 32 + rr;
-            const int col = n0 + wn0 + c4;
-            if (row >= p.M || col >= p.N) continue;
-            const f32x4 v = *reinterpret_cast<const f32x4 *>(stage + rr * L::stage_ld + c4);
-            float *crow = p.C + (size_t)row * p.ldc;
-            if (p.vec_out && col + 4 <= p.N) {
-                f32x4 bv = {0.f, 0.f, 0.f, 0.f};
-                if (p.mode == 0 && p.bias) bv = *reinterpret_cast<const f32x4 *>(p.bias + col);
-                f32x4 o, z;
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    // Source address of this lane's chunk for wave load `li` of an operand:
+    // the chunk's position in the stage fixes (row, physical chunk); the
+    // swizzle gives the logical chunk to fetch.
+    auto src_kc = [&](const float *base, int ld, int r0, int rmax, int k0, int pos) {
+        const int row = pos / (BK / 4), pc = pos % (BK / 4);
+        const int c = pc ^ swz_k<BK>(row);
+        return base + (size_t)min(r0 + row, rmax - 1) * ld + k0 + 4 * c;
+    };
+    auto src_rc = [&](const float *base, int ld, int r0, int rmax, int k0, int pos, int R) {
+        const int k = pos / (R / 4), pc = pos % (R / 4);
+        const int c = pc ^ swz_r(k);
+        return base + (size_t)(k0 + k) * ld + min(r0 + 4 * c, rmax - 4);
+    };
+    auto issue = [&](int kt, int stage) {
+        float *sa = lds + stage * kStageSz;
+        float *sb = sa + kASz;
+        const int k0 = kt * BK;
 #pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    float zt;
-                    o[t] = epi_value(p, v[t], bv[t], row, col + t, &zt);
-                    z[t] = zt;
-                }
-                if (p.mode == 0 && p.Z)
-                    *reinterpret_cast<f32x4 *>(p.Z + (size_t)row * p.ldz + col) = z;
-                if (p.accumulate) o += *reinterpret_cast<const f32x4 *>(crow + col);
-                *reinterpret_cast<f32x4 *>(crow + col) = o;
-            } else {
-                for (int t = 0; t < 4 && col + t < p.N; ++t) {
-                    const float bv = (p.mode == 0 && p.bias) ? p.bias[col + t] : 0.0f;
-                    float z;
-                    float o = epi_value(p, v[t], bv, row, col + t, &z);
-                    if (p.mode == 0 && p.Z) p.Z[(size_t)row * p.ldz + col + t] = z;
-                    if (p.accumulate) o += crow[col + t];
-                    crow[col + t] = o;
+        for (int i = 0; i < kPerA; ++i) {
+            const int li = wave * kPerA + i;
+            const int pos = li * 64 + lane;
+            const float *src = AK ? src_kc(p.A, p.lda, m0, p.M, k0, pos)
+                                  : src_rc(p.A, p.lda, m0, p.M, k0, pos, BM);
+            __builtin_amdgcn_global_load_lds(src, sa + li * 256, 16, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < kPerB; ++i) {
+            const int li = wave * kPerB + i;
+            const int pos = li * 64 + lane;
+            const float *src = BNC ? src_rc(p.B, p.ldb, n0, p.N, k0, pos, BN)
+                                   : src_kc(p.B, p.ldb, n0, p.N, k0, pos);
+            __builtin_amdgcn_global_load_lds(src, sb + li * 256, 16, 0, 0);
+        }
+    };
+
+    const int nk = p.K / BK;
+#pragma unroll
+    for (int t = 0; t < kAhead; ++t)
+        if (t < nk) issue(t, t);
+    for (int kt = 0; kt < nk; ++kt) {
+        // This wave's loads of tile kt are done once at most those of the
+        // tiles after it (kAhead - 1 of them, fewer at the end) are
+        // outstanding; the barrier then publishes every wave's.
+        if (kAhead == 2 && kt + 1 < nk)
+            wait_vmcnt<(kAhead - 1) * kLoads>();
+        else
+            wait_vmcnt<0>();
+        asm volatile("s_barrier" ::: "memory");
+        // Stage (kt + kAhead) % kStages was last read while multiplying
+        // tile kt-1, which every wave finished before the barrier.
+        if (kt + kAhead < nk) issue(kt + kAhead, (kt + kAhead) % kStages);
+        const float *As = lds + (kt % kStages) * kStageSz;
+        const float *Bs = As + kASz;
+#pragma unroll
+        for (int g = 0; g < BK / 8; ++g) {
+            const int kb = (g >> 1) * 16 + 8 * h + 4 * (g & 1);
+            f32x4 a[TM], b[TN];
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                const int row = wm0 + i * 32 + l32;
+                if constexpr (AK) {
+                    const int c = (kb >> 2) ^ swz_k<BK>(row);
+                    a[i] = *reinterpret_cast<const f32x4 *>(As + row * BK + 4 * c);
+                } else {
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) {
+                        const int k = kb + s;
+                        a[i][s] = As[k * BM + ((((row >> 2) ^ swz_r(k)) << 2) | (row & 3))];
+                    }
                 }
             }
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int col = wn0 + j * 32 + l32;
+                if constexpr (BNC) {
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) {
+                        const int k = kb + s;
+                        b[j][s] = Bs[k * BN + ((((col >> 2) ^ swz_r(k)) << 2) | (col & 3))];
+                    }
+                } else {
+                    const int c = (kb >> 2) ^ swz_k<BK>(col);
+                    b[j] = *reinterpret_cast<const f32x4 *>(Bs + col * BK + 4 * c);
+                }
+            }
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], b[j][s],
+                                                                         acc[i][j], 0, 0, 0);
         }
-        __syncthreads();
     }
+    __syncthreads();  // every wave past its last tile read before the stage reuse
+    store_tile<TM, TN, WTN, NW>(p, acc, lds, m0 + wm0, n0 + wn0, wave, lane);
+}
+
+template <int BM, int BN, int WGM, int WGN, int BK, bool AK, bool BNC>
+void launch_dma(const GemmArgs &a0, hipStream_t st) {
+    GemmArgs a = a0;
+    a.tiles_m = (a.M + BM - 1) / BM;
+    a.tiles_n = (a.N + BN - 1) / BN;
+    gemm_f32_dma<BM, BN, BK, WGM, WGN, AK, BNC><<<a.tiles_m * a.tiles_n, 64 * WGM * WGN, 0, st>>>(a);
 }
 
 template <int BM, int BN, int WGM, int WGN, int BK, bool AK, bool BNC, bool VEC>
@@ -340,10 +544,28 @@ void launch_one(const GemmArgs &a0, hipStream_t st) {
 // 64x64 is also the only scalar-load variant, for unaligned operands.
 constexpr int kNumCfgs = 8;
 
+// K depth of a configuration.
+inline int cfg_bk(int cfg) { return (cfg == 3 || cfg == 5) ? 32 : (cfg == 4 ? 16 : kBK); }
+
+// dma: K % cfg_bk(cfg) == 0 and the VEC conditions hold (the host checks):
+// the direct-to-LDS kernel with the same tile shape.
 template <bool AK, bool BNC>
-void launch_layout(const GemmArgs &a, bool vec, int cfg, hipStream_t st) {
+void launch_layout(const GemmArgs &a, bool vec, bool dma, int cfg, hipStream_t st) {
     if (!vec) {
         launch_one<64, 64, 2, 2, 16, AK, BNC, false>(a, st);
+        return;
+    }
+    if (dma) {
+        switch (cfg) {
+            case 0: launch_dma<256, 256, 2, 2, kBK, AK, BNC>(a, st); break;
+            case 1: launch_dma<256, 128, 2, 2, kBK, AK, BNC>(a, st); break;
+            case 2: launch_dma<128, 256, 2, 2, kBK, AK, BNC>(a, st); break;
+            case 3: launch_dma<128, 128, 2, 2, 32, AK, BNC>(a, st); break;
+            case 5: launch_dma<128, 64, 2, 2, 32, AK, BNC>(a, st); break;
+            case 6: launch_dma<256, 256, 2, 4, kBK, AK, BNC>(a, st); break;
+            case 7: launch_dma<256, 128, 4, 2, kBK, AK, BNC>(a, st); break;
+            default: launch_dma<64, 64, 2, 2, 16, AK, BNC>(a, st); break;
+        }
         return;
     }
     switch (cfg) {
@@ -359,9 +581,9 @@ void launch_layout(const GemmArgs &a, bool vec, int cfg, hipStream_t st) {
 }
 
 // Defined in k_gemm_{nn,nt,tn}.hip.
-void launch_nn(const GemmArgs &a, bool vec, int cfg, hipStream_t st);
-void launch_nt(const GemmArgs &a, bool vec, int cfg, hipStream_t st);
-void launch_tn(const GemmArgs &a, bool vec, int cfg, hipStream_t st);
+void launch_nn(const GemmArgs &a, bool vec, bool dma, int cfg, hipStream_t st);
+void launch_nt(const GemmArgs &a, bool vec, bool dma, int cfg, hipStream_t st);
+void launch_tn(const GemmArgs &a, bool vec, bool dma, int cfg, hipStream_t st);
 
 }  // namespace gemm
 }  // namespace fg
