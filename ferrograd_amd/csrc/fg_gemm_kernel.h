@@ -540,12 +540,12 @@ void launch_one(const GemmArgs &a0, hipStream_t st) {
 //   0: 256x256, 4 waves, BK 16      1: 256x128, 4 waves, BK 16
 //   2: 128x256, 4 waves, BK 16      3: 128x128, 4 waves, BK 32
 //   4:  64x64,  4 waves, BK 16      5: 128x64,  4 waves, BK 32
-//   6: 256x256, 8 waves, BK 16      7: 256x128, 8 waves, BK 16
+//   6: 256x256, 8 waves, BK 32      7: 256x128, 8 waves, BK 32
 // 64x64 is also the only scalar-load variant, for unaligned operands.
 constexpr int kNumCfgs = 8;
 
 // K depth of a configuration.
-inline int cfg_bk(int cfg) { return (cfg == 3 || cfg == 5) ? 32 : (cfg == 4 ? 16 : kBK); }
+inline int cfg_bk(int cfg) { return (cfg == 3 || cfg >= 5) ? 32 : (cfg == 4 ? 16 : kBK); }
 
 // dma: K % cfg_bk(cfg) == 0 and the VEC conditions hold (the host checks):
 // the direct-to-LDS kernel with the same tile shape.
@@ -562,8 +562,8 @@ void launch_layout(const GemmArgs &a, bool vec, bool dma, int cfg, hipStream_t s
             case 2: launch_dma<128, 256, 2, 2, kBK, AK, BNC>(a, st); break;
             case 3: launch_dma<128, 128, 2, 2, 32, AK, BNC>(a, st); break;
             case 5: launch_dma<128, 64, 2, 2, 32, AK, BNC>(a, st); break;
-            case 6: launch_dma<256, 256, 2, 4, kBK, AK, BNC>(a, st); break;
-            case 7: launch_dma<256, 128, 4, 2, kBK, AK, BNC>(a, st); break;
+            case 6: launch_dma<256, 256, 2, 4, 32, AK, BNC>(a, st); break;
+            case 7: launch_dma<256, 128, 4, 2, 32, AK, BNC>(a, st); break;
             default: launch_dma<64, 64, 2, 2, 16, AK, BNC>(a, st); break;
         }
         return;
@@ -574,8 +574,8 @@ void launch_layout(const GemmArgs &a, bool vec, bool dma, int cfg, hipStream_t s
         case 2: launch_one<128, 256, 2, 2, kBK, AK, BNC, true>(a, st); break;
         case 3: launch_one<128, 128, 2, 2, 32, AK, BNC, true>(a, st); break;
         case 5: launch_one<128, 64, 2, 2, 32, AK, BNC, true>(a, st); break;
-        case 6: launch_one<256, 256, 2, 4, kBK, AK, BNC, true>(a, st); break;
-        case 7: launch_one<256, 128, 4, 2, kBK, AK, BNC, true>(a, st); break;
+        case 6: launch_one<256, 256, 2, 4, 32, AK, BNC, true>(a, st); break;
+        case 7: launch_one<256, 128, 4, 2, 32, AK, BNC, true>(a, st); break;
         default: launch_one<64, 64, 2, 2, 16, AK, BNC, true>(a, st); break;
     }
 }

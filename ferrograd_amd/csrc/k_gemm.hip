@@ -18,14 +18,19 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // ------------------------------------------------------------ dispatch
 // Tile configuration per call (indices as in fg_gemm_kernel.h), from a
-// measured sweep on MI355X (256 CUs) over the BASELINE shapes:
-//  * NN (forward): 256x128 with 8 waves when it yields >= one tile per CU
-//    (105 TFLOP/s at 2048x4096x4096, 128 at 4096^3); else 128x64.
-//  * NT / TN (dA, dW): 256x256 with 8 waves for large-K squares that fill
-//    the chip (130-133 at 4096^3); 128x128 (BK 32) with >= two tiles per CU
-//    (120 at 2048x4096x4096 and 4096x4096x2048); else 128x64 with >= one
-//    tile per CU (104-108 for the 1024- and 1000-wide layers).
-//  * 64x64 for anything smaller.
+// measured sweep of every configuration on MI355X (256 CUs, direct-to-LDS
+// loads) over the BASELINE shapes, TFLOP/s:
+//  * NN (forward): 256x128 with 8 waves and BK 32 when it yields >= one tile
+//    per CU (111 at 2048x4096x4096, 103 at K = 1024); else 128x64 (95 for
+//    the 1000-wide head); 64x64 for anything smaller.
+//  * NT (dA): 256x256 with 8 waves (BK 32) for large-K squares that fill the
+//    chip (137 at 4096^3); else 256x128 with 8 waves when it gives >= one tile
+//    per CU (119 at 2048x4096x4096, 100 at K = 1000); else 128x128 or 128x64
+//    (106 at 2048x1024x4096).
+//  * TN (dW): 256x256 with 8 waves for K >= 4096 filling the chip (140 at
+//    4096^3); 256x128 with 4 waves and BK 16 at >= two tiles per CU (122 at
+//    4096x4096x2048); else 128x128 (113-115 for the 1024- and 1000-wide
+//    layers); else 128x64.
 int tiles(int M, int N, int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); }
 
 int pick_cfg(int layout, int M, int N, int K, int cus) {
@@ -35,7 +40,12 @@ int pick_cfg(int layout, int M, int N, int K, int cus) {
         return 4;
     }
     if (K >= 4096 && tiles(M, N, 256, 256) >= cus) return 6;
-    if (tiles(M, N, 128, 128) >= 2 * cus) return 3;
+    if (layout == FG_NT) {
+        if (tiles(M, N, 256, 128) >= cus) return 7;
+    } else {
+        if (tiles(M, N, 256, 128) >= 2 * cus) return 1;
+    }
+    if (tiles(M, N, 128, 128) >= cus) return 3;
     if (tiles(M, N, 128, 64) >= cus) return 5;
     return 4;
 }
