@@ -80,6 +80,45 @@ struct GemmArgs {
     int accumulate;
     int tiles_m, tiles_n;
     int vec_out;  // C (and Z / Zs) rows 16-byte aligned: float4 epilogue I/O
+    // TN only: colsum[n] (=|+=) sum_k B[k][n] -- the bias gradient of the
+    // layer whose weight gradient this GEMM computes -- taken from the B
+    // tiles already in LDS by the workgroups of the first tile row.
+    float *colsum;
+    int colsum_accumulate;
+};
+
+// Column sums of the B tiles (TN layout, B row-contiguous [k][n]) for the
+// workgroups of tile row 0: thread t owns column t % BN and k-rows
+// (t / BN) * KPT .. + KPT of each tile; partial sums are combined in a fixed
+// order at the end (deterministic).
+template <int BN, int BK, int NT>
+struct ColSum {
+    static constexpr int G = NT >= BN ? NT / BN : 1;  // k-groups
+    static constexpr int KPT = BK / G;                // k-rows per thread and tile
+    static_assert(NT % BN == 0 && BK % G == 0, "column-sum split");
+    float s = 0.0f;
+    // Bs(k, c): the tile element at k-row k, column c.
+    template <class F>
+    __device__ __forceinline__ void add(F Bs) {
+        const int c = threadIdx.x % BN, g = threadIdx.x / BN;
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) s += Bs(g * KPT + i, c);
+    }
+    // Combines the k-groups through lds (G * BN floats, free) and writes the
+    // sums of the tile's columns.  Called by every thread of the workgroup.
+    __device__ __forceinline__ void finish(const GemmArgs &p, float *lds, int n0) const {
+        const int c = threadIdx.x % BN, g = threadIdx.x / BN;
+        lds[g * BN + c] = s;
+        __syncthreads();
+        if ((int)threadIdx.x < BN && n0 + c < p.N) {
+            float t = 0.0f;
+#pragma unroll
+            for (int k = 0; k < G; ++k) t += lds[k * BN + c];
+            float *dst = p.colsum + n0 + c;
+            *dst = p.colsum_accumulate ? *dst + t : t;
+        }
+        __syncthreads();
+    }
 };
 
 // LDS footprint in floats (NW waves, each staging a 32 x WTN slice in the
@@ -285,6 +324,9 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_mfma(GemmArgs p) {
     TileLoader<BM, BK, AK, VEC, NT> la;
     TileLoader<BN, BK, !BNC, VEC, NT> lb;
     const int nk = (p.K + BK - 1) / BK;
+    constexpr bool kTN = !AK && BNC;
+    ColSum<BN, BK, NT> cs;
+    const bool do_cs = kTN && p.colsum && tile_m == 0;
 
     la.load(p.A, p.lda, m0, p.M, 0, p.K);
     lb.load(p.B, p.ldb, n0, p.N, 0, p.K);
@@ -343,6 +385,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_mfma(GemmArgs p) {
             load_frag(g, a, b);
             mfma_group(a, b);
         }
+        if constexpr (kTN)
+            if (do_cs) cs.add([&](int k, int c) { return Bs[k * L::b_ld + c]; });
         if (more) {
             float *nxt = lds + (cur ^ 1) * L::buf;
             la.store(nxt);
@@ -351,6 +395,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_mfma(GemmArgs p) {
         __syncthreads();
     }
 
+    if constexpr (kTN)
+        if (do_cs) cs.finish(p, lds, n0);
     store_tile<TM, TN, WTN, WGM * WGN>(p, acc, lds, m0 + wm0, n0 + wn0, wave, lane);
 }
 
@@ -456,6 +502,9 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_dma(GemmArgs p) {
     };
 
     const int nk = p.K / BK;
+    constexpr bool kTN = !AK && BNC;
+    ColSum<BN, BK, 64 * NW> cs;
+    const bool do_cs = kTN && p.colsum && tile_m == 0;
 #pragma unroll
     for (int t = 0; t < kAhead; ++t)
         if (t < nk) issue(t, t);
@@ -514,8 +563,15 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_dma(GemmArgs p) {
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], b[j][s],
                                                                          acc[i][j], 0, 0, 0);
         }
+        if constexpr (kTN)
+            if (do_cs)
+                cs.add([&](int k, int c) {
+                    return Bs[k * BN + ((((c >> 2) ^ swz_r(k)) << 2) | (c & 3))];
+                });
     }
     __syncthreads();  // every wave past its last tile read before the stage reuse
+    if constexpr (kTN)
+        if (do_cs) cs.finish(p, lds, n0);
     store_tile<TM, TN, WTN, NW>(p, acc, lds, m0 + wm0, n0 + wn0, wave, lane);
 }
 

@@ -230,6 +230,7 @@ struct Launch {
     int dtype = FG_DTYPE_F32;  // element type of the launch's tensors
     int layout = FG_NN, M = 0, N = 0, K = 0, lda = 0, ldb = 0, ldc = 0, ldz = 0;
     int act = FG_ACT_NONE, accumulate = 0;
+    int accumulate2 = 0;  // TN GEMM with fused bias gradient: accumulate into sExtra
     int sA = kNone, sB = kNone, sC = kNone, sZ = kNone, sBias = kNone, sExtra = kNone;
     fg::EltProgram prog{};
     int src_slot[fg::kEltMaxSrc];
@@ -848,7 +849,11 @@ int lower_backward(fg_plan &P, bool fused, std::vector<Launch> &out) {
             }
             const uint32_t a = g.nodes[G.mm].in[0], b = g.nodes[G.mm].in[1];
             const int M = (int)P.shape[a].rows, K = (int)P.shape[a].cols, N = (int)P.shape[b].cols;
-            if (G.bias_src != kNone && P.needs_grad[G.bias_src]) {
+            // fp32: the bias gradient rides on the dW GEMM (column sums of dZ
+            // from its B tiles) when that GEMM runs.
+            const bool fuse_db = G.bias_src != kNone && P.needs_grad[G.bias_src] &&
+                                 P.needs_grad[b] && P.dtype[G.mm] == FG_DTYPE_F32;
+            if (G.bias_src != kNone && P.needs_grad[G.bias_src] && !fuse_db) {
                 Launch L;
                 L.kind = LK_BIAS_GRAD;
                 L.dtype = P.sdt(gs(pre));
@@ -880,6 +885,12 @@ int lower_backward(fg_plan &P, bool fused, std::vector<Launch> &out) {
                 L.desc = "backward gemm TN " + dims_str(K, N, M) + " -> grad of node " +
                          std::to_string(b);
                 ginit[b] = 1;
+                if (fuse_db) {
+                    L.sExtra = gs(G.bias_src);
+                    L.accumulate2 = ginit[G.bias_src];
+                    ginit[G.bias_src] = 1;
+                    L.desc += " +dbias -> grad of node " + std::to_string(G.bias_src);
+                }
                 out.push_back(L);
             }
             if (P.needs_grad[a]) {  // dA = dZ B^T  (with act' of the layer below fused)
@@ -984,6 +995,7 @@ int check_launch(const fg_plan &P, const Launch &L) {
             chk(L.sC, M * N, "C");
             chk(L.sZ, M * N, "Z");
             chk(L.sBias, N, "bias");
+            chk(L.sExtra, N, "dbias");
             break;
         case LK_BIAS_GRAD:
             chk(L.sA, M * N, "dZ");
@@ -1050,7 +1062,12 @@ int run(fg_plan &P, const std::vector<Launch> &list) {
         int rc = FG_OK;
         switch (L.kind) {
             case LK_GEMM:
-                if (L.dtype == FG_DTYPE_F32)
+                if (L.sExtra != kNone)  // dW with the fused dbias (fp32, TN)
+                    rc = fg_gemm_dw_f32(ctx, L.M, L.N, L.K, (const float *)P.ptr(L.sA), L.lda,
+                                        (const float *)P.ptr(L.sB), L.ldb, (float *)P.ptr(L.sC),
+                                        L.ldc, L.accumulate, (float *)P.ptr(L.sExtra),
+                                        L.accumulate2);
+                else if (L.dtype == FG_DTYPE_F32)
                     rc = fg_gemm_f32(ctx, L.layout, L.M, L.N, L.K, (const float *)P.ptr(L.sA),
                                      L.lda, (const float *)P.ptr(L.sB), L.ldb,
                                      (const float *)P.ptr(L.sBias), L.act, (float *)P.ptr(L.sC),

@@ -223,6 +223,37 @@ FG_API int fg_gemm_bwd_f32(fg_ctx *ctx, int layout, int M, int N, int K, const f
     return gemm_common(ctx, layout, a, "fg_gemm_bwd_f32");
 }
 
+FG_API int fg_gemm_dw_f32(fg_ctx *ctx, int M, int N, int K, const float *d_A, int lda,
+                          const float *d_B, int ldb, float *d_C, int ldc, int accumulate,
+                          float *d_colsum, int colsum_accumulate) {
+    GemmArgs a{};
+    a.A = d_A;
+    a.B = d_B;
+    a.C = d_C;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.lda = lda;
+    a.ldb = ldb;
+    a.ldc = ldc;
+    a.act = FG_ACT_NONE;
+    a.mode = 0;
+    a.accumulate = accumulate ? 1 : 0;
+    a.colsum = d_colsum;
+    a.colsum_accumulate = colsum_accumulate ? 1 : 0;
+    if (d_colsum && (M == 0 || K == 0)) {
+        // No tile runs the column sums: an empty reduction.
+        FG_REQUIRE(ctx, FG_ERR_INVALID_ARGUMENT, "fg_gemm_dw_f32: ctx is NULL");
+        if (N > 0 && !colsum_accumulate) {  // a fill kernel: safe under stream capture
+            const int rc = fg_fill_u32(ctx, d_colsum, 0u, (uint64_t)N);
+            if (rc) return rc;
+        }
+        if (M == 0) return FG_OK;
+        a.colsum = nullptr;
+    }
+    return gemm_common(ctx, FG_TN, a, "fg_gemm_dw_f32");
+}
+
 FG_API int fg_bias_grad(fg_ctx *ctx, int dtype, int M, int N, const void *d_dZ, int ld,
                         void *d_dbias, int accumulate) {
     FG_REQUIRE(ctx, FG_ERR_INVALID_ARGUMENT, "fg_bias_grad: ctx is NULL");

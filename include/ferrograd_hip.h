@@ -157,6 +157,16 @@ int fg_gemm_bwd_x16(fg_ctx *ctx, int dtype, int layout, int M, int N, int K,
                     int act, const void *d_Zs, int ldzs, void *d_C, int ldc,
                     int accumulate);
 
+/* The weight and bias gradients of a Linear layer in one launch:
+ *   C (=|+=) A^T.B        A[K][M] lda, B[K][N] ldb (the TN layout: dW = X^T.dZ)
+ *   colsum[n] (=|+=) sum_k B[k][n]   (dbias = column sums of dZ; may be NULL)
+ * The column sums come from the B tiles the GEMM already stages, so dbias
+ * costs no extra pass over dZ (the reference has no bias broadcast, see
+ * binary.rs:53-63; its dB is matmul/mod.rs:85-94). */
+int fg_gemm_dw_f32(fg_ctx *ctx, int M, int N, int K, const float *d_A, int lda,
+                   const float *d_B, int ldb, float *d_C, int ldc, int accumulate,
+                   float *d_colsum, int colsum_accumulate);
+
 /* dbias[j] (=|+=) sum_i dZ[i][j]: the bias-add's backward (new broadcast
  * op; reference binary.rs:53-63 has none). Deterministic order. */
 int fg_bias_grad_f32(fg_ctx *ctx, int M, int N, const float *d_dZ, int ld,

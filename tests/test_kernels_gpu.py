@@ -192,6 +192,31 @@ def test_bias_grad_parity(gpu_ctx, shape):
     assert normwise_rel(host(out), 2 * ref.astype(np.float64)) < 1e-5
 
 
+@pytest.mark.parametrize("shape", [(256, 4096, 2048), (1024, 4096, 2048), (96, 128, 64),
+                                   (784, 256, 64), (37, 29, 300), (130, 200, 33), (4096, 1000, 2048)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_gemm_dw_fused_bias_grad(gpu_ctx, shape):
+    """dW = A^T.dZ and dbias = column sums of dZ in one launch (TN layout):
+    dW to the GEMM tolerance, dbias to 1e-5 of the float64 column sums, both
+    with and without accumulation.  The shapes cover the direct-to-LDS path
+    (K a multiple of 32) and the register-staged one (K = 300, 33)."""
+    M, N, K = shape  # dW is M x N; the reduction runs over K rows
+    note(f"gemm_dw M={M} N={N} K={K}")
+    rng = np.random.default_rng(M + 3 * N + K)
+    A = rng.standard_normal((K, M)).astype(f32)
+    dZ = rng.standard_normal((K, N)).astype(f32)
+    C, db = empty((M, N)), empty((N,))
+    gpu_ctx.gemm_dw(M, N, K, dev(A), M, dev(dZ), N, C, N, colsum=db)
+    refC = O.gemm(O.TN, A, dZ)
+    refb = O.bias_grad(dZ)
+    assert normwise_rel(host(C), refC) < 1e-5 * math.sqrt(K)
+    assert normwise_rel(host(db), refb) < 1e-5
+    gpu_ctx.gemm_dw(M, N, K, dev(A), M, dev(dZ), N, C, N, accumulate=True, colsum=db,
+                    colsum_accumulate=True)
+    assert normwise_rel(host(C), 2 * refC.astype(np.float64)) < 1e-5 * math.sqrt(K)
+    assert normwise_rel(host(db), 2 * refb.astype(np.float64)) < 1e-5
+
+
 @pytest.mark.parametrize("n", [1, 7, 4096, 1000003])
 def test_act_bwd_parity(gpu_ctx, n):
     note(f"act_bwd n={n}")

@@ -46,12 +46,15 @@ def test_mlp_lowers_to_fused_gemm_launches():
     assert n == 1 and loss[0].startswith("loss softmax+ce 2048x1000")
     n, bwd = section(desc, "backward(ce-fused)")
     kinds = [l.split(" ")[1] + " " + l.split(" ")[2] for l in bwd]
-    # per layer: bias grad, dW (TN), dX (NT, with the lower layer's gelu' fused)
-    assert kinds.count("gemm TN") == 3 and kinds.count("bias_grad 2048x1000") == 1
+    # per layer: dW (TN) with the bias gradient fused, dX (NT, with the lower
+    # layer's gelu' fused); no separate bias-gradient launch
+    assert kinds.count("gemm TN") == 3 and not any("bias_grad" in k for k in kinds)
+    assert sum("+dbias" in l for l in bwd) == 3
     assert sum("gelu'" in l for l in bwd) == 2
     assert sum(l.startswith("backward gemm NT") for l in bwd) == 3  # incl. dX of the data
     assert "eltwise" not in "\n".join(bwd)  # no standalone activation backward
     assert "adam over 6 inputs" in desc      # X is frozen: grads but no update
+    assert "kernels per step: 14 (forward 4, loss 2, backward 6, optim 2)" in desc
 
 
 def test_reference_graph_mul_add_is_one_elementwise_launch():
