@@ -200,6 +200,64 @@ __device__ __forceinline__ float epi16(const Args &p, float v, const uint16_t *b
     return v;
 }
 
+// Epilogue shared by the 16-bit kernels.  Accumulator register r of lane
+// (h, l32) in block (i, j) holds C[r0 + 32i + 8(r/4) + 4h + r%4][c0 + 32j + l32];
+// each wave stages one 32 x WTN slice of fp32 sums in LDS (stride WTN+4)
+// and writes four outputs (8 bytes) per lane.  lds must hold
+// NW * 32 * (WTN + 4) floats and be free.
+template <bool BF, int TM, int TN, int WTN, int NW>
+__device__ __forceinline__ void store_tile16(const Args &p, const f32x16 (&acc)[TM][TN],
+                                             float *lds, int r0, int c0, int wave, int lane) {
+    using E = T16<BF>;
+    constexpr int kStageLd = WTN + 4;
+    const int l32 = lane & 31, h = lane >> 5;
+    float *stage = lds + wave * (32 * kStageLd);
+    constexpr int G4 = WTN / 4;  // groups of 4 columns per slice row
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                stage[((r >> 2) * 8 + h * 4 + (r & 3)) * kStageLd + j * 32 + l32] = acc[i][j][r];
+        __syncthreads();
+        for (int e = lane; e < 32 * G4; e += 64) {
+            const int rr = e / G4, c4 = (e % G4) * 4;
+            const int row = r0 + i * 32 + rr;
+            const int col = c0 + c4;
+            if (row >= p.M || col >= p.N) continue;
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(stage + rr * kStageLd + c4);
+            uint16_t *crow = p.C + (size_t)row * p.ldc;
+            const uint16_t *bias = p.mode == 0 ? p.bias : nullptr;
+            if (p.vec_out && col + 4 <= p.N) {
+                uint16_t o[4], z[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    float zt;
+                    float ot = epi16<BF>(p, v[t], bias, row, col + t, &zt);
+                    z[t] = E::from_f(zt);
+                    if (p.accumulate) ot += E::to_f(crow[col + t]);
+                    o[t] = E::from_f(ot);
+                }
+                if (p.mode == 0 && p.Z)
+                    *reinterpret_cast<u32x2 *>(p.Z + (size_t)row * p.ldz + col) =
+                        u32x2{pack2(z[0], z[1]), pack2(z[2], z[3])};
+                *reinterpret_cast<u32x2 *>(crow + col) =
+                    u32x2{pack2(o[0], o[1]), pack2(o[2], o[3])};
+            } else {
+                for (int t = 0; t < 4 && col + t < p.N; ++t) {
+                    float zt;
+                    float ot = epi16<BF>(p, v[t], bias, row, col + t, &zt);
+                    if (p.mode == 0 && p.Z) p.Z[(size_t)row * p.ldz + col + t] = E::from_f(zt);
+                    if (p.accumulate) ot += E::to_f(crow[col + t]);
+                    crow[col + t] = E::from_f(ot);
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
 template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC, bool VEC, bool BF>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm16_mfma(Args p) {
     using E = T16<BF>;
@@ -274,53 +332,184 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm16_mfma(Args p) {
         __syncthreads();
     }
 
-    // Epilogue.  Accumulator register r of lane (h, l32) in block (i, j)
-    // holds C[wm0 + 32i + 8(r/4) + 4h + r%4][wn0 + 32j + l32].
-    float *stage = reinterpret_cast<float *>(lds) + wave * (32 * kStageLd);
-    constexpr int G4 = WTN / 4;  // groups of 4 columns per slice row
+    store_tile16<BF, TM, TN, WTN, WGM * WGN>(p, acc, reinterpret_cast<float *>(lds), m0 + wm0,
+                                             n0 + wn0, wave, lane);
+}
+
+// ------------------------------------------------ direct-to-LDS variant
+// Tiles move from global memory straight into a three-stage LDS ring
+// (global_load_lds_dwordx4: 16 bytes = 8 elements per lane, landing at the
+// wave's LDS base + 16 * lane), two tiles in flight during the MFMAs of the
+// third, one barrier per tile.  No operand is transposed on its way in:
+//  * a k-contiguous operand sits [rows][BK]; chunk c (8 k) of row r at
+//    c ^ ((r / (128 / BK)) % (BK / 8)), so the rows read together by a
+//    16-byte LDS read hit distinct banks; an MFMA operand is one such read;
+//  * a row-contiguous operand sits [BK][R] as loaded; chunk c of k-row k at
+//    c ^ (4 * (k % 4)).  Its MFMA operand (8 consecutive k of one row) comes
+//    from two ds_read_b64_tr_b16: within each 16-lane group, source lane
+//    4e + q reads the 4 elements at (k0 + e, r0 + 4q .. + 3) and output lane
+//    l receives (k0 + 0..3, r0 + l) -- the layout measured on gfx950 with an
+//    in-bounds probe; the swizzle keeps the group's 4 k-rows on distinct banks.
+// Used when K % BK == 0, leading dimensions are multiples of 8 with 16-byte
+// aligned bases, and each row-contiguous operand's row length is a multiple
+// of 8 (edge chunks are clamped to the last valid one; they reach only
+// masked outputs).
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+
+template <int BK>
+__device__ __forceinline__ int swz16_k(int row) {
+    return (row / (128 / BK)) % (BK / 8);
+}
+__device__ __forceinline__ int swz16_r(int k) { return 4 * (k & 3); }
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt16() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// 8 consecutive k (k0 .. k0+7, k0 a multiple of 8) of row `row` of a
+// row-contiguous [BK][R] tile, as one MFMA operand: two transposing reads.
+template <int R>
+__device__ __forceinline__ u32x4 read_tr(const uint16_t *tile, int k0, int row_base, int lane) {
+    const int i = lane & 15;             // source lane within the 16-lane group
+    const int e = i >> 2, q = i & 3;
+    const int r = row_base + 4 * q;      // first of the 4 elements this lane reads
+    u32x4 out;
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
+    for (int half = 0; half < 2; ++half) {
+        const int k = k0 + 4 * half + e;
+        const int idx = k * R + ((((r >> 3) ^ swz16_r(k)) << 3) | (r & 7));
+        const v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) v4i16 *)(tile + idx));
+        const u32x2 w = __builtin_bit_cast(u32x2, v);
+        out[2 * half] = w[0];
+        out[2 * half + 1] = w[1];
+    }
+    return out;
+}
+
+template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC, bool BF>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm16_dma(Args p) {
+    using E = T16<BF>;
+    constexpr int NW = WGM * WGN;
+    constexpr int WTM = BM / WGM, WTN = BN / WGN;
+    constexpr int TM = WTM / 32, TN = WTN / 32;
+    static_assert(TM >= 1 && TN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "wave tile");
+    static_assert(BK == 32 || BK == 64, "BK 32 or 64");
+    static_assert(BM >= 128 && BN >= 128, "row-contiguous tiles need >= 16 chunks per k-row");
+    constexpr int kInstA = BM * BK / 8 / 64, kInstB = BN * BK / 8 / 64;
+    static_assert(kInstA % NW == 0 && kInstB % NW == 0, "loads divide among the waves");
+    constexpr int kPerA = kInstA / NW, kPerB = kInstB / NW, kLoads = kPerA + kPerB;
+    constexpr int kASz = BM * BK, kBSz = BN * BK, kStageSz = kASz + kBSz;  // elements
+    constexpr int kStages = 3 * kStageSz * 2 <= 160 * 1024 ? 3 : 2;
+    constexpr int kAhead = kStages - 1;
+    constexpr int kEpiBytes = NW * 32 * (WTN + 4) * 4;
+    constexpr int kBytes = (kStages * kStageSz * 2 > kEpiBytes) ? kStages * kStageSz * 2 : kEpiBytes;
+    __shared__ __attribute__((aligned(16))) uint16_t lds[kBytes / 2];
+
+    int tile_m, tile_n;
+    tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tile_m, tile_n);
+    const int m0 = tile_m * BM, n0 = tile_n * BN;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int l32 = lane & 31, h = lane >> 5;
+    const int wm0 = (wave / WGN) * WTM, wn0 = (wave % WGN) * WTN;
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
-                stage[((r >> 2) * 8 + h * 4 + (r & 3)) * kStageLd + j * 32 + l32] = acc[i][j][r];
-        __syncthreads();
-        for (int e = lane; e < 32 * G4; e += 64) {
-            const int rr = e / G4, c4 = (e % G4) * 4;
-            const int row = m0 + wm0 + i * 32 + rr;
-            const int col = n0 + wn0 + c4;
-            if (row >= p.M || col >= p.N) continue;
-            const f32x4 v = *reinterpret_cast<const f32x4 *>(stage + rr * kStageLd + c4);
-            uint16_t *crow = p.C + (size_t)row * p.ldc;
-            const uint16_t *bias = p.mode == 0 ? p.bias : nullptr;
-            if (p.vec_out && col + 4 <= p.N) {
-                uint16_t o[4], z[4];
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    auto src_kc = [&](const uint16_t *base, int ld, int r0, int rmax, int k0, int pos) {
+        const int row = pos / (BK / 8), pc = pos % (BK / 8);
+        const int c = pc ^ swz16_k<BK>(row);
+        return base + (size_t)min(r0 + row, rmax - 1) * ld + k0 + 8 * c;
+    };
+    auto src_rc = [&](const uint16_t *base, int ld, int r0, int rmax, int k0, int pos, int R) {
+        const int k = pos / (R / 8), pc = pos % (R / 8);
+        const int c = pc ^ swz16_r(k);
+        return base + (size_t)(k0 + k) * ld + min(r0 + 8 * c, rmax - 8);
+    };
+    auto issue = [&](int kt, int stage) {
+        uint16_t *sa = lds + stage * kStageSz;
+        uint16_t *sb = sa + kASz;
+        const int k0 = kt * BK;
 #pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    float zt;
-                    float ot = epi16<BF>(p, v[t], bias, row, col + t, &zt);
-                    z[t] = E::from_f(zt);
-                    if (p.accumulate) ot += E::to_f(crow[col + t]);
-                    o[t] = E::from_f(ot);
-                }
-                if (p.mode == 0 && p.Z)
-                    *reinterpret_cast<u32x2 *>(p.Z + (size_t)row * p.ldz + col) =
-                        u32x2{pack2(z[0], z[1]), pack2(z[2], z[3])};
-                *reinterpret_cast<u32x2 *>(crow + col) =
-                    u32x2{pack2(o[0], o[1]), pack2(o[2], o[3])};
-            } else {
-                for (int t = 0; t < 4 && col + t < p.N; ++t) {
-                    float zt;
-                    float ot = epi16<BF>(p, v[t], bias, row, col + t, &zt);
-                    if (p.mode == 0 && p.Z) p.Z[(size_t)row * p.ldz + col + t] = E::from_f(zt);
-                    if (p.accumulate) ot += E::to_f(crow[col + t]);
-                    crow[col + t] = E::from_f(ot);
+        for (int i = 0; i < kPerA; ++i) {
+            const int li = wave * kPerA + i;
+            const int pos = li * 64 + lane;
+            const uint16_t *src = AK ? src_kc(p.A, p.lda, m0, p.M, k0, pos)
+                                     : src_rc(p.A, p.lda, m0, p.M, k0, pos, BM);
+            __builtin_amdgcn_global_load_lds(src, sa + li * 512, 16, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < kPerB; ++i) {
+            const int li = wave * kPerB + i;
+            const int pos = li * 64 + lane;
+            const uint16_t *src = BNC ? src_rc(p.B, p.ldb, n0, p.N, k0, pos, BN)
+                                      : src_kc(p.B, p.ldb, n0, p.N, k0, pos);
+            __builtin_amdgcn_global_load_lds(src, sb + li * 512, 16, 0, 0);
+        }
+    };
+
+    const int nk = p.K / BK;
+#pragma unroll
+    for (int t = 0; t < kAhead; ++t)
+        if (t < nk) issue(t, t);
+    for (int kt = 0; kt < nk; ++kt) {
+        if (kAhead == 2 && kt + 1 < nk)
+            wait_vmcnt16<(kAhead - 1) * kLoads>();
+        else
+            wait_vmcnt16<0>();
+        asm volatile("s_barrier" ::: "memory");
+        if (kt + kAhead < nk) issue(kt + kAhead, (kt + kAhead) % kStages);
+        const uint16_t *As = lds + (kt % kStages) * kStageSz;
+        const uint16_t *Bs = As + kASz;
+#pragma unroll
+        for (int u = 0; u < BK / 16; ++u) {
+            const int kb = u * 16 + 8 * h;  // this lane half's 8 k
+            u32x4 a[TM], b[TN];
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                if constexpr (AK) {
+                    const int row = wm0 + i * 32 + l32;
+                    const int c = (kb >> 3) ^ swz16_k<BK>(row);
+                    a[i] = *reinterpret_cast<const u32x4 *>(As + row * BK + 8 * c);
+                } else {
+                    a[i] = read_tr<BM>(As, kb, wm0 + i * 32 + 16 * ((lane >> 4) & 1), lane);
                 }
             }
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                if constexpr (BNC) {
+                    b[j] = read_tr<BN>(Bs, kb, wn0 + j * 32 + 16 * ((lane >> 4) & 1), lane);
+                } else {
+                    const int col = wn0 + j * 32 + l32;
+                    const int c = (kb >> 3) ^ swz16_k<BK>(col);
+                    b[j] = *reinterpret_cast<const u32x4 *>(Bs + col * BK + 8 * c);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) acc[i][j] = E::mfma(a[i], b[j], acc[i][j]);
         }
-        __syncthreads();
     }
+    __syncthreads();
+    store_tile16<BF, TM, TN, WTN, NW>(p, acc, reinterpret_cast<float *>(lds), m0 + wm0, n0 + wn0,
+                                      wave, lane);
+}
+
+template <int BM, int BN, int WGM, int WGN, int BK, bool AK, bool BNC, bool BF>
+void launch_dma16(const Args &a0, hipStream_t st) {
+    Args a = a0;
+    a.tiles_m = (a.M + BM - 1) / BM;
+    a.tiles_n = (a.N + BN - 1) / BN;
+    gemm16_dma<BM, BN, BK, WGM, WGN, AK, BNC, BF>
+        <<<a.tiles_m * a.tiles_n, 64 * WGM * WGN, 0, st>>>(a);
 }
 
 template <int BM, int BN, int WGM, int WGN, int BK, bool AK, bool BNC, bool VEC, bool BF>
@@ -339,10 +528,23 @@ void launch_one(const Args &a0, hipStream_t st) {
 // 64x64 is also the only element-load variant, for unaligned operands.
 constexpr int kNumCfgs = 6;
 
+// K depth of a configuration.
+inline int cfg_bk16(int cfg) { return cfg == 5 ? 64 : 32; }
+
 template <bool AK, bool BNC, bool BF>
-void launch_layout(const Args &a, bool vec, int cfg, hipStream_t st) {
+void launch_layout(const Args &a, bool vec, bool dma, int cfg, hipStream_t st) {
     if (!vec) {
         launch_one<64, 64, 2, 2, 32, AK, BNC, false, BF>(a, st);
+        return;
+    }
+    if (dma && cfg != 3) {
+        switch (cfg) {
+            case 0: launch_dma16<256, 256, 2, 2, 32, AK, BNC, BF>(a, st); break;
+            case 1: launch_dma16<256, 256, 2, 4, 32, AK, BNC, BF>(a, st); break;
+            case 2: launch_dma16<128, 128, 2, 2, 32, AK, BNC, BF>(a, st); break;
+            case 4: launch_dma16<256, 128, 2, 2, 32, AK, BNC, BF>(a, st); break;
+            default: launch_dma16<256, 256, 2, 2, 64, AK, BNC, BF>(a, st); break;
+        }
         return;
     }
     switch (cfg) {
@@ -356,8 +558,8 @@ void launch_layout(const Args &a, bool vec, int cfg, hipStream_t st) {
 }
 
 // Defined in k_gemm16_{bf16,f16}.hip.  layout: FG_NN / FG_NT / FG_TN.
-void launch_bf16(int layout, const Args &a, bool vec, int cfg, hipStream_t st);
-void launch_f16(int layout, const Args &a, bool vec, int cfg, hipStream_t st);
+void launch_bf16(int layout, const Args &a, bool vec, bool dma, int cfg, hipStream_t st);
+void launch_f16(int layout, const Args &a, bool vec, bool dma, int cfg, hipStream_t st);
 
 }  // namespace gemm16
 }  // namespace fg

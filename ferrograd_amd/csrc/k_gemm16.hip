@@ -12,6 +12,12 @@ namespace {
 
 using fg::gemm16::Args;
 
+// Direct-to-LDS variant on (1) or off (0): a knob for measurement builds.
+#ifndef FG_GEMM16_DMA
+#define FG_GEMM16_DMA 1
+#endif
+constexpr bool kDma16 = FG_GEMM16_DMA != 0;
+
 int tiles(int M, int N, int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); }
 
 // Tile configuration (indices as in fg_gemm16_kernel.h), from a measured
@@ -69,10 +75,15 @@ int gemm16_common(fg_ctx *ctx, int dtype, int layout, Args &a, const char *who) 
 #else
     const int cfg = pick_cfg16(layout, a.M, a.N, ctx->cu_count > 0 ? ctx->cu_count : 256);
 #endif
+    // Direct-to-LDS loads: whole K tiles, 16-byte chunks of 8 elements along
+    // each row-contiguous operand's rows (B of NN / TN, A of TN).
+    const bool rc_ok = (layout == FG_NT || a.N % 8 == 0) && (layout != FG_TN || a.M % 8 == 0);
+    const bool dma = kDma16 && vec && rc_ok && a.K > 0 &&
+                     a.K % fg::gemm16::cfg_bk16(cfg) == 0 && a.M >= 8 && a.N >= 8;
     if (dtype == FG_DTYPE_BF16)
-        fg::gemm16::launch_bf16(layout, a, vec, cfg, ctx->stream);
+        fg::gemm16::launch_bf16(layout, a, vec, dma, cfg, ctx->stream);
     else
-        fg::gemm16::launch_f16(layout, a, vec, cfg, ctx->stream);
+        fg::gemm16::launch_f16(layout, a, vec, dma, cfg, ctx->stream);
     FG_LAUNCH_CHECK(who);
     return FG_OK;
 }
