@@ -337,10 +337,13 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm16_mfma(Args p) {
 }
 
 // ------------------------------------------------ direct-to-LDS variant
-// Tiles move from global memory straight into a three-stage LDS ring
-// (global_load_lds_dwordx4: 16 bytes = 8 elements per lane, landing at the
-// wave's LDS base + 16 * lane), two tiles in flight during the MFMAs of the
-// third, one barrier per tile.  No operand is transposed on its way in:
+// Tiles move from global memory straight into an LDS ring of up to four
+// stages (global_load_lds_dwordx4: 16 bytes = 8 elements per lane, landing
+// at the wave's LDS base + 16 * lane), all but one tile in flight during the
+// MFMAs of the current one, one barrier per tile.  A BK of 32 or 64 is only
+// 1-2 thousand MFMA cycles per SIMD, so the barrier is overlapped: the last
+// k16 step of each tile is multiplied after it, from registers.  No operand
+// is transposed on its way in:
 //  * a k-contiguous operand sits [rows][BK]; chunk c (8 k) of row r at
 //    c ^ ((r / (128 / BK)) % (BK / 8)), so the rows read together by a
 //    16-byte LDS read hit distinct banks; an MFMA operand is one such read;
@@ -402,8 +405,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm16_dma(Args p) {
     static_assert(kInstA % NW == 0 && kInstB % NW == 0, "loads divide among the waves");
     constexpr int kPerA = kInstA / NW, kPerB = kInstB / NW, kLoads = kPerA + kPerB;
     constexpr int kASz = BM * BK, kBSz = BN * BK, kStageSz = kASz + kBSz;  // elements
-    constexpr int kStages = 3 * kStageSz * 2 <= 160 * 1024 ? 3 : 2;
-    constexpr int kAhead = kStages - 1;
+    // Up to four stages, as many as fit in the 160 KiB of LDS.
+    constexpr int kStages = 4 * kStageSz * 2 <= 160 * 1024   ? 4
+                            : 3 * kStageSz * 2 <= 160 * 1024 ? 3
+                                                              : 2;
     constexpr int kEpiBytes = NW * 32 * (WTN + 4) * 4;
     constexpr int kBytes = (kStages * kStageSz * 2 > kEpiBytes) ? kStages * kStageSz * 2 : kEpiBytes;
     __shared__ __attribute__((aligned(16))) uint16_t lds[kBytes / 2];
@@ -456,48 +461,80 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm16_dma(Args p) {
     };
 
     const int nk = p.K / BK;
+    // MFMA operands of k16 step u of a stage: lane half h takes k 8h .. 8h+7.
+    auto frag = [&](const uint16_t *As, const uint16_t *Bs, int u, u32x4 (&a)[TM], u32x4 (&b)[TN]) {
+        const int kb = u * 16 + 8 * h;
 #pragma unroll
-    for (int t = 0; t < kAhead; ++t)
-        if (t < nk) issue(t, t);
-    for (int kt = 0; kt < nk; ++kt) {
-        if (kAhead == 2 && kt + 1 < nk)
-            wait_vmcnt16<(kAhead - 1) * kLoads>();
-        else
+        for (int i = 0; i < TM; ++i) {
+            if constexpr (AK) {
+                const int row = wm0 + i * 32 + l32;
+                const int c = (kb >> 3) ^ swz16_k<BK>(row);
+                a[i] = *reinterpret_cast<const u32x4 *>(As + row * BK + 8 * c);
+            } else {
+                a[i] = read_tr<BM>(As, kb, wm0 + i * 32 + 16 * ((lane >> 4) & 1), lane);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            if constexpr (BNC) {
+                b[j] = read_tr<BN>(Bs, kb, wn0 + j * 32 + 16 * ((lane >> 4) & 1), lane);
+            } else {
+                const int col = wn0 + j * 32 + l32;
+                const int c = (kb >> 3) ^ swz16_k<BK>(col);
+                b[j] = *reinterpret_cast<const u32x4 *>(Bs + col * BK + 8 * c);
+            }
+        }
+    };
+    auto mma = [&](const u32x4 (&a)[TM], const u32x4 (&b)[TN]) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) acc[i][j] = E::mfma(a[i], b[j], acc[i][j]);
+    };
+    constexpr int NU = BK / 16;
+    // Barrier-overlapped loop: the last k16 step of tile kt is read into
+    // registers before the barrier that ends tile kt and multiplied after
+    // it, so the matrix units stay busy across the barrier while the first
+    // operands of tile kt+1 are read.  Past that barrier every wave holds
+    // all of tile kt's operands, so tile kt's stage takes tile kt + kStages:
+    // kStages - 1 tiles are in flight behind the one being multiplied.
+    // At most `n` tiles' loads of this wave may still be outstanding.
+    auto wait_tiles = [&](int n) {
+        if (n <= 0)
             wait_vmcnt16<0>();
-        asm volatile("s_barrier" ::: "memory");
-        if (kt + kAhead < nk) issue(kt + kAhead, (kt + kAhead) % kStages);
+        else if (n == 1)
+            wait_vmcnt16<kLoads>();
+        else if (n == 2)
+            wait_vmcnt16<2 * kLoads>();
+        else
+            wait_vmcnt16<3 * kLoads>();
+    };
+#pragma unroll
+    for (int t = 0; t < kStages; ++t)
+        if (t < nk) issue(t, t);
+    wait_tiles(min(kStages, nk) - 1);
+    asm volatile("s_barrier" ::: "memory");
+    u32x4 la[TM], lb[TN];
+    for (int kt = 0; kt < nk; ++kt) {
         const uint16_t *As = lds + (kt % kStages) * kStageSz;
         const uint16_t *Bs = As + kASz;
+        if (kt >= 1 && kt - 1 + kStages < nk) issue(kt - 1 + kStages, (kt - 1) % kStages);
+        if (kt >= 1) mma(la, lb);
 #pragma unroll
-        for (int u = 0; u < BK / 16; ++u) {
-            const int kb = u * 16 + 8 * h;  // this lane half's 8 k
+        for (int u = 0; u < NU - 1; ++u) {
             u32x4 a[TM], b[TN];
-#pragma unroll
-            for (int i = 0; i < TM; ++i) {
-                if constexpr (AK) {
-                    const int row = wm0 + i * 32 + l32;
-                    const int c = (kb >> 3) ^ swz16_k<BK>(row);
-                    a[i] = *reinterpret_cast<const u32x4 *>(As + row * BK + 8 * c);
-                } else {
-                    a[i] = read_tr<BM>(As, kb, wm0 + i * 32 + 16 * ((lane >> 4) & 1), lane);
-                }
-            }
-#pragma unroll
-            for (int j = 0; j < TN; ++j) {
-                if constexpr (BNC) {
-                    b[j] = read_tr<BN>(Bs, kb, wn0 + j * 32 + 16 * ((lane >> 4) & 1), lane);
-                } else {
-                    const int col = wn0 + j * 32 + l32;
-                    const int c = (kb >> 3) ^ swz16_k<BK>(col);
-                    b[j] = *reinterpret_cast<const u32x4 *>(Bs + col * BK + 8 * c);
-                }
-            }
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int j = 0; j < TN; ++j) acc[i][j] = E::mfma(a[i], b[j], acc[i][j]);
+            frag(As, Bs, u, a, b);
+            mma(a, b);
         }
+        frag(As, Bs, NU - 1, la, lb);
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of tile kt done
+        // Tile kt+1 has landed once only the tiles issued after it remain.
+        wait_tiles(min(kt + kStages - 1, nk - 1) - (kt + 1));
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_barrier" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
     }
+    if (nk > 0) mma(la, lb);
     __syncthreads();
     store_tile16<BF, TM, TN, WTN, NW>(p, acc, reinterpret_cast<float *>(lds), m0 + wm0, n0 + wn0,
                                       wave, lane);
@@ -525,11 +562,13 @@ void launch_one(const Args &a0, hipStream_t st) {
 //   0: 256x256, 4 waves, BK 32     1: 256x256, 8 waves, BK 32
 //   2: 128x128, 4 waves, BK 32     3:  64x64,  4 waves, BK 32
 //   4: 256x128, 4 waves, BK 32     5: 256x256, 4 waves, BK 64
+//   6: 256x256, 8 waves, BK 64     7: 256x128, 4 waves, BK 64
+//   8: 256x128, 8 waves, BK 64
 // 64x64 is also the only element-load variant, for unaligned operands.
-constexpr int kNumCfgs = 6;
+constexpr int kNumCfgs = 9;
 
 // K depth of a configuration.
-inline int cfg_bk16(int cfg) { return cfg == 5 ? 64 : 32; }
+inline int cfg_bk16(int cfg) { return cfg >= 5 ? 64 : 32; }
 
 template <bool AK, bool BNC, bool BF>
 void launch_layout(const Args &a, bool vec, bool dma, int cfg, hipStream_t st) {
@@ -543,7 +582,10 @@ void launch_layout(const Args &a, bool vec, bool dma, int cfg, hipStream_t st) {
             case 1: launch_dma16<256, 256, 2, 4, 32, AK, BNC, BF>(a, st); break;
             case 2: launch_dma16<128, 128, 2, 2, 32, AK, BNC, BF>(a, st); break;
             case 4: launch_dma16<256, 128, 2, 2, 32, AK, BNC, BF>(a, st); break;
-            default: launch_dma16<256, 256, 2, 2, 64, AK, BNC, BF>(a, st); break;
+            case 5: launch_dma16<256, 256, 2, 2, 64, AK, BNC, BF>(a, st); break;
+            case 6: launch_dma16<256, 256, 2, 4, 64, AK, BNC, BF>(a, st); break;
+            case 7: launch_dma16<256, 128, 2, 2, 64, AK, BNC, BF>(a, st); break;
+            default: launch_dma16<256, 128, 4, 2, 64, AK, BNC, BF>(a, st); break;
         }
         return;
     }
@@ -553,6 +595,9 @@ void launch_layout(const Args &a, bool vec, bool dma, int cfg, hipStream_t st) {
         case 2: launch_one<128, 128, 2, 2, 32, AK, BNC, true, BF>(a, st); break;
         case 4: launch_one<256, 128, 2, 2, 32, AK, BNC, true, BF>(a, st); break;
         case 5: launch_one<256, 256, 2, 2, 64, AK, BNC, true, BF>(a, st); break;
+        case 6: launch_one<256, 256, 2, 4, 64, AK, BNC, true, BF>(a, st); break;
+        case 7: launch_one<256, 128, 2, 2, 64, AK, BNC, true, BF>(a, st); break;
+        case 8: launch_one<256, 128, 4, 2, 64, AK, BNC, true, BF>(a, st); break;
         default: launch_one<64, 64, 2, 2, 32, AK, BNC, true, BF>(a, st); break;
     }
 }

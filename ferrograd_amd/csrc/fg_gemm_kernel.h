@@ -505,6 +505,60 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_dma(GemmArgs p) {
     constexpr bool kTN = !AK && BNC;
     ColSum<BN, BK, 64 * NW> cs;
     const bool do_cs = kTN && p.colsum && tile_m == 0;
+
+    // Fragments of 4-k group g (of BK / 8) of a stage: lane half h holds k
+    // 8h .. 8h+3 of the group's 16-k block, so the 4 MFMA steps of the
+    // group cover all 16 k across both halves.
+    auto frag = [&](const float *As, const float *Bs, int g, f32x4 (&a)[TM], f32x4 (&b)[TN]) {
+        const int kb = (g >> 1) * 16 + 8 * h + 4 * (g & 1);
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const int row = wm0 + i * 32 + l32;
+            if constexpr (AK) {
+                const int c = (kb >> 2) ^ swz_k<BK>(row);
+                a[i] = *reinterpret_cast<const f32x4 *>(As + row * BK + 4 * c);
+            } else {
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const int k = kb + s;
+                    a[i][s] = As[k * BM + ((((row >> 2) ^ swz_r(k)) << 2) | (row & 3))];
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int col = wn0 + j * 32 + l32;
+            if constexpr (BNC) {
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const int k = kb + s;
+                    b[j][s] = Bs[k * BN + ((((col >> 2) ^ swz_r(k)) << 2) | (col & 3))];
+                }
+            } else {
+                const int c = (kb >> 2) ^ swz_k<BK>(col);
+                b[j] = *reinterpret_cast<const f32x4 *>(Bs + col * BK + 4 * c);
+            }
+        }
+    };
+    auto mfma_g = [&](const f32x4 (&a)[TM], const f32x4 (&b)[TN]) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], b[j][s], acc[i][j],
+                                                                     0, 0, 0);
+    };
+    auto colsum_add = [&](const float *Bs) {
+        if constexpr (kTN)
+            if (do_cs)
+                cs.add([&](int k, int c) {
+                    return Bs[k * BN + ((((c >> 2) ^ swz_r(k)) << 2) | (c & 3))];
+                });
+    };
+    constexpr int NG = BK / 8;
+
 #pragma unroll
     for (int t = 0; t < kAhead; ++t)
         if (t < nk) issue(t, t);
@@ -523,51 +577,12 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_dma(GemmArgs p) {
         const float *As = lds + (kt % kStages) * kStageSz;
         const float *Bs = As + kASz;
 #pragma unroll
-        for (int g = 0; g < BK / 8; ++g) {
-            const int kb = (g >> 1) * 16 + 8 * h + 4 * (g & 1);
+        for (int g = 0; g < NG; ++g) {
             f32x4 a[TM], b[TN];
-#pragma unroll
-            for (int i = 0; i < TM; ++i) {
-                const int row = wm0 + i * 32 + l32;
-                if constexpr (AK) {
-                    const int c = (kb >> 2) ^ swz_k<BK>(row);
-                    a[i] = *reinterpret_cast<const f32x4 *>(As + row * BK + 4 * c);
-                } else {
-#pragma unroll
-                    for (int s = 0; s < 4; ++s) {
-                        const int k = kb + s;
-                        a[i][s] = As[k * BM + ((((row >> 2) ^ swz_r(k)) << 2) | (row & 3))];
-                    }
-                }
-            }
-#pragma unroll
-            for (int j = 0; j < TN; ++j) {
-                const int col = wn0 + j * 32 + l32;
-                if constexpr (BNC) {
-#pragma unroll
-                    for (int s = 0; s < 4; ++s) {
-                        const int k = kb + s;
-                        b[j][s] = Bs[k * BN + ((((col >> 2) ^ swz_r(k)) << 2) | (col & 3))];
-                    }
-                } else {
-                    const int c = (kb >> 2) ^ swz_k<BK>(col);
-                    b[j] = *reinterpret_cast<const f32x4 *>(Bs + col * BK + 4 * c);
-                }
-            }
-#pragma unroll
-            for (int s = 0; s < 4; ++s)
-#pragma unroll
-                for (int i = 0; i < TM; ++i)
-#pragma unroll
-                    for (int j = 0; j < TN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], b[j][s],
-                                                                         acc[i][j], 0, 0, 0);
+            frag(As, Bs, g, a, b);
+            mfma_g(a, b);
         }
-        if constexpr (kTN)
-            if (do_cs)
-                cs.add([&](int k, int c) {
-                    return Bs[k * BN + ((((c >> 2) ^ swz_r(k)) << 2) | (c & 3))];
-                });
+        colsum_add(Bs);
     }
     __syncthreads();  // every wave past its last tile read before the stage reuse
     if constexpr (kTN)

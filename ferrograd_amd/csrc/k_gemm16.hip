@@ -21,27 +21,25 @@ constexpr bool kDma16 = FG_GEMM16_DMA != 0;
 int tiles(int M, int N, int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); }
 
 // Tile configuration (indices as in fg_gemm16_kernel.h), from a measured
-// sweep on MI355X over the configurations' shapes (TFLOP/s, bf16):
-//  * NN: 256x128 when it gives >= one tile per CU (506 at 4096^3, 330 at
-//    2048x4096x4096), else 128x128 with >= one tile per CU, else 64x64
-//    (85 for the 1000-wide head, where larger tiles leave CUs idle);
-//  * NT: 256x256 with 8 waves when it fills the chip (783 at 4096^3), else
-//    128x128 (569 at 2048x4096x4096), else 64x64;
-//  * TN: 256x256 with 8 waves when it gives >= half a tile per CU (336-367
-//    for the 4096-wide weight gradients), else 128x128, else 64x64.
-int pick_cfg16(int layout, int M, int N, int cus) {
-    if (layout == FG_NN) {
-        if (tiles(M, N, 256, 128) >= cus) return 4;
-        if (tiles(M, N, 128, 128) >= cus) return 2;
-        return 3;
-    }
-    if (layout == FG_NT) {
+// sweep on MI355X of every configuration on the direct-to-LDS path
+// (TFLOP/s, bf16; fp16 within a few percent):
+//  * 256x256 with 8 waves and BK 64 when it gives >= one tile per CU: 908 /
+//    830 / 903 for NN / NT / TN at 4096^3, 1022 at 8192^3;
+//  * else 256x128 with 8 waves and BK 64 down to a quarter tile per CU: 607
+//    for the 2048x4096x4096 forward, 715 for its NT data gradient, 180 for
+//    the 1000-wide head, where every smaller tile measured lower;
+//  * else 128x128, else 64x64.
+// The BK 64 tiles need K % 64 == 0 for the direct-to-LDS path; when only
+// K % 32 == 0 holds, 256x256 with 8 waves and BK 32 (775 / 823 / 822) or
+// 128x128 keep it.
+int pick_cfg16(int M, int N, int K, int cus) {
+    if (K % 64 == 0) {
+        if (tiles(M, N, 256, 256) >= cus) return 6;
+        if (tiles(M, N, 256, 128) >= cus / 4) return 8;
+    } else if (K % 32 == 0) {
         if (tiles(M, N, 256, 256) >= cus) return 1;
-        if (tiles(M, N, 128, 128) >= cus) return 2;
-        return 3;
     }
-    if (tiles(M, N, 256, 256) >= cus / 2) return 1;
-    if (tiles(M, N, 128, 128) >= cus) return 2;
+    if (tiles(M, N, 128, 128) >= cus / 4) return 2;
     return 3;
 }
 
@@ -73,7 +71,7 @@ int gemm16_common(fg_ctx *ctx, int dtype, int layout, Args &a, const char *who) 
 #ifdef FG_GEMM16_FORCE_CFG  // tuning builds: one tile configuration for every shape
     const int cfg = FG_GEMM16_FORCE_CFG;
 #else
-    const int cfg = pick_cfg16(layout, a.M, a.N, ctx->cu_count > 0 ? ctx->cu_count : 256);
+    const int cfg = pick_cfg16(a.M, a.N, a.K, ctx->cu_count > 0 ? ctx->cu_count : 256);
 #endif
     // Direct-to-LDS loads: whole K tiles, 16-byte chunks of 8 elements along
     // each row-contiguous operand's rows (B of NN / TN, A of TN).

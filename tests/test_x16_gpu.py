@@ -139,14 +139,17 @@ def test_gemm_x16_exact_bits(gpu_ctx, dtype, layout, shape):
 @pytest.mark.parametrize("dtype", [F16, BF16], ids=lambda d: DT_IDS[d])
 @pytest.mark.parametrize("case", [(O.NN, 4096, 2048, 64), (O.NT, 4096, 4096, 64),
                                   (O.TN, 4096, 4096, 48), (O.NN, 2050, 4000, 96),
-                                  (O.NT, 4096, 4000, 96), (O.TN, 4000, 4096, 96)],
+                                  (O.NT, 4096, 4000, 96), (O.TN, 4000, 4096, 96),
+                                  (O.NN, 2050, 4000, 128), (O.NT, 4096, 4000, 192),
+                                  (O.TN, 4000, 4096, 128)],
                          ids=["NN-4096x2048x64", "NT-4096x4096x64", "TN-4096x4096x48",
-                              "NN-2050x4000x96", "NT-4096x4000x96", "TN-4000x4096x96"])
+                              "NN-2050x4000x96", "NT-4096x4000x96", "TN-4000x4096x96",
+                              "NN-2050x4000x128", "NT-4096x4000x192", "TN-4000x4096x128"])
 def test_gemm_x16_exact_bits_large_tiles(gpu_ctx, dtype, case):
     """Shapes large enough for the 256-wide tile configurations the
-    dispatcher picks for full-chip GEMMs (8-wave 256x256, 256x128), on the
-    direct-to-LDS path (K a multiple of 32; edge tiles in M and N) and off
-    it (K = 48)."""
+    dispatcher picks for full-chip GEMMs (8-wave 256x256 and 256x128 at
+    BK 64, 256x256 at BK 32, 128x128), on the direct-to-LDS path (K a
+    multiple of 32 or 64; edge tiles in M and N) and off it (K = 48)."""
     layout, M, N, K = case
     note(f"gemm_x16 exact large {DT_IDS[dtype]} layout={layout} {M}x{N}x{K}")
     rng = np.random.default_rng(M + K + layout)
