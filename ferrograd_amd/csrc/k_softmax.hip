@@ -10,12 +10,21 @@
 // second time (defect).
 //
 // Here one workgroup owns one row.  The fast path keeps the whole row in
-// registers (NV float4 per thread, 256 threads: up to 32768 columns), so the
-// logits are read from HBM exactly once and dlogits written exactly once:
-// 8*C bytes per row, the minimum.  Reductions are wavefront shuffles (64
-// lanes) followed by one LDS exchange across the 4 waves.  Rows too long for
-// registers, or not 16-byte aligned, use a two-pass streaming kernel with an
-// online max/sum.
+// registers (NV float4 per thread; 256 threads, or 512 for rows of more
+// than 16384 columns: up to 32768 columns), so the logits are read from HBM
+// exactly once and dlogits written exactly once: 8*C bytes per row, the
+// minimum.  Reductions are wavefront shuffles (64 lanes) followed by one LDS
+// exchange across the waves.  Rows too long for registers, or not 16-byte
+// aligned, use a two-pass streaming kernel with an online max/sum.
+//
+// Long rows: 512 threads with 16 float4 each, read and written with buffer
+// instructions, take 363.5 us on the 8192 x 32000 CE (5.77 TB/s) against
+// 372.5 us for 256 threads with 32 float4 and plain global accesses.
+// Measured and dropped: rotating each row's chunk order by the row index
+// (366.9 us), holding the 512-thread kernel to 80 VGPRs for a sixth wave per
+// SIMD (it then spills: 381 us), 256 threads with buffer instructions
+// (377 us).  For scale, a flat copy of the same bytes reaches 6.6 TB/s, and a
+// copy kernel with this kernel's row structure 5.6-5.9 TB/s.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -37,7 +46,9 @@ __device__ __forceinline__ void argmax_combine(float &m, int &i, float m2, int i
     }
 }
 
-// Block-wide (max, lowest index of max); every thread receives the result.
+// Block-wide (max, lowest index of max) over NW waves; every thread
+// receives the result.
+template <int NW = kWaves>
 __device__ __forceinline__ void block_argmax(float &m, int &idx, float *sm, int *si) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
@@ -54,10 +65,11 @@ __device__ __forceinline__ void block_argmax(float &m, int &idx, float *sm, int 
     m = sm[0];
     idx = si[0];
 #pragma unroll
-    for (int k = 1; k < kWaves; ++k) argmax_combine(m, idx, sm[k], si[k]);
+    for (int k = 1; k < NW; ++k) argmax_combine(m, idx, sm[k], si[k]);
     __syncthreads();
 }
 
+template <int NW = kWaves>
 __device__ __forceinline__ float block_sum(float s, float *sm) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
@@ -66,7 +78,7 @@ __device__ __forceinline__ float block_sum(float s, float *sm) {
     __syncthreads();
     float t = 0.0f;
 #pragma unroll
-    for (int k = 0; k < kWaves; ++k) t += sm[k];
+    for (int k = 0; k < NW; ++k) t += sm[k];
     __syncthreads();
     return t;
 }
@@ -114,41 +126,64 @@ __device__ __forceinline__ void row_outputs(const void *xr, int dt, int C, const
     }
 }
 
-// Register-resident fast path.  out (may be NULL) receives
+// Register-resident fast path with NT threads.  out (may be NULL) receives
 //   labels ? scale*(p - onehot) : scale*p.
-template <int NV>
-__global__ __launch_bounds__(kNT) void softmax_rows_v4(const float *__restrict__ x, int ldx,
-                                                       const uint32_t *__restrict__ labels, int C,
-                                                       float scale, float *__restrict__ row_loss,
-                                                       float *__restrict__ out, int ldo,
-                                                       uint32_t *__restrict__ argmax) {
-    __shared__ float sm[kWaves];
-    __shared__ int si[kWaves];
+// Thread t holds the float4 chunks t + NT*i of the row (i < NV); argmax ties
+// go to the lowest column (a row of -inf gives 0, as the CPU restatement's
+// first-maximum scan does).  Rows are
+// read and written with buffer instructions: each chunk gets a descriptor
+// (uniform, in scalar registers) whose base is the chunk's start and whose
+// size is what remains of the row, and every access takes the one 32-bit
+// lane offset 16 * t.  The NV loads in flight then hold no 64-bit addresses
+// in vector registers, and lanes past the row end read zero (replaced by
+// -inf) and have their stores dropped by the descriptor's range check,
+// which covers the vector offset (a raw buffer access does not range-check
+// its scalar offset, so none is used).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kBufWord3 = 0x00020000;  // buffer descriptor word 3 for gfx9 targets
+constexpr int kBufNT = 2;              // cache-policy bits: non-temporal
+
+template <int NV, int NT>
+__global__ __launch_bounds__(NT) void softmax_rows_v4(const float *__restrict__ x, int ldx,
+                                                      const uint32_t *__restrict__ labels, int C,
+                                                      float scale, float *__restrict__ row_loss,
+                                                      float *__restrict__ out, int ldo,
+                                                      uint32_t *__restrict__ argmax) {
+    constexpr int NW = NT / 64;
+    __shared__ float sm[NW];
+    __shared__ int si[NW];
     const int r = blockIdx.x;
     const float *xr = x + (size_t)r * ldx;
     const int C4 = C >> 2;
+    const int lane_off = (int)threadIdx.x * 16;
+    // Descriptor of chunk k of a row: base at the chunk, size = the row's
+    // remaining bytes (0 past the end).
+    auto rsrc = [&](const float *row, int k) {
+        const int skip = k * NT * 16;
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(row) + skip / 4, (short)0,
+                                                 max(C * 4 - skip, 0), kBufWord3);
+    };
     f32x4 v[NV];
     float m = -INFINITY;
     int am = 0x7fffffff;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-        const int j = threadIdx.x + i * kNT;
-        if (j < C4)
-            v[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(xr) + j);
-        else
-            v[i] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rsrc(xr, i), lane_off, 0,
+                                                              kBufNT);
+        v[i] = __builtin_bit_cast(f32x4, w);
     }
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-        const int c0 = 4 * (threadIdx.x + i * kNT);
+        const int j = (int)threadIdx.x + NT * i;
+        if (j >= C4) v[i] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-            if (v[i][e] > m) {
+            if (v[i][e] > m || (v[i][e] == m && 4 * j + e < am)) {
                 m = v[i][e];
-                am = c0 + e;
+                am = 4 * j + e;
             }
     }
-    block_argmax(m, am, sm, si);
+    block_argmax<NW>(m, am, sm, si);
     float s = 0.0f;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
@@ -158,24 +193,21 @@ __global__ __launch_bounds__(kNT) void softmax_rows_v4(const float *__restrict__
             s += v[i][e];
         }
     }
-    s = block_sum(s, sm);
+    s = block_sum<NW>(s, sm);
     row_outputs(xr, fg::kF32, C, labels, r, m, s, am, row_loss, argmax);
     if (out) {
         const float inv = 1.0f / s;
+        // The label's chunk and lane (none when unlabelled or out of range).
         const int t = labels ? (int)labels[r] : -1;
-        float *orow = out + (size_t)r * ldo;
+        const int jt = t >= 0 ? t >> 2 : -1, et = t & 3;
+        const float *orow = out + (size_t)r * ldo;
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
-            const int j = threadIdx.x + i * kNT;
-            if (j < C4) {
-                f32x4 d;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float p = v[i][e] * inv;
-                    d[e] = scale * (4 * j + e == t ? p - 1.0f : p);
-                }
-                __builtin_nontemporal_store(d, reinterpret_cast<f32x4 *>(orow) + j);
-            }
+            const int j = (int)threadIdx.x + NT * i;
+            f32x4 d = v[i] * inv;
+            if (j == jt) d[et] -= 1.0f;
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, scale * d),
+                                                   rsrc(orow, i), lane_off, 0, kBufNT);
         }
     }
 }
@@ -336,20 +368,21 @@ int launch_rows(fg_ctx *ctx, int dt, const void *x, int ldx, const uint32_t *lab
     if (dt == fg::kF32) {
         const float *xf = static_cast<const float *>(x);
         float *of = static_cast<float *>(out);
-#define FG_SM_LAUNCH(NV) \
-    softmax_rows_v4<NV><<<grid, block, 0, st>>>(xf, ldx, labels, C, scale, row_loss, of, ldo, argmax)
+#define FG_SM_LAUNCH(NV, NT)                                                               \
+    softmax_rows_v4<NV, NT><<<grid, NT, 0, st>>>(xf, ldx, labels, C, scale, row_loss, of, ldo, \
+                                                 argmax)
         if (aligned && C4 <= kNT * 1)
-            FG_SM_LAUNCH(1);
+            FG_SM_LAUNCH(1, kNT);
         else if (aligned && C4 <= kNT * 2)
-            FG_SM_LAUNCH(2);
+            FG_SM_LAUNCH(2, kNT);
         else if (aligned && C4 <= kNT * 4)
-            FG_SM_LAUNCH(4);
+            FG_SM_LAUNCH(4, kNT);
         else if (aligned && C4 <= kNT * 8)
-            FG_SM_LAUNCH(8);
+            FG_SM_LAUNCH(8, kNT);
         else if (aligned && C4 <= kNT * 16)
-            FG_SM_LAUNCH(16);
-        else if (aligned && C4 <= kNT * 32)
-            FG_SM_LAUNCH(32);
+            FG_SM_LAUNCH(16, kNT);
+        else if (aligned && C4 <= 2 * kNT * 16)
+            FG_SM_LAUNCH(16, 2 * kNT);
         else
             softmax_rows_stream<<<grid, block, 0, st>>>(x, ldx, labels, C, scale, row_loss, out,
                                                         ldo, argmax, dt);

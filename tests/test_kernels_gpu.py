@@ -262,6 +262,14 @@ def test_softmax_ce_parity(gpu_ctx, shape):
     rng = np.random.default_rng(R * C)
     x = (2 * rng.standard_normal((R, C))).astype(f32)
     x[0, C // 3] = x[0, C // 2] = 50.0   # tie: argmax must be the first
+    # Ties 2048 columns apart fall to one thread of a 256- or 512-thread row
+    # in different chunks; rows start their chunk walk at different places,
+    # so some rows meet the higher column first.  The lowest must still win.
+    for r in range(1, min(R, 17)):
+        a = 28 + 2048 * (r % 4)
+        b = a + 2048 * (1 + r % 6)
+        if b < C:
+            x[r, a] = x[r, b] = 60.0
     labels = rng.integers(0, C, R)
     check_softmax_ce(gpu_ctx, x, labels, scale=1.0)
     check_softmax_ce(gpu_ctx, x, labels, scale=1.0 / R)
