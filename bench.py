@@ -405,7 +405,42 @@ def only_copy_256mib(ctx, reps):
         b.copy_(a)
 
 
+def only_c5_step(ctx, reps, dtype="f32"):
+    """The c5 training step as a captured hipGraph, replayed (for kernel
+    traces of the step alone)."""
+    tr = MLPStep(ctx, [1024] + [4096] * 7 + [1000], 2048, dtype=dtype)
+    tr.capture()
+    for _ in range(reps):
+        tr.step_graph()
+
+
+def only_c5_step_bf16(ctx, reps):
+    """The c5 step with bfloat16 tensors, captured and replayed."""
+    only_c5_step(ctx, reps, dtype="bf16")
+
+
+def only_gemm_bf16_c2(ctx, reps):
+    """The c2-shaped 4096^3 bf16 GEMMs: forward (bias + ReLU), dA, dB."""
+    import torch
+
+    import ferrograd_amd as fa
+
+    n, bf = 4096, fa.DTYPE_BF16
+    g = torch.Generator(device="cuda").manual_seed(1)
+    A, Bm, dC = (torch.randn((n, n), device="cuda", generator=g).to(torch.bfloat16)
+                 for _ in range(3))
+    bias = (0.1 * torch.randn((n,), device="cuda", generator=g)).to(torch.bfloat16)
+    C, Z, dA, dB = (torch.empty((n, n), device="cuda", dtype=torch.bfloat16) for _ in range(4))
+    for _ in range(reps):
+        ctx.gemm_x16(bf, fa.NN, n, n, n, A, n, Bm, n, C, n, bias=bias, act=fa.ACT_RELU, Z=Z, ldz=n)
+        ctx.gemm_bwd_x16(bf, fa.NT, n, n, n, dC, n, Bm, n, dA, n, act=fa.ACT_RELU, Zs=Z, ldzs=n)
+        ctx.gemm_x16(bf, fa.TN, n, n, n, A, n, dC, n, dB, n)
+
+
 ONLY = {
+    "c5_step": only_c5_step,
+    "c5_step_bf16": only_c5_step_bf16,
+    "gemm_bf16_c2": only_gemm_bf16_c2,
     "gemm_c5_hidden": only_gemm_c5_hidden,
     "softmax_ce_c3": only_softmax_ce_c3,
     "adam_c4": only_adam_c4,

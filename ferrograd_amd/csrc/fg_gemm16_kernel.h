@@ -359,6 +359,12 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm16_mfma(Args p) {
 // masked outputs).
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 
+// Register double-buffering of the MFMA operands in gemm16_dma (1), or
+// read-then-multiply per k16 step (0): a knob for measurement builds.
+#ifndef FG_GEMM16_PIPE
+#define FG_GEMM16_PIPE 1
+#endif
+
 template <int BK>
 __device__ __forceinline__ int swz16_k(int row) {
     return (row / (128 / BK)) % (BK / 8);
@@ -390,6 +396,19 @@ __device__ __forceinline__ u32x4 read_tr(const uint16_t *tile, int k0, int row_b
         out[2 * half + 1] = w[1];
     }
     return out;
+}
+
+// Scheduling groups for one k16 step: MFMA q (of NM) followed by its share
+// (PER) of the NR LDS reads of the next step.
+template <int Q, int NM, int NR, int PER>
+__device__ __forceinline__ void sched_interleave() {
+    if constexpr (Q < NM) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        constexpr int left = NR - Q * PER;
+        if constexpr (left > 0)
+            __builtin_amdgcn_sched_group_barrier(0x100, left < PER ? left : PER, 0);  // LDS reads
+        sched_interleave<Q + 1, NM, NR, PER>();
+    }
 }
 
 template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC, bool BF>
@@ -514,6 +533,56 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm16_dma(Args p) {
         if (t < nk) issue(t, t);
     wait_tiles(min(kStages, nk) - 1);
     asm volatile("s_barrier" ::: "memory");
+#if FG_GEMM16_PIPE
+    // Operands double-buffered in registers: the LDS reads of k16 step u+1
+    // are issued before the MFMAs of step u, so the matrix units never wait
+    // for the reads of the step they are about to run.  ca / cb hold the
+    // operands of the next step to multiply.
+    // LDS read instructions per k16 step (a row-contiguous operand takes two
+    // transposing reads) and the order the scheduler is held to: one MFMA,
+    // then that MFMA's share of the next step's reads.
+    constexpr int kReads = (AK ? TM : 2 * TM) + (BNC ? 2 * TN : TN);
+    constexpr int kMfma = TM * TN;
+    constexpr int kPerMfma = (kReads + kMfma - 1) / kMfma;
+    auto interleave = [&]() { sched_interleave<0, kMfma, kReads, kPerMfma>(); };
+    u32x4 ca[TM], cb[TN];
+    if (nk > 0) frag(lds, lds + kASz, 0, ca, cb);
+    for (int kt = 0; kt < nk; ++kt) {
+        const uint16_t *As = lds + (kt % kStages) * kStageSz;
+        const uint16_t *Bs = As + kASz;
+        if (kt >= 1 && kt - 1 + kStages < nk) issue(kt - 1 + kStages, (kt - 1) % kStages);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < NU - 1; ++u) {
+            u32x4 na[TM], nb[TN];
+            frag(As, Bs, u + 1, na, nb);
+            mma(ca, cb);
+            interleave();
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < TM; ++i) ca[i] = na[i];
+#pragma unroll
+            for (int j = 0; j < TN; ++j) cb[j] = nb[j];
+        }
+        // ca / cb: the last step of tile kt.  Every wave's reads of tile kt
+        // must be done before the barrier (its stage is refilled after it).
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        wait_tiles(min(kt + kStages - 1, nk - 1) - (kt + 1));
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_barrier" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        u32x4 na[TM], nb[TN];
+        if (kt + 1 < nk) {
+            const uint16_t *An = lds + ((kt + 1) % kStages) * kStageSz;
+            frag(An, An + kASz, 0, na, nb);
+        }
+        mma(ca, cb);
+#pragma unroll
+        for (int i = 0; i < TM; ++i) ca[i] = na[i];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) cb[j] = nb[j];
+    }
+#else
     u32x4 la[TM], lb[TN];
     for (int kt = 0; kt < nk; ++kt) {
         const uint16_t *As = lds + (kt % kStages) * kStageSz;
@@ -535,6 +604,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm16_dma(Args p) {
         __builtin_amdgcn_sched_barrier(0);
     }
     if (nk > 0) mma(la, lb);
+#endif
     __syncthreads();
     store_tile16<BF, TM, TN, WTN, NW>(p, acc, reinterpret_cast<float *>(lds), m0 + wm0, n0 + wn0,
                                       wave, lane);

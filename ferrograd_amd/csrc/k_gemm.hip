@@ -19,22 +19,26 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // ------------------------------------------------------------ dispatch
 // Tile configuration per call (indices as in fg_gemm_kernel.h), from a
 // measured sweep of every configuration on MI355X (256 CUs, direct-to-LDS
-// loads) over the BASELINE shapes, TFLOP/s:
-//  * NN (forward): 256x128 with 8 waves and BK 32 when it yields >= one tile
-//    per CU (111 at 2048x4096x4096, 103 at K = 1024); else 128x64 (95 for
-//    the 1000-wide head); 64x64 for anything smaller.
+// loads, N(0,1) operands, HIP events) over the BASELINE shapes, TFLOP/s:
+//  * NN (forward): 256x256 with 8 waves for K >= 4096 squares that fill the
+//    chip (134 at 4096^3, against 130 for 256x128); else 256x128 with 8
+//    waves and BK 32 when it yields >= one tile per CU (125 at
+//    2048x4096x4096, 99 at K = 1024); else 128x64 (104 for the 1000-wide
+//    head); 64x64 for anything smaller.
 //  * NT (dA): 256x256 with 8 waves (BK 32) for large-K squares that fill the
-//    chip (137 at 4096^3); else 256x128 with 8 waves when it gives >= one tile
-//    per CU (119 at 2048x4096x4096, 100 at K = 1000); else 128x128 or 128x64
-//    (106 at 2048x1024x4096).
-//  * TN (dW): 256x256 with 8 waves for K >= 4096 filling the chip (140 at
-//    4096^3); 256x128 with 4 waves and BK 16 at >= two tiles per CU (122 at
-//    4096x4096x2048); else 128x128 (113-115 for the 1024- and 1000-wide
-//    layers); else 128x64.
+//    chip (138 at 4096^3); else 256x128 with 8 waves when it gives >= one tile
+//    per CU (127 at 2048x4096x4096, 96-104 at K = 1000); else 128x128 or
+//    128x64 (96 at 2048x1024x4096).
+//  * TN (dW): 256x256 with 8 waves for K >= 4096 filling the chip (138 at
+//    4096^3); 256x128 with 4 waves and BK 16 at >= two tiles per CU (129 at
+//    4096x4096x2048); then 128x64 at >= two tiles per CU (111 for the
+//    1000-wide layer and 103 for the 1024-deep one, against 106 / 102 for
+//    128x128); else 128x128; else 128x64.
 int tiles(int M, int N, int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); }
 
 int pick_cfg(int layout, int M, int N, int K, int cus) {
     if (layout == FG_NN) {
+        if (K >= 4096 && tiles(M, N, 256, 256) >= cus) return 6;
         if (tiles(M, N, 256, 128) >= cus) return 7;
         if (tiles(M, N, 128, 64) >= cus) return 5;
         return 4;
@@ -44,6 +48,7 @@ int pick_cfg(int layout, int M, int N, int K, int cus) {
         if (tiles(M, N, 256, 128) >= cus) return 7;
     } else {
         if (tiles(M, N, 256, 128) >= 2 * cus) return 1;
+        if (tiles(M, N, 128, 64) >= 2 * cus) return 5;
     }
     if (tiles(M, N, 128, 128) >= cus) return 3;
     if (tiles(M, N, 128, 64) >= cus) return 5;
