@@ -435,7 +435,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm16_dma(Args p) {
     int tile_m, tile_n;
     tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tile_m, tile_n);
     const int m0 = tile_m * BM, n0 = tile_n * BN;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // The wave index, as a uniform (scalar) value: it selects LDS destinations
+    // and operands per wave, which the compiler would otherwise treat as
+    // varying across lanes.
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l32 = lane & 31, h = lane >> 5;
     const int wm0 = (wave / WGN) * WTM, wn0 = (wave % WGN) * WTN;
 
