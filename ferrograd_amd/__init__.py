@@ -108,6 +108,13 @@ class Context:
         call("fg_gemm_dw_f32", self.handle, M, N, K, _ptr(A), lda, _ptr(B), ldb, _ptr(C), ldc,
              int(accumulate), _ptr(colsum), int(colsum_accumulate))
 
+    def gemm_dw_x16(self, dtype: int, M: int, N: int, K: int, A, lda: int, B, ldb: int, C,
+                    ldc: int, accumulate: bool = False, colsum=None,
+                    colsum_accumulate: bool = False) -> None:
+        """16-bit C (=|+=) A^T.B and colsum (=|+=) column sums of B in one launch."""
+        call("fg_gemm_dw_x16", self.handle, dtype, M, N, K, _ptr(A), lda, _ptr(B), ldb, _ptr(C),
+             ldc, int(accumulate), _ptr(colsum), int(colsum_accumulate))
+
     def gemm_x16(self, dtype: int, layout: int, M: int, N: int, K: int, A, lda: int, B,
                  ldb: int, C, ldc: int, bias=None, act: int = ACT_NONE, Z=None, ldz: int = 0,
                  accumulate: bool = False) -> None:

@@ -55,6 +55,12 @@ struct Args {
     int accumulate;
     int tiles_m, tiles_n;
     int vec_out;  // C / Z / Zs rows and bias 8-byte aligned: 4-element epilogue I/O
+    // TN on the direct-to-LDS path only: colsum[n] (=|+=) sum_k B[k][n] --
+    // the bias gradient of the layer whose weight gradient this GEMM
+    // computes -- summed in fp32 from the B tiles already in LDS by the
+    // workgroups of the first tile row, rounded to the storage type once.
+    uint16_t *colsum;
+    int colsum_accumulate;
 };
 
 // Element conversion and the MFMA of one storage type.
@@ -359,12 +365,6 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm16_mfma(Args p) {
 // masked outputs).
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 
-// Register double-buffering of the MFMA operands in gemm16_dma (1), or
-// read-then-multiply per k16 step (0): a knob for measurement builds.
-#ifndef FG_GEMM16_PIPE
-#define FG_GEMM16_PIPE 1
-#endif
-
 template <int BK>
 __device__ __forceinline__ int swz16_k(int row) {
     return (row / (128 / BK)) % (BK / 8);
@@ -397,6 +397,51 @@ __device__ __forceinline__ u32x4 read_tr(const uint16_t *tile, int k0, int row_b
     }
     return out;
 }
+
+// Column sums of the B tiles of the TN layout (B row-contiguous, [BK][BN]
+// in LDS with chunk c of k-row k at chunk c ^ swz16_r(k)), for the bias
+// gradient, taken by the workgroups of tile row 0: thread t owns the 8
+// columns of chunk t % (BN / 8) and k-rows (t / (BN / 8)) * KPT .. + KPT of
+// each tile, summed in fp32; the k-groups are added in a fixed order at the
+// end (deterministic).
+template <int BN, int BK, int NT, bool BF>
+struct ColSum16 {
+    static constexpr int kChunks = BN / 8;
+    static constexpr int G = NT / kChunks;  // k-groups
+    static constexpr int KPT = BK / G;      // k-rows per thread and tile
+    static_assert(NT % kChunks == 0 && BK % G == 0 && KPT >= 1, "column-sum split");
+    float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+
+    __device__ __forceinline__ void add(const uint16_t *Bs) {
+        const int c = threadIdx.x % kChunks, g = threadIdx.x / kChunks;
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const int k = g * KPT + i;
+            const u32x4 w =
+                *reinterpret_cast<const u32x4 *>(Bs + k * BN + ((c ^ swz16_r(k)) << 3));
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                s[e] += T16<BF>::to_f((uint16_t)(w[e >> 1] >> (16 * (e & 1))));
+        }
+    }
+    // Combines the k-groups through lds (G * BN floats, free) and writes the
+    // tile's columns.  Called by every thread of the workgroup.
+    __device__ __forceinline__ void finish(const Args &p, float *lds, int n0) const {
+        const int c = threadIdx.x % kChunks, g = threadIdx.x / kChunks;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) lds[g * BN + c * 8 + e] = s[e];
+        __syncthreads();
+        for (int col = threadIdx.x; col < BN; col += NT) {
+            if (n0 + col >= p.N) continue;
+            float t = 0.0f;
+#pragma unroll
+            for (int k = 0; k < G; ++k) t += lds[k * BN + col];
+            uint16_t *dst = p.colsum + n0 + col;
+            *dst = T16<BF>::from_f(p.colsum_accumulate ? T16<BF>::to_f(*dst) + t : t);
+        }
+        __syncthreads();
+    }
+};
 
 // Scheduling groups for one k16 step: MFMA q (of NM) followed by its share
 // (PER) of the NR LDS reads of the next step.
@@ -483,6 +528,9 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm16_dma(Args p) {
     };
 
     const int nk = p.K / BK;
+    constexpr bool kTN = !AK && BNC;
+    ColSum16<BN, BK, 64 * NW, BF> cs;
+    const bool do_cs = kTN && p.colsum && tile_m == 0;
     // MFMA operands of k16 step u of a stage: lane half h takes k 8h .. 8h+7.
     auto frag = [&](const uint16_t *As, const uint16_t *Bs, int u, u32x4 (&a)[TM], u32x4 (&b)[TN]) {
         const int kb = u * 16 + 8 * h;
@@ -536,7 +584,6 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm16_dma(Args p) {
         if (t < nk) issue(t, t);
     wait_tiles(min(kStages, nk) - 1);
     asm volatile("s_barrier" ::: "memory");
-#if FG_GEMM16_PIPE
     // Operands double-buffered in registers: the LDS reads of k16 step u+1
     // are issued before the MFMAs of step u, so the matrix units never wait
     // for the reads of the step they are about to run.  ca / cb hold the
@@ -567,6 +614,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm16_dma(Args p) {
 #pragma unroll
             for (int j = 0; j < TN; ++j) cb[j] = nb[j];
         }
+        if constexpr (kTN)
+            if (do_cs) cs.add(Bs);
         // ca / cb: the last step of tile kt.  Every wave's reads of tile kt
         // must be done before the barrier (its stage is refilled after it).
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
@@ -585,30 +634,9 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm16_dma(Args p) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) cb[j] = nb[j];
     }
-#else
-    u32x4 la[TM], lb[TN];
-    for (int kt = 0; kt < nk; ++kt) {
-        const uint16_t *As = lds + (kt % kStages) * kStageSz;
-        const uint16_t *Bs = As + kASz;
-        if (kt >= 1 && kt - 1 + kStages < nk) issue(kt - 1 + kStages, (kt - 1) % kStages);
-        if (kt >= 1) mma(la, lb);
-#pragma unroll
-        for (int u = 0; u < NU - 1; ++u) {
-            u32x4 a[TM], b[TN];
-            frag(As, Bs, u, a, b);
-            mma(a, b);
-        }
-        frag(As, Bs, NU - 1, la, lb);
-        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of tile kt done
-        // Tile kt+1 has landed once only the tiles issued after it remain.
-        wait_tiles(min(kt + kStages - 1, nk - 1) - (kt + 1));
-        __builtin_amdgcn_sched_barrier(0);
-        asm volatile("s_barrier" ::: "memory");
-        __builtin_amdgcn_sched_barrier(0);
-    }
-    if (nk > 0) mma(la, lb);
-#endif
     __syncthreads();
+    if constexpr (kTN)
+        if (do_cs) cs.finish(p, reinterpret_cast<float *>(lds), n0);
     store_tile16<BF, TM, TN, WTN, NW>(p, acc, reinterpret_cast<float *>(lds), m0 + wm0, n0 + wn0,
                                       wave, lane);
 }

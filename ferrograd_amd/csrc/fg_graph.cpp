@@ -849,10 +849,12 @@ int lower_backward(fg_plan &P, bool fused, std::vector<Launch> &out) {
             }
             const uint32_t a = g.nodes[G.mm].in[0], b = g.nodes[G.mm].in[1];
             const int M = (int)P.shape[a].rows, K = (int)P.shape[a].cols, N = (int)P.shape[b].cols;
-            // fp32: the bias gradient rides on the dW GEMM (column sums of dZ
-            // from its B tiles) when that GEMM runs.
+            // The bias gradient rides on the dW GEMM (column sums of dZ from
+            // its B tiles) when that GEMM runs and dZ and the bias share its
+            // element type.
             const bool fuse_db = G.bias_src != kNone && P.needs_grad[G.bias_src] &&
-                                 P.needs_grad[b] && P.dtype[G.mm] == FG_DTYPE_F32;
+                                 P.needs_grad[b] && P.sdt(gs(G.bias_src)) == P.dtype[G.mm] &&
+                                 P.sdt(gs(pre)) == P.dtype[G.mm];
             if (G.bias_src != kNone && P.needs_grad[G.bias_src] && !fuse_db) {
                 Launch L;
                 L.kind = LK_BIAS_GRAD;
@@ -1062,11 +1064,15 @@ int run(fg_plan &P, const std::vector<Launch> &list) {
         int rc = FG_OK;
         switch (L.kind) {
             case LK_GEMM:
-                if (L.sExtra != kNone)  // dW with the fused dbias (fp32, TN)
+                if (L.sExtra != kNone && L.dtype == FG_DTYPE_F32)  // dW with the fused dbias (TN)
                     rc = fg_gemm_dw_f32(ctx, L.M, L.N, L.K, (const float *)P.ptr(L.sA), L.lda,
                                         (const float *)P.ptr(L.sB), L.ldb, (float *)P.ptr(L.sC),
                                         L.ldc, L.accumulate, (float *)P.ptr(L.sExtra),
                                         L.accumulate2);
+                else if (L.sExtra != kNone)
+                    rc = fg_gemm_dw_x16(ctx, L.dtype, L.M, L.N, L.K, P.ptr(L.sA), L.lda,
+                                        P.ptr(L.sB), L.ldb, P.ptr(L.sC), L.ldc, L.accumulate,
+                                        P.ptr(L.sExtra), L.accumulate2);
                 else if (L.dtype == FG_DTYPE_F32)
                     rc = fg_gemm_f32(ctx, L.layout, L.M, L.N, L.K, (const float *)P.ptr(L.sA),
                                      L.lda, (const float *)P.ptr(L.sB), L.ldb,

@@ -51,7 +51,14 @@ int gemm16_common(fg_ctx *ctx, int dtype, int layout, Args &a, const char *who) 
                who, layout);
     FG_REQUIRE(a.M >= 0 && a.N >= 0 && a.K >= 0, FG_ERR_SHAPE, "%s: negative dimension", who);
     FG_REQUIRE(a.act >= 0 && a.act <= 2, FG_ERR_INVALID_ARGUMENT, "%s: bad act %d", who, a.act);
-    if (a.M == 0 || a.N == 0) return FG_OK;
+    FG_REQUIRE(!a.colsum || layout == FG_TN, FG_ERR_INVALID_ARGUMENT,
+               "%s: column sums need the TN layout", who);
+    if (a.N == 0) return FG_OK;
+    if (a.M == 0) {  // no output rows, but the column sums of B still run
+        if (!a.colsum) return FG_OK;
+        FG_REQUIRE(a.B && a.ldb >= a.N, FG_ERR_INVALID_ARGUMENT, "%s: bad B", who);
+        return fg_bias_grad(ctx, dtype, a.K, a.N, a.B, a.ldb, a.colsum, a.colsum_accumulate);
+    }
     FG_REQUIRE(a.A && a.B && a.C, FG_ERR_INVALID_ARGUMENT, "%s: NULL operand", who);
     const int a_cols = layout == FG_TN ? a.M : a.K;
     const int b_cols = layout == FG_NT ? a.K : a.N;
@@ -59,6 +66,7 @@ int gemm16_common(fg_ctx *ctx, int dtype, int layout, Args &a, const char *who) 
                FG_ERR_SHAPE, "%s: leading dimension too small (lda=%d ldb=%d ldc=%d)", who, a.lda,
                a.ldb, a.ldc);
     FG_HIP(hipSetDevice(ctx->device));
+    uint16_t *colsum = a.colsum;  // the bias gradient of fg_gemm_dw_x16, if any
     if (a.K == 0) a.A = a.B;  // loads are all masked; K=0 yields the epilogue of zero
     // 16-byte operand loads need 16-byte aligned bases and leading
     // dimensions that keep every row start aligned (multiples of 8
@@ -77,12 +85,18 @@ int gemm16_common(fg_ctx *ctx, int dtype, int layout, Args &a, const char *who) 
     // each row-contiguous operand's rows (B of NN / TN, A of TN).
     const bool rc_ok = (layout == FG_NT || a.N % 8 == 0) && (layout != FG_TN || a.M % 8 == 0);
     const bool dma = kDma16 && vec && rc_ok && a.K > 0 &&
-                     a.K % fg::gemm16::cfg_bk16(cfg) == 0 && a.M >= 8 && a.N >= 8;
+                     a.K % fg::gemm16::cfg_bk16(cfg) == 0 && a.M >= 8 && a.N >= 8 && cfg != 3;
+    // Only the direct-to-LDS kernel sums B's columns; elsewhere the separate
+    // reduction runs after the GEMM (same result up to the order of the
+    // fp32 sums).
+    if (colsum && !dma) a.colsum = nullptr;
     if (dtype == FG_DTYPE_BF16)
         fg::gemm16::launch_bf16(layout, a, vec, dma, cfg, ctx->stream);
     else
         fg::gemm16::launch_f16(layout, a, vec, dma, cfg, ctx->stream);
     FG_LAUNCH_CHECK(who);
+    if (colsum && !dma)
+        return fg_bias_grad(ctx, dtype, a.K, a.N, a.B, a.ldb, colsum, a.colsum_accumulate);
     return FG_OK;
 }
 
@@ -111,6 +125,27 @@ FG_API int fg_gemm_x16(fg_ctx *ctx, int dtype, int layout, int M, int N, int K, 
     FG_REQUIRE(!(accumulate && act != FG_ACT_NONE), FG_ERR_INVALID_ARGUMENT,
                "fg_gemm_x16: accumulate requires act NONE");
     return gemm16_common(ctx, dtype, layout, a, "fg_gemm_x16");
+}
+
+FG_API int fg_gemm_dw_x16(fg_ctx *ctx, int dtype, int M, int N, int K, const void *d_A, int lda,
+                          const void *d_B, int ldb, void *d_C, int ldc, int accumulate,
+                          void *d_colsum, int colsum_accumulate) {
+    Args a{};
+    a.A = static_cast<const uint16_t *>(d_A);
+    a.B = static_cast<const uint16_t *>(d_B);
+    a.C = static_cast<uint16_t *>(d_C);
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.lda = lda;
+    a.ldb = ldb;
+    a.ldc = ldc;
+    a.act = FG_ACT_NONE;
+    a.mode = 0;
+    a.accumulate = accumulate ? 1 : 0;
+    a.colsum = static_cast<uint16_t *>(d_colsum);
+    a.colsum_accumulate = colsum_accumulate ? 1 : 0;
+    return gemm16_common(ctx, dtype, FG_TN, a, "fg_gemm_dw_x16");
 }
 
 FG_API int fg_gemm_bwd_x16(fg_ctx *ctx, int dtype, int layout, int M, int N, int K,

@@ -167,6 +167,18 @@ int fg_gemm_dw_f32(fg_ctx *ctx, int M, int N, int K, const float *d_A, int lda,
                    const float *d_B, int ldb, float *d_C, int ldc, int accumulate,
                    float *d_colsum, int colsum_accumulate);
 
+/* The same for 16-bit tensors (dtype FG_DTYPE_F16 / FG_DTYPE_BF16 for every
+ * operand, colsum included): C as fg_gemm_x16 in the TN layout; colsum[n]
+ * (=|+=) sum_k B[k][n] summed in fp32 and rounded to dtype once (with
+ * colsum_accumulate: round(colsum + sum)). Shapes off the direct-to-LDS
+ * path (K not a multiple of the tile depth, unaligned rows) take the GEMM
+ * plus fg_bias_grad's reduction: the same values up to the order of the
+ * fp32 sums. Replaces the 16-bit dB lowering (matmul/mod.rs:85-94) and the
+ * bias add's backward, which the reference lacks (binary.rs:53-63). */
+int fg_gemm_dw_x16(fg_ctx *ctx, int dtype, int M, int N, int K, const void *d_A, int lda,
+                   const void *d_B, int ldb, void *d_C, int ldc, int accumulate,
+                   void *d_colsum, int colsum_accumulate);
+
 /* dbias[j] (=|+=) sum_i dZ[i][j]: the bias-add's backward (new broadcast
  * op; reference binary.rs:53-63 has none). Deterministic order. */
 int fg_bias_grad_f32(fg_ctx *ctx, int M, int N, const float *d_dZ, int ld,

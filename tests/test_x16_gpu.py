@@ -321,6 +321,42 @@ def test_bias_grad_x16_exact(gpu_ctx, dtype, shape):
     assert np.array_equal(host16(out), want)
 
 
+@pytest.mark.parametrize("dtype", [F16, BF16], ids=lambda d: DT_IDS[d])
+@pytest.mark.parametrize("shape", [(4096, 4096, 64), (1024, 4096, 192), (4000, 1000, 128),
+                                   (1024, 1024, 32), (512, 512, 96), (37, 29, 300),
+                                   (64, 10, 256), (0, 64, 128), (64, 64, 0)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_gemm_dw_x16_fused_bias_grad(gpu_ctx, dtype, shape):
+    """dW = A^T.dZ and dbias = column sums of dZ in one call (TN layout): on
+    k/4 operands every fp32 sum is exact in any order, so both 16-bit results
+    equal the oracle's bit for bit, with and without accumulation.  The
+    shapes take the direct-to-LDS kernels that sum the columns in the GEMM
+    (8-wave 256x256 and 256x128 tiles at BK 64 with edge tiles, 4-wave
+    128x128 at BK 32) and the fallback of GEMM + separate reduction (K off
+    the tile depth, unaligned, N = 10, no rows, K = 0)."""
+    M, N, K = shape  # dW is M x N; the reduction runs over K rows
+    note(f"gemm_dw_x16 {DT_IDS[dtype]} M={M} N={N} K={K}")
+    rng = np.random.default_rng(7 + M + 3 * N + K)
+    A, dZ = quarter_ints(rng, (K, M), dtype), quarter_ints(rng, (K, N), dtype)
+    exact = O.to_f32(dtype, dZ).astype(np.float64).sum(axis=0)
+    # Device operands are never empty (K = 0 reads nothing from them).
+    dA = dev16(A if K > 0 else quarter_ints(rng, (1, max(M, 1)), dtype))
+    ddZ = dev16(dZ if K > 0 else quarter_ints(rng, (1, N), dtype))
+    C, db = empty16((max(M, 1), N)), empty16((N,))
+    gpu_ctx.gemm_dw_x16(dtype, M, N, K, dA, max(M, 1), ddZ, N, C, N, colsum=db)
+    assert np.array_equal(host16(db), O.from_f32(dtype, exact.astype(np.float32)))
+    if M > 0:
+        assert np.array_equal(host16(C), O.gemm_x16(dtype, O.TN, A, dZ))
+    C0, old = quarter_ints(rng, (max(M, 1), N), dtype), quarter_ints(rng, (N,), dtype)
+    C, db = dev16(C0), dev16(old)
+    gpu_ctx.gemm_dw_x16(dtype, M, N, K, dA, max(M, 1), ddZ, N, C, N,
+                        accumulate=True, colsum=db, colsum_accumulate=True)
+    want = O.from_f32(dtype, (exact + O.to_f32(dtype, old)).astype(np.float32))
+    assert np.array_equal(host16(db), want)
+    if M > 0:
+        assert np.array_equal(host16(C), O.gemm_x16(dtype, O.TN, A, dZ, C=C0))
+
+
 # ------------------------------------------------------------ optimisers
 @pytest.mark.parametrize("dtype", [F16, BF16], ids=lambda d: DT_IDS[d])
 def test_sgd_adam_x16_bit_exact(gpu_ctx, dtype):
