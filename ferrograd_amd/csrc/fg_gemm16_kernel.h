@@ -206,11 +206,61 @@ __device__ __forceinline__ float epi16(const Args &p, float v, const uint16_t *b
     return v;
 }
 
+// Four consecutive outputs of one row (the vector path of the epilogue):
+// the same operation sequence as epi16 per element, with the uniform
+// choices (mode, activation, bias, accumulate) taken once per four.
+template <bool BF>
+__device__ __forceinline__ void epi16_x4(const Args &p, f32x4 v, f32x4 bv, int row, int col) {
+    using E = T16<BF>;
+    auto rnd = [](f32x4 x) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) x[t] = E::to_f(E::from_f(x[t]));
+        return x;
+    };
+    auto ld4 = [](const uint16_t *q) {
+        const u32x2 w = *reinterpret_cast<const u32x2 *>(q);
+        return f32x4{E::to_f((uint16_t)w[0]), E::to_f((uint16_t)(w[0] >> 16)),
+                     E::to_f((uint16_t)w[1]), E::to_f((uint16_t)(w[1] >> 16))};
+    };
+    auto st4 = [](uint16_t *q, f32x4 x) {
+        *reinterpret_cast<u32x2 *>(q) = u32x2{pack2(E::from_f(x[0]), E::from_f(x[1])),
+                                              pack2(E::from_f(x[2]), E::from_f(x[3]))};
+    };
+    v = rnd(v);
+    if (p.mode == 0) {
+        if (p.bias) v = rnd(v + bv);
+        if (p.Z) st4(p.Z + (size_t)row * p.ldz + col, v);
+        if (p.act != kActNone) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) v[t] = act_fwd(p.act, v[t]);
+            v = rnd(v);
+        }
+    } else if (p.act != kActNone) {
+        const f32x4 z = ld4(p.Zs + (size_t)row * p.ldzs + col);
+        if (p.act == kActRelu) {
+            // ReLU' masks (a select: +0 where z <= 0).
+#pragma unroll
+            for (int t = 0; t < 4; ++t) v[t] = z[t] > 0.0f ? v[t] : 0.0f;
+        } else {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) v[t] = v[t] * act_grad(p.act, z[t]);
+            v = rnd(v);
+        }
+    }
+    uint16_t *c = p.C + (size_t)row * p.ldc + col;
+    if (p.accumulate) v += ld4(c);
+    st4(c, v);
+}
+
 // Epilogue shared by the 16-bit kernels.  Accumulator register r of lane
 // (h, l32) in block (i, j) holds C[r0 + 32i + 8(r/4) + 4h + r%4][c0 + 32j + l32];
 // each wave stages one 32 x WTN slice of fp32 sums in LDS (stride WTN+4)
-// and writes four outputs (8 bytes) per lane.  lds must hold
-// NW * 32 * (WTN + 4) floats and be free.
+// and writes four outputs (8 bytes) per lane.  A lane keeps the same four
+// columns through the slice (its bias is loaded once) and reads the next
+// row group from LDS while it processes the current one.  Each CU runs the
+// epilogue once per launch, so its code is fetched cold: the uniform
+// choices sit outside the per-element arithmetic and the row loop stays
+// rolled.  lds must hold NW * 32 * (WTN + 4) floats and be free.
 template <bool BF, int TM, int TN, int WTN, int NW>
 __device__ __forceinline__ void store_tile16(const Args &p, const f32x16 (&acc)[TM][TN],
                                              float *lds, int r0, int c0, int wave, int lane) {
@@ -218,7 +268,19 @@ __device__ __forceinline__ void store_tile16(const Args &p, const f32x16 (&acc)[
     constexpr int kStageLd = WTN + 4;
     const int l32 = lane & 31, h = lane >> 5;
     float *stage = lds + wave * (32 * kStageLd);
-    constexpr int G4 = WTN / 4;  // groups of 4 columns per slice row
+    constexpr int G4 = WTN / 4;    // groups of 4 columns per slice row
+    constexpr int RPP = 64 / G4;   // slice rows per pass of the wave
+    constexpr int NP = 32 / RPP;   // passes per slice
+    static_assert(64 % G4 == 0 && 32 % RPP == 0, "epilogue lane mapping");
+    const int c4 = (lane % G4) * 4, rr0 = lane / G4;
+    const int col = c0 + c4;
+    const bool vec = p.vec_out && col + 4 <= p.N;
+    f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+    if (p.mode == 0 && p.bias && vec) {
+        const u32x2 w = *reinterpret_cast<const u32x2 *>(p.bias + col);
+        bv = f32x4{E::to_f((uint16_t)w[0]), E::to_f((uint16_t)(w[0] >> 16)),
+                   E::to_f((uint16_t)w[1]), E::to_f((uint16_t)(w[1] >> 16))};
+    }
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -227,30 +289,20 @@ __device__ __forceinline__ void store_tile16(const Args &p, const f32x16 (&acc)[
             for (int r = 0; r < 16; ++r)
                 stage[((r >> 2) * 8 + h * 4 + (r & 3)) * kStageLd + j * 32 + l32] = acc[i][j][r];
         __syncthreads();
-        for (int e = lane; e < 32 * G4; e += 64) {
-            const int rr = e / G4, c4 = (e % G4) * 4;
-            const int row = r0 + i * 32 + rr;
-            const int col = c0 + c4;
+        f32x4 nxt = *reinterpret_cast<const f32x4 *>(stage + rr0 * kStageLd + c4);
+#pragma unroll 1
+        for (int q = 0; q < NP; ++q) {
+            const f32x4 v = nxt;
+            if (q + 1 < NP)
+                nxt = *reinterpret_cast<const f32x4 *>(stage + (rr0 + (q + 1) * RPP) * kStageLd + c4);
+            const int row = r0 + i * 32 + rr0 + q * RPP;
             if (row >= p.M || col >= p.N) continue;
-            const f32x4 v = *reinterpret_cast<const f32x4 *>(stage + rr * kStageLd + c4);
-            uint16_t *crow = p.C + (size_t)row * p.ldc;
-            const uint16_t *bias = p.mode == 0 ? p.bias : nullptr;
-            if (p.vec_out && col + 4 <= p.N) {
-                uint16_t o[4], z[4];
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    float zt;
-                    float ot = epi16<BF>(p, v[t], bias, row, col + t, &zt);
-                    z[t] = E::from_f(zt);
-                    if (p.accumulate) ot += E::to_f(crow[col + t]);
-                    o[t] = E::from_f(ot);
-                }
-                if (p.mode == 0 && p.Z)
-                    *reinterpret_cast<u32x2 *>(p.Z + (size_t)row * p.ldz + col) =
-                        u32x2{pack2(z[0], z[1]), pack2(z[2], z[3])};
-                *reinterpret_cast<u32x2 *>(crow + col) =
-                    u32x2{pack2(o[0], o[1]), pack2(o[2], o[3])};
+            if (vec) {
+                epi16_x4<BF>(p, v, bv, row, col);
             } else {
+                uint16_t *crow = p.C + (size_t)row * p.ldc;
+                const uint16_t *bias = p.mode == 0 ? p.bias : nullptr;
+#pragma unroll 1
                 for (int t = 0; t < 4 && col + t < p.N; ++t) {
                     float zt;
                     float ot = epi16<BF>(p, v[t], bias, row, col + t, &zt);

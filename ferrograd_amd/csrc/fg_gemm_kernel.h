@@ -237,20 +237,54 @@ __device__ __forceinline__ float epi_value(const GemmArgs &p, float v, float bv,
     return v;
 }
 
+// Four consecutive outputs of one row (the vector path of the epilogue):
+// the same operations as epi_value per element, with the uniform choices
+// (mode, activation, Z, accumulate) taken once per four.
+__device__ __forceinline__ void epi_x4(const GemmArgs &p, f32x4 v, f32x4 bv, int row, int col) {
+    if (p.mode == 0) {
+        v += bv;
+        if (p.Z) *reinterpret_cast<f32x4 *>(p.Z + (size_t)row * p.ldz + col) = v;
+        if (p.act != kActNone) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) v[t] = act_fwd(p.act, v[t]);
+        }
+    } else if (p.act != kActNone) {
+        const f32x4 z = *reinterpret_cast<const f32x4 *>(p.Zs + (size_t)row * p.ldzs + col);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) v[t] *= act_grad(p.act, z[t]);
+    }
+    float *c = p.C + (size_t)row * p.ldc + col;
+    if (p.accumulate) v += *reinterpret_cast<const f32x4 *>(c);
+    *reinterpret_cast<f32x4 *>(c) = v;
+}
+
 // Epilogue shared by the GEMM kernels.  Accumulator register r of lane
 // (h, l32) in block (i, j) holds C[r0 + 32i + 8(r/4) + 4h + r%4][c0 + 32j + l32]
 // (r0, c0: the wave's first row and column).  Each wave writes one
 // 32 x WTN slice to its LDS stage (stride WTN+4 floats), then reads it back
 // as float4 rows and applies bias / activation / activation-derivative with
-// 16-byte global accesses.  lds must hold NW * 32 * (WTN + 4) floats and be
-// free (every wave past its last read of the operand tiles).
+// 16-byte global accesses.  A lane keeps the same four columns through the
+// slice (its bias is loaded once) and reads the next row group from LDS
+// while it processes the current one.  Each CU runs the epilogue once per
+// launch, so its code is fetched cold: the uniform choices sit outside the
+// per-element arithmetic and the row loop stays rolled.  lds must hold
+// NW * 32 * (WTN + 4) floats and be free (every wave past its last read of
+// the operand tiles).
 template <int TM, int TN, int WTN, int NW>
 __device__ __forceinline__ void store_tile(const GemmArgs &p, const f32x16 (&acc)[TM][TN],
                                            float *lds, int r0, int c0, int wave, int lane) {
     constexpr int kStageLd = WTN + 4;
     const int l32 = lane & 31, h = lane >> 5;
     float *stage = lds + wave * (32 * kStageLd);
-    constexpr int F4 = WTN / 4;  // float4 per slice row
+    constexpr int F4 = WTN / 4;   // float4 per slice row
+    constexpr int RPP = 64 / F4;  // slice rows per pass of the wave
+    constexpr int NP = 32 / RPP;  // passes per slice
+    static_assert(64 % F4 == 0 && 32 % RPP == 0, "epilogue lane mapping");
+    const int c4 = (lane % F4) * 4, rr0 = lane / F4;
+    const int col = c0 + c4;
+    const bool vec = p.vec_out && col + 4 <= p.N;
+    f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+    if (p.mode == 0 && p.bias && vec) bv = *reinterpret_cast<const f32x4 *>(p.bias + col);
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -259,32 +293,23 @@ __device__ __forceinline__ void store_tile(const GemmArgs &p, const f32x16 (&acc
             for (int r = 0; r < 16; ++r)
                 stage[((r >> 2) * 8 + h * 4 + (r & 3)) * kStageLd + j * 32 + l32] = acc[i][j][r];
         __syncthreads();
-        for (int e = lane; e < 32 * F4; e += 64) {
-            const int rr = e / F4, c4 = (e % F4) * 4;
-            const int row = r0 + i * 32 + rr;
-            const int col = c0 + c4;
+        f32x4 nxt = *reinterpret_cast<const f32x4 *>(stage + rr0 * kStageLd + c4);
+#pragma unroll 1
+        for (int q = 0; q < NP; ++q) {
+            const f32x4 v = nxt;
+            if (q + 1 < NP)
+                nxt = *reinterpret_cast<const f32x4 *>(stage + (rr0 + (q + 1) * RPP) * kStageLd + c4);
+            const int row = r0 + i * 32 + rr0 + q * RPP;
             if (row >= p.M || col >= p.N) continue;
-            const f32x4 v = *reinterpret_cast<const f32x4 *>(stage + rr * kStageLd + c4);
-            float *crow = p.C + (size_t)row * p.ldc;
-            if (p.vec_out && col + 4 <= p.N) {
-                f32x4 bv = {0.f, 0.f, 0.f, 0.f};
-                if (p.mode == 0 && p.bias) bv = *reinterpret_cast<const f32x4 *>(p.bias + col);
-                f32x4 o, z;
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    float zt;
-                    o[t] = epi_value(p, v[t], bv[t], row, col + t, &zt);
-                    z[t] = zt;
-                }
-                if (p.mode == 0 && p.Z)
-                    *reinterpret_cast<f32x4 *>(p.Z + (size_t)row * p.ldz + col) = z;
-                if (p.accumulate) o += *reinterpret_cast<const f32x4 *>(crow + col);
-                *reinterpret_cast<f32x4 *>(crow + col) = o;
+            if (vec) {
+                epi_x4(p, v, bv, row, col);
             } else {
+                float *crow = p.C + (size_t)row * p.ldc;
+#pragma unroll 1
                 for (int t = 0; t < 4 && col + t < p.N; ++t) {
-                    const float bv = (p.mode == 0 && p.bias) ? p.bias[col + t] : 0.0f;
+                    const float b = (p.mode == 0 && p.bias) ? p.bias[col + t] : 0.0f;
                     float z;
-                    float o = epi_value(p, v[t], bv, row, col + t, &z);
+                    float o = epi_value(p, v[t], b, row, col + t, &z);
                     if (p.mode == 0 && p.Z) p.Z[(size_t)row * p.ldz + col + t] = z;
                     if (p.accumulate) o += crow[col + t];
                     crow[col + t] = o;
