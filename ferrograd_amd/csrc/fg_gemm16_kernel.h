@@ -30,6 +30,7 @@
 
 #include "fg_act.h"
 #include "fg_half.h"
+#include "fg_sched.h"
 
 namespace fg {
 namespace gemm16 {
@@ -423,12 +424,6 @@ __device__ __forceinline__ int swz16_k(int row) {
 }
 __device__ __forceinline__ int swz16_r(int k) { return 4 * (k & 3); }
 
-template <int N>
-__device__ __forceinline__ void wait_vmcnt16() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-
 // 8 consecutive k (k0 .. k0+7, k0 a multiple of 8) of row `row` of a
 // row-contiguous [BK][R] tile, as one MFMA operand: two transposing reads.
 template <int R>
@@ -494,19 +489,6 @@ struct ColSum16 {
         __syncthreads();
     }
 };
-
-// Scheduling groups for one k16 step: MFMA q (of NM) followed by its share
-// (PER) of the NR LDS reads of the next step.
-template <int Q, int NM, int NR, int PER>
-__device__ __forceinline__ void sched_interleave() {
-    if constexpr (Q < NM) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-        constexpr int left = NR - Q * PER;
-        if constexpr (left > 0)
-            __builtin_amdgcn_sched_group_barrier(0x100, left < PER ? left : PER, 0);  // LDS reads
-        sched_interleave<Q + 1, NM, NR, PER>();
-    }
-}
 
 template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC, bool BF>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm16_dma(Args p) {
@@ -623,13 +605,13 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm16_dma(Args p) {
     // At most `n` tiles' loads of this wave may still be outstanding.
     auto wait_tiles = [&](int n) {
         if (n <= 0)
-            wait_vmcnt16<0>();
+            wait_vmcnt<0>();
         else if (n == 1)
-            wait_vmcnt16<kLoads>();
+            wait_vmcnt<kLoads>();
         else if (n == 2)
-            wait_vmcnt16<2 * kLoads>();
+            wait_vmcnt<2 * kLoads>();
         else
-            wait_vmcnt16<3 * kLoads>();
+            wait_vmcnt<3 * kLoads>();
     };
 #pragma unroll
     for (int t = 0; t < kStages; ++t)
@@ -670,7 +652,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm16_dma(Args p) {
             if (do_cs) cs.add(Bs);
         // ca / cb: the last step of tile kt.  Every wave's reads of tile kt
         // must be done before the barrier (its stage is refilled after it).
-        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        wait_lgkm0();
         wait_tiles(min(kt + kStages - 1, nk - 1) - (kt + 1));
         __builtin_amdgcn_sched_barrier(0);
         asm volatile("s_barrier" ::: "memory");

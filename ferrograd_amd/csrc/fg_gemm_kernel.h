@@ -41,6 +41,7 @@
 #include <hip/hip_runtime.h>
 
 #include "fg_act.h"
+#include "fg_sched.h"
 
 namespace fg {
 namespace gemm {
@@ -450,13 +451,6 @@ __device__ __forceinline__ int swz_k(int row) {
 }
 __device__ __forceinline__ int swz_r(int k) { return ((k >> 3) & 1) * 8; }
 
-// s_waitcnt with vmcnt <= N and no wait on the other counters.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-
 template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_dma(GemmArgs p) {
     constexpr int NW = WGM * WGN;
@@ -471,7 +465,6 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_dma(GemmArgs p) {
     // Three stages (two tiles in flight) when they fit in the 160 KiB of
     // LDS, else two.
     constexpr int kStages = 3 * kStageSz * 4 <= 160 * 1024 ? 3 : 2;
-    constexpr int kAhead = kStages - 1;
     constexpr int kEpi = NW * 32 * (WTN + 4);
     constexpr int kLds = (kStages * kStageSz > kEpi) ? kStages * kStageSz : kEpi;
     __shared__ __attribute__((aligned(16))) float lds[kLds];
@@ -506,26 +499,29 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_dma(GemmArgs p) {
         const int c = pc ^ swz_r(k);
         return base + (size_t)(k0 + k) * ld + min(r0 + 4 * c, rmax - 4);
     };
-    auto issue = [&](int kt, int stage) {
+    // Wave load q (0 .. kLoads-1) of tile kt into stage `stage`: this wave's
+    // share of A first, then of B.
+    auto issue_one = [&](int kt, int stage, int q) {
         float *sa = lds + stage * kStageSz;
         float *sb = sa + kASz;
         const int k0 = kt * BK;
-#pragma unroll
-        for (int i = 0; i < kPerA; ++i) {
-            const int li = wave * kPerA + i;
+        if (q < kPerA) {
+            const int li = wave * kPerA + q;
             const int pos = li * 64 + lane;
             const float *src = AK ? src_kc(p.A, p.lda, m0, p.M, k0, pos)
                                   : src_rc(p.A, p.lda, m0, p.M, k0, pos, BM);
             __builtin_amdgcn_global_load_lds(src, sa + li * 256, 16, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < kPerB; ++i) {
-            const int li = wave * kPerB + i;
+        } else {
+            const int li = wave * kPerB + (q - kPerA);
             const int pos = li * 64 + lane;
             const float *src = BNC ? src_rc(p.B, p.ldb, n0, p.N, k0, pos, BN)
                                    : src_kc(p.B, p.ldb, n0, p.N, k0, pos);
             __builtin_amdgcn_global_load_lds(src, sb + li * 256, 16, 0, 0);
         }
+    };
+    auto issue = [&](int kt, int stage) {
+#pragma unroll
+        for (int q = 0; q < kLoads; ++q) issue_one(kt, stage, q);
     };
 
     const int nk = p.K / BK;
@@ -536,46 +532,48 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_dma(GemmArgs p) {
     // Fragments of 4-k group g (of BK / 8) of a stage: lane half h holds k
     // 8h .. 8h+3 of the group's 16-k block, so the 4 MFMA steps of the
     // group cover all 16 k across both halves.
-    auto frag = [&](const float *As, const float *Bs, int g, f32x4 (&a)[TM], f32x4 (&b)[TN]) {
-        const int kb = (g >> 1) * 16 + 8 * h + 4 * (g & 1);
+    auto k_of = [&](int g) { return (g >> 1) * 16 + 8 * h + 4 * (g & 1); };
+    auto frag_a = [&](const float *As, int g, int i) {
+        const int kb = k_of(g), row = wm0 + i * 32 + l32;
+        f32x4 a;
+        if constexpr (AK) {
+            const int c = (kb >> 2) ^ swz_k<BK>(row);
+            a = *reinterpret_cast<const f32x4 *>(As + row * BK + 4 * c);
+        } else {
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
-            const int row = wm0 + i * 32 + l32;
-            if constexpr (AK) {
-                const int c = (kb >> 2) ^ swz_k<BK>(row);
-                a[i] = *reinterpret_cast<const f32x4 *>(As + row * BK + 4 * c);
-            } else {
-#pragma unroll
-                for (int s = 0; s < 4; ++s) {
-                    const int k = kb + s;
-                    a[i][s] = As[k * BM + ((((row >> 2) ^ swz_r(k)) << 2) | (row & 3))];
-                }
+            for (int s = 0; s < 4; ++s) {
+                const int k = kb + s;
+                a[s] = As[k * BM + ((((row >> 2) ^ swz_r(k)) << 2) | (row & 3))];
             }
         }
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const int col = wn0 + j * 32 + l32;
-            if constexpr (BNC) {
-#pragma unroll
-                for (int s = 0; s < 4; ++s) {
-                    const int k = kb + s;
-                    b[j][s] = Bs[k * BN + ((((col >> 2) ^ swz_r(k)) << 2) | (col & 3))];
-                }
-            } else {
-                const int c = (kb >> 2) ^ swz_k<BK>(col);
-                b[j] = *reinterpret_cast<const f32x4 *>(Bs + col * BK + 4 * c);
-            }
-        }
+        return a;
     };
-    auto mfma_g = [&](const f32x4 (&a)[TM], const f32x4 (&b)[TN]) {
+    auto frag_b = [&](const float *Bs, int g, int j) {
+        const int kb = k_of(g), col = wn0 + j * 32 + l32;
+        f32x4 b;
+        if constexpr (BNC) {
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
+            for (int s = 0; s < 4; ++s) {
+                const int k = kb + s;
+                b[s] = Bs[k * BN + ((((col >> 2) ^ swz_r(k)) << 2) | (col & 3))];
+            }
+        } else {
+            const int c = (kb >> 2) ^ swz_k<BK>(col);
+            b = *reinterpret_cast<const f32x4 *>(Bs + col * BK + 4 * c);
+        }
+        return b;
+    };
+    auto frag = [&](const float *As, const float *Bs, int g, f32x4 (&a)[TM], f32x4 (&b)[TN]) {
 #pragma unroll
-            for (int i = 0; i < TM; ++i)
+        for (int i = 0; i < TM; ++i) a[i] = frag_a(As, g, i);
 #pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], b[j][s], acc[i][j],
-                                                                     0, 0, 0);
+        for (int j = 0; j < TN; ++j) b[j] = frag_b(Bs, g, j);
+    };
+    // MFMA m (of 4 TM TN) of a group: k step m / (TM TN), then i, then j,
+    // so consecutive MFMAs update different accumulators.
+    auto mfma_one = [&](const f32x4 (&a)[TM], const f32x4 (&b)[TN], int m) {
+        const int s = m / (TM * TN), i = (m / TN) % TM, j = m % TN;
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], b[j][s], acc[i][j], 0, 0, 0);
     };
     auto colsum_add = [&](const float *Bs) {
         if constexpr (kTN)
@@ -586,30 +584,91 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_dma(GemmArgs p) {
     };
     constexpr int NG = BK / 8;
 
+    // Barrier-overlapped loop: the last 8-k group of tile kt is read into
+    // registers before the barrier that ends tile kt and multiplied after
+    // it, so the matrix units stay busy across the barrier while the first
+    // operands of tile kt+1 are read.  Tile t lives in stage t % kStages.
+    // The prologue issues tiles 0 .. kAhead-1; iteration kt issues tile
+    // kt + kAhead into the stage of tile kt-1, which every wave finished
+    // reading before the barrier that ended tile kt-1.  Past the last tile
+    // an iteration reloads tile nk-1 into that free stage, which nothing
+    // reads again: the loop body has no branch, so its loads are scheduled
+    // among the MFMAs of its first group, and every iteration leaves the
+    // same kAhead tiles in flight.
+    constexpr int kAhead = kStages - 1;
+    // Each group runs its MFMAs in a fixed order: after MFMA m, the reads of
+    // fragment m of the next group (A fragments, then B) and, in the first
+    // group of a tile, one of the tile's loads every kStride MFMAs.  Reads
+    // or loads issued in a burst fill the wave's memory queues and hold up
+    // the MFMAs behind them, which no other wave hides when a SIMD runs one
+    // (measured: issuing the reads first, or the loads on consecutive MFMAs,
+    // costs up to 10 % on the 4-wave tiles).
+    constexpr int kMfma = 4 * TM * TN;
+    static_assert(kLoads >= 1 && kLoads <= kMfma, "at most one load per MFMA");
+    constexpr int kStride = kMfma / kLoads;
+    auto run_group = [&](const f32x4 (&ca)[TM], const f32x4 (&cb)[TN], const float *An,
+                         const float *Bn, int gn, f32x4 (&na)[TM], f32x4 (&nb)[TN], bool loads,
+                         int kl, int sl) {
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int t = 0; t < kAhead; ++t)
-        if (t < nk) issue(t, t);
-    for (int kt = 0; kt < nk; ++kt) {
-        // This wave's loads of tile kt are done once at most those of the
-        // tiles after it (kAhead - 1 of them, fewer at the end) are
-        // outstanding; the barrier then publishes every wave's.
-        if (kAhead == 2 && kt + 1 < nk)
-            wait_vmcnt<(kAhead - 1) * kLoads>();
-        else
-            wait_vmcnt<0>();
-        asm volatile("s_barrier" ::: "memory");
-        // Stage (kt + kAhead) % kStages was last read while multiplying
-        // tile kt-1, which every wave finished before the barrier.
-        if (kt + kAhead < nk) issue(kt + kAhead, (kt + kAhead) % kStages);
-        const float *As = lds + (kt % kStages) * kStageSz;
-        const float *Bs = As + kASz;
-#pragma unroll
-        for (int g = 0; g < NG; ++g) {
-            f32x4 a[TM], b[TN];
-            frag(As, Bs, g, a, b);
-            mfma_g(a, b);
+        for (int m = 0; m < kMfma; ++m) {
+            mfma_one(ca, cb, m);
+            if (m < TM)
+                na[m] = frag_a(An, gn, m);
+            else if (m < TM + TN)
+                nb[m - TM] = frag_b(Bn, gn, m - TM);
+            if (loads && m % kStride == 0 && m / kStride < kLoads) issue_one(kl, sl, m / kStride);
+            __builtin_amdgcn_sched_barrier(0);
         }
-        colsum_add(Bs);
+    };
+    if (nk > 0) {
+#pragma unroll
+        for (int t = 0; t < kAhead; ++t) issue(min(t, nk - 1), t);
+        wait_vmcnt<(kAhead - 1) * kLoads>();  // tile 0 landed
+        asm volatile("s_barrier" ::: "memory");
+        // Operands double-buffered in registers: the LDS reads of group g+1
+        // are issued among the MFMAs of group g, so the matrix units never
+        // wait for the reads of the group they are about to run.  ca / cb
+        // hold the operands of the next group to multiply.
+        f32x4 ca[TM], cb[TN];
+        frag(lds, lds + kASz, 0, ca, cb);
+        for (int kt = 0; kt < nk; ++kt) {
+            const float *As = lds + (kt % kStages) * kStageSz;
+            const float *Bs = As + kASz;
+            const int kl = min(kt + kAhead, nk - 1), sl = (kt + kAhead) % kStages;
+#pragma unroll
+            for (int g = 0; g < NG - 1; ++g) {
+                // Group g's operands (read during the previous group) have
+                // landed; waiting here, before the next group's reads are
+                // issued, leaves those in flight behind the MFMAs.
+                wait_lgkm0();
+                f32x4 na[TM], nb[TN];
+                run_group(ca, cb, As, Bs, g + 1, na, nb, g == 0, kl, sl);
+#pragma unroll
+                for (int i = 0; i < TM; ++i) ca[i] = na[i];
+#pragma unroll
+                for (int j = 0; j < TN; ++j) cb[j] = nb[j];
+            }
+            colsum_add(Bs);
+            // ca / cb: the last group of tile kt.  Every wave's reads of tile
+            // kt are done before the barrier (its stage is refilled after
+            // it), and so are this wave's loads of tile kt+1 (the newest
+            // kAhead-1 tiles may still be in flight).
+            wait_lgkm0();
+            wait_vmcnt<(kAhead - 1) * kLoads>();
+            __builtin_amdgcn_sched_barrier(0);
+            asm volatile("s_barrier" ::: "memory");
+            // Group 0 of tile kt+1 (past the last tile: a stage nothing
+            // uses, read and discarded).
+            f32x4 na[TM], nb[TN];
+            const float *An = lds + ((kt + 1) % kStages) * kStageSz;
+            run_group(ca, cb, An, An + kASz, 0, na, nb, false, 0, 0);
+#pragma unroll
+            for (int i = 0; i < TM; ++i) ca[i] = na[i];
+#pragma unroll
+            for (int j = 0; j < TN; ++j) cb[j] = nb[j];
+        }
+        wait_vmcnt<0>();  // the reloads past the last tile, before the LDS reuse
     }
     __syncthreads();  // every wave past its last tile read before the stage reuse
     if constexpr (kTN)
