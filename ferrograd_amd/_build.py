@@ -88,7 +88,10 @@ def build(verbose: bool = True, lib: str = LIB, obj_dir: str = OBJ, defines=()) 
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
         objs = list(ex.map(lambda s: _compile(s, obj_dir, defines), SOURCES))
     tmp = lib + ".tmp"
-    cmd = [HIPCC, "-shared", f"--offload-arch={ARCH}", "-fPIC", "-o", tmp, *objs, "-lpthread"]
+    # -z defs: an undefined symbol (e.g. a kernel launch stub that a
+    # compilation pass failed to emit) fails the link, not the first load.
+    cmd = [HIPCC, "-shared", f"--offload-arch={ARCH}", "-fPIC", "-Wl,-z,defs", "-o", tmp, *objs,
+           "-lpthread"]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{res.stdout}\n{res.stderr}")

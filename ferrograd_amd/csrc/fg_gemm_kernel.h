@@ -13,11 +13,12 @@
 //    C held in TM*TN 16-register MFMA accumulators (up to 256 registers,
 //    which the compiler places in AGPRs).
 //  * K is consumed in BK-deep tiles (16 or 32) staged through LDS.  Where
-//    whole K tiles and 16-byte alignment allow, gemm_f32_dma moves them
-//    straight from global memory into a three-stage LDS ring (two tiles in
-//    flight, swizzled unpadded layout); otherwise gemm_f32_mfma stages them
-//    through registers into double-buffered LDS (the loads of tile t+1 in
-//    flight during the MFMAs of tile t).  One barrier per tile either way.
+//    whole K tiles and 16-byte alignment allow, gemm_f32_pipe runs a
+//    software pipeline over them (loads two tiles ahead, fragments
+//    double-buffered in registers, a fixed MFMA / LDS-read / load order,
+//    swizzled unpadded layout); otherwise gemm_f32_mfma stages them through
+//    registers into double-buffered LDS (the loads of tile t+1 in flight
+//    during the MFMAs of tile t).  One barrier per tile either way.
 //  * No operand is transposed on its way to LDS.  A k-contiguous operand is
 //    kept [row][k] (row stride BK+4 floats, conflict-free 16-byte reads) and
 //    a row-contiguous one [k][row] (stride rows+4).  The MFMA's k index is
@@ -58,13 +59,13 @@ constexpr int kThreads = 256;
 #endif
 constexpr int kBK = FG_GEMM_BK;
 
-// Direct-to-LDS operand loads (gemm_f32_dma) where the shapes allow; 0
-// keeps every call on the register-staged kernel.  A compile-time knob for
-// measurement builds.
-#ifndef FG_GEMM_DMA
-#define FG_GEMM_DMA 1
+// The pipelined whole-tile kernel (gemm_f32_pipe) where the shapes allow; 0
+// keeps every call on gemm_f32_mfma.  A compile-time knob for measurement
+// builds.
+#ifndef FG_GEMM_PIPE
+#define FG_GEMM_PIPE 1
 #endif
-constexpr bool kDma = FG_GEMM_DMA != 0;
+constexpr bool kPipe = FG_GEMM_PIPE != 0;
 
 
 struct GemmArgs {
@@ -427,18 +428,27 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_mfma(GemmArgs p) {
 }
 
 // ------------------------------------------------ direct-to-LDS variant
-// The same GEMM with the operand tiles moved from global memory straight
-// into LDS (global_load_lds_dwordx4: each lane's 16 bytes land at the wave's
-// LDS base + 16 * lane), a three-stage LDS ring with the loads of tile t+2
-// in flight while tile t is multiplied (two stages and tile t+1 where three
-// do not fit), and one barrier per tile.  Used when
-// every 16-byte chunk of a tile is either in bounds or belongs only to
-// outputs that are masked: K % BK == 0 and the VEC alignment conditions.
-// Rows (or columns) past the matrix edge are clamped to the last valid one,
-// so every load reads mapped memory; the values they bring only reach
-// masked outputs.
+// The same GEMM, software-pipelined over whole K tiles: used when every
+// 16-byte chunk of a tile is either in bounds or belongs only to outputs that
+// are masked (K % BK == 0 and the VEC alignment conditions).  Rows (or
+// columns) past the matrix edge are clamped to the last valid one, so every
+// load reads mapped memory; the values they bring only reach masked outputs.
+// Each wave loads its share of a tile as 16 bytes per lane; lane l's chunk of
+// wave load li lands at LDS float offset li * 256 + 4 l of the operand's
+// stage area, and the source address of that chunk is chosen so that the
+// stage ends up in the swizzled layout below.  Two ways to move the chunks:
+//  * staged (every tile but 256x256): global loads into registers, two
+//    register sets alternating by tile parity, written to a two-stage LDS
+//    ring by ds_write_b128 one tile later;
+//  * direct (256x256, whose accumulators leave no room for two register
+//    sets): global_load_lds_dwordx4 straight into a three-stage LDS ring
+//    (two stages where three do not fit).
+// Measured on gfx950 (2048x4096x4096 NN, same inputs): MFMA busy 87.5 % with
+// direct loads for every tile, 90.4 % with staged loads; direct loads cost
+// the same whether they come from HBM or from L2, so it is the asynchronous
+// LDS writes, not memory, that the staged path saves.
 //
-// LDS layout per stage (no padding -- DMA writes whole 1 KiB runs per wave):
+// LDS layout per stage (no padding -- each wave load fills a whole 1 KiB run):
 //  * a k-contiguous operand [rows][BK], 16-byte chunk c of row r stored at
 //    chunk c ^ ((r / (64 / BK)) % (BK / 4)): the 8 rows read together by a
 //    16-byte LDS read then hit distinct banks;
@@ -452,7 +462,7 @@ __device__ __forceinline__ int swz_k(int row) {
 __device__ __forceinline__ int swz_r(int k) { return ((k >> 3) & 1) * 8; }
 
 template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC>
-__global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_dma(GemmArgs p) {
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_pipe(GemmArgs p) {
     constexpr int NW = WGM * WGN;
     constexpr int WTM = BM / WGM, WTN = BN / WGN;
     constexpr int TM = WTM / 32, TN = WTN / 32;
@@ -462,9 +472,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_dma(GemmArgs p) {
     static_assert(kInstA % NW == 0 && kInstB % NW == 0, "loads divide among the waves");
     constexpr int kPerA = kInstA / NW, kPerB = kInstB / NW, kLoads = kPerA + kPerB;
     constexpr int kASz = BM * BK, kBSz = BN * BK, kStageSz = kASz + kBSz;
-    // Three stages (two tiles in flight) when they fit in the 160 KiB of
-    // LDS, else two.
-    constexpr int kStages = 3 * kStageSz * 4 <= 160 * 1024 ? 3 : 2;
+    constexpr bool kStaged = !(BM == 256 && BN == 256);
+    // Staged: two stages.  Direct: three (two tiles in flight) when they fit
+    // in the 160 KiB of LDS, else two.
+    constexpr int kStages = kStaged ? 2 : 3 * kStageSz * 4 <= 160 * 1024 ? 3 : 2;
     constexpr int kEpi = NW * 32 * (WTN + 4);
     constexpr int kLds = (kStages * kStageSz > kEpi) ? kStages * kStageSz : kEpi;
     __shared__ __attribute__((aligned(16))) float lds[kLds];
@@ -499,29 +510,44 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_dma(GemmArgs p) {
         const int c = pc ^ swz_r(k);
         return base + (size_t)(k0 + k) * ld + min(r0 + 4 * c, rmax - 4);
     };
-    // Wave load q (0 .. kLoads-1) of tile kt into stage `stage`: this wave's
-    // share of A first, then of B.
-    auto issue_one = [&](int kt, int stage, int q) {
-        float *sa = lds + stage * kStageSz;
-        float *sb = sa + kASz;
+    // Wave load q (0 .. kLoads-1) of a tile: this wave's share of A first,
+    // then of B.  Source of this lane's chunk, and its place in a stage.
+    auto src_of = [&](int kt, int q) -> const float * {
         const int k0 = kt * BK;
         if (q < kPerA) {
-            const int li = wave * kPerA + q;
-            const int pos = li * 64 + lane;
+            const int pos = (wave * kPerA + q) * 64 + lane;
+            return AK ? src_kc(p.A, p.lda, m0, p.M, k0, pos)
+                      : src_rc(p.A, p.lda, m0, p.M, k0, pos, BM);
+        }
+        const int pos = (wave * kPerB + (q - kPerA)) * 64 + lane;
+        return BNC ? src_rc(p.B, p.ldb, n0, p.N, k0, pos, BN) : src_kc(p.B, p.ldb, n0, p.N, k0, pos);
+    };
+    auto run_of = [&](int stage, int q) -> float * {  // the wave load's 1 KiB run
+        float *sa = lds + stage * kStageSz;
+        return q < kPerA ? sa + (wave * kPerA + q) * 256 : sa + kASz + (wave * kPerB + q - kPerA) * 256;
+    };
+    // (Source and destination are formed here rather than taken from src_of
+    // / run_of: the LDS-load builtin fed from those lambdas' return values
+    // makes the host compilation pass drop the kernel's launch stub without a
+    // diagnostic.)
+    auto issue_direct = [&](int kt, int stage, int q) {
+        float *sa = lds + stage * kStageSz;
+        const int k0 = kt * BK;
+        if (q < kPerA) {
+            const int li = wave * kPerA + q, pos = li * 64 + lane;
             const float *src = AK ? src_kc(p.A, p.lda, m0, p.M, k0, pos)
                                   : src_rc(p.A, p.lda, m0, p.M, k0, pos, BM);
             __builtin_amdgcn_global_load_lds(src, sa + li * 256, 16, 0, 0);
         } else {
-            const int li = wave * kPerB + (q - kPerA);
-            const int pos = li * 64 + lane;
+            const int li = wave * kPerB + (q - kPerA), pos = li * 64 + lane;
             const float *src = BNC ? src_rc(p.B, p.ldb, n0, p.N, k0, pos, BN)
                                    : src_kc(p.B, p.ldb, n0, p.N, k0, pos);
-            __builtin_amdgcn_global_load_lds(src, sb + li * 256, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(src, sa + kASz + li * 256, 16, 0, 0);
         }
     };
-    auto issue = [&](int kt, int stage) {
-#pragma unroll
-        for (int q = 0; q < kLoads; ++q) issue_one(kt, stage, q);
+    auto load_reg = [&](int kt, int q) { return *reinterpret_cast<const f32x4 *>(src_of(kt, q)); };
+    auto store_reg = [&](int stage, int q, const f32x4 &v) {
+        *reinterpret_cast<f32x4 *>(run_of(stage, q) + 4 * lane) = v;
     };
 
     const int nk = p.K / BK;
@@ -595,20 +621,25 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_dma(GemmArgs p) {
     // reads again: the loop body has no branch, so its loads are scheduled
     // among the MFMAs of its first group, and every iteration leaves the
     // same kAhead tiles in flight.
-    constexpr int kAhead = kStages - 1;
     // Each group runs its MFMAs in a fixed order: after MFMA m, the reads of
     // fragment m of the next group (A fragments, then B) and, in the first
-    // group of a tile, one of the tile's loads every kStride MFMAs.  Reads
-    // or loads issued in a burst fill the wave's memory queues and hold up
-    // the MFMAs behind them, which no other wave hides when a SIMD runs one
+    // group of a tile, the tile's memory operations (`mem(m)`).  Reads or
+    // loads issued in a burst fill the wave's memory queues and hold up the
+    // MFMAs behind them, which no other wave hides when a SIMD runs one
     // (measured: issuing the reads first, or the loads on consecutive MFMAs,
     // costs up to 10 % on the 4-wave tiles).
     constexpr int kMfma = 4 * TM * TN;
     static_assert(kLoads >= 1 && kLoads <= kMfma, "at most one load per MFMA");
-    constexpr int kStride = kMfma / kLoads;
+    constexpr int kAhead = kStages - 1;     // direct: tiles in flight
+    constexpr int kStride = kMfma / kLoads;  // direct: MFMAs per load
+    // One group's MFMAs on (ca, cb).  With `ld` (the first group of a tile)
+    // the tile's memory operations go out among them: staged, after MFMA m <
+    // kLoads, register set Rw's chunk m is written to stage `slot` and its
+    // register refilled from tile kl (Rl); direct, every kStride-th MFMA
+    // issues one load of tile kl into stage `slot`.
     auto run_group = [&](const f32x4 (&ca)[TM], const f32x4 (&cb)[TN], const float *An,
-                         const float *Bn, int gn, f32x4 (&na)[TM], f32x4 (&nb)[TN], bool loads,
-                         int kl, int sl) {
+                         const float *Bn, int gn, f32x4 (&na)[TM], f32x4 (&nb)[TN], bool ld,
+                         int kl, int slot, const f32x4 *Rw, f32x4 *Rl) {
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int m = 0; m < kMfma; ++m) {
@@ -617,58 +648,118 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_dma(GemmArgs p) {
                 na[m] = frag_a(An, gn, m);
             else if (m < TM + TN)
                 nb[m - TM] = frag_b(Bn, gn, m - TM);
-            if (loads && m % kStride == 0 && m / kStride < kLoads) issue_one(kl, sl, m / kStride);
+            if (ld) {
+                if constexpr (kStaged) {
+                    if (m < kLoads) {
+                        store_reg(slot, m, Rw[m]);
+                        Rl[m] = load_reg(kl, m);
+                    }
+                } else {
+                    if (m % kStride == 0 && m / kStride < kLoads) issue_direct(kl, slot, m / kStride);
+                }
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
     };
-    if (nk > 0) {
+    // Operands double-buffered in registers: the LDS reads of group g+1 are
+    // issued among the MFMAs of group g, so the matrix units never wait for
+    // the reads of the group they are about to run; ca / cb hold the
+    // operands of the next group to multiply.  The loop is barrier-
+    // overlapped: the last group of tile kt is read into registers before
+    // the barrier that ends tile kt and multiplied after it, while the first
+    // operands of tile kt+1 are read, so the matrix units stay busy across
+    // the barrier.  Past that barrier every wave holds all of tile kt's
+    // operands and its stage may be refilled.
+    f32x4 ca[TM], cb[TN];
+    auto tile = [&](int kt, int kl, int slot, const f32x4 *Rw, f32x4 *Rl) {
+        const float *As = lds + (kt % kStages) * kStageSz;
+        const float *Bs = As + kASz;
 #pragma unroll
-        for (int t = 0; t < kAhead; ++t) issue(min(t, nk - 1), t);
-        wait_vmcnt<(kAhead - 1) * kLoads>();  // tile 0 landed
-        asm volatile("s_barrier" ::: "memory");
-        // Operands double-buffered in registers: the LDS reads of group g+1
-        // are issued among the MFMAs of group g, so the matrix units never
-        // wait for the reads of the group they are about to run.  ca / cb
-        // hold the operands of the next group to multiply.
-        f32x4 ca[TM], cb[TN];
-        frag(lds, lds + kASz, 0, ca, cb);
-        for (int kt = 0; kt < nk; ++kt) {
-            const float *As = lds + (kt % kStages) * kStageSz;
-            const float *Bs = As + kASz;
-            const int kl = min(kt + kAhead, nk - 1), sl = (kt + kAhead) % kStages;
-#pragma unroll
-            for (int g = 0; g < NG - 1; ++g) {
-                // Group g's operands (read during the previous group) have
-                // landed; waiting here, before the next group's reads are
-                // issued, leaves those in flight behind the MFMAs.
-                wait_lgkm0();
-                f32x4 na[TM], nb[TN];
-                run_group(ca, cb, As, Bs, g + 1, na, nb, g == 0, kl, sl);
-#pragma unroll
-                for (int i = 0; i < TM; ++i) ca[i] = na[i];
-#pragma unroll
-                for (int j = 0; j < TN; ++j) cb[j] = nb[j];
-            }
-            colsum_add(Bs);
-            // ca / cb: the last group of tile kt.  Every wave's reads of tile
-            // kt are done before the barrier (its stage is refilled after
-            // it), and so are this wave's loads of tile kt+1 (the newest
-            // kAhead-1 tiles may still be in flight).
+        for (int g = 0; g < NG - 1; ++g) {
+            // Group g's operands (read during the previous group) have
+            // landed; waiting here, before the next group's reads are
+            // issued, leaves those in flight behind the MFMAs.
             wait_lgkm0();
-            wait_vmcnt<(kAhead - 1) * kLoads>();
-            __builtin_amdgcn_sched_barrier(0);
-            asm volatile("s_barrier" ::: "memory");
-            // Group 0 of tile kt+1 (past the last tile: a stage nothing
-            // uses, read and discarded).
             f32x4 na[TM], nb[TN];
-            const float *An = lds + ((kt + 1) % kStages) * kStageSz;
-            run_group(ca, cb, An, An + kASz, 0, na, nb, false, 0, 0);
+            run_group(ca, cb, As, Bs, g + 1, na, nb, g == 0, kl, slot, Rw, Rl);
 #pragma unroll
             for (int i = 0; i < TM; ++i) ca[i] = na[i];
 #pragma unroll
             for (int j = 0; j < TN; ++j) cb[j] = nb[j];
         }
-        wait_vmcnt<0>();  // the reloads past the last tile, before the LDS reuse
+        colsum_add(Bs);
+        // ca / cb: the last group of tile kt.  Every wave's reads (and LDS
+        // writes) of this tile are done before the barrier; direct, this
+        // wave's loads of tile kt+1 are done once at most the newest
+        // kAhead-1 tiles' are outstanding, and the barrier publishes every
+        // wave's.
+        wait_lgkm0();
+        if constexpr (!kStaged) wait_vmcnt<(kAhead - 1) * kLoads>();
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_barrier" ::: "memory");
+        // Group 0 of tile kt+1 (past the last tile: a stage nothing uses,
+        // read and discarded).
+        f32x4 na[TM], nb[TN];
+        const float *An = lds + ((kt + 1) % kStages) * kStageSz;
+        run_group(ca, cb, An, An + kASz, 0, na, nb, false, 0, 0, Rw, Rl);
+#pragma unroll
+        for (int i = 0; i < TM; ++i) ca[i] = na[i];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) cb[j] = nb[j];
+    };
+    if constexpr (kStaged) {
+        // Tile t is loaded into register set t % 2 during tile t-2 (one load
+        // after each of the first kLoads MFMAs of the tile's first group),
+        // and written from there to stage t % 2 during tile t-1 (the stage of
+        // tile t-2, free since the barrier that ended tile t-2); each write
+        // goes out right before the load that refills its registers.  Past
+        // the last tile, tile nk-1 is reloaded and written to the free stage,
+        // which nothing reads.  The kt loop is unrolled by two so that the
+        // register sets swap roles without copies.
+        if (nk > 0) {
+            f32x4 R0[kLoads], R1[kLoads];
+#pragma unroll
+            for (int q = 0; q < kLoads; ++q) R0[q] = load_reg(0, q);
+#pragma unroll
+            for (int q = 0; q < kLoads; ++q) R1[q] = load_reg(min(1, nk - 1), q);
+#pragma unroll
+            for (int q = 0; q < kLoads; ++q) store_reg(0, q, R0[q]);
+            wait_lgkm0();
+            asm volatile("s_barrier" ::: "memory");
+            frag(lds, lds + kASz, 0, ca, cb);
+            // Tile kt writes the set holding tile kt+1 and refills the other
+            // with tile kt+2; that set was loaded a whole tile ago.
+            int kt = 0;
+            for (; kt + 1 < nk; kt += 2) {
+                wait_vmcnt<0>();
+                tile(kt, min(kt + 2, nk - 1), (kt + 1) % kStages, R1, R0);
+                wait_vmcnt<0>();
+                tile(kt + 1, min(kt + 3, nk - 1), kt % kStages, R0, R1);
+            }
+            if (kt < nk) {
+                wait_vmcnt<0>();
+                tile(kt, nk - 1, (kt + 1) % kStages, R1, R0);
+            }
+        }
+    } else {
+        // Tile t goes to stage t % kStages.  The prologue issues tiles
+        // 0 .. kAhead-1; iteration kt issues tile kt + kAhead into the stage
+        // of tile kt-1, free since the barrier that ended tile kt-1.  Past
+        // the last tile an iteration reloads tile nk-1 into that free stage,
+        // which nothing reads again: the loop body has no branch, and every
+        // iteration leaves the same kAhead tiles in flight.
+        if (nk > 0) {
+#pragma unroll
+            for (int t = 0; t < kAhead; ++t)
+#pragma unroll
+                for (int q = 0; q < kLoads; ++q) issue_direct(min(t, nk - 1), t, q);
+            wait_vmcnt<(kAhead - 1) * kLoads>();  // tile 0 landed
+            asm volatile("s_barrier" ::: "memory");
+            frag(lds, lds + kASz, 0, ca, cb);
+            for (int kt = 0; kt < nk; ++kt)
+                tile(kt, min(kt + kAhead, nk - 1), (kt + kAhead) % kStages, nullptr, nullptr);
+            wait_vmcnt<0>();  // the reloads past the last tile, before the LDS reuse
+        }
     }
     __syncthreads();  // every wave past its last tile read before the stage reuse
     if constexpr (kTN)
@@ -677,11 +768,11 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_dma(GemmArgs p) {
 }
 
 template <int BM, int BN, int WGM, int WGN, int BK, bool AK, bool BNC>
-void launch_dma(const GemmArgs &a0, hipStream_t st) {
+void launch_pipe(const GemmArgs &a0, hipStream_t st) {
     GemmArgs a = a0;
     a.tiles_m = (a.M + BM - 1) / BM;
     a.tiles_n = (a.N + BN - 1) / BN;
-    gemm_f32_dma<BM, BN, BK, WGM, WGN, AK, BNC><<<a.tiles_m * a.tiles_n, 64 * WGM * WGN, 0, st>>>(a);
+    gemm_f32_pipe<BM, BN, BK, WGM, WGN, AK, BNC><<<a.tiles_m * a.tiles_n, 64 * WGM * WGN, 0, st>>>(a);
 }
 
 template <int BM, int BN, int WGM, int WGN, int BK, bool AK, bool BNC, bool VEC>
@@ -704,24 +795,24 @@ constexpr int kNumCfgs = 8;
 // K depth of a configuration.
 inline int cfg_bk(int cfg) { return (cfg == 3 || cfg >= 5) ? 32 : (cfg == 4 ? 16 : kBK); }
 
-// dma: K % cfg_bk(cfg) == 0 and the VEC conditions hold (the host checks):
-// the direct-to-LDS kernel with the same tile shape.
+// pipe: K % cfg_bk(cfg) == 0 and the VEC conditions hold (the host checks):
+// the pipelined whole-tile kernel with the same tile shape.
 template <bool AK, bool BNC>
-void launch_layout(const GemmArgs &a, bool vec, bool dma, int cfg, hipStream_t st) {
+void launch_layout(const GemmArgs &a, bool vec, bool pipe, int cfg, hipStream_t st) {
     if (!vec) {
         launch_one<64, 64, 2, 2, 16, AK, BNC, false>(a, st);
         return;
     }
-    if (dma) {
+    if (pipe) {
         switch (cfg) {
-            case 0: launch_dma<256, 256, 2, 2, kBK, AK, BNC>(a, st); break;
-            case 1: launch_dma<256, 128, 2, 2, kBK, AK, BNC>(a, st); break;
-            case 2: launch_dma<128, 256, 2, 2, kBK, AK, BNC>(a, st); break;
-            case 3: launch_dma<128, 128, 2, 2, 32, AK, BNC>(a, st); break;
-            case 5: launch_dma<128, 64, 2, 2, 32, AK, BNC>(a, st); break;
-            case 6: launch_dma<256, 256, 2, 4, 32, AK, BNC>(a, st); break;
-            case 7: launch_dma<256, 128, 4, 2, 32, AK, BNC>(a, st); break;
-            default: launch_dma<64, 64, 2, 2, 16, AK, BNC>(a, st); break;
+            case 0: launch_pipe<256, 256, 2, 2, kBK, AK, BNC>(a, st); break;
+            case 1: launch_pipe<256, 128, 2, 2, kBK, AK, BNC>(a, st); break;
+            case 2: launch_pipe<128, 256, 2, 2, kBK, AK, BNC>(a, st); break;
+            case 3: launch_pipe<128, 128, 2, 2, 32, AK, BNC>(a, st); break;
+            case 5: launch_pipe<128, 64, 2, 2, 32, AK, BNC>(a, st); break;
+            case 6: launch_pipe<256, 256, 2, 4, 32, AK, BNC>(a, st); break;
+            case 7: launch_pipe<256, 128, 4, 2, 32, AK, BNC>(a, st); break;
+            default: launch_pipe<64, 64, 2, 2, 16, AK, BNC>(a, st); break;
         }
         return;
     }
@@ -738,9 +829,9 @@ void launch_layout(const GemmArgs &a, bool vec, bool dma, int cfg, hipStream_t s
 }
 
 // Defined in k_gemm_{nn,nt,tn}.hip.
-void launch_nn(const GemmArgs &a, bool vec, bool dma, int cfg, hipStream_t st);
-void launch_nt(const GemmArgs &a, bool vec, bool dma, int cfg, hipStream_t st);
-void launch_tn(const GemmArgs &a, bool vec, bool dma, int cfg, hipStream_t st);
+void launch_nn(const GemmArgs &a, bool vec, bool pipe, int cfg, hipStream_t st);
+void launch_nt(const GemmArgs &a, bool vec, bool pipe, int cfg, hipStream_t st);
+void launch_tn(const GemmArgs &a, bool vec, bool pipe, int cfg, hipStream_t st);
 
 }  // namespace gemm
 }  // namespace fg

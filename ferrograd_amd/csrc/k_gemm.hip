@@ -89,15 +89,16 @@ int gemm_common(fg_ctx *ctx, int layout, GemmArgs &a, const char *who) {
     auto al16 = [](const void *q) { return (((uintptr_t)q) & 15u) == 0; };
     a.vec_out = al16(a.C) && a.ldc % 4 == 0 && (!a.Z || (al16(a.Z) && a.ldz % 4 == 0)) &&
                 (!a.bias || al16(a.bias));
-    // Direct-to-LDS loads need whole K tiles (a partial one would bring
-    // neighbouring k into valid outputs) and at least one 16-byte chunk per
-    // row-contiguous operand row (edge chunks are clamped, not masked).
-    const bool dma = fg::gemm::kDma && vec && a.K > 0 && a.K % fg::gemm::cfg_bk(cfg) == 0 &&
-                     a.M >= 4 && a.N >= 4;
+    // The pipelined kernel's 16-byte tile loads need whole K tiles (a partial
+    // one would bring neighbouring k into valid outputs) and at least one
+    // 16-byte chunk per row-contiguous operand row (edge chunks are clamped,
+    // not masked).
+    const bool pipe = fg::gemm::kPipe && vec && a.K > 0 && a.K % fg::gemm::cfg_bk(cfg) == 0 &&
+                      a.M >= 4 && a.N >= 4;
     switch (layout) {
-        case FG_NN: fg::gemm::launch_nn(a, vec, dma, cfg, ctx->stream); break;
-        case FG_NT: fg::gemm::launch_nt(a, vec, dma, cfg, ctx->stream); break;
-        default: fg::gemm::launch_tn(a, vec, dma, cfg, ctx->stream); break;
+        case FG_NN: fg::gemm::launch_nn(a, vec, pipe, cfg, ctx->stream); break;
+        case FG_NT: fg::gemm::launch_nt(a, vec, pipe, cfg, ctx->stream); break;
+        default: fg::gemm::launch_tn(a, vec, pipe, cfg, ctx->stream); break;
     }
     FG_LAUNCH_CHECK(who);
     return FG_OK;

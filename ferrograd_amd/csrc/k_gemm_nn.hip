@@ -5,8 +5,8 @@
 namespace fg {
 namespace gemm {
 
-void launch_nn(const GemmArgs &a, bool vec, bool dma, int cfg, hipStream_t st) {
-    launch_layout<true, true>(a, vec, dma, cfg, st);
+void launch_nn(const GemmArgs &a, bool vec, bool pipe, int cfg, hipStream_t st) {
+    launch_layout<true, true>(a, vec, pipe, cfg, st);
 }
 
 }  // namespace gemm

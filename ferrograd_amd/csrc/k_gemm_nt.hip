@@ -5,8 +5,8 @@
 namespace fg {
 namespace gemm {
 
-void launch_nt(const GemmArgs &a, bool vec, bool dma, int cfg, hipStream_t st) {
-    launch_layout<true, false>(a, vec, dma, cfg, st);
+void launch_nt(const GemmArgs &a, bool vec, bool pipe, int cfg, hipStream_t st) {
+    launch_layout<true, false>(a, vec, pipe, cfg, st);
 }
 
 }  // namespace gemm

@@ -5,8 +5,8 @@
 namespace fg {
 namespace gemm {
 
-void launch_tn(const GemmArgs &a, bool vec, bool dma, int cfg, hipStream_t st) {
-    launch_layout<false, true>(a, vec, dma, cfg, st);
+void launch_tn(const GemmArgs &a, bool vec, bool pipe, int cfg, hipStream_t st) {
+    launch_layout<false, true>(a, vec, pipe, cfg, st);
 }
 
 }  // namespace gemm
