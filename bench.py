@@ -582,7 +582,7 @@ def main() -> int:
     hid = comps["c5_hidden_fwd_gemm"]
     roofline = {
         "bound": "mfma",
-        "kernel": "gemm_f32_mfma NN 2048x4096x4096 + bias + GELU (c5 hidden-layer forward)",
+        "kernel": "gemm_f32_pipe NN 2048x4096x4096 + bias + GELU (c5 hidden-layer forward)",
         "achieved": hid["tflops"],
         "peak": PEAK_FP32_MFMA_TFLOPS,
         "unit": "TFLOP/s",
