@@ -18,22 +18,24 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // ------------------------------------------------------------ dispatch
 // Tile configuration per call (indices as in fg_gemm_kernel.h), from a
-// measured sweep of every configuration on MI355X (256 CUs, direct-to-LDS
-// loads, N(0,1) operands, HIP events) over the BASELINE shapes, TFLOP/s:
+// measured sweep of every configuration of the pipelined kernel on MI355X
+// (256 CUs, N(0,1) operands, HIP events) over the BASELINE shapes, TFLOP/s:
 //  * NN (forward): 256x256 with 8 waves for K >= 4096 squares that fill the
-//    chip (134 at 4096^3, against 130 for 256x128); else 256x128 with 8
-//    waves and BK 32 when it yields >= one tile per CU (125 at
-//    2048x4096x4096, 99 at K = 1024); else 128x64 (104 for the 1000-wide
-//    head); 64x64 for anything smaller.
-//  * NT (dA): 256x256 with 8 waves (BK 32) for large-K squares that fill the
-//    chip (138 at 4096^3); else 256x128 with 8 waves when it gives >= one tile
-//    per CU (127 at 2048x4096x4096, 96-104 at K = 1000); else 128x128 or
-//    128x64 (96 at 2048x1024x4096).
-//  * TN (dW): 256x256 with 8 waves for K >= 4096 filling the chip (138 at
-//    4096^3); 256x128 with 4 waves and BK 16 at >= two tiles per CU (129 at
-//    4096x4096x2048); then 128x64 at >= two tiles per CU (111 for the
-//    1000-wide layer and 103 for the 1024-deep one, against 106 / 102 for
-//    128x128); else 128x128; else 128x64.
+//    chip (138-145 at 4096^3, against 139-142 for the 256x128 tiles); else
+//    256x128 with 8 waves when it yields >= one tile per CU (125 at
+//    2048x4096x4096, 135 at K = 1024); else 128x64 (131 for the 1000-wide
+//    head, against 70 for 128x128 on a quarter of the CUs); 64x64 for
+//    anything smaller.
+//  * NT (dA): 256x256 with 8 waves for large-K squares that fill the chip
+//    (145 at 4096^3); else 256x128 with 8 waves when it gives >= one tile per
+//    CU (137 at 2048x4096x4096); else 128x128 or 128x64 (137 for 128x64 at
+//    2048x1024x4096, against 73 for 128x128).
+//  * TN (dW): 256x256 with 8 waves for K >= 4096 filling the chip (144 at
+//    4096^3); 256x128 with 4 waves at >= two tiles per CU (140 at
+//    4096x4096x2048, 137-140 for the other 256-row tiles); then 128x64 at >=
+//    two tiles per CU (131-133 for the 1024- and 1000-wide layers, against
+//    125-127 for 128x128); else 128x128; else 128x64.
+// K % BK != 0 (the 1000-deep head dA) takes gemm_f32_mfma with the same tile.
 int tiles(int M, int N, int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); }
 
 int pick_cfg(int layout, int M, int N, int K, int cus) {

@@ -176,6 +176,60 @@ def test_gemm_c2_full_size_sampled(gpu_ctx):
     assert normwise_rel(host(dW)[rows], Wr) < tol
 
 
+@pytest.mark.parametrize("case", [
+    # (layout, M, N, K, mode): shapes that select each configuration of the
+    # pipelined kernel (k_gemm.hip pick_cfg), edge tiles included.
+    (O.NN, 2000, 4000, 4096, "fwd"),   # 256x128, 8 waves; partial M and N tiles
+    (O.NT, 2048, 4096, 4096, "bwd"),   # 256x128, 8 waves; GELU' epilogue
+    (O.TN, 4096, 4096, 2048, "fwd"),   # 256x128, 4 waves (c5 dW)
+    (O.NT, 2048, 2000, 1024, "fwd"),   # 128x128
+    (O.NN, 2048, 1000, 4096, "fwd"),   # 128x64 (c5 head)
+    (O.TN, 1000, 4096, 2048, "bwd"),   # 128x64; partial M tile
+    # K % BK != 0: the register-staged kernel with the same tiles
+    (O.NT, 2048, 4096, 1000, "bwd"),   # 256x128, 8 waves (c5 head dA)
+    (O.TN, 1024, 4096, 1000, "fwd"),   # 128x64, row-contiguous operands
+    (O.NN, 2048, 4096, 20, "fwd"),     # K below one tile
+], ids=lambda c: f"{['NN', 'NT', 'TN'][c[0]]}-{c[1]}x{c[2]}x{c[3]}-{c[4]}")
+def test_gemm_pipe_configs_sampled(gpu_ctx, case):
+    """The large tile configurations at full size (and the same tiles for K
+    not a multiple of the tile depth), checked on 32 sampled output rows
+    against float64 dot products: forward with bias + GELU (C and Z), or
+    backward with the GELU derivative of a saved Zs."""
+    torch = _torch()
+    layout, M, N, K, mode = case
+    note(f"gemm pipe config layout={layout} M={M} N={N} K={K} mode={mode}")
+    g = torch.Generator(device="cuda").manual_seed(M + N + K + layout)
+    a_shape = (K, M) if layout == O.TN else (M, K)
+    b_shape = (N, K) if layout == O.NT else (K, N)
+    dA = torch.randn(a_shape, device="cuda", generator=g)
+    dB = 0.05 * torch.randn(b_shape, device="cuda", generator=g)
+    dC, dZ = empty((M, N)), empty((M, N))
+    lda, ldb = a_shape[1], b_shape[1]
+    if mode == "fwd":
+        dbias = 0.1 * torch.randn((N,), device="cuda", generator=g)
+        gpu_ctx.gemm(layout, M, N, K, dA, lda, dB, ldb, dC, N, bias=dbias, act=O.ACT_GELU,
+                     Z=dZ, ldz=N)
+    else:
+        dZs = torch.randn((M, N), device="cuda", generator=g)
+        gpu_ctx.gemm_bwd(layout, M, N, K, dA, lda, dB, ldb, dC, N, act=O.ACT_GELU, Zs=dZs,
+                         ldzs=N)
+    rows = np.sort(np.random.default_rng(M * 3 + N).choice(M, 32, replace=False))
+    rows[-1] = M - 1  # the last row sits in the edge tile when M is not a tile multiple
+    A = host(dA).astype(np.float64)
+    B = host(dB).astype(np.float64)
+    Ar = A[:, rows].T if layout == O.TN else A[rows]
+    Bf = B.T if layout == O.NT else B
+    P = Ar @ Bf
+    tol = 1e-5 * math.sqrt(K)
+    if mode == "fwd":
+        Zr = P + host(dbias).astype(np.float64)
+        assert normwise_rel(host(dZ)[rows], Zr) < tol
+        assert normwise_rel(host(dC)[rows], O.act(O.ACT_GELU, Zr)) < tol
+    else:
+        ref = O.act_bwd(O.ACT_GELU, P, host(dZs)[rows].astype(np.float64))
+        assert normwise_rel(host(dC)[rows], ref) < tol
+
+
 # ----------------------------------------------------- bias grad, act bwd
 @pytest.mark.parametrize("shape", [(2048, 4096), (64, 10), (1, 5), (1000, 1000), (3, 4097),
                                    (4096, 1000)], ids=lambda s: "x".join(map(str, s)))
