@@ -9,7 +9,8 @@
 // as the reference's node values are, the bias-add node and the activation
 // node are each rounded to the storage type.
 //
-// Design (gfx950):
+// Design of gemm16_mfma, the kernel for any shape (gfx950; the pipelined
+// kernel for whole tiles, gemm16_pipe, is described at its definition):
 //  * Each MFMA consumes, per lane, 8 consecutive k of one row of A and of
 //    one column of B (16 bytes each).  Both operands are therefore kept in
 //    LDS k-contiguous, [row][k] with a row stride of BK+8 elements (16-byte
@@ -56,7 +57,7 @@ struct Args {
     int accumulate;
     int tiles_m, tiles_n;
     int vec_out;  // C / Z / Zs rows and bias 8-byte aligned: 4-element epilogue I/O
-    // TN on the direct-to-LDS path only: colsum[n] (=|+=) sum_k B[k][n] --
+    // TN on the pipelined path only: colsum[n] (=|+=) sum_k B[k][n] --
     // the bias gradient of the layer whose weight gradient this GEMM
     // computes -- summed in fp32 from the B tiles already in LDS by the
     // workgroups of the first tile row, rounded to the storage type once.
@@ -395,14 +396,24 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm16_mfma(Args p) {
                                              n0 + wn0, wave, lane);
 }
 
-// ------------------------------------------------ direct-to-LDS variant
-// Tiles move from global memory straight into an LDS ring of up to four
-// stages (global_load_lds_dwordx4: 16 bytes = 8 elements per lane, landing
-// at the wave's LDS base + 16 * lane), all but one tile in flight during the
-// MFMAs of the current one, one barrier per tile.  A BK of 32 or 64 is only
-// 1-2 thousand MFMA cycles per SIMD, so the barrier is overlapped: the last
-// k16 step of each tile is multiplied after it, from registers.  No operand
-// is transposed on its way in:
+// ------------------------------------------------ pipelined variant
+// Software-pipelined over whole K tiles, one barrier per tile.  Each wave
+// loads its share of a tile as 16 bytes (8 elements) per lane, lane l's
+// chunk of wave load li landing at element 512 li + 8 l of the operand's
+// stage area; the source of each chunk is chosen so that the stage ends up
+// in the swizzled layout below.  Two ways to move the chunks:
+//  * staged (every tile but 256x256 with 4 waves or BK 64): global loads
+//    into registers, two register sets alternating by tile parity, written
+//    to a two-stage LDS ring by ds_write_b128 one tile later;
+//  * direct (256x256 with 4 waves or BK 64, whose accumulators leave no room
+//    for two register sets): global_load_lds_dwordx4 straight into an LDS
+//    ring of up to four stages.  The compiler cannot tell a transposing LDS
+//    read from the direct loads in flight and waits for all of them before
+//    each such read, so the tile rule keeps these tiles to layouts without a
+//    row-contiguous operand.
+// A BK of 32 or 64 is only 1-2 thousand MFMA cycles per SIMD, so the barrier
+// is overlapped: the last k16 step of each tile is multiplied after it, from
+// registers.  No operand is transposed on its way in:
 //  * a k-contiguous operand sits [rows][BK]; chunk c (8 k) of row r at
 //    c ^ ((r / (128 / BK)) % (BK / 8)), so the rows read together by a
 //    16-byte LDS read hit distinct banks; an MFMA operand is one such read;
@@ -491,7 +502,7 @@ struct ColSum16 {
 };
 
 template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC, bool BF>
-__global__ __launch_bounds__(64 * WGM * WGN) void gemm16_dma(Args p) {
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm16_pipe(Args p) {
     using E = T16<BF>;
     constexpr int NW = WGM * WGN;
     constexpr int WTM = BM / WGM, WTN = BN / WGN;
@@ -503,8 +514,14 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm16_dma(Args p) {
     static_assert(kInstA % NW == 0 && kInstB % NW == 0, "loads divide among the waves");
     constexpr int kPerA = kInstA / NW, kPerB = kInstB / NW, kLoads = kPerA + kPerB;
     constexpr int kASz = BM * BK, kBSz = BN * BK, kStageSz = kASz + kBSz;  // elements
-    // Up to four stages, as many as fit in the 160 KiB of LDS.
-    constexpr int kStages = 4 * kStageSz * 2 <= 160 * 1024   ? 4
+    // Staged loads (global -> registers -> ds_write) for every tile but
+    // 256x256 with 4 waves (256 accumulator registers) or with BK 64 (eight
+    // 16-byte loads per wave and tile, which with the 128 accumulators of 8
+    // waves exceed the registers): those load straight into LDS, with up to
+    // four stages, as many as fit in the 160 KiB of LDS.
+    constexpr bool kStaged = !(BM == 256 && BN == 256 && (NW == 4 || BK == 64));
+    constexpr int kStages = kStaged                             ? 2
+                            : 4 * kStageSz * 2 <= 160 * 1024   ? 4
                             : 3 * kStageSz * 2 <= 160 * 1024 ? 3
                                                               : 2;
     constexpr int kEpiBytes = NW * 32 * (WTN + 4) * 4;
@@ -539,26 +556,47 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm16_dma(Args p) {
         const int c = pc ^ swz16_r(k);
         return base + (size_t)(k0 + k) * ld + min(r0 + 8 * c, rmax - 8);
     };
-    auto issue = [&](int kt, int stage) {
+    // Wave load q (0 .. kLoads-1) of tile kt into stage `stage`: this wave's
+    // share of A first, then of B.
+    auto issue_one = [&](int kt, int stage, int q) {
         uint16_t *sa = lds + stage * kStageSz;
-        uint16_t *sb = sa + kASz;
         const int k0 = kt * BK;
-#pragma unroll
-        for (int i = 0; i < kPerA; ++i) {
-            const int li = wave * kPerA + i;
-            const int pos = li * 64 + lane;
+        if (q < kPerA) {
+            const int li = wave * kPerA + q, pos = li * 64 + lane;
             const uint16_t *src = AK ? src_kc(p.A, p.lda, m0, p.M, k0, pos)
                                      : src_rc(p.A, p.lda, m0, p.M, k0, pos, BM);
             __builtin_amdgcn_global_load_lds(src, sa + li * 512, 16, 0, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < kPerB; ++i) {
-            const int li = wave * kPerB + i;
-            const int pos = li * 64 + lane;
+        } else {
+            const int li = wave * kPerB + (q - kPerA), pos = li * 64 + lane;
             const uint16_t *src = BNC ? src_rc(p.B, p.ldb, n0, p.N, k0, pos, BN)
                                       : src_kc(p.B, p.ldb, n0, p.N, k0, pos);
-            __builtin_amdgcn_global_load_lds(src, sb + li * 512, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(src, sa + kASz + li * 512, 16, 0, 0);
         }
+    };
+    auto issue = [&](int kt, int stage) {
+#pragma unroll
+        for (int q = 0; q < kLoads; ++q) issue_one(kt, stage, q);
+    };
+    // Staged: wave load q of tile kt into registers, and from there to its
+    // place in a stage (lane l's 16 bytes at element 8 l of the wave load's
+    // 1 KiB run, as the direct loads would put them).
+    auto load_reg = [&](int kt, int q) {
+        const int k0 = kt * BK;
+        const uint16_t *src;
+        if (q < kPerA) {
+            const int pos = (wave * kPerA + q) * 64 + lane;
+            src = AK ? src_kc(p.A, p.lda, m0, p.M, k0, pos) : src_rc(p.A, p.lda, m0, p.M, k0, pos, BM);
+        } else {
+            const int pos = (wave * kPerB + (q - kPerA)) * 64 + lane;
+            src = BNC ? src_rc(p.B, p.ldb, n0, p.N, k0, pos, BN) : src_kc(p.B, p.ldb, n0, p.N, k0, pos);
+        }
+        return *reinterpret_cast<const u32x4 *>(src);
+    };
+    auto store_reg = [&](int stage, int q, const u32x4 &v) {
+        uint16_t *sa = lds + stage * kStageSz;
+        uint16_t *run = q < kPerA ? sa + (wave * kPerA + q) * 512
+                                  : sa + kASz + (wave * kPerB + q - kPerA) * 512;
+        *reinterpret_cast<u32x4 *>(run + 8 * lane) = v;
     };
 
     const int nk = p.K / BK;
@@ -566,83 +604,95 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm16_dma(Args p) {
     ColSum16<BN, BK, 64 * NW, BF> cs;
     const bool do_cs = kTN && p.colsum && tile_m == 0;
     // MFMA operands of k16 step u of a stage: lane half h takes k 8h .. 8h+7.
-    auto frag = [&](const uint16_t *As, const uint16_t *Bs, int u, u32x4 (&a)[TM], u32x4 (&b)[TN]) {
+    auto frag_a = [&](const uint16_t *As, int u, int i) {
         const int kb = u * 16 + 8 * h;
-#pragma unroll
-        for (int i = 0; i < TM; ++i) {
-            if constexpr (AK) {
-                const int row = wm0 + i * 32 + l32;
-                const int c = (kb >> 3) ^ swz16_k<BK>(row);
-                a[i] = *reinterpret_cast<const u32x4 *>(As + row * BK + 8 * c);
-            } else {
-                a[i] = read_tr<BM>(As, kb, wm0 + i * 32 + 16 * ((lane >> 4) & 1), lane);
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            if constexpr (BNC) {
-                b[j] = read_tr<BN>(Bs, kb, wn0 + j * 32 + 16 * ((lane >> 4) & 1), lane);
-            } else {
-                const int col = wn0 + j * 32 + l32;
-                const int c = (kb >> 3) ^ swz16_k<BK>(col);
-                b[j] = *reinterpret_cast<const u32x4 *>(Bs + col * BK + 8 * c);
-            }
+        if constexpr (AK) {
+            const int row = wm0 + i * 32 + l32;
+            const int c = (kb >> 3) ^ swz16_k<BK>(row);
+            return *reinterpret_cast<const u32x4 *>(As + row * BK + 8 * c);
+        } else {
+            return read_tr<BM>(As, kb, wm0 + i * 32 + 16 * ((lane >> 4) & 1), lane);
         }
     };
-    auto mma = [&](const u32x4 (&a)[TM], const u32x4 (&b)[TN]) {
+    auto frag_b = [&](const uint16_t *Bs, int u, int j) {
+        const int kb = u * 16 + 8 * h;
+        if constexpr (BNC) {
+            return read_tr<BN>(Bs, kb, wn0 + j * 32 + 16 * ((lane >> 4) & 1), lane);
+        } else {
+            const int col = wn0 + j * 32 + l32;
+            const int c = (kb >> 3) ^ swz16_k<BK>(col);
+            return *reinterpret_cast<const u32x4 *>(Bs + col * BK + 8 * c);
+        }
+    };
+    auto frag = [&](const uint16_t *As, const uint16_t *Bs, int u, u32x4 (&a)[TM], u32x4 (&b)[TN]) {
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+        for (int i = 0; i < TM; ++i) a[i] = frag_a(As, u, i);
 #pragma unroll
-            for (int j = 0; j < TN; ++j) acc[i][j] = E::mfma(a[i], b[j], acc[i][j]);
+        for (int j = 0; j < TN; ++j) b[j] = frag_b(Bs, u, j);
     };
     constexpr int NU = BK / 16;
+    constexpr int kMfma = TM * TN;                       // MFMAs per k16 step
+    constexpr int kPieces = TM + TN;                     // operand fragments per step
+    constexpr int kSlots = (NU - 1) * kMfma;             // MFMAs of a tile before its barrier
+    static_assert(NU >= 2 && kLoads <= kSlots, "a tile's loads fit among its MFMAs");
+    constexpr int kStride = kSlots / kLoads;             // MFMAs per load
+    constexpr int kAhead = kStages - 1;                  // direct: tiles in flight
+    // One k16 step's MFMAs on (ca, cb) in a fixed order: after MFMA m, the
+    // reads of operand fragment m of step un (A fragments, then B), and, when
+    // `ld`, the tile's memory operations that fall on this step's slots (one
+    // every kStride MFMAs over the steps before the tile's barrier): staged,
+    // register set Rw's chunk q (tile kt+1) written to stage `slot` and the
+    // register refilled from tile kl (Rl); direct, one load of tile kl into
+    // stage `slot`.  Reads or loads issued in a burst fill the wave's memory
+    // queues and hold up the MFMAs behind them.
+    auto run_step = [&](const u32x4 (&ca)[TM], const u32x4 (&cb)[TN], const uint16_t *An,
+                        const uint16_t *Bn, int un, u32x4 (&na)[TM], u32x4 (&nb)[TN], int u,
+                        bool ld, int kl, int slot, const u32x4 *Rw, u32x4 *Rl) {
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int m = 0; m < (kMfma > kPieces ? kMfma : kPieces); ++m) {
+            if (m < kMfma) {
+                const int i = m / TN, j = m % TN;
+                acc[i][j] = E::mfma(ca[i], cb[j], acc[i][j]);
+            }
+            if (m < TM)
+                na[m] = frag_a(An, un, m);
+            else if (m < kPieces)
+                nb[m - TM] = frag_b(Bn, un, m - TM);
+            if (ld && m < kMfma) {
+                const int sidx = u * kMfma + m;
+                if (sidx % kStride == 0 && sidx / kStride < kLoads) {
+                    const int q = sidx / kStride;
+                    if constexpr (kStaged) {
+                        store_reg(slot, q, Rw[q]);
+                        Rl[q] = load_reg(kl, q);
+                    } else {
+                        issue_one(kl, slot, q);
+                    }
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
     // Barrier-overlapped loop: the last k16 step of tile kt is read into
     // registers before the barrier that ends tile kt and multiplied after
     // it, so the matrix units stay busy across the barrier while the first
-    // operands of tile kt+1 are read.  Past that barrier every wave holds
-    // all of tile kt's operands, so tile kt's stage takes tile kt + kStages:
-    // kStages - 1 tiles are in flight behind the one being multiplied.
-    // At most `n` tiles' loads of this wave may still be outstanding.
-    auto wait_tiles = [&](int n) {
-        if (n <= 0)
-            wait_vmcnt<0>();
-        else if (n == 1)
-            wait_vmcnt<kLoads>();
-        else if (n == 2)
-            wait_vmcnt<2 * kLoads>();
-        else
-            wait_vmcnt<3 * kLoads>();
-    };
-#pragma unroll
-    for (int t = 0; t < kStages; ++t)
-        if (t < nk) issue(t, t);
-    wait_tiles(min(kStages, nk) - 1);
-    asm volatile("s_barrier" ::: "memory");
-    // Operands double-buffered in registers: the LDS reads of k16 step u+1
-    // are issued before the MFMAs of step u, so the matrix units never wait
-    // for the reads of the step they are about to run.  ca / cb hold the
-    // operands of the next step to multiply.
-    // LDS read instructions per k16 step (a row-contiguous operand takes two
-    // transposing reads) and the order the scheduler is held to: one MFMA,
-    // then that MFMA's share of the next step's reads.
-    constexpr int kReads = (AK ? TM : 2 * TM) + (BNC ? 2 * TN : TN);
-    constexpr int kMfma = TM * TN;
-    constexpr int kPerMfma = (kReads + kMfma - 1) / kMfma;
-    auto interleave = [&]() { sched_interleave<0, kMfma, kReads, kPerMfma>(); };
+    // operands of tile kt+1 are read.  Tile t lives in stage t % kStages.
+    // Operands are double-buffered in registers: the reads of step u+1 go
+    // out among the MFMAs of step u; ca / cb hold the operands of the next
+    // step to multiply.
     u32x4 ca[TM], cb[TN];
-    if (nk > 0) frag(lds, lds + kASz, 0, ca, cb);
-    for (int kt = 0; kt < nk; ++kt) {
+    auto tile = [&](int kt, int kl, int slot, const u32x4 *Rw, u32x4 *Rl) {
         const uint16_t *As = lds + (kt % kStages) * kStageSz;
         const uint16_t *Bs = As + kASz;
-        if (kt >= 1 && kt - 1 + kStages < nk) issue(kt - 1 + kStages, (kt - 1) % kStages);
-        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int u = 0; u < NU - 1; ++u) {
+            // Step u's operands (read during the previous step) have landed;
+            // waiting here, before the next step's reads are issued, leaves
+            // those in flight behind the MFMAs.
+            wait_lgkm0();
             u32x4 na[TM], nb[TN];
-            frag(As, Bs, u + 1, na, nb);
-            mma(ca, cb);
-            interleave();
-            __builtin_amdgcn_sched_barrier(0);
+            run_step(ca, cb, As, Bs, u + 1, na, nb, u, true, kl, slot, Rw, Rl);
 #pragma unroll
             for (int i = 0; i < TM; ++i) ca[i] = na[i];
 #pragma unroll
@@ -650,23 +700,75 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm16_dma(Args p) {
         }
         if constexpr (kTN)
             if (do_cs) cs.add(Bs);
-        // ca / cb: the last step of tile kt.  Every wave's reads of tile kt
-        // must be done before the barrier (its stage is refilled after it).
+        // ca / cb: the last step of tile kt.  Every wave's reads (and LDS
+        // writes) of this tile are done before the barrier; direct, this
+        // wave's loads of tile kt+1 are done once at most the newest
+        // kAhead-1 tiles' are outstanding, and the barrier publishes every
+        // wave's.
         wait_lgkm0();
-        wait_tiles(min(kt + kStages - 1, nk - 1) - (kt + 1));
+        if constexpr (!kStaged) wait_vmcnt<(kAhead - 1) * kLoads>();
         __builtin_amdgcn_sched_barrier(0);
         asm volatile("s_barrier" ::: "memory");
-        __builtin_amdgcn_sched_barrier(0);
+        // Step 0 of tile kt+1 (past the last tile: a stage nothing uses,
+        // read and discarded).
         u32x4 na[TM], nb[TN];
-        if (kt + 1 < nk) {
-            const uint16_t *An = lds + ((kt + 1) % kStages) * kStageSz;
-            frag(An, An + kASz, 0, na, nb);
-        }
-        mma(ca, cb);
+        const uint16_t *An = lds + ((kt + 1) % kStages) * kStageSz;
+        run_step(ca, cb, An, An + kASz, 0, na, nb, 0, false, 0, 0, Rw, Rl);
 #pragma unroll
         for (int i = 0; i < TM; ++i) ca[i] = na[i];
 #pragma unroll
         for (int j = 0; j < TN; ++j) cb[j] = nb[j];
+    };
+    if constexpr (kStaged) {
+        // Tile t is loaded into register set t % 2 during tile t-2 and
+        // written from there to stage t % 2 during tile t-1 (the stage of
+        // tile t-2, free since the barrier that ended tile t-2); each write
+        // goes out right before the load that refills its registers.  Past
+        // the last tile, tile nk-1 is reloaded and written to the free
+        // stage, which nothing reads.  The kt loop is unrolled by two so
+        // that the register sets swap roles without copies.
+        if (nk > 0) {
+            u32x4 R0[kLoads], R1[kLoads];
+#pragma unroll
+            for (int q = 0; q < kLoads; ++q) R0[q] = load_reg(0, q);
+#pragma unroll
+            for (int q = 0; q < kLoads; ++q) R1[q] = load_reg(min(1, nk - 1), q);
+#pragma unroll
+            for (int q = 0; q < kLoads; ++q) store_reg(0, q, R0[q]);
+            wait_lgkm0();
+            asm volatile("s_barrier" ::: "memory");
+            frag(lds, lds + kASz, 0, ca, cb);
+            // Tile kt writes the set holding tile kt+1 and refills the other
+            // with tile kt+2; that set was loaded a whole tile ago.
+            int kt = 0;
+            for (; kt + 1 < nk; kt += 2) {
+                wait_vmcnt<0>();
+                tile(kt, min(kt + 2, nk - 1), (kt + 1) % kStages, R1, R0);
+                wait_vmcnt<0>();
+                tile(kt + 1, min(kt + 3, nk - 1), kt % kStages, R0, R1);
+            }
+            if (kt < nk) {
+                wait_vmcnt<0>();
+                tile(kt, nk - 1, (kt + 1) % kStages, R1, R0);
+            }
+        }
+    } else {
+        // Tile t goes to stage t % kStages.  The prologue issues tiles
+        // 0 .. kAhead-1; iteration kt issues tile kt + kAhead into the stage
+        // of tile kt-1, free since the barrier that ended tile kt-1.  Past
+        // the last tile an iteration reloads tile nk-1 into that free stage,
+        // which nothing reads again: the loop body has no branch, and every
+        // iteration leaves the same kAhead tiles in flight.
+        if (nk > 0) {
+#pragma unroll
+            for (int t = 0; t < kAhead; ++t) issue(min(t, nk - 1), t);
+            wait_vmcnt<(kAhead - 1) * kLoads>();  // tile 0 landed
+            asm volatile("s_barrier" ::: "memory");
+            frag(lds, lds + kASz, 0, ca, cb);
+            for (int kt = 0; kt < nk; ++kt)
+                tile(kt, min(kt + kAhead, nk - 1), (kt + kAhead) % kStages, nullptr, nullptr);
+            wait_vmcnt<0>();  // the reloads past the last tile, before the LDS reuse
+        }
     }
     __syncthreads();
     if constexpr (kTN)
@@ -676,11 +778,11 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm16_dma(Args p) {
 }
 
 template <int BM, int BN, int WGM, int WGN, int BK, bool AK, bool BNC, bool BF>
-void launch_dma16(const Args &a0, hipStream_t st) {
+void launch_pipe16(const Args &a0, hipStream_t st) {
     Args a = a0;
     a.tiles_m = (a.M + BM - 1) / BM;
     a.tiles_n = (a.N + BN - 1) / BN;
-    gemm16_dma<BM, BN, BK, WGM, WGN, AK, BNC, BF>
+    gemm16_pipe<BM, BN, BK, WGM, WGN, AK, BNC, BF>
         <<<a.tiles_m * a.tiles_n, 64 * WGM * WGN, 0, st>>>(a);
 }
 
@@ -706,21 +808,21 @@ constexpr int kNumCfgs = 9;
 inline int cfg_bk16(int cfg) { return cfg >= 5 ? 64 : 32; }
 
 template <bool AK, bool BNC, bool BF>
-void launch_layout(const Args &a, bool vec, bool dma, int cfg, hipStream_t st) {
+void launch_layout(const Args &a, bool vec, bool pipe, int cfg, hipStream_t st) {
     if (!vec) {
         launch_one<64, 64, 2, 2, 32, AK, BNC, false, BF>(a, st);
         return;
     }
-    if (dma && cfg != 3) {
+    if (pipe && cfg != 3) {
         switch (cfg) {
-            case 0: launch_dma16<256, 256, 2, 2, 32, AK, BNC, BF>(a, st); break;
-            case 1: launch_dma16<256, 256, 2, 4, 32, AK, BNC, BF>(a, st); break;
-            case 2: launch_dma16<128, 128, 2, 2, 32, AK, BNC, BF>(a, st); break;
-            case 4: launch_dma16<256, 128, 2, 2, 32, AK, BNC, BF>(a, st); break;
-            case 5: launch_dma16<256, 256, 2, 2, 64, AK, BNC, BF>(a, st); break;
-            case 6: launch_dma16<256, 256, 2, 4, 64, AK, BNC, BF>(a, st); break;
-            case 7: launch_dma16<256, 128, 2, 2, 64, AK, BNC, BF>(a, st); break;
-            default: launch_dma16<256, 128, 4, 2, 64, AK, BNC, BF>(a, st); break;
+            case 0: launch_pipe16<256, 256, 2, 2, 32, AK, BNC, BF>(a, st); break;
+            case 1: launch_pipe16<256, 256, 2, 4, 32, AK, BNC, BF>(a, st); break;
+            case 2: launch_pipe16<128, 128, 2, 2, 32, AK, BNC, BF>(a, st); break;
+            case 4: launch_pipe16<256, 128, 2, 2, 32, AK, BNC, BF>(a, st); break;
+            case 5: launch_pipe16<256, 256, 2, 2, 64, AK, BNC, BF>(a, st); break;
+            case 6: launch_pipe16<256, 256, 2, 4, 64, AK, BNC, BF>(a, st); break;
+            case 7: launch_pipe16<256, 128, 2, 2, 64, AK, BNC, BF>(a, st); break;
+            default: launch_pipe16<256, 128, 4, 2, 64, AK, BNC, BF>(a, st); break;
         }
         return;
     }
@@ -738,8 +840,8 @@ void launch_layout(const Args &a, bool vec, bool dma, int cfg, hipStream_t st) {
 }
 
 // Defined in k_gemm16_{bf16,f16}.hip.  layout: FG_NN / FG_NT / FG_TN.
-void launch_bf16(int layout, const Args &a, bool vec, bool dma, int cfg, hipStream_t st);
-void launch_f16(int layout, const Args &a, bool vec, bool dma, int cfg, hipStream_t st);
+void launch_bf16(int layout, const Args &a, bool vec, bool pipe, int cfg, hipStream_t st);
+void launch_f16(int layout, const Args &a, bool vec, bool pipe, int cfg, hipStream_t st);
 
 }  // namespace gemm16
 }  // namespace fg

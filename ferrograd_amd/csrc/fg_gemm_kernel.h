@@ -427,7 +427,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_mfma(GemmArgs p) {
     store_tile<TM, TN, WTN, WGM * WGN>(p, acc, lds, m0 + wm0, n0 + wn0, wave, lane);
 }
 
-// ------------------------------------------------ direct-to-LDS variant
+// ------------------------------------------------ pipelined variant
 // The same GEMM, software-pipelined over whole K tiles: used when every
 // 16-byte chunk of a tile is either in bounds or belongs only to outputs that
 // are masked (K % BK == 0 and the VEC alignment conditions).  Rows (or

@@ -12,29 +12,33 @@ namespace {
 
 using fg::gemm16::Args;
 
-// Direct-to-LDS variant on (1) or off (0): a knob for measurement builds.
-#ifndef FG_GEMM16_DMA
-#define FG_GEMM16_DMA 1
+// Pipelined whole-tile kernel on (1) or off (0): a knob for measurement builds.
+#ifndef FG_GEMM16_PIPE
+#define FG_GEMM16_PIPE 1
 #endif
-constexpr bool kDma16 = FG_GEMM16_DMA != 0;
+constexpr bool kPipe16 = FG_GEMM16_PIPE != 0;
 
 int tiles(int M, int N, int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); }
 
 // Tile configuration (indices as in fg_gemm16_kernel.h), from a measured
-// sweep on MI355X of every configuration on the direct-to-LDS path
-// (TFLOP/s, bf16; fp16 within a few percent):
-//  * 256x256 with 8 waves and BK 64 when it gives >= one tile per CU: 908 /
-//    830 / 903 for NN / NT / TN at 4096^3, 1022 at 8192^3;
-//  * else 256x128 with 8 waves and BK 64 down to a quarter tile per CU: 607
-//    for the 2048x4096x4096 forward, 715 for its NT data gradient, 180 for
-//    the 1000-wide head, where every smaller tile measured lower;
+// sweep on MI355X of every configuration of the pipelined kernel (TFLOP/s,
+// bf16, N(0,1) operands; fp16 within a few percent):
+//  * squares that give >= one 256x256 tile per CU: NT (both operands
+//    k-contiguous) 256x256 with 8 waves and BK 64, direct loads (1178-1209
+//    at 4096^3, against 1049 for the staged BK 32 tile); NN and TN 256x256
+//    with 8 waves and BK 32, staged loads (1147 / 1073 at 4096^3, 1002 for
+//    the 4096x4096x2048 weight gradient, against 933 / 714 / 600 for the
+//    direct BK 64 tile: the compiler makes each transposing LDS read wait for
+//    every direct load in flight, as it cannot tell them apart);
+//  * else 256x128 with 8 waves and BK 64 down to a quarter tile per CU: 956
+//    for the 2048x4096x4096 forward, 799-855 for its NT data gradient, 302
+//    for the 1000-wide head, where every smaller tile measured lower;
 //  * else 128x128, else 64x64.
-// The BK 64 tiles need K % 64 == 0 for the direct-to-LDS path; when only
-// K % 32 == 0 holds, 256x256 with 8 waves and BK 32 (775 / 823 / 822) or
-// 128x128 keep it.
-int pick_cfg16(int M, int N, int K, int cus) {
+// The BK 64 tiles need K % 64 == 0; when only K % 32 == 0 holds, 256x256
+// with 8 waves and BK 32 or 128x128 keep the pipelined kernel.
+int pick_cfg16(int layout, int M, int N, int K, int cus) {
     if (K % 64 == 0) {
-        if (tiles(M, N, 256, 256) >= cus) return 6;
+        if (tiles(M, N, 256, 256) >= cus) return layout == FG_NT ? 6 : 1;
         if (tiles(M, N, 256, 128) >= cus / 4) return 8;
     } else if (K % 32 == 0) {
         if (tiles(M, N, 256, 256) >= cus) return 1;
@@ -79,23 +83,23 @@ int gemm16_common(fg_ctx *ctx, int dtype, int layout, Args &a, const char *who) 
 #ifdef FG_GEMM16_FORCE_CFG  // tuning builds: one tile configuration for every shape
     const int cfg = FG_GEMM16_FORCE_CFG;
 #else
-    const int cfg = pick_cfg16(a.M, a.N, a.K, ctx->cu_count > 0 ? ctx->cu_count : 256);
+    const int cfg = pick_cfg16(layout, a.M, a.N, a.K, ctx->cu_count > 0 ? ctx->cu_count : 256);
 #endif
-    // Direct-to-LDS loads: whole K tiles, 16-byte chunks of 8 elements along
+    // The pipelined kernel: whole K tiles, 16-byte chunks of 8 elements along
     // each row-contiguous operand's rows (B of NN / TN, A of TN).
     const bool rc_ok = (layout == FG_NT || a.N % 8 == 0) && (layout != FG_TN || a.M % 8 == 0);
-    const bool dma = kDma16 && vec && rc_ok && a.K > 0 &&
+    const bool pipe = kPipe16 && vec && rc_ok && a.K > 0 &&
                      a.K % fg::gemm16::cfg_bk16(cfg) == 0 && a.M >= 8 && a.N >= 8 && cfg != 3;
-    // Only the direct-to-LDS kernel sums B's columns; elsewhere the separate
+    // Only the pipelined kernel sums B's columns; elsewhere the separate
     // reduction runs after the GEMM (same result up to the order of the
     // fp32 sums).
-    if (colsum && !dma) a.colsum = nullptr;
+    if (colsum && !pipe) a.colsum = nullptr;
     if (dtype == FG_DTYPE_BF16)
-        fg::gemm16::launch_bf16(layout, a, vec, dma, cfg, ctx->stream);
+        fg::gemm16::launch_bf16(layout, a, vec, pipe, cfg, ctx->stream);
     else
-        fg::gemm16::launch_f16(layout, a, vec, dma, cfg, ctx->stream);
+        fg::gemm16::launch_f16(layout, a, vec, pipe, cfg, ctx->stream);
     FG_LAUNCH_CHECK(who);
-    if (colsum && !dma)
+    if (colsum && !pipe)
         return fg_bias_grad(ctx, dtype, a.K, a.N, a.B, a.ldb, colsum, a.colsum_accumulate);
     return FG_OK;
 }

@@ -7,11 +7,11 @@
 namespace fg {
 namespace gemm16 {
 
-void launch_bf16(int layout, const Args &a, bool vec, bool dma, int cfg, hipStream_t st) {
+void launch_bf16(int layout, const Args &a, bool vec, bool pipe, int cfg, hipStream_t st) {
     switch (layout) {
-        case FG_NN: launch_layout<true, true, true>(a, vec, dma, cfg, st); break;
-        case FG_NT: launch_layout<true, false, true>(a, vec, dma, cfg, st); break;
-        default: launch_layout<false, true, true>(a, vec, dma, cfg, st); break;
+        case FG_NN: launch_layout<true, true, true>(a, vec, pipe, cfg, st); break;
+        case FG_NT: launch_layout<true, false, true>(a, vec, pipe, cfg, st); break;
+        default: launch_layout<false, true, true>(a, vec, pipe, cfg, st); break;
     }
 }
 

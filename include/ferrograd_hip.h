@@ -170,7 +170,7 @@ int fg_gemm_dw_f32(fg_ctx *ctx, int M, int N, int K, const float *d_A, int lda,
 /* The same for 16-bit tensors (dtype FG_DTYPE_F16 / FG_DTYPE_BF16 for every
  * operand, colsum included): C as fg_gemm_x16 in the TN layout; colsum[n]
  * (=|+=) sum_k B[k][n] summed in fp32 and rounded to dtype once (with
- * colsum_accumulate: round(colsum + sum)). Shapes off the direct-to-LDS
+ * colsum_accumulate: round(colsum + sum)). Shapes off the pipelined
  * path (K not a multiple of the tile depth, unaligned rows) take the GEMM
  * plus fg_bias_grad's reduction: the same values up to the order of the
  * fp32 sums. Replaces the 16-bit dB lowering (matmul/mod.rs:85-94) and the

@@ -252,8 +252,8 @@ def test_bias_grad_parity(gpu_ctx, shape):
 def test_gemm_dw_fused_bias_grad(gpu_ctx, shape):
     """dW = A^T.dZ and dbias = column sums of dZ in one launch (TN layout):
     dW to the GEMM tolerance, dbias to 1e-5 of the float64 column sums, both
-    with and without accumulation.  The shapes cover the direct-to-LDS path
-    (K a multiple of 32) and the register-staged one (K = 300, 33)."""
+    with and without accumulation.  The shapes cover the pipelined path
+    (K a multiple of 32) and the other kernel (K = 300, 33)."""
     M, N, K = shape  # dW is M x N; the reduction runs over K rows
     note(f"gemm_dw M={M} N={N} K={K}")
     rng = np.random.default_rng(M + 3 * N + K)

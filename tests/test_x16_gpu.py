@@ -148,7 +148,7 @@ def test_gemm_x16_exact_bits(gpu_ctx, dtype, layout, shape):
 def test_gemm_x16_exact_bits_large_tiles(gpu_ctx, dtype, case):
     """Shapes large enough for the 256-wide tile configurations the
     dispatcher picks for full-chip GEMMs (8-wave 256x256 and 256x128 at
-    BK 64, 256x256 at BK 32, 128x128), on the direct-to-LDS path (K a
+    BK 64, 256x256 at BK 32, 128x128), on the pipelined path (K a
     multiple of 32 or 64; edge tiles in M and N) and off it (K = 48)."""
     layout, M, N, K = case
     note(f"gemm_x16 exact large {DT_IDS[dtype]} layout={layout} {M}x{N}x{K}")
@@ -330,7 +330,7 @@ def test_gemm_dw_x16_fused_bias_grad(gpu_ctx, dtype, shape):
     """dW = A^T.dZ and dbias = column sums of dZ in one call (TN layout): on
     k/4 operands every fp32 sum is exact in any order, so both 16-bit results
     equal the oracle's bit for bit, with and without accumulation.  The
-    shapes take the direct-to-LDS kernels that sum the columns in the GEMM
+    shapes take the pipelined kernels that sum the columns in the GEMM
     (8-wave 256x256 and 256x128 tiles at BK 64 with edge tiles, 4-wave
     128x128 at BK 32) and the fallback of GEMM + separate reduction (K off
     the tile depth, unaligned, N = 10, no rows, K = 0)."""
