@@ -35,13 +35,16 @@ int tiles(int M, int N, int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn 
 //    for the 1000-wide head, where every smaller tile measured lower;
 //  * else 128x128, else 64x64.
 // The BK 64 tiles need K % 64 == 0; when only K % 32 == 0 holds, 256x256
-// with 8 waves and BK 32 or 128x128 keep the pipelined kernel.
+// with 8 waves and BK 32 or 128x128 keep the pipelined kernel.  Other K take
+// gemm16_mfma, with 256x128 / 8 waves where it gives a quarter tile per CU.
 int pick_cfg16(int layout, int M, int N, int K, int cus) {
     if (K % 64 == 0) {
         if (tiles(M, N, 256, 256) >= cus) return layout == FG_NT ? 6 : 1;
         if (tiles(M, N, 256, 128) >= cus / 4) return 8;
     } else if (K % 32 == 0) {
         if (tiles(M, N, 256, 256) >= cus) return 1;
+    } else if (tiles(M, N, 256, 128) >= cus / 4) {
+        return 8;  // gemm16_mfma: 529 against 453 for 128x128 (2048x4096x1000 NT)
     }
     if (tiles(M, N, 128, 128) >= cus / 4) return 2;
     return 3;
