@@ -230,6 +230,39 @@ def test_gemm_pipe_configs_sampled(gpu_ctx, case):
         assert normwise_rel(host(dC)[rows], ref) < tol
 
 
+@pytest.mark.parametrize("layout", [O.NN, O.NT, O.TN], ids=["NN", "NT", "TN"])
+@pytest.mark.parametrize("shape", [(2048, 4096, 512), (1024, 1024, 256), (200, 136, 64)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_gemm_pipe_strided_accumulate(gpu_ctx, layout, shape):
+    """The pipelined kernel on operands and output with leading dimensions
+    wider than their rows (padding filled with NaN, which must not be
+    read into valid outputs) and C += A.B into a NaN-free C: checked in full
+    against float64, padding of C untouched."""
+    torch = _torch()
+    M, N, K = shape
+    note(f"gemm pipe strided accumulate layout={layout} M={M} N={N} K={K}")
+    rng = np.random.default_rng(M + 3 * N + 7 * K + layout)
+    A = rng.standard_normal((M, K)).astype(f32)
+    B = (0.05 * rng.standard_normal((K, N))).astype(f32)
+    As, Bs = storage(layout, A, B)
+    pa, pb, pc = 8, 4, 12
+    Ap = np.full((As.shape[0], As.shape[1] + pa), np.nan, f32)
+    Ap[:, :As.shape[1]] = As
+    Bp = np.full((Bs.shape[0], Bs.shape[1] + pb), np.nan, f32)
+    Bp[:, :Bs.shape[1]] = Bs
+    C0 = rng.standard_normal((M, N)).astype(f32)
+    Cp = np.full((M, N + pc), -7.0, f32)
+    Cp[:, :N] = C0
+    dC = dev(Cp)
+    gpu_ctx.gemm(layout, M, N, K, dev(Ap), Ap.shape[1], dev(Bp), Bp.shape[1], dC, N + pc,
+                 accumulate=True)
+    got = host(dC)
+    ref = C0.astype(np.float64) + A.astype(np.float64) @ B.astype(np.float64)
+    assert normwise_rel(got[:, :N], ref) < 1e-5 * math.sqrt(K)
+    assert np.array_equal(got[:, N:], Cp[:, N:])
+    del torch
+
+
 # ----------------------------------------------------- bias grad, act bwd
 @pytest.mark.parametrize("shape", [(2048, 4096), (64, 10), (1, 5), (1000, 1000), (3, 4097),
                                    (4096, 1000)], ids=lambda s: "x".join(map(str, s)))
