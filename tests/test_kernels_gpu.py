@@ -185,6 +185,8 @@ def test_gemm_c2_full_size_sampled(gpu_ctx):
     (O.NT, 2048, 2000, 1024, "fwd"),   # 128x128
     (O.NN, 2048, 1000, 4096, "fwd"),   # 128x64 (c5 head)
     (O.TN, 1000, 4096, 2048, "bwd"),   # 128x64; partial M tile
+    (O.NN, 2048, 4096, 32, "fwd"),     # one K tile (256x128, 8 waves, BK 32)
+    (O.TN, 4096, 4096, 16, "fwd"),     # one K tile (256x128, 4 waves, BK 16)
     # K % BK != 0: the register-staged kernel with the same tiles
     (O.NT, 2048, 4096, 1000, "bwd"),   # 256x128, 8 waves (c5 head dA)
     (O.TN, 1024, 4096, 1000, "fwd"),   # 128x64, row-contiguous operands
