@@ -87,7 +87,33 @@ struct GemmArgs {
     // tiles already in LDS by the workgroups of the first tile row.
     float *colsum;
     int colsum_accumulate;
+    // Split K (0: off): workgroup row blockIdx.y multiplies the K slice
+    // [ksplit * y, ksplit * (y + 1)) into its own M x N slot of `partial`
+    // (row stride N); splitk_reduce then sums the slots in order and applies
+    // the epilogue.
+    float *partial;
+    int ksplit;
 };
+
+// The view of a split-K workgroup: its K slice of A and B, its raw-product
+// slot as C, no epilogue.
+template <bool AK, bool BNC>
+__device__ __forceinline__ void split_k_view(GemmArgs &p) {
+    if (p.ksplit <= 0) return;
+    const int s = blockIdx.y, kb = s * p.ksplit;
+    p.A += AK ? (size_t)kb : (size_t)kb * p.lda;
+    p.B += BNC ? (size_t)kb * p.ldb : (size_t)kb;
+    p.K = min(p.ksplit, p.K - kb);
+    p.C = p.partial + (size_t)s * p.M * p.N;
+    p.ldc = p.N;
+    p.mode = 0;
+    p.act = kActNone;
+    p.bias = nullptr;
+    p.Z = nullptr;
+    p.accumulate = 0;
+    p.colsum = nullptr;
+    p.vec_out = p.N % 4 == 0;
+}
 
 // Column sums of the B tiles (TN layout, B row-contiguous [k][n]) for the
 // workgroups of tile row 0: thread t owns column t % BN and k-rows
@@ -324,6 +350,7 @@ __device__ __forceinline__ void store_tile(const GemmArgs &p, const f32x16 (&acc
 
 template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC, bool VEC>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_mfma(GemmArgs p) {
+    split_k_view<AK, BNC>(p);
     constexpr int NT = 64 * WGM * WGN;
     static_assert(WGM * WGN == 4 || WGM * WGN == 8, "4 or 8 waves per workgroup");
     constexpr int WTM = BM / WGM, WTN = BN / WGN;
@@ -463,6 +490,7 @@ __device__ __forceinline__ int swz_r(int k) { return ((k >> 3) & 1) * 8; }
 
 template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_pipe(GemmArgs p) {
+    split_k_view<AK, BNC>(p);
     constexpr int NW = WGM * WGN;
     constexpr int WTM = BM / WGM, WTN = BN / WGN;
     constexpr int TM = WTM / 32, TN = WTN / 32;
@@ -772,7 +800,9 @@ void launch_pipe(const GemmArgs &a0, hipStream_t st) {
     GemmArgs a = a0;
     a.tiles_m = (a.M + BM - 1) / BM;
     a.tiles_n = (a.N + BN - 1) / BN;
-    gemm_f32_pipe<BM, BN, BK, WGM, WGN, AK, BNC><<<a.tiles_m * a.tiles_n, 64 * WGM * WGN, 0, st>>>(a);
+    const int splits = a.ksplit > 0 ? (a.K + a.ksplit - 1) / a.ksplit : 1;
+    gemm_f32_pipe<BM, BN, BK, WGM, WGN, AK, BNC>
+        <<<dim3(a.tiles_m * a.tiles_n, splits), 64 * WGM * WGN, 0, st>>>(a);
 }
 
 template <int BM, int BN, int WGM, int WGN, int BK, bool AK, bool BNC, bool VEC>
@@ -780,8 +810,9 @@ void launch_one(const GemmArgs &a0, hipStream_t st) {
     GemmArgs a = a0;
     a.tiles_m = (a.M + BM - 1) / BM;
     a.tiles_n = (a.N + BN - 1) / BN;
+    const int splits = a.ksplit > 0 ? (a.K + a.ksplit - 1) / a.ksplit : 1;
     gemm_f32_mfma<BM, BN, BK, WGM, WGN, AK, BNC, VEC>
-        <<<a.tiles_m * a.tiles_n, 64 * WGM * WGN, 0, st>>>(a);
+        <<<dim3(a.tiles_m * a.tiles_n, splits), 64 * WGM * WGN, 0, st>>>(a);
 }
 
 // Tile configurations (index: BM x BN, waves, K depth):
@@ -794,6 +825,14 @@ constexpr int kNumCfgs = 8;
 
 // K depth of a configuration.
 inline int cfg_bk(int cfg) { return (cfg == 3 || cfg >= 5) ? 32 : (cfg == 4 ? 16 : kBK); }
+
+// Output tile of a configuration (the element-load variant is 64x64).
+inline void cfg_tile(int cfg, bool vec, int &bm, int &bn) {
+    static const int kBm[kNumCfgs] = {256, 256, 128, 128, 64, 128, 256, 256};
+    static const int kBn[kNumCfgs] = {256, 128, 256, 128, 64, 64, 256, 128};
+    bm = vec ? kBm[cfg] : 64;
+    bn = vec ? kBn[cfg] : 64;
+}
 
 // pipe: K % cfg_bk(cfg) == 0 and the VEC conditions hold (the host checks):
 // the pipelined whole-tile kernel with the same tile shape.

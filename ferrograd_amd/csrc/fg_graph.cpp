@@ -1882,11 +1882,18 @@ FG_API int fg_plan_describe(const fg_plan *p, char *buf, size_t len, size_t *nee
     };
     // Kernel dispatches per planned launch: the bias-gradient reduction is a
     // partial and a final pass, the fused softmax + CE adds the mean-loss
-    // reduction, the Adam update is preceded by its step-counter advance.
+    // reduction, an fp32 GEMM that splits K adds its summing epilogue, the
+    // Adam update is preceded by its step-counter advance.
     auto kernels = [&](const std::vector<Launch> &v) {
         int n = 0;
-        for (const Launch &L : v)
-            n += (L.kind == LK_BIAS_GRAD || (L.kind == LK_SMCE && L.sBias != kNone)) ? 2 : 1;
+        for (const Launch &L : v) {
+            if ((L.kind == LK_GEMM || L.kind == LK_GEMM_BWD) && L.dtype == FG_DTYPE_F32)
+                n += fg::gemm_f32_dispatches(p->ctx, L.sExtra != kNone ? FG_TN : L.layout, L.M,
+                                             L.N, L.K, p->ptr(L.sA), L.lda, p->ptr(L.sB), L.ldb,
+                                             L.kind == LK_GEMM && L.sExtra != kNone);
+            else
+                n += (L.kind == LK_BIAS_GRAD || (L.kind == LK_SMCE && L.sBias != kNone)) ? 2 : 1;
+        }
         return n;
     };
     add("forward", p->fwd);

@@ -54,6 +54,10 @@ int mt_adam_dev(fg_ctx *ctx, fg_mt *mt, float lr, float b1, float b2, float eps,
 // Elementwise program launch (k_eltwise_prog.hip).
 struct EltProgram;
 int launch_eltwise(fg_ctx *ctx, const EltProgram &p);
+// Kernel dispatches of one fp32 GEMM call with these operands (2 when K is
+// split: the slices, then the summing epilogue), for plan descriptions.
+int gemm_f32_dispatches(fg_ctx *ctx, int layout, int M, int N, int K, const void *A, int lda,
+                        const void *B, int ldb, bool colsum);
 }  // namespace fg
 
 #define FG_HIP(call)                                                     \

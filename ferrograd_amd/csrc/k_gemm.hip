@@ -57,6 +57,81 @@ int pick_cfg(int layout, int M, int N, int K, int cus) {
     return 4;
 }
 
+// Split-K epilogue: out[m][n] = epilogue(sum over the slots, in order, of
+// partial[s][m][n]) -- the same per-element operations as the GEMM kernels'
+// epilogue (fg_gemm_kernel.h epi_value), so bias / activation / Z / act' /
+// accumulate behave alike.  Deterministic: the slot order is fixed.
+__global__ __launch_bounds__(kThreads) void splitk_reduce(GemmArgs p, int splits) {
+    const size_t mn = (size_t)p.M * p.N;
+    for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < mn;
+         i += (size_t)gridDim.x * kThreads) {
+        const int row = (int)(i / p.N), col = (int)(i % p.N);
+        float v = p.partial[i];
+        for (int s = 1; s < splits; ++s) v += p.partial[s * mn + i];
+        const float b = (p.mode == 0 && p.bias) ? p.bias[col] : 0.0f;
+        float z;
+        float o = fg::gemm::epi_value(p, v, b, row, col, &z);
+        if (p.mode == 0 && p.Z) p.Z[(size_t)row * p.ldz + col] = z;
+        float *c = p.C + (size_t)row * p.ldc + col;
+        if (p.accumulate) o += *c;
+        *c = o;
+    }
+}
+
+// Split K over workgroup rows when the output gives few tiles (under half
+// the CUs) and K is long (at least 4 K tiles per slice): each slice's raw
+// product goes to the context's workspace, which must already hold them
+// (a plan reserves 1 MiB; the workspace is never grown here, so launches
+// stay capturable).  The fused column sum of fg_gemm_dw is not split.
+// Returns the number of slices (1: no split).
+int plan_split_k(fg_ctx *ctx, GemmArgs &a, int cfg, bool vec) {
+    if (a.colsum || a.K <= 0) return 1;
+    int bm, bn;
+    fg::gemm::cfg_tile(cfg, vec, bm, bn);
+    const int bk = vec ? fg::gemm::cfg_bk(cfg) : 16;
+    const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    int s = std::min(cus / (2 * tiles(a.M, a.N, bm, bn)), a.K / (4 * bk));
+    if (s < 2) return 1;
+    int ks = (a.K + s - 1) / s;
+    ks = (ks + bk - 1) / bk * bk;  // whole K tiles per slice
+    s = (a.K + ks - 1) / ks;
+    if (s < 2 || (uint64_t)s * a.M * a.N * sizeof(float) > ctx->ws_bytes) return 1;
+    a.partial = static_cast<float *>(ctx->ws);
+    a.ksplit = ks;
+    return s;
+}
+
+// The kernel choices of one GEMM call (sets a.vec_out, and a.partial /
+// a.ksplit when K is split): 16-byte operand loads (vec), the pipelined
+// kernel (pipe), the tile configuration and the number of K slices.
+void plan_gemm(fg_ctx *ctx, int layout, GemmArgs &a, bool &vec, bool &pipe, int &cfg,
+               int &splits) {
+    // The 16-byte path needs 16-byte aligned bases and every row start
+    // aligned, i.e. leading dimensions and the contiguous extents that the
+    // bounds checks split on (K for k-contiguous operands, M / N otherwise)
+    // divisible by 4.
+    const bool aligned_ptrs = ((((uintptr_t)a.A) | ((uintptr_t)a.B)) & 15u) == 0;
+    vec = aligned_ptrs && a.lda % 4 == 0 && a.ldb % 4 == 0;
+    if (layout == FG_NN) vec = vec && a.K % 4 == 0 && a.N % 4 == 0;
+    if (layout == FG_NT) vec = vec && a.K % 4 == 0;
+    if (layout == FG_TN) vec = vec && a.M % 4 == 0 && a.N % 4 == 0;
+#ifdef FG_GEMM_FORCE_CFG  // tuning builds: one tile configuration for every shape
+    cfg = FG_GEMM_FORCE_CFG;
+#else
+    cfg = pick_cfg(layout, a.M, a.N, a.K, ctx->cu_count > 0 ? ctx->cu_count : 256);
+#endif
+    auto al16 = [](const void *q) { return (((uintptr_t)q) & 15u) == 0; };
+    a.vec_out = al16(a.C) && a.ldc % 4 == 0 && (!a.Z || (al16(a.Z) && a.ldz % 4 == 0)) &&
+                (!a.bias || al16(a.bias));
+    // The pipelined kernel's 16-byte tile loads need whole K tiles (a partial
+    // one would bring neighbouring k into valid outputs) and at least one
+    // 16-byte chunk per row-contiguous operand row (edge chunks are clamped,
+    // not masked).
+    pipe = fg::gemm::kPipe && vec && a.K > 0 && a.K % fg::gemm::cfg_bk(cfg) == 0 && a.M >= 4 &&
+           a.N >= 4;
+    splits = plan_split_k(ctx, a, cfg, vec);
+}
+
 int gemm_common(fg_ctx *ctx, int layout, GemmArgs &a, const char *who) {
     FG_REQUIRE(ctx, FG_ERR_INVALID_ARGUMENT, "%s: ctx is NULL", who);
     FG_REQUIRE(layout >= FG_NN && layout <= FG_TN, FG_ERR_INVALID_ARGUMENT, "%s: bad layout %d",
@@ -74,37 +149,49 @@ int gemm_common(fg_ctx *ctx, int layout, GemmArgs &a, const char *who) {
                a.ldb, a.ldc);
     FG_HIP(hipSetDevice(ctx->device));
     if (a.K == 0) a.A = a.B;  // loads are all masked; K=0 yields the epilogue of zero
-    // The 16-byte path needs 16-byte aligned bases and every row start
-    // aligned, i.e. leading dimensions and the contiguous extents that the
-    // bounds checks split on (K for k-contiguous operands, M / N otherwise)
-    // divisible by 4.
-    const bool aligned_ptrs = ((((uintptr_t)a.A) | ((uintptr_t)a.B)) & 15u) == 0;
-    bool vec = aligned_ptrs && a.lda % 4 == 0 && a.ldb % 4 == 0;
-    if (layout == FG_NN) vec = vec && a.K % 4 == 0 && a.N % 4 == 0;
-    if (layout == FG_NT) vec = vec && a.K % 4 == 0;
-    if (layout == FG_TN) vec = vec && a.M % 4 == 0 && a.N % 4 == 0;
-#ifdef FG_GEMM_FORCE_CFG  // tuning builds: one tile configuration for every shape
-    const int cfg = FG_GEMM_FORCE_CFG;
-#else
-    const int cfg = pick_cfg(layout, a.M, a.N, a.K, ctx->cu_count > 0 ? ctx->cu_count : 256);
-#endif
-    auto al16 = [](const void *q) { return (((uintptr_t)q) & 15u) == 0; };
-    a.vec_out = al16(a.C) && a.ldc % 4 == 0 && (!a.Z || (al16(a.Z) && a.ldz % 4 == 0)) &&
-                (!a.bias || al16(a.bias));
-    // The pipelined kernel's 16-byte tile loads need whole K tiles (a partial
-    // one would bring neighbouring k into valid outputs) and at least one
-    // 16-byte chunk per row-contiguous operand row (edge chunks are clamped,
-    // not masked).
-    const bool pipe = fg::gemm::kPipe && vec && a.K > 0 && a.K % fg::gemm::cfg_bk(cfg) == 0 &&
-                      a.M >= 4 && a.N >= 4;
+    bool vec, pipe;
+    int cfg, splits;
+    plan_gemm(ctx, layout, a, vec, pipe, cfg, splits);
     switch (layout) {
         case FG_NN: fg::gemm::launch_nn(a, vec, pipe, cfg, ctx->stream); break;
         case FG_NT: fg::gemm::launch_nt(a, vec, pipe, cfg, ctx->stream); break;
         default: fg::gemm::launch_tn(a, vec, pipe, cfg, ctx->stream); break;
     }
     FG_LAUNCH_CHECK(who);
+    if (splits > 1) {
+        const size_t mn = (size_t)a.M * a.N;
+        const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+        const int grid = (int)std::min<size_t>((mn + kThreads - 1) / kThreads, 4 * (size_t)cus);
+        splitk_reduce<<<grid, kThreads, 0, ctx->stream>>>(a, splits);
+        FG_LAUNCH_CHECK(who);
+    }
     return FG_OK;
 }
+
+}  // namespace
+
+namespace fg {
+int gemm_f32_dispatches(fg_ctx *ctx, int layout, int M, int N, int K, const void *A, int lda,
+                        const void *B, int ldb, bool colsum) {
+    if (!ctx || M <= 0 || N <= 0) return 1;  // no workspace (or nothing to do): no split
+    GemmArgs a{};
+    a.A = static_cast<const float *>(A);
+    a.B = static_cast<const float *>(B);
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.lda = lda;
+    a.ldb = ldb;
+    a.colsum = colsum ? reinterpret_cast<float *>(1) : nullptr;  // only tested for null
+    if (K == 0) a.A = a.B;
+    bool vec, pipe;
+    int cfg, splits;
+    plan_gemm(ctx, layout, a, vec, pipe, cfg, splits);
+    return splits > 1 ? 2 : 1;
+}
+}  // namespace fg
+
+namespace {
 
 // ----------------------------------------------------------- bias grad
 // Column sums of dZ[M][N]: phase 1 -- grid (column strips of 256 columns,

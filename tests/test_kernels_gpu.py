@@ -265,6 +265,70 @@ def test_gemm_pipe_strided_accumulate(gpu_ctx, layout, shape):
     del torch
 
 
+@pytest.mark.parametrize("case", [
+    # (layout, M, N, K, mode, act, accumulate): outputs of a few tiles with
+    # long K, which split K over workgroups when the workspace holds the slots
+    (O.NN, 64, 256, 784, "fwd", O.ACT_RELU, False),   # c1 layer 1 (4 tiles)
+    (O.NN, 64, 10, 256, "fwd", O.ACT_NONE, False),    # c1 layer 2 (N = 10: element loads)
+    (O.NT, 64, 784, 256, "bwd", O.ACT_NONE, False),   # c1 dX
+    (O.NN, 100, 200, 3000, "fwd", O.ACT_GELU, False),  # edge tiles, K off the tile depth
+    (O.NT, 96, 128, 4096, "bwd", O.ACT_GELU, False),   # act' of a saved Zs
+    (O.TN, 128, 64, 2048, "fwd", O.ACT_NONE, True),    # C += A^T.B
+], ids=lambda c: f"{['NN', 'NT', 'TN'][c[0]]}-{c[1]}x{c[2]}x{c[3]}-{c[4]}-act{c[5]}"
+                 f"{'-acc' if c[6] else ''}")
+def test_gemm_split_k(gpu_ctx, case):
+    """Split-K GEMMs (slots summed in a fixed order, then the epilogue):
+    against float64 with the CPU oracle's epilogue, bit-identical on a
+    second run, and within tolerance of the unsplit kernel (a context with
+    no workspace)."""
+    torch = _torch()
+    import ferrograd_amd as fa
+    layout, M, N, K, mode, act, acc = case
+    note(f"gemm split-K layout={layout} M={M} N={N} K={K} mode={mode} act={act} acc={acc}")
+    rng = np.random.default_rng(M * 5 + N + K + layout)
+    A = rng.standard_normal((M, K)).astype(f32)
+    B = (0.05 * rng.standard_normal((K, N))).astype(f32)
+    bias = (0.1 * rng.standard_normal(N)).astype(f32)
+    Zs = rng.standard_normal((M, N)).astype(f32)
+    C0 = rng.standard_normal((M, N)).astype(f32)
+    As, Bs = storage(layout, A, B)
+    dA, dB, db, dZs = dev(As), dev(Bs), dev(bias), dev(Zs)
+
+    def run(ctx):
+        dC = dev(C0) if acc else empty((M, N))
+        dZ = empty((M, N))
+        if mode == "fwd":
+            ctx.gemm(layout, M, N, K, dA, As.shape[1], dB, Bs.shape[1], dC, N,
+                     bias=None if acc else db, act=act, Z=None if acc else dZ, ldz=N,
+                     accumulate=acc)
+        else:
+            ctx.gemm_bwd(layout, M, N, K, dA, As.shape[1], dB, Bs.shape[1], dC, N, act=act,
+                         Zs=dZs, ldzs=N)
+        return host(dC), host(dZ)
+
+    gpu_ctx.reserve_workspace(16 << 20)
+    C1, Z1 = run(gpu_ctx)
+    C2, Z2 = run(gpu_ctx)
+    assert np.array_equal(C1, C2)
+    P = A.astype(np.float64) @ B.astype(np.float64)
+    tol = 1e-5 * math.sqrt(K)
+    if mode == "fwd" and acc:
+        assert normwise_rel(C1, C0 + P) < tol
+    elif mode == "fwd":
+        Zr = P + bias
+        assert normwise_rel(Z1, Zr) < tol
+        assert normwise_rel(C1, O.act(act, Zr)) < tol
+    else:
+        assert normwise_rel(C1, O.act_bwd(act, P, Zs)) < tol
+    plain = fa.Context(0, torch.cuda.current_stream().cuda_stream)  # no workspace: no split
+    try:
+        C3, _ = run(plain)
+    finally:
+        plain.sync()
+        plain.close()
+    assert normwise_rel(C1, C3) < tol
+
+
 # ----------------------------------------------------- bias grad, act bwd
 @pytest.mark.parametrize("shape", [(2048, 4096), (64, 10), (1, 5), (1000, 1000), (3, 4097),
                                    (4096, 1000)], ids=lambda s: "x".join(map(str, s)))
