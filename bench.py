@@ -437,7 +437,12 @@ def only_gemm_bf16_c2(ctx, reps):
         ctx.gemm_x16(bf, fa.TN, n, n, n, A, n, dC, n, dB, n)
 
 
+def only_c1_step(ctx, reps):
+    print(json.dumps(c1_component(ctx, steps=max(reps, 10))), flush=True)
+
+
 ONLY = {
+    "c1_step": only_c1_step,
     "c5_step": only_c5_step,
     "c5_step_bf16": only_c5_step_bf16,
     "gemm_bf16_c2": only_gemm_bf16_c2,
