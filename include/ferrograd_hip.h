@@ -121,7 +121,7 @@ typedef enum fg_act { FG_ACT_NONE = 0, FG_ACT_RELU = 1, FG_ACT_GELU = 2 } fg_act
  * An output of few tiles with a long K (and the backward form below) may be
  * split over K into the context's workspace when what is already reserved
  * holds the slices (it is never grown for this), then summed in a fixed
- * order: deterministic, within the GEMM tolerance of the unsplit sum. */
+ * order: deterministic, within the GEMM tolerance of the unsplit sum.
  * Replaces the matmul-rooted fused kernel (forward.rs:298-464 with
  * generic.rs:13-325) plus the bias/activation consumers inlined after it. */
 int fg_gemm_f32(fg_ctx *ctx, int layout, int M, int N, int K,

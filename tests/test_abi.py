@@ -37,6 +37,24 @@ def test_library_exports_every_declared_symbol():
         declared ^ set(_lib.SIGNATURES))
 
 
+@pytest.mark.parametrize("lang,compiler", [("c", "gcc"), ("c++", "g++")])
+def test_headers_compile_standalone(lang, compiler, tmp_path):
+    """Every public header is valid C and C++ on its own (a library built
+    before a header edit would hide a broken declaration from the symbol
+    check above)."""
+    import shutil
+    import subprocess
+    if shutil.which(compiler) is None:
+        pytest.skip(f"{compiler} not installed")
+    for fn in sorted(os.listdir(os.path.join(ROOT, "include"))):
+        if not fn.endswith(".h"):
+            continue
+        r = subprocess.run([compiler, "-fsyntax-only", "-Wall", "-Werror", "-x", lang,
+                            os.path.join(ROOT, "include", fn)],
+                           capture_output=True, text=True, cwd=tmp_path)
+        assert r.returncode == 0, f"{fn} ({lang}):\n{r.stderr}"
+
+
 def test_version_and_error_message():
     lib = _lib.load()
     assert lib.fg_version() >= 100
