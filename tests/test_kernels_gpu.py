@@ -401,6 +401,32 @@ def check_softmax_ce(ctx, x, labels, scale=1.0):
     assert abs(float(host(mean)[0]) - m) <= 1e-5 * max(1.0, abs(m))
 
 
+def test_softmax_ce_mean_across_paths(gpu_ctx):
+    """Calls of changing row counts, on the register path (C % 4 == 0, 256
+    and 512 threads), the streaming path (C = 10) and the 16-bit path: each
+    mean loss matches the float64 mean of the row losses the same call
+    wrote, and a mean requested without row losses (the row losses then go
+    to the context's workspace) is the same value."""
+    torch = _torch()
+    import ferrograd_amd as fa
+    rng = np.random.default_rng(5)
+    for R, C, dt in [(8192, 1000, None), (3, 10, None), (1, 32000, None), (600, 10, None),
+                     (257, 1000, fa.DTYPE_BF16), (2, 64, fa.DTYPE_BF16), (65, 20000, None)]:
+        note(f"softmax_ce mean R={R} C={C} dtype={dt}")
+        x = (2 * rng.standard_normal((R, C))).astype(f32)
+        lab = rng.integers(0, C, R).astype(np.uint32)
+        dl = dev(lab.view(np.int32))
+        loss, mean, mean2 = empty((R,)), empty((1,)), empty((1,))
+        dx = dev(x) if dt is None else dev(x).to(torch.bfloat16)
+        dt = fa.DTYPE_F32 if dt is None else dt
+        gpu_ctx.softmax_ce(dx, C, dl, R, C, 1.0, row_loss=loss, mean_loss=mean, dtype=dt)
+        gpu_ctx.softmax_ce(dx, C, dl, R, C, 1.0, mean_loss=mean2, dtype=dt)
+        rl = host(loss).astype(np.float64)
+        m, m2 = float(host(mean)[0]), float(host(mean2)[0])
+        assert abs(m - rl.mean()) <= 1e-6 * max(1.0, abs(rl.mean())), (R, C, m, rl.mean())
+        assert m2 == m
+
+
 def test_softmax_ce_fixture(gpu_ctx):
     note("softmax_ce fixture 9x37")
     g = golden("softmax_ce_9x37.npz")
