@@ -289,6 +289,12 @@ struct fg_plan {
     std::vector<fg_mt *> mt_single;
     bool mt_dirty = true;
     float lr = 1e-3f, b1 = 0.9f, b2 = 0.999f, eps = 1e-8f;
+    // The plan's own view of its context: same device and stream, with a
+    // fixed workspace inside the arena (split-K slices, bias-gradient
+    // partials).  Captured steps bake this address in; it lives exactly as
+    // long as the plan, and other plans or direct calls never touch it.
+    fg_ctx wctx;
+    int ws_slot = kNone;
     uint64_t ws_bytes = 0;
     std::vector<uint32_t> saved_nodes, grad_nodes;
     hipGraph_t graph = nullptr;
@@ -1059,7 +1065,7 @@ int check_launch(const fg_plan &P, const Launch &L) {
 
 // ------------------------------------------------------------ execute
 int run(fg_plan &P, const std::vector<Launch> &list) {
-    fg_ctx *ctx = P.ctx;
+    fg_ctx *ctx = &P.wctx;
     for (const Launch &L : list) {
         int rc = FG_OK;
         switch (L.kind) {
@@ -1491,6 +1497,19 @@ FG_API int fg_plan_create(fg_ctx *ctx, const fg_graph *g, const uint32_t *meta, 
         for (const Launch &L : *list)
             if ((rc = check_launch(*P, L))) return rc;
 
+    // Workspace: at least 1 MiB (what lets few-tile GEMMs split K), and the
+    // partial sums of the largest unfused bias-gradient reduction.
+    {
+        const int cus = ctx && ctx->cu_count > 0 ? ctx->cu_count : 256;
+        uint64_t ws = 1u << 20;
+        for (auto *list : {&P->bwd_seed, &P->bwd_fused})
+            for (const Launch &L : *list)
+                if (L.kind == LK_BIAS_GRAD)
+                    ws = std::max<uint64_t>(ws, fg::bias_grad_ws_bytes(cus, L.M, L.N));
+        P->ws_bytes = ws;
+        P->ws_slot = P->new_slot(ws / 4);
+    }
+
     // Arena: every plan-owned tensor, 256-byte aligned, one allocation.
     uint64_t off = 0;
     for (Slot &s : P->slots) {
@@ -1513,13 +1532,14 @@ FG_API int fg_plan_create(fg_ctx *ctx, const fg_graph *g, const uint32_t *meta, 
         rc = fg_fill_u32(ctx, P->arena, 0u, off / 4);
         if (rc) return rc;
     }
-    // Workspace for bias-gradient partials (the largest column reduction),
-    // reserved now so dispatch and capture never allocate.
-    uint64_t ws = 1u << 20;
-    for (auto *list : {&P->bwd_seed, &P->bwd_fused})
-        for (const Launch &L : *list)
-            if (L.kind == LK_BIAS_GRAD) ws = std::max<uint64_t>(ws, (uint64_t)L.N * 4 * 1024);
-    if (!fg::workspace(ctx, ws)) return FG_ERR_OUT_OF_MEMORY;
+    P->wctx.device = ctx->device;
+    P->wctx.stream = ctx->stream;
+    P->wctx.own_stream = false;
+    P->wctx.cu_count = ctx->cu_count;
+    std::memcpy(P->wctx.arch, ctx->arch, sizeof ctx->arch);
+    P->wctx.ws = P->ptr(P->ws_slot);
+    P->wctx.ws_bytes = P->ws_bytes;
+    P->wctx.ws_fixed = true;
     FG_HIP(hipStreamSynchronize(ctx->stream));
     *out = P.release();
     return FG_OK;
@@ -1888,7 +1908,8 @@ FG_API int fg_plan_describe(const fg_plan *p, char *buf, size_t len, size_t *nee
         int n = 0;
         for (const Launch &L : v) {
             if ((L.kind == LK_GEMM || L.kind == LK_GEMM_BWD) && L.dtype == FG_DTYPE_F32)
-                n += fg::gemm_f32_dispatches(p->ctx, L.sExtra != kNone ? FG_TN : L.layout, L.M,
+                n += fg::gemm_f32_dispatches(p->ctx ? const_cast<fg_ctx *>(&p->wctx) : nullptr,
+                                             L.sExtra != kNone ? FG_TN : L.layout, L.M,
                                              L.N, L.K, p->ptr(L.sA), L.lda, p->ptr(L.sB), L.ldb,
                                              L.kind == LK_GEMM && L.sExtra != kNone);
             else

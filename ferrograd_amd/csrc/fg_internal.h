@@ -6,6 +6,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <string>
+#include <vector>
 
 #include "../../include/ferrograd_hip.h"
 
@@ -27,10 +28,16 @@ struct fg_ctx {
     bool own_stream = false;
     int cu_count = 0;
     char arch[64] = {0};
-    // Scratch workspace for kernels that need partial results.  Grown by
-    // fg::workspace(); plans reserve it before stream capture.
+    // Scratch workspace for direct kernel calls that need partial results.
+    // Grown by fg::workspace(); a workspace it replaces stays allocated in
+    // ws_retired until fg_ctx_destroy, because a graph captured earlier may
+    // still hold its address.
     void *ws = nullptr;
     uint64_t ws_bytes = 0;
+    std::vector<void *> ws_retired;
+    // Set on a plan's own view of its context: ws is a fixed part of the
+    // plan's arena and fg::workspace() never replaces it.
+    bool ws_fixed = false;
 };
 
 struct fg_buf {
@@ -40,10 +47,15 @@ struct fg_buf {
 };
 
 namespace fg {
-// Returns a workspace pointer of at least `bytes` (grows the context's
-// workspace with a synchronizing reallocation if needed), or nullptr with
-// the error set.
+// Returns a workspace pointer of at least `bytes`, or nullptr with the error
+// set.  A context's workspace grows by allocating a larger one; the old one
+// is retired, not freed (captured graphs may use it).  A fixed workspace (a
+// plan's) never grows: a request beyond it fails.
 void *workspace(fg_ctx *ctx, uint64_t bytes);
+
+// Bytes of workspace fg_bias_grad needs for an M x N reduction on a device
+// with `cus` compute units (the partial sums of its row splits).
+uint64_t bias_grad_ws_bytes(int cus, int M, int N);
 
 // Adam with device-resident step counter / bias-correction scalars
 // (k_optim.hip).  d_state points at adam_dev_state_bytes() zeroed bytes.

@@ -40,17 +40,13 @@ int hip_fail(hipError_t e, const char *what, const char *file, int line) {
 
 void *workspace(fg_ctx *ctx, uint64_t bytes) {
     if (bytes <= ctx->ws_bytes) return ctx->ws;
+    if (ctx->ws_fixed) {
+        set_error("workspace: %llu bytes requested from a fixed workspace of %llu bytes",
+                  (unsigned long long)bytes, (unsigned long long)ctx->ws_bytes);
+        return nullptr;
+    }
     // Round up to 1 MiB so repeated small growth does not thrash.
     uint64_t want = (bytes + (1u << 20) - 1) & ~uint64_t((1u << 20) - 1);
-    if (ctx->ws) {
-        if (hipStreamSynchronize(ctx->stream) != hipSuccess) {
-            set_error("workspace: stream synchronize failed");
-            return nullptr;
-        }
-        (void)hipFree(ctx->ws);
-        ctx->ws = nullptr;
-        ctx->ws_bytes = 0;
-    }
     void *p = nullptr;
     hipError_t e = hipMalloc(&p, want);
     if (e != hipSuccess) {
@@ -58,6 +54,9 @@ void *workspace(fg_ctx *ctx, uint64_t bytes) {
                   hipGetErrorString(e));
         return nullptr;
     }
+    // The old workspace may be baked into a captured graph or still in use
+    // by queued work: keep it until the context is destroyed.
+    if (ctx->ws) ctx->ws_retired.push_back(ctx->ws);
     ctx->ws = p;
     ctx->ws_bytes = want;
     return p;
@@ -114,6 +113,7 @@ FG_API int fg_ctx_destroy(fg_ctx *ctx) {
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     if (ctx->ws) (void)hipFree(ctx->ws);
+    for (void *w : ctx->ws_retired) (void)hipFree(w);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return FG_OK;

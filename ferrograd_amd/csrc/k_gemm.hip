@@ -6,6 +6,7 @@
 #include <algorithm>
 #include <cmath>
 
+#include "fg_bias_grad.h"
 #include "fg_gemm_kernel.h"
 #include "fg_half.h"
 #include "fg_internal.h"
@@ -81,8 +82,9 @@ __global__ __launch_bounds__(kThreads) void splitk_reduce(GemmArgs p, int splits
 // Split K over workgroup rows when the output gives few tiles (under half
 // the CUs) and K is long (at least 4 K tiles per slice): each slice's raw
 // product goes to the context's workspace, which must already hold them
-// (a plan reserves 1 MiB; the workspace is never grown here, so launches
-// stay capturable).  The fused column sum of fg_gemm_dw is not split.
+// (every plan has its own of at least 1 MiB; direct callers reserve one with
+// fg_ctx_reserve_workspace; it is never grown here, so launches stay
+// capturable).  The fused column sum of fg_gemm_dw is not split.
 // Returns the number of slices (1: no split).
 int plan_split_k(fg_ctx *ctx, GemmArgs &a, int cfg, bool vec) {
     if (a.colsum || a.K <= 0) return 1;
@@ -191,91 +193,6 @@ int gemm_f32_dispatches(fg_ctx *ctx, int layout, int M, int N, int K, const void
 }
 }  // namespace fg
 
-namespace {
-
-// ----------------------------------------------------------- bias grad
-// Column sums of dZ[M][N]: phase 1 -- grid (column strips of 256 columns,
-// row splits); each thread sums 4 columns (float4) over its rows; partial
-// results per split go to workspace.  Phase 2 -- one thread per column adds
-// the splits in order.  Deterministic.
-constexpr int kBgCols = 256;  // columns per strip (64 lanes x float4)
-constexpr int kBgRowsPerThreadGroup = kThreads / (kBgCols / 4);  // 4 row groups
-
-// DT: element type of dZ (fg_half.h codes); 16-bit rows are read 4
-// elements (8 bytes) at a time when aligned.
-template <int DT>
-__global__ __launch_bounds__(kThreads) void bias_grad_partial(const void *__restrict__ dZ, int M,
-                                                              int N, int ld, int rows_per_split,
-                                                              float *__restrict__ partial,
-                                                              int vec) {
-    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-    __shared__ f32x4 sh[kThreads];
-    const int strip = blockIdx.x, split = blockIdx.y;
-    const int cq = threadIdx.x % (kBgCols / 4);
-    const int rg = threadIdx.x / (kBgCols / 4);
-    const int col = strip * kBgCols + cq * 4;
-    const int r0 = split * rows_per_split;
-    const int r1 = min(M, r0 + rows_per_split);
-    f32x4 s = {0.f, 0.f, 0.f, 0.f};
-    if (col < N) {
-        for (int r = r0 + rg; r < r1; r += kBgRowsPerThreadGroup) {
-            const uint64_t row = (uint64_t)r * ld;
-            if (vec && col + 4 <= N) {
-                if constexpr (DT == fg::kF32) {
-                    s += *reinterpret_cast<const f32x4 *>(static_cast<const float *>(dZ) + row +
-                                                          col);
-                } else {
-                    const u32x2 w = *reinterpret_cast<const u32x2 *>(
-                        static_cast<const uint16_t *>(dZ) + row + col);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        s[e] += fg::h16_to_f(DT, (uint16_t)(w[e >> 1] >> (16 * (e & 1))));
-                }
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (col + e < N) s[e] += fg::load_as_f(dZ, DT, row + col + e);
-            }
-        }
-    }
-    sh[threadIdx.x] = s;
-    __syncthreads();
-    if (rg == 0 && col < N) {
-        f32x4 t = sh[cq];
-#pragma unroll
-        for (int g = 1; g < kBgRowsPerThreadGroup; ++g) t += sh[g * (kBgCols / 4) + cq];
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-            if (col + e < N) partial[(size_t)split * N + col + e] = t[e];
-    }
-}
-
-// Adds the splits of each column in order; the sum is rounded to the
-// element type dt once (with accumulate: round(dbias + sum)).  The partials
-// are loaded 16 at a time before they are added (in the same order), so a
-// thread waits for one memory round trip per 16 splits rather than per split.
-__global__ __launch_bounds__(kThreads) void bias_grad_final(const float *__restrict__ partial,
-                                                            int splits, int N,
-                                                            void *__restrict__ dbias,
-                                                            int accumulate, int dt) {
-    const int col = blockIdx.x * kThreads + threadIdx.x;
-    if (col >= N) return;
-    constexpr int kBatch = 16;
-    float s = 0.0f;
-    int k = 0;
-    for (; k + kBatch <= splits; k += kBatch) {
-        float v[kBatch];
-#pragma unroll
-        for (int u = 0; u < kBatch; ++u) v[u] = partial[(size_t)(k + u) * N + col];
-#pragma unroll
-        for (int u = 0; u < kBatch; ++u) s += v[u];
-    }
-    for (; k < splits; ++k) s += partial[(size_t)k * N + col];
-    fg::store_from_f(dbias, dt, col, accumulate ? fg::load_as_f(dbias, dt, col) + s : s);
-}
-
-}  // namespace
-
 FG_API int fg_gemm_f32(fg_ctx *ctx, int layout, int M, int N, int K, const float *d_A, int lda,
                        const float *d_B, int ldb, const float *d_bias, int act, float *d_C,
                        int ldc, float *d_Z, int ldz, int accumulate) {
@@ -360,6 +277,12 @@ FG_API int fg_gemm_dw_f32(fg_ctx *ctx, int M, int N, int K, const float *d_A, in
     return gemm_common(ctx, FG_TN, a, "fg_gemm_dw_f32");
 }
 
+namespace fg {
+uint64_t bias_grad_ws_bytes(int cus, int M, int N) {
+    return colsum::split_of(cus > 0 ? cus : 256, M, N).partial_floats(N) * sizeof(float);
+}
+}  // namespace fg
+
 FG_API int fg_bias_grad(fg_ctx *ctx, int dtype, int M, int N, const void *d_dZ, int ld,
                         void *d_dbias, int accumulate) {
     FG_REQUIRE(ctx, FG_ERR_INVALID_ARGUMENT, "fg_bias_grad: ctx is NULL");
@@ -370,37 +293,13 @@ FG_API int fg_bias_grad(fg_ctx *ctx, int dtype, int M, int N, const void *d_dZ, 
     if (N == 0) return FG_OK;
     FG_REQUIRE(d_dZ && d_dbias, FG_ERR_INVALID_ARGUMENT, "fg_bias_grad: NULL pointer");
     FG_HIP(hipSetDevice(ctx->device));
-    const int strips = (N + kBgCols - 1) / kBgCols;
-    const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
-    // Enough splits for ~4 workgroups per CU, each covering >= 16 rows.
-    int splits = std::max(1, std::min((4 * cus + strips - 1) / strips, (M + 15) / 16));
-    const int rows_per_split = M > 0 ? (M + splits - 1) / splits : 0;
-    splits = M > 0 ? (M + rows_per_split - 1) / rows_per_split : 1;
-    float *partial = (float *)fg::workspace(ctx, (uint64_t)splits * N * sizeof(float));
+    const fg::colsum::Split sp =
+        fg::colsum::split_of(ctx->cu_count > 0 ? ctx->cu_count : 256, M, N);
+    float *partial = (float *)fg::workspace(ctx, std::max<uint64_t>(sp.partial_floats(N), 1) *
+                                                     sizeof(float));
     if (!partial) return FG_ERR_OUT_OF_MEMORY;
-    const unsigned align = dtype == FG_DTYPE_F32 ? 16u : 8u;
-    const int vec = ((((uintptr_t)d_dZ) & (align - 1)) == 0) && (ld % 4 == 0);
-    if (M > 0) {
-        const dim3 grid(strips, splits);
-        if (dtype == FG_DTYPE_F32)
-            bias_grad_partial<fg::kF32><<<grid, kThreads, 0, ctx->stream>>>(d_dZ, M, N, ld,
-                                                                            rows_per_split,
-                                                                            partial, vec);
-        else if (dtype == FG_DTYPE_F16)
-            bias_grad_partial<fg::kF16><<<grid, kThreads, 0, ctx->stream>>>(d_dZ, M, N, ld,
-                                                                            rows_per_split,
-                                                                            partial, vec);
-        else
-            bias_grad_partial<fg::kBF16><<<grid, kThreads, 0, ctx->stream>>>(d_dZ, M, N, ld,
-                                                                             rows_per_split,
-                                                                             partial, vec);
-        FG_LAUNCH_CHECK("bias_grad_partial");
-    } else {
-        splits = 0;
-    }
-    bias_grad_final<<<(N + kThreads - 1) / kThreads, kThreads, 0, ctx->stream>>>(
-        partial, splits, N, d_dbias, accumulate, dtype);
-    FG_LAUNCH_CHECK("bias_grad_final");
+    FG_HIP(fg::colsum::launch(ctx->stream, sp, dtype, M, N, d_dZ, ld, d_dbias, accumulate,
+                              partial));
     return FG_OK;
 }
 

@@ -436,6 +436,70 @@ def test_captured_step_replays_like_eager(ctx):
             assert np.array_equal(x, y2)
 
 
+def test_captured_step_survives_workspace_growth(ctx):
+    """A captured c1 step (its 64x256x784 forward GEMM splits K into the
+    plan's workspace) replays bit for bit like eager steps of an identical
+    plan after the context's workspace grows and a larger plan is created on
+    the same context: each plan's workspace is its own, and a context
+    workspace that grows is retired, not freed."""
+    import ferrograd_amd as fa
+    from ferrograd_amd._lib import call
+    G = api()
+    # A context of its own on the same stream: growing its workspace must not
+    # change what later tests' direct GEMM calls on the shared context do.
+    own = fa.Context(0, ctx.ctx.stream)
+    ctx = G.GpuContext(own)
+    dims, B = [784, 256, 10], 64
+    runs = []
+    plans = []
+    for captured in (False, True):
+        graph, meta, mb, st = build_mlp(ctx, dims, B, "relu", G.Optim.sgd())
+        X = fa.rng_uniform(0, 0, (B, 784))
+        y = fa.rng_int(0, 1, (B,), 10)
+        ins = [ctx.init_tensor_f32(X.shape, X)]
+        for l in range(2):
+            W = fa.rng_uniform(0, 10 + l, (dims[l], dims[l + 1]), -math.sqrt(6 / dims[l]),
+                               math.sqrt(6 / dims[l]))
+            ins += [ctx.init_tensor_f32(W.shape, W),
+                    ctx.init_tensor_f32((dims[l + 1],), np.zeros(dims[l + 1]))]
+        tgt = ctx.new_onehot_init(y)
+        sch = ctx.schedule(graph.lower(meta), [G.f32_bits(0.01)] + mb[1:], ins, st)
+        plans.append((sch, st, ins, tgt))
+    desc = plans[1][1].plan.describe()
+    # The split forward GEMM adds its summing epilogue: 2 dispatches for one launch.
+    fwd_kernels = int(desc.split("(forward ")[1].split(",")[0])
+    assert fwd_kernels == 2, desc
+    sch, st, ins, tgt = plans[1]
+    call("fg_plan_bind_target", sch.plan.handle, tgt.data_ptr(), tgt.nbytes)
+    call("fg_plan_capture_step", sch.plan.handle)
+    # Grow the context's own workspace and create a larger plan on it.
+    ctx.ctx.reserve_workspace(64 << 20)
+    big, bmeta, bmb, bst = build_mlp(ctx, [512, 2048, 1000], 256, "gelu", G.Optim.adam())
+    for captured, (sch, st, ins, tgt) in zip((False, True), plans):
+        hist = []
+        for _ in range(3):
+            if captured:
+                call("fg_plan_launch_step", sch.plan.handle)
+                ctx.download(st.forward_out)  # eager work between replays
+            else:
+                ctx.dispatch_forward(sch)
+                ctx.dispatch_loss(sch, tgt)
+                ctx.dispatch_backward(sch)
+                ctx.dispatch_optim(sch)
+            ctx.sync()
+            hist.append([ctx.download(t).copy() for t in ins[1:]] +
+                        [ctx.download(st.mean_loss).copy()])
+        runs.append(hist)
+    for a, b in zip(*runs):
+        for x, y2 in zip(a, b):
+            assert np.array_equal(x, y2)
+    bst.plan.close()
+    for sch, st, _, _ in plans:
+        st.plan.close()
+    own.sync()
+    own.close()
+
+
 # --------------------------------------------------- losses and elementwise
 @pytest.mark.parametrize("loss", ["MEAN_SQUARED_ERROR", "BINARY_CROSS_ENTROPY", "CROSS_ENTROPY"])
 def test_losses_on_tanh_output(ctx, loss):

@@ -280,7 +280,9 @@ def test_gemm_split_k(gpu_ctx, case):
     """Split-K GEMMs (slots summed in a fixed order, then the epilogue):
     against float64 with the CPU oracle's epilogue, bit-identical on a
     second run, and within tolerance of the unsplit kernel (a context with
-    no workspace)."""
+    no workspace) but not bit-identical to it (the split did happen).  The
+    workspace is reserved on a context of the test's own, so the shared
+    context's direct GEMMs keep their unsplit path."""
     torch = _torch()
     import ferrograd_amd as fa
     layout, M, N, K, mode, act, acc = case
@@ -306,9 +308,15 @@ def test_gemm_split_k(gpu_ctx, case):
                          Zs=dZs, ldzs=N)
         return host(dC), host(dZ)
 
-    gpu_ctx.reserve_workspace(16 << 20)
-    C1, Z1 = run(gpu_ctx)
-    C2, Z2 = run(gpu_ctx)
+    stream = torch.cuda.current_stream().cuda_stream
+    split = fa.Context(0, stream)
+    try:
+        split.reserve_workspace(16 << 20)
+        C1, Z1 = run(split)
+        C2, Z2 = run(split)
+    finally:
+        split.sync()
+        split.close()
     assert np.array_equal(C1, C2)
     P = A.astype(np.float64) @ B.astype(np.float64)
     tol = 1e-5 * math.sqrt(K)
@@ -320,13 +328,15 @@ def test_gemm_split_k(gpu_ctx, case):
         assert normwise_rel(C1, O.act(act, Zr)) < tol
     else:
         assert normwise_rel(C1, O.act_bwd(act, P, Zs)) < tol
-    plain = fa.Context(0, torch.cuda.current_stream().cuda_stream)  # no workspace: no split
+    plain = fa.Context(0, stream)  # no workspace: no split
     try:
         C3, _ = run(plain)
     finally:
         plain.sync()
         plain.close()
     assert normwise_rel(C1, C3) < tol
+    # Another summation order: some of the M*N sums round differently.
+    assert not np.array_equal(C1, C3)
 
 
 # ----------------------------------------------------- bias grad, act bwd
