@@ -9,7 +9,8 @@ parameters resident in HBM.  value = training steps per second.
 Also measured in the same run (HIP events on the stream the kernels run on):
   * the dominant kernel of the step, the hidden-layer forward GEMM
     (2048 x 4096 x 4096, bias + GELU epilogue) -> roofline vs fp32 MFMA peak;
-  * c2: 4096^3 GEMM forward (bias + ReLU) and its dA / dB backward;
+  * c2: 4096^3 GEMM forward (bias + ReLU) and its backward through the
+    ReLU mask (dA, dB, dbias);
   * c3: fused softmax + CE forward/backward over [8192, 32000];
   * c4: multi-tensor Adam over 64 x 4 Mi parameters;
   * c1: the 2-layer MLP step (latency bound: steps/s, launches, us/launch);
@@ -177,33 +178,68 @@ class MLPStep:
         return sum(w.numel() for w in self.W) + sum(b.numel() for b in self.b)
 
 
-def gemm_components(ctx, reps: int):
-    """c2 (4096^3) forward + dA + dB, and the c5 hidden-layer forward GEMM."""
+def c2_inputs(ctx, n: int = 4096):
+    """BASELINE c2 inputs from the library's generator, seed 1: A, B ~ N(0,1)
+    (tensor ids 0, 1), bias ~ N(0, 0.1^2) (id 2; the configuration's
+    "N(0,0.1)" read as a standard deviation of 0.1), dC ~ N(0,1) (id 3)."""
+    import torch
+
+    A, Bm, dC = (torch.empty((n, n), device="cuda") for _ in range(3))
+    bias = torch.empty((n,), device="cuda")
+    ctx.rng_normal(1, 0, 0.0, 1.0, A, n * n)
+    ctx.rng_normal(1, 1, 0.0, 1.0, Bm, n * n)
+    ctx.rng_normal(1, 2, 0.0, 0.1, bias, n)
+    ctx.rng_normal(1, 3, 0.0, 1.0, dC, n * n)
+    return A, Bm, bias, dC
+
+
+def gemm_components(ctx, reps: int, want_host: bool = False):
+    """c2 (4096^3): forward C = ReLU(A.B + bias), then the backward through
+    the ReLU mask -- dA = (dC*[Z>0]).B^T and dB = A^T.(dC*[Z>0]) with dbias
+    = colsum(dC*[Z>0]) fused into dB -- where the mask is applied as the two
+    GEMMs load dC (fg_linear_bwd_f32; the forward output C gives the mask,
+    so the forward stores no Z).  Also the c5 hidden-layer forward GEMM.
+    Returns (timings, sample): with want_host the sample holds the inputs
+    and outputs (the parity sample of the CPU leg), else it is None."""
     import torch
 
     import ferrograd_amd as fa
 
     out = {}
     n = 4096
-    g = torch.Generator(device="cuda").manual_seed(1)
-    A = torch.randn((n, n), device="cuda", generator=g)
-    Bm = torch.randn((n, n), device="cuda", generator=g)
-    bias = 0.1 * torch.randn((n,), device="cuda", generator=g)
-    dC = torch.randn((n, n), device="cuda", generator=g)
-    C, Z, dA, dB = (torch.empty((n, n), device="cuda") for _ in range(4))
+    A, Bm, bias, dC = c2_inputs(ctx, n)
+    C, dA, dB = (torch.empty((n, n), device="cuda") for _ in range(3))
+    db = torch.empty((n,), device="cuda")
     flops = 2.0 * n * n * n
-    t_f = event_time_ms(lambda: ctx.gemm(fa.NN, n, n, n, A, n, Bm, n, C, n, bias=bias,
-                                         act=fa.ACT_RELU, Z=Z, ldz=n), reps, warm_ms=200)
-    t_a = event_time_ms(lambda: ctx.gemm_bwd(fa.NT, n, n, n, dC, n, Bm, n, dA, n,
-                                             act=fa.ACT_RELU, Zs=Z, ldzs=n), reps, warm_ms=200)
-    t_b = event_time_ms(lambda: ctx.gemm(fa.TN, n, n, n, A, n, dC, n, dB, n), reps, warm_ms=200)
+
+    def fwd():
+        ctx.gemm(fa.NN, n, n, n, A, n, Bm, n, C, n, bias=bias, act=fa.ACT_RELU)
+
+    def bwd(dX=None, dW=None, dbias=None):
+        ctx.linear_bwd(fa.ACT_RELU, n, n, n, A, n, Bm, n, C, n, dC, n, dX=dX, lddx=n, dW=dW,
+                       lddw=n, dbias=dbias)
+
+    t_f = event_time_ms(fwd, reps, warm_ms=200)
+    t_a = event_time_ms(lambda: bwd(dX=dA), reps, warm_ms=200)
+    t_b = event_time_ms(lambda: bwd(dW=dB, dbias=db), reps, warm_ms=200)
+    t_bwd = event_time_ms(lambda: bwd(dX=dA, dW=dB, dbias=db), reps, warm_ms=200)
     out["c2_gemm_4096"] = {
-        "fwd_ms": t_f, "dA_ms": t_a, "dB_ms": t_b,
+        "fwd_ms": t_f, "dA_ms": t_a, "dB_dbias_ms": t_b, "bwd_ms": t_bwd,
         "fwd_tflops": flops / t_f / 1e9, "dA_tflops": flops / t_a / 1e9,
         "dB_tflops": flops / t_b / 1e9,
-        "fwd_bwd_tflops": 3 * flops / (t_f + t_a + t_b) / 1e9,
+        "fwd_bwd_ms": t_f + t_bwd,
+        "fwd_bwd_tflops": 3 * flops / (t_f + t_bwd) / 1e9,
+        "backward": "dZ = dC*[C>0] applied on load (never stored); dA = dZ.B^T; "
+                    "dB = A^T.dZ with dbias = colsum(dZ) fused",
     }
-    del A, Bm, bias, dC, C, Z, dA, dB
+    sample = None
+    if want_host:
+        torch.cuda.synchronize()
+        sample = {k: v.cpu().numpy() for k, v in (("A", A), ("B", Bm), ("bias", bias),
+                                                   ("dC", dC), ("C", C), ("dA", dA),
+                                                   ("dB", dB), ("db", db))}
+    del A, Bm, bias, dC, C, dA, dB, db
+    g = torch.Generator(device="cuda").manual_seed(1)
     # c5 hidden layer forward: [2048,4096] x [4096,4096] + bias, GELU.
     M, N, K = 2048, 4096, 4096
     X = torch.randn((M, K), device="cuda", generator=g)
@@ -216,10 +252,61 @@ def gemm_components(ctx, reps: int):
                                  "tflops": 2.0 * M * N * K / t / 1e9,
                                  # X, W, bias read once; H and Z written once.
                                  "bytes": 4 * (M * K + K * N + N + 2 * M * N)}
+    return out, sample
+
+
+def c5_gemm_kernels(ctx):
+    """The three hidden-layer GEMMs of the c5 step on its shapes and
+    epilogues (random operands, library generator): key -> (description,
+    launch closure, algorithmic bytes per launch)."""
+    import torch
+
+    import ferrograd_amd as fa
+
+    M, N, K = 2048, 4096, 4096
+    X, W, dZ, Zs = (torch.empty(shape, device="cuda") for shape in
+                    ((M, K), (K, N), (M, N), (M, K)))
+    b, db = torch.empty((N,), device="cuda"), torch.empty((N,), device="cuda")
+    for i, t in enumerate((X, W, dZ, Zs, b)):
+        ctx.rng_normal(4, 500 + i, 0.0, 1.0, t, t.numel())
+    H, Z, dX, dW = (torch.empty(shape, device="cuda") for shape in
+                    ((M, N), (M, N), (M, K), (K, N)))
+    return {
+        "gemm_c5_fwd": ("NN 2048x4096x4096 + bias + GELU, Z stored (forward)",
+                        lambda: ctx.gemm(fa.NN, M, N, K, X, K, W, N, H, N, bias=b,
+                                         act=fa.ACT_GELU, Z=Z, ldz=N),
+                        4 * (M * K + K * N + N + 2 * M * N)),
+        "gemm_c5_dx": ("NT 2048x4096x4096 * GELU'(Z) (dX of a hidden layer)",
+                       lambda: ctx.gemm_bwd(fa.NT, M, K, N, dZ, N, W, N, dX, K,
+                                            act=fa.ACT_GELU, Zs=Zs, ldzs=K),
+                       4 * (M * N + K * N + 2 * M * K)),
+        "gemm_c5_dw": ("TN 4096x4096x2048 + fused dbias (dW, db of a hidden layer)",
+                       lambda: ctx.gemm_dw(K, N, M, X, K, dZ, N, dW, N, colsum=db),
+                       4 * (M * K + M * N + K * N + N)),
+    }
+
+
+def c5_gemm_shares(ctx, reps: int, step_ms: float):
+    """The three GEMMs that make up 18 of the c5 step's 24 (6 of each per
+    step), timed alone with HIP events on the step's own shapes and
+    epilogues: forward NN 2048x4096x4096 + bias + GELU (+Z), dX NT
+    2048x4096x4096 with the GELU derivative, dW TN 4096x4096x2048 with the
+    fused dbias.  share = 6 * time / step time."""
+    flops = 2.0 * 2048 * 4096 * 4096
+    out = {}
+    for key, (what, fn, nbytes) in c5_gemm_kernels(ctx).items():
+        t = event_time_ms(fn, reps, warm_ms=200)
+        out[key] = {"what": what, "ms": t, "tflops": flops / t / 1e9,
+                    "frac": flops / t / 1e9 / PEAK_FP32_MFMA_TFLOPS, "per_step": 6,
+                    "step_share": 6 * t / step_ms, "flops_per_launch": flops,
+                    "algorithmic_bytes": nbytes}
     return out
 
 
-def softmax_component(ctx, reps: int):
+def softmax_component(ctx, reps: int, want_host: bool = False):
+    """c3: fused softmax + CE forward / backward over [8192, 32000] (library
+    generator, seed 2: logits N(0, 2^2) id 0, labels U{0..31999} id 1).  With
+    want_host, also returns inputs and outputs as the CPU leg's sample."""
     import torch
 
     R, C = 8192, 32000
@@ -234,8 +321,16 @@ def softmax_component(ctx, reps: int):
                                              mean_loss=mean, dlogits=d, ldd=C, argmax=am),
                       reps, warm_ms=200)
     nbytes = 2 * R * C * 4 + R * 4 * 3  # logits in, dlogits out, labels/loss/argmax
-    return {"c3_softmax_ce_8192x32000": {"ms": t, "bytes": nbytes, "gbs": nbytes / t / 1e6,
-                                         "frac_hbm": nbytes / t / 1e6 / PEAK_HBM_GBS}}
+    out = {"c3_softmax_ce_8192x32000": {"ms": t, "bytes": nbytes, "gbs": nbytes / t / 1e6,
+                                        "frac_hbm": nbytes / t / 1e6 / PEAK_HBM_GBS}}
+    if not want_host:
+        return out
+    import numpy as np
+    torch.cuda.synchronize()
+    sample = {"x": x.cpu().numpy(), "y": lab.cpu().numpy().view(np.uint32),
+              "row_loss": loss.cpu().numpy(), "mean": float(mean.cpu()[0]),
+              "d": d.cpu().numpy(), "argmax": am.cpu().numpy().view(np.uint32)}
+    return out, sample
 
 
 def adam_component(ctx, reps: int):
@@ -326,14 +421,32 @@ def gemm_bf16_component(ctx, reps: int):
                                   "fwd_ms": t_f, "dA_ms": t_a, "dB_ms": t_b}}
 
 
-def c1_component(ctx, steps: int = 2000):
+def c1_component(ctx, steps: int = 2000, want_host: bool = True):
     """c1: the 2-layer MLP step (batch 64, 784 -> 256 -> 10, ReLU, softmax-CE,
     SGD lr 0.01), latency bound: steps/s of the captured step, launches per
-    step and the average time per launch."""
+    step and the average time per launch.  With want_host, also returns the
+    inputs and the first step's loss, gradients and SGD result (the parity
+    sample for the CPU leg) as a second value."""
     import torch
 
     tr = MLPStep(ctx, [784, 256, 10], 64, act="relu", optim="sgd", lr=0.01, seed=0,
                  x_dist="uniform")
+    sample = None
+    if want_host:
+        import numpy as np
+        sample = {"X": tr.X.cpu().numpy(), "y": tr.labels.cpu().numpy().view(np.uint32),
+                  "W": [w.cpu().numpy() for w in tr.W]}
+        tr.forward()
+        tr.loss()
+        tr.backward()
+        torch.cuda.synchronize()
+        sample["mean_loss"] = tr.mean_loss()
+        sample["dW"] = [tr.download(t).reshape(w.shape) for t, w in zip(tr.dW, tr.W)]
+        sample["db"] = [tr.download(t) for t in tr.db]
+        tr.gctx.dispatch_optim(tr.sch)
+        torch.cuda.synchronize()
+        sample["W_after"] = [w.cpu().numpy() for w in tr.W]
+        sample["b_after"] = [b.cpu().numpy() for b in tr.b]
     for _ in range(3):
         tr.step_eager()
     torch.cuda.synchronize()
@@ -351,10 +464,11 @@ def c1_component(ctx, steps: int = 2000):
     torch.cuda.synchronize()
     ms = 1000.0 * (time.perf_counter() - t0) / steps
     n = tr.launches_per_step()
-    return {"c1_mlp_step": {"steps_per_s": 1000.0 / ms, "ms_per_step": ms,
-                            "eager_ms_per_step": eager_ms, "launches_per_step": n,
-                            "us_per_launch": 1000.0 * ms / n, "loss": tr.mean_loss(),
-                            "steps_timed": steps}}
+    out = {"c1_mlp_step": {"steps_per_s": 1000.0 / ms, "ms_per_step": ms,
+                           "eager_ms_per_step": eager_ms, "launches_per_step": n,
+                           "us_per_launch": 1000.0 * ms / n, "loss": tr.mean_loss(),
+                           "steps_timed": steps}}
+    return (out, sample) if want_host else out
 
 
 def only_gemm_c5_hidden(ctx, reps):
@@ -447,8 +561,34 @@ def only_gemm_bf16_c2(ctx, reps):
         ctx.gemm_x16(bf, fa.TN, n, n, n, A, n, dC, n, dB, n)
 
 
+def only_gemm_c2(ctx, reps):
+    """The c2 GEMMs: forward (bias + ReLU) and the masked backward (dA, dB +
+    dbias) through fg_linear_bwd_f32."""
+    import torch
+
+    import ferrograd_amd as fa
+
+    n = 4096
+    A, Bm, bias, dC = c2_inputs(ctx, n)
+    C, dA, dB = (torch.empty((n, n), device="cuda") for _ in range(3))
+    db = torch.empty((n,), device="cuda")
+    for _ in range(reps):
+        ctx.gemm(fa.NN, n, n, n, A, n, Bm, n, C, n, bias=bias, act=fa.ACT_RELU)
+        ctx.linear_bwd(fa.ACT_RELU, n, n, n, A, n, Bm, n, C, n, dC, n, dX=dA, lddx=n, dW=dB,
+                       lddw=n, dbias=db)
+
+
+def only_c5_gemm(key):
+    def run(ctx, reps):
+        fn = c5_gemm_kernels(ctx)[key][1]
+        for _ in range(reps):
+            fn()
+    run.__doc__ = f"The c5 step's {key} GEMM alone (for counter passes)."
+    return run
+
+
 def only_c1_step(ctx, reps):
-    print(json.dumps(c1_component(ctx, steps=max(reps, 10))), flush=True)
+    print(json.dumps(c1_component(ctx, steps=max(reps, 10), want_host=False)), flush=True)
 
 
 ONLY = {
@@ -456,7 +596,11 @@ ONLY = {
     "c5_step": only_c5_step,
     "c5_step_bf16": only_c5_step_bf16,
     "gemm_bf16_c2": only_gemm_bf16_c2,
+    "gemm_c2": only_gemm_c2,
     "gemm_c5_hidden": only_gemm_c5_hidden,
+    "gemm_c5_fwd": only_c5_gemm("gemm_c5_fwd"),
+    "gemm_c5_dx": only_c5_gemm("gemm_c5_dx"),
+    "gemm_c5_dw": only_c5_gemm("gemm_c5_dw"),
     "softmax_ce_c3": only_softmax_ce_c3,
     "adam_c4": only_adam_c4,
     "copy_256mib": only_copy_256mib,
@@ -476,9 +620,217 @@ def measured_traffic(kernel):
         return None
 
 
-def cpu_baseline_c5(host, dims, batch, threads):
-    """One full c5 training step (forward, CE, backward incl. dX, Adam) with
-    the CPU restatement, on the same initial inputs as the GPU run."""
+# ----------------------------------------------------------- CPU baselines
+# The CPU restatement (oracle/, C with OpenMP) timed on the host cores on the
+# same inputs as the GPU run (copied from the device, so both sides consume
+# identical bits), and the parity of each configuration: normwise relative
+# error max|gpu - cpu| / max|cpu| per tensor against the tolerances of the
+# configurations (GEMM 1e-5*sqrt(K), elementwise / softmax / optimiser 1e-5;
+# argmax, labels and the optimiser updates bit-exact).
+
+def cpu_threads() -> int:
+    """Threads of the CPU legs: the job's CPU share -- OMP_NUM_THREADS when
+    set (one GPU's share of the GPU box's cores), else the CPUs this process
+    may run on."""
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        return int(env)
+    return len(os.sched_getaffinity(0))
+
+
+def cpu_time_s(fn, repeats: int = 5) -> float:
+    """Median wall time of fn() over `repeats` runs after one warm-up run."""
+    fn()
+    ts = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    return ts[len(ts) // 2]
+
+
+def rel_err(a, b) -> float:
+    import numpy as np
+    a = np.asarray(a, np.float64).reshape(-1)
+    b = np.asarray(b, np.float64).reshape(-1)
+    if b.size == 0:
+        return 0.0
+    return float(np.max(np.abs(a - b)) / max(float(np.max(np.abs(b))), 1e-30))
+
+
+def oracle_mlp_grads(X, y, W, b, act):
+    """Forward, softmax-CE and backward (dX of the data included) of an MLP
+    with the CPU restatement: (mean loss, dW list, db list)."""
+    import oracle as O
+
+    L = len(W)
+    Zs, Hs, inp = [], [], X
+    for l in range(L):
+        Z, H = O.bias_act(O.gemm(O.NN, inp, W[l]), b[l], O.ACT_NONE if l == L - 1 else act)
+        Zs.append(Z)
+        Hs.append(H)
+        inp = H
+    _, dZ, _, mean = O.softmax_ce(Zs[-1], y)
+    dW, db = [None] * L, [None] * L
+    for l in range(L - 1, -1, -1):
+        prev = Hs[l - 1] if l > 0 else X
+        dW[l] = O.gemm(O.TN, prev, dZ)
+        db[l] = O.bias_grad(dZ)
+        up = O.gemm(O.NT, dZ, W[l])
+        dZ = O.act_bwd(act, up, Zs[l - 1]) if l > 0 else up
+    return mean, dW, db
+
+
+def cpu_c1(sample, threads):
+    """c1 on the CPU: the whole step (forward, CE, backward incl. dX, SGD),
+    single-threaded and on `threads` threads; parity of the GPU's first step
+    (loss, gradients; SGD bit-exact on the GPU's own gradients)."""
+    import numpy as np
+
+    import oracle as O
+
+    X, y, W = sample["X"], sample["y"], sample["W"]
+    b = [np.zeros(w.shape[1], np.float32) for w in W]
+
+    def step():
+        mean, dW, db = oracle_mlp_grads(X, y, W, b, O.ACT_RELU)
+        for p, g in zip(W + b, dW + db):
+            O.sgd_(p.copy().reshape(-1), g.copy().reshape(-1), np.float32(0.01), True)
+        return mean, dW, db
+
+    O.set_num_threads(1)
+    t1 = cpu_time_s(step, 20)
+    O.set_num_threads(threads)
+    tn = cpu_time_s(step, 20)
+    mean, dW, db = step()
+    sgd_exact = True
+    for p0, g, got in zip(W + b, sample["dW"] + sample["db"], sample["W_after"] + sample["b_after"]):
+        w = p0.copy().reshape(-1)
+        O.sgd_(w, np.ascontiguousarray(g, np.float32).reshape(-1).copy(), np.float32(0.01), True)
+        sgd_exact &= bool(np.array_equal(w, got.reshape(-1)))
+    tol = 1e-5 * math.sqrt(784)
+    err = {"loss": abs(sample["mean_loss"] - mean) / max(1.0, abs(mean)),
+           "dW": max(rel_err(a, r) for a, r in zip(sample["dW"], dW)),
+           "db": max(rel_err(a, r) for a, r in zip(sample["db"], db))}
+    return {"cpu_steps_per_s_1thread": 1.0 / t1, "cpu_steps_per_s": 1.0 / tn,
+            "cpu_ms_per_step_1thread": 1e3 * t1, "cpu_ms_per_step": 1e3 * tn,
+            "cores": threads, "kind": "port", "max_rel_err": err, "tolerance": tol,
+            "sgd_bit_exact": sgd_exact,
+            "parity_ok": bool(err["loss"] < 1e-5 and err["dW"] < tol and err["db"] < tol
+                              and sgd_exact)}
+
+
+def cpu_c2(sample, threads):
+    """c2 on the CPU: forward ReLU(A.B + bias) and the masked backward (dA,
+    dB, dbias), timed once each on `threads` threads (412 GFLOP).  The CPU
+    backward takes the GPU forward's mask ([C_gpu > 0]; a sign that fp32
+    rounding decides differently would otherwise flip single terms), and the
+    flipped signs are counted."""
+    import numpy as np
+
+    import oracle as O
+
+    O.set_num_threads(threads)
+    A, B, bias, dC = sample["A"], sample["B"], sample["bias"], sample["dC"]
+    t0 = time.perf_counter()
+    _, C = O.bias_act(O.gemm(O.NN, A, B), bias, O.ACT_RELU)
+    t_f = time.perf_counter() - t0
+    Cg = sample["C"]
+    t0 = time.perf_counter()
+    dZ = O.act_bwd(O.ACT_RELU, dC, Cg)
+    dA = O.gemm(O.NT, dZ, B)
+    dB = O.gemm(O.TN, A, dZ)
+    db = O.bias_grad(dZ)
+    t_b = time.perf_counter() - t0
+    flops = 3 * 2.0 * A.shape[0] * A.shape[1] * B.shape[1]
+    tol = 1e-5 * math.sqrt(A.shape[1])
+    err = {"C": rel_err(Cg, C), "dA": rel_err(sample["dA"], dA), "dB": rel_err(sample["dB"], dB),
+           "dbias": rel_err(sample["db"], db)}
+    return {"cpu_ms": 1e3 * (t_f + t_b), "cpu_fwd_ms": 1e3 * t_f, "cpu_bwd_ms": 1e3 * t_b,
+            "cpu_tflops": flops / (t_f + t_b) / 1e12, "cores": threads, "kind": "port",
+            "mask_sign_flips": int(np.count_nonzero((Cg > 0) != (C > 0))),
+            "max_rel_err": err, "tolerance": tol,
+            "parity_ok": bool(max(err.values()) < tol)}
+
+
+def cpu_c3(sample, threads):
+    """c3 on the CPU: softmax + CE forward and backward over [8192, 32000]
+    (median of 3 after a warm-up) on `threads` threads; argmax bit-exact."""
+    import numpy as np
+
+    import oracle as O
+
+    O.set_num_threads(threads)
+    x, y = sample["x"], sample["y"]
+    t = cpu_time_s(lambda: O.softmax_ce(x, y), 3)
+    rl, d, am, mean = O.softmax_ce(x, y)
+    err = {"row_loss": rel_err(sample["row_loss"], rl),
+           "mean_loss": abs(float(sample["mean"]) - mean) / max(1.0, abs(mean)),
+           "dlogits": rel_err(sample["d"], d)}
+    am_exact = int(np.count_nonzero(sample["argmax"] == am))
+    nbytes = 2 * x.size * 4
+    return {"cpu_ms": 1e3 * t, "cpu_gbs": nbytes / t / 1e9, "cores": threads, "kind": "port",
+            "max_rel_err": err, "tolerance": 1e-5, "argmax_exact": am_exact,
+            "rows": int(x.shape[0]),
+            "parity_ok": bool(max(err.values()) < 1e-5 and am_exact == x.shape[0])}
+
+
+def adam_sample_run(ctx, nt: int = 8, steps: int = 10, threads: int = 1):
+    """c4's parity and CPU sample: the first `nt` of its 64 tensors (4 Mi
+    parameters each), `steps` Adam steps with fresh gradients each step
+    (library generator, seed 3: parameters N(0, 0.02^2) ids 0..63, step s's
+    gradients N(0, 1e-3^2) ids 1000 + 64(s-1) + i), on the GPU and with the
+    CPU restatement on the same bits; the CPU's update is timed (`threads`
+    threads) and scaled to the 64 tensors."""
+    import numpy as np
+    import torch
+
+    import ferrograd_amd as fa
+    import oracle as O
+
+    O.set_num_threads(threads)
+    n = 4 * 1024 * 1024
+    P = [torch.empty(n, device="cuda") for _ in range(nt)]
+    G = [torch.empty(n, device="cuda") for _ in range(nt)]
+    M = [torch.zeros(n, device="cuda") for _ in range(nt)]
+    V = [torch.zeros(n, device="cuda") for _ in range(nt)]
+    for i in range(nt):
+        ctx.rng_normal(3, i, 0.0, 0.02, P[i], n)
+    hp = [p.cpu().numpy() for p in P]
+    hm = [np.zeros(n, np.float32) for _ in range(nt)]
+    hv = [np.zeros(n, np.float32) for _ in range(nt)]
+    mt = fa.MultiTensor(ctx, P, G, M, V)
+    t_cpu = 0.0
+    for step in range(1, steps + 1):
+        for i in range(nt):
+            ctx.rng_normal(3, 1000 + 64 * (step - 1) + i, 0.0, 1e-3, G[i], n)
+        hg = [g.cpu().numpy() for g in G]
+        mt.adam(1e-3, 0.9, 0.999, 1e-8, step)
+        sc, r = O.adam_scalars(np.float32(1e-3), np.float32(0.9), np.float32(0.999), step)
+        t0 = time.perf_counter()
+        for i in range(nt):
+            O.adam_(hp[i], hg[i], hm[i], hv[i], np.float32(0.9), np.float32(0.999),
+                    np.float32(1e-8), sc, r)
+        t_cpu += time.perf_counter() - t0
+    torch.cuda.synchronize()
+    exact = all(np.array_equal(a.cpu().numpy(), b) for X, H in ((P, hp), (M, hm), (V, hv))
+                for a, b in zip(X, H))
+    err = max(rel_err(a.cpu().numpy(), b) for a, b in zip(P, hp))
+    mt.close()
+    per_step_64 = t_cpu / steps * (64 / nt)
+    return {"cpu_ms_per_step": 1e3 * per_step_64, "cpu_gbs": 28 * 64 * n / per_step_64 / 1e9,
+            "cores": threads, "kind": "port",
+            "sample": f"{nt} of 64 tensors x {steps} steps, fresh gradients each step; time "
+                      f"scaled to 64 tensors",
+            "max_rel_err": {"params": err}, "tolerance": 1e-5, "bit_exact_p_m_v": exact,
+            "parity_ok": bool(exact)}
+
+
+def cpu_c5(host, first, dims, threads):
+    """c5 on the CPU: one full training step (forward, CE, backward incl. dX,
+    Adam) on the same initial inputs; parity of the GPU's first step (loss,
+    every dW / db) and Adam bit-exact on the GPU's own gradients."""
     import numpy as np
 
     import oracle as O
@@ -487,32 +839,29 @@ def cpu_baseline_c5(host, dims, batch, threads):
     X, y, W = host["X"], host["y"], host["W"]
     L = len(W)
     b = [np.zeros(dims[l + 1], np.float32) for l in range(L)]
-    t0 = time.perf_counter()
-    Zs, Hs = [], []
-    inp = X
-    for l in range(L):
-        last = l == L - 1
-        Z, H = O.bias_act(O.gemm(O.NN, inp, W[l]), b[l], O.ACT_NONE if last else O.ACT_GELU)
-        Zs.append(Z)
-        Hs.append(H)
-        inp = H
-    row_loss, dZ, _, mean = O.softmax_ce(Zs[-1], y)
-    dW, db = [None] * L, [None] * L
-    for l in range(L - 1, -1, -1):
-        prev = Hs[l - 1] if l > 0 else X
-        dW[l] = O.gemm(O.TN, prev, dZ)
-        db[l] = O.bias_grad(dZ)
-        up = O.gemm(O.NT, dZ, W[l])
-        dZ = O.act_bwd(O.ACT_GELU, up, Zs[l - 1]) if l > 0 else up
     s, r = O.adam_scalars(np.float32(1e-3), np.float32(0.9), np.float32(0.999), 1)
-    Wn = []
-    for l in range(L):
-        for p, g in ((W[l].copy(), dW[l]), (b[l].copy(), db[l])):
-            m, v = np.zeros_like(p), np.zeros_like(p)
-            O.adam_(p, g, m, v, np.float32(0.9), np.float32(0.999), np.float32(1e-8), s, r)
-            Wn.append(p)
+    t0 = time.perf_counter()
+    mean, dW, db = oracle_mlp_grads(X, y, W, b, O.ACT_GELU)
+    for p0, g in zip(W + b, dW + db):
+        p = p0.copy()
+        O.adam_(p, g, np.zeros_like(p), np.zeros_like(p), np.float32(0.9), np.float32(0.999),
+                np.float32(1e-8), s, r)
     dt = time.perf_counter() - t0
-    return dt, {"mean_loss": mean, "dW": dW, "db": db, "params": Wn}
+    # Adam on the GPU's own gradients: the update itself, bit for bit.
+    adam_exact = True
+    for p0, g, got in zip(W + b, first["dW"] + first["db"], first["W"] + first["b"]):
+        p = p0.copy()
+        g = np.ascontiguousarray(g, np.float32).reshape(p.shape).copy()
+        O.adam_(p, g, np.zeros_like(p), np.zeros_like(p), np.float32(0.9), np.float32(0.999),
+                np.float32(1e-8), s, r)
+        adam_exact &= bool(np.array_equal(p, got.reshape(p.shape)))
+    tol = 1e-5 * math.sqrt(4096)
+    err = {"loss": abs(first["mean_loss"] - mean) / max(1.0, abs(mean)),
+           "dW": max(rel_err(a, r_) for a, r_ in zip(first["dW"], dW)),
+           "db": max(rel_err(a, r_) for a, r_ in zip(first["db"], db))}
+    return dt, {"max_rel_err": err, "tolerance_gemm": tol, "adam_bit_exact_on_gpu_grads":
+                adam_exact, "parity_ok": bool(err["loss"] < 1e-5 and err["dW"] < tol and
+                                              err["db"] < tol and adam_exact)}
 
 
 def main() -> int:
@@ -560,7 +909,8 @@ def main() -> int:
     torch.cuda.synchronize()
     first = {"mean_loss": tr.mean_loss(),
              "dW": [tr.download(t).reshape(w.shape) for t, w in zip(tr.dW, tr.W)],
-             "db": [tr.download(t) for t in tr.db], "W": [w.cpu().numpy() for w in tr.W]}
+             "db": [tr.download(t) for t in tr.db], "W": [w.cpu().numpy() for w in tr.W],
+             "b": [b.cpu().numpy() for b in tr.b]}
     for _ in range(max(0, args.warmup - 1)):
         tr.step_eager()
     torch.cuda.synchronize()
@@ -593,23 +943,40 @@ def main() -> int:
     }
     step_flops = tr.gemm_flops()
 
-    comps = gemm_components(ctx, args.reps)
-    hid = comps["c5_hidden_fwd_gemm"]
+    want_cpu = not args.no_cpu
+    comps, c2_sample = gemm_components(ctx, args.reps, want_host=want_cpu and
+                                       not args.no_components)
+    # The dominant kernel of the step by time share (6 launches of each of
+    # the three hidden-layer GEMMs per step).
+    shares = c5_gemm_shares(ctx, args.reps, ms_per_step)
+    comps["c5_step_gemms"] = shares
+    dom_key = max(shares, key=lambda k: shares[k]["step_share"])
+    dom = shares[dom_key]
     roofline = {
         "bound": "mfma",
-        "kernel": "gemm_f32_pipe NN 2048x4096x4096 + bias + GELU (c5 hidden-layer forward)",
-        "achieved": hid["tflops"],
+        "kernel": "gemm_f32_pipe " + dom["what"] + " -- the c5 step's largest kernel time share",
+        "achieved": dom["tflops"],
         "peak": PEAK_FP32_MFMA_TFLOPS,
         "unit": "TFLOP/s",
-        "frac": hid["tflops"] / PEAK_FP32_MFMA_TFLOPS,
-        "traffic": measured_traffic("gemm_c5_hidden"),
+        "frac": dom["frac"],
+        "traffic": measured_traffic(dom_key),
         "traffic_unit": "HBM bytes per launch (rocprofv3 FETCH_SIZE/WRITE_SIZE, copy-calibrated)",
-        "algorithmic_bytes": hid["bytes"],
+        "algorithmic_bytes": dom["algorithmic_bytes"],
+        "step_share": dom["step_share"],
+        "others": {k: {"tflops": v["tflops"], "frac": v["frac"], "step_share": v["step_share"]}
+                   for k, v in shares.items() if k != dom_key},
     }
+    samples = {}
     if not args.no_components:
-        comps.update(softmax_component(ctx, args.reps))
+        r = softmax_component(ctx, args.reps, want_host=want_cpu)
+        if want_cpu:
+            r, samples["c3"] = r
+        comps.update(r)
         comps.update(adam_component(ctx, 10))
-        comps.update(c1_component(ctx))
+        r = c1_component(ctx, want_host=want_cpu)
+        if want_cpu:
+            r, samples["c1"] = r
+        comps.update(r)
         comps.update(gemm_bf16_component(ctx, args.reps))
         comps.update(c5_bf16_component(ctx))
         comps.update(copy_component(args.reps))
@@ -617,32 +984,39 @@ def main() -> int:
 
     cpu = None
     parity = None
-    if host is not None:
-        threads = min(16, os.cpu_count() or 1)
+    if want_cpu:
+        threads = cpu_threads()
+        log(f"CPU legs on {threads} threads (os.cpu_count() = {os.cpu_count()}, "
+            f"affinity {len(os.sched_getaffinity(0))}, OMP_NUM_THREADS = "
+            f"{os.environ.get('OMP_NUM_THREADS')})")
+        parity = {}
+        if not args.no_components:
+            c1c = cpu_c1(samples.pop("c1"), threads)
+            comps["c1_mlp_step"]["cpu"] = c1c
+            parity["c1"] = c1c["parity_ok"]
+            log("c1 CPU: " + json.dumps(c1c))
+            c2c = cpu_c2(c2_sample, threads)
+            c2_sample = None
+            comps["c2_gemm_4096"]["cpu"] = c2c
+            parity["c2"] = c2c["parity_ok"]
+            log("c2 CPU: " + json.dumps(c2c))
+            c3c = cpu_c3(samples.pop("c3"), threads)
+            comps["c3_softmax_ce_8192x32000"]["cpu"] = c3c
+            parity["c3"] = c3c["parity_ok"]
+            log("c3 CPU: " + json.dumps(c3c))
+            c4c = adam_sample_run(ctx, threads=threads)
+            comps["c4_adam_64x4Mi"]["cpu"] = c4c
+            parity["c4"] = c4c["parity_ok"]
+            log("c4 CPU: " + json.dumps(c4c))
         log(f"CPU baseline: one c5 step on {threads} threads")
-        dt, ref = cpu_baseline_c5(host, dims, batch, threads)
+        dt, c5p = cpu_c5(host, first, dims, threads)
         cpu = {"value": 1.0 / dt, "unit": "steps/s", "cores": threads, "kind": "port",
                "sample": "one full c5 training step (forward, CE, backward incl. dX, Adam) "
-                         "on the same inputs, oracle/ C restatement with OpenMP"}
-
-        def rel(a, b):
-            b = np.asarray(b, np.float64)
-            return float(np.max(np.abs(np.asarray(a, np.float64) - b)) /
-                         max(float(np.max(np.abs(b))), 1e-30))
-
-        parity = {
-            "loss_rel": abs(first["mean_loss"] - ref["mean_loss"]) / max(1.0, abs(ref["mean_loss"])),
-            "dW_max_rel": max(rel(a, b) for a, b in zip(first["dW"], ref["dW"])),
-            "db_max_rel": max(rel(a, b) for a, b in zip(first["db"], ref["db"])),
-            # Adam's first step is p - lr*g/(|g|+eps), i.e. nearly -lr*sign(g):
-            # where a gradient entry is within rounding noise of zero its sign
-            # (and so a 2*lr step) can differ, so report the fraction of
-            # parameters off by more than 1e-5 relative.
-            "W_after_adam_mismatch_frac": float(np.mean(np.concatenate([
-                (np.abs(a.astype(np.float64) - b) > 1e-5 * np.max(np.abs(b))).ravel()
-                for a, b in zip(first["W"], ref["params"][0::2])]))),
-            "tolerance_gemm": 1e-5 * math.sqrt(4096),
-        }
+                         "on the same inputs, oracle/ C restatement with OpenMP",
+               "nproc": os.cpu_count()}
+        parity["c5"] = c5p["parity_ok"]
+        parity["c5_detail"] = c5p
+        parity["all_ok"] = all(v for k, v in parity.items() if not k.endswith("_detail"))
         log("parity vs CPU: " + json.dumps(parity))
 
     result = {
@@ -676,6 +1050,10 @@ def main() -> int:
         "parity": parity,
     }
     print(json.dumps(result), flush=True)
+    if parity is not None and not parity["all_ok"]:
+        log("PARITY FAILED: " + json.dumps({k: v for k, v in parity.items()
+                                              if not k.endswith("_detail")}))
+        return 1
     return 0
 
 

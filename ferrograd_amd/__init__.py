@@ -108,6 +108,15 @@ class Context:
         call("fg_gemm_dw_f32", self.handle, M, N, K, _ptr(A), lda, _ptr(B), ldb, _ptr(C), ldc,
              int(accumulate), _ptr(colsum), int(colsum_accumulate))
 
+    def linear_bwd(self, act: int, M: int, N: int, K: int, X, ldx: int, W, ldw: int, Zs,
+                   ldzs: int, dC, lddc: int, dX=None, lddx: int = 0, dW=None, lddw: int = 0,
+                   dbias=None, accumulate: bool = False) -> None:
+        """Backward of C = act(X.W + bias): dZ = dC * act'(Zs) applied on load,
+        dX = dZ.W^T, dW = X^T.dZ, dbias = colsum(dZ) (any may be None)."""
+        call("fg_linear_bwd_f32", self.handle, act, M, N, K, _ptr(X), ldx, _ptr(W), ldw,
+             _ptr(Zs), ldzs, _ptr(dC), lddc, _ptr(dX), lddx or K, _ptr(dW), lddw or N,
+             _ptr(dbias), int(accumulate))
+
     def gemm_dw_x16(self, dtype: int, M: int, N: int, K: int, A, lda: int, B, ldb: int, C,
                     ldc: int, accumulate: bool = False, colsum=None,
                     colsum_accumulate: bool = False) -> None:

@@ -17,6 +17,7 @@
 #include <algorithm>
 #include <cstdint>
 
+#include "fg_act.h"
 #include "fg_half.h"
 
 namespace fg {
@@ -46,12 +47,18 @@ inline Split split_of(int cus, int M, int N) {
 }
 
 // DT: element type of dZ (fg_half.h codes); 16-bit rows are read 4
-// elements (8 bytes) at a time when aligned.
-template <int DT>
+// elements (8 bytes) at a time when aligned.  PACT != kActNone (fp32 only):
+// the rows summed are dZ * act'(Pz) (Pz[M][N], row stride ldp, the same
+// alignment as dZ), i.e. the bias gradient below an activation whose
+// derivative was not applied yet.
+template <int DT, int PACT = kActNone>
 __global__ __launch_bounds__(kThreads) void bias_grad_partial(const void *__restrict__ dZ, int M,
                                                               int N, int ld, int rows_per_split,
                                                               float *__restrict__ partial,
-                                                              int vec) {
+                                                              int vec,
+                                                              const float *__restrict__ Pz = nullptr,
+                                                              int ldp = 0) {
+    static_assert(PACT == kActNone || DT == fg::kF32, "prologue on fp32 rows only");
     typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
     __shared__ f32x4 sh[kThreads];
     const int strip = blockIdx.x, split = blockIdx.y;
@@ -66,8 +73,15 @@ __global__ __launch_bounds__(kThreads) void bias_grad_partial(const void *__rest
             const uint64_t row = (uint64_t)r * ld;
             if (vec && col + 4 <= N) {
                 if constexpr (DT == fg::kF32) {
-                    s += *reinterpret_cast<const f32x4 *>(static_cast<const float *>(dZ) + row +
-                                                          col);
+                    f32x4 v = *reinterpret_cast<const f32x4 *>(static_cast<const float *>(dZ) +
+                                                               row + col);
+                    if constexpr (PACT != kActNone) {
+                        const f32x4 z =
+                            *reinterpret_cast<const f32x4 *>(Pz + (uint64_t)r * ldp + col);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) v[e] *= act_grad(PACT, z[e]);
+                    }
+                    s += v;
                 } else {
                     const u32x2 w = *reinterpret_cast<const u32x2 *>(
                         static_cast<const uint16_t *>(dZ) + row + col);
@@ -77,8 +91,13 @@ __global__ __launch_bounds__(kThreads) void bias_grad_partial(const void *__rest
                 }
             } else {
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (col + e < N) s[e] += fg::load_as_f(dZ, DT, row + col + e);
+                for (int e = 0; e < 4; ++e) {
+                    if (col + e >= N) continue;
+                    float v = fg::load_as_f(dZ, DT, row + col + e);
+                    if constexpr (PACT != kActNone)
+                        v *= act_grad(PACT, Pz[(uint64_t)r * ldp + col + e]);
+                    s[e] += v;
+                }
             }
         }
     }
@@ -120,15 +139,25 @@ __global__ __launch_bounds__(kThreads) void bias_grad_final(const float *__restr
 }
 
 // Enqueues both passes; `partial` holds at least sp.splits * N floats.
-// dtype is an FG_DTYPE_* code (the fg_half.h codes coincide).
+// dtype is an FG_DTYPE_* code (the fg_half.h codes coincide).  pact / Pz /
+// ldp: the optional prologue of bias_grad_partial (fp32 dZ only; the caller
+// checks).
 inline hipError_t launch(hipStream_t st, const Split &sp, int dtype, int M, int N,
-                         const void *dZ, int ld, void *dbias, int accumulate, float *partial) {
+                         const void *dZ, int ld, void *dbias, int accumulate, float *partial,
+                         int pact = kActNone, const float *Pz = nullptr, int ldp = 0) {
     const unsigned align = dtype == fg::kF32 ? 16u : 8u;
-    const int vec = ((((uintptr_t)dZ) & (align - 1)) == 0) && (ld % 4 == 0);
+    int vec = ((((uintptr_t)dZ) & (align - 1)) == 0) && (ld % 4 == 0);
+    if (pact != kActNone) vec = vec && (((uintptr_t)Pz) & 15u) == 0 && ldp % 4 == 0;
     int splits = sp.splits;
     if (M > 0) {
         const dim3 grid(sp.strips, splits);
-        if (dtype == fg::kF32)
+        if (pact == kActRelu)
+            bias_grad_partial<fg::kF32, kActRelu><<<grid, kThreads, 0, st>>>(
+                dZ, M, N, ld, sp.rows_per_split, partial, vec, Pz, ldp);
+        else if (pact == kActGelu)
+            bias_grad_partial<fg::kF32, kActGelu><<<grid, kThreads, 0, st>>>(
+                dZ, M, N, ld, sp.rows_per_split, partial, vec, Pz, ldp);
+        else if (dtype == fg::kF32)
             bias_grad_partial<fg::kF32>
                 <<<grid, kThreads, 0, st>>>(dZ, M, N, ld, sp.rows_per_split, partial, vec);
         else if (dtype == fg::kF16)

@@ -93,16 +93,41 @@ struct GemmArgs {
     // the epilogue.
     float *partial;
     int ksplit;
+    // Prologue (kernels instantiated with PRO != 0): the operand that holds
+    // dC -- A of NT (dA = dZ.B^T) or B of TN (dB = A^T.dZ) -- is multiplied
+    // elementwise by act'(Pz) as its tiles are loaded, so dZ = dC * act'(Z)
+    // is never materialised.  Pz has that operand's shape, row stride ldp.
+    const float *Pz;
+    int ldp;
 };
+
+// Prologue codes (template parameter PRO of the kernels): which operand is
+// multiplied by act'(Pz) on load, and which activation.
+enum : int { kProNone = 0, kProAReLU = 1, kProAGelu = 2, kProBReLU = 3, kProBGelu = 4 };
+constexpr bool pro_on_a(int pro) { return pro == kProAReLU || pro == kProAGelu; }
+constexpr bool pro_on_b(int pro) { return pro == kProBReLU || pro == kProBGelu; }
+constexpr int pro_act(int pro) {
+    return (pro == kProAReLU || pro == kProBReLU) ? kActRelu : kActGelu;
+}
+
+// v * act'(z), elementwise (the same fp32 product as the unfused dact pass).
+template <int ACT>
+__device__ __forceinline__ f32x4 pro_scale(f32x4 v, f32x4 z) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] *= act_grad(ACT, z[e]);
+    return v;
+}
 
 // The view of a split-K workgroup: its K slice of A and B, its raw-product
 // slot as C, no epilogue.
-template <bool AK, bool BNC>
+template <bool AK, bool BNC, int PRO>
 __device__ __forceinline__ void split_k_view(GemmArgs &p) {
     if (p.ksplit <= 0) return;
     const int s = blockIdx.y, kb = s * p.ksplit;
     p.A += AK ? (size_t)kb : (size_t)kb * p.lda;
     p.B += BNC ? (size_t)kb * p.ldb : (size_t)kb;
+    if constexpr (pro_on_a(PRO)) p.Pz += AK ? (size_t)kb : (size_t)kb * p.ldp;
+    if constexpr (pro_on_b(PRO)) p.Pz += BNC ? (size_t)kb * p.ldp : (size_t)kb;
     p.K = min(p.ksplit, p.K - kb);
     p.C = p.partial + (size_t)s * p.M * p.N;
     p.ldc = p.N;
@@ -207,6 +232,19 @@ struct TileLoader {
                 const bool ok = (gr < rmax) && (gk < K);
                 v1[q] = ok ? (KC ? base[(size_t)gr * ld + gk] : base[(size_t)gk * ld + gr]) : 0.0f;
             }
+        }
+    }
+
+    // Multiplies the loaded elements by act'(z) of the same elements (z
+    // loaded by a loader of the same shape from the prologue tensor).
+    template <int ACT>
+    __device__ __forceinline__ void scale_by(const TileLoader &z) {
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) {
+            if constexpr (VEC)
+                v4[q] = pro_scale<ACT>(v4[q], z.v4[q]);
+            else
+                v1[q] *= act_grad(ACT, z.v1[q]);
         }
     }
 
@@ -348,9 +386,9 @@ __device__ __forceinline__ void store_tile(const GemmArgs &p, const f32x16 (&acc
     }
 }
 
-template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC, bool VEC>
+template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC, bool VEC, int PRO>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_mfma(GemmArgs p) {
-    split_k_view<AK, BNC>(p);
+    split_k_view<AK, BNC, PRO>(p);
     constexpr int NT = 64 * WGM * WGN;
     static_assert(WGM * WGN == 4 || WGM * WGN == 8, "4 or 8 waves per workgroup");
     constexpr int WTM = BM / WGM, WTN = BN / WGN;
@@ -377,24 +415,34 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_mfma(GemmArgs p) {
 
     TileLoader<BM, BK, AK, VEC, NT> la;
     TileLoader<BN, BK, !BNC, VEC, NT> lb;
+    // Prologue: act' tiles of the operand that holds dC (loaded with it).
+    TileLoader<BM, BK, AK, VEC, NT> za;
+    TileLoader<BN, BK, !BNC, VEC, NT> zb;
     const int nk = (p.K + BK - 1) / BK;
     constexpr bool kTN = !AK && BNC;
     ColSum<BN, BK, NT> cs;
     const bool do_cs = kTN && p.colsum && tile_m == 0;
+    auto load_tiles = [&](int k0) {
+        la.load(p.A, p.lda, m0, p.M, k0, p.K);
+        lb.load(p.B, p.ldb, n0, p.N, k0, p.K);
+        if constexpr (pro_on_a(PRO)) za.load(p.Pz, p.ldp, m0, p.M, k0, p.K);
+        if constexpr (pro_on_b(PRO)) zb.load(p.Pz, p.ldp, n0, p.N, k0, p.K);
+    };
+    auto store_tiles = [&](float *dst) {
+        if constexpr (pro_on_a(PRO)) la.template scale_by<pro_act(PRO)>(za);
+        if constexpr (pro_on_b(PRO)) lb.template scale_by<pro_act(PRO)>(zb);
+        la.store(dst);
+        lb.store(dst + L::a_sz);
+    };
 
-    la.load(p.A, p.lda, m0, p.M, 0, p.K);
-    lb.load(p.B, p.ldb, n0, p.N, 0, p.K);
-    la.store(lds);
-    lb.store(lds + L::a_sz);
+    load_tiles(0);
+    store_tiles(lds);
     __syncthreads();
 
     for (int kt = 0; kt < nk; ++kt) {
         const int cur = kt & 1;
         const bool more = kt + 1 < nk;
-        if (more) {
-            la.load(p.A, p.lda, m0, p.M, (kt + 1) * BK, p.K);
-            lb.load(p.B, p.ldb, n0, p.N, (kt + 1) * BK, p.K);
-        }
+        if (more) load_tiles((kt + 1) * BK);
         const float *As = lds + cur * L::buf;
         const float *Bs = As + L::a_sz;
         // Group g of the tile (4 consecutive k per lane half): lane half h
@@ -441,11 +489,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_mfma(GemmArgs p) {
         }
         if constexpr (kTN)
             if (do_cs) cs.add([&](int k, int c) { return Bs[k * L::b_ld + c]; });
-        if (more) {
-            float *nxt = lds + (cur ^ 1) * L::buf;
-            la.store(nxt);
-            lb.store(nxt + L::a_sz);
-        }
+        if (more) store_tiles(lds + (cur ^ 1) * L::buf);
         __syncthreads();
     }
 
@@ -488,9 +532,9 @@ __device__ __forceinline__ int swz_k(int row) {
 }
 __device__ __forceinline__ int swz_r(int k) { return ((k >> 3) & 1) * 8; }
 
-template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC>
+template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC, int PRO>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_pipe(GemmArgs p) {
-    split_k_view<AK, BNC>(p);
+    split_k_view<AK, BNC, PRO>(p);
     constexpr int NW = WGM * WGN;
     constexpr int WTM = BM / WGM, WTN = BN / WGN;
     constexpr int TM = WTM / 32, TN = WTN / 32;
@@ -501,6 +545,9 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_pipe(GemmArgs p) {
     constexpr int kPerA = kInstA / NW, kPerB = kInstB / NW, kLoads = kPerA + kPerB;
     constexpr int kASz = BM * BK, kBSz = BN * BK, kStageSz = kASz + kBSz;
     constexpr bool kStaged = !(BM == 256 && BN == 256);
+    // The prologue scales a tile in registers, between its load and its LDS
+    // write: staged tiles only.
+    static_assert(PRO == kProNone || kStaged, "prologue needs the staged path");
     // Staged: two stages.  Direct: three (two tiles in flight) when they fit
     // in the 160 KiB of LDS, else two.
     constexpr int kStages = kStaged ? 2 : 3 * kStageSz * 4 <= 160 * 1024 ? 3 : 2;
@@ -576,6 +623,33 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_pipe(GemmArgs p) {
     auto load_reg = [&](int kt, int q) { return *reinterpret_cast<const f32x4 *>(src_of(kt, q)); };
     auto store_reg = [&](int stage, int q, const f32x4 &v) {
         *reinterpret_cast<f32x4 *>(run_of(stage, q) + 4 * lane) = v;
+    };
+    // Prologue: each wave load of the operand that holds dC (loads
+    // kProFirst .. kProFirst+kPro-1) is paired with a load of Pz at the same
+    // position; the chunk is multiplied by act'(Pz) before its LDS write.
+    constexpr int kPro = pro_on_a(PRO) ? kPerA : pro_on_b(PRO) ? kPerB : 0;
+    constexpr int kProFirst = pro_on_a(PRO) ? 0 : kPerA;
+    constexpr int kProN = kPro > 0 ? kPro : 1;  // register-set size
+    auto is_pro = [](int q) { return q >= kProFirst && q < kProFirst + kPro; };
+    auto load_pz = [&](int kt, int q) -> f32x4 {
+        const int k0 = kt * BK;
+        const float *src;
+        if constexpr (pro_on_a(PRO)) {
+            const int pos = (wave * kPerA + q) * 64 + lane;
+            src = AK ? src_kc(p.Pz, p.ldp, m0, p.M, k0, pos)
+                     : src_rc(p.Pz, p.ldp, m0, p.M, k0, pos, BM);
+        } else {
+            const int pos = (wave * kPerB + (q - kPerA)) * 64 + lane;
+            src = BNC ? src_rc(p.Pz, p.ldp, n0, p.N, k0, pos, BN)
+                      : src_kc(p.Pz, p.ldp, n0, p.N, k0, pos);
+        }
+        return *reinterpret_cast<const f32x4 *>(src);
+    };
+    // Chunk q of register set (R, Z) as it goes to LDS.
+    auto staged_value = [&](const f32x4 *R, const f32x4 *Zr, int q) -> f32x4 {
+        if constexpr (PRO != kProNone)
+            if (is_pro(q)) return pro_scale<pro_act(PRO)>(R[q], Zr[q - kProFirst]);
+        return R[q];
     };
 
     const int nk = p.K / BK;
@@ -667,7 +741,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_pipe(GemmArgs p) {
     // issues one load of tile kl into stage `slot`.
     auto run_group = [&](const f32x4 (&ca)[TM], const f32x4 (&cb)[TN], const float *An,
                          const float *Bn, int gn, f32x4 (&na)[TM], f32x4 (&nb)[TN], bool ld,
-                         int kl, int slot, const f32x4 *Rw, f32x4 *Rl) {
+                         int kl, int slot, const f32x4 *Rw, f32x4 *Rl, const f32x4 *Zw,
+                         f32x4 *Zl) {
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int m = 0; m < kMfma; ++m) {
@@ -679,8 +754,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_pipe(GemmArgs p) {
             if (ld) {
                 if constexpr (kStaged) {
                     if (m < kLoads) {
-                        store_reg(slot, m, Rw[m]);
+                        store_reg(slot, m, staged_value(Rw, Zw, m));
                         Rl[m] = load_reg(kl, m);
+                        if constexpr (PRO != kProNone)
+                            if (is_pro(m)) Zl[m - kProFirst] = load_pz(kl, m);
                     }
                 } else {
                     if (m % kStride == 0 && m / kStride < kLoads) issue_direct(kl, slot, m / kStride);
@@ -699,7 +776,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_pipe(GemmArgs p) {
     // the barrier.  Past that barrier every wave holds all of tile kt's
     // operands and its stage may be refilled.
     f32x4 ca[TM], cb[TN];
-    auto tile = [&](int kt, int kl, int slot, const f32x4 *Rw, f32x4 *Rl) {
+    auto tile = [&](int kt, int kl, int slot, const f32x4 *Rw, f32x4 *Rl, const f32x4 *Zw,
+                    f32x4 *Zl) {
         const float *As = lds + (kt % kStages) * kStageSz;
         const float *Bs = As + kASz;
 #pragma unroll
@@ -709,7 +787,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_pipe(GemmArgs p) {
             // issued, leaves those in flight behind the MFMAs.
             wait_lgkm0();
             f32x4 na[TM], nb[TN];
-            run_group(ca, cb, As, Bs, g + 1, na, nb, g == 0, kl, slot, Rw, Rl);
+            run_group(ca, cb, As, Bs, g + 1, na, nb, g == 0, kl, slot, Rw, Rl, Zw, Zl);
 #pragma unroll
             for (int i = 0; i < TM; ++i) ca[i] = na[i];
 #pragma unroll
@@ -729,7 +807,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_pipe(GemmArgs p) {
         // read and discarded).
         f32x4 na[TM], nb[TN];
         const float *An = lds + ((kt + 1) % kStages) * kStageSz;
-        run_group(ca, cb, An, An + kASz, 0, na, nb, false, 0, 0, Rw, Rl);
+        run_group(ca, cb, An, An + kASz, 0, na, nb, false, 0, 0, Rw, Rl, Zw, Zl);
 #pragma unroll
         for (int i = 0; i < TM; ++i) ca[i] = na[i];
 #pragma unroll
@@ -746,12 +824,21 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_pipe(GemmArgs p) {
         // register sets swap roles without copies.
         if (nk > 0) {
             f32x4 R0[kLoads], R1[kLoads];
+            f32x4 Z0[kProN], Z1[kProN];  // prologue chunks (unused without PRO)
 #pragma unroll
-            for (int q = 0; q < kLoads; ++q) R0[q] = load_reg(0, q);
+            for (int q = 0; q < kLoads; ++q) {
+                R0[q] = load_reg(0, q);
+                if constexpr (PRO != kProNone)
+                    if (is_pro(q)) Z0[q - kProFirst] = load_pz(0, q);
+            }
 #pragma unroll
-            for (int q = 0; q < kLoads; ++q) R1[q] = load_reg(min(1, nk - 1), q);
+            for (int q = 0; q < kLoads; ++q) {
+                R1[q] = load_reg(min(1, nk - 1), q);
+                if constexpr (PRO != kProNone)
+                    if (is_pro(q)) Z1[q - kProFirst] = load_pz(min(1, nk - 1), q);
+            }
 #pragma unroll
-            for (int q = 0; q < kLoads; ++q) store_reg(0, q, R0[q]);
+            for (int q = 0; q < kLoads; ++q) store_reg(0, q, staged_value(R0, Z0, q));
             wait_lgkm0();
             asm volatile("s_barrier" ::: "memory");
             frag(lds, lds + kASz, 0, ca, cb);
@@ -760,13 +847,13 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_pipe(GemmArgs p) {
             int kt = 0;
             for (; kt + 1 < nk; kt += 2) {
                 wait_vmcnt<0>();
-                tile(kt, min(kt + 2, nk - 1), (kt + 1) % kStages, R1, R0);
+                tile(kt, min(kt + 2, nk - 1), (kt + 1) % kStages, R1, R0, Z1, Z0);
                 wait_vmcnt<0>();
-                tile(kt + 1, min(kt + 3, nk - 1), kt % kStages, R0, R1);
+                tile(kt + 1, min(kt + 3, nk - 1), kt % kStages, R0, R1, Z0, Z1);
             }
             if (kt < nk) {
                 wait_vmcnt<0>();
-                tile(kt, nk - 1, (kt + 1) % kStages, R1, R0);
+                tile(kt, nk - 1, (kt + 1) % kStages, R1, R0, Z1, Z0);
             }
         }
     } else {
@@ -785,7 +872,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_pipe(GemmArgs p) {
             asm volatile("s_barrier" ::: "memory");
             frag(lds, lds + kASz, 0, ca, cb);
             for (int kt = 0; kt < nk; ++kt)
-                tile(kt, min(kt + kAhead, nk - 1), (kt + kAhead) % kStages, nullptr, nullptr);
+                tile(kt, min(kt + kAhead, nk - 1), (kt + kAhead) % kStages, nullptr, nullptr,
+                     nullptr, nullptr);
             wait_vmcnt<0>();  // the reloads past the last tile, before the LDS reuse
         }
     }
@@ -795,23 +883,23 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_pipe(GemmArgs p) {
     store_tile<TM, TN, WTN, NW>(p, acc, lds, m0 + wm0, n0 + wn0, wave, lane);
 }
 
-template <int BM, int BN, int WGM, int WGN, int BK, bool AK, bool BNC>
+template <int BM, int BN, int WGM, int WGN, int BK, bool AK, bool BNC, int PRO>
 void launch_pipe(const GemmArgs &a0, hipStream_t st) {
     GemmArgs a = a0;
     a.tiles_m = (a.M + BM - 1) / BM;
     a.tiles_n = (a.N + BN - 1) / BN;
     const int splits = a.ksplit > 0 ? (a.K + a.ksplit - 1) / a.ksplit : 1;
-    gemm_f32_pipe<BM, BN, BK, WGM, WGN, AK, BNC>
+    gemm_f32_pipe<BM, BN, BK, WGM, WGN, AK, BNC, PRO>
         <<<dim3(a.tiles_m * a.tiles_n, splits), 64 * WGM * WGN, 0, st>>>(a);
 }
 
-template <int BM, int BN, int WGM, int WGN, int BK, bool AK, bool BNC, bool VEC>
+template <int BM, int BN, int WGM, int WGN, int BK, bool AK, bool BNC, bool VEC, int PRO>
 void launch_one(const GemmArgs &a0, hipStream_t st) {
     GemmArgs a = a0;
     a.tiles_m = (a.M + BM - 1) / BM;
     a.tiles_n = (a.N + BN - 1) / BN;
     const int splits = a.ksplit > 0 ? (a.K + a.ksplit - 1) / a.ksplit : 1;
-    gemm_f32_mfma<BM, BN, BK, WGM, WGN, AK, BNC, VEC>
+    gemm_f32_mfma<BM, BN, BK, WGM, WGN, AK, BNC, VEC, PRO>
         <<<dim3(a.tiles_m * a.tiles_n, splits), 64 * WGM * WGN, 0, st>>>(a);
 }
 
@@ -834,43 +922,61 @@ inline void cfg_tile(int cfg, bool vec, int &bm, int &bn) {
     bn = vec ? kBn[cfg] : 64;
 }
 
+// Configuration used with a prologue: the 256x256 tiles load directly into
+// LDS, which leaves no point to scale a tile at, so they give way to the
+// 256x128 tile with the same waves.
+inline int pro_cfg(int cfg) { return cfg == 0 ? 1 : cfg == 6 ? 7 : cfg; }
+
 // pipe: K % cfg_bk(cfg) == 0 and the VEC conditions hold (the host checks):
-// the pipelined whole-tile kernel with the same tile shape.
-template <bool AK, bool BNC>
+// the pipelined whole-tile kernel with the same tile shape.  With PRO != 0
+// the host has mapped cfg through pro_cfg.
+template <bool AK, bool BNC, int PRO>
 void launch_layout(const GemmArgs &a, bool vec, bool pipe, int cfg, hipStream_t st) {
     if (!vec) {
-        launch_one<64, 64, 2, 2, 16, AK, BNC, false>(a, st);
+        launch_one<64, 64, 2, 2, 16, AK, BNC, false, PRO>(a, st);
         return;
     }
     if (pipe) {
         switch (cfg) {
-            case 0: launch_pipe<256, 256, 2, 2, kBK, AK, BNC>(a, st); break;
-            case 1: launch_pipe<256, 128, 2, 2, kBK, AK, BNC>(a, st); break;
-            case 2: launch_pipe<128, 256, 2, 2, kBK, AK, BNC>(a, st); break;
-            case 3: launch_pipe<128, 128, 2, 2, 32, AK, BNC>(a, st); break;
-            case 5: launch_pipe<128, 64, 2, 2, 32, AK, BNC>(a, st); break;
-            case 6: launch_pipe<256, 256, 2, 4, 32, AK, BNC>(a, st); break;
-            case 7: launch_pipe<256, 128, 4, 2, 32, AK, BNC>(a, st); break;
-            default: launch_pipe<64, 64, 2, 2, 16, AK, BNC>(a, st); break;
+            case 0:
+                if constexpr (PRO == kProNone) launch_pipe<256, 256, 2, 2, kBK, AK, BNC, PRO>(a, st);
+                break;
+            case 1: launch_pipe<256, 128, 2, 2, kBK, AK, BNC, PRO>(a, st); break;
+            case 2: launch_pipe<128, 256, 2, 2, kBK, AK, BNC, PRO>(a, st); break;
+            case 3: launch_pipe<128, 128, 2, 2, 32, AK, BNC, PRO>(a, st); break;
+            case 5: launch_pipe<128, 64, 2, 2, 32, AK, BNC, PRO>(a, st); break;
+            case 6:
+                if constexpr (PRO == kProNone) launch_pipe<256, 256, 2, 4, 32, AK, BNC, PRO>(a, st);
+                break;
+            case 7: launch_pipe<256, 128, 4, 2, 32, AK, BNC, PRO>(a, st); break;
+            default: launch_pipe<64, 64, 2, 2, 16, AK, BNC, PRO>(a, st); break;
         }
         return;
     }
     switch (cfg) {
-        case 0: launch_one<256, 256, 2, 2, kBK, AK, BNC, true>(a, st); break;
-        case 1: launch_one<256, 128, 2, 2, kBK, AK, BNC, true>(a, st); break;
-        case 2: launch_one<128, 256, 2, 2, kBK, AK, BNC, true>(a, st); break;
-        case 3: launch_one<128, 128, 2, 2, 32, AK, BNC, true>(a, st); break;
-        case 5: launch_one<128, 64, 2, 2, 32, AK, BNC, true>(a, st); break;
-        case 6: launch_one<256, 256, 2, 4, 32, AK, BNC, true>(a, st); break;
-        case 7: launch_one<256, 128, 4, 2, 32, AK, BNC, true>(a, st); break;
-        default: launch_one<64, 64, 2, 2, 16, AK, BNC, true>(a, st); break;
+        case 0:
+            if constexpr (PRO == kProNone) launch_one<256, 256, 2, 2, kBK, AK, BNC, true, PRO>(a, st);
+            break;
+        case 1: launch_one<256, 128, 2, 2, kBK, AK, BNC, true, PRO>(a, st); break;
+        case 2: launch_one<128, 256, 2, 2, kBK, AK, BNC, true, PRO>(a, st); break;
+        case 3: launch_one<128, 128, 2, 2, 32, AK, BNC, true, PRO>(a, st); break;
+        case 5: launch_one<128, 64, 2, 2, 32, AK, BNC, true, PRO>(a, st); break;
+        case 6:
+            if constexpr (PRO == kProNone) launch_one<256, 256, 2, 4, 32, AK, BNC, true, PRO>(a, st);
+            break;
+        case 7: launch_one<256, 128, 4, 2, 32, AK, BNC, true, PRO>(a, st); break;
+        default: launch_one<64, 64, 2, 2, 16, AK, BNC, true, PRO>(a, st); break;
     }
 }
 
 // Defined in k_gemm_{nn,nt,tn}.hip.
+// pro: kProNone, or for NT kProAReLU / kProAGelu, for TN kProBReLU / kProBGelu.
 void launch_nn(const GemmArgs &a, bool vec, bool pipe, int cfg, hipStream_t st);
-void launch_nt(const GemmArgs &a, bool vec, bool pipe, int cfg, hipStream_t st);
-void launch_tn(const GemmArgs &a, bool vec, bool pipe, int cfg, hipStream_t st);
+void launch_nt(const GemmArgs &a, bool vec, bool pipe, int cfg, int pro, hipStream_t st);
+void launch_tn(const GemmArgs &a, bool vec, bool pipe, int cfg, int pro, hipStream_t st);
+// The prologue instances (k_gemm_{nt,tn}_pro.hip), pro != kProNone.
+void launch_nt_pro(const GemmArgs &a, bool vec, bool pipe, int cfg, int pro, hipStream_t st);
+void launch_tn_pro(const GemmArgs &a, bool vec, bool pipe, int cfg, int pro, hipStream_t st);
 
 }  // namespace gemm
 }  // namespace fg

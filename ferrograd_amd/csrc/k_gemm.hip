@@ -105,9 +105,11 @@ int plan_split_k(fg_ctx *ctx, GemmArgs &a, int cfg, bool vec) {
 
 // The kernel choices of one GEMM call (sets a.vec_out, and a.partial /
 // a.ksplit when K is split): 16-byte operand loads (vec), the pipelined
-// kernel (pipe), the tile configuration and the number of K slices.
+// kernel (pipe), the tile configuration and the number of K slices.  pro:
+// the prologue code (fg::gemm::kPro*), whose tensor Pz must meet the same
+// 16-byte conditions as the operand it scales.
 void plan_gemm(fg_ctx *ctx, int layout, GemmArgs &a, bool &vec, bool &pipe, int &cfg,
-               int &splits) {
+               int &splits, int pro = fg::gemm::kProNone) {
     // The 16-byte path needs 16-byte aligned bases and every row start
     // aligned, i.e. leading dimensions and the contiguous extents that the
     // bounds checks split on (K for k-contiguous operands, M / N otherwise)
@@ -117,11 +119,13 @@ void plan_gemm(fg_ctx *ctx, int layout, GemmArgs &a, bool &vec, bool &pipe, int 
     if (layout == FG_NN) vec = vec && a.K % 4 == 0 && a.N % 4 == 0;
     if (layout == FG_NT) vec = vec && a.K % 4 == 0;
     if (layout == FG_TN) vec = vec && a.M % 4 == 0 && a.N % 4 == 0;
+    if (pro != fg::gemm::kProNone) vec = vec && (((uintptr_t)a.Pz) & 15u) == 0 && a.ldp % 4 == 0;
 #ifdef FG_GEMM_FORCE_CFG  // tuning builds: one tile configuration for every shape
     cfg = FG_GEMM_FORCE_CFG;
 #else
     cfg = pick_cfg(layout, a.M, a.N, a.K, ctx->cu_count > 0 ? ctx->cu_count : 256);
 #endif
+    if (pro != fg::gemm::kProNone) cfg = fg::gemm::pro_cfg(cfg);
     auto al16 = [](const void *q) { return (((uintptr_t)q) & 15u) == 0; };
     a.vec_out = al16(a.C) && a.ldc % 4 == 0 && (!a.Z || (al16(a.Z) && a.ldz % 4 == 0)) &&
                 (!a.bias || al16(a.bias));
@@ -134,7 +138,8 @@ void plan_gemm(fg_ctx *ctx, int layout, GemmArgs &a, bool &vec, bool &pipe, int 
     splits = plan_split_k(ctx, a, cfg, vec);
 }
 
-int gemm_common(fg_ctx *ctx, int layout, GemmArgs &a, const char *who) {
+int gemm_common(fg_ctx *ctx, int layout, GemmArgs &a, const char *who,
+                int pro = fg::gemm::kProNone) {
     FG_REQUIRE(ctx, FG_ERR_INVALID_ARGUMENT, "%s: ctx is NULL", who);
     FG_REQUIRE(layout >= FG_NN && layout <= FG_TN, FG_ERR_INVALID_ARGUMENT, "%s: bad layout %d",
                who, layout);
@@ -153,11 +158,11 @@ int gemm_common(fg_ctx *ctx, int layout, GemmArgs &a, const char *who) {
     if (a.K == 0) a.A = a.B;  // loads are all masked; K=0 yields the epilogue of zero
     bool vec, pipe;
     int cfg, splits;
-    plan_gemm(ctx, layout, a, vec, pipe, cfg, splits);
+    plan_gemm(ctx, layout, a, vec, pipe, cfg, splits, pro);
     switch (layout) {
         case FG_NN: fg::gemm::launch_nn(a, vec, pipe, cfg, ctx->stream); break;
-        case FG_NT: fg::gemm::launch_nt(a, vec, pipe, cfg, ctx->stream); break;
-        default: fg::gemm::launch_tn(a, vec, pipe, cfg, ctx->stream); break;
+        case FG_NT: fg::gemm::launch_nt(a, vec, pipe, cfg, pro, ctx->stream); break;
+        default: fg::gemm::launch_tn(a, vec, pipe, cfg, pro, ctx->stream); break;
     }
     FG_LAUNCH_CHECK(who);
     if (splits > 1) {
@@ -246,9 +251,12 @@ FG_API int fg_gemm_bwd_f32(fg_ctx *ctx, int layout, int M, int N, int K, const f
     return gemm_common(ctx, layout, a, "fg_gemm_bwd_f32");
 }
 
-FG_API int fg_gemm_dw_f32(fg_ctx *ctx, int M, int N, int K, const float *d_A, int lda,
-                          const float *d_B, int ldb, float *d_C, int ldc, int accumulate,
-                          float *d_colsum, int colsum_accumulate) {
+namespace {
+// C (=|+=) A^T.B with colsum (=|+=) the column sums of B (TN); with a
+// prologue, B is scaled by act'(Pz) on load and the sums are of the scaled B.
+int gemm_dw(fg_ctx *ctx, int M, int N, int K, const float *d_A, int lda, const float *d_B,
+            int ldb, float *d_C, int ldc, int accumulate, float *d_colsum, int colsum_accumulate,
+            const float *d_Pz, int ldp, int pro, const char *who) {
     GemmArgs a{};
     a.A = d_A;
     a.B = d_B;
@@ -264,9 +272,11 @@ FG_API int fg_gemm_dw_f32(fg_ctx *ctx, int M, int N, int K, const float *d_A, in
     a.accumulate = accumulate ? 1 : 0;
     a.colsum = d_colsum;
     a.colsum_accumulate = colsum_accumulate ? 1 : 0;
+    a.Pz = d_Pz;
+    a.ldp = ldp;
     if (d_colsum && (M == 0 || K == 0)) {
         // No tile runs the column sums: an empty reduction.
-        FG_REQUIRE(ctx, FG_ERR_INVALID_ARGUMENT, "fg_gemm_dw_f32: ctx is NULL");
+        FG_REQUIRE(ctx, FG_ERR_INVALID_ARGUMENT, "%s: ctx is NULL", who);
         if (N > 0 && !colsum_accumulate) {  // a fill kernel: safe under stream capture
             const int rc = fg_fill_u32(ctx, d_colsum, 0u, (uint64_t)N);
             if (rc) return rc;
@@ -274,7 +284,71 @@ FG_API int fg_gemm_dw_f32(fg_ctx *ctx, int M, int N, int K, const float *d_A, in
         if (M == 0) return FG_OK;
         a.colsum = nullptr;
     }
-    return gemm_common(ctx, FG_TN, a, "fg_gemm_dw_f32");
+    return gemm_common(ctx, FG_TN, a, who, pro);
+}
+}  // namespace
+
+FG_API int fg_gemm_dw_f32(fg_ctx *ctx, int M, int N, int K, const float *d_A, int lda,
+                          const float *d_B, int ldb, float *d_C, int ldc, int accumulate,
+                          float *d_colsum, int colsum_accumulate) {
+    return gemm_dw(ctx, M, N, K, d_A, lda, d_B, ldb, d_C, ldc, accumulate, d_colsum,
+                   colsum_accumulate, nullptr, 0, fg::gemm::kProNone, "fg_gemm_dw_f32");
+}
+
+FG_API int fg_linear_bwd_f32(fg_ctx *ctx, int act, int M, int N, int K, const float *d_X,
+                             int ldx, const float *d_W, int ldw, const float *d_Zs, int ldzs,
+                             const float *d_dC, int lddc, float *d_dX, int lddx, float *d_dW,
+                             int lddw, float *d_dbias, int accumulate) {
+    const char *who = "fg_linear_bwd_f32";
+    FG_REQUIRE(ctx, FG_ERR_INVALID_ARGUMENT, "%s: ctx is NULL", who);
+    FG_REQUIRE(act >= FG_ACT_NONE && act <= FG_ACT_GELU, FG_ERR_INVALID_ARGUMENT,
+               "%s: bad act %d", who, act);
+    FG_REQUIRE(M >= 0 && N >= 0 && K >= 0, FG_ERR_SHAPE, "%s: negative dimension", who);
+    if (N == 0) return FG_OK;
+    FG_REQUIRE(d_dC && lddc >= N, FG_ERR_INVALID_ARGUMENT, "%s: dC NULL or lddc < N", who);
+    FG_REQUIRE(act == FG_ACT_NONE || (d_Zs && ldzs >= N), FG_ERR_INVALID_ARGUMENT,
+               "%s: act %d needs Zs with ldzs >= N", who, act);
+    using namespace fg::gemm;
+    const int pro_tn = act == FG_ACT_RELU ? kProBReLU : act == FG_ACT_GELU ? kProBGelu : kProNone;
+    const int pro_nt = act == FG_ACT_RELU ? kProAReLU : act == FG_ACT_GELU ? kProAGelu : kProNone;
+    if (d_dW && K > 0) {  // dW = X^T.dZ (TN, dZ the B operand) with dbias from its tiles
+        FG_REQUIRE(d_X && ldx >= std::max(K, 1) && lddw >= N, FG_ERR_INVALID_ARGUMENT,
+                   "%s: X NULL or ldx < K or lddw < N", who);
+        const int rc = gemm_dw(ctx, K, N, M, d_X, ldx, d_dC, lddc, d_dW, lddw, accumulate,
+                               d_dbias, accumulate, d_Zs, ldzs, pro_tn, who);
+        if (rc) return rc;
+    } else if (d_dbias) {  // dbias alone: the column reduction with the prologue
+        FG_HIP(hipSetDevice(ctx->device));
+        const fg::colsum::Split sp =
+            fg::colsum::split_of(ctx->cu_count > 0 ? ctx->cu_count : 256, M, N);
+        float *partial = (float *)fg::workspace(
+            ctx, std::max<uint64_t>(sp.partial_floats(N), 1) * sizeof(float));
+        if (!partial) return FG_ERR_OUT_OF_MEMORY;
+        FG_HIP(fg::colsum::launch(ctx->stream, sp, FG_DTYPE_F32, M, N, d_dC, lddc, d_dbias,
+                                  accumulate, partial, act, d_Zs, ldzs));
+    }
+    if (d_dX && K > 0) {  // dX = dZ.W^T (NT, dZ the A operand)
+        FG_REQUIRE(d_W && ldw >= N && lddx >= K, FG_ERR_INVALID_ARGUMENT,
+                   "%s: W NULL or ldw < N or lddx < K", who);
+        GemmArgs a{};
+        a.A = d_dC;
+        a.lda = lddc;
+        a.B = d_W;
+        a.ldb = ldw;
+        a.C = d_dX;
+        a.ldc = lddx;
+        a.M = M;
+        a.N = K;
+        a.K = N;
+        a.mode = 1;
+        a.act = FG_ACT_NONE;
+        a.accumulate = accumulate ? 1 : 0;
+        a.Pz = d_Zs;
+        a.ldp = ldzs;
+        const int rc = gemm_common(ctx, FG_NT, a, who, pro_nt);
+        if (rc) return rc;
+    }
+    return FG_OK;
 }
 
 namespace fg {

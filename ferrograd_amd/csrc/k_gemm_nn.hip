@@ -6,7 +6,7 @@ namespace fg {
 namespace gemm {
 
 void launch_nn(const GemmArgs &a, bool vec, bool pipe, int cfg, hipStream_t st) {
-    launch_layout<true, true>(a, vec, pipe, cfg, st);
+    launch_layout<true, true, kProNone>(a, vec, pipe, cfg, st);
 }
 
 }  // namespace gemm

@@ -5,8 +5,11 @@
 namespace fg {
 namespace gemm {
 
-void launch_nt(const GemmArgs &a, bool vec, bool pipe, int cfg, hipStream_t st) {
-    launch_layout<true, false>(a, vec, pipe, cfg, st);
+void launch_nt(const GemmArgs &a, bool vec, bool pipe, int cfg, int pro, hipStream_t st) {
+    if (pro == kProNone)
+        launch_layout<true, false, kProNone>(a, vec, pipe, cfg, st);
+    else
+        launch_nt_pro(a, vec, pipe, cfg, pro, st);
 }
 
 }  // namespace gemm

@@ -5,8 +5,11 @@
 namespace fg {
 namespace gemm {
 
-void launch_tn(const GemmArgs &a, bool vec, bool pipe, int cfg, hipStream_t st) {
-    launch_layout<false, true>(a, vec, pipe, cfg, st);
+void launch_tn(const GemmArgs &a, bool vec, bool pipe, int cfg, int pro, hipStream_t st) {
+    if (pro == kProNone)
+        launch_layout<false, true, kProNone>(a, vec, pipe, cfg, st);
+    else
+        launch_tn_pro(a, vec, pipe, cfg, pro, st);
 }
 
 }  // namespace gemm

@@ -26,7 +26,8 @@ Differences, all deliberate:
   * dims need not be multiples of 16 (the reference asserts they are,
     backend/mod.rs:617-619);
   * `bias_add` (and broadcast in add / sub) exist;
-  * `Optim.adam()` exists; `SimpleDType` is F32 only on this path;
+  * `Optim.adam()` exists; `SimpleDType` covers F32, F16 and BF16 (F64 and
+    the integer types have no op on this path);
   * after `dispatch_loss` with CROSS_ENTROPY on a final softmax the next
     `dispatch_backward` starts from dlogits = p - onehot (the reference
     pushes that gradient through the softmax Jacobian a second time);

@@ -139,6 +139,28 @@ int fg_gemm_bwd_f32(fg_ctx *ctx, int layout, int M, int N, int K,
                     int act, const float *d_Zs, int ldzs, float *d_C, int ldc,
                     int accumulate);
 
+/* Backward of a Linear layer through its activation, C = act(X.W + bias):
+ *   dZ = dC * act'(Zs)        never written to memory: each dC tile is
+ *                             multiplied by act'(Zs) as the GEMMs load it
+ *   dX (=|+=) dZ . W^T        [M][K], ld lddx   (NULL: skipped)
+ *   dW (=|+=) X^T . dZ        [K][N], ld lddw   (NULL: skipped)
+ *   dbias (=|+=) colsum(dZ)   [N]               (NULL: skipped; summed from
+ *                             the dW GEMM's dZ tiles, or by the column
+ *                             reduction when dW is skipped)
+ * X[M][K] ld ldx, W[K][N] ld ldw, Zs and dC [M][N] (ld ldzs, lddc).  act is
+ * FG_ACT_RELU, FG_ACT_GELU or FG_ACT_NONE (Zs unused).  For ReLU, Zs may be
+ * the forward output C itself: [C > 0] == [Z > 0].  `accumulate` applies to
+ * all three outputs.  Replaces the matmul backward (op/matmul/mod.rs:75-125
+ * driven by kernel/backward.rs:229-371), which evaluates dC inline on every
+ * tile load, with the activation's backward inlined there (relu
+ * unary.rs:456-469, with the mask corrected to [z > 0]; gelu
+ * unary.rs:588-714, corrected to the derivative in z). */
+int fg_linear_bwd_f32(fg_ctx *ctx, int act, int M, int N, int K,
+                      const float *d_X, int ldx, const float *d_W, int ldw,
+                      const float *d_Zs, int ldzs, const float *d_dC, int lddc,
+                      float *d_dX, int lddx, float *d_dW, int lddw, float *d_dbias,
+                      int accumulate);
+
 /* Element types of tensors: SimpleDType F32 / F16 / BF16
  * (crates/fused_gpu/src/dispatch/backend/mod.rs:335-427). 16-bit tensors are
  * stored as 16-bit words; kernels compute in fp32 and round to the storage

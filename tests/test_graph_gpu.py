@@ -437,67 +437,121 @@ def test_captured_step_replays_like_eager(ctx):
 
 
 def test_captured_step_survives_workspace_growth(ctx):
-    """A captured c1 step (its 64x256x784 forward GEMM splits K into the
-    plan's workspace) replays bit for bit like eager steps of an identical
-    plan after the context's workspace grows and a larger plan is created on
-    the same context: each plan's workspace is its own, and a context
-    workspace that grows is retired, not freed."""
+    """A captured c1 step (its two GEMMs split K into the plan's workspace)
+    replays bit for bit like eager steps of an identical plan after the
+    context's workspace grows and a larger plan is created on the same
+    context: each plan's workspace is its own, and a context workspace that
+    grows is retired, not freed."""
     import ferrograd_amd as fa
     from ferrograd_amd._lib import call
     G = api()
     # A context of its own on the same stream: growing its workspace must not
     # change what later tests' direct GEMM calls on the shared context do.
     own = fa.Context(0, ctx.ctx.stream)
-    ctx = G.GpuContext(own)
+    gctx = G.GpuContext(own)
     dims, B = [784, 256, 10], 64
-    runs = []
-    plans = []
-    for captured in (False, True):
-        graph, meta, mb, st = build_mlp(ctx, dims, B, "relu", G.Optim.sgd())
-        X = fa.rng_uniform(0, 0, (B, 784))
-        y = fa.rng_int(0, 1, (B,), 10)
-        ins = [ctx.init_tensor_f32(X.shape, X)]
-        for l in range(2):
-            W = fa.rng_uniform(0, 10 + l, (dims[l], dims[l + 1]), -math.sqrt(6 / dims[l]),
-                               math.sqrt(6 / dims[l]))
-            ins += [ctx.init_tensor_f32(W.shape, W),
-                    ctx.init_tensor_f32((dims[l + 1],), np.zeros(dims[l + 1]))]
-        tgt = ctx.new_onehot_init(y)
-        sch = ctx.schedule(graph.lower(meta), [G.f32_bits(0.01)] + mb[1:], ins, st)
-        plans.append((sch, st, ins, tgt))
-    desc = plans[1][1].plan.describe()
-    # The split forward GEMM adds its summing epilogue: 2 dispatches for one launch.
-    fwd_kernels = int(desc.split("(forward ")[1].split(",")[0])
-    assert fwd_kernels == 2, desc
-    sch, st, ins, tgt = plans[1]
-    call("fg_plan_bind_target", sch.plan.handle, tgt.data_ptr(), tgt.nbytes)
-    call("fg_plan_capture_step", sch.plan.handle)
-    # Grow the context's own workspace and create a larger plan on it.
-    ctx.ctx.reserve_workspace(64 << 20)
-    big, bmeta, bmb, bst = build_mlp(ctx, [512, 2048, 1000], 256, "gelu", G.Optim.adam())
-    for captured, (sch, st, ins, tgt) in zip((False, True), plans):
-        hist = []
-        for _ in range(3):
-            if captured:
-                call("fg_plan_launch_step", sch.plan.handle)
-                ctx.download(st.forward_out)  # eager work between replays
-            else:
-                ctx.dispatch_forward(sch)
-                ctx.dispatch_loss(sch, tgt)
-                ctx.dispatch_backward(sch)
-                ctx.dispatch_optim(sch)
-            ctx.sync()
-            hist.append([ctx.download(t).copy() for t in ins[1:]] +
-                        [ctx.download(st.mean_loss).copy()])
-        runs.append(hist)
-    for a, b in zip(*runs):
-        for x, y2 in zip(a, b):
-            assert np.array_equal(x, y2)
-    bst.plan.close()
-    for sch, st, _, _ in plans:
-        st.plan.close()
-    own.sync()
-    own.close()
+    runs, plans, extra = [], [], []
+    try:
+        for captured in (False, True):
+            graph, meta, mb, st = build_mlp(gctx, dims, B, "relu", G.Optim.sgd())
+            X = fa.rng_uniform(0, 0, (B, 784))
+            y = fa.rng_int(0, 1, (B,), 10)
+            ins = [gctx.init_tensor_f32(X.shape, X)]
+            for l in range(2):
+                W = fa.rng_uniform(0, 10 + l, (dims[l], dims[l + 1]), -math.sqrt(6 / dims[l]),
+                                   math.sqrt(6 / dims[l]))
+                ins += [gctx.init_tensor_f32(W.shape, W),
+                        gctx.init_tensor_f32((dims[l + 1],), np.zeros(dims[l + 1]))]
+            tgt = gctx.new_onehot_init(y)
+            sch = gctx.schedule(graph.lower(meta), [G.f32_bits(0.01)] + mb[1:], ins, st)
+            plans.append((sch, st, ins, tgt))
+        desc = plans[1][1].plan.describe()
+        # Forward: two GEMMs that split K (slices + summing epilogue each) and
+        # the softmax = 5 dispatches (3 unsplit).
+        fwd_kernels = int(desc.split("(forward ")[1].split(",")[0])
+        assert fwd_kernels == 5, desc
+        sch, st, ins, tgt = plans[1]
+        call("fg_plan_bind_target", sch.plan.handle, tgt.data_ptr(), tgt.nbytes)
+        call("fg_plan_capture_step", sch.plan.handle)
+        # Grow the context's own workspace and create a larger plan on it.
+        own.reserve_workspace(64 << 20)
+        extra.append(build_mlp(gctx, [512, 2048, 1000], 256, "gelu", G.Optim.adam())[3])
+        for captured, (sch, st, ins, tgt) in zip((False, True), plans):
+            hist = []
+            for _ in range(3):
+                if captured:
+                    call("fg_plan_launch_step", sch.plan.handle)
+                    gctx.download(st.forward_out)  # eager work between replays
+                else:
+                    gctx.dispatch_forward(sch)
+                    gctx.dispatch_loss(sch, tgt)
+                    gctx.dispatch_backward(sch)
+                    gctx.dispatch_optim(sch)
+                gctx.sync()
+                hist.append([gctx.download(t).copy() for t in ins[1:]] +
+                            [gctx.download(st.mean_loss).copy()])
+            runs.append(hist)
+        for a, b in zip(*runs):
+            for x, y2 in zip(a, b):
+                assert np.array_equal(x, y2)
+    finally:
+        own.sync()
+        for st in extra:
+            st.plan.close()
+        for _, st, _, _ in plans:
+            st.plan.close()
+        own.close()
+
+
+@pytest.mark.parametrize("act", ["relu", "gelu"])
+@pytest.mark.parametrize("seeded", [True, False], ids=["seed", "mse"])
+def test_linear_root_activation_backward(ctx, act, seeded):
+    """A graph that ends in act(bias_add(matmul(X, W), b)): the planner's
+    root-activation path (dZ = dH * act'(Z) as an elementwise program that
+    also fills the matmul's gradient tensor, then dW with the fused dbias and
+    dX).  dH is an uploaded seed, or the MSE loss's gradient written by
+    dispatch_loss (taken back from the seed buffer).  Forward output and
+    every gradient, the matmul node's included, against the oracle."""
+    import ferrograd_amd as fa
+    G = api()
+    M, K, N = 96, 200, 136
+    graph, meta = new_graph(G.MEAN_SQUARED_ERROR)
+    m, k, n = meta.new_field(), meta.new_field(), meta.new_field()
+    with graph.define_ops() as ops:
+        x = ops.input([m, k])
+        w = ops.input([k, n])
+        b = ops.input([n])
+        mm = ops.matmul(x, w)
+        getattr(ops, act)(ops.bias_add(mm, b))
+    mb = [G.f32_bits(1e-3), M, K, N]
+    st = ctx.alloc_tensors(graph, graph.compute_saved_nodes(), mb)
+    X = fa.rng_normal(9, 0, (M, K))
+    Wv = fa.rng_uniform(9, 1, (K, N), -math.sqrt(6 / K), math.sqrt(6 / K))
+    bv = fa.rng_normal(9, 2, (N,), 0.0, 0.1)
+    ins = [ctx.init_tensor_f32(X.shape, X), ctx.init_tensor_f32(Wv.shape, Wv),
+           ctx.init_tensor_f32(bv.shape, bv)]
+    sch = ctx.schedule(graph.lower(meta), mb, ins, st)
+    a = O.ACT_RELU if act == "relu" else O.ACT_GELU
+    Zr, Hr = O.bias_act(O.gemm(O.NN, X, Wv), bv, a)
+    ctx.dispatch_forward(sch)
+    if seeded:
+        dH = fa.rng_normal(9, 3, (M, N))
+        ctx.upload(st.seed, dH)
+    else:
+        tgt = ctx.init_tensor_f32((M, N), fa.rng_normal(9, 4, (M, N)))
+        ctx.dispatch_loss(sch, tgt)
+    ctx.dispatch_backward(sch)
+    ctx.sync()
+    assert normwise_rel(ctx.download(st.forward_out).reshape(M, N), Hr) < 1e-5 * math.sqrt(K)
+    if not seeded:
+        dH = ctx.download(st.seed).reshape(M, N)
+    dZ = O.act_bwd(a, dH, Zr)
+    grads = {t.node: ctx.download(t) for t in st.grad_tensors}
+    exp = {x: O.gemm(O.NT, dZ, Wv), w: O.gemm(O.TN, X, dZ), b: O.bias_grad(dZ), mm: dZ}
+    for node, ref in exp.items():
+        tol = 1e-5 * math.sqrt(max(N, M))
+        assert normwise_rel(grads[node].reshape(ref.shape), ref) < tol, node
+    st.plan.close()
 
 
 # --------------------------------------------------- losses and elementwise

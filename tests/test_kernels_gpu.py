@@ -146,34 +146,128 @@ def test_gemm_backward_epilogue_parity(gpu_ctx, layout, act):
 
 
 def test_gemm_c2_full_size_sampled(gpu_ctx):
-    """Config 2 at its real shape, 4096^3: forward NN + bias + ReLU, dA (NT
-    with the ReLU mask) and dB (TN), checked on 48 sampled rows against
-    float64 dot products."""
-    torch = _torch()
+    """Config 2 at its real shape, 4096^3, on the configuration's inputs
+    (library generator, seed 1: A, B ~ N(0,1), bias ~ N(0, 0.1^2), dC ~
+    N(0,1)): forward C = ReLU(A.B + bias) in one NN launch, then the
+    backward through the ReLU mask, dZ = dC * [Z > 0], dA = dZ.B^T,
+    dB = A^T.dZ, dbias = colsum(dZ), with the mask applied as the NT and TN
+    GEMMs load dC (fg_linear_bwd_f32; the forward output C stands in for Z,
+    [C > 0] == [Z > 0]).  Checked against float64 on 24 sampled rows
+    (forward, dA) and 24 sampled columns (dB, dbias); the mask of the
+    float64 reference is the GPU forward's own (a sign decided by fp32
+    rounding would otherwise flip single terms)."""
+    import ferrograd_amd as fa
     n = 4096
-    note("gemm c2 4096^3 sampled")
-    g = torch.Generator(device="cuda").manual_seed(1)
-    dA = torch.randn((n, n), device="cuda", generator=g)
-    dB = torch.randn((n, n), device="cuda", generator=g)
-    dbias = 0.1 * torch.randn((n,), device="cuda", generator=g)
-    dG = torch.randn((n, n), device="cuda", generator=g)
-    dC, dZ, dX, dW = (empty((n, n)) for _ in range(4))
-    gpu_ctx.gemm(O.NN, n, n, n, dA, n, dB, n, dC, n, bias=dbias, act=O.ACT_RELU, Z=dZ, ldz=n)
-    gpu_ctx.gemm_bwd(O.NT, n, n, n, dG, n, dB, n, dX, n, act=O.ACT_RELU, Zs=dZ, ldzs=n)
-    gpu_ctx.gemm_bwd(O.TN, n, n, n, dA, n, dG, n, dW, n)
-    rows = np.random.default_rng(5).choice(n, 48, replace=False)
-    A, B, bias, G = host(dA), host(dB), host(dbias), host(dG)
-    A64, B64, G64 = A.astype(np.float64), B.astype(np.float64), G.astype(np.float64)
+    note("gemm c2 4096^3 sampled: forward, masked dA / dB / dbias")
+    A, B, G = empty((n, n)), empty((n, n)), empty((n, n))
+    bias = empty((n,))
+    gpu_ctx.rng_normal(1, 0, 0.0, 1.0, A, n * n)
+    gpu_ctx.rng_normal(1, 1, 0.0, 1.0, B, n * n)
+    gpu_ctx.rng_normal(1, 2, 0.0, 0.1, bias, n)
+    gpu_ctx.rng_normal(1, 3, 0.0, 1.0, G, n * n)
+    C, dX, dW, db = empty((n, n)), empty((n, n)), empty((n, n)), empty((n,))
+    gpu_ctx.gemm(fa.NN, n, n, n, A, n, B, n, C, n, bias=bias, act=fa.ACT_RELU)
+    gpu_ctx.linear_bwd(fa.ACT_RELU, n, n, n, A, n, B, n, C, n, G, n, dX=dX, lddx=n, dW=dW,
+                       lddw=n, dbias=db)
+    sel = np.random.default_rng(5)
+    rows = np.sort(sel.choice(n, 24, replace=False))
+    cols = np.sort(sel.choice(n, 24, replace=False))
+    A64, B64, G64 = (host(t).astype(np.float64) for t in (A, B, G))
+    Ch, bh = host(C), host(bias).astype(np.float64)
     tol = 1e-5 * math.sqrt(n)
-    Zr = A64[rows] @ B64 + bias
-    Z = host(dZ)[rows]
-    assert normwise_rel(Z, Zr) < tol
-    assert normwise_rel(host(dC)[rows], np.maximum(Zr, 0)) < tol
-    mask = host(dZ)[rows] > 0
-    Xr = (G64[rows] @ B64.T) * mask
-    assert normwise_rel(host(dX)[rows], Xr) < tol
-    Wr = A64[:, rows].T @ G64      # rows of dW = A^T . G
-    assert normwise_rel(host(dW)[rows], Wr) < tol
+    Zr = A64[rows] @ B64 + bh
+    assert normwise_rel(Ch[rows], np.maximum(Zr, 0)) < tol
+    dZr = G64[rows] * (Ch[rows] > 0)
+    assert normwise_rel(host(dX)[rows], dZr @ B64.T) < tol
+    dZc = G64[:, cols] * (Ch[:, cols] > 0)
+    assert normwise_rel(host(dW)[:, cols], A64.T @ dZc) < tol
+    assert normwise_rel(host(db)[cols], dZc.sum(axis=0)) < tol
+    # The mask matters: without it dbias would be the plain column sums.
+    assert normwise_rel(host(db)[cols], G64[:, cols].sum(axis=0)) > 1e-2
+
+
+@pytest.mark.parametrize("case", [
+    # (M, N, K, act, outputs, accumulate, workspace): C = act(X.W + b) with
+    # X[M][K], W[K][N]; dX = dZ.W^T (NT, prologue on A), dW = X^T.dZ (TN,
+    # prologue on B, dbias from its tiles).
+    (17, 33, 29, O.ACT_RELU, "xwb", False, False),     # element loads, edge tiles
+    (17, 33, 29, O.ACT_GELU, "xwb", True, False),
+    (200, 136, 300, O.ACT_GELU, "xwb", False, False),  # any-shape kernel, K off tiles
+    (512, 512, 512, O.ACT_RELU, "xwb", False, False),  # pipelined 128x128 / 128x64
+    (256, 1000, 2048, O.ACT_GELU, "xwb", False, False),  # NT K = 1000: any-shape
+    (2048, 4096, 1024, O.ACT_RELU, "xwb", True, False),  # 256x128 8-wave pipe (NT)
+    (2048, 1024, 4096, O.ACT_GELU, "xwb", False, False),  # c5-like hidden shapes
+    (64, 4096, 256, O.ACT_RELU, "x", False, True),     # dX splits K (own workspace)
+    (300, 260, 100, O.ACT_RELU, "b", False, False),    # dbias alone: masked reduction
+    (300, 260, 100, O.ACT_GELU, "wb", True, False),
+    (128, 96, 64, O.ACT_NONE, "xwb", False, False),    # no activation: no prologue
+], ids=lambda c: f"{c[0]}x{c[1]}x{c[2]}-act{c[3]}-{c[4]}{'-acc' if c[5] else ''}"
+                 f"{'-ws' if c[6] else ''}")
+def test_linear_bwd_prologue_parity(gpu_ctx, case):
+    """fg_linear_bwd_f32 against the oracle: dZ = act_bwd(dC, Z) materialised
+    on the CPU, then the oracle's NT / TN GEMMs and column sums; the GPU
+    never materialises dZ (the GEMMs scale dC tiles by act'(Z) on load).
+    GEMM tolerance 1e-5*sqrt(reduction length)."""
+    torch = _torch()
+    import ferrograd_amd as fa
+    M, N, K, act, outs, acc, ws = case
+    note(f"linear_bwd M={M} N={N} K={K} act={act} outputs={outs} acc={acc} ws={ws}")
+    rng = np.random.default_rng(M + 7 * N + 3 * K + act)
+    X = rng.standard_normal((M, K)).astype(f32)
+    W = (rng.standard_normal((K, N)) / math.sqrt(K)).astype(f32)
+    Z = rng.standard_normal((M, N)).astype(f32)
+    dC = rng.standard_normal((M, N)).astype(f32)
+    dX0 = rng.standard_normal((M, K)).astype(f32)
+    dW0 = rng.standard_normal((K, N)).astype(f32)
+    db0 = rng.standard_normal(N).astype(f32)
+    dZ = O.act_bwd(act, dC, Z) if act != O.ACT_NONE else dC
+    ref_x = O.gemm(O.NT, dZ, W) + (dX0 if acc else 0)
+    ref_w = O.gemm(O.TN, X, dZ) + (dW0 if acc else 0)
+    ref_b = O.bias_grad(dZ) + (db0 if acc else 0)
+    ctx = gpu_ctx
+    own = None
+    if ws:
+        own = fa.Context(0, torch.cuda.current_stream().cuda_stream)
+        own.reserve_workspace(16 << 20)
+        ctx = own
+    try:
+        gx = dev(dX0) if "x" in outs else None
+        gw = dev(dW0) if "w" in outs else None
+        gb = dev(db0) if "b" in outs else None
+        ctx.linear_bwd(act, M, N, K, dev(X), K, dev(W), N, dev(Z), N, dev(dC), N, dX=gx,
+                       lddx=K, dW=gw, lddw=N, dbias=gb, accumulate=acc)
+        if "x" in outs:
+            assert normwise_rel(host(gx), ref_x) < 1e-5 * math.sqrt(N)
+        if "w" in outs:
+            assert normwise_rel(host(gw), ref_w) < 1e-5 * math.sqrt(M)
+        if "b" in outs:
+            assert normwise_rel(host(gb), ref_b) < 1e-5 * math.sqrt(M)
+    finally:
+        if own is not None:
+            own.sync()
+            own.close()
+
+
+def test_linear_bwd_relu_mask_from_output(gpu_ctx):
+    """For ReLU the forward output C = max(Z, 0) gives the same mask as Z,
+    including Z == 0 exactly (gradient 0, the [z > 0] convention): the
+    results with Zs = C and Zs = Z are identical bit for bit."""
+    M, N, K = 256, 512, 384
+    rng = np.random.default_rng(3)
+    X = rng.standard_normal((M, K)).astype(f32)
+    W = rng.standard_normal((K, N)).astype(f32)
+    Z = rng.standard_normal((M, N)).astype(f32)
+    Z[rng.random((M, N)) < 0.05] = 0.0
+    Cm = np.maximum(Z, 0)
+    dC = rng.standard_normal((M, N)).astype(f32)
+    res = []
+    for zs in (Z, Cm):
+        gx, gw, gb = empty((M, K)), empty((K, N)), empty((N,))
+        gpu_ctx.linear_bwd(O.ACT_RELU, M, N, K, dev(X), K, dev(W), N, dev(zs), N, dev(dC), N,
+                           dX=gx, lddx=K, dW=gw, lddw=N, dbias=gb)
+        res.append([host(gx), host(gw), host(gb)])
+    for a, b in zip(*res):
+        assert np.array_equal(a, b)
 
 
 @pytest.mark.parametrize("case", [
