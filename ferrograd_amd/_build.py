@@ -33,6 +33,7 @@ SOURCES = [
     "k_gemm16_bf16.hip",
     "k_gemm16_f16.hip",
     "k_eltwise_prog.hip",
+    "k_noalloc.hip",
     "fg_graph.cpp",
     "fg_bpat.cpp",
     "fg_telemetry.cpp",

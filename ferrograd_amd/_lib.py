@@ -52,6 +52,7 @@ SIGNATURES = {
                                 i32, vp, i32, vp, i32]),
     "fg_gemm_dw_x16": (i32, [vp, i32, i32, i32, i32, vp, i32, vp, i32, vp, i32, i32, vp, i32]),
     "fg_bias_grad": (i32, [vp, i32, i32, i32, vp, i32, vp, i32]),
+    "fg_bias_grad_noalloc": (i32, [vp, i32, i32, i32, vp, i32, vp, i32]),
     "fg_softmax_ce": (i32, [vp, i32, vp, i32, vp, i32, i32, f32, vp, vp, vp, i32, vp]),
     "fg_softmax": (i32, [vp, i32, vp, i32, i32, vp]),
     "fg_softmax_bwd": (i32, [vp, i32, vp, vp, i32, i32, vp, i32]),

@@ -53,6 +53,10 @@ namespace fg {
 // plan's) never grows: a request beyond it fails.
 void *workspace(fg_ctx *ctx, uint64_t bytes);
 
+// Looks up the device address of the fixed scratch array of
+// fg_bias_grad_noalloc on `device` (current), once per device (k_noalloc.hip).
+int noalloc_init(int device);
+
 // Bytes of workspace fg_bias_grad needs for an M x N reduction on a device
 // with `cus` compute units (the partial sums of its row splits).
 uint64_t bias_grad_ws_bytes(int cus, int M, int N);

@@ -93,6 +93,11 @@ FG_API int fg_ctx_create(int device, void *stream, fg_ctx **out) {
         delete ctx;
         return FG_ERR_UNSUPPORTED;
     }
+    // Device address of the fixed scratch of fg_bias_grad_noalloc.
+    if (int rc = fg::noalloc_init(device)) {
+        delete ctx;
+        return rc;
+    }
     if (stream) {
         ctx->stream = (hipStream_t)stream;
         ctx->own_stream = false;

@@ -215,6 +215,18 @@ int fg_bias_grad_f32(fg_ctx *ctx, int M, int N, const float *d_dZ, int ld,
 int fg_bias_grad(fg_ctx *ctx, int dtype, int M, int N, const void *d_dZ, int ld,
                  void *d_dbias, int accumulate);
 
+/* fg_bias_grad without any device allocation: no counterpart in the
+ * reference.  For callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The same
+ * launches and bits as fg_bias_grad; its partial sums go to a fixed 4 MiB
+ * device array of the library (one per GPU, held until the process ends)
+ * instead of the context workspace, so N is limited to 1,048,576 columns
+ * (FG_ERR_OUT_OF_BOUNDS beyond).  Calls on one GPU share that array: calls
+ * that overlap on one GPU (other streams or threads) race and must be
+ * ordered by the caller. */
+int fg_bias_grad_noalloc(fg_ctx *ctx, int dtype, int M, int N, const void *d_dZ, int ld,
+                         void *d_dbias, int accumulate);
+
 /* dZ[i] = dH[i] * act'(Z[i]) over n elements (unary backward, unary.rs). */
 int fg_act_bwd_f32(fg_ctx *ctx, int act, uint64_t n, const float *d_dH,
                    const float *d_Z, float *d_dZ);
