@@ -195,10 +195,12 @@ def c2_inputs(ctx, n: int = 4096):
 
 def gemm_components(ctx, reps: int, want_host: bool = False):
     """c2 (4096^3): forward C = ReLU(A.B + bias), then the backward through
-    the ReLU mask -- dA = (dC*[Z>0]).B^T and dB = A^T.(dC*[Z>0]) with dbias
-    = colsum(dC*[Z>0]) fused into dB -- where the mask is applied as the two
-    GEMMs load dC (fg_linear_bwd_f32; the forward output C gives the mask,
-    so the forward stores no Z).  Also the c5 hidden-layer forward GEMM.
+    the ReLU mask, dZ = dC*[Z>0], dA = dZ.B^T, dB = A^T.dZ, dbias =
+    colsum(dZ) (fg_linear_bwd_f32; the forward output C gives the mask, so
+    the forward stores no Z).  The backward is timed both ways: dZ
+    materialised by one pass that also sums its columns, then plain GEMMs
+    (the figure reported), and the mask applied as the GEMMs load dC (no dZ
+    buffer).  Also the c5 hidden-layer forward GEMM.
     Returns (timings, sample): with want_host the sample holds the inputs
     and outputs (the parity sample of the CPU leg), else it is None."""
     import torch
@@ -208,37 +210,45 @@ def gemm_components(ctx, reps: int, want_host: bool = False):
     out = {}
     n = 4096
     A, Bm, bias, dC = c2_inputs(ctx, n)
-    C, dA, dB = (torch.empty((n, n), device="cuda") for _ in range(3))
+    C, dA, dB, dZ = (torch.empty((n, n), device="cuda") for _ in range(4))
     db = torch.empty((n,), device="cuda")
     flops = 2.0 * n * n * n
 
     def fwd():
         ctx.gemm(fa.NN, n, n, n, A, n, Bm, n, C, n, bias=bias, act=fa.ACT_RELU)
 
-    def bwd(dX=None, dW=None, dbias=None):
+    def bwd(dX=None, dW=None, dbias=None, mat=True):
         ctx.linear_bwd(fa.ACT_RELU, n, n, n, A, n, Bm, n, C, n, dC, n, dX=dX, lddx=n, dW=dW,
-                       lddw=n, dbias=dbias)
+                       lddw=n, dbias=dbias, dZ=dZ if mat else None, lddz=n)
 
     t_f = event_time_ms(fwd, reps, warm_ms=200)
-    t_a = event_time_ms(lambda: bwd(dX=dA), reps, warm_ms=200)
-    t_b = event_time_ms(lambda: bwd(dW=dB, dbias=db), reps, warm_ms=200)
+    # The mask pass alone (dZ and dbias), then each GEMM on dZ, then all.
+    t_m = event_time_ms(lambda: bwd(dbias=db), reps, warm_ms=200)
+    t_a = event_time_ms(lambda: ctx.gemm_bwd(fa.NT, n, n, n, dZ, n, Bm, n, dA, n), reps,
+                        warm_ms=200)
+    t_b = event_time_ms(lambda: ctx.gemm(fa.TN, n, n, n, A, n, dZ, n, dB, n), reps, warm_ms=200)
     t_bwd = event_time_ms(lambda: bwd(dX=dA, dW=dB, dbias=db), reps, warm_ms=200)
+    t_pro = event_time_ms(lambda: bwd(dX=dA, dW=dB, dbias=db, mat=False), reps, warm_ms=200)
     out["c2_gemm_4096"] = {
-        "fwd_ms": t_f, "dA_ms": t_a, "dB_dbias_ms": t_b, "bwd_ms": t_bwd,
+        "fwd_ms": t_f, "mask_dbias_ms": t_m, "dA_ms": t_a, "dB_ms": t_b, "bwd_ms": t_bwd,
+        "bwd_prologue_ms": t_pro,
         "fwd_tflops": flops / t_f / 1e9, "dA_tflops": flops / t_a / 1e9,
         "dB_tflops": flops / t_b / 1e9,
+        "mask_pass_gbs": 12 * n * n / t_m / 1e6,
         "fwd_bwd_ms": t_f + t_bwd,
         "fwd_bwd_tflops": 3 * flops / (t_f + t_bwd) / 1e9,
-        "backward": "dZ = dC*[C>0] applied on load (never stored); dA = dZ.B^T; "
-                    "dB = A^T.dZ with dbias = colsum(dZ) fused",
+        "backward": "one pass dZ = dC*[C>0] with dbias = colsum(dZ), then dA = dZ.B^T (NT) "
+                    "and dB = A^T.dZ (TN); bwd_prologue_ms: the mask applied as the GEMMs "
+                    "load dC instead (no dZ buffer)",
     }
     sample = None
     if want_host:
+        bwd(dX=dA, dW=dB, dbias=db)  # the reported path's outputs for the parity sample
         torch.cuda.synchronize()
         sample = {k: v.cpu().numpy() for k, v in (("A", A), ("B", Bm), ("bias", bias),
                                                    ("dC", dC), ("C", C), ("dA", dA),
                                                    ("dB", dB), ("db", db))}
-    del A, Bm, bias, dC, C, dA, dB, db
+    del A, Bm, bias, dC, C, dA, dB, db, dZ
     g = torch.Generator(device="cuda").manual_seed(1)
     # c5 hidden layer forward: [2048,4096] x [4096,4096] + bias, GELU.
     M, N, K = 2048, 4096, 4096
@@ -570,12 +580,12 @@ def only_gemm_c2(ctx, reps):
 
     n = 4096
     A, Bm, bias, dC = c2_inputs(ctx, n)
-    C, dA, dB = (torch.empty((n, n), device="cuda") for _ in range(3))
+    C, dA, dB, dZ = (torch.empty((n, n), device="cuda") for _ in range(4))
     db = torch.empty((n,), device="cuda")
     for _ in range(reps):
         ctx.gemm(fa.NN, n, n, n, A, n, Bm, n, C, n, bias=bias, act=fa.ACT_RELU)
         ctx.linear_bwd(fa.ACT_RELU, n, n, n, A, n, Bm, n, C, n, dC, n, dX=dA, lddx=n, dW=dB,
-                       lddw=n, dbias=db)
+                       lddw=n, dbias=db, dZ=dZ, lddz=n)
 
 
 def only_c5_gemm(key):

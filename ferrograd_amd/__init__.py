@@ -110,12 +110,14 @@ class Context:
 
     def linear_bwd(self, act: int, M: int, N: int, K: int, X, ldx: int, W, ldw: int, Zs,
                    ldzs: int, dC, lddc: int, dX=None, lddx: int = 0, dW=None, lddw: int = 0,
-                   dbias=None, accumulate: bool = False) -> None:
-        """Backward of C = act(X.W + bias): dZ = dC * act'(Zs) applied on load,
-        dX = dZ.W^T, dW = X^T.dZ, dbias = colsum(dZ) (any may be None)."""
+                   dbias=None, accumulate: bool = False, dZ=None, lddz: int = 0) -> None:
+        """Backward of C = act(X.W + bias): dZ = dC * act'(Zs), dX = dZ.W^T,
+        dW = X^T.dZ, dbias = colsum(dZ) (any output may be None).  With a dZ
+        buffer, dZ is materialised by one pass; without, act' is applied to
+        the dC tiles as the GEMMs load them."""
         call("fg_linear_bwd_f32", self.handle, act, M, N, K, _ptr(X), ldx, _ptr(W), ldw,
              _ptr(Zs), ldzs, _ptr(dC), lddc, _ptr(dX), lddx or K, _ptr(dW), lddw or N,
-             _ptr(dbias), int(accumulate))
+             _ptr(dbias), int(accumulate), _ptr(dZ), lddz or N)
 
     def gemm_dw_x16(self, dtype: int, M: int, N: int, K: int, A, lda: int, B, ldb: int, C,
                     ldc: int, accumulate: bool = False, colsum=None,

@@ -50,14 +50,18 @@ inline Split split_of(int cus, int M, int N) {
 // elements (8 bytes) at a time when aligned.  PACT != kActNone (fp32 only):
 // the rows summed are dZ * act'(Pz) (Pz[M][N], row stride ldp, the same
 // alignment as dZ), i.e. the bias gradient below an activation whose
-// derivative was not applied yet.
+// derivative was not applied yet; with `out` (fp32, row stride ldo, the same
+// alignment) the scaled rows are also written there, so one pass
+// materialises dZ = dC * act'(Pz) and sums its columns.
 template <int DT, int PACT = kActNone>
 __global__ __launch_bounds__(kThreads) void bias_grad_partial(const void *__restrict__ dZ, int M,
                                                               int N, int ld, int rows_per_split,
                                                               float *__restrict__ partial,
                                                               int vec,
                                                               const float *__restrict__ Pz = nullptr,
-                                                              int ldp = 0) {
+                                                              int ldp = 0,
+                                                              float *__restrict__ out = nullptr,
+                                                              int ldo = 0) {
     static_assert(PACT == kActNone || DT == fg::kF32, "prologue on fp32 rows only");
     typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
     __shared__ f32x4 sh[kThreads];
@@ -80,6 +84,7 @@ __global__ __launch_bounds__(kThreads) void bias_grad_partial(const void *__rest
                             *reinterpret_cast<const f32x4 *>(Pz + (uint64_t)r * ldp + col);
 #pragma unroll
                         for (int e = 0; e < 4; ++e) v[e] *= act_grad(PACT, z[e]);
+                        if (out) *reinterpret_cast<f32x4 *>(out + (uint64_t)r * ldo + col) = v;
                     }
                     s += v;
                 } else {
@@ -94,8 +99,10 @@ __global__ __launch_bounds__(kThreads) void bias_grad_partial(const void *__rest
                 for (int e = 0; e < 4; ++e) {
                     if (col + e >= N) continue;
                     float v = fg::load_as_f(dZ, DT, row + col + e);
-                    if constexpr (PACT != kActNone)
+                    if constexpr (PACT != kActNone) {
                         v *= act_grad(PACT, Pz[(uint64_t)r * ldp + col + e]);
+                        if (out) out[(uint64_t)r * ldo + col + e] = v;
+                    }
                     s[e] += v;
                 }
             }
@@ -141,22 +148,25 @@ __global__ __launch_bounds__(kThreads) void bias_grad_final(const float *__restr
 // Enqueues both passes; `partial` holds at least sp.splits * N floats.
 // dtype is an FG_DTYPE_* code (the fg_half.h codes coincide).  pact / Pz /
 // ldp: the optional prologue of bias_grad_partial (fp32 dZ only; the caller
-// checks).
+// checks), and `out` / ldo its optional output of the scaled rows.  dbias
+// NULL: the first pass only (out written, no sums kept).
 inline hipError_t launch(hipStream_t st, const Split &sp, int dtype, int M, int N,
                          const void *dZ, int ld, void *dbias, int accumulate, float *partial,
-                         int pact = kActNone, const float *Pz = nullptr, int ldp = 0) {
+                         int pact = kActNone, const float *Pz = nullptr, int ldp = 0,
+                         float *out = nullptr, int ldo = 0) {
     const unsigned align = dtype == fg::kF32 ? 16u : 8u;
     int vec = ((((uintptr_t)dZ) & (align - 1)) == 0) && (ld % 4 == 0);
     if (pact != kActNone) vec = vec && (((uintptr_t)Pz) & 15u) == 0 && ldp % 4 == 0;
+    if (out) vec = vec && (((uintptr_t)out) & 15u) == 0 && ldo % 4 == 0;
     int splits = sp.splits;
     if (M > 0) {
         const dim3 grid(sp.strips, splits);
         if (pact == kActRelu)
             bias_grad_partial<fg::kF32, kActRelu><<<grid, kThreads, 0, st>>>(
-                dZ, M, N, ld, sp.rows_per_split, partial, vec, Pz, ldp);
+                dZ, M, N, ld, sp.rows_per_split, partial, vec, Pz, ldp, out, ldo);
         else if (pact == kActGelu)
             bias_grad_partial<fg::kF32, kActGelu><<<grid, kThreads, 0, st>>>(
-                dZ, M, N, ld, sp.rows_per_split, partial, vec, Pz, ldp);
+                dZ, M, N, ld, sp.rows_per_split, partial, vec, Pz, ldp, out, ldo);
         else if (dtype == fg::kF32)
             bias_grad_partial<fg::kF32>
                 <<<grid, kThreads, 0, st>>>(dZ, M, N, ld, sp.rows_per_split, partial, vec);
@@ -171,6 +181,7 @@ inline hipError_t launch(hipStream_t st, const Split &sp, int dtype, int M, int 
     } else {
         splits = 0;
     }
+    if (!dbias) return hipSuccess;
     bias_grad_final<><<<(N + kThreads - 1) / kThreads, kThreads, 0, st>>>(partial, splits, N,
                                                                          dbias, accumulate, dtype);
     return hipGetLastError();

@@ -298,7 +298,7 @@ FG_API int fg_gemm_dw_f32(fg_ctx *ctx, int M, int N, int K, const float *d_A, in
 FG_API int fg_linear_bwd_f32(fg_ctx *ctx, int act, int M, int N, int K, const float *d_X,
                              int ldx, const float *d_W, int ldw, const float *d_Zs, int ldzs,
                              const float *d_dC, int lddc, float *d_dX, int lddx, float *d_dW,
-                             int lddw, float *d_dbias, int accumulate) {
+                             int lddw, float *d_dbias, int accumulate, float *d_dZ, int lddz) {
     const char *who = "fg_linear_bwd_f32";
     FG_REQUIRE(ctx, FG_ERR_INVALID_ARGUMENT, "%s: ctx is NULL", who);
     FG_REQUIRE(act >= FG_ACT_NONE && act <= FG_ACT_GELU, FG_ERR_INVALID_ARGUMENT,
@@ -308,16 +308,44 @@ FG_API int fg_linear_bwd_f32(fg_ctx *ctx, int act, int M, int N, int K, const fl
     FG_REQUIRE(d_dC && lddc >= N, FG_ERR_INVALID_ARGUMENT, "%s: dC NULL or lddc < N", who);
     FG_REQUIRE(act == FG_ACT_NONE || (d_Zs && ldzs >= N), FG_ERR_INVALID_ARGUMENT,
                "%s: act %d needs Zs with ldzs >= N", who, act);
-    using namespace fg::gemm;
-    const int pro_tn = act == FG_ACT_RELU ? kProBReLU : act == FG_ACT_GELU ? kProBGelu : kProNone;
-    const int pro_nt = act == FG_ACT_RELU ? kProAReLU : act == FG_ACT_GELU ? kProAGelu : kProNone;
-    if (d_dW && K > 0) {  // dW = X^T.dZ (TN, dZ the B operand) with dbias from its tiles
-        FG_REQUIRE(d_X && ldx >= std::max(K, 1) && lddw >= N, FG_ERR_INVALID_ARGUMENT,
+    FG_REQUIRE(!d_dZ || lddz >= N, FG_ERR_INVALID_ARGUMENT, "%s: lddz < N", who);
+    const bool want_w = d_dW && K > 0;
+    if (want_w)
+        FG_REQUIRE(d_X && ldx >= K && lddw >= N, FG_ERR_INVALID_ARGUMENT,
                    "%s: X NULL or ldx < K or lddw < N", who);
-        const int rc = gemm_dw(ctx, K, N, M, d_X, ldx, d_dC, lddc, d_dW, lddw, accumulate,
-                               d_dbias, accumulate, d_Zs, ldzs, pro_tn, who);
+    const bool want_x = d_dX && K > 0;
+    if (want_x)
+        FG_REQUIRE(d_W && ldw >= N && lddx >= K, FG_ERR_INVALID_ARGUMENT,
+                   "%s: W NULL or ldw < N or lddx < K", who);
+    using namespace fg::gemm;
+    // The GEMMs' dC operand: dC itself with the prologue, or the materialised
+    // dZ (act NONE: dC is dZ).
+    const float *g = d_dC;
+    int ldg = lddc, pro_tn = kProNone, pro_nt = kProNone;
+    bool dbias_done = false;
+    if (act != FG_ACT_NONE && d_dZ) {
+        // One pass over dC and Zs writes dZ and, when asked, sums its columns.
+        FG_HIP(hipSetDevice(ctx->device));
+        const fg::colsum::Split sp =
+            fg::colsum::split_of(ctx->cu_count > 0 ? ctx->cu_count : 256, M, N);
+        float *partial = (float *)fg::workspace(
+            ctx, std::max<uint64_t>(sp.partial_floats(N), 1) * sizeof(float));
+        if (!partial) return FG_ERR_OUT_OF_MEMORY;
+        FG_HIP(fg::colsum::launch(ctx->stream, sp, FG_DTYPE_F32, M, N, d_dC, lddc, d_dbias,
+                                  accumulate, partial, act, d_Zs, ldzs, d_dZ, lddz));
+        dbias_done = true;
+        g = d_dZ;
+        ldg = lddz;
+    } else if (act != FG_ACT_NONE) {
+        pro_tn = act == FG_ACT_RELU ? kProBReLU : kProBGelu;
+        pro_nt = act == FG_ACT_RELU ? kProAReLU : kProAGelu;
+    }
+    if (want_w) {  // dW = X^T.dZ (TN, dZ the B operand), dbias from its tiles if still due
+        const int rc = gemm_dw(ctx, K, N, M, d_X, ldx, g, ldg, d_dW, lddw, accumulate,
+                               dbias_done ? nullptr : d_dbias, accumulate, d_Zs, ldzs, pro_tn,
+                               who);
         if (rc) return rc;
-    } else if (d_dbias) {  // dbias alone: the column reduction with the prologue
+    } else if (d_dbias && !dbias_done) {  // dbias alone: the column reduction (+ prologue)
         FG_HIP(hipSetDevice(ctx->device));
         const fg::colsum::Split sp =
             fg::colsum::split_of(ctx->cu_count > 0 ? ctx->cu_count : 256, M, N);
@@ -327,12 +355,10 @@ FG_API int fg_linear_bwd_f32(fg_ctx *ctx, int act, int M, int N, int K, const fl
         FG_HIP(fg::colsum::launch(ctx->stream, sp, FG_DTYPE_F32, M, N, d_dC, lddc, d_dbias,
                                   accumulate, partial, act, d_Zs, ldzs));
     }
-    if (d_dX && K > 0) {  // dX = dZ.W^T (NT, dZ the A operand)
-        FG_REQUIRE(d_W && ldw >= N && lddx >= K, FG_ERR_INVALID_ARGUMENT,
-                   "%s: W NULL or ldw < N or lddx < K", who);
+    if (want_x) {  // dX = dZ.W^T (NT, dZ the A operand)
         GemmArgs a{};
-        a.A = d_dC;
-        a.lda = lddc;
+        a.A = g;
+        a.lda = ldg;
         a.B = d_W;
         a.ldb = ldw;
         a.C = d_dX;

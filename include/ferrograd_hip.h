@@ -140,26 +140,30 @@ int fg_gemm_bwd_f32(fg_ctx *ctx, int layout, int M, int N, int K,
                     int accumulate);
 
 /* Backward of a Linear layer through its activation, C = act(X.W + bias):
- *   dZ = dC * act'(Zs)        never written to memory: each dC tile is
- *                             multiplied by act'(Zs) as the GEMMs load it
+ *   dZ = dC * act'(Zs)
  *   dX (=|+=) dZ . W^T        [M][K], ld lddx   (NULL: skipped)
  *   dW (=|+=) X^T . dZ        [K][N], ld lddw   (NULL: skipped)
- *   dbias (=|+=) colsum(dZ)   [N]               (NULL: skipped; summed from
- *                             the dW GEMM's dZ tiles, or by the column
- *                             reduction when dW is skipped)
+ *   dbias (=|+=) colsum(dZ)   [N]               (NULL: skipped)
  * X[M][K] ld ldx, W[K][N] ld ldw, Zs and dC [M][N] (ld ldzs, lddc).  act is
- * FG_ACT_RELU, FG_ACT_GELU or FG_ACT_NONE (Zs unused).  For ReLU, Zs may be
- * the forward output C itself: [C > 0] == [Z > 0].  `accumulate` applies to
- * all three outputs.  Replaces the matmul backward (op/matmul/mod.rs:75-125
- * driven by kernel/backward.rs:229-371), which evaluates dC inline on every
- * tile load, with the activation's backward inlined there (relu
- * unary.rs:456-469, with the mask corrected to [z > 0]; gelu
- * unary.rs:588-714, corrected to the derivative in z). */
+ * FG_ACT_RELU, FG_ACT_GELU or FG_ACT_NONE (Zs unused, dZ = dC).  For ReLU, Zs
+ * may be the forward output C itself: [C > 0] == [Z > 0].  `accumulate`
+ * applies to dX, dW and dbias.  Two ways to apply act':
+ *   d_dZ given ([M][N], ld lddz): one HBM pass writes dZ there and sums its
+ *     columns into dbias, then plain GEMMs read dZ (the faster way for large
+ *     layers: one extra pass of 12 bytes per element);
+ *   d_dZ NULL: dZ is never stored -- each dC tile is multiplied by act'(Zs)
+ *     as the two GEMMs load it, and dbias is summed from the dW GEMM's
+ *     scaled tiles (no extra memory; the GEMMs run some per cent slower).
+ * Replaces the matmul backward (op/matmul/mod.rs:75-125 driven by
+ * kernel/backward.rs:229-371), which evaluates dC inline on every tile load,
+ * with the activation's backward inlined there (relu unary.rs:456-469, with
+ * the mask corrected to [z > 0]; gelu unary.rs:588-714, corrected to the
+ * derivative in z). */
 int fg_linear_bwd_f32(fg_ctx *ctx, int act, int M, int N, int K,
                       const float *d_X, int ldx, const float *d_W, int ldw,
                       const float *d_Zs, int ldzs, const float *d_dC, int lddc,
                       float *d_dX, int lddx, float *d_dW, int lddw, float *d_dbias,
-                      int accumulate);
+                      int accumulate, float *d_dZ, int lddz);
 
 /* Element types of tensors: SimpleDType F32 / F16 / BF16
  * (crates/fused_gpu/src/dispatch/backend/mod.rs:335-427). 16-bit tensors are

@@ -167,8 +167,14 @@ def test_gemm_c2_full_size_sampled(gpu_ctx):
     gpu_ctx.rng_normal(1, 3, 0.0, 1.0, G, n * n)
     C, dX, dW, db = empty((n, n)), empty((n, n)), empty((n, n)), empty((n,))
     gpu_ctx.gemm(fa.NN, n, n, n, A, n, B, n, C, n, bias=bias, act=fa.ACT_RELU)
+    # Both ways of applying the mask: dZ materialised by one pass, and the
+    # prologue on the GEMMs' dC tiles (dZ never stored).
+    dZ = empty((n, n))
     gpu_ctx.linear_bwd(fa.ACT_RELU, n, n, n, A, n, B, n, C, n, G, n, dX=dX, lddx=n, dW=dW,
-                       lddw=n, dbias=db)
+                       lddw=n, dbias=db, dZ=dZ, lddz=n)
+    pX, pW, pb = empty((n, n)), empty((n, n)), empty((n,))
+    gpu_ctx.linear_bwd(fa.ACT_RELU, n, n, n, A, n, B, n, C, n, G, n, dX=pX, lddx=n, dW=pW,
+                       lddw=n, dbias=pb)
     sel = np.random.default_rng(5)
     rows = np.sort(sel.choice(n, 24, replace=False))
     cols = np.sort(sel.choice(n, 24, replace=False))
@@ -184,6 +190,12 @@ def test_gemm_c2_full_size_sampled(gpu_ctx):
     assert normwise_rel(host(db)[cols], dZc.sum(axis=0)) < tol
     # The mask matters: without it dbias would be the plain column sums.
     assert normwise_rel(host(db)[cols], G64[:, cols].sum(axis=0)) > 1e-2
+    # The materialised dZ is exactly dC or 0; the prologue path agrees.
+    dZh = host(dZ)
+    assert np.array_equal(dZh[rows], host(G)[rows] * (Ch[rows] > 0))
+    assert normwise_rel(host(pX)[rows], host(dX)[rows]) < tol
+    assert normwise_rel(host(pW)[:, cols], host(dW)[:, cols]) < tol
+    assert normwise_rel(host(pb), host(db)) < tol
 
 
 @pytest.mark.parametrize("case", [
@@ -203,15 +215,18 @@ def test_gemm_c2_full_size_sampled(gpu_ctx):
     (128, 96, 64, O.ACT_NONE, "xwb", False, False),    # no activation: no prologue
 ], ids=lambda c: f"{c[0]}x{c[1]}x{c[2]}-act{c[3]}-{c[4]}{'-acc' if c[5] else ''}"
                  f"{'-ws' if c[6] else ''}")
-def test_linear_bwd_prologue_parity(gpu_ctx, case):
-    """fg_linear_bwd_f32 against the oracle: dZ = act_bwd(dC, Z) materialised
-    on the CPU, then the oracle's NT / TN GEMMs and column sums; the GPU
-    never materialises dZ (the GEMMs scale dC tiles by act'(Z) on load).
-    GEMM tolerance 1e-5*sqrt(reduction length)."""
+@pytest.mark.parametrize("mat", [False, True], ids=["prologue", "dZ"])
+def test_linear_bwd_parity(gpu_ctx, case, mat):
+    """fg_linear_bwd_f32 against the oracle: dZ = act_bwd(dC, Z) on the CPU,
+    then the oracle's NT / TN GEMMs and column sums.  The GPU either scales
+    the dC tiles by act'(Z) as the GEMMs load them (prologue; dZ never
+    stored) or materialises dZ in one pass that also sums its columns (dZ
+    checked too: bit-exact for ReLU, 1e-5 for GELU).  GEMM tolerance
+    1e-5*sqrt(reduction length)."""
     torch = _torch()
     import ferrograd_amd as fa
     M, N, K, act, outs, acc, ws = case
-    note(f"linear_bwd M={M} N={N} K={K} act={act} outputs={outs} acc={acc} ws={ws}")
+    note(f"linear_bwd M={M} N={N} K={K} act={act} outputs={outs} acc={acc} ws={ws} mat={mat}")
     rng = np.random.default_rng(M + 7 * N + 3 * K + act)
     X = rng.standard_normal((M, K)).astype(f32)
     W = (rng.standard_normal((K, N)) / math.sqrt(K)).astype(f32)
@@ -234,8 +249,14 @@ def test_linear_bwd_prologue_parity(gpu_ctx, case):
         gx = dev(dX0) if "x" in outs else None
         gw = dev(dW0) if "w" in outs else None
         gb = dev(db0) if "b" in outs else None
+        gz = empty((M, N)) if mat else None
         ctx.linear_bwd(act, M, N, K, dev(X), K, dev(W), N, dev(Z), N, dev(dC), N, dX=gx,
-                       lddx=K, dW=gw, lddw=N, dbias=gb, accumulate=acc)
+                       lddx=K, dW=gw, lddw=N, dbias=gb, accumulate=acc, dZ=gz, lddz=N)
+        if mat and act != O.ACT_NONE:
+            if act == O.ACT_RELU:
+                assert np.array_equal(host(gz), dZ)
+            else:
+                assert normwise_rel(host(gz), dZ) < 1e-5
         if "x" in outs:
             assert normwise_rel(host(gx), ref_x) < 1e-5 * math.sqrt(N)
         if "w" in outs:
@@ -248,7 +269,8 @@ def test_linear_bwd_prologue_parity(gpu_ctx, case):
             own.close()
 
 
-def test_linear_bwd_relu_mask_from_output(gpu_ctx):
+@pytest.mark.parametrize("mat", [False, True], ids=["prologue", "dZ"])
+def test_linear_bwd_relu_mask_from_output(gpu_ctx, mat):
     """For ReLU the forward output C = max(Z, 0) gives the same mask as Z,
     including Z == 0 exactly (gradient 0, the [z > 0] convention): the
     results with Zs = C and Zs = Z are identical bit for bit."""
@@ -263,8 +285,9 @@ def test_linear_bwd_relu_mask_from_output(gpu_ctx):
     res = []
     for zs in (Z, Cm):
         gx, gw, gb = empty((M, K)), empty((K, N)), empty((N,))
+        gz = empty((M, N)) if mat else None
         gpu_ctx.linear_bwd(O.ACT_RELU, M, N, K, dev(X), K, dev(W), N, dev(zs), N, dev(dC), N,
-                           dX=gx, lddx=K, dW=gw, lddw=N, dbias=gb)
+                           dX=gx, lddx=K, dW=gw, lddw=N, dbias=gb, dZ=gz, lddz=N)
         res.append([host(gx), host(gw), host(gb)])
     for a, b in zip(*res):
         assert np.array_equal(a, b)
