@@ -7,6 +7,7 @@
 // rocm/generate.rs:17-70).
 #pragma once
 
+#include <cstddef>
 #include <cstdint>
 
 namespace fg {
@@ -75,5 +76,16 @@ struct EltProgram {
     int32_t n_instr;
     EltInstr ins[kEltMaxInstr];
 };
+
+// The rule above, checked: every array the kernel indexes with a run-time
+// value has elements of a whole number of 4-byte words, at a 4-byte aligned
+// offset, so no scalar load of one can start at a byte address.
+static_assert(sizeof(EltProgram::src[0]) % 4 == 0 && offsetof(EltProgram, src) % 4 == 0,
+              "src[] elements must be whole 4-byte words");
+static_assert(sizeof(EltProgram::dst[0]) % 4 == 0 && offsetof(EltProgram, dst) % 4 == 0,
+              "dst[] elements must be whole 4-byte words");
+static_assert(sizeof(EltInstr) % 4 == 0 && alignof(EltInstr) >= 4 &&
+                  offsetof(EltProgram, ins) % 4 == 0,
+              "ins[] elements must be whole 4-byte words");
 
 }  // namespace fg

@@ -67,6 +67,14 @@ constexpr int kBK = FG_GEMM_BK;
 #endif
 constexpr bool kPipe = FG_GEMM_PIPE != 0;
 
+// Interleaved MFMA blocks for row-contiguous operands in the pipelined
+// kernel (gemm_f32_pipe); 0 keeps one block per 32 consecutive rows.  A
+// compile-time knob for measurement builds.
+#ifndef FG_GEMM_INTERLEAVE
+#define FG_GEMM_INTERLEAVE 1
+#endif
+constexpr bool kInterleave = FG_GEMM_INTERLEAVE != 0;
+
 
 struct GemmArgs {
     const float *A;
@@ -326,7 +334,9 @@ __device__ __forceinline__ void epi_x4(const GemmArgs &p, f32x4 v, f32x4 bv, int
 
 // Epilogue shared by the GEMM kernels.  Accumulator register r of lane
 // (h, l32) in block (i, j) holds C[r0 + 32i + 8(r/4) + 4h + r%4][c0 + 32j + l32]
-// (r0, c0: the wave's first row and column).  Each wave writes one
+// (r0, c0: the wave's first row and column); with interleaved blocks (IA =
+// TM > 1, IB = TN > 1) row 32i + x becomes TM x + i and column 32j + l32
+// becomes TN l32 + j.  Each wave writes one
 // 32 x WTN slice to its LDS stage (stride WTN+4 floats), then reads it back
 // as float4 rows and applies bias / activation / activation-derivative with
 // 16-byte global accesses.  A lane keeps the same four columns through the
@@ -336,9 +346,10 @@ __device__ __forceinline__ void epi_x4(const GemmArgs &p, f32x4 v, f32x4 bv, int
 // per-element arithmetic and the row loop stays rolled.  lds must hold
 // NW * 32 * (WTN + 4) floats and be free (every wave past its last read of
 // the operand tiles).
-template <int TM, int TN, int WTN, int NW>
+template <int TM, int TN, int WTN, int NW, int IA = 1, int IB = 1>
 __device__ __forceinline__ void store_tile(const GemmArgs &p, const f32x16 (&acc)[TM][TN],
                                            float *lds, int r0, int c0, int wave, int lane) {
+    static_assert((IA == 1 || IA == TM) && (IB == 1 || IB == TN), "interleave factors");
     constexpr int kStageLd = WTN + 4;
     const int l32 = lane & 31, h = lane >> 5;
     float *stage = lds + wave * (32 * kStageLd);
@@ -357,7 +368,8 @@ __device__ __forceinline__ void store_tile(const GemmArgs &p, const f32x16 (&acc
         for (int j = 0; j < TN; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r)
-                stage[((r >> 2) * 8 + h * 4 + (r & 3)) * kStageLd + j * 32 + l32] = acc[i][j][r];
+                stage[((r >> 2) * 8 + h * 4 + (r & 3)) * kStageLd +
+                      (IB > 1 ? TN * l32 + j : j * 32 + l32)] = acc[i][j][r];
         __syncthreads();
         f32x4 nxt = *reinterpret_cast<const f32x4 *>(stage + rr0 * kStageLd + c4);
 #pragma unroll 1
@@ -365,7 +377,7 @@ __device__ __forceinline__ void store_tile(const GemmArgs &p, const f32x16 (&acc
             const f32x4 v = nxt;
             if (q + 1 < NP)
                 nxt = *reinterpret_cast<const f32x4 *>(stage + (rr0 + (q + 1) * RPP) * kStageLd + c4);
-            const int row = r0 + i * 32 + rr0 + q * RPP;
+            const int row = IA > 1 ? r0 + TM * (rr0 + q * RPP) + i : r0 + i * 32 + rr0 + q * RPP;
             if (row >= p.M || col >= p.N) continue;
             if (vec) {
                 epi_x4(p, v, bv, row, col);
@@ -532,7 +544,10 @@ __device__ __forceinline__ int swz_k(int row) {
 }
 __device__ __forceinline__ int swz_r(int k) { return ((k >> 3) & 1) * 8; }
 
-template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC, int PRO>
+// KT: K need not be a multiple of BK (staged tiles, no prologue): the last
+// tile's chunks past K are loaded from a clamped address and zeroed before
+// their LDS write, so they add nothing to any output.
+template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC, int PRO, bool KT>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_pipe(GemmArgs p) {
     split_k_view<AK, BNC, PRO>(p);
     constexpr int NW = WGM * WGN;
@@ -548,6 +563,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_pipe(GemmArgs p) {
     // The prologue scales a tile in registers, between its load and its LDS
     // write: staged tiles only.
     static_assert(PRO == kProNone || kStaged, "prologue needs the staged path");
+    static_assert(!KT || (kStaged && PRO == kProNone), "K tail: staged tiles, no prologue");
     // Staged: two stages.  Direct: three (two tiles in flight) when they fit
     // in the 160 KiB of LDS, else two.
     constexpr int kStages = kStaged ? 2 : 3 * kStageSz * 4 <= 160 * 1024 ? 3 : 2;
@@ -575,15 +591,32 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_pipe(GemmArgs p) {
     // Source address of this lane's chunk for wave load `li` of an operand:
     // the chunk's position in the stage fixes (row, physical chunk); the
     // swizzle gives the logical chunk to fetch.
+    // (KT: a chunk past K is fetched from the last valid k; staged_value
+    // zeroes it.)
     auto src_kc = [&](const float *base, int ld, int r0, int rmax, int k0, int pos) {
         const int row = pos / (BK / 4), pc = pos % (BK / 4);
         const int c = pc ^ swz_k<BK>(row);
-        return base + (size_t)min(r0 + row, rmax - 1) * ld + k0 + 4 * c;
+        int k = k0 + 4 * c;
+        if constexpr (KT) k = min(k, p.K - 4);
+        return base + (size_t)min(r0 + row, rmax - 1) * ld + k;
     };
     auto src_rc = [&](const float *base, int ld, int r0, int rmax, int k0, int pos, int R) {
         const int k = pos / (R / 4), pc = pos % (R / 4);
         const int c = pc ^ swz_r(k);
-        return base + (size_t)(k0 + k) * ld + min(r0 + 4 * c, rmax - 4);
+        int kk = k0 + k;
+        if constexpr (KT) kk = min(kk, p.K - 1);
+        return base + (size_t)kk * ld + min(r0 + 4 * c, rmax - 4);
+    };
+    // The tile-local k of this lane's chunk of wave load q.
+    auto koff_of = [&](int q) -> int {
+        if (q < kPerA) {
+            const int pos = (wave * kPerA + q) * 64 + lane;
+            if constexpr (AK) return 4 * ((pos % (BK / 4)) ^ swz_k<BK>(pos / (BK / 4)));
+            return pos / (BM / 4);
+        }
+        const int pos = (wave * kPerB + (q - kPerA)) * 64 + lane;
+        if constexpr (BNC) return pos / (BN / 4);
+        return 4 * ((pos % (BK / 4)) ^ swz_k<BK>(pos / (BK / 4)));
     };
     // Wave load q (0 .. kLoads-1) of a tile: this wave's share of A first,
     // then of B.  Source of this lane's chunk, and its place in a stage.
@@ -645,14 +678,16 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_pipe(GemmArgs p) {
         }
         return *reinterpret_cast<const f32x4 *>(src);
     };
-    // Chunk q of register set (R, Z) as it goes to LDS.
-    auto staged_value = [&](const f32x4 *R, const f32x4 *Zr, int q) -> f32x4 {
+    // Chunk q of register set (R, Z), holding tile kst, as it goes to LDS.
+    auto staged_value = [&](const f32x4 *R, const f32x4 *Zr, int q, int kst) -> f32x4 {
         if constexpr (PRO != kProNone)
             if (is_pro(q)) return pro_scale<pro_act(PRO)>(R[q], Zr[q - kProFirst]);
+        if constexpr (KT)
+            if (kst * BK + koff_of(q) >= p.K) return f32x4{0.f, 0.f, 0.f, 0.f};
         return R[q];
     };
 
-    const int nk = p.K / BK;
+    const int nk = KT ? (p.K + BK - 1) / BK : p.K / BK;
     constexpr bool kTN = !AK && BNC;
     ColSum<BN, BK, 64 * NW> cs;
     const bool do_cs = kTN && p.colsum && tile_m == 0;
@@ -691,19 +726,69 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_pipe(GemmArgs p) {
         }
         return b;
     };
+    // Row-contiguous operands with more than one MFMA block per wave are
+    // interleaved: block i of A covers wave rows TM r + i (r = 0..31) and
+    // block j of B wave columns TN c + j, so a lane's operands for all its
+    // blocks at one k are TM (TN) consecutive floats -- one ds_read_b64 /
+    // b128 per k step instead of TM (TN) scalar reads.  The fragment
+    // registers then hold, at flat position s T + block, the value of k step
+    // s; store_tile maps the blocks back.
+    // Used in the TN layout (both operands row-contiguous: +1.7 % on the
+    // 256-row tiles); for NN's B operand the four extra read units crowd
+    // the MFMA slots that also carry the staged tile loads (-6 % on the
+    // 256x128 8-wave tile), so NN keeps one block per 32 columns.
+    constexpr bool kIl = kInterleave && !AK && BNC;
+    constexpr int IA = (kIl && TM > 1) ? TM : 1;
+    constexpr int IB = (kIl && TN > 1) ? TN : 1;
+    static_assert(IA == 1 || IA == 2 || IA == 4, "A interleave of 2 or 4 blocks");
+    static_assert(IB == 1 || IB == 2 || IB == 4, "B interleave of 2 or 4 blocks");
+    constexpr int NRA = IA > 1 ? 4 : TM;  // LDS read units of A per group
+    constexpr int NRB = IB > 1 ? 4 : TN;
+    static_assert(NRA + NRB <= 4 * TM * TN, "one read unit per MFMA slot");
+    // T consecutive floats at `src` into flat positions s T .. s T + T - 1.
+    auto read_run = [&](const float *src, int s, auto &f) {
+        constexpr int T = sizeof(f) / sizeof(f32x4);
+        if constexpr (T == 4) {
+            f[s] = *reinterpret_cast<const f32x4 *>(src);
+        } else {
+            typedef float f32x2 __attribute__((ext_vector_type(2)));
+            const f32x2 v = *reinterpret_cast<const f32x2 *>(src);
+            f[s >> 1][2 * (s & 1)] = v[0];
+            f[s >> 1][2 * (s & 1) + 1] = v[1];
+        }
+    };
+    // Read unit u of group g: block u (k-contiguous, or one block per wave),
+    // or k step u of every block (interleaved).
+    auto read_a = [&](const float *As, int g, int u, f32x4 (&a)[TM]) {
+        if constexpr (IA > 1) {
+            const int k = k_of(g) + u, row = wm0 + TM * l32;
+            read_run(As + k * BM + ((((row >> 2) ^ swz_r(k)) << 2) | (row & 3)), u, a);
+        } else {
+            a[u] = frag_a(As, g, u);
+        }
+    };
+    auto read_b = [&](const float *Bs, int g, int u, f32x4 (&b)[TN]) {
+        if constexpr (IB > 1) {
+            const int k = k_of(g) + u, col = wn0 + TN * l32;
+            read_run(Bs + k * BN + ((((col >> 2) ^ swz_r(k)) << 2) | (col & 3)), u, b);
+        } else {
+            b[u] = frag_b(Bs, g, u);
+        }
+    };
     auto frag = [&](const float *As, const float *Bs, int g, f32x4 (&a)[TM], f32x4 (&b)[TN]) {
 #pragma unroll
-        for (int i = 0; i < TM; ++i) a[i] = frag_a(As, g, i);
+        for (int u = 0; u < NRA; ++u) read_a(As, g, u, a);
 #pragma unroll
-        for (int j = 0; j < TN; ++j) b[j] = frag_b(Bs, g, j);
+        for (int u = 0; u < NRB; ++u) read_b(Bs, g, u, b);
     };
     // MFMA m (of 4 TM TN) of a group: k step m / (TM TN), then i, then j,
     // so consecutive MFMAs update different accumulators.
     auto mfma_one = [&](const f32x4 (&a)[TM], const f32x4 (&b)[TN], int m) {
         const int s = m / (TM * TN), i = (m / TN) % TM, j = m % TN;
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s], b[j][s], acc[i][j], 0, 0, 0);
-    };
-    auto colsum_add = [&](const float *Bs) {
+        const int fa = IA > 1 ? s * TM + i : i * 4 + s, fb = IB > 1 ? s * TN + j : j * 4 + s;
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[fa >> 2][fa & 3], b[fb >> 2][fb & 3],
+                                                         acc[i][j], 0, 0, 0);
+    };    auto colsum_add = [&](const float *Bs) {
         if constexpr (kTN)
             if (do_cs)
                 cs.add([&](int k, int c) {
@@ -724,7 +809,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_pipe(GemmArgs p) {
     // among the MFMAs of its first group, and every iteration leaves the
     // same kAhead tiles in flight.
     // Each group runs its MFMAs in a fixed order: after MFMA m, the reads of
-    // fragment m of the next group (A fragments, then B) and, in the first
+    // read unit m of the next group (A units, then B) and, in the first
     // group of a tile, the tile's memory operations (`mem(m)`).  Reads or
     // loads issued in a burst fill the wave's memory queues and hold up the
     // MFMAs behind them, which no other wave hides when a SIMD runs one
@@ -742,19 +827,19 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_pipe(GemmArgs p) {
     auto run_group = [&](const f32x4 (&ca)[TM], const f32x4 (&cb)[TN], const float *An,
                          const float *Bn, int gn, f32x4 (&na)[TM], f32x4 (&nb)[TN], bool ld,
                          int kl, int slot, const f32x4 *Rw, f32x4 *Rl, const f32x4 *Zw,
-                         f32x4 *Zl) {
+                         f32x4 *Zl, int kst) {
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int m = 0; m < kMfma; ++m) {
             mfma_one(ca, cb, m);
-            if (m < TM)
-                na[m] = frag_a(An, gn, m);
-            else if (m < TM + TN)
-                nb[m - TM] = frag_b(Bn, gn, m - TM);
+            if (m < NRA)
+                read_a(An, gn, m, na);
+            else if (m < NRA + NRB)
+                read_b(Bn, gn, m - NRA, nb);
             if (ld) {
                 if constexpr (kStaged) {
                     if (m < kLoads) {
-                        store_reg(slot, m, staged_value(Rw, Zw, m));
+                        store_reg(slot, m, staged_value(Rw, Zw, m, kst));
                         Rl[m] = load_reg(kl, m);
                         if constexpr (PRO != kProNone)
                             if (is_pro(m)) Zl[m - kProFirst] = load_pz(kl, m);
@@ -780,6 +865,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_pipe(GemmArgs p) {
                     f32x4 *Zl) {
         const float *As = lds + (kt % kStages) * kStageSz;
         const float *Bs = As + kASz;
+        const int kst = min(kt + 1, nk - 1);  // staged: the tile Rw holds
 #pragma unroll
         for (int g = 0; g < NG - 1; ++g) {
             // Group g's operands (read during the previous group) have
@@ -787,7 +873,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_pipe(GemmArgs p) {
             // issued, leaves those in flight behind the MFMAs.
             wait_lgkm0();
             f32x4 na[TM], nb[TN];
-            run_group(ca, cb, As, Bs, g + 1, na, nb, g == 0, kl, slot, Rw, Rl, Zw, Zl);
+            run_group(ca, cb, As, Bs, g + 1, na, nb, g == 0, kl, slot, Rw, Rl, Zw, Zl, kst);
 #pragma unroll
             for (int i = 0; i < TM; ++i) ca[i] = na[i];
 #pragma unroll
@@ -807,7 +893,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_pipe(GemmArgs p) {
         // read and discarded).
         f32x4 na[TM], nb[TN];
         const float *An = lds + ((kt + 1) % kStages) * kStageSz;
-        run_group(ca, cb, An, An + kASz, 0, na, nb, false, 0, 0, Rw, Rl, Zw, Zl);
+        run_group(ca, cb, An, An + kASz, 0, na, nb, false, 0, 0, Rw, Rl, Zw, Zl, 0);
 #pragma unroll
         for (int i = 0; i < TM; ++i) ca[i] = na[i];
 #pragma unroll
@@ -838,7 +924,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_pipe(GemmArgs p) {
                     if (is_pro(q)) Z1[q - kProFirst] = load_pz(min(1, nk - 1), q);
             }
 #pragma unroll
-            for (int q = 0; q < kLoads; ++q) store_reg(0, q, staged_value(R0, Z0, q));
+            for (int q = 0; q < kLoads; ++q) store_reg(0, q, staged_value(R0, Z0, q, 0));
             wait_lgkm0();
             asm volatile("s_barrier" ::: "memory");
             frag(lds, lds + kASz, 0, ca, cb);
@@ -880,16 +966,16 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_pipe(GemmArgs p) {
     __syncthreads();  // every wave past its last tile read before the stage reuse
     if constexpr (kTN)
         if (do_cs) cs.finish(p, lds, n0);
-    store_tile<TM, TN, WTN, NW>(p, acc, lds, m0 + wm0, n0 + wn0, wave, lane);
+    store_tile<TM, TN, WTN, NW, IA, IB>(p, acc, lds, m0 + wm0, n0 + wn0, wave, lane);
 }
 
-template <int BM, int BN, int WGM, int WGN, int BK, bool AK, bool BNC, int PRO>
+template <int BM, int BN, int WGM, int WGN, int BK, bool AK, bool BNC, int PRO, bool KT = false>
 void launch_pipe(const GemmArgs &a0, hipStream_t st) {
     GemmArgs a = a0;
     a.tiles_m = (a.M + BM - 1) / BM;
     a.tiles_n = (a.N + BN - 1) / BN;
     const int splits = a.ksplit > 0 ? (a.K + a.ksplit - 1) / a.ksplit : 1;
-    gemm_f32_pipe<BM, BN, BK, WGM, WGN, AK, BNC, PRO>
+    gemm_f32_pipe<BM, BN, BK, WGM, WGN, AK, BNC, PRO, KT>
         <<<dim3(a.tiles_m * a.tiles_n, splits), 64 * WGM * WGN, 0, st>>>(a);
 }
 
@@ -927,14 +1013,28 @@ inline void cfg_tile(int cfg, bool vec, int &bm, int &bn) {
 // 256x128 tile with the same waves.
 inline int pro_cfg(int cfg) { return cfg == 0 ? 1 : cfg == 6 ? 7 : cfg; }
 
-// pipe: K % cfg_bk(cfg) == 0 and the VEC conditions hold (the host checks):
-// the pipelined whole-tile kernel with the same tile shape.  With PRO != 0
-// the host has mapped cfg through pro_cfg.
+// pipe: the VEC conditions hold (the host checks): the pipelined kernel with
+// the same tile shape, over whole K tiles, or (ktail, no prologue) with a
+// zero-filled last tile.  With PRO != 0 or ktail the host has mapped cfg
+// through pro_cfg (staged tiles).
 template <bool AK, bool BNC, int PRO>
-void launch_layout(const GemmArgs &a, bool vec, bool pipe, int cfg, hipStream_t st) {
+void launch_layout(const GemmArgs &a, bool vec, bool pipe, bool ktail, int cfg, hipStream_t st) {
     if (!vec) {
         launch_one<64, 64, 2, 2, 16, AK, BNC, false, PRO>(a, st);
         return;
+    }
+    if constexpr (PRO == kProNone) {
+        if (pipe && ktail) {
+            switch (cfg) {
+                case 1: launch_pipe<256, 128, 2, 2, kBK, AK, BNC, PRO, true>(a, st); break;
+                case 2: launch_pipe<128, 256, 2, 2, kBK, AK, BNC, PRO, true>(a, st); break;
+                case 3: launch_pipe<128, 128, 2, 2, 32, AK, BNC, PRO, true>(a, st); break;
+                case 5: launch_pipe<128, 64, 2, 2, 32, AK, BNC, PRO, true>(a, st); break;
+                case 7: launch_pipe<256, 128, 4, 2, 32, AK, BNC, PRO, true>(a, st); break;
+                default: launch_pipe<64, 64, 2, 2, 16, AK, BNC, PRO, true>(a, st); break;
+            }
+            return;
+        }
     }
     if (pipe) {
         switch (cfg) {
@@ -970,10 +1070,13 @@ void launch_layout(const GemmArgs &a, bool vec, bool pipe, int cfg, hipStream_t 
 }
 
 // Defined in k_gemm_{nn,nt,tn}.hip.
-// pro: kProNone, or for NT kProAReLU / kProAGelu, for TN kProBReLU / kProBGelu.
-void launch_nn(const GemmArgs &a, bool vec, bool pipe, int cfg, hipStream_t st);
-void launch_nt(const GemmArgs &a, bool vec, bool pipe, int cfg, int pro, hipStream_t st);
-void launch_tn(const GemmArgs &a, bool vec, bool pipe, int cfg, int pro, hipStream_t st);
+// pro: kProNone, or for NT kProAReLU / kProAGelu, for TN kProBReLU / kProBGelu
+// (never with ktail).
+void launch_nn(const GemmArgs &a, bool vec, bool pipe, bool ktail, int cfg, hipStream_t st);
+void launch_nt(const GemmArgs &a, bool vec, bool pipe, bool ktail, int cfg, int pro,
+               hipStream_t st);
+void launch_tn(const GemmArgs &a, bool vec, bool pipe, bool ktail, int cfg, int pro,
+               hipStream_t st);
 // The prologue instances (k_gemm_{nt,tn}_pro.hip), pro != kProNone.
 void launch_nt_pro(const GemmArgs &a, bool vec, bool pipe, int cfg, int pro, hipStream_t st);
 void launch_tn_pro(const GemmArgs &a, bool vec, bool pipe, int cfg, int pro, hipStream_t st);

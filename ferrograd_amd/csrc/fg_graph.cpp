@@ -1298,8 +1298,14 @@ FG_API int fg_graph_constant_f32(fg_graph *g, float value, uint32_t *node) {
 FG_API int fg_graph_op(fg_graph *g, int op, const uint32_t *inputs, int n_inputs, uint32_t *node) {
     FG_REQUIRE(g && node && (inputs || n_inputs == 0), FG_ERR_INVALID_ARGUMENT,
                "fg_graph_op: NULL argument");
-    FG_REQUIRE(op >= FG_OP_ADD && op <= FG_OP_BIAS_ADD, FG_ERR_INVALID_ARGUMENT,
-               "fg_graph_op: op %d is not an operation (use fg_graph_input/constant)", op);
+    FG_REQUIRE(op != FG_OP_INPUT && op != FG_OP_CONST, FG_ERR_INVALID_ARGUMENT,
+               "fg_graph_op: op %d is a leaf (use fg_graph_input / fg_graph_constant)", op);
+    // A GraphOp::Custom the mirror could not map to a ferrograd-nn builder
+    // (backend/mod.rs:659-726) arrives as a code outside fg_op.
+    FG_REQUIRE(op >= FG_OP_ADD && op <= FG_OP_BIAS_ADD, FG_ERR_UNSUPPORTED,
+               "fg_graph_op: operation kind %d is not one this backend lowers (fg_op covers "
+               "ferrograd-nn's builders: add sub mul div matmul relu gelu elu tanh exp log abs "
+               "neg softmax bias_add)", op);
     FG_REQUIRE(n_inputs == arity(op), FG_ERR_GRAPH, "fg_graph_op: %s takes %d inputs, got %d",
                op_name(op), arity(op), n_inputs);
     for (int k = 0; k < n_inputs; ++k)

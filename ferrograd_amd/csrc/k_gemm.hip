@@ -31,12 +31,15 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 //    (145 at 4096^3); else 256x128 with 8 waves when it gives >= one tile per
 //    CU (137 at 2048x4096x4096); else 128x128 or 128x64 (137 for 128x64 at
 //    2048x1024x4096, against 73 for 128x128).
-//  * TN (dW): 256x256 with 8 waves for K >= 4096 filling the chip (144 at
-//    4096^3); 256x128 with 4 waves at >= two tiles per CU (140 at
-//    4096x4096x2048, 137-140 for the other 256-row tiles); then 128x64 at >=
-//    two tiles per CU (131-133 for the 1024- and 1000-wide layers, against
-//    125-127 for 128x128); else 128x128; else 128x64.
-// K % BK != 0 (the 1000-deep head dA) takes gemm_f32_mfma with the same tile.
+//  * TN (dW): 256x256 with 8 waves whenever it fills the chip (143 at 4096^3;
+//    141 at 4096x4096x2048, the c5 hidden dW, against 136.5 for 256x128 with
+//    4 waves, with the interleaved fragments of the TN layout); 256x128 with
+//    4 waves at >= two tiles per CU; then 128x64 at >= two tiles per CU
+//    (131-133 for the 1024- and 1000-wide layers, against 125-127 for
+//    128x128); else 128x128; else 128x64.
+// K % BK != 0 (the 1000-deep head dA) takes the pipelined kernel's staged
+// instances with a zero-filled last K tile (the 256x256 tiles give way to
+// 256x128).
 int tiles(int M, int N, int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); }
 
 int pick_cfg(int layout, int M, int N, int K, int cus) {
@@ -46,7 +49,7 @@ int pick_cfg(int layout, int M, int N, int K, int cus) {
         if (tiles(M, N, 128, 64) >= cus) return 5;
         return 4;
     }
-    if (K >= 4096 && tiles(M, N, 256, 256) >= cus) return 6;
+    if ((K >= 4096 || layout == FG_TN) && tiles(M, N, 256, 256) >= cus) return 6;
     if (layout == FG_NT) {
         if (tiles(M, N, 256, 128) >= cus) return 7;
     } else {
@@ -105,11 +108,12 @@ int plan_split_k(fg_ctx *ctx, GemmArgs &a, int cfg, bool vec) {
 
 // The kernel choices of one GEMM call (sets a.vec_out, and a.partial /
 // a.ksplit when K is split): 16-byte operand loads (vec), the pipelined
-// kernel (pipe), the tile configuration and the number of K slices.  pro:
-// the prologue code (fg::gemm::kPro*), whose tensor Pz must meet the same
-// 16-byte conditions as the operand it scales.
-void plan_gemm(fg_ctx *ctx, int layout, GemmArgs &a, bool &vec, bool &pipe, int &cfg,
-               int &splits, int pro = fg::gemm::kProNone) {
+// kernel (pipe) and whether its last K tile is partial (ktail), the tile
+// configuration and the number of K slices.  pro: the prologue code
+// (fg::gemm::kPro*), whose tensor Pz must meet the same 16-byte conditions as
+// the operand it scales.
+void plan_gemm(fg_ctx *ctx, int layout, GemmArgs &a, bool &vec, bool &pipe, bool &ktail,
+               int &cfg, int &splits, int pro = fg::gemm::kProNone) {
     // The 16-byte path needs 16-byte aligned bases and every row start
     // aligned, i.e. leading dimensions and the contiguous extents that the
     // bounds checks split on (K for k-contiguous operands, M / N otherwise)
@@ -129,12 +133,21 @@ void plan_gemm(fg_ctx *ctx, int layout, GemmArgs &a, bool &vec, bool &pipe, int 
     auto al16 = [](const void *q) { return (((uintptr_t)q) & 15u) == 0; };
     a.vec_out = al16(a.C) && a.ldc % 4 == 0 && (!a.Z || (al16(a.Z) && a.ldz % 4 == 0)) &&
                 (!a.bias || al16(a.bias));
-    // The pipelined kernel's 16-byte tile loads need whole K tiles (a partial
-    // one would bring neighbouring k into valid outputs) and at least one
-    // 16-byte chunk per row-contiguous operand row (edge chunks are clamped,
-    // not masked).
-    pipe = fg::gemm::kPipe && vec && a.K > 0 && a.K % fg::gemm::cfg_bk(cfg) == 0 && a.M >= 4 &&
-           a.N >= 4;
+    // The pipelined kernel's 16-byte tile loads need at least one 16-byte
+    // chunk per row-contiguous operand row (edge chunks are clamped, not
+    // masked).  A partial last K tile (K % BK != 0) is zero-filled by the
+    // staged-tile instances (ktail); the prologue instances need whole tiles
+    // and leave such shapes to gemm_f32_mfma.
+    pipe = fg::gemm::kPipe && vec && a.K > 0 && a.M >= 4 && a.N >= 4;
+    ktail = false;
+    if (pipe && a.K % fg::gemm::cfg_bk(cfg) != 0) {
+        if (pro != fg::gemm::kProNone) {
+            pipe = false;
+        } else {
+            ktail = true;
+            cfg = fg::gemm::pro_cfg(cfg);  // staged tiles
+        }
+    }
     splits = plan_split_k(ctx, a, cfg, vec);
 }
 
@@ -156,13 +169,13 @@ int gemm_common(fg_ctx *ctx, int layout, GemmArgs &a, const char *who,
                a.ldb, a.ldc);
     FG_HIP(hipSetDevice(ctx->device));
     if (a.K == 0) a.A = a.B;  // loads are all masked; K=0 yields the epilogue of zero
-    bool vec, pipe;
+    bool vec, pipe, ktail;
     int cfg, splits;
-    plan_gemm(ctx, layout, a, vec, pipe, cfg, splits, pro);
+    plan_gemm(ctx, layout, a, vec, pipe, ktail, cfg, splits, pro);
     switch (layout) {
-        case FG_NN: fg::gemm::launch_nn(a, vec, pipe, cfg, ctx->stream); break;
-        case FG_NT: fg::gemm::launch_nt(a, vec, pipe, cfg, pro, ctx->stream); break;
-        default: fg::gemm::launch_tn(a, vec, pipe, cfg, pro, ctx->stream); break;
+        case FG_NN: fg::gemm::launch_nn(a, vec, pipe, ktail, cfg, ctx->stream); break;
+        case FG_NT: fg::gemm::launch_nt(a, vec, pipe, ktail, cfg, pro, ctx->stream); break;
+        default: fg::gemm::launch_tn(a, vec, pipe, ktail, cfg, pro, ctx->stream); break;
     }
     FG_LAUNCH_CHECK(who);
     if (splits > 1) {
@@ -191,9 +204,9 @@ int gemm_f32_dispatches(fg_ctx *ctx, int layout, int M, int N, int K, const void
     a.ldb = ldb;
     a.colsum = colsum ? reinterpret_cast<float *>(1) : nullptr;  // only tested for null
     if (K == 0) a.A = a.B;
-    bool vec, pipe;
+    bool vec, pipe, ktail;
     int cfg, splits;
-    plan_gemm(ctx, layout, a, vec, pipe, cfg, splits);
+    plan_gemm(ctx, layout, a, vec, pipe, ktail, cfg, splits);
     return splits > 1 ? 2 : 1;
 }
 }  // namespace fg

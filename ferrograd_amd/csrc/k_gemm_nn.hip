@@ -5,8 +5,8 @@
 namespace fg {
 namespace gemm {
 
-void launch_nn(const GemmArgs &a, bool vec, bool pipe, int cfg, hipStream_t st) {
-    launch_layout<true, true, kProNone>(a, vec, pipe, cfg, st);
+void launch_nn(const GemmArgs &a, bool vec, bool pipe, bool ktail, int cfg, hipStream_t st) {
+    launch_layout<true, true, kProNone>(a, vec, pipe, ktail, cfg, st);
 }
 
 }  // namespace gemm

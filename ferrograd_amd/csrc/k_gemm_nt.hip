@@ -5,9 +5,10 @@
 namespace fg {
 namespace gemm {
 
-void launch_nt(const GemmArgs &a, bool vec, bool pipe, int cfg, int pro, hipStream_t st) {
+void launch_nt(const GemmArgs &a, bool vec, bool pipe, bool ktail, int cfg, int pro,
+               hipStream_t st) {
     if (pro == kProNone)
-        launch_layout<true, false, kProNone>(a, vec, pipe, cfg, st);
+        launch_layout<true, false, kProNone>(a, vec, pipe, ktail, cfg, st);
     else
         launch_nt_pro(a, vec, pipe, cfg, pro, st);
 }

@@ -9,9 +9,9 @@ namespace gemm {
 
 void launch_nt_pro(const GemmArgs &a, bool vec, bool pipe, int cfg, int pro, hipStream_t st) {
     if (pro == kProAReLU)
-        launch_layout<true, false, kProAReLU>(a, vec, pipe, cfg, st);
+        launch_layout<true, false, kProAReLU>(a, vec, pipe, false, cfg, st);
     else
-        launch_layout<true, false, kProAGelu>(a, vec, pipe, cfg, st);
+        launch_layout<true, false, kProAGelu>(a, vec, pipe, false, cfg, st);
 }
 
 }  // namespace gemm

@@ -5,9 +5,10 @@
 namespace fg {
 namespace gemm {
 
-void launch_tn(const GemmArgs &a, bool vec, bool pipe, int cfg, int pro, hipStream_t st) {
+void launch_tn(const GemmArgs &a, bool vec, bool pipe, bool ktail, int cfg, int pro,
+               hipStream_t st) {
     if (pro == kProNone)
-        launch_layout<false, true, kProNone>(a, vec, pipe, cfg, st);
+        launch_layout<false, true, kProNone>(a, vec, pipe, ktail, cfg, st);
     else
         launch_tn_pro(a, vec, pipe, cfg, pro, st);
 }

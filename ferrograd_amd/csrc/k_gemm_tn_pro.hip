@@ -9,9 +9,9 @@ namespace gemm {
 
 void launch_tn_pro(const GemmArgs &a, bool vec, bool pipe, int cfg, int pro, hipStream_t st) {
     if (pro == kProBReLU)
-        launch_layout<false, true, kProBReLU>(a, vec, pipe, cfg, st);
+        launch_layout<false, true, kProBReLU>(a, vec, pipe, false, cfg, st);
     else
-        launch_layout<false, true, kProBGelu>(a, vec, pipe, cfg, st);
+        launch_layout<false, true, kProBGelu>(a, vec, pipe, false, cfg, st);
 }
 
 }  // namespace gemm

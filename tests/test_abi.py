@@ -97,3 +97,23 @@ def test_context_without_gpu_reports_no_device():
     with pytest.raises(fa.FgError) as e:
         fa.Context(0)
     assert e.value.code in (8, 4)
+
+
+def test_rust_ffi_crate_declares_every_function():
+    """crates/ferrograd-hip-sys (unbuilt here: no Rust toolchain) declares
+    each function of include/ferrograd_hip.h with the same parameter names in
+    the same order, and nothing else."""
+    hdr = open(os.path.join(ROOT, "include", "ferrograd_hip.h")).read()
+    hdr = re.sub(r"/\*.*?\*/", "", hdr, flags=re.S)
+    c_decl = {}
+    for m in re.finditer(r"\b(fg_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", hdr):
+        args = [a.strip() for a in m.group(2).split(",") if a.strip() and a.strip() != "void"]
+        c_decl[m.group(1)] = [re.findall(r"[A-Za-z_][A-Za-z_0-9]*$", a)[0] for a in args]
+    rs = open(os.path.join(ROOT, "crates", "ferrograd-hip-sys", "src", "lib.rs")).read()
+    r_decl = {}
+    for m in re.finditer(r"pub fn (fg_[a-z0-9_]+)\(([^)]*)\)", rs, re.S):
+        args = [a.strip() for a in m.group(2).split(",") if a.strip()]
+        r_decl[m.group(1)] = [a.split(":")[0].strip() for a in args]
+    assert set(c_decl) == set(r_decl), set(c_decl) ^ set(r_decl)
+    for name, params in c_decl.items():
+        assert r_decl[name] == params, name

@@ -129,3 +129,32 @@ def test_losses_lower():
         desc = g.describe([f32_bits(1e-3), 8, 10])
         n_l, lines = section(desc, "loss")
         assert n_l == 1 and "eltwise" in lines[0]
+
+
+def test_unknown_operation_kind_is_unsupported():
+    """An operation code outside fg_op -- a GraphOp::Custom the Rust mirror
+    could not map to a ferrograd-nn builder -- is refused with
+    FG_ERR_UNSUPPORTED (ErrorKind::UnsupportedFeature) and a message that
+    names it; leaves passed to fg_graph_op are invalid arguments."""
+    import ctypes
+
+    from ferrograd_amd._lib import call
+    g = ctypes.c_void_p()
+    call("fg_graph_create", 0, 0, ctypes.byref(g))
+    try:
+        f = ctypes.c_uint32()
+        call("fg_graph_new_field", g, ctypes.byref(f))
+        fields = (ctypes.c_uint32 * 2)(f.value, f.value)
+        x = ctypes.c_uint32()
+        call("fg_graph_input", g, fields, 2, ctypes.byref(x))
+        ins = (ctypes.c_uint32 * 1)(x.value)
+        node = ctypes.c_uint32()
+        with pytest.raises(FgError) as e:
+            call("fg_graph_op", g, 99, ins, 1, ctypes.byref(node))
+        assert e.value.code == 3 and "operation kind 99" in str(e.value)
+        with pytest.raises(FgError) as e:
+            call("fg_graph_op", g, 0, ins, 1, ctypes.byref(node))  # FG_OP_INPUT
+        assert e.value.code == 1
+        call("fg_graph_op", g, 7, ins, 1, ctypes.byref(node))  # relu: fine
+    finally:
+        call("fg_graph_destroy", g)
