@@ -237,6 +237,10 @@ struct Launch {
     int dst_slot[fg::kEltMaxDst];
     int label_slot = kNone;
     uint64_t count = 0;
+    // The final forward softmax when the fused CE loss follows it: a captured
+    // step leaves it out and the loss launch writes its output (sProbs).
+    bool elidable = false;
+    int sProbs = kNone;
     std::string desc;
     Launch() {
         std::fill(src_slot, src_slot + fg::kEltMaxSrc, kNone);
@@ -549,6 +553,7 @@ int lower_forward(fg_plan &P) {
             L.N = (int)P.shape[n].cols;
             L.sA = P.vslot(nd.in[0]);
             L.sC = P.vslot(n);
+            L.elidable = P.ce_fused_possible && (int)n == P.last;
             L.desc = "forward softmax " + std::to_string(L.M) + "x" + std::to_string(L.N) +
                      " -> node " + std::to_string(n);
             P.fwd.push_back(L);
@@ -599,6 +604,7 @@ int lower_loss(fg_plan &P) {
         L.sB = P.loss_slot;    // row loss
         L.sBias = P.mean_slot;
         L.sC = P.needs_grad[x] ? P.grad_slot[x] : kNone;
+        L.sProbs = P.vslot(last);
         L.desc = "loss softmax+ce " + std::to_string(L.M) + "x" + std::to_string(L.N) +
                  " (dlogits -> grad of node " + std::to_string(x) + ")";
         P.loss.push_back(L);
@@ -1021,6 +1027,7 @@ int check_launch(const fg_plan &P, const Launch &L) {
             chk(L.sB, M, "row loss");
             chk(L.sBias, 1, "mean loss");
             chk(L.sC, M * N, "dlogits");
+            chk(L.sProbs, M * N, "probabilities");
             break;
         case LK_FILL0:
             chk(L.sC, L.count, "fill");
@@ -1064,10 +1071,13 @@ int check_launch(const fg_plan &P, const Launch &L) {
 }
 
 // ------------------------------------------------------------ execute
-int run(fg_plan &P, const std::vector<Launch> &list) {
+// step: the launches belong to a whole captured step (forward through
+// optimiser), so the final forward softmax is left to the loss launch.
+int run(fg_plan &P, const std::vector<Launch> &list, bool step = false) {
     fg_ctx *ctx = &P.wctx;
     for (const Launch &L : list) {
         int rc = FG_OK;
+        if (step && L.elidable) continue;
         switch (L.kind) {
             case LK_GEMM:
                 if (L.sExtra != kNone && L.dtype == FG_DTYPE_F32)  // dW with the fused dbias (TN)
@@ -1115,9 +1125,11 @@ int run(fg_plan &P, const std::vector<Launch> &list) {
             case LK_SMCE:
                 FG_REQUIRE(P.ptr(L.sZ), FG_ERR_INVALID_ARGUMENT,
                            "dispatch_loss: no target bound (fg_plan_bind_target)");
-                rc = fg_softmax_ce(ctx, L.dtype, P.ptr(L.sA), L.N, (const uint32_t *)P.ptr(L.sZ),
-                                   L.M, L.N, 1.0f, (float *)P.ptr(L.sB), (float *)P.ptr(L.sBias),
-                                   P.ptr(L.sC), L.N, nullptr);
+                rc = fg::softmax_ce_ex(ctx, L.dtype, P.ptr(L.sA), L.N,
+                                       (const uint32_t *)P.ptr(L.sZ), L.M, L.N, 1.0f,
+                                       (float *)P.ptr(L.sB), (float *)P.ptr(L.sBias),
+                                       P.ptr(L.sC), L.N, nullptr,
+                                       step ? P.ptr(L.sProbs) : nullptr, L.N);
                 break;
             case LK_ELT: {
                 fg::EltProgram p = L.prog;
@@ -1746,8 +1758,8 @@ FG_API int fg_plan_capture_step(fg_plan *p) {
     drop_graph(*p);
     FG_HIP(hipStreamSynchronize(p->ctx->stream));
     FG_HIP(hipStreamBeginCapture(p->ctx->stream, hipStreamCaptureModeThreadLocal));
-    rc = run(*p, p->fwd);
-    if (rc == FG_OK) rc = run(*p, p->loss);
+    rc = run(*p, p->fwd, true);
+    if (rc == FG_OK) rc = run(*p, p->loss, true);
     if (rc == FG_OK) rc = run(*p, p->ce_fused_possible ? p->bwd_fused : p->bwd_seed);
     if (rc == FG_OK) rc = run_optim(*p, p->mt_all);
     hipGraph_t graph = nullptr;
@@ -1902,24 +1914,39 @@ FG_API int fg_plan_load(fg_plan *p, const char *path) {
 FG_API int fg_plan_describe(const fg_plan *p, char *buf, size_t len, size_t *needed) {
     FG_REQUIRE(p, FG_ERR_INVALID_ARGUMENT, "fg_plan_describe: plan is NULL");
     std::string s;
+    fg_ctx *wc = p->ctx ? const_cast<fg_ctx *>(&p->wctx) : nullptr;
+    // Dispatches of a GEMM launch: 2 when K is split (the slices, then the
+    // kernel that sums them in slice order and applies the epilogue).
+    auto gemm_dispatches = [&](const Launch &L) {
+        if ((L.kind != LK_GEMM && L.kind != LK_GEMM_BWD) || L.dtype != FG_DTYPE_F32) return 1;
+        return fg::gemm_f32_dispatches(wc, L.sExtra != kNone ? FG_TN : L.layout, L.M, L.N, L.K,
+                                       p->ptr(L.sA), L.lda, p->ptr(L.sB), L.ldb,
+                                       L.kind == LK_GEMM && L.sExtra != kNone);
+    };
     auto add = [&](const char *title, const std::vector<Launch> &v) {
         s += std::string(title) + ": " + std::to_string(v.size()) + " launches\n";
-        for (const Launch &L : v) s += "  " + L.desc + "\n";
+        for (const Launch &L : v) {
+            s += "  " + L.desc;
+            if (gemm_dispatches(L) > 1) s += " [K split: slices + summing kernel]";
+            s += "\n";
+        }
     };
-    // Kernel dispatches per planned launch: the bias-gradient reduction is a
-    // partial and a final pass, the fused softmax + CE adds the mean-loss
-    // reduction, an fp32 GEMM that splits K adds its summing epilogue, the
-    // Adam update is preceded by its step-counter advance.
+    // Kernel dispatches per planned launch in a captured step: the
+    // bias-gradient reduction is a partial and a final pass, a GEMM that
+    // splits K adds its summing kernel, the fused softmax + CE adds the
+    // mean-loss reduction unless its one-workgroup form computes the mean,
+    // the final forward softmax is left to the loss launch, the Adam update
+    // is preceded by its step-counter advance.
     auto kernels = [&](const std::vector<Launch> &v) {
         int n = 0;
         for (const Launch &L : v) {
-            if ((L.kind == LK_GEMM || L.kind == LK_GEMM_BWD) && L.dtype == FG_DTYPE_F32)
-                n += fg::gemm_f32_dispatches(p->ctx ? const_cast<fg_ctx *>(&p->wctx) : nullptr,
-                                             L.sExtra != kNone ? FG_TN : L.layout, L.M,
-                                             L.N, L.K, p->ptr(L.sA), L.lda, p->ptr(L.sB), L.ldb,
-                                             L.kind == LK_GEMM && L.sExtra != kNone);
+            if (L.elidable) continue;
+            if (L.kind == LK_SMCE)
+                n += fg::softmax_ce_dispatches(L.M, L.N, L.sBias != kNone);
+            else if (L.kind == LK_BIAS_GRAD)
+                n += 2;
             else
-                n += (L.kind == LK_BIAS_GRAD || (L.kind == LK_SMCE && L.sBias != kNone)) ? 2 : 1;
+                n += gemm_dispatches(L);
         }
         return n;
     };

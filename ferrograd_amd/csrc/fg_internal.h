@@ -67,6 +67,16 @@ uint64_t adam_dev_state_bytes();
 int mt_adam_dev(fg_ctx *ctx, fg_mt *mt, float lr, float b1, float b2, float eps, void *d_state,
                 int zero_grad);
 
+// fg_softmax_ce with one more output: probs[r][c] = softmax(x_r)[c] (ld
+// ldp, element type dtype; NULL: none), so a fused loss launch can also
+// produce the forward's softmax output (k_softmax.hip).
+int softmax_ce_ex(fg_ctx *ctx, int dtype, const void *d_logits, int ldx, const uint32_t *d_labels,
+                  int R, int C, float grad_scale, float *d_row_loss, float *d_mean_loss,
+                  void *d_dlogits, int ldd, uint32_t *d_argmax, void *d_probs, int ldp);
+
+// Kernel dispatches of softmax_ce_ex for R x C (with or without the mean).
+int softmax_ce_dispatches(int R, int C, bool mean);
+
 // Elementwise program launch (k_eltwise_prog.hip).
 struct EltProgram;
 int launch_eltwise(fg_ctx *ctx, const EltProgram &p);

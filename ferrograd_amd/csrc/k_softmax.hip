@@ -148,7 +148,8 @@ __global__ __launch_bounds__(NT) void softmax_rows_v4(const float *__restrict__ 
                                                       const uint32_t *__restrict__ labels, int C,
                                                       float scale, float *__restrict__ row_loss,
                                                       float *__restrict__ out, int ldo,
-                                                      uint32_t *__restrict__ argmax) {
+                                                      uint32_t *__restrict__ argmax,
+                                                      float *__restrict__ probs, int ldp) {
     constexpr int NW = NT / 64;
     __shared__ float sm[NW];
     __shared__ int si[NW];
@@ -210,6 +211,14 @@ __global__ __launch_bounds__(NT) void softmax_rows_v4(const float *__restrict__ 
                                                    rsrc(orow, i), lane_off, 0, kBufNT);
         }
     }
+    if (probs) {  // the softmax itself (the forward's output, when the loss writes it)
+        const float inv = 1.0f / s;
+        const float *prow = probs + (size_t)r * ldp;
+#pragma unroll
+        for (int i = 0; i < NV; ++i)
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[i] * inv),
+                                                   rsrc(prow, i), lane_off, 0, kBufNT);
+    }
 }
 
 // Streaming path for any C, alignment and element type dt (x and out share
@@ -220,7 +229,8 @@ __global__ __launch_bounds__(kNT) void softmax_rows_stream(const void *__restric
                                                            int C, float scale,
                                                            float *__restrict__ row_loss,
                                                            void *__restrict__ out, int ldo,
-                                                           uint32_t *__restrict__ argmax, int dt) {
+                                                           uint32_t *__restrict__ argmax, int dt,
+                                                           void *__restrict__ probs, int ldp) {
     __shared__ float sm[kWaves], ss[kWaves];
     __shared__ int si[kWaves];
     const int r = blockIdx.x;
@@ -240,13 +250,14 @@ __global__ __launch_bounds__(kNT) void softmax_rows_stream(const void *__restric
     const size_t esz = dt == fg::kF32 ? 4 : 2;
     row_outputs(static_cast<const char *>(x) + xb * esz, dt, C, labels, r, m, s, am, row_loss,
                 argmax);
-    if (out) {
+    if (out || probs) {
         const float inv = 1.0f / s;
         const int t = labels ? (int)labels[r] : -1;
-        const uint64_t ob = (uint64_t)r * ldo;
+        const uint64_t ob = (uint64_t)r * ldo, pb = (uint64_t)r * ldp;
         for (int c = threadIdx.x; c < C; c += kNT) {
             const float p = expf(fg::load_as_f(x, dt, xb + c) - m) * inv;
-            fg::store_from_f(out, dt, ob + c, scale * (c == t ? p - 1.0f : p));
+            if (out) fg::store_from_f(out, dt, ob + c, scale * (c == t ? p - 1.0f : p));
+            if (probs) fg::store_from_f(probs, dt, pb + c, p);
         }
     }
 }
@@ -258,7 +269,8 @@ __global__ __launch_bounds__(kNT) void softmax_rows_h4(const uint16_t *__restric
                                                        const uint32_t *__restrict__ labels, int C,
                                                        float scale, float *__restrict__ row_loss,
                                                        uint16_t *__restrict__ out, int ldo,
-                                                       uint32_t *__restrict__ argmax, int dt) {
+                                                       uint32_t *__restrict__ argmax, int dt,
+                                                       uint16_t *__restrict__ probs, int ldp) {
     typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
     __shared__ float sm[kWaves];
     __shared__ int si[kWaves];
@@ -322,6 +334,80 @@ __global__ __launch_bounds__(kNT) void softmax_rows_h4(const uint16_t *__restric
             }
         }
     }
+    if (probs) {
+        const float inv = 1.0f / s;
+        uint16_t *prow = probs + (size_t)r * ldp;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int j = threadIdx.x + i * kNT;
+            if (j < C4) {
+                uint16_t d[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) d[e] = fg::f_to_h16(dt, v[i][e] * inv);
+                const u32x2 w = {(uint32_t)d[0] | ((uint32_t)d[1] << 16),
+                                 (uint32_t)d[2] | ((uint32_t)d[3] << 16)};
+                __builtin_nontemporal_store(w, reinterpret_cast<u32x2 *>(prow) + j);
+            }
+        }
+    }
+}
+
+// Small problems in one workgroup (R*C <= kSmallElems, C <= kSmallCols): one
+// row per thread (rows t, t + 256, ...), so softmax + CE and the mean of the
+// row losses take a single launch; the mean sums the rows in a fixed order
+// (each thread's rows in order, then a fixed tree over the threads, in
+// double).  The same outputs, conventions (argmax = first maximum, NaN loss
+// for a label outside [0, C)) and element-type handling as the row kernels;
+// `probs` receives the softmax itself.
+constexpr int kSmallCols = 64;
+constexpr int64_t kSmallElems = 65536;
+
+__global__ __launch_bounds__(kNT) void softmax_ce_small(
+    const void *__restrict__ x, int ldx, const uint32_t *__restrict__ labels, int R, int C,
+    float scale, float *__restrict__ row_loss, void *__restrict__ out, int ldo,
+    uint32_t *__restrict__ argmax, void *__restrict__ probs, int ldp, float *__restrict__ mean,
+    int dt) {
+    __shared__ double sh[kNT];
+    double acc = 0.0;
+    for (int r = threadIdx.x; r < R; r += kNT) {
+        const uint64_t xb = (uint64_t)r * ldx;
+        float m = -INFINITY;
+        int am = 0;
+        for (int c = 0; c < C; ++c) {
+            const float v = fg::load_as_f(x, dt, xb + c);
+            if (v > m) {
+                m = v;
+                am = c;
+            }
+        }
+        float s = 0.0f;
+        for (int c = 0; c < C; ++c) s += expf(fg::load_as_f(x, dt, xb + c) - m);
+        if (argmax) argmax[r] = (uint32_t)am;
+        if (row_loss || mean) {
+            const uint32_t t = labels ? labels[r] : 0u;
+            const float l = (t < (uint32_t)C) ? (m + logf(s)) - fg::load_as_f(x, dt, xb + t)
+                                              : __builtin_nanf("");
+            if (row_loss) row_loss[r] = l;
+            acc += (double)l;
+        }
+        if (out || probs) {
+            const float inv = 1.0f / s;
+            const int t = labels ? (int)labels[r] : -1;
+            for (int c = 0; c < C; ++c) {
+                const float p = expf(fg::load_as_f(x, dt, xb + c) - m) * inv;
+                if (out) fg::store_from_f(out, dt, (uint64_t)r * ldo + c, scale * (c == t ? p - 1.0f : p));
+                if (probs) fg::store_from_f(probs, dt, (uint64_t)r * ldp + c, p);
+            }
+        }
+    }
+    if (!mean) return;
+    sh[threadIdx.x] = acc;
+    __syncthreads();
+    for (int o = kNT / 2; o > 0; o >>= 1) {
+        if ((int)threadIdx.x < o) sh[threadIdx.x] += sh[threadIdx.x + o];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) mean[0] = (float)(sh[0] / (double)R);
 }
 
 // mean[0] = sum(vals[0..n)) / n in a fixed order (one block).
@@ -357,20 +443,36 @@ __global__ __launch_bounds__(kNT) void softmax_bwd_rows(const void *__restrict__
     }
 }
 
+// The row kernels for R rows of C; `probs` (may be NULL) receives the
+// softmax.  With `mean` given and a small problem, the one-workgroup kernel
+// also writes the mean loss and *mean_done is set; otherwise the caller
+// reduces the row losses.
 int launch_rows(fg_ctx *ctx, int dt, const void *x, int ldx, const uint32_t *labels, int R, int C,
-                float scale, float *row_loss, void *out, int ldo, uint32_t *argmax) {
+                float scale, float *row_loss, void *out, int ldo, uint32_t *argmax,
+                void *probs = nullptr, int ldp = 0, float *mean = nullptr,
+                bool *mean_done = nullptr) {
+    hipStream_t st = ctx->stream;
+    if (mean_done) *mean_done = false;
+    if (C <= kSmallCols && (int64_t)R * C <= kSmallElems) {
+        softmax_ce_small<<<1, kNT, 0, st>>>(x, ldx, labels, R, C, scale, row_loss, out, ldo,
+                                            argmax, probs, ldp, mean, dt);
+        FG_LAUNCH_CHECK("softmax_ce_small");
+        if (mean_done) *mean_done = mean != nullptr;
+        return FG_OK;
+    }
     const unsigned align = dt == fg::kF32 ? 16u : 8u;
-    const bool aligned = ((((uintptr_t)x) | ((uintptr_t)out)) & (align - 1)) == 0 &&
-                         (C % 4 == 0) && (ldx % 4 == 0) && (!out || ldo % 4 == 0);
+    const bool aligned = ((((uintptr_t)x) | ((uintptr_t)out) | ((uintptr_t)probs)) &
+                          (align - 1)) == 0 &&
+                         (C % 4 == 0) && (ldx % 4 == 0) && (!out || ldo % 4 == 0) &&
+                         (!probs || ldp % 4 == 0);
     const int C4 = C / 4;
     dim3 grid(R), block(kNT);
-    hipStream_t st = ctx->stream;
     if (dt == fg::kF32) {
         const float *xf = static_cast<const float *>(x);
         float *of = static_cast<float *>(out);
 #define FG_SM_LAUNCH(NV, NT)                                                               \
     softmax_rows_v4<NV, NT><<<grid, NT, 0, st>>>(xf, ldx, labels, C, scale, row_loss, of, ldo, \
-                                                 argmax)
+                                                 argmax, static_cast<float *>(probs), ldp)
         if (aligned && C4 <= kNT * 1)
             FG_SM_LAUNCH(1, kNT);
         else if (aligned && C4 <= kNT * 2)
@@ -385,14 +487,14 @@ int launch_rows(fg_ctx *ctx, int dt, const void *x, int ldx, const uint32_t *lab
             FG_SM_LAUNCH(16, 2 * kNT);
         else
             softmax_rows_stream<<<grid, block, 0, st>>>(x, ldx, labels, C, scale, row_loss, out,
-                                                        ldo, argmax, dt);
+                                                        ldo, argmax, dt, probs, ldp);
 #undef FG_SM_LAUNCH
     } else {
         const uint16_t *xh = static_cast<const uint16_t *>(x);
         uint16_t *oh = static_cast<uint16_t *>(out);
 #define FG_SM_LAUNCH(NV)                                                                        \
     softmax_rows_h4<NV><<<grid, block, 0, st>>>(xh, ldx, labels, C, scale, row_loss, oh, ldo, \
-                                                argmax, dt)
+                                                argmax, dt, static_cast<uint16_t *>(probs), ldp)
         if (aligned && C4 <= kNT * 1)
             FG_SM_LAUNCH(1);
         else if (aligned && C4 <= kNT * 4)
@@ -403,7 +505,7 @@ int launch_rows(fg_ctx *ctx, int dt, const void *x, int ldx, const uint32_t *lab
             FG_SM_LAUNCH(32);
         else
             softmax_rows_stream<<<grid, block, 0, st>>>(x, ldx, labels, C, scale, row_loss, out,
-                                                        ldo, argmax, dt);
+                                                        ldo, argmax, dt, probs, ldp);
 #undef FG_SM_LAUNCH
     }
     FG_LAUNCH_CHECK("softmax_rows");
@@ -412,33 +514,50 @@ int launch_rows(fg_ctx *ctx, int dt, const void *x, int ldx, const uint32_t *lab
 
 }  // namespace
 
-FG_API int fg_softmax_ce(fg_ctx *ctx, int dtype, const void *d_logits, int ldx,
-                         const uint32_t *d_labels, int R, int C, float grad_scale,
-                         float *d_row_loss, float *d_mean_loss, void *d_dlogits, int ldd,
-                         uint32_t *d_argmax) {
+namespace fg {
+int softmax_ce_dispatches(int R, int C, bool mean) {
+    const bool small = C <= kSmallCols && (int64_t)R * C <= kSmallElems;
+    return (mean && !small) ? 2 : 1;
+}
+
+int softmax_ce_ex(fg_ctx *ctx, int dtype, const void *d_logits, int ldx, const uint32_t *d_labels,
+                  int R, int C, float grad_scale, float *d_row_loss, float *d_mean_loss,
+                  void *d_dlogits, int ldd, uint32_t *d_argmax, void *d_probs, int ldp) {
     FG_REQUIRE(ctx, FG_ERR_INVALID_ARGUMENT, "fg_softmax_ce: ctx is NULL");
     FG_REQUIRE(dtype >= FG_DTYPE_F32 && dtype <= FG_DTYPE_BF16, FG_ERR_INVALID_ARGUMENT,
                "fg_softmax_ce: bad dtype %d", dtype);
     FG_REQUIRE(R >= 0 && C > 0 && ldx >= C, FG_ERR_SHAPE,
                "fg_softmax_ce: bad shape R=%d C=%d ldx=%d", R, C, ldx);
     FG_REQUIRE(!d_dlogits || ldd >= C, FG_ERR_SHAPE, "fg_softmax_ce: ldd=%d < C=%d", ldd, C);
+    FG_REQUIRE(!d_probs || ldp >= C, FG_ERR_SHAPE, "fg_softmax_ce: ldp=%d < C=%d", ldp, C);
     FG_REQUIRE(d_logits && d_labels, FG_ERR_INVALID_ARGUMENT,
                "fg_softmax_ce: logits and labels are required");
     if (R == 0) return FG_OK;
     FG_HIP(hipSetDevice(ctx->device));
+    const bool small = C <= kSmallCols && (int64_t)R * C <= kSmallElems;
     float *row_loss = d_row_loss;
-    if (!row_loss && d_mean_loss) {
+    if (!row_loss && d_mean_loss && !small) {
         row_loss = (float *)fg::workspace(ctx, (uint64_t)R * sizeof(float));
         if (!row_loss) return FG_ERR_OUT_OF_MEMORY;
     }
+    bool mean_done = false;
     int rc = launch_rows(ctx, dtype, d_logits, ldx, d_labels, R, C, grad_scale, row_loss,
-                         d_dlogits, ldd, d_argmax);
+                         d_dlogits, ldd, d_argmax, d_probs, ldp, d_mean_loss, &mean_done);
     if (rc) return rc;
-    if (d_mean_loss) {
+    if (d_mean_loss && !mean_done) {
         mean_kernel<<<1, 1024, 0, ctx->stream>>>(row_loss, R, d_mean_loss);
         FG_LAUNCH_CHECK("mean_kernel");
     }
     return FG_OK;
+}
+}  // namespace fg
+
+FG_API int fg_softmax_ce(fg_ctx *ctx, int dtype, const void *d_logits, int ldx,
+                         const uint32_t *d_labels, int R, int C, float grad_scale,
+                         float *d_row_loss, float *d_mean_loss, void *d_dlogits, int ldd,
+                         uint32_t *d_argmax) {
+    return fg::softmax_ce_ex(ctx, dtype, d_logits, ldx, d_labels, R, C, grad_scale, d_row_loss,
+                             d_mean_loss, d_dlogits, ldd, d_argmax, nullptr, 0);
 }
 
 FG_API int fg_softmax_ce_f32(fg_ctx *ctx, const float *d_logits, int ldx, const uint32_t *d_labels,

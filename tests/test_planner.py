@@ -54,7 +54,9 @@ def test_mlp_lowers_to_fused_gemm_launches():
     assert sum(l.startswith("backward gemm NT") for l in bwd) == 3  # incl. dX of the data
     assert "eltwise" not in "\n".join(bwd)  # no standalone activation backward
     assert "adam over 6 inputs" in desc      # X is frozen: grads but no update
-    assert "kernels per step: 14 (forward 4, loss 2, backward 6, optim 2)" in desc
+    # A captured step leaves the final softmax to the loss launch (which
+    # writes forward_out too): forward 3; the loss is the row kernel + mean.
+    assert "kernels per step: 13 (forward 3, loss 2, backward 6, optim 2)" in desc
 
 
 def test_reference_graph_mul_add_is_one_elementwise_launch():
@@ -158,3 +160,14 @@ def test_unknown_operation_kind_is_unsupported():
         call("fg_graph_op", g, 7, ins, 1, ctypes.byref(node))  # relu: fine
     finally:
         call("fg_graph_destroy", g)
+
+
+def test_c1_step_dispatches():
+    """BASELINE c1 (batch 64, 784 -> 256 -> ReLU -> 10, CE, SGD), planned
+    without a device (so no GEMM splits K): a captured step is 2 forward
+    GEMMs (the final softmax is left to the loss launch), 1 loss launch (one
+    workgroup, the mean included), 4 backward GEMMs (dbias fused into the dW
+    GEMMs) and 1 SGD update."""
+    g, meta = mlp_graph([784, 256, 10], act="relu", optim=Optim.sgd())
+    desc = g.describe([f32_bits(0.01), 64, 784, 256, 10])
+    assert "kernels per step: 8 (forward 2, loss 1, backward 4, optim 1)" in desc, desc
