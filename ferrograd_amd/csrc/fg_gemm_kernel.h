@@ -596,9 +596,11 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_pipe(GemmArgs p) {
     auto src_kc = [&](const float *base, int ld, int r0, int rmax, int k0, int pos) {
         const int row = pos / (BK / 4), pc = pos % (BK / 4);
         const int c = pc ^ swz_k<BK>(row);
-        int k = k0 + 4 * c;
-        if constexpr (KT) k = min(k, p.K - 4);
-        return base + (size_t)min(r0 + row, rmax - 1) * ld + k;
+        const float *rp = base + (size_t)min(r0 + row, rmax - 1) * ld;
+        // Whole tiles: the per-lane part (row, chunk) stays loop-invariant
+        // and k0 is added as a uniform offset.
+        if constexpr (KT) return rp + min(k0 + 4 * c, p.K - 4);
+        return rp + 4 * c + k0;
     };
     auto src_rc = [&](const float *base, int ld, int r0, int rmax, int k0, int pos, int R) {
         const int k = pos / (R / 4), pc = pos % (R / 4);
