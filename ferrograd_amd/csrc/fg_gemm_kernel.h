@@ -1083,5 +1083,13 @@ void launch_tn(const GemmArgs &a, bool vec, bool pipe, bool ktail, int cfg, int 
 void launch_nt_pro(const GemmArgs &a, bool vec, bool pipe, int cfg, int pro, hipStream_t st);
 void launch_tn_pro(const GemmArgs &a, bool vec, bool pipe, int cfg, int pro, hipStream_t st);
 
+// Skinny GEMMs (k_gemm_skinny.hip): N <= kSkinnyN and K <= kSkinnyK, any
+// layout (0 NN, 1 NT, 2 TN), no prologue, no split; one workgroup per 16
+// output rows loads its whole A row panel and the B panel at once.  Takes
+// the epilogue (bias, act, Z, act'(Zs), accumulate) and the TN column sums.
+constexpr int kSkinnyN = 16;
+constexpr int kSkinnyK = 256;
+void launch_skinny(const GemmArgs &a, int layout, hipStream_t st);
+
 }  // namespace gemm
 }  // namespace fg

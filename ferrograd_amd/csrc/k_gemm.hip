@@ -83,17 +83,25 @@ __global__ __launch_bounds__(kThreads) void splitk_reduce(GemmArgs p, int splits
 }
 
 // Split K over workgroup rows when the output gives few tiles (under half
-// the CUs) and K is long (at least 4 K tiles per slice): each slice's raw
+// the CUs) and K is long (at least kSplitMinKTiles K tiles, and at least 4
+// per slice; c1's K = 256 GEMMs, 16 K tiles, run 62 us per step split and
+// 69 us unsplit, though unsplit saves two dispatches): each slice's raw
 // product goes to the context's workspace, which must already hold them
 // (every plan has its own of at least 1 MiB; direct callers reserve one with
 // fg_ctx_reserve_workspace; it is never grown here, so launches stay
 // capturable).  The fused column sum of fg_gemm_dw is not split.
 // Returns the number of slices (1: no split).
+#ifndef FG_SPLIT_MIN_KTILES  // tuning builds may set it
+#define FG_SPLIT_MIN_KTILES 8
+#endif
+constexpr int kSplitMinKTiles = FG_SPLIT_MIN_KTILES;
+
 int plan_split_k(fg_ctx *ctx, GemmArgs &a, int cfg, bool vec) {
     if (a.colsum || a.K <= 0) return 1;
     int bm, bn;
     fg::gemm::cfg_tile(cfg, vec, bm, bn);
     const int bk = vec ? fg::gemm::cfg_bk(cfg) : 16;
+    if (a.K < kSplitMinKTiles * bk) return 1;
     const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
     int s = std::min(cus / (2 * tiles(a.M, a.N, bm, bn)), a.K / (4 * bk));
     if (s < 2) return 1;
@@ -106,14 +114,28 @@ int plan_split_k(fg_ctx *ctx, GemmArgs &a, int cfg, bool vec) {
     return s;
 }
 
+// Skinny shapes (few columns, short K, at most one 16-row workgroup per CU)
+// take the one-round-trip kernel of k_gemm_skinny.hip: c1's second layer
+// (64x10x256) and its weight gradient with the bias gradient (TN 256x10x64).
+bool use_skinny(fg_ctx *ctx, const GemmArgs &a, int pro) {
+    const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    return pro == fg::gemm::kProNone && a.N <= fg::gemm::kSkinnyN && a.K > 0 &&
+           a.K <= fg::gemm::kSkinnyK && (int64_t)a.M <= 16LL * cus;
+}
+
 // The kernel choices of one GEMM call (sets a.vec_out, and a.partial /
-// a.ksplit when K is split): 16-byte operand loads (vec), the pipelined
-// kernel (pipe) and whether its last K tile is partial (ktail), the tile
-// configuration and the number of K slices.  pro: the prologue code
-// (fg::gemm::kPro*), whose tensor Pz must meet the same 16-byte conditions as
-// the operand it scales.
-void plan_gemm(fg_ctx *ctx, int layout, GemmArgs &a, bool &vec, bool &pipe, bool &ktail,
-               int &cfg, int &splits, int pro = fg::gemm::kProNone) {
+// a.ksplit when K is split): the skinny kernel (skinny; then nothing else
+// applies), 16-byte operand loads (vec), the pipelined kernel (pipe) and
+// whether its last K tile is partial (ktail), the tile configuration and the
+// number of K slices.  pro: the prologue code (fg::gemm::kPro*), whose
+// tensor Pz must meet the same 16-byte conditions as the operand it scales.
+void plan_gemm(fg_ctx *ctx, int layout, GemmArgs &a, bool &skinny, bool &vec, bool &pipe,
+               bool &ktail, int &cfg, int &splits, int pro = fg::gemm::kProNone) {
+    skinny = use_skinny(ctx, a, pro);
+    vec = pipe = ktail = false;
+    cfg = 0;
+    splits = 1;
+    if (skinny) return;
     // The 16-byte path needs 16-byte aligned bases and every row start
     // aligned, i.e. leading dimensions and the contiguous extents that the
     // bounds checks split on (K for k-contiguous operands, M / N otherwise)
@@ -169,9 +191,14 @@ int gemm_common(fg_ctx *ctx, int layout, GemmArgs &a, const char *who,
                a.ldb, a.ldc);
     FG_HIP(hipSetDevice(ctx->device));
     if (a.K == 0) a.A = a.B;  // loads are all masked; K=0 yields the epilogue of zero
-    bool vec, pipe, ktail;
+    bool skinny, vec, pipe, ktail;
     int cfg, splits;
-    plan_gemm(ctx, layout, a, vec, pipe, ktail, cfg, splits, pro);
+    plan_gemm(ctx, layout, a, skinny, vec, pipe, ktail, cfg, splits, pro);
+    if (skinny) {
+        fg::gemm::launch_skinny(a, layout, ctx->stream);
+        FG_LAUNCH_CHECK(who);
+        return FG_OK;
+    }
     switch (layout) {
         case FG_NN: fg::gemm::launch_nn(a, vec, pipe, ktail, cfg, ctx->stream); break;
         case FG_NT: fg::gemm::launch_nt(a, vec, pipe, ktail, cfg, pro, ctx->stream); break;
@@ -204,9 +231,9 @@ int gemm_f32_dispatches(fg_ctx *ctx, int layout, int M, int N, int K, const void
     a.ldb = ldb;
     a.colsum = colsum ? reinterpret_cast<float *>(1) : nullptr;  // only tested for null
     if (K == 0) a.A = a.B;
-    bool vec, pipe, ktail;
+    bool skinny, vec, pipe, ktail;
     int cfg, splits;
-    plan_gemm(ctx, layout, a, vec, pipe, ktail, cfg, splits);
+    plan_gemm(ctx, layout, a, skinny, vec, pipe, ktail, cfg, splits);
     return splits > 1 ? 2 : 1;
 }
 }  // namespace fg

@@ -352,62 +352,90 @@ __global__ __launch_bounds__(kNT) void softmax_rows_h4(const uint16_t *__restric
     }
 }
 
-// Small problems in one workgroup (R*C <= kSmallElems, C <= kSmallCols): one
-// row per thread (rows t, t + 256, ...), so softmax + CE and the mean of the
-// row losses take a single launch; the mean sums the rows in a fixed order
-// (each thread's rows in order, then a fixed tree over the threads, in
-// double).  The same outputs, conventions (argmax = first maximum, NaN loss
-// for a label outside [0, C)) and element-type handling as the row kernels;
-// `probs` receives the softmax itself.
+// Small problems in one workgroup (R <= kSmallRows, C <= kSmallCols): one
+// wave per row (rows w, w + 16, ... for wave w of 16), a lane per column, so
+// softmax + CE and the mean of the row losses take a single launch.  Max,
+// argmax and the sum of exponentials are 64-lane shuffle trees; the mean sums
+// each wave's rows in order (lane 0, double), then the waves in order.  The
+// same outputs, conventions (argmax = first maximum, NaN loss for a label
+// outside [0, C)) and element-type handling as the row kernels; `probs`
+// receives the softmax itself.  A wave loads kSmallBatch rows (and labels)
+// at once and takes the label's logit from the lane holding it, so c1's
+// 64 x 10 loss is one memory round trip.
 constexpr int kSmallCols = 64;
-constexpr int64_t kSmallElems = 65536;
+constexpr int kSmallRows = 1024;
+constexpr int kSmallNT = 1024;
+constexpr int kSmallWaves = kSmallNT / 64;
+constexpr int kSmallBatch = 4;
+bool small_case(int R, int C) { return C <= kSmallCols && R <= kSmallRows; }
 
-__global__ __launch_bounds__(kNT) void softmax_ce_small(
+template <int DT>
+__device__ __forceinline__ float small_load(const void *p, uint64_t i) {
+    if constexpr (DT == fg::kF32) return static_cast<const float *>(p)[i];
+    else return fg::h16_to_f(DT, static_cast<const uint16_t *>(p)[i]);
+}
+template <int DT>
+__device__ __forceinline__ void small_store(void *p, uint64_t i, float v) {
+    if constexpr (DT == fg::kF32) static_cast<float *>(p)[i] = v;
+    else static_cast<uint16_t *>(p)[i] = fg::f_to_h16(DT, v);
+}
+
+template <int DT>
+__global__ __launch_bounds__(kSmallNT) void softmax_ce_small(
     const void *__restrict__ x, int ldx, const uint32_t *__restrict__ labels, int R, int C,
     float scale, float *__restrict__ row_loss, void *__restrict__ out, int ldo,
-    uint32_t *__restrict__ argmax, void *__restrict__ probs, int ldp, float *__restrict__ mean,
-    int dt) {
-    __shared__ double sh[kNT];
-    double acc = 0.0;
-    for (int r = threadIdx.x; r < R; r += kNT) {
-        const uint64_t xb = (uint64_t)r * ldx;
-        float m = -INFINITY;
-        int am = 0;
-        for (int c = 0; c < C; ++c) {
-            const float v = fg::load_as_f(x, dt, xb + c);
-            if (v > m) {
-                m = v;
-                am = c;
+    uint32_t *__restrict__ argmax, void *__restrict__ probs, int ldp, float *__restrict__ mean) {
+    __shared__ double sh[kSmallWaves];
+    const int c = threadIdx.x & 63, w = threadIdx.x >> 6;
+    double acc = 0.0;  // this wave's row losses, in row order
+    // kSmallBatch rows per pass: their loads are all issued before any use.
+    for (int r0 = w; r0 < R; r0 += kSmallWaves * kSmallBatch) {
+        float v[kSmallBatch];
+        uint32_t t[kSmallBatch];
+#pragma unroll
+        for (int j = 0; j < kSmallBatch; ++j) {
+            const int r = r0 + j * kSmallWaves;
+            v[j] = (r < R && c < C) ? small_load<DT>(x, (uint64_t)r * ldx + c) : -INFINITY;
+            t[j] = (r < R && labels) ? labels[r] : 0u;
+        }
+#pragma unroll
+        for (int j = 0; j < kSmallBatch; ++j) {
+            const int r = r0 + j * kSmallWaves;
+            if (r >= R) break;
+            float m = v[j];
+            int am = c < C ? c : C;
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1)
+                argmax_combine(m, am, __shfl_xor(m, o), __shfl_xor(am, o));
+            const float e = c < C ? expf(v[j] - m) : 0.0f;
+            float s = e;
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+            if (argmax && c == 0) argmax[r] = (uint32_t)am;
+            if (row_loss || mean) {
+                // The label's logit from the lane that holds it.
+                const float xt = __shfl(v[j], (int)(t[j] & 63u));
+                const float l = (t[j] < (uint32_t)C) ? (m + logf(s)) - xt : __builtin_nanf("");
+                if (row_loss && c == 0) row_loss[r] = l;
+                acc += (double)l;
             }
-        }
-        float s = 0.0f;
-        for (int c = 0; c < C; ++c) s += expf(fg::load_as_f(x, dt, xb + c) - m);
-        if (argmax) argmax[r] = (uint32_t)am;
-        if (row_loss || mean) {
-            const uint32_t t = labels ? labels[r] : 0u;
-            const float l = (t < (uint32_t)C) ? (m + logf(s)) - fg::load_as_f(x, dt, xb + t)
-                                              : __builtin_nanf("");
-            if (row_loss) row_loss[r] = l;
-            acc += (double)l;
-        }
-        if (out || probs) {
-            const float inv = 1.0f / s;
-            const int t = labels ? (int)labels[r] : -1;
-            for (int c = 0; c < C; ++c) {
-                const float p = expf(fg::load_as_f(x, dt, xb + c) - m) * inv;
-                if (out) fg::store_from_f(out, dt, (uint64_t)r * ldo + c, scale * (c == t ? p - 1.0f : p));
-                if (probs) fg::store_from_f(probs, dt, (uint64_t)r * ldp + c, p);
+            if ((out || probs) && c < C) {
+                const float pv = e * (1.0f / s);
+                if (out)
+                    small_store<DT>(out, (uint64_t)r * ldo + c,
+                                    scale * (labels && (uint32_t)c == t[j] ? pv - 1.0f : pv));
+                if (probs) small_store<DT>(probs, (uint64_t)r * ldp + c, pv);
             }
         }
     }
     if (!mean) return;
-    sh[threadIdx.x] = acc;
+    if (c == 0) sh[w] = acc;
     __syncthreads();
-    for (int o = kNT / 2; o > 0; o >>= 1) {
-        if ((int)threadIdx.x < o) sh[threadIdx.x] += sh[threadIdx.x + o];
-        __syncthreads();
+    if (threadIdx.x == 0) {
+        double tot = sh[0];
+        for (int k = 1; k < kSmallWaves; ++k) tot += sh[k];
+        mean[0] = (float)(tot / (double)R);
     }
-    if (threadIdx.x == 0) mean[0] = (float)(sh[0] / (double)R);
 }
 
 // mean[0] = sum(vals[0..n)) / n in a fixed order (one block).
@@ -453,9 +481,17 @@ int launch_rows(fg_ctx *ctx, int dt, const void *x, int ldx, const uint32_t *lab
                 bool *mean_done = nullptr) {
     hipStream_t st = ctx->stream;
     if (mean_done) *mean_done = false;
-    if (C <= kSmallCols && (int64_t)R * C <= kSmallElems) {
-        softmax_ce_small<<<1, kNT, 0, st>>>(x, ldx, labels, R, C, scale, row_loss, out, ldo,
-                                            argmax, probs, ldp, mean, dt);
+    if (small_case(R, C)) {
+#define FG_SMALL_LAUNCH(DT)                                                                  \
+    softmax_ce_small<DT><<<1, kSmallNT, 0, st>>>(x, ldx, labels, R, C, scale, row_loss, out, ldo, \
+                                            argmax, probs, ldp, mean)
+        if (dt == fg::kF32)
+            FG_SMALL_LAUNCH(fg::kF32);
+        else if (dt == fg::kBF16)
+            FG_SMALL_LAUNCH(fg::kBF16);
+        else
+            FG_SMALL_LAUNCH(fg::kF16);
+#undef FG_SMALL_LAUNCH
         FG_LAUNCH_CHECK("softmax_ce_small");
         if (mean_done) *mean_done = mean != nullptr;
         return FG_OK;
@@ -516,7 +552,7 @@ int launch_rows(fg_ctx *ctx, int dt, const void *x, int ldx, const uint32_t *lab
 
 namespace fg {
 int softmax_ce_dispatches(int R, int C, bool mean) {
-    const bool small = C <= kSmallCols && (int64_t)R * C <= kSmallElems;
+    const bool small = small_case(R, C);
     return (mean && !small) ? 2 : 1;
 }
 
@@ -534,7 +570,7 @@ int softmax_ce_ex(fg_ctx *ctx, int dtype, const void *d_logits, int ldx, const u
                "fg_softmax_ce: logits and labels are required");
     if (R == 0) return FG_OK;
     FG_HIP(hipSetDevice(ctx->device));
-    const bool small = C <= kSmallCols && (int64_t)R * C <= kSmallElems;
+    const bool small = small_case(R, C);
     float *row_loss = d_row_loss;
     if (!row_loss && d_mean_loss && !small) {
         row_loss = (float *)fg::workspace(ctx, (uint64_t)R * sizeof(float));

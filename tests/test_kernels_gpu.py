@@ -386,7 +386,7 @@ def test_gemm_pipe_strided_accumulate(gpu_ctx, layout, shape):
     # (layout, M, N, K, mode, act, accumulate): outputs of a few tiles with
     # long K, which split K over workgroups when the workspace holds the slots
     (O.NN, 64, 256, 784, "fwd", O.ACT_RELU, False),   # c1 layer 1 (4 tiles)
-    (O.NN, 64, 10, 256, "fwd", O.ACT_NONE, False),    # c1 layer 2 (N = 10: element loads)
+    (O.NN, 64, 10, 1024, "fwd", O.ACT_NONE, False),   # N = 10 past the skinny kernel's K
     (O.NT, 64, 784, 256, "bwd", O.ACT_NONE, False),   # c1 dX
     (O.NN, 100, 200, 3000, "fwd", O.ACT_GELU, False),  # edge tiles, K off the tile depth
     (O.NT, 96, 128, 4096, "bwd", O.ACT_GELU, False),   # act' of a saved Zs
@@ -497,6 +497,55 @@ def test_gemm_dw_fused_bias_grad(gpu_ctx, shape):
     assert normwise_rel(host(db), 2 * refb.astype(np.float64)) < 1e-5
 
 
+SKINNY = [(64, 10, 256), (1, 1, 1), (130, 16, 255), (200, 3, 17), (64, 16, 1), (257, 10, 64)]
+
+
+@pytest.mark.parametrize("layout", [O.NN, O.NT, O.TN], ids=["NN", "NT", "TN"])
+@pytest.mark.parametrize("shape", SKINNY, ids=lambda s: "x".join(map(str, s)))
+def test_gemm_skinny_parity(gpu_ctx, layout, shape):
+    """Shapes with N <= 16 and K <= 256 (the second layer and head gradients
+    of a small MLP) take the one-round-trip kernel of k_gemm_skinny.hip.
+    Against the oracle: the forward epilogue (bias + GELU, Z stored), bias
+    placement exactly (A = 0 gives Z = bias), the act' backward epilogue,
+    accumulate, and for TN the fused column sums, plain and accumulated.  M
+    up to five 64-row workgroups, N from 1 to 16, K from 1 to 256."""
+    M, N, K = shape
+    note(f"gemm skinny layout={layout} M={M} N={N} K={K}")
+    rng = np.random.default_rng(M * 5 + N * 11 + K + layout)
+    A = rng.standard_normal((M, K)).astype(f32)
+    B = rng.standard_normal((K, N)).astype(f32)
+    bias = (0.1 * rng.standard_normal(N)).astype(f32)
+    tol = 1e-5 * math.sqrt(K)
+    C, Z = run_gemm(gpu_ctx, layout, A, B, bias, O.ACT_GELU)
+    Zr, Hr = O.bias_act(O.gemm(O.NN, A, B), bias, O.ACT_GELU)
+    assert normwise_rel(Z, Zr) < tol
+    assert normwise_rel(C, Hr) < tol
+    C0, Z0 = run_gemm(gpu_ctx, layout, np.zeros_like(A), B, bias, O.ACT_RELU)
+    assert np.array_equal(Z0, np.tile(bias, (M, 1)))
+    assert np.array_equal(C0, np.tile(np.maximum(bias, 0), (M, 1)))
+    As, Bs = storage(layout, A, B)
+    Zs = rng.standard_normal((M, N)).astype(f32)
+    dC = empty((M, N))
+    gpu_ctx.gemm_bwd(layout, M, N, K, dev(As), As.shape[1], dev(Bs), Bs.shape[1], dC, N,
+                     act=O.ACT_GELU, Zs=dev(Zs), ldzs=N)
+    assert normwise_rel(host(dC), O.act_bwd(O.ACT_GELU, O.gemm(O.NN, A, B), Zs)) < tol
+    Cin = rng.standard_normal((M, N)).astype(f32)
+    dC = dev(Cin)
+    gpu_ctx.gemm(layout, M, N, K, dev(As), As.shape[1], dev(Bs), Bs.shape[1], dC, N,
+                 accumulate=True)
+    assert normwise_rel(host(dC), Cin + O.gemm(O.NN, A, B)) < tol
+    if layout == O.TN:
+        # dW = X^T.dZ with dbias = column sums of dZ: here X = As ([K][M]), dZ = Bs.
+        C, db = empty((M, N)), empty((N,))
+        gpu_ctx.gemm_dw(M, N, K, dev(As), M, dev(Bs), N, C, N, colsum=db)
+        refb = O.bias_grad(Bs)
+        assert normwise_rel(host(C), O.gemm(O.TN, As, Bs)) < tol
+        assert normwise_rel(host(db), refb) < 1e-5
+        gpu_ctx.gemm_dw(M, N, K, dev(As), M, dev(Bs), N, C, N, accumulate=True, colsum=db,
+                        colsum_accumulate=True)
+        assert normwise_rel(host(db), 2 * refb.astype(np.float64)) < 1e-5
+
+
 @pytest.mark.parametrize("n", [1, 7, 4096, 1000003])
 def test_act_bwd_parity(gpu_ctx, n):
     note(f"act_bwd n={n}")
@@ -560,8 +609,9 @@ def test_softmax_ce_fixture(gpu_ctx):
     check_softmax_ce(gpu_ctx, g["x"], g["labels"])
 
 
-@pytest.mark.parametrize("shape", [(64, 10), (7, 1024), (2048, 1000), (256, 32000), (16, 40000),
-                                   (33, 4100), (5, 8192)], ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("shape", [(64, 10), (1024, 64), (1025, 10), (5, 1), (7, 1024), (2048, 1000),
+                                   (256, 32000), (16, 40000), (33, 4100), (5, 8192)],
+                         ids=lambda s: "x".join(map(str, s)))
 def test_softmax_ce_parity(gpu_ctx, shape):
     R, C = shape
     note(f"softmax_ce R={R} C={C}")
