@@ -17,6 +17,7 @@ import fails loudly when the library has not been built.
 from __future__ import annotations
 
 import ctypes
+import weakref
 from typing import Optional, Sequence
 
 import numpy as np
@@ -60,6 +61,13 @@ class Context:
         self.arch = arch.value.decode()
         self.flags = flags.value
         self.cu_count = cus.value
+        # Plans and tensor lists made on this context (they keep a pointer to
+        # it): closed before it, whatever order the garbage collector picks.
+        self._dependents = weakref.WeakSet()
+
+    def adopt(self, obj) -> None:
+        """Close `obj` (anything with close()) before this context closes."""
+        self._dependents.add(obj)
 
     @property
     def stream(self) -> int:
@@ -80,6 +88,8 @@ class Context:
 
     def close(self) -> None:
         if self.handle:
+            for d in list(getattr(self, "_dependents", ())):
+                d.close()
             call("fg_ctx_destroy", self.handle)
             self.handle = None
 
@@ -211,6 +221,7 @@ class MultiTensor:
         call("fg_mt_create_x", ctx.handle, n, D, P, G, Mv, Vv, S, ctypes.byref(h))
         self.ctx = ctx
         self.handle = h
+        ctx.adopt(self)
 
     def sgd(self, lr: float, zero_grad: bool = True) -> None:
         call("fg_sgd_step", self.ctx.handle, self.handle, lr, int(zero_grad))

@@ -30,6 +30,7 @@ SOURCES = [
     "k_gemm_nt_pro.hip",
     "k_gemm_tn_pro.hip",
     "k_gemm_skinny.hip",
+    "k_gemm_pair.hip",
     "k_gemm16.hip",
     "k_gemm16_bf16.hip",
     "k_gemm16_f16.hip",

@@ -126,12 +126,12 @@ __device__ __forceinline__ f32x4 pro_scale(f32x4 v, f32x4 z) {
     return v;
 }
 
-// The view of a split-K workgroup: its K slice of A and B, its raw-product
-// slot as C, no epilogue.
+// The view of split-K workgroup row s: its K slice of A and B, its
+// raw-product slot as C, no epilogue.
 template <bool AK, bool BNC, int PRO>
-__device__ __forceinline__ void split_k_view(GemmArgs &p) {
+__device__ __forceinline__ void split_k_view(GemmArgs &p, int s) {
     if (p.ksplit <= 0) return;
-    const int s = blockIdx.y, kb = s * p.ksplit;
+    const int kb = s * p.ksplit;
     p.A += AK ? (size_t)kb : (size_t)kb * p.lda;
     p.B += BNC ? (size_t)kb * p.ldb : (size_t)kb;
     if constexpr (pro_on_a(PRO)) p.Pz += AK ? (size_t)kb : (size_t)kb * p.ldp;
@@ -398,9 +398,12 @@ __device__ __forceinline__ void store_tile(const GemmArgs &p, const f32x16 (&acc
     }
 }
 
+// The kernel bodies take their workgroup's coordinates (bx: output tile,
+// by: K slice) as arguments, so that a launch of two independent GEMMs
+// (gemm_pair, k_gemm_pair.hip) can run either body in a workgroup.
 template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC, bool VEC, int PRO>
-__global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_mfma(GemmArgs p) {
-    split_k_view<AK, BNC, PRO>(p);
+__device__ __forceinline__ void gemm_f32_mfma_body(GemmArgs p, int bx, int by) {
+    split_k_view<AK, BNC, PRO>(p, by);
     constexpr int NT = 64 * WGM * WGN;
     static_assert(WGM * WGN == 4 || WGM * WGN == 8, "4 or 8 waves per workgroup");
     constexpr int WTM = BM / WGM, WTN = BN / WGN;
@@ -411,7 +414,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_mfma(GemmArgs p) {
     __shared__ __attribute__((aligned(16))) float lds[L::total];
 
     int tile_m, tile_n;
-    tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tile_m, tile_n);
+    tile_of(bx, p.tiles_m, p.tiles_n, tile_m, tile_n);
     const int m0 = tile_m * BM, n0 = tile_n * BN;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int l32 = lane & 31, h = lane >> 5;
@@ -544,12 +547,17 @@ __device__ __forceinline__ int swz_k(int row) {
 }
 __device__ __forceinline__ int swz_r(int k) { return ((k >> 3) & 1) * 8; }
 
+template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC, bool VEC, int PRO>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_mfma(GemmArgs p) {
+    gemm_f32_mfma_body<BM, BN, BK, WGM, WGN, AK, BNC, VEC, PRO>(p, blockIdx.x, blockIdx.y);
+}
+
 // KT: K need not be a multiple of BK (staged tiles, no prologue): the last
 // tile's chunks past K are loaded from a clamped address and zeroed before
 // their LDS write, so they add nothing to any output.
 template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC, int PRO, bool KT>
-__global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_pipe(GemmArgs p) {
-    split_k_view<AK, BNC, PRO>(p);
+__device__ __forceinline__ void gemm_f32_pipe_body(GemmArgs p, int bx, int by) {
+    split_k_view<AK, BNC, PRO>(p, by);
     constexpr int NW = WGM * WGN;
     constexpr int WTM = BM / WGM, WTN = BN / WGN;
     constexpr int TM = WTM / 32, TN = WTN / 32;
@@ -572,7 +580,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_pipe(GemmArgs p) {
     __shared__ __attribute__((aligned(16))) float lds[kLds];
 
     int tile_m, tile_n;
-    tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tile_m, tile_n);
+    tile_of(bx, p.tiles_m, p.tiles_n, tile_m, tile_n);
     const int m0 = tile_m * BM, n0 = tile_n * BN;
     // The wave index as a uniform (scalar) value: it selects each wave's LDS
     // destinations, which the compiler would otherwise treat as varying.
@@ -971,6 +979,11 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_pipe(GemmArgs p) {
     store_tile<TM, TN, WTN, NW, IA, IB>(p, acc, lds, m0 + wm0, n0 + wn0, wave, lane);
 }
 
+template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC, int PRO, bool KT>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_pipe(GemmArgs p) {
+    gemm_f32_pipe_body<BM, BN, BK, WGM, WGN, AK, BNC, PRO, KT>(p, blockIdx.x, blockIdx.y);
+}
+
 template <int BM, int BN, int WGM, int WGN, int BK, bool AK, bool BNC, int PRO, bool KT = false>
 void launch_pipe(const GemmArgs &a0, hipStream_t st) {
     GemmArgs a = a0;
@@ -1090,6 +1103,15 @@ void launch_tn_pro(const GemmArgs &a, bool vec, bool pipe, int cfg, int pro, hip
 constexpr int kSkinnyN = 16;
 constexpr int kSkinnyK = 256;
 void launch_skinny(const GemmArgs &a, int layout, hipStream_t st);
+
+// A layer's dW (TN, GEMM 1) and dX (NT, GEMM 2) in one launch
+// (k_gemm_pair.hip): kinds of the kernels they would take alone, which must
+// be one of these 256-thread ones.  x1 / x2: output tiles (skinny: its
+// workgroups), n1 / n2: workgroups (tiles x K slices).  tiles_m / tiles_n
+// of each GemmArgs are set by the caller.
+enum : int { kPairSkinny = 0, kPairElem = 1, kPairPipe = 2 };
+void launch_pair(int k1, int k2, const GemmArgs &a1, const GemmArgs &a2, int x1, int n1, int x2,
+                 int n2, hipStream_t st);
 
 }  // namespace gemm
 }  // namespace fg

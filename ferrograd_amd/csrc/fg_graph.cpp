@@ -241,6 +241,11 @@ struct Launch {
     // step leaves it out and the loss launch writes its output (sProbs).
     bool elidable = false;
     int sProbs = kNone;
+    // A weight-gradient GEMM (fp32, TN) followed by the data-gradient GEMM
+    // of the same layer (NT): the two read the same dZ and write different
+    // gradients, so they go to fg::gemm_dw_dx_f32 together, which puts them
+    // in one launch when both take small kernels.
+    bool pair_next = false;
     std::string desc;
     Launch() {
         std::fill(src_slot, src_slot + fg::kEltMaxSrc, kNone);
@@ -881,7 +886,9 @@ int lower_backward(fg_plan &P, bool fused, std::vector<Launch> &out) {
                 ginit[G.bias_src] = 1;
                 out.push_back(L);
             }
+            int idx_db = kNone;
             if (P.needs_grad[b]) {  // dB = A^T dZ
+                idx_db = (int)out.size();
                 Launch L;
                 L.kind = LK_GEMM;
                 L.dtype = P.dtype[G.mm];
@@ -941,6 +948,10 @@ int lower_backward(fg_plan &P, bool fused, std::vector<Launch> &out) {
                     ginit[a] = 1;
                     L.desc = "backward gemm NT " + dims_str(M, K, N) + " -> grad of node " +
                              std::to_string(a);
+                }
+                if (idx_db != kNone && a != b && L.dtype == FG_DTYPE_F32) {
+                    out[idx_db].pair_next = true;
+                    out[idx_db].desc += " [with the next]";
                 }
                 out.push_back(L);
             }
@@ -1075,9 +1086,27 @@ int check_launch(const fg_plan &P, const Launch &L) {
 // optimiser), so the final forward softmax is left to the loss launch.
 int run(fg_plan &P, const std::vector<Launch> &list, bool step = false) {
     fg_ctx *ctx = &P.wctx;
+    bool skip_next = false;  // the launch just run as the second of a pair
     for (const Launch &L : list) {
         int rc = FG_OK;
+        if (skip_next) {
+            skip_next = false;
+            continue;
+        }
         if (step && L.elidable) continue;
+        if (L.pair_next && &L + 1 < list.data() + list.size()) {
+            const Launch &X = *(&L + 1);  // the same layer's dX (NT, act')
+            rc = fg::gemm_dw_dx_f32(ctx, L.M, L.N, L.K, (const float *)P.ptr(L.sA), L.lda,
+                                    (const float *)P.ptr(L.sB), L.ldb, (float *)P.ptr(L.sC),
+                                    L.ldc, L.accumulate, (float *)P.ptr(L.sExtra), L.accumulate2,
+                                    X.M, X.N, X.K, (const float *)P.ptr(X.sA), X.lda,
+                                    (const float *)P.ptr(X.sB), X.ldb, X.act,
+                                    (const float *)P.ptr(X.sZ), X.ldz, (float *)P.ptr(X.sC),
+                                    X.ldc, X.accumulate);
+            if (rc != FG_OK) return rc;
+            skip_next = true;
+            continue;
+        }
         switch (L.kind) {
             case LK_GEMM:
                 if (L.sExtra != kNone && L.dtype == FG_DTYPE_F32)  // dW with the fused dbias (TN)
@@ -1939,9 +1968,17 @@ FG_API int fg_plan_describe(const fg_plan *p, char *buf, size_t len, size_t *nee
     // is preceded by its step-counter advance.
     auto kernels = [&](const std::vector<Launch> &v) {
         int n = 0;
-        for (const Launch &L : v) {
+        for (size_t i = 0; i < v.size(); ++i) {
+            const Launch &L = v[i];
             if (L.elidable) continue;
-            if (L.kind == LK_SMCE)
+            if (L.pair_next && i + 1 < v.size()) {
+                const Launch &X = v[i + 1];
+                n += wc ? fg::gemm_dw_dx_dispatches(wc, L.M, L.N, L.K, p->ptr(L.sA), L.lda,
+                                                    p->ptr(L.sB), L.ldb, X.M, X.N, X.K,
+                                                    p->ptr(X.sA), X.lda, p->ptr(X.sB), X.ldb)
+                        : gemm_dispatches(L) + gemm_dispatches(X);
+                ++i;
+            } else if (L.kind == LK_SMCE)
                 n += fg::softmax_ce_dispatches(L.M, L.N, L.sBias != kNone);
             else if (L.kind == LK_BIAS_GRAD)
                 n += 2;

@@ -84,6 +84,16 @@ int launch_eltwise(fg_ctx *ctx, const EltProgram &p);
 // split: the slices, then the summing epilogue), for plan descriptions.
 int gemm_f32_dispatches(fg_ctx *ctx, int layout, int M, int N, int K, const void *A, int lda,
                         const void *B, int ldb, bool colsum);
+// A layer's dW (TN, fused column sums) and dX (NT, act'(Zs)) GEMMs, in one
+// launch when both take small kernels (k_gemm.hip), and its dispatch count.
+int gemm_dw_dx_f32(fg_ctx *ctx, int M1, int N1, int K1, const float *A1, int lda1,
+                   const float *B1, int ldb1, float *C1, int ldc1, int acc1, float *colsum,
+                   int colsum_acc, int M2, int N2, int K2, const float *A2, int lda2,
+                   const float *B2, int ldb2, int act, const float *Zs, int ldzs, float *C2,
+                   int ldc2, int acc2);
+int gemm_dw_dx_dispatches(fg_ctx *ctx, int M1, int N1, int K1, const void *A1, int lda1,
+                          const void *B1, int ldb1, int M2, int N2, int K2, const void *A2,
+                          int lda2, const void *B2, int ldb2);
 }  // namespace fg
 
 #define FG_HIP(call)                                                     \

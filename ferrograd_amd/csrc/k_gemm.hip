@@ -8,6 +8,7 @@
 
 #include "fg_bias_grad.h"
 #include "fg_gemm_kernel.h"
+#include "fg_gemm_skinny.h"
 #include "fg_half.h"
 #include "fg_internal.h"
 
@@ -173,14 +174,30 @@ void plan_gemm(fg_ctx *ctx, int layout, GemmArgs &a, bool &skinny, bool &vec, bo
     splits = plan_split_k(ctx, a, cfg, vec);
 }
 
-int gemm_common(fg_ctx *ctx, int layout, GemmArgs &a, const char *who,
-                int pro = fg::gemm::kProNone) {
+// One GEMM call, validated and planned (gemm_prepare), then launched
+// (gemm_launch): alone, or beside another in one launch (fg::gemm_dw_dx_f32).
+struct Planned {
+    GemmArgs a{};
+    int layout = FG_NN, pro = fg::gemm::kProNone, cfg = 0, splits = 1;
+    bool skinny = false, vec = false, pipe = false, ktail = false;
+    bool empty = false;  // M == 0 or N == 0: nothing to launch
+};
+
+int gemm_prepare(fg_ctx *ctx, int layout, const GemmArgs &a0, const char *who, int pro,
+                 Planned &P) {
     FG_REQUIRE(ctx, FG_ERR_INVALID_ARGUMENT, "%s: ctx is NULL", who);
     FG_REQUIRE(layout >= FG_NN && layout <= FG_TN, FG_ERR_INVALID_ARGUMENT, "%s: bad layout %d",
                who, layout);
+    GemmArgs &a = P.a;
+    a = a0;
+    P.layout = layout;
+    P.pro = pro;
     FG_REQUIRE(a.M >= 0 && a.N >= 0 && a.K >= 0, FG_ERR_SHAPE, "%s: negative dimension", who);
     FG_REQUIRE(a.act >= 0 && a.act <= 2, FG_ERR_INVALID_ARGUMENT, "%s: bad act %d", who, a.act);
-    if (a.M == 0 || a.N == 0) return FG_OK;
+    if (a.M == 0 || a.N == 0) {
+        P.empty = true;
+        return FG_OK;
+    }
     FG_REQUIRE(a.A && a.B && a.C, FG_ERR_INVALID_ARGUMENT, "%s: NULL operand", who);
     // Leading dimensions: A is [M][K] (NN/NT) or [K][M] (TN); B is [K][N]
     // (NN/TN) or [N][K] (NT); C is [M][N].
@@ -191,28 +208,66 @@ int gemm_common(fg_ctx *ctx, int layout, GemmArgs &a, const char *who,
                a.ldb, a.ldc);
     FG_HIP(hipSetDevice(ctx->device));
     if (a.K == 0) a.A = a.B;  // loads are all masked; K=0 yields the epilogue of zero
-    bool skinny, vec, pipe, ktail;
-    int cfg, splits;
-    plan_gemm(ctx, layout, a, skinny, vec, pipe, ktail, cfg, splits, pro);
-    if (skinny) {
-        fg::gemm::launch_skinny(a, layout, ctx->stream);
+    plan_gemm(ctx, layout, a, P.skinny, P.vec, P.pipe, P.ktail, P.cfg, P.splits, pro);
+    return FG_OK;
+}
+
+void launch_reduce(fg_ctx *ctx, const GemmArgs &a, int splits) {
+    const size_t mn = (size_t)a.M * a.N;
+    const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    const int grid = (int)std::min<size_t>((mn + kThreads - 1) / kThreads, 4 * (size_t)cus);
+    splitk_reduce<<<grid, kThreads, 0, ctx->stream>>>(a, splits);
+}
+
+int gemm_launch(fg_ctx *ctx, const Planned &P, const char *who) {
+    if (P.empty) return FG_OK;
+    if (P.skinny) {
+        fg::gemm::launch_skinny(P.a, P.layout, ctx->stream);
         FG_LAUNCH_CHECK(who);
         return FG_OK;
     }
-    switch (layout) {
-        case FG_NN: fg::gemm::launch_nn(a, vec, pipe, ktail, cfg, ctx->stream); break;
-        case FG_NT: fg::gemm::launch_nt(a, vec, pipe, ktail, cfg, pro, ctx->stream); break;
-        default: fg::gemm::launch_tn(a, vec, pipe, ktail, cfg, pro, ctx->stream); break;
+    switch (P.layout) {
+        case FG_NN: fg::gemm::launch_nn(P.a, P.vec, P.pipe, P.ktail, P.cfg, ctx->stream); break;
+        case FG_NT:
+            fg::gemm::launch_nt(P.a, P.vec, P.pipe, P.ktail, P.cfg, P.pro, ctx->stream);
+            break;
+        default: fg::gemm::launch_tn(P.a, P.vec, P.pipe, P.ktail, P.cfg, P.pro, ctx->stream); break;
     }
     FG_LAUNCH_CHECK(who);
-    if (splits > 1) {
-        const size_t mn = (size_t)a.M * a.N;
-        const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
-        const int grid = (int)std::min<size_t>((mn + kThreads - 1) / kThreads, 4 * (size_t)cus);
-        splitk_reduce<<<grid, kThreads, 0, ctx->stream>>>(a, splits);
+    if (P.splits > 1) {
+        launch_reduce(ctx, P.a, P.splits);
         FG_LAUNCH_CHECK(who);
     }
     return FG_OK;
+}
+
+int gemm_common(fg_ctx *ctx, int layout, GemmArgs &a, const char *who,
+                int pro = fg::gemm::kProNone) {
+    Planned P;
+    const int rc = gemm_prepare(ctx, layout, a, who, pro, P);
+    if (rc) return rc;
+    return gemm_launch(ctx, P, who);
+}
+
+// The pair kernel that a planned GEMM would take (-1: it does not pair).
+int pair_kind(const Planned &P) {
+    if (P.empty || P.pro != fg::gemm::kProNone) return -1;
+    if (P.skinny) return fg::gemm::kPairSkinny;
+    if (!P.vec) return fg::gemm::kPairElem;
+    if (P.pipe && !P.ktail && P.cfg == 4) return fg::gemm::kPairPipe;
+    return -1;
+}
+
+// Output tiles x and workgroups n of a paired GEMM (sets its tile counts).
+void pair_grid(Planned &P, int &x, int &n) {
+    if (P.skinny) {
+        x = n = fg::gemm::skinny_workgroups(P.a.M);
+        return;
+    }
+    P.a.tiles_m = (P.a.M + 63) / 64;  // the 64x64 tiles of both pairing kernels
+    P.a.tiles_n = (P.a.N + 63) / 64;
+    x = P.a.tiles_m * P.a.tiles_n;
+    n = x * P.splits;
 }
 
 }  // namespace
@@ -334,6 +389,133 @@ FG_API int fg_gemm_dw_f32(fg_ctx *ctx, int M, int N, int K, const float *d_A, in
     return gemm_dw(ctx, M, N, K, d_A, lda, d_B, ldb, d_C, ldc, accumulate, d_colsum,
                    colsum_accumulate, nullptr, 0, fg::gemm::kProNone, "fg_gemm_dw_f32");
 }
+
+namespace {
+// The arguments of the pair's two GEMMs as the single-GEMM entry points build
+// them: dW (TN) with the column sums, dX (NT) with act'(Zs).
+GemmArgs dw_args(int M, int N, int K, const float *A, int lda, const float *B, int ldb, float *C,
+                 int ldc, int accumulate, float *colsum, int colsum_accumulate) {
+    GemmArgs a{};
+    a.A = A;
+    a.B = B;
+    a.C = C;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.lda = lda;
+    a.ldb = ldb;
+    a.ldc = ldc;
+    a.act = FG_ACT_NONE;
+    a.mode = 0;
+    a.accumulate = accumulate ? 1 : 0;
+    a.colsum = colsum;
+    a.colsum_accumulate = colsum_accumulate ? 1 : 0;
+    return a;
+}
+GemmArgs dx_args(int M, int N, int K, const float *A, int lda, const float *B, int ldb, int act,
+                 const float *Zs, int ldzs, float *C, int ldc, int accumulate) {
+    GemmArgs a{};
+    a.A = A;
+    a.B = B;
+    a.C = C;
+    a.Zs = Zs;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.lda = lda;
+    a.ldb = ldb;
+    a.ldc = ldc;
+    a.ldzs = ldzs;
+    a.act = act;
+    a.mode = 1;
+    a.accumulate = accumulate ? 1 : 0;
+    return a;
+}
+
+// Both pairable: at most one of them splits K (the slices of a split GEMM
+// take the whole workspace).
+bool pairable(const Planned &P1, const Planned &P2) {
+    return pair_kind(P1) >= 0 && pair_kind(P2) >= 0 && (P1.splits == 1 || P2.splits == 1);
+}
+
+// Both validated and planned, and pairable.
+bool plan_pair(fg_ctx *ctx, const GemmArgs &w, const GemmArgs &x, Planned &P1, Planned &P2) {
+    if (gemm_prepare(ctx, FG_TN, w, "fg_gemm_dw_f32", fg::gemm::kProNone, P1) ||
+        gemm_prepare(ctx, FG_NT, x, "fg_gemm_bwd_f32", fg::gemm::kProNone, P2))
+        return false;
+    return pairable(P1, P2);
+}
+
+// The kernel choices alone, for counting dispatches: no validation, no error
+// message, operands not bound yet taken as 16-byte aligned.
+void plan_quiet(fg_ctx *ctx, int layout, const GemmArgs &a0, Planned &P) {
+    P.a = a0;
+    P.layout = layout;
+    const float *aligned = reinterpret_cast<const float *>(256);
+    if (!P.a.A) P.a.A = aligned;
+    if (!P.a.B) P.a.B = aligned;
+    plan_gemm(ctx, layout, P.a, P.skinny, P.vec, P.pipe, P.ktail, P.cfg, P.splits);
+}
+}  // namespace
+
+namespace fg {
+// A layer's weight gradient dW (=|+=) X^T.dZ with dbias (=|+=) the column
+// sums of dZ (as fg_gemm_dw_f32) and its data gradient dX (=|+=)
+// (dZ.W^T) * act'(Zs) (as fg_gemm_bwd_f32, NT): independent GEMMs, one
+// launch when both take small 256-thread kernels, else one after the other.
+// The same results, bit for bit, either way.
+int gemm_dw_dx_f32(fg_ctx *ctx, int M1, int N1, int K1, const float *A1, int lda1,
+                   const float *B1, int ldb1, float *C1, int ldc1, int acc1, float *colsum,
+                   int colsum_acc, int M2, int N2, int K2, const float *A2, int lda2,
+                   const float *B2, int ldb2, int act, const float *Zs, int ldzs, float *C2,
+                   int ldc2, int acc2) {
+    auto separate = [&]() {
+        const int rc = fg_gemm_dw_f32(ctx, M1, N1, K1, A1, lda1, B1, ldb1, C1, ldc1, acc1, colsum,
+                                      colsum_acc);
+        if (rc) return rc;
+        return fg_gemm_bwd_f32(ctx, FG_NT, M2, N2, K2, A2, lda2, B2, ldb2, act, Zs, ldzs, C2, ldc2,
+                               acc2);
+    };
+    // Empty shapes (the column-sum fill of an empty reduction) stay separate.
+    if (!ctx || M1 <= 0 || N1 <= 0 || K1 <= 0 || M2 <= 0 || N2 <= 0 || K2 <= 0) return separate();
+    FG_REQUIRE(act == FG_ACT_NONE || (Zs && ldzs >= N2), FG_ERR_INVALID_ARGUMENT,
+               "fg_gemm_bwd_f32: act %d needs Zs with ldzs >= N", act);
+    Planned P1, P2;
+    if (!plan_pair(ctx, dw_args(M1, N1, K1, A1, lda1, B1, ldb1, C1, ldc1, acc1, colsum, colsum_acc),
+                   dx_args(M2, N2, K2, A2, lda2, B2, ldb2, act, Zs, ldzs, C2, ldc2, acc2), P1, P2))
+        return separate();
+    int x1, n1, x2, n2;
+    pair_grid(P1, x1, n1);
+    pair_grid(P2, x2, n2);
+    fg::gemm::launch_pair(pair_kind(P1), pair_kind(P2), P1.a, P2.a, x1, n1, x2, n2, ctx->stream);
+    FG_LAUNCH_CHECK("gemm_dw_dx_f32");
+    for (const Planned *P : {&P1, &P2})
+        if (P->splits > 1) {
+            launch_reduce(ctx, P->a, P->splits);
+            FG_LAUNCH_CHECK("gemm_dw_dx_f32");
+        }
+    return FG_OK;
+}
+
+// Dispatches of gemm_dw_dx_f32 for these shapes: 1 (+1 per split GEMM) when
+// the two pair, else the sum of the two calls'.  No launch.
+int gemm_dw_dx_dispatches(fg_ctx *ctx, int M1, int N1, int K1, const void *A1, int lda1,
+                          const void *B1, int ldb1, int M2, int N2, int K2, const void *A2,
+                          int lda2, const void *B2, int ldb2) {
+    const int sep = gemm_f32_dispatches(ctx, FG_TN, M1, N1, K1, A1, lda1, B1, ldb1, true) +
+                    gemm_f32_dispatches(ctx, FG_NT, M2, N2, K2, A2, lda2, B2, ldb2, false);
+    if (!ctx || M1 <= 0 || N1 <= 0 || K1 <= 0 || M2 <= 0 || N2 <= 0 || K2 <= 0) return sep;
+    // Dummy aligned outputs: only the operands' alignment enters the choice.
+    float *c = reinterpret_cast<float *>(256);
+    Planned P1, P2;
+    plan_quiet(ctx, FG_TN, dw_args(M1, N1, K1, (const float *)A1, lda1, (const float *)B1, ldb1,
+                                   c, N1, 0, c, 0), P1);
+    plan_quiet(ctx, FG_NT, dx_args(M2, N2, K2, (const float *)A2, lda2, (const float *)B2, ldb2,
+                                   FG_ACT_NONE, nullptr, 0, c, N2, 0), P2);
+    if (!pairable(P1, P2)) return sep;
+    return 1 + (P1.splits > 1) + (P2.splits > 1);
+}
+}  // namespace fg
 
 FG_API int fg_linear_bwd_f32(fg_ctx *ctx, int act, int M, int N, int K, const float *d_X,
                              int ldx, const float *d_W, int ldw, const float *d_Zs, int ldzs,

@@ -1,0 +1,78 @@
+// k_gemm_pair.hip -- a layer's two gradient GEMMs in one launch.  dW = X^T.dZ
+// (TN, with the fused bias gradient) and dX = (dZ.W^T) * act'(Z) (NT) read
+// the same dZ and write different tensors, so neither waits for the other.
+// On a latency-bound step (c1: every kernel a few microseconds, dispatches
+// back to back) launching them separately costs one whole dispatch; here the
+// first n1 workgroups run the dW body and the rest the dX body, each exactly
+// as its own kernel would (same tile walk, same K slices, same bits).  Only
+// the small 256-thread kernels pair: the skinny kernel and the 64x64 tiles
+// (element loads or pipelined).
+#include "fg_gemm_skinny.h"
+
+namespace fg {
+namespace gemm {
+namespace {
+
+template <bool AK, bool BNC>
+struct PkSkinny {
+    __device__ static void run(const GemmArgs &p, int bx, int) {
+        gemm_f32_skinny_body<AK, BNC>(p, bx);
+    }
+};
+template <bool AK, bool BNC>
+struct PkElem {  // 64x64, element loads (gemm_f32_mfma, VEC false)
+    __device__ static void run(const GemmArgs &p, int bx, int by) {
+        gemm_f32_mfma_body<64, 64, 16, 2, 2, AK, BNC, false, kProNone>(p, bx, by);
+    }
+};
+template <bool AK, bool BNC>
+struct PkPipe {  // 64x64, pipelined whole K tiles
+    __device__ static void run(const GemmArgs &p, int bx, int by) {
+        gemm_f32_pipe_body<64, 64, 16, 2, 2, AK, BNC, kProNone, false>(p, bx, by);
+    }
+};
+
+// Workgroup w < n1: GEMM 1 at (w % x1, w / x1); else GEMM 2 at
+// (v % x2, v / x2) with v = w - n1 (x: output tiles, the quotient: K slice).
+template <class G1, class G2>
+__global__ __launch_bounds__(256) void gemm_pair(GemmArgs a1, GemmArgs a2, int x1, int n1,
+                                                 int x2) {
+    const int w = blockIdx.x;
+    if (w < n1) {
+        G1::run(a1, w % x1, w / x1);
+    } else {
+        const int v = w - n1;
+        G2::run(a2, v % x2, v / x2);
+    }
+}
+
+template <class G1>
+void launch_with(int k2, const GemmArgs &a1, const GemmArgs &a2, int x1, int n1, int x2, int n2,
+                 hipStream_t st) {
+    const dim3 grid(n1 + n2), block(256);
+    switch (k2) {  // GEMM 2 is the NT data gradient
+        case kPairSkinny:
+            gemm_pair<G1, PkSkinny<true, false>><<<grid, block, 0, st>>>(a1, a2, x1, n1, x2);
+            break;
+        case kPairElem:
+            gemm_pair<G1, PkElem<true, false>><<<grid, block, 0, st>>>(a1, a2, x1, n1, x2);
+            break;
+        default:
+            gemm_pair<G1, PkPipe<true, false>><<<grid, block, 0, st>>>(a1, a2, x1, n1, x2);
+            break;
+    }
+}
+
+}  // namespace
+
+void launch_pair(int k1, int k2, const GemmArgs &a1, const GemmArgs &a2, int x1, int n1, int x2,
+                 int n2, hipStream_t st) {
+    switch (k1) {  // GEMM 1 is the TN weight gradient
+        case kPairSkinny: launch_with<PkSkinny<false, true>>(k2, a1, a2, x1, n1, x2, n2, st); break;
+        case kPairElem: launch_with<PkElem<false, true>>(k2, a1, a2, x1, n1, x2, n2, st); break;
+        default: launch_with<PkPipe<false, true>>(k2, a1, a2, x1, n1, x2, n2, st); break;
+    }
+}
+
+}  // namespace gemm
+}  // namespace fg

@@ -1,151 +1,19 @@
-// k_gemm_skinny.hip -- GEMMs with few output columns and a short K (N <= 16,
-// K <= 256), in every layout: the second layer and the head gradients of a
-// small MLP (c1: 64x10x256 forward, dW = X^T.dZ of 256x10x64 with its bias
-// gradient).  The tiled kernels walk such shapes as a chain of K tiles, one
-// memory round trip each, on a handful of workgroups.  Here a workgroup owns
-// 16 output rows and every column: it issues all the loads of its A row panel
-// and of the whole B panel at once (one round trip), stages them in LDS, and
-// sums from there with no K loop of loads, 16 k-groups of at most 16 k in
-// parallel.  Deterministic: each output is the 16 group sums (ascending k)
-// added in group order.
-#include "fg_gemm_kernel.h"
+// k_gemm_skinny.hip -- launches of the skinny GEMM kernel (fg_gemm_skinny.h).
+#include "fg_gemm_skinny.h"
 
 namespace fg {
 namespace gemm {
 namespace {
 
-constexpr int kSkRows = 16;              // output rows per workgroup
-constexpr int kSkThreads = 256;
-constexpr int kSkGroups = kSkThreads / kSkRows;              // K groups: 16
-constexpr int kAPerThread = kSkRows * kSkinnyK / kSkThreads;  // 16
-constexpr int kBPerThread = kSkinnyK * kSkinnyN / kSkThreads;  // 16
-constexpr int kAStride = kSkRows + 1;    // As[k][row], padded
-static_assert(kSkinnyN == 16 && kSkinnyK == kSkThreads && kSkGroups == 16,
-              "thread layouts below assume these");
-
 template <bool AK, bool BNC>
 __global__ __launch_bounds__(kSkThreads) void gemm_f32_skinny(GemmArgs p) {
-    __shared__ float As[kSkinnyK * kAStride];
-    __shared__ __attribute__((aligned(16))) float Bs[kSkinnyK * kSkinnyN];
-    __shared__ float red[kSkGroups * kSkinnyN * kSkRows];
-    const int t = threadIdx.x;
-    const int m0 = blockIdx.x * kSkRows;
-
-    // All loads first (registers), then the LDS stores: one round trip.
-    float ra[kAPerThread], rb[kBPerThread];
-    if constexpr (AK) {
-        // A[m][k]: thread t holds column k = t of the 16 rows (coalesced in k).
-#pragma unroll
-        for (int i = 0; i < kAPerThread; ++i)
-            ra[i] = (t < p.K && m0 + i < p.M) ? p.A[(size_t)(m0 + i) * p.lda + t] : 0.0f;
-    } else {
-        // A[k][m]: thread t holds row t % 16 at k = t / 16 + 16i (coalesced in m).
-        const int r = t % kSkRows, k0 = t / kSkRows;
-#pragma unroll
-        for (int i = 0; i < kAPerThread; ++i) {
-            const int k = k0 + kSkGroups * i;
-            ra[i] = (k < p.K && m0 + r < p.M) ? p.A[(size_t)k * p.lda + m0 + r] : 0.0f;
-        }
-    }
-    if constexpr (BNC) {
-        // B[k][n]: thread t holds column n = t % 16 at k = t / 16 + 16i.
-        const int n = t % kSkinnyN, k0 = t / kSkinnyN;
-#pragma unroll
-        for (int i = 0; i < kBPerThread; ++i) {
-            const int k = k0 + kSkinnyN * i;
-            rb[i] = (k < p.K && n < p.N) ? p.B[(size_t)k * p.ldb + n] : 0.0f;
-        }
-    } else {
-        // B[n][k]: thread t holds k = t of the 16 columns (coalesced in k).
-#pragma unroll
-        for (int n = 0; n < kBPerThread; ++n)
-            rb[n] = (t < p.K && n < p.N) ? p.B[(size_t)n * p.ldb + t] : 0.0f;
-    }
-    if constexpr (AK) {
-#pragma unroll
-        for (int i = 0; i < kAPerThread; ++i) As[t * kAStride + i] = ra[i];
-    } else {
-        const int r = t % kSkRows, k0 = t / kSkRows;
-#pragma unroll
-        for (int i = 0; i < kAPerThread; ++i) As[(k0 + kSkGroups * i) * kAStride + r] = ra[i];
-    }
-    if constexpr (BNC) {
-        const int n = t % kSkinnyN, k0 = t / kSkinnyN;
-#pragma unroll
-        for (int i = 0; i < kBPerThread; ++i) Bs[(k0 + kSkinnyN * i) * kSkinnyN + n] = rb[i];
-    } else {
-#pragma unroll
-        for (int n = 0; n < kBPerThread; ++n) Bs[t * kSkinnyN + n] = rb[n];
-    }
-    __syncthreads();
-
-    // Thread (r, g): row r over the g-th K group (at most 16 k), all 16
-    // columns.
-    {
-        const int r = t % kSkRows, g = t / kSkRows;
-        const int kg = (p.K + kSkGroups - 1) / kSkGroups;
-        const int kb = g * kg, ke = min(p.K, kb + kg);
-        float acc[kSkinnyN];
-#pragma unroll
-        for (int n = 0; n < kSkinnyN; ++n) acc[n] = 0.0f;
-        for (int k = kb; k < ke; ++k) {
-            const float a = As[k * kAStride + r];
-            const f32x4 *b = reinterpret_cast<const f32x4 *>(Bs + k * kSkinnyN);
-#pragma unroll
-            for (int j = 0; j < kSkinnyN / 4; ++j) {
-                const f32x4 bj = b[j];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) acc[4 * j + e] += a * bj[e];
-            }
-        }
-#pragma unroll
-        for (int n = 0; n < kSkinnyN; ++n) red[(g * kSkinnyN + n) * kSkRows + r] = acc[n];
-    }
-    // Bias gradient (TN with colsum): workgroup 0 sums each column of the B
-    // panel, 16 k-groups in ascending k, then the groups in order.
-    const bool do_cs = p.colsum && blockIdx.x == 0;
-    float csum = 0.0f;
-    if (do_cs) {
-        const int n = t % kSkinnyN, g = t / kSkinnyN;
-        for (int k = g; k < p.K; k += kSkinnyN) csum += Bs[k * kSkinnyN + n];
-    }
-    __syncthreads();
-
-    // Epilogue: thread (r, n) finishes output (m0 + r, n): the 16 K-group
-    // sums in group order.
-    {
-        const int r = t % kSkRows, col = t / kSkRows;
-        const int row = m0 + r;
-        if (row < p.M && col < p.N) {
-            float v = red[col * kSkRows + r];
-#pragma unroll
-            for (int g = 1; g < kSkGroups; ++g) v += red[(g * kSkinnyN + col) * kSkRows + r];
-            const float b = (p.mode == 0 && p.bias) ? p.bias[col] : 0.0f;
-            float z;
-            float o = epi_value(p, v, b, row, col, &z);
-            if (p.mode == 0 && p.Z) p.Z[(size_t)row * p.ldz + col] = z;
-            float *c = p.C + (size_t)row * p.ldc + col;
-            if (p.accumulate) o += *c;
-            *c = o;
-        }
-    }
-    if (do_cs) {
-        // The 16 k-group sums of each column, through the (now free) B panel.
-        __syncthreads();
-        Bs[t] = csum;  // [group][n]
-        __syncthreads();
-        if (t < p.N) {
-            float s = Bs[t];
-            for (int g = 1; g < kSkThreads / kSkinnyN; ++g) s += Bs[g * kSkinnyN + t];
-            p.colsum[t] = p.colsum_accumulate ? p.colsum[t] + s : s;
-        }
-    }
+    gemm_f32_skinny_body<AK, BNC>(p, blockIdx.x);
 }
 
 }  // namespace
 
 void launch_skinny(const GemmArgs &a, int layout, hipStream_t st) {
-    const dim3 grid((a.M + kSkRows - 1) / kSkRows), block(kSkThreads);
+    const dim3 grid(skinny_workgroups(a.M)), block(kSkThreads);
     switch (layout) {
         case 0: gemm_f32_skinny<true, true><<<grid, block, 0, st>>>(a); break;   // NN
         case 1: gemm_f32_skinny<true, false><<<grid, block, 0, st>>>(a); break;  // NT

@@ -382,6 +382,7 @@ class Plan:
         finally:
             call("fg_graph_destroy", h)
         self.handle = p
+        ctx.ctx.adopt(self)
 
     def count(self, role: int) -> int:
         c = ctypes.c_int()

@@ -452,7 +452,9 @@ typedef enum fg_role {
 } fg_role;
 
 /* ctx may be NULL for a dry plan: lowering only (fg_plan_describe and
- * fg_plan_count work; nothing is allocated and dispatch fails). */
+ * fg_plan_count work; nothing is allocated and dispatch fails).  A plan
+ * keeps ctx: destroy the plan before the context (the Rust binding's
+ * Plan<'ctx> lifetime says the same). */
 int fg_plan_create(fg_ctx *ctx, const fg_graph *g, const uint32_t *meta, int n_meta,
                    fg_plan **out);
 int fg_plan_destroy(fg_plan *p);

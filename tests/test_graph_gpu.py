@@ -436,6 +436,68 @@ def test_captured_step_replays_like_eager(ctx):
             assert np.array_equal(x, y2)
 
 
+def test_paired_gradient_gemms_match_separate_calls(ctx):
+    """Each layer's dW (+ dbias) and dX GEMMs share one launch when both take
+    small kernels (the c1 shapes).  An eager c1 step through the planner
+    against the same step built from single calls on a context with the
+    plan's workspace size (so the same kernels and K splits): forward
+    fg_gemm_f32, loss fg_softmax_ce, then fg_gemm_dw_f32 and fg_gemm_bwd_f32
+    one at a time.  Every gradient equal bit for bit."""
+    import ferrograd_amd as fa
+    G = api()
+    torch = pytest.importorskip("torch")
+    own = fa.Context(0, ctx.ctx.stream)
+    try:
+        own.reserve_workspace(1 << 20)
+        dims, B = [784, 256, 10], 64
+        graph, meta, mb, st = build_mlp(ctx, dims, B, "relu", G.Optim.sgd())
+        desc = st.plan.describe()
+        # Both backward variants (seed, CE-fused) pair both layers.
+        assert desc.count("[with the next]") == 4, desc
+        assert "kernels per step: 8 (forward 3, loss 1, backward 3, optim 1)" in desc, desc
+        X = fa.rng_uniform(0, 0, (B, 784))
+        y = fa.rng_int(0, 1, (B,), 10)
+        Ws = [fa.rng_uniform(0, 10 + l, (dims[l], dims[l + 1]), -math.sqrt(6 / dims[l]),
+                             math.sqrt(6 / dims[l])) for l in range(2)]
+        bs = [(0.01 * np.arange(d) - 0.02).astype(f32) for d in dims[1:]]
+        ins = [ctx.init_tensor_f32(X.shape, X)]
+        for W, b in zip(Ws, bs):
+            ins += [ctx.init_tensor_f32(W.shape, W), ctx.init_tensor_f32(b.shape, b)]
+        tgt = ctx.new_onehot_init(y)
+        sch = ctx.schedule(graph.lower(meta), [G.f32_bits(0.01)] + mb[1:], ins, st)
+        ctx.dispatch_forward(sch)
+        ctx.dispatch_loss(sch, tgt)
+        ctx.dispatch_backward(sch)
+        ctx.sync()
+        grads = {t.node: ctx.download(t) for t in st.grad_tensors}
+        in_nodes = [i for i, nd in enumerate(graph.nodes) if nd.op == 0]
+        x, w1, b1, w2, b2 = ins
+
+        def buf(*shape):
+            return torch.empty(shape, device="cuda")
+        Z1, H1, L = buf(B, 256), buf(B, 256), buf(B, 10)
+        own.gemm(fa.NN, B, 256, 784, x, 784, w1, 256, H1, 256, bias=b1, act=fa.ACT_RELU, Z=Z1,
+                 ldz=256)
+        own.gemm(fa.NN, B, 10, 256, H1, 256, w2, 10, L, 10, bias=b2)
+        dl = buf(B, 10)
+        own.softmax_ce(L, 10, tgt, B, 10, 1.0, dlogits=dl, ldd=10)
+        dW2, db2, dZ1 = buf(256, 10), buf(10), buf(B, 256)
+        own.gemm_dw(256, 10, B, H1, 256, dl, 10, dW2, 10, colsum=db2)
+        own.gemm_bwd(fa.NT, B, 256, 10, dl, 10, w2, 10, dZ1, 256, act=fa.ACT_RELU, Zs=Z1,
+                     ldzs=256)
+        dW1, db1, dX = buf(784, 256), buf(256), buf(B, 784)
+        own.gemm_dw(784, 256, B, x, 784, dZ1, 256, dW1, 256, colsum=db1)
+        own.gemm_bwd(fa.NT, B, 784, 256, dZ1, 256, w1, 256, dX, 784)
+        own.sync()
+        ref = [dX, dW1, db1, dW2, db2]
+        for node, r in zip(in_nodes, ref):
+            assert np.array_equal(grads[node], r.cpu().numpy().reshape(-1)), node
+    finally:
+        if "st" in locals():
+            st.plan.close()
+        own.close()
+
+
 @pytest.mark.parametrize("classes,dtype", [(10, "f32"), (1000, "f32"), (1001, "f32"),
                                            (1000, "bf16"), (37, "bf16")],
                          ids=["C10-small", "C1000-rows", "C1001-stream", "C1000-bf16",
@@ -531,11 +593,11 @@ def test_captured_step_survives_workspace_growth(ctx):
         desc = plans[1][1].plan.describe()
         # The first layer's forward and the data-input dX split K in the
         # plan's own workspace (slices + summing kernel each); the 64x10x256
-        # second layer takes the skinny kernel; a captured step leaves the
-        # softmax to the loss launch.
+        # second layer takes the skinny kernel; each layer's dW and dX share
+        # a launch; a captured step leaves the softmax to the loss launch.
         fwd = desc.split("forward:")[1].split("loss:")[0]
         assert fwd.count("[K split") == 1, desc
-        assert "kernels per step: 10 (forward 3, loss 1, backward 5, optim 1)" in desc, desc
+        assert "kernels per step: 8 (forward 3, loss 1, backward 3, optim 1)" in desc, desc
         sch, st, ins, tgt = plans[1]
         call("fg_plan_bind_target", sch.plan.handle, tgt.data_ptr(), tgt.nbytes)
         call("fg_plan_capture_step", sch.plan.handle)
