@@ -370,6 +370,69 @@ def adam_component(ctx, reps: int):
                                "frac_hbm": nbytes / t / 1e6 / PEAK_HBM_GBS}}
 
 
+def hbm_kernels_component(ctx, reps: int):
+    """The other HBM-bound kernels of the path, in GB/s of algorithmic bytes
+    (each launch timed with HIP events after 200 ms of the same launches):
+    * eltwise: a fused elementwise program, the planner's forward of
+      y = tanh(a * b + c) over 8192 x 8192 fp32 -- one launch reading a, b,
+      c and writing the three node values the plan keeps (a * b, a * b + c
+      and y, its forward_saved tensors): 24 B per element;
+    * act_bwd: dZ = dH * GELU'(Z) over 2^28 elements (12 B per element);
+    * sgd: the multi-tensor SGD over c4's 64 x 4 Mi parameters, gradients
+      zeroed after the update (read p, g; write p, g: 16 B per parameter)."""
+    import numpy as np
+    import torch
+
+    import ferrograd_amd as fa
+    from ferrograd_amd import graph as G
+
+    out = {}
+    R = C = 8192
+    gctx = G.GpuContext(ctx)
+    graph, meta = G.Graph(G.MEAN_SQUARED_ERROR, G.Optim.sgd().lower), G.Metadata.new()
+    fr, fc = meta.new_field(), meta.new_field()
+    with graph.define_ops() as ops:
+        a, b, c = (ops.input([fr, fc], trainable=False) for _ in range(3))
+        ops.tanh(ops.add(ops.mul(a, b), c))
+    mb = [G.f32_bits(1e-3), R, C]
+    st = gctx.alloc_tensors(graph, graph.compute_saved_nodes(), mb)
+    xs = [torch.empty((R, C), device="cuda") for _ in range(3)]
+    for i, x in enumerate(xs):
+        ctx.rng_normal(7, i, 0.0, 1.0, x, x.numel())
+    ins = [G.Tensor(x.data_ptr(), x.numel() * 4, x.shape, np.float32, owner=x) for x in xs]
+    sch = gctx.schedule(graph.lower(meta), mb, ins, st)
+    assert "forward: 1 launches" in st.plan.describe()
+    t = event_time_ms(lambda: gctx.dispatch_forward(sch), reps, warm_ms=200)
+    nbytes = 24 * R * C
+    out["eltwise_fwd_8192x8192"] = {"ms": t, "bytes": nbytes, "gbs": nbytes / t / 1e6,
+                                    "frac_hbm": nbytes / t / 1e6 / PEAK_HBM_GBS}
+    st.plan.close()
+    del xs, ins
+
+    n = 1 << 28
+    dH, Z, dZ = (torch.empty(n, device="cuda") for _ in range(3))
+    ctx.rng_normal(7, 10, 0.0, 1.0, dH, n)
+    ctx.rng_normal(7, 11, 0.0, 1.0, Z, n)
+    t = event_time_ms(lambda: ctx.act_bwd(fa.ACT_GELU, n, dH, Z, dZ), reps, warm_ms=200)
+    nbytes = 12 * n
+    out["act_bwd_gelu_2p28"] = {"ms": t, "bytes": nbytes, "gbs": nbytes / t / 1e6,
+                                "frac_hbm": nbytes / t / 1e6 / PEAK_HBM_GBS}
+    del dH, Z, dZ
+
+    nt, n = 64, 4 * 1024 * 1024
+    P = [torch.empty(n, device="cuda") for _ in range(nt)]
+    Gr = [torch.empty(n, device="cuda") for _ in range(nt)]
+    for i in range(nt):
+        ctx.rng_normal(3, i, 0.0, 0.02, P[i], n)
+    mt = fa.MultiTensor(ctx, P, Gr)
+    t = event_time_ms(lambda: mt.sgd(1e-3, True), reps, warm_ms=200)
+    mt.close()
+    nbytes = 16 * nt * n
+    out["sgd_64x4Mi"] = {"ms": t, "bytes": nbytes, "gbs": nbytes / t / 1e6,
+                         "frac_hbm": nbytes / t / 1e6 / PEAK_HBM_GBS}
+    return out
+
+
 def copy_component(reps: int):
     """Context for the HBM-bound kernels: a plain device copy of 1 GiB
     (torch's copy kernel), read + write bytes per second."""
@@ -614,6 +677,8 @@ ONLY = {
     "softmax_ce_c3": only_softmax_ce_c3,
     "adam_c4": only_adam_c4,
     "copy_256mib": only_copy_256mib,
+    "hbm_kernels": lambda ctx, reps: print(json.dumps(hbm_kernels_component(ctx, reps)),
+                                           flush=True),
 }
 
 
@@ -983,6 +1048,7 @@ def main() -> int:
             r, samples["c3"] = r
         comps.update(r)
         comps.update(adam_component(ctx, 10))
+        comps.update(hbm_kernels_component(ctx, args.reps))
         r = c1_component(ctx, want_host=want_cpu)
         if want_cpu:
             r, samples["c1"] = r

@@ -3,6 +3,7 @@
 // variants produce the same values for the same key).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <thread>
 #include <vector>
@@ -139,8 +140,13 @@ FG_API int fg_act_bwd_f32(fg_ctx *ctx, int act, uint64_t n, const float *d_dH, c
     FG_REQUIRE(d_dH && d_Z && d_dZ, FG_ERR_INVALID_ARGUMENT, "fg_act_bwd_f32: NULL pointer");
     FG_HIP(hipSetDevice(ctx->device));
     const int vec = ((((uintptr_t)d_dH) | ((uintptr_t)d_Z) | ((uintptr_t)d_dZ)) & 15u) == 0;
-    act_bwd_kernel<<<grid_for(vec ? (n + 3) / 4 : n, ctx->cu_count), kThreads, 0, ctx->stream>>>(
-        act, n, d_dH, d_Z, d_dZ, vec);
+    // One 16-byte quad per thread and as many workgroups as that takes (a
+    // plain stream, each workgroup touching one contiguous 16 KiB span),
+    // up to the grid limit; the kernel's loop covers anything beyond.
+    const uint64_t items = vec ? (n + 3) / 4 : n;
+    const unsigned grid =
+        (unsigned)std::min<uint64_t>((items + kThreads - 1) / kThreads, 1u << 30);
+    act_bwd_kernel<<<grid, kThreads, 0, ctx->stream>>>(act, n, d_dH, d_Z, d_dZ, vec);
     FG_LAUNCH_CHECK("act_bwd_kernel");
     return FG_OK;
 }

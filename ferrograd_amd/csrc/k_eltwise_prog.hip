@@ -15,67 +15,163 @@ namespace {
 
 constexpr int kThreads = 256;
 
-__device__ __forceinline__ float elt_load(const EltProgram &p, int s, int mode, int dt,
-                                          uint64_t i) {
-    const uint64_t j = mode == kModeScalar ? 0 : mode == kModeRow ? i % p.cols : i;
-    return load_as_f(p.src[s], dt, j);
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Each thread runs the program over a quad of 4 consecutive elements
+// (i0 .. i0+3, i0 % 4 == 0): registers are f32x4, and a load or store moves
+// the quad with one 16-byte (fp32) or 8-byte (16-bit) access when the
+// pointer allows it (the pointer test is uniform, so it costs scalar work).
+// Quads that cross the end of the tensor, unaligned pointers and the
+// row-broadcast of a row whose length is not a multiple of 4 go element by
+// element.  Every element sees the same fp32 operations as the one-element
+// form, in the same order: the results are bit-identical.
+__device__ __forceinline__ bool quad_aligned(const void *q, int dt) {
+    return (((uintptr_t)q) & (dt == kF32 ? 15u : 7u)) == 0;
+}
+
+__device__ __forceinline__ f32x4 quad_get(const void *q, int dt, uint64_t j) {
+    if (dt == kF32) return *reinterpret_cast<const f32x4 *>(static_cast<const float *>(q) + j);
+    const uint2 w = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(q) + j);
+    return f32x4{h16_to_f(dt, (uint16_t)(w.x & 0xffffu)), h16_to_f(dt, (uint16_t)(w.x >> 16)),
+                 h16_to_f(dt, (uint16_t)(w.y & 0xffffu)), h16_to_f(dt, (uint16_t)(w.y >> 16))};
+}
+
+__device__ __forceinline__ void quad_put(void *q, int dt, uint64_t j, f32x4 v) {
+    if (dt == kF32) {
+        *reinterpret_cast<f32x4 *>(static_cast<float *>(q) + j) = v;
+        return;
+    }
+    uint2 w;
+    w.x = (uint32_t)f_to_h16(dt, v[0]) | ((uint32_t)f_to_h16(dt, v[1]) << 16);
+    w.y = (uint32_t)f_to_h16(dt, v[2]) | ((uint32_t)f_to_h16(dt, v[3]) << 16);
+    *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(q) + j) = w;
+}
+
+// Source s at elements i0 .. i0+nv-1 (missing lanes of a partial quad are 0).
+__device__ __forceinline__ f32x4 quad_load(const EltProgram &p, int s, int mode, int dt,
+                                           uint64_t i0, int nv) {
+    const void *q = p.src[s];
+    if (mode == kModeScalar) {
+        const float x = load_as_f(q, dt, 0);
+        return f32x4{x, x, x, x};
+    }
+    if (mode == kModeFull) {
+        if (nv == 4 && quad_aligned(q, dt)) return quad_get(q, dt, i0);
+        f32x4 r{0.f, 0.f, 0.f, 0.f};
+        for (int e = 0; e < nv; ++e) r[e] = load_as_f(q, dt, i0 + e);
+        return r;
+    }
+    // Row broadcast: element i reads src[i % cols].
+    const uint32_t c0 = (uint32_t)(i0 % p.cols);
+    if (nv == 4 && p.cols % 4 == 0 && quad_aligned(q, dt)) return quad_get(q, dt, c0);
+    f32x4 r{0.f, 0.f, 0.f, 0.f};
+    for (int e = 0; e < nv; ++e) r[e] = load_as_f(q, dt, (c0 + (uint32_t)e) % p.cols);
+    return r;
+}
+
+__device__ __forceinline__ void quad_store(const EltProgram &p, int d, int dt, uint64_t i0, int nv,
+                                           f32x4 v, bool accum) {
+    void *q = p.dst[d];
+    if (nv == 4 && quad_aligned(q, dt)) {
+        if (accum) v += quad_get(q, dt, i0);
+        quad_put(q, dt, i0, v);
+        return;
+    }
+    for (int e = 0; e < nv; ++e)
+        store_from_f(q, dt, i0 + e, accum ? load_as_f(q, dt, i0 + e) + v[e] : v[e]);
+}
+
+template <class F>
+__device__ __forceinline__ f32x4 quad_map(f32x4 x, F f) {
+    f32x4 r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r[e] = f(x[e]);
+    return r;
 }
 
 __global__ __launch_bounds__(kThreads) void eltwise_prog_kernel(const EltProgram p) {
+    const uint64_t nq = (p.n + 3) / 4;
     const uint64_t stride = (uint64_t)gridDim.x * kThreads;
-    for (uint64_t i = (uint64_t)blockIdx.x * kThreads + threadIdx.x; i < p.n; i += stride) {
-        float r[kEltRegs];
+    for (uint64_t q = (uint64_t)blockIdx.x * kThreads + threadIdx.x; q < nq; q += stride) {
+        const uint64_t i0 = 4 * q;
+        const int nv = p.n - i0 >= 4 ? 4 : (int)(p.n - i0);
+        // The register file as four plain arrays, one per element of the
+        // quad, each indexed by the same uniform register number (a float4
+        // array indexed at run time would go to scratch memory).
+        float r0[kEltRegs], r1[kEltRegs], r2[kEltRegs], r3[kEltRegs];
 #pragma unroll
-        for (int k = 0; k < kEltRegs; ++k) r[k] = 0.0f;
+        for (int k = 0; k < kEltRegs; ++k) r0[k] = r1[k] = r2[k] = r3[k] = 0.0f;
+        auto get = [&](int k) { return f32x4{r0[k & 15], r1[k & 15], r2[k & 15], r3[k & 15]}; };
         for (int k = 0; k < p.n_instr; ++k) {
             const EltInstr in = p.ins[k];
+            const f32x4 x = get(in.a), y = get(in.b);
+            f32x4 o = x;
+            bool wr = true;  // the instruction writes register in.dst
             switch (in.op) {
-                case kEltLoad: r[in.dst & 15] = elt_load(p, in.a, in.c, in.b, i); break;
-                case kEltImm: r[in.dst & 15] = in.imm; break;
-                case kEltStore: store_from_f(p.dst[in.a], in.c, i, r[in.b & 15]); break;
+                case kEltLoad: o = quad_load(p, in.a, in.c, in.b, i0, nv); break;
+                case kEltImm: o = f32x4{in.imm, in.imm, in.imm, in.imm}; break;
+                case kEltStore:
+                    quad_store(p, in.a, in.c, i0, nv, y, false);
+                    wr = false;
+                    break;
                 case kEltAccum:
-                    store_from_f(p.dst[in.a], in.c, i,
-                                 load_as_f(p.dst[in.a], in.c, i) + r[in.b & 15]);
+                    quad_store(p, in.a, in.c, i0, nv, y, true);
+                    wr = false;
                     break;
-                case kEltRound: r[in.dst & 15] = round_to(in.c, r[in.a & 15]); break;
-                case kEltAdd: r[in.dst & 15] = r[in.a & 15] + r[in.b & 15]; break;
-                case kEltSub: r[in.dst & 15] = r[in.a & 15] - r[in.b & 15]; break;
-                case kEltMul: r[in.dst & 15] = r[in.a & 15] * r[in.b & 15]; break;
-                case kEltDiv: r[in.dst & 15] = r[in.a & 15] / r[in.b & 15]; break;
-                case kEltNeg: r[in.dst & 15] = -r[in.a & 15]; break;
-                case kEltRelu: r[in.dst & 15] = act_fwd(kActRelu, r[in.a & 15]); break;
-                case kEltGelu: r[in.dst & 15] = act_fwd(kActGelu, r[in.a & 15]); break;
-                case kEltElu: {
-                    const float x = r[in.a & 15];
-                    r[in.dst & 15] = x >= 0.0f ? x : expf(x) - 1.0f;
+                case kEltRound: o = quad_map(x, [&](float v) { return round_to(in.c, v); }); break;
+                case kEltAdd: o = x + y; break;
+                case kEltSub: o = x - y; break;
+                case kEltMul: o = x * y; break;
+                case kEltDiv: o = x / y; break;
+                case kEltNeg: o = -x; break;
+                case kEltRelu: o = quad_map(x, [](float v) { return act_fwd(kActRelu, v); }); break;
+                case kEltGelu: o = quad_map(x, [](float v) { return act_fwd(kActGelu, v); }); break;
+                case kEltElu:
+                    o = quad_map(x, [](float v) { return v >= 0.0f ? v : expf(v) - 1.0f; });
                     break;
-                }
-                case kEltTanh: r[in.dst & 15] = tanhf(r[in.a & 15]); break;
-                case kEltExp: r[in.dst & 15] = expf(r[in.a & 15]); break;
-                case kEltLog: r[in.dst & 15] = logf(r[in.a & 15]); break;
-                case kEltAbs: r[in.dst & 15] = fabsf(r[in.a & 15]); break;
-                case kEltReluD: r[in.dst & 15] = act_grad(kActRelu, r[in.a & 15]); break;
-                case kEltGeluD: r[in.dst & 15] = act_grad(kActGelu, r[in.a & 15]); break;
-                case kEltEluD: {
-                    const float x = r[in.a & 15];
-                    r[in.dst & 15] = x >= 0.0f ? 1.0f : expf(x);
+                case kEltTanh: o = quad_map(x, [](float v) { return tanhf(v); }); break;
+                case kEltExp: o = quad_map(x, [](float v) { return expf(v); }); break;
+                case kEltLog: o = quad_map(x, [](float v) { return logf(v); }); break;
+                case kEltAbs: o = quad_map(x, [](float v) { return fabsf(v); }); break;
+                case kEltReluD: o = quad_map(x, [](float v) { return act_grad(kActRelu, v); }); break;
+                case kEltGeluD: o = quad_map(x, [](float v) { return act_grad(kActGelu, v); }); break;
+                case kEltEluD:
+                    o = quad_map(x, [](float v) { return v >= 0.0f ? 1.0f : expf(v); });
                     break;
-                }
-                case kEltSign: {
-                    const float x = r[in.a & 15];
-                    r[in.dst & 15] = x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : 0.0f);
+                case kEltSign:
+                    o = quad_map(x, [](float v) { return v > 0.0f ? 1.0f : (v < 0.0f ? -1.0f : 0.0f); });
                     break;
-                }
                 case kEltLabelEq: {
-                    const uint64_t row = i / p.cols, col = i % p.cols;
-                    r[in.dst & 15] = (p.labels[row] == (uint32_t)col) ? 1.0f : 0.0f;
+                    f32x4 t{0.f, 0.f, 0.f, 0.f};
+                    for (int e = 0; e < nv; ++e) {
+                        const uint64_t row = (i0 + e) / p.cols, col = (i0 + e) % p.cols;
+                        t[e] = (p.labels[row] == (uint32_t)col) ? 1.0f : 0.0f;
+                    }
+                    o = t;
                     break;
                 }
-                case kEltSelect:
-                    r[in.dst & 15] = r[in.a & 15] != 0.0f ? r[in.b & 15] : r[in.c & 15];
+                case kEltSelect: {
+                    const f32x4 z = get(in.c);
+                    f32x4 t;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) t[e] = x[e] != 0.0f ? y[e] : z[e];
+                    o = t;
                     break;
-                case kEltMax: r[in.dst & 15] = fmaxf(r[in.a & 15], r[in.b & 15]); break;
-                default: break;
+                }
+                case kEltMax: {
+                    f32x4 t;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) t[e] = fmaxf(x[e], y[e]);
+                    o = t;
+                    break;
+                }
+                default: wr = false; break;
+            }
+            if (wr) {
+                r0[in.dst & 15] = o[0];
+                r1[in.dst & 15] = o[1];
+                r2[in.dst & 15] = o[2];
+                r3[in.dst & 15] = o[3];
             }
         }
     }
@@ -116,9 +212,11 @@ int launch_eltwise(fg_ctx *ctx, const EltProgram &p) {
         }
     }
     FG_REQUIRE(!needs_cols || p.cols > 0, FG_ERR_INTERNAL, "eltwise program: cols is 0");
-    uint64_t blocks = (p.n + kThreads - 1) / kThreads;
-    const uint64_t cap = (uint64_t)(ctx->cu_count > 0 ? ctx->cu_count : 256) * 8;
-    if (blocks > cap) blocks = cap;
+    // One quad per thread and as many workgroups as that takes, up to the
+    // grid limit (a capped grid looping over the tensor streamed at a
+    // fraction of the rate); the kernel's loop covers anything beyond.
+    uint64_t blocks = ((p.n + 3) / 4 + kThreads - 1) / kThreads;
+    if (blocks > (1u << 30)) blocks = 1u << 30;
     eltwise_prog_kernel<<<(unsigned)blocks, kThreads, 0, ctx->stream>>>(p);
     FG_LAUNCH_CHECK("eltwise_prog_kernel");
     return FG_OK;
