@@ -774,11 +774,15 @@ def test_unary_forward_backward(ctx, op):
     assert normwise_rel(ctx.download(st.grad_tensors[0]).reshape(R, C), exp) < 1e-5
 
 
-def test_binary_broadcast_and_div_backward(ctx):
+@pytest.mark.parametrize("C", [300, 301])
+def test_binary_broadcast_and_div_backward(ctx, C):
     """(a / b) * c - bias (row-broadcast sub): forward and every gradient
-    against float64 numpy, including the negated column reduction."""
+    against float64 numpy, including the negated column reduction.  The
+    elementwise kernel runs float4 quads: C = 300 reads the bias four columns
+    at a time; C = 301 takes the element-wise row broadcast, with quads that
+    cross rows and a one-element last quad (9 x 301 elements)."""
     G = api()
-    R, C = 9, 300
+    R = 9
     graph, meta = new_graph(G.MEAN_SQUARED_ERROR)
     r, c = meta.new_field(), meta.new_field()
     with graph.define_ops() as ops:
