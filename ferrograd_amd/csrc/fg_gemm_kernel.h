@@ -313,8 +313,9 @@ __device__ __forceinline__ float epi_value(const GemmArgs &p, float v, float bv,
 
 // Four consecutive outputs of one row (the vector path of the epilogue):
 // the same operations as epi_value per element, with the uniform choices
-// (mode, activation, Z, accumulate) taken once per four.
-__device__ __forceinline__ void epi_x4(const GemmArgs &p, f32x4 v, f32x4 bv, int row, int col) {
+// (mode, activation, Z, accumulate) taken once per four.  Returns the four
+// values stored to C.
+__device__ __forceinline__ f32x4 epi_x4(const GemmArgs &p, f32x4 v, f32x4 bv, int row, int col) {
     if (p.mode == 0) {
         v += bv;
         if (p.Z) *reinterpret_cast<f32x4 *>(p.Z + (size_t)row * p.ldz + col) = v;
@@ -330,6 +331,7 @@ __device__ __forceinline__ void epi_x4(const GemmArgs &p, f32x4 v, f32x4 bv, int
     float *c = p.C + (size_t)row * p.ldc + col;
     if (p.accumulate) v += *reinterpret_cast<const f32x4 *>(c);
     *reinterpret_cast<f32x4 *>(c) = v;
+    return v;
 }
 
 // Epilogue shared by the GEMM kernels.  Accumulator register r of lane
@@ -380,7 +382,7 @@ __device__ __forceinline__ void store_tile(const GemmArgs &p, const f32x16 (&acc
             const int row = IA > 1 ? r0 + TM * (rr0 + q * RPP) + i : r0 + i * 32 + rr0 + q * RPP;
             if (row >= p.M || col >= p.N) continue;
             if (vec) {
-                epi_x4(p, v, bv, row, col);
+                (void)epi_x4(p, v, bv, row, col);
             } else {
                 float *crow = p.C + (size_t)row * p.ldc;
 #pragma unroll 1
@@ -1103,6 +1105,14 @@ void launch_tn_pro(const GemmArgs &a, bool vec, bool pipe, int cfg, int pro, hip
 constexpr int kSkinnyN = 16;
 constexpr int kSkinnyK = 256;
 void launch_skinny(const GemmArgs &a, int layout, hipStream_t st);
+// NN skinny GEMM whose A operand is the output of the split-K GEMM `pre`
+// (its slices written, not yet summed): sums them with pre's epilogue as it
+// loads its A panel, and writes pre's outputs; the same bits as the summing
+// kernel followed by launch_skinny.  Conditions on the host
+// (fg::gemm_fwd_chain_f32): pre splits into at most kSkPreMaxSlices slices,
+// its N (a.K) is a multiple of 4 and pre.vec_out holds.
+constexpr int kSkPreMaxSlices = 12;
+void launch_skinny_pre(const GemmArgs &a, const GemmArgs &pre, hipStream_t st);
 
 // A layer's dW (TN, GEMM 1) and dX (NT, GEMM 2) in one launch
 // (k_gemm_pair.hip): kinds of the kernels they would take alone, which must

@@ -144,5 +144,110 @@ __device__ __forceinline__ void gemm_f32_skinny_body(GemmArgs p, int bx) {
     }
 }
 
+// NN with a summing prologue: A is the output of a split-K GEMM `pre` whose
+// slices have not been summed.  A workgroup owns kSpRows output rows, a
+// quarter of the plain kernel's, so the slices' bytes spread over four
+// times as many CUs (one CU pulls them at a few tens of GB/s).  It sums its
+// rows' slices in slice order, applies pre's epilogue (bias, activation, Z)
+// and writes pre's outputs -- per element the operations of splitk_reduce,
+// so the same bits -- and takes its A panel from those values.  The product
+// is then exactly the plain kernel's (16 k-groups of the same extent, each
+// in ascending k, the group sums added in group order), so the same bits as
+// gemm_f32_skinny_body.  Host conditions (fg::gemm_fwd_chain_f32): at most
+// kSkPreMaxSlices slices, pre's N (this GEMM's K) a multiple of 4, pre's
+// rows 16-byte aligned (pre.vec_out).
+constexpr int kSpRows = 4;
+static_assert(kSpRows * kSkinnyK == 4 * kSkThreads, "one float4 of A per thread");
+inline int skinny_pre_workgroups(int M) { return (M + kSpRows - 1) / kSpRows; }
+
+__device__ __forceinline__ void gemm_f32_skinny_pre_body(const GemmArgs &p, const GemmArgs &pre,
+                                                         int bx) {
+    __shared__ float As[kSkinnyK * kSpRows];  // As[k][r]
+    __shared__ __attribute__((aligned(16))) float Bs[kSkinnyK * kSkinnyN];
+    __shared__ float red[kSkGroups * kSkinnyN * kSpRows];
+    const int t = threadIdx.x;
+    const int m0 = bx * kSpRows;
+
+    // Every load first: thread t holds columns c4..c4+3 of local row r, all
+    // slices, and its part of the B panel (B[k][n]).
+    const int c4 = 4 * (t % (kSkinnyK / 4)), r = t / (kSkinnyK / 4);
+    const int row = m0 + r;
+    const int S = (pre.K + pre.ksplit - 1) / pre.ksplit;
+    const bool ok = row < pre.M && c4 < pre.N;
+    const float *src = pre.partial + (size_t)row * pre.N + c4;
+    const size_t mn = (size_t)pre.M * pre.N;
+    f32x4 sl[kSkPreMaxSlices];
+#pragma unroll
+    for (int s = 0; s < kSkPreMaxSlices; ++s)
+        sl[s] = (ok && s < S) ? *reinterpret_cast<const f32x4 *>(src + s * mn)
+                              : f32x4{0.f, 0.f, 0.f, 0.f};
+    float rb[kSkBPerThread];
+    const int bn = t % kSkinnyN, bk0 = t / kSkinnyN;
+#pragma unroll
+    for (int i = 0; i < kSkBPerThread; ++i) {
+        const int k = bk0 + kSkinnyN * i;
+        rb[i] = (k < p.K && bn < p.N) ? p.B[(size_t)k * p.ldb + bn] : 0.0f;
+    }
+    const f32x4 bv = (pre.bias && c4 < pre.N) ? *reinterpret_cast<const f32x4 *>(pre.bias + c4)
+                                              : f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // pre's outputs: the slices in slice order, then pre's epilogue.
+    f32x4 h = {0.f, 0.f, 0.f, 0.f};
+    if (ok) {
+        f32x4 v = sl[0];
+#pragma unroll
+        for (int s = 1; s < kSkPreMaxSlices; ++s)
+            if (s < S) v += sl[s];
+        h = epi_x4(pre, v, bv, row, c4);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) As[(c4 + e) * kSpRows + r] = h[e];
+#pragma unroll
+    for (int i = 0; i < kSkBPerThread; ++i) Bs[(bk0 + kSkinnyN * i) * kSkinnyN + bn] = rb[i];
+    __syncthreads();
+
+    // The plain kernel's sums: thread (r, g) = (t % kSpRows, t / kSpRows)
+    // takes row r over the g-th K group, all 16 columns.
+    if (t < kSpRows * kSkGroups) {
+        const int rr = t % kSpRows, g = t / kSpRows;
+        const int kg = (p.K + kSkGroups - 1) / kSkGroups;
+        const int kb = g * kg, ke = min(p.K, kb + kg);
+        float acc[kSkinnyN];
+#pragma unroll
+        for (int n = 0; n < kSkinnyN; ++n) acc[n] = 0.0f;
+        for (int k = kb; k < ke; ++k) {
+            const float a = As[k * kSpRows + rr];
+            const f32x4 *b = reinterpret_cast<const f32x4 *>(Bs + k * kSkinnyN);
+#pragma unroll
+            for (int j = 0; j < kSkinnyN / 4; ++j) {
+                const f32x4 bj = b[j];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[4 * j + e] += a * bj[e];
+            }
+        }
+#pragma unroll
+        for (int n = 0; n < kSkinnyN; ++n) red[(g * kSkinnyN + n) * kSpRows + rr] = acc[n];
+    }
+    __syncthreads();
+
+    // Epilogue: thread (r, n) finishes output (m0 + r, n).
+    if (t < kSpRows * kSkinnyN) {
+        const int rr = t % kSpRows, col = t / kSpRows;
+        const int orow = m0 + rr;
+        if (orow < p.M && col < p.N) {
+            float v = red[col * kSpRows + rr];
+#pragma unroll
+            for (int g = 1; g < kSkGroups; ++g) v += red[(g * kSkinnyN + col) * kSpRows + rr];
+            const float b = (p.mode == 0 && p.bias) ? p.bias[col] : 0.0f;
+            float z;
+            float o = epi_value(p, v, b, orow, col, &z);
+            if (p.mode == 0 && p.Z) p.Z[(size_t)orow * p.ldz + col] = z;
+            float *c = p.C + (size_t)orow * p.ldc + col;
+            if (p.accumulate) o += *c;
+            *c = o;
+        }
+    }
+}
+
 }  // namespace gemm
 }  // namespace fg

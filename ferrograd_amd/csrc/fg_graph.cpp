@@ -246,6 +246,11 @@ struct Launch {
     // gradients, so they go to fg::gemm_dw_dx_f32 together, which puts them
     // in one launch when both take small kernels.
     bool pair_next = false;
+    // A forward GEMM (fp32, NN) whose output is the A operand of the next
+    // launch, a forward GEMM (fp32, NN): the two go to
+    // fg::gemm_fwd_chain_f32, where the second sums the first's K slices
+    // when the first splits K and the second takes the skinny kernel.
+    bool chain_next = false;
     std::string desc;
     Launch() {
         std::fill(src_slot, src_slot + fg::kEltMaxSrc, kNone);
@@ -590,6 +595,20 @@ int lower_forward(fg_plan &P) {
         eb.names.push_back(std::string(op_name(nd.op)) + "#" + std::to_string(n));
     }
     eb.flush(P.fwd, "forward");
+    // Forward GEMM chains (the first's output is the next's A operand).
+    for (size_t i = 0; i + 1 < P.fwd.size(); ++i) {
+        Launch &L = P.fwd[i];
+        const Launch &X = P.fwd[i + 1];
+        const bool gemm = L.kind == LK_GEMM && X.kind == LK_GEMM && L.sExtra == kNone &&
+                          X.sExtra == kNone && L.dtype == FG_DTYPE_F32 &&
+                          X.dtype == FG_DTYPE_F32 && L.layout == FG_NN && X.layout == FG_NN;
+        if (gemm && X.sA == L.sC && X.lda == L.ldc && X.K == L.N && X.M == L.M &&
+            !L.accumulate) {
+            L.chain_next = true;
+            L.desc += " [chained with the next]";
+            ++i;  // a launch is the second of at most one chain
+        }
+    }
     return FG_OK;
 }
 
@@ -1094,6 +1113,18 @@ int run(fg_plan &P, const std::vector<Launch> &list, bool step = false) {
             continue;
         }
         if (step && L.elidable) continue;
+        if (L.chain_next && &L + 1 < list.data() + list.size()) {
+            const Launch &X = *(&L + 1);  // reads L's output as its A operand
+            rc = fg::gemm_fwd_chain_f32(
+                ctx, L.M, L.N, L.K, (const float *)P.ptr(L.sA), L.lda, (const float *)P.ptr(L.sB),
+                L.ldb, (const float *)P.ptr(L.sBias), L.act, (float *)P.ptr(L.sC), L.ldc,
+                (float *)P.ptr(L.sZ), L.ldz, X.M, X.N, X.K, (const float *)P.ptr(X.sA), X.lda,
+                (const float *)P.ptr(X.sB), X.ldb, (const float *)P.ptr(X.sBias), X.act,
+                (float *)P.ptr(X.sC), X.ldc, (float *)P.ptr(X.sZ), X.ldz, X.accumulate);
+            if (rc != FG_OK) return rc;
+            skip_next = true;
+            continue;
+        }
         if (L.pair_next && &L + 1 < list.data() + list.size()) {
             const Launch &X = *(&L + 1);  // the same layer's dX (NT, act')
             rc = fg::gemm_dw_dx_f32(ctx, L.M, L.N, L.K, (const float *)P.ptr(L.sA), L.lda,
@@ -1952,11 +1983,25 @@ FG_API int fg_plan_describe(const fg_plan *p, char *buf, size_t len, size_t *nee
                                        p->ptr(L.sA), L.lda, p->ptr(L.sB), L.ldb,
                                        L.kind == LK_GEMM && L.sExtra != kNone);
     };
+    // Dispatches of a forward chain (L and the next launch X).
+    auto chain_dispatches = [&](const Launch &L, const Launch &X) {
+        if (!wc) return gemm_dispatches(L) + gemm_dispatches(X);
+        return fg::gemm_fwd_chain_dispatches(
+            wc, L.M, L.N, L.K, p->ptr(L.sA), L.lda, p->ptr(L.sB), L.ldb, p->ptr(L.sBias),
+            p->ptr(L.sC), L.ldc, p->ptr(L.sZ), L.ldz, X.M, X.N, X.K, p->ptr(X.sA), X.lda,
+            p->ptr(X.sB), X.ldb);
+    };
     auto add = [&](const char *title, const std::vector<Launch> &v) {
         s += std::string(title) + ": " + std::to_string(v.size()) + " launches\n";
-        for (const Launch &L : v) {
+        for (size_t i = 0; i < v.size(); ++i) {
+            const Launch &L = v[i];
             s += "  " + L.desc;
-            if (gemm_dispatches(L) > 1) s += " [K split: slices + summing kernel]";
+            if (gemm_dispatches(L) > 1) {
+                const bool summed_by_next = L.chain_next && i + 1 < v.size() &&
+                                            chain_dispatches(L, v[i + 1]) == 2;
+                s += summed_by_next ? " [K split: slices, summed by the next launch]"
+                                    : " [K split: slices + summing kernel]";
+            }
             s += "\n";
         }
     };
@@ -1971,7 +2016,10 @@ FG_API int fg_plan_describe(const fg_plan *p, char *buf, size_t len, size_t *nee
         for (size_t i = 0; i < v.size(); ++i) {
             const Launch &L = v[i];
             if (L.elidable) continue;
-            if (L.pair_next && i + 1 < v.size()) {
+            if (L.chain_next && i + 1 < v.size()) {
+                n += chain_dispatches(L, v[i + 1]);
+                ++i;
+            } else if (L.pair_next && i + 1 < v.size()) {
                 const Launch &X = v[i + 1];
                 n += wc ? fg::gemm_dw_dx_dispatches(wc, L.M, L.N, L.K, p->ptr(L.sA), L.lda,
                                                     p->ptr(L.sB), L.ldb, X.M, X.N, X.K,

@@ -94,6 +94,19 @@ int gemm_dw_dx_f32(fg_ctx *ctx, int M1, int N1, int K1, const float *A1, int lda
 int gemm_dw_dx_dispatches(fg_ctx *ctx, int M1, int N1, int K1, const void *A1, int lda1,
                           const void *B1, int ldb1, int M2, int N2, int K2, const void *A2,
                           int lda2, const void *B2, int ldb2);
+// Two forward GEMMs in a row, the second (NN) reading the first's output as
+// its A operand: when the first splits K and the second takes the skinny
+// kernel, the second sums the first's slices (k_gemm.hip); and the dispatch
+// count of that call.
+int gemm_fwd_chain_f32(fg_ctx *ctx, int M1, int N1, int K1, const float *A1, int lda1,
+                       const float *B1, int ldb1, const float *bias1, int act1, float *C1,
+                       int ldc1, float *Z1, int ldz1, int M2, int N2, int K2, const float *A2,
+                       int lda2, const float *B2, int ldb2, const float *bias2, int act2,
+                       float *C2, int ldc2, float *Z2, int ldz2, int acc2);
+int gemm_fwd_chain_dispatches(fg_ctx *ctx, int M1, int N1, int K1, const void *A1, int lda1,
+                              const void *B1, int ldb1, const void *bias1, void *C1, int ldc1,
+                              void *Z1, int ldz1, int M2, int N2, int K2, const void *A2, int lda2,
+                              const void *B2, int ldb2);
 }  // namespace fg
 
 #define FG_HIP(call)                                                     \

@@ -219,7 +219,9 @@ void launch_reduce(fg_ctx *ctx, const GemmArgs &a, int splits) {
     splitk_reduce<<<grid, kThreads, 0, ctx->stream>>>(a, splits);
 }
 
-int gemm_launch(fg_ctx *ctx, const Planned &P, const char *who) {
+// reduce: launch the summing kernel of a split GEMM (false: its consumer
+// sums the slices).
+int gemm_launch(fg_ctx *ctx, const Planned &P, const char *who, bool reduce = true) {
     if (P.empty) return FG_OK;
     if (P.skinny) {
         fg::gemm::launch_skinny(P.a, P.layout, ctx->stream);
@@ -234,7 +236,7 @@ int gemm_launch(fg_ctx *ctx, const Planned &P, const char *who) {
         default: fg::gemm::launch_tn(P.a, P.vec, P.pipe, P.ktail, P.cfg, P.pro, ctx->stream); break;
     }
     FG_LAUNCH_CHECK(who);
-    if (P.splits > 1) {
+    if (P.splits > 1 && reduce) {
         launch_reduce(ctx, P.a, P.splits);
         FG_LAUNCH_CHECK(who);
     }
@@ -446,6 +448,42 @@ bool plan_pair(fg_ctx *ctx, const GemmArgs &w, const GemmArgs &x, Planned &P1, P
     return pairable(P1, P2);
 }
 
+// Forward GEMM arguments (as fg_gemm_f32 takes them).
+GemmArgs fwd_args(int M, int N, int K, const float *A, int lda, const float *B, int ldb,
+                  const float *bias, int act, float *C, int ldc, float *Z, int ldz,
+                  int accumulate) {
+    GemmArgs a{};
+    a.A = A;
+    a.B = B;
+    a.C = C;
+    a.Z = Z;
+    a.bias = bias;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.lda = lda;
+    a.ldb = ldb;
+    a.ldc = ldc;
+    a.ldz = Z ? ldz : 0;
+    a.act = act;
+    a.mode = 0;
+    a.accumulate = accumulate ? 1 : 0;
+    return a;
+}
+
+// GEMM 1's slices summed by GEMM 2's skinny kernel: GEMM 1 splits K into at
+// most kSkPreMaxSlices slices, without accumulation, its output (N a
+// multiple of 4, 16-byte rows) is exactly GEMM 2's A operand, and GEMM 2
+// takes the skinny kernel in the NN layout.
+bool chainable(const Planned &P1, const Planned &P2) {
+    const GemmArgs &a = P1.a, &b = P2.a;
+    return !P1.empty && !P2.empty && P1.layout == FG_NN && P2.layout == FG_NN &&
+           P1.pro == fg::gemm::kProNone && P1.splits > 1 &&
+           P1.splits <= fg::gemm::kSkPreMaxSlices && !a.accumulate && a.mode == 0 &&
+           a.N % 4 == 0 && a.vec_out && P2.skinny && b.A == a.C && b.lda == a.ldc &&
+           b.K == a.N && b.M == a.M;
+}
+
 // The kernel choices alone, for counting dispatches: no validation, no error
 // message, operands not bound yet taken as 16-byte aligned.
 void plan_quiet(fg_ctx *ctx, int layout, const GemmArgs &a0, Planned &P) {
@@ -495,6 +533,61 @@ int gemm_dw_dx_f32(fg_ctx *ctx, int M1, int N1, int K1, const float *A1, int lda
             FG_LAUNCH_CHECK("gemm_dw_dx_f32");
         }
     return FG_OK;
+}
+
+// Two forward GEMMs in a row where the second reads the first's output as
+// its A operand (NN both; GEMM 1 with bias / activation / Z as fg_gemm_f32):
+// when GEMM 1 splits K and GEMM 2 takes the skinny kernel, GEMM 2's kernel
+// sums GEMM 1's slices (slice order, GEMM 1's epilogue, GEMM 1's outputs
+// written) instead of a summing kernel -- one dispatch fewer, the same bits.
+// Otherwise the two calls one after the other.
+int gemm_fwd_chain_f32(fg_ctx *ctx, int M1, int N1, int K1, const float *A1, int lda1,
+                       const float *B1, int ldb1, const float *bias1, int act1, float *C1,
+                       int ldc1, float *Z1, int ldz1, int M2, int N2, int K2, const float *A2,
+                       int lda2, const float *B2, int ldb2, const float *bias2, int act2,
+                       float *C2, int ldc2, float *Z2, int ldz2, int acc2) {
+    auto separate = [&]() {
+        const int rc = fg_gemm_f32(ctx, FG_NN, M1, N1, K1, A1, lda1, B1, ldb1, bias1, act1, C1,
+                                   ldc1, Z1, ldz1, 0);
+        if (rc) return rc;
+        return fg_gemm_f32(ctx, FG_NN, M2, N2, K2, A2, lda2, B2, ldb2, bias2, act2, C2, ldc2, Z2,
+                           ldz2, acc2);
+    };
+    if (!ctx || (Z1 && ldz1 < N1) || (Z2 && ldz2 < N2) || (acc2 && act2 != FG_ACT_NONE))
+        return separate();  // the plain calls report the argument errors
+    Planned P1, P2;
+    if (gemm_prepare(ctx, FG_NN, fwd_args(M1, N1, K1, A1, lda1, B1, ldb1, bias1, act1, C1, ldc1,
+                                          Z1, ldz1, 0),
+                     "fg_gemm_f32", fg::gemm::kProNone, P1) ||
+        gemm_prepare(ctx, FG_NN, fwd_args(M2, N2, K2, A2, lda2, B2, ldb2, bias2, act2, C2, ldc2,
+                                          Z2, ldz2, acc2),
+                     "fg_gemm_f32", fg::gemm::kProNone, P2) ||
+        !chainable(P1, P2)) {
+        fg::clear_error();
+        return separate();
+    }
+    if (int rc = gemm_launch(ctx, P1, "gemm_fwd_chain_f32", false)) return rc;
+    fg::gemm::launch_skinny_pre(P2.a, P1.a, ctx->stream);
+    FG_LAUNCH_CHECK("gemm_fwd_chain_f32");
+    return FG_OK;
+}
+
+// Dispatches of gemm_fwd_chain_f32 for these operands (no launch).
+int gemm_fwd_chain_dispatches(fg_ctx *ctx, int M1, int N1, int K1, const void *A1, int lda1,
+                              const void *B1, int ldb1, const void *bias1, void *C1, int ldc1,
+                              void *Z1, int ldz1, int M2, int N2, int K2, const void *A2, int lda2,
+                              const void *B2, int ldb2) {
+    const int sep = gemm_f32_dispatches(ctx, FG_NN, M1, N1, K1, A1, lda1, B1, ldb1, false) +
+                    gemm_f32_dispatches(ctx, FG_NN, M2, N2, K2, A2, lda2, B2, ldb2, false);
+    if (!ctx || M1 <= 0 || N1 <= 0 || M2 <= 0 || N2 <= 0) return sep;
+    Planned P1, P2;
+    GemmArgs a1 = fwd_args(M1, N1, K1, (const float *)A1, lda1, (const float *)B1, ldb1,
+                           (const float *)bias1, FG_ACT_NONE, (float *)C1, ldc1, (float *)Z1,
+                           ldz1, 0);
+    plan_quiet(ctx, FG_NN, a1, P1);
+    plan_quiet(ctx, FG_NN, fwd_args(M2, N2, K2, (const float *)A2, lda2, (const float *)B2, ldb2,
+                                    nullptr, FG_ACT_NONE, nullptr, N2, nullptr, 0, 0), P2);
+    return chainable(P1, P2) ? 2 : sep;
 }
 
 // Dispatches of gemm_dw_dx_f32 for these shapes: 1 (+1 per split GEMM) when

@@ -10,7 +10,16 @@ __global__ __launch_bounds__(kSkThreads) void gemm_f32_skinny(GemmArgs p) {
     gemm_f32_skinny_body<AK, BNC>(p, blockIdx.x);
 }
 
+// NN, A summed from the slices of the split GEMM `pre`.
+__global__ __launch_bounds__(kSkThreads) void gemm_f32_skinny_pre(GemmArgs p, GemmArgs pre) {
+    gemm_f32_skinny_pre_body(p, pre, blockIdx.x);
+}
+
 }  // namespace
+
+void launch_skinny_pre(const GemmArgs &a, const GemmArgs &pre, hipStream_t st) {
+    gemm_f32_skinny_pre<<<dim3(skinny_pre_workgroups(a.M)), dim3(kSkThreads), 0, st>>>(a, pre);
+}
 
 void launch_skinny(const GemmArgs &a, int layout, hipStream_t st) {
     const dim3 grid(skinny_workgroups(a.M)), block(kSkThreads);

@@ -454,7 +454,9 @@ def test_paired_gradient_gemms_match_separate_calls(ctx):
         desc = st.plan.describe()
         # Both backward variants (seed, CE-fused) pair both layers.
         assert desc.count("[with the next]") == 4, desc
-        assert "kernels per step: 8 (forward 3, loss 1, backward 3, optim 1)" in desc, desc
+        # The first layer's K slices are summed by the second layer's kernel.
+        assert "[K split: slices, summed by the next launch]" in desc, desc
+        assert "kernels per step: 7 (forward 2, loss 1, backward 3, optim 1)" in desc, desc
         X = fa.rng_uniform(0, 0, (B, 784))
         y = fa.rng_int(0, 1, (B,), 10)
         Ws = [fa.rng_uniform(0, 10 + l, (dims[l], dims[l + 1]), -math.sqrt(6 / dims[l]),
@@ -488,6 +490,73 @@ def test_paired_gradient_gemms_match_separate_calls(ctx):
         dW1, db1, dX = buf(784, 256), buf(256), buf(B, 784)
         own.gemm_dw(784, 256, B, x, 784, dZ1, 256, dW1, 256, colsum=db1)
         own.gemm_bwd(fa.NT, B, 784, 256, dZ1, 256, w1, 256, dX, 784)
+        own.sync()
+        ref = [dX, dW1, db1, dW2, db2]
+        for node, r in zip(in_nodes, ref):
+            assert np.array_equal(grads[node], r.cpu().numpy().reshape(-1)), node
+    finally:
+        if "st" in locals():
+            st.plan.close()
+        own.close()
+
+
+@pytest.mark.parametrize("k1,chained", [(768, True), (1000, False)],
+                         ids=["K768-chained", "K1000-13-slices"])
+def test_forward_chain_matches_separate_calls(ctx, k1, chained):
+    """A split-K first layer whose output feeds a skinny second layer: the
+    second layer's kernel sums the first's 12 K slices (slice order, bias,
+    GELU, Z and H written) instead of a summing kernel.  100 rows (a partial
+    last 16-row workgroup), 128 hidden, 12 classes.  With K = 1000 the first
+    layer takes 13 slices, more than the summing prologue loads, and the
+    plan falls back to the summing kernel.  An eager step through the plan
+    against single calls on a context with the plan's workspace size: the
+    loss and every gradient equal bit for bit."""
+    import ferrograd_amd as fa
+    G = api()
+    torch = pytest.importorskip("torch")
+    own = fa.Context(0, ctx.ctx.stream)
+    try:
+        own.reserve_workspace(1 << 20)
+        dims, B = [k1, 128, 12], 100
+        graph, meta, mb, st = build_mlp(ctx, dims, B, "gelu", G.Optim.sgd())
+        desc = st.plan.describe()
+        assert "[chained with the next]" in desc, desc
+        summed = "[K split: slices, summed by the next launch]" in desc
+        assert summed == chained, desc
+        assert ("summing kernel" in desc.split("loss:")[0]) != chained, desc
+        X = fa.rng_uniform(0, 0, (B, k1))
+        y = fa.rng_int(0, 1, (B,), 12)
+        Ws = [fa.rng_uniform(0, 10 + l, (dims[l], dims[l + 1]), -math.sqrt(6 / dims[l]),
+                             math.sqrt(6 / dims[l])) for l in range(2)]
+        bs = [(0.01 * np.arange(d) - 0.3).astype(f32) for d in dims[1:]]
+        ins = [ctx.init_tensor_f32(X.shape, X)]
+        for W, b in zip(Ws, bs):
+            ins += [ctx.init_tensor_f32(W.shape, W), ctx.init_tensor_f32(b.shape, b)]
+        tgt = ctx.new_onehot_init(y)
+        sch = ctx.schedule(graph.lower(meta), [G.f32_bits(0.01)] + mb[1:], ins, st)
+        ctx.dispatch_forward(sch)
+        ctx.dispatch_loss(sch, tgt)
+        ctx.dispatch_backward(sch)
+        ctx.sync()
+        grads = {t.node: ctx.download(t) for t in st.grad_tensors}
+        in_nodes = [i for i, nd in enumerate(graph.nodes) if nd.op == 0]
+        x, w1, b1, w2, b2 = ins
+
+        def buf(*shape):
+            return torch.empty(shape, device="cuda")
+        Z1, H1, L = buf(B, 128), buf(B, 128), buf(B, 12)
+        own.gemm(fa.NN, B, 128, k1, x, k1, w1, 128, H1, 128, bias=b1, act=fa.ACT_GELU, Z=Z1,
+                 ldz=128)
+        own.gemm(fa.NN, B, 12, 128, H1, 128, w2, 12, L, 12, bias=b2)
+        dl = buf(B, 12)
+        own.softmax_ce(L, 12, tgt, B, 12, 1.0, dlogits=dl, ldd=12)
+        dW2, db2, dZ1 = buf(128, 12), buf(12), buf(B, 128)
+        own.gemm_dw(128, 12, B, H1, 128, dl, 12, dW2, 12, colsum=db2)
+        own.gemm_bwd(fa.NT, B, 128, 12, dl, 12, w2, 12, dZ1, 128, act=fa.ACT_GELU, Zs=Z1,
+                     ldzs=128)
+        dW1, db1, dX = buf(k1, 128), buf(128), buf(B, k1)
+        own.gemm_dw(k1, 128, B, x, k1, dZ1, 128, dW1, 128, colsum=db1)
+        own.gemm_bwd(fa.NT, B, k1, 128, dZ1, 128, w1, 128, dX, k1)
         own.sync()
         ref = [dX, dW1, db1, dW2, db2]
         for node, r in zip(in_nodes, ref):
@@ -596,8 +665,8 @@ def test_captured_step_survives_workspace_growth(ctx):
         # second layer takes the skinny kernel; each layer's dW and dX share
         # a launch; a captured step leaves the softmax to the loss launch.
         fwd = desc.split("forward:")[1].split("loss:")[0]
-        assert fwd.count("[K split") == 1, desc
-        assert "kernels per step: 8 (forward 3, loss 1, backward 3, optim 1)" in desc, desc
+        assert fwd.count("[K split: slices, summed by the next launch]") == 1, desc
+        assert "kernels per step: 7 (forward 2, loss 1, backward 3, optim 1)" in desc, desc
         sch, st, ins, tgt = plans[1]
         call("fg_plan_bind_target", sch.plan.handle, tgt.data_ptr(), tgt.nbytes)
         call("fg_plan_capture_step", sch.plan.handle)
