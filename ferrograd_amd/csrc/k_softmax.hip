@@ -438,6 +438,118 @@ __global__ __launch_bounds__(kSmallNT) void softmax_ce_small(
     }
 }
 
+// Heads of at most kTinyCols columns (c1's ten classes) in the same one
+// workgroup: a row fits in one 16-lane row of a wave, so a wave takes four
+// rows at once and reduces each inside its 16 lanes with four DPP moves
+// (swap neighbours, swap pairs, half-row mirror, row mirror) -- register
+// moves, where the wave-per-row kernel above chains 19 LDS-routed shuffles
+// per row.  Each step combines a lane's value with another's by a
+// commutative operation, so every lane of a row ends with the same max,
+// argmax (first maximum) and sum, the sum always in the same order.  The
+// label's logit is the row sum of (column == label ? logit : 0), exact.
+// Row slot q (4 per wave, 64 in all) takes rows q, q + 64, ...; a wave
+// loads kSmallBatch rows per slot at once; the mean adds each slot's rows
+// in order (double), then the slots in order.  Outputs and conventions as
+// softmax_ce_small.
+constexpr int kTinyCols = 16;
+constexpr int kTinySlots = kSmallNT / kTinyCols;
+bool tiny_case(int R, int C) { return C <= kTinyCols && R <= kSmallRows; }
+
+// DPP controls within a row of 16 lanes: quad permutations [1,0,3,2] and
+// [2,3,0,1], the half-row mirror (lane i <-> 7 - i of each 8) and the row
+// mirror (lane i <-> 15 - i).
+constexpr int kDppSwap1 = 0xB1, kDppSwap2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
+}
+template <int CTRL>
+__device__ __forceinline__ void row16_step(float &s) {
+    s += dpp_f<CTRL>(s);
+}
+template <int CTRL>
+__device__ __forceinline__ void row16_step(float &m, int &am) {
+    argmax_combine(m, am, dpp_f<CTRL>(m), dpp_i<CTRL>(am));
+}
+// Sum / max and first argmax over the 16 lanes of each row (all lanes of
+// the wave active).
+__device__ __forceinline__ float row16_sum(float s) {
+    row16_step<kDppSwap1>(s);
+    row16_step<kDppSwap2>(s);
+    row16_step<kDppHalfMirror>(s);
+    row16_step<kDppMirror>(s);
+    return s;
+}
+__device__ __forceinline__ void row16_argmax(float &m, int &am) {
+    row16_step<kDppSwap1>(m, am);
+    row16_step<kDppSwap2>(m, am);
+    row16_step<kDppHalfMirror>(m, am);
+    row16_step<kDppMirror>(m, am);
+}
+
+template <int DT>
+__global__ __launch_bounds__(kSmallNT) void softmax_ce_tiny(
+    const void *__restrict__ x, int ldx, const uint32_t *__restrict__ labels, int R, int C,
+    float scale, float *__restrict__ row_loss, void *__restrict__ out, int ldo,
+    uint32_t *__restrict__ argmax, void *__restrict__ probs, int ldp, float *__restrict__ mean) {
+    __shared__ double sh[kTinySlots];
+    const int lane = threadIdx.x & 63, c = lane & (kTinyCols - 1);
+    const int q = lane / kTinyCols, w = threadIdx.x >> 6;
+    const int slot = w * (64 / kTinyCols) + q;
+    double acc = 0.0;  // this slot's row losses, in row order
+    // The wave's first slot bounds the loop, so all 64 lanes run every pass
+    // (the DPP moves read the other lanes of the row); rows past R compute
+    // and store nothing.
+    for (int b0 = w * (64 / kTinyCols); b0 < R; b0 += kTinySlots * kSmallBatch) {
+        const int r0 = b0 + q;
+        float v[kSmallBatch];
+        uint32_t t[kSmallBatch];
+#pragma unroll
+        for (int j = 0; j < kSmallBatch; ++j) {
+            const int r = r0 + j * kTinySlots;
+            v[j] = (r < R && c < C) ? small_load<DT>(x, (uint64_t)r * ldx + c) : -INFINITY;
+            t[j] = (r < R && labels) ? labels[r] : 0u;
+        }
+#pragma unroll
+        for (int j = 0; j < kSmallBatch; ++j) {
+            const int r = r0 + j * kTinySlots;
+            float m = v[j];
+            int am = c < C ? c : C;
+            row16_argmax(m, am);
+            const float e = c < C ? expf(v[j] - m) : 0.0f;
+            const float s = row16_sum(e);
+            const float xt = row16_sum((c < C && (uint32_t)c == t[j]) ? v[j] : 0.0f);
+            if (r >= R) continue;
+            if (argmax && c == 0) argmax[r] = (uint32_t)am;
+            if (row_loss || mean) {
+                const float l = (t[j] < (uint32_t)C) ? (m + logf(s)) - xt : __builtin_nanf("");
+                if (row_loss && c == 0) row_loss[r] = l;
+                acc += (double)l;
+            }
+            if ((out || probs) && c < C) {
+                const float pv = e * (1.0f / s);
+                if (out)
+                    small_store<DT>(out, (uint64_t)r * ldo + c,
+                                    scale * (labels && (uint32_t)c == t[j] ? pv - 1.0f : pv));
+                if (probs) small_store<DT>(probs, (uint64_t)r * ldp + c, pv);
+            }
+        }
+    }
+    if (!mean) return;
+    if (c == 0) sh[slot] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double tot = sh[0];
+        for (int k = 1; k < kTinySlots; ++k) tot += sh[k];
+        mean[0] = (float)(tot / (double)R);
+    }
+}
+
 // mean[0] = sum(vals[0..n)) / n in a fixed order (one block).
 __global__ __launch_bounds__(1024) void mean_kernel(const float *__restrict__ vals, int n,
                                                     float *__restrict__ mean) {
@@ -475,6 +587,20 @@ __global__ __launch_bounds__(kNT) void softmax_bwd_rows(const void *__restrict__
 // softmax.  With `mean` given and a small problem, the one-workgroup kernel
 // also writes the mean loss and *mean_done is set; otherwise the caller
 // reduces the row losses.
+// The one-workgroup kernels (small_case): 16-lane rows for heads of at
+// most kTinyCols columns, else a wave per row.
+template <int DT>
+void launch_small(hipStream_t st, const void *x, int ldx, const uint32_t *labels, int R, int C,
+                  float scale, float *row_loss, void *out, int ldo, uint32_t *argmax, void *probs,
+                  int ldp, float *mean) {
+    if (tiny_case(R, C))
+        softmax_ce_tiny<DT><<<1, kSmallNT, 0, st>>>(x, ldx, labels, R, C, scale, row_loss, out, ldo,
+                                                   argmax, probs, ldp, mean);
+    else
+        softmax_ce_small<DT><<<1, kSmallNT, 0, st>>>(x, ldx, labels, R, C, scale, row_loss, out,
+                                                    ldo, argmax, probs, ldp, mean);
+}
+
 int launch_rows(fg_ctx *ctx, int dt, const void *x, int ldx, const uint32_t *labels, int R, int C,
                 float scale, float *row_loss, void *out, int ldo, uint32_t *argmax,
                 void *probs = nullptr, int ldp = 0, float *mean = nullptr,
@@ -482,16 +608,15 @@ int launch_rows(fg_ctx *ctx, int dt, const void *x, int ldx, const uint32_t *lab
     hipStream_t st = ctx->stream;
     if (mean_done) *mean_done = false;
     if (small_case(R, C)) {
-#define FG_SMALL_LAUNCH(DT)                                                                  \
-    softmax_ce_small<DT><<<1, kSmallNT, 0, st>>>(x, ldx, labels, R, C, scale, row_loss, out, ldo, \
-                                            argmax, probs, ldp, mean)
         if (dt == fg::kF32)
-            FG_SMALL_LAUNCH(fg::kF32);
+            launch_small<fg::kF32>(st, x, ldx, labels, R, C, scale, row_loss, out, ldo, argmax,
+                                   probs, ldp, mean);
         else if (dt == fg::kBF16)
-            FG_SMALL_LAUNCH(fg::kBF16);
+            launch_small<fg::kBF16>(st, x, ldx, labels, R, C, scale, row_loss, out, ldo, argmax,
+                                    probs, ldp, mean);
         else
-            FG_SMALL_LAUNCH(fg::kF16);
-#undef FG_SMALL_LAUNCH
+            launch_small<fg::kF16>(st, x, ldx, labels, R, C, scale, row_loss, out, ldo, argmax,
+                                   probs, ldp, mean);
         FG_LAUNCH_CHECK("softmax_ce_small");
         if (mean_done) *mean_done = mean != nullptr;
         return FG_OK;

@@ -587,7 +587,8 @@ def test_softmax_ce_mean_across_paths(gpu_ctx):
     import ferrograd_amd as fa
     rng = np.random.default_rng(5)
     for R, C, dt in [(8192, 1000, None), (3, 10, None), (1, 32000, None), (600, 10, None),
-                     (257, 1000, fa.DTYPE_BF16), (2, 64, fa.DTYPE_BF16), (65, 20000, None)]:
+                     (1024, 16, None), (257, 1000, fa.DTYPE_BF16), (2, 64, fa.DTYPE_BF16),
+                     (37, 12, fa.DTYPE_BF16), (65, 20000, None)]:
         note(f"softmax_ce mean R={R} C={C} dtype={dt}")
         x = (2 * rng.standard_normal((R, C))).astype(f32)
         lab = rng.integers(0, C, R).astype(np.uint32)
@@ -609,7 +610,8 @@ def test_softmax_ce_fixture(gpu_ctx):
     check_softmax_ce(gpu_ctx, g["x"], g["labels"])
 
 
-@pytest.mark.parametrize("shape", [(64, 10), (1024, 64), (1025, 10), (5, 1), (7, 1024), (2048, 1000),
+@pytest.mark.parametrize("shape", [(64, 10), (1024, 16), (100, 16), (33, 17), (1024, 64), (1025, 10),
+                                   (5, 1), (7, 1024), (2048, 1000),
                                    (256, 32000), (16, 40000), (33, 4100), (5, 8192)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_softmax_ce_parity(gpu_ctx, shape):
