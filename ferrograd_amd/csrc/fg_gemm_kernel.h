@@ -311,6 +311,31 @@ __device__ __forceinline__ float epi_value(const GemmArgs &p, float v, float bv,
     return v;
 }
 
+// Split K: output (row, col) of the whole product -- the slots' raw
+// products summed in slot order, then the epilogue (splitk_reduce and the
+// summing blocks of the fused SGD launch, k_optim.hip).
+__device__ __forceinline__ void split_sum_store(const GemmArgs &p, int splits, int row, int col) {
+    const size_t mn = (size_t)p.M * p.N, i = (size_t)row * p.N + col;
+    float v = p.partial[i];
+    for (int s = 1; s < splits; ++s) v += p.partial[s * mn + i];
+    const float b = (p.mode == 0 && p.bias) ? p.bias[col] : 0.0f;
+    float z;
+    float o = epi_value(p, v, b, row, col, &z);
+    if (p.mode == 0 && p.Z) p.Z[(size_t)row * p.ldz + col] = z;
+    float *c = p.C + (size_t)row * p.ldc + col;
+    if (p.accumulate) o += *c;
+    *c = o;
+}
+
+// Blocks [0, nblocks) of a summing pass over M x N outputs, block b of them
+// (kThreads threads, grid-stride).
+__device__ __forceinline__ void split_sum_blocks(const GemmArgs &p, int splits, int b,
+                                                 int nblocks) {
+    const size_t mn = (size_t)p.M * p.N;
+    for (size_t i = (size_t)b * kThreads + threadIdx.x; i < mn; i += (size_t)nblocks * kThreads)
+        split_sum_store(p, splits, (int)(i / p.N), (int)(i % p.N));
+}
+
 // Four consecutive outputs of one row (the vector path of the epilogue):
 // the same operations as epi_value per element, with the uniform choices
 // (mode, activation, Z, accumulate) taken once per four.  Returns the four

@@ -1103,7 +1103,10 @@ int check_launch(const fg_plan &P, const Launch &L) {
 // ------------------------------------------------------------ execute
 // step: the launches belong to a whole captured step (forward through
 // optimiser), so the final forward softmax is left to the loss launch.
-int run(fg_plan &P, const std::vector<Launch> &list, bool step = false) {
+// defer_last: the summing launch of a split GEMM in the list's last launch
+// (or the pair or chain ending it) is held in the plan's context view for the
+// optimiser launch that follows (captured steps, run_optim).
+int run(fg_plan &P, const std::vector<Launch> &list, bool step = false, bool defer_last = false) {
     fg_ctx *ctx = &P.wctx;
     bool skip_next = false;  // the launch just run as the second of a pair
     for (const Launch &L : list) {
@@ -1112,6 +1115,8 @@ int run(fg_plan &P, const std::vector<Launch> &list, bool step = false) {
             skip_next = false;
             continue;
         }
+        const bool with_next = (L.pair_next || L.chain_next) && &L + 1 < list.data() + list.size();
+        ctx->defer_reduce = defer_last && &L + (with_next ? 1 : 0) == &list.back();
         if (step && L.elidable) continue;
         if (L.chain_next && &L + 1 < list.data() + list.size()) {
             const Launch &X = *(&L + 1);  // reads L's output as its A operand
@@ -1218,6 +1223,7 @@ int run(fg_plan &P, const std::vector<Launch> &list, bool step = false) {
         }
         if (rc != FG_OK) return rc;
     }
+    ctx->defer_reduce = false;
     return FG_OK;
 }
 
@@ -1264,7 +1270,32 @@ int ensure_mt(fg_plan &P) {
     return FG_OK;
 }
 
+// The memory the optimiser touches: every optimised input and its gradient.
+std::vector<fg::ByteRange> optim_ranges(const fg_plan &P) {
+    std::vector<fg::ByteRange> r;
+    for (uint32_t idx : P.opt_inputs) {
+        const uint32_t n = P.inputs[idx];
+        const uint64_t bytes = (uint64_t)P.shape[n].numel() * esize(P.dtype[n]);
+        for (const void *q : {P.ptr(P.input_slot[idx]), P.ptr(P.grad_slot[n])})
+            r.push_back({(uintptr_t)q, (uintptr_t)q + bytes});
+    }
+    return r;
+}
+
 int run_optim(fg_plan &P, fg_mt *mt) {
+    // A summing launch held back by the backward (captured steps): beside
+    // SGD in one launch when the two touch disjoint memory, else first.
+    if (P.wctx.pending_splits > 0) {
+        bool fuse = mt && P.g.optim == FG_OPTIM_SGD;
+        if (fuse) {
+            fg::ByteRange red[3];
+            fg::pending_reduce_ranges(&P.wctx, red);
+            for (const fg::ByteRange &o : optim_ranges(P))
+                for (const fg::ByteRange &q : red) fuse = fuse && !q.overlaps(o);
+        }
+        if (fuse) return fg::sgd_step_with_pending(P.ctx, mt, P.lr, 1, &P.wctx);
+        if (int rc = fg::launch_pending_reduce(&P.wctx)) return rc;
+    }
     if (!mt) return FG_OK;
     if (P.g.optim == FG_OPTIM_ADAM)
         return fg::mt_adam_dev(P.ctx, mt, P.lr, P.b1, P.b2, P.eps, P.ptr(P.adam_slot), 0);
@@ -1820,8 +1851,13 @@ FG_API int fg_plan_capture_step(fg_plan *p) {
     FG_HIP(hipStreamBeginCapture(p->ctx->stream, hipStreamCaptureModeThreadLocal));
     rc = run(*p, p->fwd, true);
     if (rc == FG_OK) rc = run(*p, p->loss, true);
-    if (rc == FG_OK) rc = run(*p, p->ce_fused_possible ? p->bwd_fused : p->bwd_seed);
+    // The backward's last summing launch may share the SGD launch.
+    if (rc == FG_OK)
+        rc = run(*p, p->ce_fused_possible ? p->bwd_fused : p->bwd_seed, false,
+                 p->g.optim == FG_OPTIM_SGD && p->mt_all);
     if (rc == FG_OK) rc = run_optim(*p, p->mt_all);
+    p->wctx.defer_reduce = false;
+    if (rc != FG_OK) p->wctx.pending_splits = 0;
     hipGraph_t graph = nullptr;
     hipError_t e = hipStreamEndCapture(p->ctx->stream, &graph);
     if (rc != FG_OK) {
@@ -2043,7 +2079,31 @@ FG_API int fg_plan_describe(const fg_plan *p, char *buf, size_t len, size_t *nee
     s += "optim: " + std::string(adam ? "adam" : "sgd") + " over " +
          std::to_string(p->opt_inputs.size()) + " inputs, 1 multi-tensor launch\n";
     const int k_opt = p->opt_inputs.empty() ? 0 : (adam ? 2 : 1);
-    const int k_bwd = kernels(p->ce_fused_possible ? p->bwd_fused : p->bwd_seed);
+    const std::vector<Launch> &bwd = p->ce_fused_possible ? p->bwd_fused : p->bwd_seed;
+    int k_bwd = kernels(bwd);
+    // A captured SGD step runs the backward's last summing launch beside the
+    // SGD update (run_optim), when the two touch disjoint memory.
+    if (!adam && wc && !p->opt_inputs.empty() && !bwd.empty()) {
+        const Launch &X = bwd.back();
+        const Launch *L = bwd.size() >= 2 && bwd[bwd.size() - 2].pair_next ? &bwd[bwd.size() - 2]
+                                                                           : nullptr;
+        const Launch *H = gemm_dispatches(X) > 1 ? &X : L && gemm_dispatches(*L) > 1 ? L : nullptr;
+        if (H) {
+            auto slot_range = [&](int slot) {
+                const uintptr_t b0 = (uintptr_t)p->ptr(slot);
+                return fg::ByteRange{b0, b0 + p->slots[slot].bytes};
+            };
+            std::vector<fg::ByteRange> held = {slot_range(H->sC)};
+            if (H->kind == LK_GEMM_BWD && H->act != FG_ACT_NONE) held.push_back(slot_range(H->sZ));
+            bool shared = true;
+            for (const fg::ByteRange &o : optim_ranges(*p))
+                for (const fg::ByteRange &q : held) shared = shared && !q.overlaps(o);
+            if (shared) {
+                --k_bwd;
+                s += "(captured step: the backward's last summing launch shares the SGD launch)\n";
+            }
+        }
+    }
     s += "kernels per step: " +
          std::to_string(kernels(p->fwd) + kernels(p->loss) + k_bwd + k_opt) +
          " (forward " + std::to_string(kernels(p->fwd)) + ", loss " +

@@ -38,6 +38,13 @@ struct fg_ctx {
     // Set on a plan's own view of its context: ws is a fixed part of the
     // plan's arena and fg::workspace() never replaces it.
     bool ws_fixed = false;
+    // The planner's captured steps: with defer_reduce set, the next split-K
+    // summing launch is not launched but held here (its GemmArgs and slice
+    // count), for the optimiser launch that follows to run beside its own
+    // work (fg::sgd_step_with_pending) or to launch first.
+    bool defer_reduce = false;
+    int pending_splits = 0;
+    alignas(16) unsigned char pending[256];
 };
 
 struct fg_buf {
@@ -47,6 +54,25 @@ struct fg_buf {
 };
 
 namespace fg {
+// [begin, end) of device memory, as addresses.
+struct ByteRange {
+    uintptr_t begin, end;
+    bool overlaps(const ByteRange &o) const {
+        return begin < end && o.begin < o.end && begin < o.end && o.begin < end;
+    }
+};
+
+// The held split-K summing launch (fg_ctx::pending, k_gemm.hip): its block
+// count for M x N outputs, a launch of it alone (clears it), and the memory
+// it writes (C) and reads besides its slices (act' operand, bias).
+int reduce_blocks(const fg_ctx *ctx, int M, int N);
+int launch_pending_reduce(fg_ctx *ctx);
+void pending_reduce_ranges(const fg_ctx *ctx, ByteRange out[3]);
+// SGD over `mt` with the summing launch held in `held` (a plan's context
+// view) run by extra workgroups of the same launch (k_optim.hip); the
+// caller has checked that the two touch disjoint memory.  Clears it.
+int sgd_step_with_pending(fg_ctx *ctx, fg_mt *mt, float lr, int zero_grad, fg_ctx *held);
+
 // Returns a workspace pointer of at least `bytes`, or nullptr with the error
 // set.  A context's workspace grows by allocating a larger one; the old one
 // is retired, not freed (captured graphs may use it).  A fixed workspace (a

@@ -5,12 +5,14 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstring>
 
 #include "fg_bias_grad.h"
 #include "fg_gemm_kernel.h"
 #include "fg_gemm_skinny.h"
 #include "fg_half.h"
 #include "fg_internal.h"
+#include "fg_optim.h"
 
 namespace {
 
@@ -67,20 +69,21 @@ int pick_cfg(int layout, int M, int N, int K, int cus) {
 // epilogue (fg_gemm_kernel.h epi_value), so bias / activation / Z / act' /
 // accumulate behave alike.  Deterministic: the slot order is fixed.
 __global__ __launch_bounds__(kThreads) void splitk_reduce(GemmArgs p, int splits) {
-    const size_t mn = (size_t)p.M * p.N;
-    for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < mn;
-         i += (size_t)gridDim.x * kThreads) {
-        const int row = (int)(i / p.N), col = (int)(i % p.N);
-        float v = p.partial[i];
-        for (int s = 1; s < splits; ++s) v += p.partial[s * mn + i];
-        const float b = (p.mode == 0 && p.bias) ? p.bias[col] : 0.0f;
-        float z;
-        float o = fg::gemm::epi_value(p, v, b, row, col, &z);
-        if (p.mode == 0 && p.Z) p.Z[(size_t)row * p.ldz + col] = z;
-        float *c = p.C + (size_t)row * p.ldc + col;
-        if (p.accumulate) o += *c;
-        *c = o;
-    }
+    fg::gemm::split_sum_blocks(p, splits, blockIdx.x, gridDim.x);
+}
+
+// SGD over a tensor list (workgroups below nchunks, one chunk each) and a
+// held split-K summing pass (the rest) in one launch: independent work
+// (the caller has checked that they touch disjoint memory), each part
+// exactly as its own kernel does it.
+static_assert(fg::optim::kThreads == kThreads, "one block size for both parts");
+__global__ __launch_bounds__(kThreads) void sgd_and_split_sum(
+    const fg::optim::MTTensor *__restrict__ tensors, const fg::optim::MTChunk *__restrict__ chunks,
+    float lr, int zero_grad, int vec, uint32_t nchunks, GemmArgs red, int splits) {
+    if (blockIdx.x < nchunks)
+        fg::optim::sgd_chunk(tensors, chunks, lr, zero_grad, vec, blockIdx.x);
+    else
+        fg::gemm::split_sum_blocks(red, splits, blockIdx.x - nchunks, gridDim.x - nchunks);
 }
 
 // Split K over workgroup rows when the output gives few tiles (under half
@@ -213,10 +216,14 @@ int gemm_prepare(fg_ctx *ctx, int layout, const GemmArgs &a0, const char *who, i
 }
 
 void launch_reduce(fg_ctx *ctx, const GemmArgs &a, int splits) {
-    const size_t mn = (size_t)a.M * a.N;
-    const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
-    const int grid = (int)std::min<size_t>((mn + kThreads - 1) / kThreads, 4 * (size_t)cus);
-    splitk_reduce<<<grid, kThreads, 0, ctx->stream>>>(a, splits);
+    if (ctx->defer_reduce) {  // held for the optimiser launch that follows
+        static_assert(sizeof(GemmArgs) <= sizeof(ctx->pending), "pending summing launch");
+        std::memcpy(ctx->pending, &a, sizeof a);
+        ctx->pending_splits = splits;
+        ctx->defer_reduce = false;
+        return;
+    }
+    splitk_reduce<<<fg::reduce_blocks(ctx, a.M, a.N), kThreads, 0, ctx->stream>>>(a, splits);
 }
 
 // reduce: launch the summing kernel of a split GEMM (false: its consumer
@@ -275,6 +282,50 @@ void pair_grid(Planned &P, int &x, int &n) {
 }  // namespace
 
 namespace fg {
+int reduce_blocks(const fg_ctx *ctx, int M, int N) {
+    const size_t mn = (size_t)M * N;
+    const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    return (int)std::min<size_t>((mn + kThreads - 1) / kThreads, 4 * (size_t)cus);
+}
+
+int launch_pending_reduce(fg_ctx *ctx) {
+    if (ctx->pending_splits <= 0) return FG_OK;
+    GemmArgs a;
+    std::memcpy(&a, ctx->pending, sizeof a);
+    const int splits = ctx->pending_splits;
+    ctx->pending_splits = 0;
+    splitk_reduce<<<reduce_blocks(ctx, a.M, a.N), kThreads, 0, ctx->stream>>>(a, splits);
+    FG_LAUNCH_CHECK("splitk_reduce");
+    return FG_OK;
+}
+
+int sgd_step_with_pending(fg_ctx *ctx, fg_mt *mt, float lr, int zero_grad, fg_ctx *held) {
+    FG_REQUIRE(ctx && mt && held, FG_ERR_INVALID_ARGUMENT, "sgd_step_with_pending: NULL argument");
+    if (held->pending_splits <= 0) return fg_sgd_step(ctx, mt, lr, zero_grad);
+    FG_HIP(hipSetDevice(ctx->device));
+    GemmArgs a;
+    std::memcpy(&a, held->pending, sizeof a);
+    const int splits = held->pending_splits;
+    held->pending_splits = 0;
+    const int nred = reduce_blocks(held, a.M, a.N);
+    sgd_and_split_sum<<<mt->nchunks + nred, kThreads, 0, ctx->stream>>>(
+        mt->d_tensors, mt->d_chunks, lr, zero_grad, mt->vec, mt->nchunks, a, splits);
+    FG_LAUNCH_CHECK("sgd_and_split_sum");
+    return FG_OK;
+}
+
+void pending_reduce_ranges(const fg_ctx *ctx, ByteRange out[3]) {
+    GemmArgs a;
+    std::memcpy(&a, ctx->pending, sizeof a);
+    const uintptr_t rows = a.M > 0 ? (uintptr_t)(a.M - 1) : 0;
+    out[0] = {(uintptr_t)a.C, (uintptr_t)(a.C + rows * a.ldc + a.N)};
+    out[1] = a.mode == 1 && a.act != FG_ACT_NONE && a.Zs
+                 ? ByteRange{(uintptr_t)a.Zs, (uintptr_t)(a.Zs + rows * a.ldzs + a.N)}
+                 : ByteRange{0, 0};
+    out[2] = a.mode == 0 && a.bias ? ByteRange{(uintptr_t)a.bias, (uintptr_t)(a.bias + a.N)}
+                                   : ByteRange{0, 0};
+}
+
 int gemm_f32_dispatches(fg_ctx *ctx, int layout, int M, int N, int K, const void *A, int lda,
                         const void *B, int ldb, bool colsum) {
     if (!ctx || M <= 0 || N <= 0) return 1;  // no workspace (or nothing to do): no split
