@@ -604,9 +604,8 @@ int lower_forward(fg_plan &P) {
                           X.dtype == FG_DTYPE_F32 && L.layout == FG_NN && X.layout == FG_NN;
         if (gemm && X.sA == L.sC && X.lda == L.ldc && X.K == L.N && X.M == L.M &&
             !L.accumulate) {
-            L.chain_next = true;
-            L.desc += " [chained with the next]";
-            ++i;  // a launch is the second of at most one chain
+            L.chain_next = true;  // described where it chains (fg_plan_describe)
+            ++i;                  // a launch is the second of at most one chain
         }
     }
     return FG_OK;

@@ -520,7 +520,6 @@ def test_forward_chain_matches_separate_calls(ctx, k1, chained):
         dims, B = [k1, 128, 12], 100
         graph, meta, mb, st = build_mlp(ctx, dims, B, "gelu", G.Optim.sgd())
         desc = st.plan.describe()
-        assert "[chained with the next]" in desc, desc
         summed = "[K split: slices, summed by the next launch]" in desc
         assert summed == chained, desc
         assert ("summing kernel" in desc.split("loss:")[0]) != chained, desc
