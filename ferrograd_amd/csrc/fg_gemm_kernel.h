@@ -1136,8 +1136,14 @@ void launch_skinny(const GemmArgs &a, int layout, hipStream_t st);
 // kernel followed by launch_skinny.  Conditions on the host
 // (fg::gemm_fwd_chain_f32): pre splits into at most kSkPreMaxSlices slices,
 // its N (a.K) is a multiple of 4 and pre.vec_out holds.
+// With `ce` (fg_internal.h) the kernel also finishes the softmax + CE of
+// the rows it computes (a head of at most 16 columns).
 constexpr int kSkPreMaxSlices = 12;
-void launch_skinny_pre(const GemmArgs &a, const GemmArgs &pre, hipStream_t st);
+}  // namespace gemm
+struct CeOut;
+namespace gemm {
+void launch_skinny_pre(const GemmArgs &a, const GemmArgs &pre, hipStream_t st,
+                       const CeOut *ce = nullptr);
 
 // A layer's dW (TN, GEMM 1) and dX (NT, GEMM 2) in one launch
 // (k_gemm_pair.hip): kinds of the kernels they would take alone, which must

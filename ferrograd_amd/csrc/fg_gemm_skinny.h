@@ -11,6 +11,8 @@
 #pragma once
 
 #include "fg_gemm_kernel.h"
+#include "fg_internal.h"
+#include "fg_softmax_row.h"
 
 namespace fg {
 namespace gemm {
@@ -156,12 +158,22 @@ __device__ __forceinline__ void gemm_f32_skinny_body(GemmArgs p, int bx) {
 // gemm_f32_skinny_body.  Host conditions (fg::gemm_fwd_chain_f32): at most
 // kSkPreMaxSlices slices, pre's N (this GEMM's K) a multiple of 4, pre's
 // rows 16-byte aligned (pre.vec_out).
+//
+// With CE the outputs are a head's logits (N <= 16 columns, forward
+// epilogue, no accumulation) and the workgroup also finishes the softmax +
+// cross-entropy of its rows: wave 0 holds them as four 16-lane row groups
+// and runs the one-workgroup loss kernel's row code (fg::smrow::ce_row16),
+// writing dlogits, the row losses and the probabilities exactly as that
+// kernel would from the stored logits.
 constexpr int kSpRows = 4;
 static_assert(kSpRows * kSkinnyK == 4 * kSkThreads, "one float4 of A per thread");
 inline int skinny_pre_workgroups(int M) { return (M + kSpRows - 1) / kSpRows; }
 
+template <bool CE = false>
 __device__ __forceinline__ void gemm_f32_skinny_pre_body(const GemmArgs &p, const GemmArgs &pre,
-                                                         int bx) {
+                                                         int bx, const CeOut &ce) {
+    static_assert(kSkinnyN == smrow::kCols && kSpRows * smrow::kCols == 64,
+                  "one wave holds the workgroup's rows as 16-lane groups");
     __shared__ float As[kSkinnyK * kSpRows];  // As[k][r]
     __shared__ __attribute__((aligned(16))) float Bs[kSkinnyK * kSkinnyN];
     __shared__ float red[kSkGroups * kSkinnyN * kSpRows];
@@ -231,6 +243,7 @@ __device__ __forceinline__ void gemm_f32_skinny_pre_body(const GemmArgs &p, cons
     __syncthreads();
 
     // Epilogue: thread (r, n) finishes output (m0 + r, n).
+    __shared__ float logits[CE ? kSpRows * kSkinnyN : 1];
     if (t < kSpRows * kSkinnyN) {
         const int rr = t % kSpRows, col = t / kSpRows;
         const int orow = m0 + rr;
@@ -245,6 +258,18 @@ __device__ __forceinline__ void gemm_f32_skinny_pre_body(const GemmArgs &p, cons
             float *c = p.C + (size_t)orow * p.ldc + col;
             if (p.accumulate) o += *c;
             *c = o;
+            if constexpr (CE) logits[rr * kSkinnyN + col] = o;
+        }
+    }
+    if constexpr (CE) {
+        __syncthreads();
+        if (t < 64) {  // wave 0: lane 16 r + c holds column c of local row r
+            const int r = t / smrow::kCols, c = t % smrow::kCols, row = m0 + r;
+            const bool valid = row < p.M;
+            const float v = (valid && c < p.N) ? logits[r * kSkinnyN + c] : -INFINITY;
+            const uint32_t lab = valid ? ce.labels[row] : 0u;
+            (void)smrow::ce_row16<kF32>(v, lab, c, p.N, row, valid, true, ce.scale, ce.row_loss,
+                                        ce.dlogits, ce.ldd, nullptr, ce.probs, ce.ldp, true);
         }
     }
 }

@@ -1102,10 +1102,32 @@ int check_launch(const fg_plan &P, const Launch &L) {
 // ------------------------------------------------------------ execute
 // step: the launches belong to a whole captured step (forward through
 // optimiser), so the final forward softmax is left to the loss launch.
+// The loss of a captured SGD step finished in its head GEMM: the plan's one
+// loss launch, an fp32 softmax + CE on the 16-lane row path, whose logits
+// are the whole output of the second GEMM of a forward chain.  Returns the
+// index in fwd of the chain's first launch, or -1.  (Whether the chain
+// chains is decided when it runs, fg::gemm_fwd_chain_f32.)
+int head_loss_chain(const fg_plan &P) {
+    if (P.g.optim != FG_OPTIM_SGD || P.opt_inputs.empty() || P.loss.size() != 1) return -1;
+    const Launch &S = P.loss[0];
+    if (S.kind != LK_SMCE || S.dtype != FG_DTYPE_F32 || !fg::softmax_ce_row16_case(S.M, S.N))
+        return -1;
+    for (size_t i = 0; i + 1 < P.fwd.size(); ++i) {
+        const Launch &L = P.fwd[i], &X = P.fwd[i + 1];
+        if (L.chain_next && X.sC == S.sA && X.act == FG_ACT_NONE && !X.accumulate &&
+            X.M == S.M && X.N == S.N && X.ldc == S.N)
+            return (int)i;
+    }
+    return -1;
+}
+
 // defer_last: the summing launch of a split GEMM in the list's last launch
 // (or the pair or chain ending it) is held in the plan's context view for the
-// optimiser launch that follows (captured steps, run_optim).
-int run(fg_plan &P, const std::vector<Launch> &list, bool step = false, bool defer_last = false) {
+// optimiser launch that follows (captured steps, run_optim).  ce_loss: the
+// loss launch that the chain producing its logits may finish (head_loss_chain);
+// *ce_done tells whether it did.
+int run(fg_plan &P, const std::vector<Launch> &list, bool step = false, bool defer_last = false,
+        const Launch *ce_loss = nullptr, bool *ce_done = nullptr) {
     fg_ctx *ctx = &P.wctx;
     bool skip_next = false;  // the launch just run as the second of a pair
     for (const Launch &L : list) {
@@ -1119,12 +1141,22 @@ int run(fg_plan &P, const std::vector<Launch> &list, bool step = false, bool def
         if (step && L.elidable) continue;
         if (L.chain_next && &L + 1 < list.data() + list.size()) {
             const Launch &X = *(&L + 1);  // reads L's output as its A operand
+            fg::CeOut ce{};
+            const bool want_ce = ce_loss && ce_done && X.sC == ce_loss->sA;
+            if (want_ce) {
+                const Launch &S = *ce_loss;
+                FG_REQUIRE(P.ptr(S.sZ), FG_ERR_INVALID_ARGUMENT,
+                           "dispatch_loss: no target bound (fg_plan_bind_target)");
+                ce = {(const uint32_t *)P.ptr(S.sZ), (float *)P.ptr(S.sB), (float *)P.ptr(S.sC),
+                      step ? (float *)P.ptr(S.sProbs) : nullptr, S.N, S.N, 1.0f};
+            }
             rc = fg::gemm_fwd_chain_f32(
                 ctx, L.M, L.N, L.K, (const float *)P.ptr(L.sA), L.lda, (const float *)P.ptr(L.sB),
                 L.ldb, (const float *)P.ptr(L.sBias), L.act, (float *)P.ptr(L.sC), L.ldc,
                 (float *)P.ptr(L.sZ), L.ldz, X.M, X.N, X.K, (const float *)P.ptr(X.sA), X.lda,
                 (const float *)P.ptr(X.sB), X.ldb, (const float *)P.ptr(X.sBias), X.act,
-                (float *)P.ptr(X.sC), X.ldc, (float *)P.ptr(X.sZ), X.ldz, X.accumulate);
+                (float *)P.ptr(X.sC), X.ldc, (float *)P.ptr(X.sZ), X.ldz, X.accumulate,
+                want_ce ? &ce : nullptr, want_ce ? ce_done : nullptr);
             if (rc != FG_OK) return rc;
             skip_next = true;
             continue;
@@ -1282,18 +1314,25 @@ std::vector<fg::ByteRange> optim_ranges(const fg_plan &P) {
 }
 
 int run_optim(fg_plan &P, fg_mt *mt) {
-    // A summing launch held back by the backward (captured steps): beside
-    // SGD in one launch when the two touch disjoint memory, else first.
+    // Work held for this launch (captured steps): the backward's last
+    // summing pass, beside SGD when the two touch disjoint memory, else
+    // first; the mean loss of a loss finished in the head GEMM, beside SGD
+    // (it touches only the loss buffers), else first.
+    const bool sgd = mt && P.g.optim == FG_OPTIM_SGD;
     if (P.wctx.pending_splits > 0) {
-        bool fuse = mt && P.g.optim == FG_OPTIM_SGD;
+        bool fuse = sgd;
         if (fuse) {
             fg::ByteRange red[3];
             fg::pending_reduce_ranges(&P.wctx, red);
             for (const fg::ByteRange &o : optim_ranges(P))
                 for (const fg::ByteRange &q : red) fuse = fuse && !q.overlaps(o);
         }
-        if (fuse) return fg::sgd_step_with_pending(P.ctx, mt, P.lr, 1, &P.wctx);
-        if (int rc = fg::launch_pending_reduce(&P.wctx)) return rc;
+        if (!fuse)
+            if (int rc = fg::launch_pending_reduce(&P.wctx)) return rc;
+    }
+    if (P.wctx.pending_splits > 0 || P.wctx.mean_dst) {
+        if (sgd) return fg::sgd_step_with_pending(P.ctx, mt, P.lr, 1, &P.wctx);
+        if (int rc = fg::launch_pending_mean(&P.wctx)) return rc;
     }
     if (!mt) return FG_OK;
     if (P.g.optim == FG_OPTIM_ADAM)
@@ -1848,15 +1887,29 @@ FG_API int fg_plan_capture_step(fg_plan *p) {
     drop_graph(*p);
     FG_HIP(hipStreamSynchronize(p->ctx->stream));
     FG_HIP(hipStreamBeginCapture(p->ctx->stream, hipStreamCaptureModeThreadLocal));
-    rc = run(*p, p->fwd, true);
-    if (rc == FG_OK) rc = run(*p, p->loss, true);
+    // With SGD the head GEMM may finish the loss (its mean then runs in the
+    // SGD launch).
+    const int hc = head_loss_chain(*p);
+    bool ce_done = false;
+    rc = run(*p, p->fwd, true, false, hc >= 0 ? &p->loss[0] : nullptr, &ce_done);
+    if (rc == FG_OK && ce_done) {
+        const Launch &S = p->loss[0];
+        p->wctx.mean_src = (const float *)p->ptr(S.sB);
+        p->wctx.mean_dst = (float *)p->ptr(S.sBias);
+        p->wctx.mean_rows = S.M;
+    } else if (rc == FG_OK) {
+        rc = run(*p, p->loss, true);
+    }
     // The backward's last summing launch may share the SGD launch.
     if (rc == FG_OK)
         rc = run(*p, p->ce_fused_possible ? p->bwd_fused : p->bwd_seed, false,
                  p->g.optim == FG_OPTIM_SGD && p->mt_all);
     if (rc == FG_OK) rc = run_optim(*p, p->mt_all);
     p->wctx.defer_reduce = false;
-    if (rc != FG_OK) p->wctx.pending_splits = 0;
+    if (rc != FG_OK) {
+        p->wctx.pending_splits = 0;
+        p->wctx.mean_dst = nullptr;
+    }
     hipGraph_t graph = nullptr;
     hipError_t e = hipStreamEndCapture(p->ctx->stream, &graph);
     if (rc != FG_OK) {
@@ -2080,6 +2133,13 @@ FG_API int fg_plan_describe(const fg_plan *p, char *buf, size_t len, size_t *nee
     const int k_opt = p->opt_inputs.empty() ? 0 : (adam ? 2 : 1);
     const std::vector<Launch> &bwd = p->ce_fused_possible ? p->bwd_fused : p->bwd_seed;
     int k_bwd = kernels(bwd);
+    int k_loss = kernels(p->loss);
+    // A captured SGD step may finish the loss in the head GEMM.
+    if (const int hc = head_loss_chain(*p); hc >= 0 && wc &&
+                                            chain_dispatches(p->fwd[hc], p->fwd[hc + 1]) == 2) {
+        k_loss = 0;
+        s += "(captured step: the head GEMM finishes the loss; its mean runs in the SGD launch)\n";
+    }
     // A captured SGD step runs the backward's last summing launch beside the
     // SGD update (run_optim), when the two touch disjoint memory.
     if (!adam && wc && !p->opt_inputs.empty() && !bwd.empty()) {
@@ -2104,9 +2164,9 @@ FG_API int fg_plan_describe(const fg_plan *p, char *buf, size_t len, size_t *nee
         }
     }
     s += "kernels per step: " +
-         std::to_string(kernels(p->fwd) + kernels(p->loss) + k_bwd + k_opt) +
+         std::to_string(kernels(p->fwd) + k_loss + k_bwd + k_opt) +
          " (forward " + std::to_string(kernels(p->fwd)) + ", loss " +
-         std::to_string(kernels(p->loss)) + ", backward " + std::to_string(k_bwd) +
+         std::to_string(k_loss) + ", backward " + std::to_string(k_bwd) +
          ", optim " + std::to_string(k_opt) + ")\n";
     s += "arena: " + std::to_string(p->arena_bytes) + " bytes\n";
     if (needed) *needed = s.size() + 1;

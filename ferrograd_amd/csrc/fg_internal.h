@@ -45,6 +45,12 @@ struct fg_ctx {
     bool defer_reduce = false;
     int pending_splits = 0;
     alignas(16) unsigned char pending[256];
+    // A mean loss left by a loss finished in the head GEMM (captured steps):
+    // mean_dst = mean of mean_rows row losses at mean_src, for the optimiser
+    // launch to compute (or fg::launch_pending_mean).
+    const float *mean_src = nullptr;
+    float *mean_dst = nullptr;
+    int mean_rows = 0;
 };
 
 struct fg_buf {
@@ -54,6 +60,18 @@ struct fg_buf {
 };
 
 namespace fg {
+// A captured step's softmax + CE loss finished by the skinny head GEMM that
+// computes its logits (fg_gemm_skinny.h, fg_softmax_row.h): labels, and
+// where it writes (probs may be NULL).  The mean is left to a later launch.
+struct CeOut {
+    const uint32_t *labels;
+    float *row_loss;
+    float *dlogits;
+    float *probs;
+    int ldd, ldp;
+    float scale;
+};
+
 // [begin, end) of device memory, as addresses.
 struct ByteRange {
     uintptr_t begin, end;
@@ -68,9 +86,12 @@ struct ByteRange {
 int reduce_blocks(const fg_ctx *ctx, int M, int N);
 int launch_pending_reduce(fg_ctx *ctx);
 void pending_reduce_ranges(const fg_ctx *ctx, ByteRange out[3]);
-// SGD over `mt` with the summing launch held in `held` (a plan's context
-// view) run by extra workgroups of the same launch (k_optim.hip); the
-// caller has checked that the two touch disjoint memory.  Clears it.
+// The held mean loss (fg_ctx::mean_*) in a launch of its own; clears it.
+int launch_pending_mean(fg_ctx *ctx);
+// SGD over `mt` with the summing launch and / or the mean loss held in
+// `held` (a plan's context view) run by extra workgroups of the same launch
+// (k_gemm.hip); the caller has checked that the held summing pass and the
+// SGD update touch disjoint memory.  Clears what it runs.
 int sgd_step_with_pending(fg_ctx *ctx, fg_mt *mt, float lr, int zero_grad, fg_ctx *held);
 
 // Returns a workspace pointer of at least `bytes`, or nullptr with the error
@@ -102,6 +123,9 @@ int softmax_ce_ex(fg_ctx *ctx, int dtype, const void *d_logits, int ldx, const u
 
 // Kernel dispatches of softmax_ce_ex for R x C (with or without the mean).
 int softmax_ce_dispatches(int R, int C, bool mean);
+// R x C takes the 16-lane row kernel (fg_softmax_row.h), whose row code the
+// skinny head GEMM can run in a captured step.
+bool softmax_ce_row16_case(int R, int C);
 
 // Elementwise program launch (k_eltwise_prog.hip).
 struct EltProgram;
@@ -124,11 +148,15 @@ int gemm_dw_dx_dispatches(fg_ctx *ctx, int M1, int N1, int K1, const void *A1, i
 // its A operand: when the first splits K and the second takes the skinny
 // kernel, the second sums the first's slices (k_gemm.hip); and the dispatch
 // count of that call.
+// With `ce` (a loss over the second GEMM's output, at most 16 columns and
+// 1024 rows, no accumulation) the chained kernel also finishes that loss and
+// *ce_done is set; otherwise *ce_done stays false and the caller runs it.
 int gemm_fwd_chain_f32(fg_ctx *ctx, int M1, int N1, int K1, const float *A1, int lda1,
                        const float *B1, int ldb1, const float *bias1, int act1, float *C1,
                        int ldc1, float *Z1, int ldz1, int M2, int N2, int K2, const float *A2,
                        int lda2, const float *B2, int ldb2, const float *bias2, int act2,
-                       float *C2, int ldc2, float *Z2, int ldz2, int acc2);
+                       float *C2, int ldc2, float *Z2, int ldz2, int acc2,
+                       const CeOut *ce = nullptr, bool *ce_done = nullptr);
 int gemm_fwd_chain_dispatches(fg_ctx *ctx, int M1, int N1, int K1, const void *A1, int lda1,
                               const void *B1, int ldb1, const void *bias1, void *C1, int ldc1,
                               void *Z1, int ldz1, int M2, int N2, int K2, const void *A2, int lda2,

@@ -13,6 +13,7 @@
 #include "fg_half.h"
 #include "fg_internal.h"
 #include "fg_optim.h"
+#include "fg_softmax_row.h"
 
 namespace {
 
@@ -76,14 +77,28 @@ __global__ __launch_bounds__(kThreads) void splitk_reduce(GemmArgs p, int splits
 // held split-K summing pass (the rest) in one launch: independent work
 // (the caller has checked that they touch disjoint memory), each part
 // exactly as its own kernel does it.
-static_assert(fg::optim::kThreads == kThreads, "one block size for both parts");
+// The last workgroup (with mean_dst) computes a held mean loss as the
+// one-workgroup loss kernel would.
+static_assert(fg::optim::kThreads == kThreads, "one block size for every part");
+static_assert(kThreads >= fg::smrow::kSlots, "the mean's slots");
 __global__ __launch_bounds__(kThreads) void sgd_and_split_sum(
     const fg::optim::MTTensor *__restrict__ tensors, const fg::optim::MTChunk *__restrict__ chunks,
-    float lr, int zero_grad, int vec, uint32_t nchunks, GemmArgs red, int splits) {
-    if (blockIdx.x < nchunks)
-        fg::optim::sgd_chunk(tensors, chunks, lr, zero_grad, vec, blockIdx.x);
+    float lr, int zero_grad, int vec, uint32_t nchunks, GemmArgs red, int splits, uint32_t nred,
+    const float *__restrict__ mean_src, int mean_rows, float *__restrict__ mean_dst) {
+    __shared__ double sh[fg::smrow::kSlots];
+    const uint32_t b = blockIdx.x;
+    if (b < nchunks)
+        fg::optim::sgd_chunk(tensors, chunks, lr, zero_grad, vec, b);
+    else if (b < nchunks + nred)
+        fg::gemm::split_sum_blocks(red, splits, b - nchunks, nred);
     else
-        fg::gemm::split_sum_blocks(red, splits, blockIdx.x - nchunks, gridDim.x - nchunks);
+        fg::smrow::mean_rows(mean_src, mean_rows, mean_dst, sh);
+}
+
+__global__ __launch_bounds__(kThreads) void mean_rows_kernel(const float *__restrict__ src, int R,
+                                                             float *__restrict__ dst) {
+    __shared__ double sh[fg::smrow::kSlots];
+    fg::smrow::mean_rows(src, R, dst, sh);
 }
 
 // Split K over workgroup rows when the output gives few tiles (under half
@@ -301,16 +316,31 @@ int launch_pending_reduce(fg_ctx *ctx) {
 
 int sgd_step_with_pending(fg_ctx *ctx, fg_mt *mt, float lr, int zero_grad, fg_ctx *held) {
     FG_REQUIRE(ctx && mt && held, FG_ERR_INVALID_ARGUMENT, "sgd_step_with_pending: NULL argument");
-    if (held->pending_splits <= 0) return fg_sgd_step(ctx, mt, lr, zero_grad);
+    const bool mean = held->mean_dst != nullptr;
+    if (held->pending_splits <= 0 && !mean) return fg_sgd_step(ctx, mt, lr, zero_grad);
     FG_HIP(hipSetDevice(ctx->device));
-    GemmArgs a;
-    std::memcpy(&a, held->pending, sizeof a);
-    const int splits = held->pending_splits;
-    held->pending_splits = 0;
-    const int nred = reduce_blocks(held, a.M, a.N);
-    sgd_and_split_sum<<<mt->nchunks + nred, kThreads, 0, ctx->stream>>>(
-        mt->d_tensors, mt->d_chunks, lr, zero_grad, mt->vec, mt->nchunks, a, splits);
+    GemmArgs a{};
+    int splits = 1, nred = 0;
+    if (held->pending_splits > 0) {
+        std::memcpy(&a, held->pending, sizeof a);
+        splits = held->pending_splits;
+        nred = reduce_blocks(held, a.M, a.N);
+        held->pending_splits = 0;
+    }
+    sgd_and_split_sum<<<mt->nchunks + nred + (mean ? 1 : 0), kThreads, 0, ctx->stream>>>(
+        mt->d_tensors, mt->d_chunks, lr, zero_grad, mt->vec, mt->nchunks, a, splits, nred,
+        held->mean_src, held->mean_rows, held->mean_dst);
+    held->mean_dst = nullptr;
     FG_LAUNCH_CHECK("sgd_and_split_sum");
+    return FG_OK;
+}
+
+int launch_pending_mean(fg_ctx *ctx) {
+    if (!ctx->mean_dst) return FG_OK;
+    mean_rows_kernel<<<1, kThreads, 0, ctx->stream>>>(ctx->mean_src, ctx->mean_rows,
+                                                      ctx->mean_dst);
+    ctx->mean_dst = nullptr;
+    FG_LAUNCH_CHECK("mean_rows_kernel");
     return FG_OK;
 }
 
@@ -596,7 +626,9 @@ int gemm_fwd_chain_f32(fg_ctx *ctx, int M1, int N1, int K1, const float *A1, int
                        const float *B1, int ldb1, const float *bias1, int act1, float *C1,
                        int ldc1, float *Z1, int ldz1, int M2, int N2, int K2, const float *A2,
                        int lda2, const float *B2, int ldb2, const float *bias2, int act2,
-                       float *C2, int ldc2, float *Z2, int ldz2, int acc2) {
+                       float *C2, int ldc2, float *Z2, int ldz2, int acc2, const CeOut *ce,
+                       bool *ce_done) {
+    if (ce_done) *ce_done = false;
     auto separate = [&]() {
         const int rc = fg_gemm_f32(ctx, FG_NN, M1, N1, K1, A1, lda1, B1, ldb1, bias1, act1, C1,
                                    ldc1, Z1, ldz1, 0);
@@ -617,9 +649,14 @@ int gemm_fwd_chain_f32(fg_ctx *ctx, int M1, int N1, int K1, const float *A1, int
         fg::clear_error();
         return separate();
     }
+    // The loss too when its logits are this GEMM's whole output.
+    const bool with_ce = ce && ce_done && act2 == FG_ACT_NONE && !acc2 && N2 <= 16 &&
+                         M2 <= 1024 && ce->labels && ce->row_loss && ce->dlogits &&
+                         ce->ldd >= N2 && (!ce->probs || ce->ldp >= N2);
     if (int rc = gemm_launch(ctx, P1, "gemm_fwd_chain_f32", false)) return rc;
-    fg::gemm::launch_skinny_pre(P2.a, P1.a, ctx->stream);
+    fg::gemm::launch_skinny_pre(P2.a, P1.a, ctx->stream, with_ce ? ce : nullptr);
     FG_LAUNCH_CHECK("gemm_fwd_chain_f32");
+    if (with_ce) *ce_done = true;
     return FG_OK;
 }
 

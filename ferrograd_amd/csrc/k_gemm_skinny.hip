@@ -12,13 +12,24 @@ __global__ __launch_bounds__(kSkThreads) void gemm_f32_skinny(GemmArgs p) {
 
 // NN, A summed from the slices of the split GEMM `pre`.
 __global__ __launch_bounds__(kSkThreads) void gemm_f32_skinny_pre(GemmArgs p, GemmArgs pre) {
-    gemm_f32_skinny_pre_body(p, pre, blockIdx.x);
+    gemm_f32_skinny_pre_body<false>(p, pre, blockIdx.x, CeOut{});
+}
+
+// The same, finishing the softmax + CE of the head's rows.
+__global__ __launch_bounds__(kSkThreads) void gemm_f32_skinny_pre_ce(GemmArgs p, GemmArgs pre,
+                                                                     CeOut ce) {
+    gemm_f32_skinny_pre_body<true>(p, pre, blockIdx.x, ce);
 }
 
 }  // namespace
 
-void launch_skinny_pre(const GemmArgs &a, const GemmArgs &pre, hipStream_t st) {
-    gemm_f32_skinny_pre<<<dim3(skinny_pre_workgroups(a.M)), dim3(kSkThreads), 0, st>>>(a, pre);
+void launch_skinny_pre(const GemmArgs &a, const GemmArgs &pre, hipStream_t st,
+                       const CeOut *ce) {
+    const dim3 grid(skinny_pre_workgroups(a.M)), block(kSkThreads);
+    if (ce)
+        gemm_f32_skinny_pre_ce<<<grid, block, 0, st>>>(a, pre, *ce);
+    else
+        gemm_f32_skinny_pre<<<grid, block, 0, st>>>(a, pre);
 }
 
 void launch_skinny(const GemmArgs &a, int layout, hipStream_t st) {

@@ -31,6 +31,7 @@
 
 #include "fg_half.h"
 #include "fg_internal.h"
+#include "fg_softmax_row.h"
 
 namespace {
 
@@ -39,12 +40,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kNT = 256;
 constexpr int kWaves = kNT / 64;
 
-__device__ __forceinline__ void argmax_combine(float &m, int &i, float m2, int i2) {
-    if (m2 > m || (m2 == m && i2 < i)) {
-        m = m2;
-        i = i2;
-    }
-}
+using fg::smrow::argmax_combine;
 
 // Block-wide (max, lowest index of max) over NW waves; every thread
 // receives the result.
@@ -451,46 +447,10 @@ __global__ __launch_bounds__(kSmallNT) void softmax_ce_small(
 // loads kSmallBatch rows per slot at once; the mean adds each slot's rows
 // in order (double), then the slots in order.  Outputs and conventions as
 // softmax_ce_small.
-constexpr int kTinyCols = 16;
+constexpr int kTinyCols = fg::smrow::kCols;
 constexpr int kTinySlots = kSmallNT / kTinyCols;
+static_assert(kTinySlots == fg::smrow::kSlots, "row slots");
 bool tiny_case(int R, int C) { return C <= kTinyCols && R <= kSmallRows; }
-
-// DPP controls within a row of 16 lanes: quad permutations [1,0,3,2] and
-// [2,3,0,1], the half-row mirror (lane i <-> 7 - i of each 8) and the row
-// mirror (lane i <-> 15 - i).
-constexpr int kDppSwap1 = 0xB1, kDppSwap2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
-
-template <int CTRL>
-__device__ __forceinline__ int dpp_i(int v) {
-    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
-}
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-    return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
-}
-template <int CTRL>
-__device__ __forceinline__ void row16_step(float &s) {
-    s += dpp_f<CTRL>(s);
-}
-template <int CTRL>
-__device__ __forceinline__ void row16_step(float &m, int &am) {
-    argmax_combine(m, am, dpp_f<CTRL>(m), dpp_i<CTRL>(am));
-}
-// Sum / max and first argmax over the 16 lanes of each row (all lanes of
-// the wave active).
-__device__ __forceinline__ float row16_sum(float s) {
-    row16_step<kDppSwap1>(s);
-    row16_step<kDppSwap2>(s);
-    row16_step<kDppHalfMirror>(s);
-    row16_step<kDppMirror>(s);
-    return s;
-}
-__device__ __forceinline__ void row16_argmax(float &m, int &am) {
-    row16_step<kDppSwap1>(m, am);
-    row16_step<kDppSwap2>(m, am);
-    row16_step<kDppHalfMirror>(m, am);
-    row16_step<kDppMirror>(m, am);
-}
 
 template <int DT>
 __global__ __launch_bounds__(kSmallNT) void softmax_ce_tiny(
@@ -518,26 +478,11 @@ __global__ __launch_bounds__(kSmallNT) void softmax_ce_tiny(
 #pragma unroll
         for (int j = 0; j < kSmallBatch; ++j) {
             const int r = r0 + j * kTinySlots;
-            float m = v[j];
-            int am = c < C ? c : C;
-            row16_argmax(m, am);
-            const float e = c < C ? expf(v[j] - m) : 0.0f;
-            const float s = row16_sum(e);
-            const float xt = row16_sum((c < C && (uint32_t)c == t[j]) ? v[j] : 0.0f);
-            if (r >= R) continue;
-            if (argmax && c == 0) argmax[r] = (uint32_t)am;
-            if (row_loss || mean) {
-                const float l = (t[j] < (uint32_t)C) ? (m + logf(s)) - xt : __builtin_nanf("");
-                if (row_loss && c == 0) row_loss[r] = l;
-                acc += (double)l;
-            }
-            if ((out || probs) && c < C) {
-                const float pv = e * (1.0f / s);
-                if (out)
-                    small_store<DT>(out, (uint64_t)r * ldo + c,
-                                    scale * (labels && (uint32_t)c == t[j] ? pv - 1.0f : pv));
-                if (probs) small_store<DT>(probs, (uint64_t)r * ldp + c, pv);
-            }
+            const bool want_loss = row_loss || mean;
+            const float l = fg::smrow::ce_row16<DT>(v[j], t[j], c, C, r, r < R, labels != nullptr,
+                                                    scale, row_loss, out, ldo, argmax, probs, ldp,
+                                                    want_loss);
+            if (r < R && want_loss) acc += (double)l;
         }
     }
     if (!mean) return;
@@ -680,6 +625,8 @@ int softmax_ce_dispatches(int R, int C, bool mean) {
     const bool small = small_case(R, C);
     return (mean && !small) ? 2 : 1;
 }
+
+bool softmax_ce_row16_case(int R, int C) { return tiny_case(R, C); }
 
 int softmax_ce_ex(fg_ctx *ctx, int dtype, const void *d_logits, int ldx, const uint32_t *d_labels,
                   int R, int C, float grad_scale, float *d_row_loss, float *d_mean_loss,

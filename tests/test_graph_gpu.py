@@ -456,7 +456,7 @@ def test_paired_gradient_gemms_match_separate_calls(ctx):
         assert desc.count("[with the next]") == 4, desc
         # The first layer's K slices are summed by the second layer's kernel.
         assert "[K split: slices, summed by the next launch]" in desc, desc
-        assert "kernels per step: 6 (forward 2, loss 1, backward 2, optim 1)" in desc, desc
+        assert "kernels per step: 5 (forward 2, loss 0, backward 2, optim 1)" in desc, desc
         X = fa.rng_uniform(0, 0, (B, 784))
         y = fa.rng_int(0, 1, (B,), 10)
         Ws = [fa.rng_uniform(0, 10 + l, (dims[l], dims[l + 1]), -math.sqrt(6 / dims[l]),
@@ -667,7 +667,8 @@ def test_captured_step_survives_workspace_growth(ctx):
         fwd = desc.split("forward:")[1].split("loss:")[0]
         assert fwd.count("[K split: slices, summed by the next launch]") == 1, desc
         assert "the backward's last summing launch shares the SGD launch" in desc, desc
-        assert "kernels per step: 6 (forward 2, loss 1, backward 2, optim 1)" in desc, desc
+        assert "the head GEMM finishes the loss" in desc, desc
+        assert "kernels per step: 5 (forward 2, loss 0, backward 2, optim 1)" in desc, desc
         sch, st, ins, tgt = plans[1]
         call("fg_plan_bind_target", sch.plan.handle, tgt.data_ptr(), tgt.nbytes)
         call("fg_plan_capture_step", sch.plan.handle)
@@ -686,10 +687,13 @@ def test_captured_step_survives_workspace_growth(ctx):
                     gctx.dispatch_backward(sch)
                     gctx.dispatch_optim(sch)
                 gctx.sync()
-                # Parameters, loss, and every gradient: the data input's is
-                # summed beside the SGD update in the captured step.
+                # Parameters, the mean loss, the probabilities and every
+                # gradient: in the captured step the head GEMM finishes the
+                # loss (dlogits, probabilities), the SGD launch its mean and
+                # the data input's gradient.
                 hist.append([gctx.download(t).copy() for t in ins[1:]] +
-                            [gctx.download(st.mean_loss).copy()] +
+                            [gctx.download(st.mean_loss).copy(),
+                             gctx.download(st.forward_out).copy()] +
                             [gctx.download(t).copy() for t in st.grad_tensors])
             runs.append(hist)
         for a, b in zip(*runs):
