@@ -1153,6 +1153,10 @@ void launch_skinny_pre(const GemmArgs &a, const GemmArgs &pre, hipStream_t st,
 enum : int { kPairSkinny = 0, kPairElem = 1, kPairPipe = 2 };
 void launch_pair(int k1, int k2, const GemmArgs &a1, const GemmArgs &a2, int x1, int n1, int x2,
                  int n2, hipStream_t st);
+// A skinny TN weight gradient (n1 workgroups) with a pair (kinds k2, k3 as
+// launch_pair) in one launch.
+void launch_triple(const GemmArgs &a1, int n1, int k2, const GemmArgs &a2, int x2, int n2, int k3,
+                   const GemmArgs &a3, int x3, int n3, hipStream_t st);
 
 }  // namespace gemm
 }  // namespace fg

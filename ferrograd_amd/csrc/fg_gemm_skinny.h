@@ -203,13 +203,21 @@ __device__ __forceinline__ void gemm_f32_skinny_pre_body(const GemmArgs &p, cons
     const f32x4 bv = (pre.bias && c4 < pre.N) ? *reinterpret_cast<const f32x4 *>(pre.bias + c4)
                                               : f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // pre's outputs: the slices in slice order, then pre's epilogue.
+    // pre's outputs: the slices in slice order, then pre's epilogue.  With
+    // CE and a data gradient, pre's Z values (v + bias, as epi_x4 stores
+    // them) are kept for the act' of that gradient.
+    __shared__ float zsh[CE ? kSpRows * kSkinnyK : 1];
     f32x4 h = {0.f, 0.f, 0.f, 0.f};
     if (ok) {
         f32x4 v = sl[0];
 #pragma unroll
         for (int s = 1; s < kSkPreMaxSlices; ++s)
             if (s < S) v += sl[s];
+        if constexpr (CE) {
+            const f32x4 z = v + bv;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) zsh[r * kSkinnyK + c4 + e] = z[e];
+        }
         h = epi_x4(pre, v, bv, row, c4);
     }
 #pragma unroll
@@ -262,14 +270,57 @@ __device__ __forceinline__ void gemm_f32_skinny_pre_body(const GemmArgs &p, cons
         }
     }
     if constexpr (CE) {
+        __shared__ float dl[kSpRows * smrow::kCols];
         __syncthreads();
         if (t < 64) {  // wave 0: lane 16 r + c holds column c of local row r
             const int r = t / smrow::kCols, c = t % smrow::kCols, row = m0 + r;
             const bool valid = row < p.M;
             const float v = (valid && c < p.N) ? logits[r * kSkinnyN + c] : -INFINITY;
             const uint32_t lab = valid ? ce.labels[row] : 0u;
+            float d;
             (void)smrow::ce_row16<kF32>(v, lab, c, p.N, row, valid, true, ce.scale, ce.row_loss,
-                                        ce.dlogits, ce.ldd, nullptr, ce.probs, ce.ldp, true);
+                                        ce.dlogits, ce.ldd, nullptr, ce.probs, ce.ldp, true, &d);
+            dl[t] = d;
+        }
+        if (ce.dz) {
+            // dz rows m0.. = (dlogits . B^T) * act'(Z): an NT product of
+            // K = p.N (classes) and N = p.K (this GEMM's K).  Wave w takes
+            // 32-column blocks 2w, 2w + 1 with the 64x64 kernels' MFMA
+            // sequence for one 16-deep K tile (lane half h feeds k = 8h + 4g
+            // + s to the s-th MFMA of group g); A rows past the workgroup's
+            // four are zero, which leaves its rows' sums unchanged.
+            __syncthreads();
+            const int lane = t & 63, wave = t >> 6, l32 = lane & 31, hh = lane >> 5;
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) {
+                const int n0 = 32 * (2 * wave + jj);
+                if (n0 >= p.K) break;  // uniform
+                const int n = n0 + l32;
+                f32x16 acc;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[i] = 0.0f;
+#pragma unroll
+                for (int g = 0; g < 2; ++g) {
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) {
+                        const int k = 8 * hh + 4 * g + s;
+                        const float av = l32 < kSpRows ? dl[l32 * smrow::kCols + k] : 0.0f;
+                        const float bw = n < p.K ? Bs[n * kSkinnyN + k] : 0.0f;
+                        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bw, acc, 0, 0, 0);
+                    }
+                }
+                // Register r (< 4) of lane half 0 holds row r, column n.
+                if (hh == 0 && n < p.K) {
+#pragma unroll
+                    for (int r = 0; r < kSpRows; ++r) {
+                        const int row = m0 + r;
+                        if (row >= p.M) continue;
+                        float o = acc[r];
+                        if (ce.dz_act != kActNone) o *= act_grad(ce.dz_act, zsh[r * kSkinnyK + n]);
+                        ce.dz[(size_t)row * ce.lddz + n] = o;
+                    }
+                }
+            }
         }
     }
 }

@@ -1121,26 +1121,75 @@ int head_loss_chain(const fg_plan &P) {
     return -1;
 }
 
+// With the loss finished in the head GEMM (head_loss_chain, chain at fwd
+// index hc), the head kernel can also compute the backward's data gradient
+// of the head, dZ = (dlogits . W^T) * act'(Z): when the backward list opens
+// with the head's dW (+ dbias, paired with that dX, fp32) and the dX reads
+// the loss's dlogits and the head's weight, writes a whole fresh gradient
+// (no accumulation) through act' of the summed GEMM's Z, and takes a 64x64
+// tile kernel (more than 16 output columns).  The backward then runs the
+// head's dW with the next pair in one launch (run's triple_at = 0).
+bool head_bwd_fusable(const fg_plan &P, const std::vector<Launch> &bwd, int hc) {
+    if (hc < 0 || bwd.size() < 4) return false;
+    const Launch &S = P.loss[0], &L = P.fwd[hc], &X = P.fwd[hc + 1];
+    const Launch &W0 = bwd[0], &D0 = bwd[1], &W1 = bwd[2], &D1 = bwd[3];
+    const bool dw0 = W0.kind == LK_GEMM && W0.sExtra != kNone && W0.dtype == FG_DTYPE_F32 &&
+                     W0.pair_next && W0.sA == X.sA && W0.sB == S.sC;
+    const bool dx0 = D0.kind == LK_GEMM_BWD && D0.layout == FG_NT && D0.dtype == FG_DTYPE_F32 &&
+                     D0.sA == S.sC && D0.sB == X.sB && D0.M == S.M && D0.N == X.K &&
+                     D0.K == S.N && D0.N > fg::gemm_skinny_max_n() && !D0.accumulate &&
+                     D0.ldc == D0.N && D0.lda == S.N && D0.ldb == X.ldb &&
+                     (D0.act == FG_ACT_NONE || (D0.sZ == L.sZ && D0.ldz == D0.N && L.ldz == L.N));
+    const bool pair1 = W1.kind == LK_GEMM && W1.sExtra != kNone && W1.dtype == FG_DTYPE_F32 &&
+                       W1.pair_next && D1.kind == LK_GEMM_BWD && D1.dtype == FG_DTYPE_F32;
+    return dw0 && dx0 && pair1;
+}
+
 // defer_last: the summing launch of a split GEMM in the list's last launch
 // (or the pair or chain ending it) is held in the plan's context view for the
 // optimiser launch that follows (captured steps, run_optim).  ce_loss: the
 // loss launch that the chain producing its logits may finish (head_loss_chain);
 // *ce_done tells whether it did.
+// dz_launch: with ce_loss, the backward's data-gradient launch of the head
+// that the chained head kernel computes as well (head_bwd_fusable).
+// triple_at: index of a head's weight-gradient launch whose group runs as
+// one launch with the pair two launches on (its own pair partner, the
+// head's data gradient, was computed in the forward).
 int run(fg_plan &P, const std::vector<Launch> &list, bool step = false, bool defer_last = false,
-        const Launch *ce_loss = nullptr, bool *ce_done = nullptr) {
+        const Launch *ce_loss = nullptr, bool *ce_done = nullptr,
+        const Launch *dz_launch = nullptr, int triple_at = -1) {
     fg_ctx *ctx = &P.wctx;
-    bool skip_next = false;  // the launch just run as the second of a pair
-    for (const Launch &L : list) {
+    int skip = 0;  // launches already run as part of a group
+    for (size_t i = 0; i < list.size(); ++i) {
+        const Launch &L = list[i];
         int rc = FG_OK;
-        if (skip_next) {
-            skip_next = false;
+        if (skip > 0) {
+            --skip;
             continue;
         }
-        const bool with_next = (L.pair_next || L.chain_next) && &L + 1 < list.data() + list.size();
-        ctx->defer_reduce = defer_last && &L + (with_next ? 1 : 0) == &list.back();
+        size_t last = i;  // the group's last launch
+        if ((int)i == triple_at && i + 3 < list.size())
+            last = i + 3;
+        else if ((L.pair_next || L.chain_next) && i + 1 < list.size())
+            last = i + 1;
+        ctx->defer_reduce = defer_last && last == list.size() - 1;
         if (step && L.elidable) continue;
-        if (L.chain_next && &L + 1 < list.data() + list.size()) {
-            const Launch &X = *(&L + 1);  // reads L's output as its A operand
+        if ((int)i == triple_at && i + 3 < list.size()) {
+            const Launch &W = list[i + 2], &X = list[i + 3];  // a layer's dW (TN) and dX (NT)
+            rc = fg::gemm_dw_dw_dx_f32(
+                ctx, L.M, L.N, L.K, (const float *)P.ptr(L.sA), L.lda, (const float *)P.ptr(L.sB),
+                L.ldb, (float *)P.ptr(L.sC), L.ldc, L.accumulate, (float *)P.ptr(L.sExtra),
+                L.accumulate2, W.M, W.N, W.K, (const float *)P.ptr(W.sA), W.lda,
+                (const float *)P.ptr(W.sB), W.ldb, (float *)P.ptr(W.sC), W.ldc, W.accumulate,
+                (float *)P.ptr(W.sExtra), W.accumulate2, X.M, X.N, X.K, (const float *)P.ptr(X.sA),
+                X.lda, (const float *)P.ptr(X.sB), X.ldb, X.act, (const float *)P.ptr(X.sZ), X.ldz,
+                (float *)P.ptr(X.sC), X.ldc, X.accumulate);
+            if (rc != FG_OK) return rc;
+            skip = 3;
+            continue;
+        }
+        if (L.chain_next && i + 1 < list.size()) {
+            const Launch &X = list[i + 1];  // reads L's output as its A operand
             fg::CeOut ce{};
             const bool want_ce = ce_loss && ce_done && X.sC == ce_loss->sA;
             if (want_ce) {
@@ -1148,7 +1197,9 @@ int run(fg_plan &P, const std::vector<Launch> &list, bool step = false, bool def
                 FG_REQUIRE(P.ptr(S.sZ), FG_ERR_INVALID_ARGUMENT,
                            "dispatch_loss: no target bound (fg_plan_bind_target)");
                 ce = {(const uint32_t *)P.ptr(S.sZ), (float *)P.ptr(S.sB), (float *)P.ptr(S.sC),
-                      step ? (float *)P.ptr(S.sProbs) : nullptr, S.N, S.N, 1.0f};
+                      step ? (float *)P.ptr(S.sProbs) : nullptr, S.N, S.N, 1.0f,
+                      dz_launch ? (float *)P.ptr(dz_launch->sC) : nullptr,
+                      dz_launch ? dz_launch->ldc : 0, dz_launch ? dz_launch->act : FG_ACT_NONE};
             }
             rc = fg::gemm_fwd_chain_f32(
                 ctx, L.M, L.N, L.K, (const float *)P.ptr(L.sA), L.lda, (const float *)P.ptr(L.sB),
@@ -1158,11 +1209,11 @@ int run(fg_plan &P, const std::vector<Launch> &list, bool step = false, bool def
                 (float *)P.ptr(X.sC), X.ldc, (float *)P.ptr(X.sZ), X.ldz, X.accumulate,
                 want_ce ? &ce : nullptr, want_ce ? ce_done : nullptr);
             if (rc != FG_OK) return rc;
-            skip_next = true;
+            skip = 1;
             continue;
         }
-        if (L.pair_next && &L + 1 < list.data() + list.size()) {
-            const Launch &X = *(&L + 1);  // the same layer's dX (NT, act')
+        if (L.pair_next && i + 1 < list.size()) {
+            const Launch &X = list[i + 1];  // the same layer's dX (NT, act')
             rc = fg::gemm_dw_dx_f32(ctx, L.M, L.N, L.K, (const float *)P.ptr(L.sA), L.lda,
                                     (const float *)P.ptr(L.sB), L.ldb, (float *)P.ptr(L.sC),
                                     L.ldc, L.accumulate, (float *)P.ptr(L.sExtra), L.accumulate2,
@@ -1171,7 +1222,7 @@ int run(fg_plan &P, const std::vector<Launch> &list, bool step = false, bool def
                                     (const float *)P.ptr(X.sZ), X.ldz, (float *)P.ptr(X.sC),
                                     X.ldc, X.accumulate);
             if (rc != FG_OK) return rc;
-            skip_next = true;
+            skip = 1;
             continue;
         }
         switch (L.kind) {
@@ -1890,8 +1941,11 @@ FG_API int fg_plan_capture_step(fg_plan *p) {
     // With SGD the head GEMM may finish the loss (its mean then runs in the
     // SGD launch).
     const int hc = head_loss_chain(*p);
+    const std::vector<Launch> &bwd = p->ce_fused_possible ? p->bwd_fused : p->bwd_seed;
+    const bool hb = head_bwd_fusable(*p, bwd, hc);
     bool ce_done = false;
-    rc = run(*p, p->fwd, true, false, hc >= 0 ? &p->loss[0] : nullptr, &ce_done);
+    rc = run(*p, p->fwd, true, false, hc >= 0 ? &p->loss[0] : nullptr, &ce_done,
+             hb ? &bwd[1] : nullptr);
     if (rc == FG_OK && ce_done) {
         const Launch &S = p->loss[0];
         p->wctx.mean_src = (const float *)p->ptr(S.sB);
@@ -1900,10 +1954,12 @@ FG_API int fg_plan_capture_step(fg_plan *p) {
     } else if (rc == FG_OK) {
         rc = run(*p, p->loss, true);
     }
-    // The backward's last summing launch may share the SGD launch.
+    // The backward's last summing launch may share the SGD launch; with the
+    // head's dX computed in the forward, the head's dW runs beside the next
+    // pair.
     if (rc == FG_OK)
-        rc = run(*p, p->ce_fused_possible ? p->bwd_fused : p->bwd_seed, false,
-                 p->g.optim == FG_OPTIM_SGD && p->mt_all);
+        rc = run(*p, bwd, false, p->g.optim == FG_OPTIM_SGD && p->mt_all, nullptr, nullptr,
+                 nullptr, ce_done && hb ? 0 : -1);
     if (rc == FG_OK) rc = run_optim(*p, p->mt_all);
     p->wctx.defer_reduce = false;
     if (rc != FG_OK) {
@@ -2134,11 +2190,27 @@ FG_API int fg_plan_describe(const fg_plan *p, char *buf, size_t len, size_t *nee
     const std::vector<Launch> &bwd = p->ce_fused_possible ? p->bwd_fused : p->bwd_seed;
     int k_bwd = kernels(bwd);
     int k_loss = kernels(p->loss);
-    // A captured SGD step may finish the loss in the head GEMM.
+    // A captured SGD step may finish the loss in the head GEMM, and then the
+    // head's data gradient too, its dW joining the next pair's launch.
     if (const int hc = head_loss_chain(*p); hc >= 0 && wc &&
                                             chain_dispatches(p->fwd[hc], p->fwd[hc + 1]) == 2) {
         k_loss = 0;
         s += "(captured step: the head GEMM finishes the loss; its mean runs in the SGD launch)\n";
+        if (head_bwd_fusable(*p, bwd, hc)) {
+            auto pair_n = [&](const Launch &L, const Launch &X) {
+                return fg::gemm_dw_dx_dispatches(wc, L.M, L.N, L.K, p->ptr(L.sA), L.lda,
+                                                 p->ptr(L.sB), L.ldb, X.M, X.N, X.K,
+                                                 p->ptr(X.sA), X.lda, p->ptr(X.sB), X.ldb);
+            };
+            const Launch &W0 = bwd[0], &W1 = bwd[2], &D1 = bwd[3];
+            const int triple = fg::gemm_dw_dw_dx_dispatches(
+                wc, W0.M, W0.N, W0.K, p->ptr(W0.sA), W0.lda, p->ptr(W0.sB), W0.ldb, W1.M, W1.N,
+                W1.K, p->ptr(W1.sA), W1.lda, p->ptr(W1.sB), W1.ldb, D1.M, D1.N, D1.K,
+                p->ptr(D1.sA), D1.lda, p->ptr(D1.sB), D1.ldb);
+            k_bwd += triple - pair_n(bwd[0], bwd[1]) - pair_n(bwd[2], bwd[3]);
+            s += "(captured step: it also computes the head's data gradient; the head's dW "
+                 "runs in the next pair's launch)\n";
+        }
     }
     // A captured SGD step runs the backward's last summing launch beside the
     // SGD update (run_optim), when the two touch disjoint memory.

@@ -70,6 +70,13 @@ struct CeOut {
     float *probs;
     int ldd, ldp;
     float scale;
+    // Optionally the head's data gradient as well (fp32 dlogits only):
+    // dz = (dlogits . B^T) * act'(Z of the summed GEMM) for the kernel's
+    // rows, with the MFMA sequence of the 64x64 tile kernels, so the same
+    // bits as the backward's own NT GEMM; NULL: none.
+    float *dz;
+    int lddz;
+    int dz_act;
 };
 
 // [begin, end) of device memory, as addresses.
@@ -144,6 +151,22 @@ int gemm_dw_dx_f32(fg_ctx *ctx, int M1, int N1, int K1, const float *A1, int lda
 int gemm_dw_dx_dispatches(fg_ctx *ctx, int M1, int N1, int K1, const void *A1, int lda1,
                           const void *B1, int ldb1, int M2, int N2, int K2, const void *A2,
                           int lda2, const void *B2, int ldb2);
+// The skinny kernel's largest N (output columns).
+int gemm_skinny_max_n();
+// A small head's dW (+ dbias, TN) beside a layer's dW and dX, in one launch
+// when the head's takes the skinny kernel and the two pair (k_gemm.hip);
+// and its dispatch count.
+int gemm_dw_dw_dx_f32(fg_ctx *ctx, int M0, int N0, int K0, const float *A0, int lda0,
+                      const float *B0, int ldb0, float *C0, int ldc0, int acc0, float *colsum0,
+                      int colsum_acc0, int M1, int N1, int K1, const float *A1, int lda1,
+                      const float *B1, int ldb1, float *C1, int ldc1, int acc1, float *colsum1,
+                      int colsum_acc1, int M2, int N2, int K2, const float *A2, int lda2,
+                      const float *B2, int ldb2, int act, const float *Zs, int ldzs, float *C2,
+                      int ldc2, int acc2);
+int gemm_dw_dw_dx_dispatches(fg_ctx *ctx, int M0, int N0, int K0, const void *A0, int lda0,
+                             const void *B0, int ldb0, int M1, int N1, int K1, const void *A1,
+                             int lda1, const void *B1, int ldb1, int M2, int N2, int K2,
+                             const void *A2, int lda2, const void *B2, int ldb2);
 // Two forward GEMMs in a row, the second (NN) reading the first's output as
 // its A operand: when the first splits K and the second takes the skinny
 // kernel, the second sums the first's slices (k_gemm.hip); and the dispatch

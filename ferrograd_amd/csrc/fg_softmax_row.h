@@ -75,12 +75,15 @@ __device__ __forceinline__ void store_as(void *p, uint64_t i, float v) {
 // c >= C hold -inf), t = its label.  Writes argmax, the row loss (lane 0),
 // dlogits = scale * (p - [c == t]) (no one-hot without labels) and the
 // probabilities, each output optional; returns the row loss (NaN for a
-// label outside [0, C)) when want_loss.  Called by all 64 lanes of the wave.
+// label outside [0, C)) when want_loss, and in *dl (when given) the lane's
+// dlogit as stored (0 for lanes past C or an invalid row).  Called by all 64
+// lanes of the wave.
 template <int DT>
 __device__ __forceinline__ float ce_row16(float v, uint32_t t, int c, int C, int r, bool valid,
                                           bool labels, float scale, float *row_loss, void *out,
                                           int ldo, uint32_t *argmax, void *probs, int ldp,
-                                          bool want_loss) {
+                                          bool want_loss, float *dl = nullptr) {
+    if (dl) *dl = 0.0f;
     float m = v;
     int am = c < C ? c : C;
     row16_argmax(m, am);
@@ -96,9 +99,11 @@ __device__ __forceinline__ float ce_row16(float v, uint32_t t, int c, int C, int
     }
     if ((out || probs) && c < C) {
         const float pv = e * (1.0f / s);
-        if (out)
-            store_as<DT>(out, (uint64_t)r * ldo + c,
-                         scale * (labels && (uint32_t)c == t ? pv - 1.0f : pv));
+        if (out) {
+            const float d = scale * (labels && (uint32_t)c == t ? pv - 1.0f : pv);
+            store_as<DT>(out, (uint64_t)r * ldo + c, d);
+            if (dl) *dl = d;
+        }
         if (probs) store_as<DT>(probs, (uint64_t)r * ldp + c, pv);
     }
     return l;

@@ -678,6 +678,78 @@ int gemm_fwd_chain_dispatches(fg_ctx *ctx, int M1, int N1, int K1, const void *A
     return chainable(P1, P2) ? 2 : sep;
 }
 
+// A small head's weight gradient (with its bias gradient; TN) beside a
+// layer's dW and dX (as gemm_dw_dx_f32): one launch when the head's takes
+// the skinny kernel and the two pair; otherwise the head's alone, then the
+// pair.  The same bits either way.
+int gemm_dw_dw_dx_f32(fg_ctx *ctx, int M0, int N0, int K0, const float *A0, int lda0,
+                      const float *B0, int ldb0, float *C0, int ldc0, int acc0, float *colsum0,
+                      int colsum_acc0, int M1, int N1, int K1, const float *A1, int lda1,
+                      const float *B1, int ldb1, float *C1, int ldc1, int acc1, float *colsum1,
+                      int colsum_acc1, int M2, int N2, int K2, const float *A2, int lda2,
+                      const float *B2, int ldb2, int act, const float *Zs, int ldzs, float *C2,
+                      int ldc2, int acc2) {
+    auto separate = [&]() {
+        const int rc = fg_gemm_dw_f32(ctx, M0, N0, K0, A0, lda0, B0, ldb0, C0, ldc0, acc0, colsum0,
+                                      colsum_acc0);
+        if (rc) return rc;
+        return gemm_dw_dx_f32(ctx, M1, N1, K1, A1, lda1, B1, ldb1, C1, ldc1, acc1, colsum1,
+                              colsum_acc1, M2, N2, K2, A2, lda2, B2, ldb2, act, Zs, ldzs, C2, ldc2,
+                              acc2);
+    };
+    if (!ctx || M0 <= 0 || N0 <= 0 || K0 <= 0 || M1 <= 0 || N1 <= 0 || K1 <= 0 || M2 <= 0 ||
+        N2 <= 0 || K2 <= 0 || (act != FG_ACT_NONE && (!Zs || ldzs < N2)))
+        return separate();
+    Planned P0, P1, P2;
+    if (gemm_prepare(ctx, FG_TN, dw_args(M0, N0, K0, A0, lda0, B0, ldb0, C0, ldc0, acc0, colsum0,
+                                         colsum_acc0),
+                     "fg_gemm_dw_f32", fg::gemm::kProNone, P0) ||
+        !plan_pair(ctx, dw_args(M1, N1, K1, A1, lda1, B1, ldb1, C1, ldc1, acc1, colsum1, colsum_acc1),
+                   dx_args(M2, N2, K2, A2, lda2, B2, ldb2, act, Zs, ldzs, C2, ldc2, acc2), P1, P2) ||
+        pair_kind(P0) != fg::gemm::kPairSkinny) {
+        fg::clear_error();
+        return separate();
+    }
+    int x0, n0, x1, n1, x2, n2;
+    pair_grid(P0, x0, n0);
+    pair_grid(P1, x1, n1);
+    pair_grid(P2, x2, n2);
+    fg::gemm::launch_triple(P0.a, n0, pair_kind(P1), P1.a, x1, n1, pair_kind(P2), P2.a, x2, n2,
+                            ctx->stream);
+    FG_LAUNCH_CHECK("gemm_dw_dw_dx_f32");
+    for (const Planned *P : {&P1, &P2})
+        if (P->splits > 1) {
+            launch_reduce(ctx, P->a, P->splits);
+            FG_LAUNCH_CHECK("gemm_dw_dw_dx_f32");
+        }
+    return FG_OK;
+}
+
+int gemm_skinny_max_n() { return fg::gemm::kSkinnyN; }
+
+// Dispatches of gemm_dw_dw_dx_f32 for these shapes (no launch).
+int gemm_dw_dw_dx_dispatches(fg_ctx *ctx, int M0, int N0, int K0, const void *A0, int lda0,
+                             const void *B0, int ldb0, int M1, int N1, int K1, const void *A1,
+                             int lda1, const void *B1, int ldb1, int M2, int N2, int K2,
+                             const void *A2, int lda2, const void *B2, int ldb2) {
+    const int sep = gemm_f32_dispatches(ctx, FG_TN, M0, N0, K0, A0, lda0, B0, ldb0, true) +
+                    gemm_dw_dx_dispatches(ctx, M1, N1, K1, A1, lda1, B1, ldb1, M2, N2, K2, A2,
+                                          lda2, B2, ldb2);
+    if (!ctx || M0 <= 0 || N0 <= 0 || K0 <= 0 || M1 <= 0 || N1 <= 0 || K1 <= 0 || M2 <= 0 ||
+        N2 <= 0 || K2 <= 0)
+        return sep;
+    float *c = reinterpret_cast<float *>(256);
+    Planned P0, P1, P2;
+    plan_quiet(ctx, FG_TN, dw_args(M0, N0, K0, (const float *)A0, lda0, (const float *)B0, ldb0,
+                                   c, N0, 0, c, 0), P0);
+    plan_quiet(ctx, FG_TN, dw_args(M1, N1, K1, (const float *)A1, lda1, (const float *)B1, ldb1,
+                                   c, N1, 0, c, 0), P1);
+    plan_quiet(ctx, FG_NT, dx_args(M2, N2, K2, (const float *)A2, lda2, (const float *)B2, ldb2,
+                                   FG_ACT_NONE, nullptr, 0, c, N2, 0), P2);
+    if (pair_kind(P0) != fg::gemm::kPairSkinny || !pairable(P1, P2)) return sep;
+    return 1 + (P1.splits > 1) + (P2.splits > 1);
+}
+
 // Dispatches of gemm_dw_dx_f32 for these shapes: 1 (+1 per split GEMM) when
 // the two pair, else the sum of the two calls'.  No launch.
 int gemm_dw_dx_dispatches(fg_ctx *ctx, int M1, int N1, int K1, const void *A1, int lda1,

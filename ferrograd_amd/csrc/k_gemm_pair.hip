@@ -63,7 +63,54 @@ void launch_with(int k2, const GemmArgs &a1, const GemmArgs &a2, int x1, int n1,
     }
 }
 
+// Three GEMMs in one launch: the skinny weight gradient of a small head
+// (G1: workgroups below n1) and a layer's dW and dX (the pair's two kinds).
+template <class G2, class G3>
+__global__ __launch_bounds__(256) void gemm_triple(GemmArgs a1, GemmArgs a2, GemmArgs a3, int n1,
+                                                   int x2, int n2, int x3) {
+    const int w = blockIdx.x;
+    if (w < n1) {
+        PkSkinny<false, true>::run(a1, w, 0);
+    } else if (w < n1 + n2) {
+        const int v = w - n1;
+        G2::run(a2, v % x2, v / x2);
+    } else {
+        const int v = w - n1 - n2;
+        G3::run(a3, v % x3, v / x3);
+    }
+}
+
+template <class G2>
+void triple_with(int k3, const GemmArgs &a1, const GemmArgs &a2, const GemmArgs &a3, int n1,
+                 int x2, int n2, int x3, int n3, hipStream_t st) {
+    const dim3 grid(n1 + n2 + n3), block(256);
+    switch (k3) {
+        case kPairSkinny:
+            gemm_triple<G2, PkSkinny<true, false>><<<grid, block, 0, st>>>(a1, a2, a3, n1, x2, n2, x3);
+            break;
+        case kPairElem:
+            gemm_triple<G2, PkElem<true, false>><<<grid, block, 0, st>>>(a1, a2, a3, n1, x2, n2, x3);
+            break;
+        default:
+            gemm_triple<G2, PkPipe<true, false>><<<grid, block, 0, st>>>(a1, a2, a3, n1, x2, n2, x3);
+            break;
+    }
+}
+
 }  // namespace
+
+void launch_triple(const GemmArgs &a1, int n1, int k2, const GemmArgs &a2, int x2, int n2, int k3,
+                   const GemmArgs &a3, int x3, int n3, hipStream_t st) {
+    switch (k2) {  // GEMM 2 is a TN weight gradient, GEMM 3 the NT data gradient
+        case kPairSkinny:
+            triple_with<PkSkinny<false, true>>(k3, a1, a2, a3, n1, x2, n2, x3, n3, st);
+            break;
+        case kPairElem:
+            triple_with<PkElem<false, true>>(k3, a1, a2, a3, n1, x2, n2, x3, n3, st);
+            break;
+        default: triple_with<PkPipe<false, true>>(k3, a1, a2, a3, n1, x2, n2, x3, n3, st); break;
+    }
+}
 
 void launch_pair(int k1, int k2, const GemmArgs &a1, const GemmArgs &a2, int x1, int n1, int x2,
                  int n2, hipStream_t st) {
