@@ -50,9 +50,11 @@ constexpr int kEltMaxInstr = 64;
 constexpr int kEltMaxSrc = 12;
 constexpr int kEltMaxDst = 8;
 constexpr int kEltRegs = 16;
+constexpr int kEltPre = 4;  // sources prefetched per quad (launch_eltwise)
 
+// pre: set by launch_eltwise on a load it prefetches, slot + 1 (0: none).
 struct EltInstr {
-    uint8_t op, dst, a, b, c, pad[3];
+    uint8_t op, dst, a, b, c, pre, pad[2];
     float imm;
 };
 
@@ -75,6 +77,10 @@ struct EltProgram {
     uint32_t cols;  // row length (for row-broadcast and labels)
     int32_t n_instr;
     EltInstr ins[kEltMaxInstr];
+    // Filled by launch_eltwise: the sources whose quads every thread loads
+    // before running the program (fp32, whole tensor, 16-byte aligned).
+    int32_t n_pre;
+    int32_t pre_src[kEltPre];
 };
 
 // The rule above, checked: every array the kernel indexes with a run-time

@@ -101,6 +101,17 @@ __global__ __launch_bounds__(kThreads) void eltwise_prog_kernel(const EltProgram
         float r0[kEltRegs], r1[kEltRegs], r2[kEltRegs], r3[kEltRegs];
 #pragma unroll
         for (int k = 0; k < kEltRegs; ++k) r0[k] = r1[k] = r2[k] = r3[k] = 0.0f;
+        // The prefetched sources' quads, all loads issued before the program
+        // runs: a load's value must be present when it is written to the
+        // register file (indexed at run time), so loads issued by the
+        // program itself each wait for their data in turn.
+        const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+        f32x4 pre[kEltPre];
+#pragma unroll
+        for (int j = 0; j < kEltPre; ++j)
+            pre[j] = (j < p.n_pre && nv == 4)
+                         ? *reinterpret_cast<const f32x4 *>(p.src[p.pre_src[j]] + i0)
+                         : zero;
         auto get = [&](int k) { return f32x4{r0[k & 15], r1[k & 15], r2[k & 15], r3[k & 15]}; };
         for (int k = 0; k < p.n_instr; ++k) {
             const EltInstr in = p.ins[k];
@@ -108,7 +119,18 @@ __global__ __launch_bounds__(kThreads) void eltwise_prog_kernel(const EltProgram
             f32x4 o = x;
             bool wr = true;  // the instruction writes register in.dst
             switch (in.op) {
-                case kEltLoad: o = quad_load(p, in.a, in.c, in.b, i0, nv); break;
+                case kEltLoad:
+                    if (in.pre && nv == 4) {
+                        switch (in.pre) {  // a constant index into pre[]
+                            case 1: o = pre[0]; break;
+                            case 2: o = pre[1]; break;
+                            case 3: o = pre[2]; break;
+                            default: o = pre[3]; break;
+                        }
+                    } else {
+                        o = quad_load(p, in.a, in.c, in.b, i0, nv);
+                    }
+                    break;
                 case kEltImm: o = f32x4{in.imm, in.imm, in.imm, in.imm}; break;
                 case kEltStore:
                     quad_store(p, in.a, in.c, i0, nv, y, false);
@@ -181,8 +203,27 @@ __global__ __launch_bounds__(kThreads) void eltwise_prog_kernel(const EltProgram
 
 // Validates the program's indices on the host (so the kernel never reads a
 // source or writes a destination that was not supplied) and launches it.
-int launch_eltwise(fg_ctx *ctx, const EltProgram &p) {
-    if (p.n == 0) return FG_OK;
+int launch_eltwise(fg_ctx *ctx, const EltProgram &p0) {
+    if (p0.n == 0) return FG_OK;
+    // Prefetch slots for up to kEltPre sources read whole as fp32 from
+    // 16-byte aligned memory (a source read by several loads takes one).
+    EltProgram p = p0;
+    p.n_pre = 0;
+    for (int k = 0; k < p.n_instr && k < kEltMaxInstr; ++k) {
+        EltInstr &in = p.ins[k];
+        in.pre = 0;
+        if (in.op != kEltLoad || in.c != kModeFull || in.b != kF32 || in.a >= kEltMaxSrc ||
+            !p.src[in.a] || (((uintptr_t)p.src[in.a]) & 15u) != 0)
+            continue;
+        int slot = -1;
+        for (int j = 0; j < p.n_pre; ++j)
+            if (p.pre_src[j] == in.a) slot = j;
+        if (slot < 0 && p.n_pre < kEltPre) {
+            slot = p.n_pre++;
+            p.pre_src[slot] = in.a;
+        }
+        if (slot >= 0) in.pre = (uint8_t)(slot + 1);
+    }
     FG_REQUIRE(p.n_instr >= 0 && p.n_instr <= kEltMaxInstr, FG_ERR_INTERNAL,
                "eltwise program: %d instructions (max %d)", p.n_instr, kEltMaxInstr);
     bool needs_cols = false;
