@@ -582,7 +582,30 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_mfma(GemmArgs p) {
 // KT: K need not be a multiple of BK (staged tiles, no prologue): the last
 // tile's chunks past K are loaded from a clamped address and zeroed before
 // their LDS write, so they add nothing to any output.
-template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC, int PRO, bool KT>
+// LDS of the pipelined kernel, in floats: its stages (staged tiles: two;
+// direct: three when they fit in the 160 KiB of LDS, else two) or the
+// epilogue's staging, whichever is larger.
+template <int BM, int BN, int BK, int WGM, int WGN>
+struct PipeLds {
+    static constexpr int kStageSz = BM * BK + BN * BK;
+    static constexpr bool kStaged = !(BM == 256 && BN == 256);
+    static constexpr int kStages = kStaged ? 2 : 3 * kStageSz * 4 <= 160 * 1024 ? 3 : 2;
+    static constexpr int kEpi = WGM * WGN * 32 * (BN / WGN + 4);
+    static constexpr int floats = (kStages * kStageSz > kEpi) ? kStages * kStageSz : kEpi;
+};
+
+// The kernel's LDS buffer of N floats: one static array per N, so bodies
+// that ask for the same N in one launch share it.
+template <int N>
+__device__ __forceinline__ float (&lds_buffer())[N] {
+    __shared__ __attribute__((aligned(16))) float buf[N];
+    return buf;
+}
+
+// LDSN: the LDS buffer's size in floats, at least PipeLds::floats (0: just
+// that) -- a launch running several bodies gives them all the largest one.
+template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC, int PRO, bool KT,
+          int LDSN = 0>
 __device__ __forceinline__ void gemm_f32_pipe_body(GemmArgs p, int bx, int by) {
     split_k_view<AK, BNC, PRO>(p, by);
     constexpr int NW = WGM * WGN;
@@ -593,18 +616,16 @@ __device__ __forceinline__ void gemm_f32_pipe_body(GemmArgs p, int bx, int by) {
     constexpr int kInstA = BM * BK / 4 / 64, kInstB = BN * BK / 4 / 64;  // wave loads per tile
     static_assert(kInstA % NW == 0 && kInstB % NW == 0, "loads divide among the waves");
     constexpr int kPerA = kInstA / NW, kPerB = kInstB / NW, kLoads = kPerA + kPerB;
-    constexpr int kASz = BM * BK, kBSz = BN * BK, kStageSz = kASz + kBSz;
-    constexpr bool kStaged = !(BM == 256 && BN == 256);
+    using PL = PipeLds<BM, BN, BK, WGM, WGN>;
+    constexpr int kASz = BM * BK, kStageSz = PL::kStageSz;
+    constexpr bool kStaged = PL::kStaged;
     // The prologue scales a tile in registers, between its load and its LDS
     // write: staged tiles only.
     static_assert(PRO == kProNone || kStaged, "prologue needs the staged path");
     static_assert(!KT || (kStaged && PRO == kProNone), "K tail: staged tiles, no prologue");
-    // Staged: two stages.  Direct: three (two tiles in flight) when they fit
-    // in the 160 KiB of LDS, else two.
-    constexpr int kStages = kStaged ? 2 : 3 * kStageSz * 4 <= 160 * 1024 ? 3 : 2;
-    constexpr int kEpi = NW * 32 * (WTN + 4);
-    constexpr int kLds = (kStages * kStageSz > kEpi) ? kStages * kStageSz : kEpi;
-    __shared__ __attribute__((aligned(16))) float lds[kLds];
+    constexpr int kStages = PL::kStages;
+    static_assert(LDSN == 0 || LDSN >= PL::floats, "LDS buffer too small");
+    float(&lds)[LDSN ? LDSN : PL::floats] = lds_buffer<LDSN ? LDSN : PL::floats>();
 
     int tile_m, tile_n;
     tile_of(bx, p.tiles_m, p.tiles_n, tile_m, tile_n);
@@ -1150,7 +1171,9 @@ void launch_skinny_pre(const GemmArgs &a, const GemmArgs &pre, hipStream_t st,
 // be one of these 256-thread ones.  x1 / x2: output tiles (skinny: its
 // workgroups), n1 / n2: workgroups (tiles x K slices).  tiles_m / tiles_n
 // of each GemmArgs are set by the caller.
-enum : int { kPairSkinny = 0, kPairElem = 1, kPairPipe = 2 };
+// kPairBig: the 8-wave pipelined tiles of large layers, dW on 256x256 (cfg
+// 6, TN) with dX on 256x128 (cfg 7, NT), 512 threads, one LDS buffer.
+enum : int { kPairSkinny = 0, kPairElem = 1, kPairPipe = 2, kPairBig = 3 };
 void launch_pair(int k1, int k2, const GemmArgs &a1, const GemmArgs &a2, int x1, int n1, int x2,
                  int n2, hipStream_t st);
 // A skinny TN weight gradient (n1 workgroups) with a pair (kinds k2, k3 as

@@ -279,6 +279,9 @@ int pair_kind(const Planned &P) {
     if (P.skinny) return fg::gemm::kPairSkinny;
     if (!P.vec) return fg::gemm::kPairElem;
     if (P.pipe && !P.ktail && P.cfg == 4) return fg::gemm::kPairPipe;
+    if (P.pipe && !P.ktail && P.splits == 1 &&
+        ((P.layout == FG_TN && P.cfg == 6) || (P.layout == FG_NT && P.cfg == 7)))
+        return fg::gemm::kPairBig;
     return -1;
 }
 
@@ -288,8 +291,13 @@ void pair_grid(Planned &P, int &x, int &n) {
         x = n = fg::gemm::skinny_workgroups(P.a.M);
         return;
     }
-    P.a.tiles_m = (P.a.M + 63) / 64;  // the 64x64 tiles of both pairing kernels
-    P.a.tiles_n = (P.a.N + 63) / 64;
+    int bm = 64, bn = 64;  // the small pairing kernels' tiles
+    if (pair_kind(P) == fg::gemm::kPairBig) {
+        bm = 256;
+        bn = P.layout == FG_TN ? 256 : 128;
+    }
+    P.a.tiles_m = (P.a.M + bm - 1) / bm;
+    P.a.tiles_n = (P.a.N + bn - 1) / bn;
     x = P.a.tiles_m * P.a.tiles_n;
     n = x * P.splits;
 }
@@ -518,7 +526,9 @@ GemmArgs dx_args(int M, int N, int K, const float *A, int lda, const float *B, i
 // Both pairable: at most one of them splits K (the slices of a split GEMM
 // take the whole workspace).
 bool pairable(const Planned &P1, const Planned &P2) {
-    return pair_kind(P1) >= 0 && pair_kind(P2) >= 0 && (P1.splits == 1 || P2.splits == 1);
+    const int k1 = pair_kind(P1), k2 = pair_kind(P2);
+    return k1 >= 0 && k2 >= 0 && (P1.splits == 1 || P2.splits == 1) &&
+           ((k1 == fg::gemm::kPairBig) == (k2 == fg::gemm::kPairBig));
 }
 
 // Both validated and planned, and pairable.
@@ -680,8 +690,8 @@ int gemm_fwd_chain_dispatches(fg_ctx *ctx, int M1, int N1, int K1, const void *A
 
 // A small head's weight gradient (with its bias gradient; TN) beside a
 // layer's dW and dX (as gemm_dw_dx_f32): one launch when the head's takes
-// the skinny kernel and the two pair; otherwise the head's alone, then the
-// pair.  The same bits either way.
+// the skinny kernel and the two pair with 256-thread kernels; otherwise the
+// head's alone, then the pair.  The same bits either way.
 int gemm_dw_dw_dx_f32(fg_ctx *ctx, int M0, int N0, int K0, const float *A0, int lda0,
                       const float *B0, int ldb0, float *C0, int ldc0, int acc0, float *colsum0,
                       int colsum_acc0, int M1, int N1, int K1, const float *A1, int lda1,
@@ -706,7 +716,7 @@ int gemm_dw_dw_dx_f32(fg_ctx *ctx, int M0, int N0, int K0, const float *A0, int 
                      "fg_gemm_dw_f32", fg::gemm::kProNone, P0) ||
         !plan_pair(ctx, dw_args(M1, N1, K1, A1, lda1, B1, ldb1, C1, ldc1, acc1, colsum1, colsum_acc1),
                    dx_args(M2, N2, K2, A2, lda2, B2, ldb2, act, Zs, ldzs, C2, ldc2, acc2), P1, P2) ||
-        pair_kind(P0) != fg::gemm::kPairSkinny) {
+        pair_kind(P0) != fg::gemm::kPairSkinny || pair_kind(P1) == fg::gemm::kPairBig) {
         fg::clear_error();
         return separate();
     }
@@ -746,7 +756,9 @@ int gemm_dw_dw_dx_dispatches(fg_ctx *ctx, int M0, int N0, int K0, const void *A0
                                    c, N1, 0, c, 0), P1);
     plan_quiet(ctx, FG_NT, dx_args(M2, N2, K2, (const float *)A2, lda2, (const float *)B2, ldb2,
                                    FG_ACT_NONE, nullptr, 0, c, N2, 0), P2);
-    if (pair_kind(P0) != fg::gemm::kPairSkinny || !pairable(P1, P2)) return sep;
+    if (pair_kind(P0) != fg::gemm::kPairSkinny || !pairable(P1, P2) ||
+        pair_kind(P1) == fg::gemm::kPairBig)
+        return sep;
     return 1 + (P1.splits > 1) + (P2.splits > 1);
 }
 

@@ -97,6 +97,27 @@ void triple_with(int k3, const GemmArgs &a1, const GemmArgs &a2, const GemmArgs 
     }
 }
 
+// The large layers' pair: dW (TN, 256x256 tiles, 8 waves) in workgroups
+// below n1, dX (NT, 256x128, 8 waves) in the rest.  Each workgroup holds a
+// CU's LDS for its whole life, so a CU takes a dX tile only when a dW tile
+// has left it: the dW tiles' output writes drain while dX tiles compute,
+// where two launches would leave the chip idle through them.
+constexpr int kBigLds = PipeLds<256, 256, 32, 2, 4>::floats > PipeLds<256, 128, 32, 4, 2>::floats
+                            ? PipeLds<256, 256, 32, 2, 4>::floats
+                            : PipeLds<256, 128, 32, 4, 2>::floats;
+__global__ __launch_bounds__(512) void gemm_pair_big(GemmArgs a1, GemmArgs a2, int x1, int n1,
+                                                     int x2) {
+    const int w = blockIdx.x;
+    if (w < n1) {
+        gemm_f32_pipe_body<256, 256, 32, 2, 4, false, true, kProNone, false, kBigLds>(a1, w % x1,
+                                                                                     w / x1);
+    } else {
+        const int v = w - n1;
+        gemm_f32_pipe_body<256, 128, 32, 4, 2, true, false, kProNone, false, kBigLds>(a2, v % x2,
+                                                                                     v / x2);
+    }
+}
+
 }  // namespace
 
 void launch_triple(const GemmArgs &a1, int n1, int k2, const GemmArgs &a2, int x2, int n2, int k3,
@@ -114,6 +135,10 @@ void launch_triple(const GemmArgs &a1, int n1, int k2, const GemmArgs &a2, int x
 
 void launch_pair(int k1, int k2, const GemmArgs &a1, const GemmArgs &a2, int x1, int n1, int x2,
                  int n2, hipStream_t st) {
+    if (k1 == kPairBig) {  // then k2 is too (pairable)
+        gemm_pair_big<<<dim3(n1 + n2), dim3(512), 0, st>>>(a1, a2, x1, n1, x2);
+        return;
+    }
     switch (k1) {  // GEMM 1 is the TN weight gradient
         case kPairSkinny: launch_with<PkSkinny<false, true>>(k2, a1, a2, x1, n1, x2, n2, st); break;
         case kPairElem: launch_with<PkElem<false, true>>(k2, a1, a2, x1, n1, x2, n2, st); break;

@@ -500,6 +500,66 @@ def test_paired_gradient_gemms_match_separate_calls(ctx):
         own.close()
 
 
+def test_big_pair_matches_separate_calls(ctx):
+    """A 4096-wide hidden layer's dW (256x256 tiles) and dX (256x128 tiles)
+    share one 512-thread launch, the dW tiles' output writes draining while
+    dX tiles compute: a 3-layer MLP (batch 2048, 256 -> 4096 -> 4096 -> 16,
+    GELU, CE) through the planner, against the same step from single calls
+    on a context with the plan's workspace size (so the same kernels and K
+    splits).  Every gradient equal bit for bit."""
+    import ferrograd_amd as fa
+    G = api()
+    torch = pytest.importorskip("torch")
+    dims, B = [256, 4096, 4096, 16], 2048
+    graph, meta, mb, st = build_mlp(ctx, dims, B, "gelu", G.Optim.sgd())
+    own = fa.Context(0, ctx.ctx.stream)
+    try:
+        own.reserve_workspace(1 << 20)
+        X = fa.rng_uniform(0, 0, (B, dims[0]))
+        y = fa.rng_int(0, 1, (B,), dims[-1])
+        ins = [ctx.init_tensor_f32(X.shape, X)]
+        for l in range(3):
+            W = fa.rng_uniform(0, 10 + l, (dims[l], dims[l + 1]), -math.sqrt(6 / dims[l]),
+                               math.sqrt(6 / dims[l]))
+            b = (0.01 * np.arange(dims[l + 1]) / dims[l + 1] - 0.005).astype(f32)
+            ins += [ctx.init_tensor_f32(W.shape, W), ctx.init_tensor_f32(b.shape, b)]
+        tgt = ctx.new_onehot_init(y)
+        sch = ctx.schedule(graph.lower(meta), [G.f32_bits(0.01)] + mb[1:], ins, st)
+        ctx.dispatch_forward(sch)
+        ctx.dispatch_loss(sch, tgt)
+        ctx.dispatch_backward(sch)
+        ctx.sync()
+        grads = {t.node: ctx.download(t) for t in st.grad_tensors}
+        in_nodes = [i for i, nd in enumerate(graph.nodes) if nd.op == 0]
+        x, w1, b1, w2, b2, w3, b3 = ins
+
+        def buf(*shape):
+            return torch.empty(shape, device="cuda")
+        d0, d1, d2, d3 = dims
+        Z1, H1, Z2, H2, L = buf(B, d1), buf(B, d1), buf(B, d2), buf(B, d2), buf(B, d3)
+        own.gemm(fa.NN, B, d1, d0, x, d0, w1, d1, H1, d1, bias=b1, act=fa.ACT_GELU, Z=Z1, ldz=d1)
+        own.gemm(fa.NN, B, d2, d1, H1, d1, w2, d2, H2, d2, bias=b2, act=fa.ACT_GELU, Z=Z2, ldz=d2)
+        own.gemm(fa.NN, B, d3, d2, H2, d2, w3, d3, L, d3, bias=b3)
+        dl = buf(B, d3)
+        own.softmax_ce(L, d3, tgt, B, d3, 1.0, dlogits=dl, ldd=d3)
+        dW3, db3, dZ2 = buf(d2, d3), buf(d3), buf(B, d2)
+        own.gemm_dw(d2, d3, B, H2, d2, dl, d3, dW3, d3, colsum=db3)
+        own.gemm_bwd(fa.NT, B, d2, d3, dl, d3, w3, d3, dZ2, d2, act=fa.ACT_GELU, Zs=Z2, ldzs=d2)
+        dW2, db2, dZ1 = buf(d1, d2), buf(d2), buf(B, d1)
+        own.gemm_dw(d1, d2, B, H1, d1, dZ2, d2, dW2, d2, colsum=db2)
+        own.gemm_bwd(fa.NT, B, d1, d2, dZ2, d2, w2, d2, dZ1, d1, act=fa.ACT_GELU, Zs=Z1, ldzs=d1)
+        dW1, db1, dX = buf(d0, d1), buf(d1), buf(B, d0)
+        own.gemm_dw(d0, d1, B, x, d0, dZ1, d1, dW1, d1, colsum=db1)
+        own.gemm_bwd(fa.NT, B, d0, d1, dZ1, d1, w1, d1, dX, d0)
+        own.sync()
+        ref = [dX, dW1, db1, dW2, db2, dW3, db3]
+        for node, r in zip(in_nodes, ref):
+            assert np.array_equal(grads[node], r.cpu().numpy().reshape(-1)), node
+    finally:
+        st.plan.close()
+        own.close()
+
+
 @pytest.mark.parametrize("k1,chained", [(768, True), (1000, False)],
                          ids=["K768-chained", "K1000-13-slices"])
 def test_forward_chain_matches_separate_calls(ctx, k1, chained):
