@@ -1167,13 +1167,16 @@ void launch_skinny_pre(const GemmArgs &a, const GemmArgs &pre, hipStream_t st,
                        const CeOut *ce = nullptr);
 
 // A layer's dW (TN, GEMM 1) and dX (NT, GEMM 2) in one launch
-// (k_gemm_pair.hip): kinds of the kernels they would take alone, which must
-// be one of these 256-thread ones.  x1 / x2: output tiles (skinny: its
-// workgroups), n1 / n2: workgroups (tiles x K slices).  tiles_m / tiles_n
-// of each GemmArgs are set by the caller.
+// (k_gemm_pair.hip): kinds of the kernels they would take alone.  x1 / x2:
+// output tiles (skinny: its workgroups), n1 / n2: workgroups (tiles x K
+// slices).  tiles_m / tiles_n of each GemmArgs are set by the caller.
+// The first three kinds (256 threads, small LDS) pair with each other; the
+// last two only with their own kind, both bodies then sharing one LDS buffer:
 // kPairBig: the 8-wave pipelined tiles of large layers, dW on 256x256 (cfg
-// 6, TN) with dX on 256x128 (cfg 7, NT), 512 threads, one LDS buffer.
-enum : int { kPairSkinny = 0, kPairElem = 1, kPairPipe = 2, kPairBig = 3 };
+// 6, TN) with dX on 256x128 (cfg 7, NT), 512 threads;
+// kPairMid: both on the 4-wave 128x64 pipelined tiles (cfg 5), 256 threads.
+enum : int { kPairSkinny = 0, kPairElem = 1, kPairPipe = 2, kPairBig = 3, kPairMid = 4 };
+inline bool pair_exclusive(int kind) { return kind == kPairBig || kind == kPairMid; }
 void launch_pair(int k1, int k2, const GemmArgs &a1, const GemmArgs &a2, int x1, int n1, int x2,
                  int n2, hipStream_t st);
 // A skinny TN weight gradient (n1 workgroups) with a pair (kinds k2, k3 as

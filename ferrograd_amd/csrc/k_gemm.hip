@@ -282,6 +282,7 @@ int pair_kind(const Planned &P) {
     if (P.pipe && !P.ktail && P.splits == 1 &&
         ((P.layout == FG_TN && P.cfg == 6) || (P.layout == FG_NT && P.cfg == 7)))
         return fg::gemm::kPairBig;
+    if (P.pipe && !P.ktail && P.cfg == 5) return fg::gemm::kPairMid;
     return -1;
 }
 
@@ -295,6 +296,8 @@ void pair_grid(Planned &P, int &x, int &n) {
     if (pair_kind(P) == fg::gemm::kPairBig) {
         bm = 256;
         bn = P.layout == FG_TN ? 256 : 128;
+    } else if (pair_kind(P) == fg::gemm::kPairMid) {
+        bm = 128;
     }
     P.a.tiles_m = (P.a.M + bm - 1) / bm;
     P.a.tiles_n = (P.a.N + bn - 1) / bn;
@@ -524,11 +527,12 @@ GemmArgs dx_args(int M, int N, int K, const float *A, int lda, const float *B, i
 }
 
 // Both pairable: at most one of them splits K (the slices of a split GEMM
-// take the whole workspace).
+// take the whole workspace), and a kind that pairs only with itself has its
+// own kind beside it.
 bool pairable(const Planned &P1, const Planned &P2) {
     const int k1 = pair_kind(P1), k2 = pair_kind(P2);
-    return k1 >= 0 && k2 >= 0 && (P1.splits == 1 || P2.splits == 1) &&
-           ((k1 == fg::gemm::kPairBig) == (k2 == fg::gemm::kPairBig));
+    if (k1 < 0 || k2 < 0 || (P1.splits > 1 && P2.splits > 1)) return false;
+    return fg::gemm::pair_exclusive(k1) || fg::gemm::pair_exclusive(k2) ? k1 == k2 : true;
 }
 
 // Both validated and planned, and pairable.
@@ -716,7 +720,7 @@ int gemm_dw_dw_dx_f32(fg_ctx *ctx, int M0, int N0, int K0, const float *A0, int 
                      "fg_gemm_dw_f32", fg::gemm::kProNone, P0) ||
         !plan_pair(ctx, dw_args(M1, N1, K1, A1, lda1, B1, ldb1, C1, ldc1, acc1, colsum1, colsum_acc1),
                    dx_args(M2, N2, K2, A2, lda2, B2, ldb2, act, Zs, ldzs, C2, ldc2, acc2), P1, P2) ||
-        pair_kind(P0) != fg::gemm::kPairSkinny || pair_kind(P1) == fg::gemm::kPairBig) {
+        pair_kind(P0) != fg::gemm::kPairSkinny || fg::gemm::pair_exclusive(pair_kind(P1))) {
         fg::clear_error();
         return separate();
     }
@@ -757,7 +761,7 @@ int gemm_dw_dw_dx_dispatches(fg_ctx *ctx, int M0, int N0, int K0, const void *A0
     plan_quiet(ctx, FG_NT, dx_args(M2, N2, K2, (const float *)A2, lda2, (const float *)B2, ldb2,
                                    FG_ACT_NONE, nullptr, 0, c, N2, 0), P2);
     if (pair_kind(P0) != fg::gemm::kPairSkinny || !pairable(P1, P2) ||
-        pair_kind(P1) == fg::gemm::kPairBig)
+        fg::gemm::pair_exclusive(pair_kind(P1)))
         return sep;
     return 1 + (P1.splits > 1) + (P2.splits > 1);
 }

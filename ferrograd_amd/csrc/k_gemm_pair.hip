@@ -4,9 +4,10 @@
 // On a latency-bound step (c1: every kernel a few microseconds, dispatches
 // back to back) launching them separately costs one whole dispatch; here the
 // first n1 workgroups run the dW body and the rest the dX body, each exactly
-// as its own kernel would (same tile walk, same K slices, same bits).  Only
-// the small 256-thread kernels pair: the skinny kernel and the 64x64 tiles
-// (element loads or pipelined).
+// as its own kernel would (same tile walk, same K slices, same bits).  The
+// small 256-thread kernels pair with each other (the skinny kernel and the
+// 64x64 tiles, element loads or pipelined); the pipelined 128x64 tiles and
+// the large layers' 8-wave tiles each pair with their own kind.
 #include "fg_gemm_skinny.h"
 
 namespace fg {
@@ -118,6 +119,21 @@ __global__ __launch_bounds__(512) void gemm_pair_big(GemmArgs a1, GemmArgs a2, i
     }
 }
 
+// The 1024-wide layers' pair: dW and dX both on the 4-wave 128x64 tiles (one
+// LDS buffer, the same size for both).  Alone, a 128x64 data gradient of
+// 256 tiles runs one wave per SIMD; beside the weight gradient's tiles the
+// CUs hold three workgroups and the waves hide each other's waits.
+__global__ __launch_bounds__(256) void gemm_pair_mid(GemmArgs a1, GemmArgs a2, int x1, int n1,
+                                                     int x2) {
+    const int w = blockIdx.x;
+    if (w < n1) {
+        gemm_f32_pipe_body<128, 64, 32, 2, 2, false, true, kProNone, false>(a1, w % x1, w / x1);
+    } else {
+        const int v = w - n1;
+        gemm_f32_pipe_body<128, 64, 32, 2, 2, true, false, kProNone, false>(a2, v % x2, v / x2);
+    }
+}
+
 }  // namespace
 
 void launch_triple(const GemmArgs &a1, int n1, int k2, const GemmArgs &a2, int x2, int n2, int k3,
@@ -137,6 +153,10 @@ void launch_pair(int k1, int k2, const GemmArgs &a1, const GemmArgs &a2, int x1,
                  int n2, hipStream_t st) {
     if (k1 == kPairBig) {  // then k2 is too (pairable)
         gemm_pair_big<<<dim3(n1 + n2), dim3(512), 0, st>>>(a1, a2, x1, n1, x2);
+        return;
+    }
+    if (k1 == kPairMid) {  // likewise
+        gemm_pair_mid<<<dim3(n1 + n2), dim3(256), 0, st>>>(a1, a2, x1, n1, x2);
         return;
     }
     switch (k1) {  // GEMM 1 is the TN weight gradient

@@ -500,20 +500,25 @@ def test_paired_gradient_gemms_match_separate_calls(ctx):
         own.close()
 
 
-def test_big_pair_matches_separate_calls(ctx):
+@pytest.mark.parametrize("d0", [256, 1024], ids=["in256", "in1024-mid-pair"])
+def test_big_pair_matches_separate_calls(ctx, d0):
     """A 4096-wide hidden layer's dW (256x256 tiles) and dX (256x128 tiles)
     share one 512-thread launch, the dW tiles' output writes draining while
-    dX tiles compute: a 3-layer MLP (batch 2048, 256 -> 4096 -> 4096 -> 16,
-    GELU, CE) through the planner, against the same step from single calls
-    on a context with the plan's workspace size (so the same kernels and K
-    splits).  Every gradient equal bit for bit."""
+    dX tiles compute; with 1024 inputs the first layer's dW and dX (both on
+    128x64 tiles) share another.  A 3-layer MLP (batch 2048, d0 -> 4096 ->
+    4096 -> 16, GELU, CE) through the planner, against the same step from
+    single calls on a context with the plan's workspace size (so the same
+    kernels and K splits).  Every gradient equal bit for bit."""
     import ferrograd_amd as fa
     G = api()
     torch = pytest.importorskip("torch")
-    dims, B = [256, 4096, 4096, 16], 2048
+    dims, B = [d0, 4096, 4096, 16], 2048
     graph, meta, mb, st = build_mlp(ctx, dims, B, "gelu", G.Optim.sgd())
     own = fa.Context(0, ctx.ctx.stream)
     try:
+        desc = st.plan.describe()
+        # one launch per layer in the backward (each layer's pair)
+        assert "kernels per step: 11 (forward 4, loss 2, backward 4, optim 1)" in desc, desc
         own.reserve_workspace(1 << 20)
         X = fa.rng_uniform(0, 0, (B, dims[0]))
         y = fa.rng_int(0, 1, (B,), dims[-1])
