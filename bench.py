@@ -266,9 +266,11 @@ def gemm_components(ctx, reps: int, want_host: bool = False):
 
 
 def c5_gemm_kernels(ctx):
-    """The three hidden-layer GEMMs of the c5 step on its shapes and
-    epilogues (random operands, library generator): key -> (description,
-    launch closure, algorithmic bytes per launch)."""
+    """The hidden-layer GEMMs of the c5 step on its shapes and epilogues
+    (random operands, library generator): key -> (description, launch
+    closure, algorithmic bytes per launch, GEMMs per launch, launches per
+    step).  The step runs the forward and the dW + dX pair
+    (fg_matmul_bwd_f32: one launch); dX and dW are also timed alone."""
     import torch
 
     import ferrograd_amd as fa
@@ -281,35 +283,46 @@ def c5_gemm_kernels(ctx):
         ctx.rng_normal(4, 500 + i, 0.0, 1.0, t, t.numel())
     H, Z, dX, dW = (torch.empty(shape, device="cuda") for shape in
                     ((M, N), (M, N), (M, K), (K, N)))
+    dx_bytes = 4 * (M * N + K * N + 2 * M * K)
+    dw_bytes = 4 * (M * K + M * N + K * N + N)
     return {
         "gemm_c5_fwd": ("NN 2048x4096x4096 + bias + GELU, Z stored (forward)",
                         lambda: ctx.gemm(fa.NN, M, N, K, X, K, W, N, H, N, bias=b,
                                          act=fa.ACT_GELU, Z=Z, ldz=N),
-                        4 * (M * K + K * N + N + 2 * M * N)),
-        "gemm_c5_dx": ("NT 2048x4096x4096 * GELU'(Z) (dX of a hidden layer)",
+                        4 * (M * K + K * N + N + 2 * M * N), 1, 6),
+        "gemm_c5_bwd_pair": ("TN 4096x4096x2048 + fused dbias and NT 2048x4096x4096 * GELU'(Z) "
+                             "in one launch (dW, db and dX of a hidden layer)",
+                             lambda: ctx.matmul_bwd(M, N, K, X, K, W, N, dZ, N, dX, K, dW, N,
+                                                    dbias=db, act=fa.ACT_GELU, Zs=Zs, ldzs=K),
+                             # dZ is read by both GEMMs
+                             dx_bytes + dw_bytes, 2, 6),
+        "gemm_c5_dx": ("NT 2048x4096x4096 * GELU'(Z) (dX of a hidden layer, alone)",
                        lambda: ctx.gemm_bwd(fa.NT, M, K, N, dZ, N, W, N, dX, K,
                                             act=fa.ACT_GELU, Zs=Zs, ldzs=K),
-                       4 * (M * N + K * N + 2 * M * K)),
-        "gemm_c5_dw": ("TN 4096x4096x2048 + fused dbias (dW, db of a hidden layer)",
+                       dx_bytes, 1, 0),
+        "gemm_c5_dw": ("TN 4096x4096x2048 + fused dbias (dW, db of a hidden layer, alone)",
                        lambda: ctx.gemm_dw(K, N, M, X, K, dZ, N, dW, N, colsum=db),
-                       4 * (M * K + M * N + K * N + N)),
+                       dw_bytes, 1, 0),
     }
 
 
 def c5_gemm_shares(ctx, reps: int, step_ms: float):
-    """The three GEMMs that make up 18 of the c5 step's 24 (6 of each per
-    step), timed alone with HIP events on the step's own shapes and
-    epilogues: forward NN 2048x4096x4096 + bias + GELU (+Z), dX NT
-    2048x4096x4096 with the GELU derivative, dW TN 4096x4096x2048 with the
-    fused dbias.  share = 6 * time / step time."""
-    flops = 2.0 * 2048 * 4096 * 4096
+    """The hidden-layer GEMMs, 18 of the c5 step's 24 GEMMs, timed with HIP
+    events on the step's own shapes and epilogues: the forward NN
+    2048x4096x4096 + bias + GELU (+Z), 6 launches per step, and the
+    backward pair (dW TN 4096x4096x2048 with the fused dbias beside dX NT
+    2048x4096x4096 with the GELU derivative, one launch), 6 per step;
+    share = launches per step * time / step time.  dX and dW alone (share
+    None: the step does not launch them alone) for comparison."""
+    gemm = 2.0 * 2048 * 4096 * 4096
     out = {}
-    for key, (what, fn, nbytes) in c5_gemm_kernels(ctx).items():
+    for key, (what, fn, nbytes, gemms, per_step) in c5_gemm_kernels(ctx).items():
         t = event_time_ms(fn, reps, warm_ms=200)
+        flops = gemms * gemm
         out[key] = {"what": what, "ms": t, "tflops": flops / t / 1e9,
-                    "frac": flops / t / 1e9 / PEAK_FP32_MFMA_TFLOPS, "per_step": 6,
-                    "step_share": 6 * t / step_ms, "flops_per_launch": flops,
-                    "algorithmic_bytes": nbytes}
+                    "frac": flops / t / 1e9 / PEAK_FP32_MFMA_TFLOPS, "per_step": per_step,
+                    "step_share": per_step * t / step_ms if per_step else None,
+                    "flops_per_launch": flops, "algorithmic_bytes": nbytes}
     return out
 
 
@@ -672,6 +685,7 @@ ONLY = {
     "gemm_c2": only_gemm_c2,
     "gemm_c5_hidden": only_gemm_c5_hidden,
     "gemm_c5_fwd": only_c5_gemm("gemm_c5_fwd"),
+    "gemm_c5_bwd_pair": only_c5_gemm("gemm_c5_bwd_pair"),
     "gemm_c5_dx": only_c5_gemm("gemm_c5_dx"),
     "gemm_c5_dw": only_c5_gemm("gemm_c5_dw"),
     "softmax_ce_c3": only_softmax_ce_c3,
@@ -1025,11 +1039,13 @@ def main() -> int:
     # the three hidden-layer GEMMs per step).
     shares = c5_gemm_shares(ctx, args.reps, ms_per_step)
     comps["c5_step_gemms"] = shares
-    dom_key = max(shares, key=lambda k: shares[k]["step_share"])
+    dom_key = max((k for k in shares if shares[k]["step_share"]),
+                  key=lambda k: shares[k]["step_share"])
     dom = shares[dom_key]
+    kernel_name = "gemm_pair_big" if dom_key == "gemm_c5_bwd_pair" else "gemm_f32_pipe"
     roofline = {
         "bound": "mfma",
-        "kernel": "gemm_f32_pipe " + dom["what"] + " -- the c5 step's largest kernel time share",
+        "kernel": kernel_name + " " + dom["what"] + " -- the c5 step's largest kernel time share",
         "achieved": dom["tflops"],
         "peak": PEAK_FP32_MFMA_TFLOPS,
         "unit": "TFLOP/s",

@@ -231,6 +231,27 @@ extern "C" {
         ldc: c_int,
         accumulate: c_int,
     ) -> c_int;
+    pub fn fg_matmul_bwd_f32(
+        ctx: *mut fg_ctx,
+        M: c_int,
+        N: c_int,
+        K: c_int,
+        d_X: *const f32,
+        ldx: c_int,
+        d_W: *const f32,
+        ldw: c_int,
+        d_dZ: *const f32,
+        lddz: c_int,
+        act: c_int,
+        d_Zs: *const f32,
+        ldzs: c_int,
+        d_dX: *mut f32,
+        lddx: c_int,
+        d_dW: *mut f32,
+        lddw: c_int,
+        d_dbias: *mut f32,
+        accumulate: c_int,
+    ) -> c_int;
     pub fn fg_linear_bwd_f32(
         ctx: *mut fg_ctx,
         act: c_int,

@@ -129,6 +129,15 @@ class Context:
              _ptr(Zs), ldzs, _ptr(dC), lddc, _ptr(dX), lddx or K, _ptr(dW), lddw or N,
              _ptr(dbias), int(accumulate), _ptr(dZ), lddz or N)
 
+    def matmul_bwd(self, M: int, N: int, K: int, X, ldx: int, W, ldw: int, dZ, lddz: int, dX,
+                   lddx: int, dW, lddw: int, dbias=None, act: int = ACT_NONE, Zs=None,
+                   ldzs: int = 0, accumulate: bool = False) -> None:
+        """A matmul node's gradients from dZ: dW = X^T.dZ (+ dbias = colsum(dZ))
+        and dX = (dZ.W^T) * act'(Zs), in one launch when their kernels pair."""
+        call("fg_matmul_bwd_f32", self.handle, M, N, K, _ptr(X), ldx, _ptr(W), ldw, _ptr(dZ),
+             lddz, act, _ptr(Zs), ldzs, _ptr(dX), lddx, _ptr(dW), lddw, _ptr(dbias),
+             int(accumulate))
+
     def gemm_dw_x16(self, dtype: int, M: int, N: int, K: int, A, lda: int, B, ldb: int, C,
                     ldc: int, accumulate: bool = False, colsum=None,
                     colsum_accumulate: bool = False) -> None:

@@ -868,6 +868,27 @@ FG_API int fg_linear_bwd_f32(fg_ctx *ctx, int act, int M, int N, int K, const fl
     return FG_OK;
 }
 
+FG_API int fg_matmul_bwd_f32(fg_ctx *ctx, int M, int N, int K, const float *d_X, int ldx,
+                             const float *d_W, int ldw, const float *d_dZ, int lddz, int act,
+                             const float *d_Zs, int ldzs, float *d_dX, int lddx, float *d_dW,
+                             int lddw, float *d_dbias, int accumulate) {
+    const char *who = "fg_matmul_bwd_f32";
+    FG_REQUIRE(ctx, FG_ERR_INVALID_ARGUMENT, "%s: ctx is NULL", who);
+    FG_REQUIRE(act >= FG_ACT_NONE && act <= FG_ACT_GELU, FG_ERR_INVALID_ARGUMENT,
+               "%s: bad act %d", who, act);
+    FG_REQUIRE(M >= 0 && N >= 0 && K >= 0, FG_ERR_SHAPE, "%s: negative dimension", who);
+    FG_REQUIRE(d_X && d_W && d_dZ && d_dX && d_dW, FG_ERR_INVALID_ARGUMENT,
+               "%s: NULL operand or output", who);
+    FG_REQUIRE(ldx >= K && ldw >= N && lddz >= N && lddx >= K && lddw >= N,
+               FG_ERR_INVALID_ARGUMENT, "%s: a leading dimension is below its row length", who);
+    FG_REQUIRE(act == FG_ACT_NONE || (d_Zs && ldzs >= K), FG_ERR_INVALID_ARGUMENT,
+               "%s: act %d needs Zs with ldzs >= K", who, act);
+    // dW: TN K x N over M; dX: NT M x K over N.
+    return fg::gemm_dw_dx_f32(ctx, K, N, M, d_X, ldx, d_dZ, lddz, d_dW, lddw, accumulate,
+                              d_dbias, accumulate, M, K, N, d_dZ, lddz, d_W, ldw, act, d_Zs,
+                              ldzs, d_dX, lddx, accumulate);
+}
+
 namespace fg {
 uint64_t bias_grad_ws_bytes(int cus, int M, int N) {
     return colsum::split_of(cus > 0 ? cus : 256, M, N).partial_floats(N) * sizeof(float);

@@ -165,6 +165,25 @@ int fg_linear_bwd_f32(fg_ctx *ctx, int act, int M, int N, int K,
                       float *d_dX, int lddx, float *d_dW, int lddw, float *d_dbias,
                       int accumulate, float *d_dZ, int lddz);
 
+/* A matmul node's two gradients from its upstream gradient dZ[M][N] (the
+ * product C = X.W with X[M][K], W[K][N]), all outputs (=|+=) by accumulate:
+ *   dW = X^T.dZ [K][N] ld lddw, and dbias = colsum(dZ) unless d_dbias is NULL;
+ *   dX = (dZ.W^T) * act'(Zs) [M][K] ld lddx, Zs[M][K] the pre-activation of
+ *   X's producer (act NONE: the plain product, Zs ignored).
+ * Both GEMMs read dZ and write different tensors, so when the kernels they
+ * would take alone pair (the large layers' 8-wave tiles, the 128x64 tiles,
+ * the small tiles), one launch runs both, each part exactly as its own call:
+ * fg_gemm_dw_f32 + fg_gemm_bwd_f32 give the same bits.  Otherwise the two
+ * calls run in turn.  Replaces the two matmul backward kernels
+ * (op/matmul/mod.rs:75-94, Some(0) and Some(1)) that
+ * kernel/backward.rs:229-371 generates for one matmul node, with the
+ * producer activation's backward (unary.rs) inlined into dA. */
+int fg_matmul_bwd_f32(fg_ctx *ctx, int M, int N, int K,
+                      const float *d_X, int ldx, const float *d_W, int ldw,
+                      const float *d_dZ, int lddz, int act, const float *d_Zs, int ldzs,
+                      float *d_dX, int lddx, float *d_dW, int lddw, float *d_dbias,
+                      int accumulate);
+
 /* Element types of tensors: SimpleDType F32 / F16 / BF16
  * (crates/fused_gpu/src/dispatch/backend/mod.rs:335-427). 16-bit tensors are
  * stored as 16-bit words; kernels compute in fp32 and round to the storage

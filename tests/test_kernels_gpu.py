@@ -269,6 +269,63 @@ def test_linear_bwd_parity(gpu_ctx, case, mat):
             own.close()
 
 
+@pytest.mark.parametrize("case", [
+    # (M, N, K, act, accumulate)
+    (2048, 4096, 4096, O.ACT_GELU, False),  # hidden layer: the 8-wave tiles' pair
+    (2048, 4096, 1024, O.ACT_NONE, False),  # first layer: the 128x64 tiles' pair
+    (64, 256, 784, O.ACT_RELU, True),       # c1's first layer: the small kernels' pair
+    (100, 33, 17, O.ACT_GELU, True),        # unaligned rows: two launches
+], ids=lambda c: f"{c[0]}x{c[1]}x{c[2]}-act{c[3]}{'-acc' if c[4] else ''}")
+def test_matmul_bwd_matches_separate_calls(case):
+    """fg_matmul_bwd_f32 (dW = X^T.dZ + dbias, dX = (dZ.W^T) * act'(Zs), one
+    launch where the two kernels pair) against fg_gemm_dw_f32 and
+    fg_gemm_bwd_f32 on the same context and workspace: every output equal
+    bit for bit.  Shapes the oracle finishes quickly are also checked
+    against it (GEMM tolerance 1e-5*sqrt(reduction length))."""
+    torch = _torch()
+    import ferrograd_amd as fa
+    M, N, K, act, acc = case
+    note(f"matmul_bwd M={M} N={N} K={K} act={act} acc={acc}")
+    rng = np.random.default_rng(M + 5 * N + 11 * K)
+    X = rng.standard_normal((M, K)).astype(f32)
+    W = (rng.standard_normal((K, N)) / math.sqrt(K)).astype(f32)
+    dZ = rng.standard_normal((M, N)).astype(f32)
+    Zs = rng.standard_normal((M, K)).astype(f32)
+    dX0, dW0, db0 = (rng.standard_normal(s).astype(f32) for s in ((M, K), (K, N), (N,)))
+    own = fa.Context(0, torch.cuda.current_stream().cuda_stream)
+    try:
+        own.reserve_workspace(1 << 20)
+        gX, gW, gdZ, gZs = dev(X), dev(W), dev(dZ), dev(Zs)
+        outs = []
+        for fused in (True, False):
+            gx, gw, gb = dev(dX0), dev(dW0), dev(db0)
+            if fused:
+                own.matmul_bwd(M, N, K, gX, K, gW, N, gdZ, N, gx, K, gw, N, dbias=gb, act=act,
+                               Zs=gZs, ldzs=K, accumulate=acc)
+            else:
+                own.gemm_dw(K, N, M, gX, K, gdZ, N, gw, N, accumulate=acc, colsum=gb,
+                            colsum_accumulate=acc)
+                own.gemm_bwd(fa.NT, M, K, N, gdZ, N, gW, N, gx, K, act=act, Zs=gZs, ldzs=K,
+                             accumulate=acc)
+            own.sync()
+            outs.append([host(gx), host(gw), host(gb)])
+        for a, b in zip(*outs):
+            assert np.array_equal(a, b)
+        if M * N * K <= 1 << 24:
+            ref_x = O.gemm(O.NT, dZ, W)
+            ref_x = (O.act_bwd(act, ref_x, Zs) if act != O.ACT_NONE else ref_x) + (
+                dX0 if acc else 0)
+            ref_w = O.gemm(O.TN, X, dZ) + (dW0 if acc else 0)
+            ref_b = O.bias_grad(dZ) + (db0 if acc else 0)
+            gx, gw, gb = outs[0]
+            assert normwise_rel(gx, ref_x) < 1e-5 * math.sqrt(N)
+            assert normwise_rel(gw, ref_w) < 1e-5 * math.sqrt(M)
+            assert normwise_rel(gb, ref_b) < 1e-5 * math.sqrt(M)
+    finally:
+        own.sync()
+        own.close()
+
+
 @pytest.mark.parametrize("mat", [False, True], ids=["prologue", "dZ"])
 def test_linear_bwd_relu_mask_from_output(gpu_ctx, mat):
     """For ReLU the forward output C = max(Z, 0) gives the same mask as Z,
