@@ -63,6 +63,13 @@ struct Args {
     // workgroups of the first tile row, rounded to the storage type once.
     uint16_t *colsum;
     int colsum_accumulate;
+    // K split (pipelined kernel only, never with colsum): workgroup row s
+    // (blockIdx.y) multiplies K elements [s * ksplit, (s + 1) * ksplit) and
+    // writes its fp32 sums, without epilogue, into the M x N slot s of
+    // partial (row length N); sum_slices16 then adds the slots in slot order
+    // and applies the epilogue.  ksplit 0: no split.
+    float *partial;
+    int ksplit;
 };
 
 // Element conversion and the MFMA of one storage type.
@@ -254,6 +261,18 @@ __device__ __forceinline__ void epi16_x4(const Args &p, f32x4 v, f32x4 bv, int r
     st4(c, v);
 }
 
+// A K slice's raw sums: four (or the last few) fp32 values of one row of
+// its slot.  The slot's rows are N floats from a 256-byte aligned base.
+__device__ __forceinline__ void store_slice16(const Args &p, f32x4 v, int row, int col) {
+    float *q = p.partial + (size_t)row * p.N + col;
+    if (p.N % 4 == 0) {
+        *reinterpret_cast<f32x4 *>(q) = v;
+    } else {
+#pragma unroll 1
+        for (int t = 0; t < 4 && col + t < p.N; ++t) q[t] = v[t];
+    }
+}
+
 // Epilogue shared by the 16-bit kernels.  Accumulator register r of lane
 // (h, l32) in block (i, j) holds C[r0 + 32i + 8(r/4) + 4h + r%4][c0 + 32j + l32];
 // each wave stages one 32 x WTN slice of fp32 sums in LDS (stride WTN+4)
@@ -299,7 +318,9 @@ __device__ __forceinline__ void store_tile16(const Args &p, const f32x16 (&acc)[
                 nxt = *reinterpret_cast<const f32x4 *>(stage + (rr0 + (q + 1) * RPP) * kStageLd + c4);
             const int row = r0 + i * 32 + rr0 + q * RPP;
             if (row >= p.M || col >= p.N) continue;
-            if (vec) {
+            if (p.ksplit > 0) {
+                store_slice16(p, v, row, col);
+            } else if (vec) {
                 epi16_x4<BF>(p, v, bv, row, col);
             } else {
                 uint16_t *crow = p.C + (size_t)row * p.ldc;
@@ -528,6 +549,13 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm16_pipe(Args p) {
     constexpr int kBytes = (kStages * kStageSz * 2 > kEpiBytes) ? kStages * kStageSz * 2 : kEpiBytes;
     __shared__ __attribute__((aligned(16))) uint16_t lds[kBytes / 2];
 
+    if (p.ksplit > 0) {  // K slice blockIdx.y: offset operands, its own slot
+        const int kb = blockIdx.y * p.ksplit;
+        p.A += AK ? (size_t)kb : (size_t)kb * p.lda;
+        p.B += BNC ? (size_t)kb * p.ldb : (size_t)kb;
+        p.K = min(p.ksplit, p.K - kb);
+        p.partial += (size_t)blockIdx.y * p.M * p.N;
+    }
     int tile_m, tile_n;
     tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tile_m, tile_n);
     const int m0 = tile_m * BM, n0 = tile_n * BN;
@@ -777,13 +805,59 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm16_pipe(Args p) {
                                       wave, lane);
 }
 
+// The slots of a K-split GEMM summed in slot order (fp32), then the GEMM's
+// epilogue applied to each sum exactly as the kernel applies it to its own
+// (epi16_x4 on four columns, epi16 on the last few of a row).  One thread
+// per four columns of a row.
+template <bool BF>
+__global__ __launch_bounds__(256) void sum_slices16(Args p, int splits) {
+    using E = T16<BF>;
+    const int g4 = (p.N + 3) / 4;
+    const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (q >= (int64_t)p.M * g4) return;
+    const int row = (int)(q / g4), col = (int)(q % g4) * 4;
+    const size_t slot = (size_t)p.M * p.N;
+    const float *src = p.partial + (size_t)row * p.N + col;
+    if (p.vec_out && p.N % 4 == 0) {
+        f32x4 v = *reinterpret_cast<const f32x4 *>(src);
+#pragma unroll 1
+        for (int s = 1; s < splits; ++s) v += *reinterpret_cast<const f32x4 *>(src + s * slot);
+        f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+        if (p.mode == 0 && p.bias) {
+            const u32x2 w = *reinterpret_cast<const u32x2 *>(p.bias + col);
+            bv = f32x4{E::to_f((uint16_t)w[0]), E::to_f((uint16_t)(w[0] >> 16)),
+                       E::to_f((uint16_t)w[1]), E::to_f((uint16_t)(w[1] >> 16))};
+        }
+        epi16_x4<BF>(p, v, bv, row, col);
+        return;
+    }
+    uint16_t *crow = p.C + (size_t)row * p.ldc;
+    const uint16_t *bias = p.mode == 0 ? p.bias : nullptr;
+#pragma unroll 1
+    for (int t = 0; t < 4 && col + t < p.N; ++t) {
+        float v = src[t];
+#pragma unroll 1
+        for (int s = 1; s < splits; ++s) v += src[t + s * slot];
+        float zt;
+        float ot = epi16<BF>(p, v, bias, row, col + t, &zt);
+        if (p.mode == 0 && p.Z) p.Z[(size_t)row * p.ldz + col + t] = E::from_f(zt);
+        if (p.accumulate) ot += E::to_f(crow[col + t]);
+        crow[col + t] = E::from_f(ot);
+    }
+}
+
 template <int BM, int BN, int WGM, int WGN, int BK, bool AK, bool BNC, bool BF>
 void launch_pipe16(const Args &a0, hipStream_t st) {
     Args a = a0;
     a.tiles_m = (a.M + BM - 1) / BM;
     a.tiles_n = (a.N + BN - 1) / BN;
+    const int splits = a.ksplit > 0 ? (a.K + a.ksplit - 1) / a.ksplit : 1;
     gemm16_pipe<BM, BN, BK, WGM, WGN, AK, BNC, BF>
-        <<<a.tiles_m * a.tiles_n, 64 * WGM * WGN, 0, st>>>(a);
+        <<<dim3(a.tiles_m * a.tiles_n, splits), 64 * WGM * WGN, 0, st>>>(a);
+    if (splits > 1) {
+        const int64_t threads = (int64_t)a.M * ((a.N + 3) / 4);
+        sum_slices16<BF><<<(unsigned)((threads + 255) / 256), 256, 0, st>>>(a, splits);
+    }
 }
 
 template <int BM, int BN, int WGM, int WGN, int BK, bool AK, bool BNC, bool VEC, bool BF>

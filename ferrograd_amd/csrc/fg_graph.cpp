@@ -1695,8 +1695,10 @@ FG_API int fg_plan_create(fg_ctx *ctx, const fg_graph *g, const uint32_t *meta, 
         for (const Launch &L : *list)
             if ((rc = check_launch(*P, L))) return rc;
 
-    // Workspace: at least 1 MiB (what lets few-tile GEMMs split K), and the
-    // partial sums of the largest unfused bias-gradient reduction.
+    // Workspace: at least 1 MiB (what lets few-tile fp32 GEMMs split K), the
+    // partial sums of the largest unfused bias-gradient reduction, and the K
+    // slices of the largest split 16-bit GEMM (fp32 slots of its output: the
+    // 1000-wide head of a batch-2048 MLP takes 4 x 8 MB).
     {
         const int cus = ctx && ctx->cu_count > 0 ? ctx->cu_count : 256;
         uint64_t ws = 1u << 20;
@@ -1704,6 +1706,12 @@ FG_API int fg_plan_create(fg_ctx *ctx, const fg_graph *g, const uint32_t *meta, 
             for (const Launch &L : *list)
                 if (L.kind == LK_BIAS_GRAD)
                     ws = std::max<uint64_t>(ws, fg::bias_grad_ws_bytes(cus, L.M, L.N));
+        for (auto *list : {&P->fwd, &P->bwd_seed, &P->bwd_fused})
+            for (const Launch &L : *list)
+                if ((L.kind == LK_GEMM || L.kind == LK_GEMM_BWD) && L.dtype != FG_DTYPE_F32 &&
+                    L.sExtra == kNone)
+                    ws = std::max<uint64_t>(
+                        ws, fg::gemm16_split_ws_bytes(cus, L.layout, L.M, L.N, L.K));
         P->ws_bytes = ws;
         P->ws_slot = P->new_slot(ws / 4);
     }
@@ -2122,7 +2130,11 @@ FG_API int fg_plan_describe(const fg_plan *p, char *buf, size_t len, size_t *nee
     // Dispatches of a GEMM launch: 2 when K is split (the slices, then the
     // kernel that sums them in slice order and applies the epilogue).
     auto gemm_dispatches = [&](const Launch &L) {
-        if ((L.kind != LK_GEMM && L.kind != LK_GEMM_BWD) || L.dtype != FG_DTYPE_F32) return 1;
+        if (L.kind != LK_GEMM && L.kind != LK_GEMM_BWD) return 1;
+        if (L.dtype != FG_DTYPE_F32)
+            return fg::gemm16_dispatches(wc, L.sExtra != kNone ? FG_TN : L.layout, L.M, L.N, L.K,
+                                         p->ptr(L.sA), L.lda, p->ptr(L.sB), L.ldb,
+                                         L.kind == LK_GEMM && L.sExtra != kNone);
         return fg::gemm_f32_dispatches(wc, L.sExtra != kNone ? FG_TN : L.layout, L.M, L.N, L.K,
                                        p->ptr(L.sA), L.lda, p->ptr(L.sB), L.ldb,
                                        L.kind == LK_GEMM && L.sExtra != kNone);
@@ -2140,7 +2152,10 @@ FG_API int fg_plan_describe(const fg_plan *p, char *buf, size_t len, size_t *nee
         for (size_t i = 0; i < v.size(); ++i) {
             const Launch &L = v[i];
             s += "  " + L.desc;
-            if (gemm_dispatches(L) > 1) {
+            const int nd = gemm_dispatches(L);
+            if (nd == 3) {  // a 16-bit dW off the pipelined kernel
+                s += " [GEMM + column-sum reduction]";
+            } else if (nd > 1) {
                 const bool summed_by_next = L.chain_next && i + 1 < v.size() &&
                                             chain_dispatches(L, v[i + 1]) == 2;
                 s += summed_by_next ? " [K split: slices, summed by the next launch]"

@@ -114,6 +114,13 @@ int noalloc_init(int device);
 // Bytes of workspace fg_bias_grad needs for an M x N reduction on a device
 // with `cus` compute units (the partial sums of its row splits).
 uint64_t bias_grad_ws_bytes(int cus, int M, int N);
+// Workspace bytes of the K slices a 16-bit GEMM of this shape takes when the
+// workspace holds them (0: no split).
+uint64_t gemm16_split_ws_bytes(int cus, int layout, int M, int N, int K);
+// Dispatches of one 16-bit GEMM call (no launch; colsum: the fused bias
+// gradient of fg_gemm_dw_x16 is asked).
+int gemm16_dispatches(fg_ctx *ctx, int layout, int M, int N, int K, const void *A, int lda,
+                      const void *B, int ldb, bool colsum);
 
 // Adam with device-resident step counter / bias-correction scalars
 // (k_optim.hip).  d_state points at adam_dev_state_bytes() zeroed bytes.

@@ -50,6 +50,68 @@ int pick_cfg16(int layout, int M, int N, int K, int cus) {
     return 3;
 }
 
+// K slices for a pipelined GEMM whose output tiles fill at most half the
+// CUs (the 1000-wide head and the 1024-wide layer's data gradient of a
+// batch-2048 MLP: 64 tiles of 256x128): enough slices to give every CU a
+// workgroup, each of whole K tiles and at least four of them.  Returns the
+// number of slices (1: no split) and their depth in ks.
+int split16(int cus, int M, int N, int K, int cfg, int &ks) {
+    ks = 0;
+    const int bk = fg::gemm16::cfg_bk16(cfg);
+    // the configurations' tiles (fg_gemm16_kernel.h)
+    const int bm = cfg == 2 ? 128 : cfg == 3 ? 64 : 256;
+    const int bn = (cfg == 2 || cfg == 4 || cfg >= 7) ? 128 : cfg == 3 ? 64 : 256;
+    const int t = tiles(M, N, bm, bn);
+    if (2 * t > cus || K < 8 * bk) return 1;
+    int s = std::min(cus / t, K / (4 * bk));
+    if (s < 2) return 1;
+    int k = (K + s - 1) / s;
+    k = (k + bk - 1) / bk * bk;  // whole K tiles per slice
+    s = (K + k - 1) / k;
+    if (s < 2) return 1;
+    ks = k;
+    return s;
+}
+
+// The kernel choices of one call (operands as passed, colsum included).
+struct Plan16 {
+    bool vec = false, pipe = false;
+    int cfg = 3, splits = 1, ks = 0;
+};
+Plan16 plan16(const fg_ctx *ctx, int layout, const Args &a) {
+    Plan16 q;
+    const int cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    // 16-byte operand loads need 16-byte aligned bases and leading
+    // dimensions that keep every row start aligned (multiples of 8
+    // elements); the bounds checks split per 8-element vector, so the
+    // extents themselves are free.
+    auto al = [](const void *p, unsigned m) { return (((uintptr_t)p) & (m - 1)) == 0; };
+    q.vec = al(a.A, 16) && al(a.B, 16) && a.lda % 8 == 0 && a.ldb % 8 == 0;
+#ifdef FG_GEMM16_FORCE_CFG  // tuning builds: one tile configuration for every shape
+    q.cfg = FG_GEMM16_FORCE_CFG;
+#else
+    q.cfg = pick_cfg16(layout, a.M, a.N, a.K, cus);
+#endif
+    // The pipelined kernel: whole K tiles, 16-byte chunks of 8 elements along
+    // each row-contiguous operand's rows (B of NN / TN, A of TN).
+    const bool rc_ok = (layout == FG_NT || a.N % 8 == 0) && (layout != FG_TN || a.M % 8 == 0);
+    q.pipe = kPipe16 && q.vec && rc_ok && a.K > 0 && a.K % fg::gemm16::cfg_bk16(q.cfg) == 0 &&
+             a.M >= 8 && a.N >= 8 && q.cfg != 3;
+    // Few tiles and a long K: K slices into the context's workspace when
+    // what is reserved holds them (it is never grown for this), summed by a
+    // second kernel in slot order -- deterministic, within the GEMM
+    // tolerance of the unsplit sum.  Never with the fused column sums.
+    if (q.pipe && !a.colsum && ctx->ws) {
+        int ks;
+        const int sl = split16(cus, a.M, a.N, a.K, q.cfg, ks);
+        if (sl > 1 && (uint64_t)sl * a.M * a.N * sizeof(float) <= ctx->ws_bytes) {
+            q.splits = sl;
+            q.ks = ks;
+        }
+    }
+    return q;
+}
+
 int gemm16_common(fg_ctx *ctx, int dtype, int layout, Args &a, const char *who) {
     FG_REQUIRE(ctx, FG_ERR_INVALID_ARGUMENT, "%s: ctx is NULL", who);
     FG_REQUIRE(dtype == FG_DTYPE_F16 || dtype == FG_DTYPE_BF16, FG_ERR_UNSUPPORTED,
@@ -75,39 +137,62 @@ int gemm16_common(fg_ctx *ctx, int dtype, int layout, Args &a, const char *who) 
     FG_HIP(hipSetDevice(ctx->device));
     uint16_t *colsum = a.colsum;  // the bias gradient of fg_gemm_dw_x16, if any
     if (a.K == 0) a.A = a.B;  // loads are all masked; K=0 yields the epilogue of zero
-    // 16-byte operand loads need 16-byte aligned bases and leading
-    // dimensions that keep every row start aligned (multiples of 8
-    // elements); the bounds checks split per 8-element vector, so the
-    // extents themselves are free.
     auto al = [](const void *q, unsigned m) { return (((uintptr_t)q) & (m - 1)) == 0; };
-    const bool vec = al(a.A, 16) && al(a.B, 16) && a.lda % 8 == 0 && a.ldb % 8 == 0;
     a.vec_out = al(a.C, 8) && a.ldc % 4 == 0 && (!a.Z || (al(a.Z, 8) && a.ldz % 4 == 0)) &&
                 (!a.bias || al(a.bias, 8));
-#ifdef FG_GEMM16_FORCE_CFG  // tuning builds: one tile configuration for every shape
-    const int cfg = FG_GEMM16_FORCE_CFG;
-#else
-    const int cfg = pick_cfg16(layout, a.M, a.N, a.K, ctx->cu_count > 0 ? ctx->cu_count : 256);
-#endif
-    // The pipelined kernel: whole K tiles, 16-byte chunks of 8 elements along
-    // each row-contiguous operand's rows (B of NN / TN, A of TN).
-    const bool rc_ok = (layout == FG_NT || a.N % 8 == 0) && (layout != FG_TN || a.M % 8 == 0);
-    const bool pipe = kPipe16 && vec && rc_ok && a.K > 0 &&
-                     a.K % fg::gemm16::cfg_bk16(cfg) == 0 && a.M >= 8 && a.N >= 8 && cfg != 3;
+    const Plan16 q = plan16(ctx, layout, a);
     // Only the pipelined kernel sums B's columns; elsewhere the separate
     // reduction runs after the GEMM (same result up to the order of the
     // fp32 sums).
-    if (colsum && !pipe) a.colsum = nullptr;
+    if (colsum && !q.pipe) a.colsum = nullptr;
+    a.partial = q.splits > 1 ? static_cast<float *>(ctx->ws) : nullptr;
+    a.ksplit = q.splits > 1 ? q.ks : 0;
     if (dtype == FG_DTYPE_BF16)
-        fg::gemm16::launch_bf16(layout, a, vec, pipe, cfg, ctx->stream);
+        fg::gemm16::launch_bf16(layout, a, q.vec, q.pipe, q.cfg, ctx->stream);
     else
-        fg::gemm16::launch_f16(layout, a, vec, pipe, cfg, ctx->stream);
+        fg::gemm16::launch_f16(layout, a, q.vec, q.pipe, q.cfg, ctx->stream);
     FG_LAUNCH_CHECK(who);
-    if (colsum && !pipe)
+    if (colsum && !q.pipe)
         return fg_bias_grad(ctx, dtype, a.K, a.N, a.B, a.ldb, colsum, a.colsum_accumulate);
     return FG_OK;
 }
 
 }  // namespace
+
+namespace fg {
+// Workspace bytes a 16-bit GEMM of this shape splits K into when the
+// workspace holds them (0: it does not split), for planners that size a
+// workspace ahead.  Assumes the pipelined kernel (aligned operands).
+// Dispatches of one 16-bit GEMM call with these operands (no launch): the
+// GEMM, its summing kernel when it splits K, the column-sum reduction's two
+// when colsum is asked off the pipelined kernel.
+int gemm16_dispatches(fg_ctx *ctx, int layout, int M, int N, int K, const void *A, int lda,
+                      const void *B, int ldb, bool colsum) {
+    if (!ctx || M <= 0 || N <= 0 || K <= 0) return 1;
+    Args a{};
+    a.A = static_cast<const uint16_t *>(A);
+    a.B = static_cast<const uint16_t *>(B);
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.lda = lda;
+    a.ldb = ldb;
+    a.colsum = colsum ? reinterpret_cast<uint16_t *>(256) : nullptr;
+    const Plan16 q = plan16(ctx, layout, a);
+    if (colsum && !q.pipe) return 3;
+    return q.splits > 1 ? 2 : 1;
+}
+
+uint64_t gemm16_split_ws_bytes(int cus, int layout, int M, int N, int K) {
+    if (M <= 0 || N <= 0 || K <= 0) return 0;
+    cus = cus > 0 ? cus : 256;
+    const int cfg = pick_cfg16(layout, M, N, K, cus);
+    if (cfg == 3 || K % fg::gemm16::cfg_bk16(cfg) != 0) return 0;
+    int ks;
+    const int sl = split16(cus, M, N, K, cfg, ks);
+    return sl > 1 ? (uint64_t)sl * M * N * sizeof(float) : 0;
+}
+}  // namespace fg
 
 FG_API int fg_gemm_x16(fg_ctx *ctx, int dtype, int layout, int M, int N, int K, const void *d_A,
                        int lda, const void *d_B, int ldb, const void *d_bias, int act, void *d_C,

@@ -66,18 +66,21 @@ def test_mul_add_16bit(ctx, kind):
     assert np.all(vals(st.grad_tensors[2]) == 1.0)
 
 
+@pytest.mark.parametrize("size", ["small", "split"])
 @pytest.mark.parametrize("kind", ["f16", "bf16"])
-def test_mlp_step_16bit_matches_oracle(ctx, kind):
-    """batch 64, 96 -> 128 -> ReLU -> 40, softmax-CE, SGD lr 0.01, all
-    tensors of one 16-bit type.  The oracle composes its 16-bit GEMMs (fp32
-    sums, each node value rounded), softmax-CE on the widened logits with
-    dlogits rounded, column sums rounded; the GPU must agree within two
-    units in the last place of the type (normwise)."""
+def test_mlp_step_16bit_matches_oracle(ctx, kind, size):
+    """batch 64, 96 -> 128 -> ReLU -> 40 (small), or batch 2048, 1024 ->
+    1024 -> ReLU -> 1000 (split: the two forward GEMMs and the first layer's
+    data gradient split K into the plan's workspace), softmax-CE, SGD lr
+    0.01, all tensors of one 16-bit type.  The oracle composes its 16-bit
+    GEMMs (fp32 sums, each node value rounded), softmax-CE on the widened
+    logits with dlogits rounded, column sums rounded; the GPU must agree
+    within two units in the last place of the type (normwise)."""
     import ferrograd_amd as fa
     G = api()
     dt = O.F16 if kind == "f16" else O.BF16
     eps = 2.0 ** -10 if kind == "f16" else 2.0 ** -7
-    dims, B = [96, 128, 40], 64
+    dims, B = ([96, 128, 40], 64) if size == "small" else ([1024, 1024, 1000], 2048)
     graph, meta = G.Graph(G.CROSS_ENTROPY, G.Optim.sgd().lower), G.Metadata.new()
     fb = meta.new_field()
     fd = [meta.new_field() for _ in dims]
@@ -108,6 +111,8 @@ def test_mlp_step_16bit_matches_oracle(ctx, kind):
         ins += [dev(W), dev(b)]
     tgt = ctx.new_onehot_init(y)
     sch = ctx.schedule(graph.lower(meta), mb, ins, st)
+    desc = st.plan.describe()
+    assert ("[K split: slices + summing kernel]" in desc) == (size == "split"), desc
     ctx.dispatch_forward(sch)
     ctx.dispatch_loss(sch, tgt)
     ctx.dispatch_backward(sch)

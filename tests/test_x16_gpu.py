@@ -235,6 +235,91 @@ def test_gemm_x16_c5_hidden_shape_sampled(gpu_ctx, dtype):
                    O.ACT_GELU, sum_error_bound(dtype, O.NN, A[rows], B))
 
 
+@pytest.mark.parametrize("dtype", [F16, BF16], ids=lambda d: DT_IDS[d])
+@pytest.mark.parametrize("case", [
+    # (layout, M, N, K, mode): 64 output tiles of 256x128 over a long K, the
+    # shapes of a batch-2048 MLP's 1000-wide head and 1024-wide data gradient
+    (O.NN, 2048, 1000, 4096, "fwd"),
+    (O.NT, 2048, 1024, 4096, "bwd"),
+    (O.NN, 1024, 1024, 2048, "fwd"),   # 128x128 tiles, BK 32
+], ids=lambda c: f"{['NN', 'NT', 'TN'][c[0]]}-{c[1]}x{c[2]}x{c[3]}-{c[4]}")
+def test_gemm_x16_split_k(dtype, case):
+    """Few output tiles and a long K: the 16-bit GEMM splits K into fp32 slots
+    of the context's workspace (when reserved) and a second kernel sums them
+    in slot order and applies the epilogue.  On operands whose sums are exact
+    in fp32 (multiples of 1/4; ReLU, whose mask is exact, and C += with no
+    epilogue) the split result equals the oracle bit for bit -- every slice
+    offset and slot index is pinned; on random operands with GELU a sample
+    of rows is within the rounding bounds, as the unsplit kernel's result on
+    a context without workspace is."""
+    torch = _torch()
+    import ferrograd_amd as fa
+    layout, M, N, K, mode = case
+    note(f"gemm_x16 split-K {DT_IDS[dtype]} {case}")
+    split = fa.Context(0, torch.cuda.current_stream().cuda_stream)
+    plain = fa.Context(0, torch.cuda.current_stream().cuda_stream)
+    try:
+        split.reserve_workspace(64 << 20)
+        rng = np.random.default_rng(M + N + K + layout)
+        sa, sb = storage_shapes(layout, M, N, K)
+        rows = np.sort(rng.choice(M, size=48, replace=False))
+        rows_a = (lambda X: X[rows]) if layout != O.TN else (lambda X: X[:, rows])
+        for exact in (True, False):
+            act = O.ACT_RELU if exact else O.ACT_GELU
+            if exact:
+                A, B = quarter_ints(rng, sa, dtype), quarter_ints(rng, sb, dtype)
+                bias, Zs = quarter_ints(rng, (N,), dtype), quarter_ints(rng, (M, N), dtype)
+            else:
+                A, B = normal16(rng, sa, dtype), normal16(rng, sb, dtype, 1.0 / np.sqrt(K))
+                bias, Zs = normal16(rng, (N,), dtype, 0.1), normal16(rng, (M, N), dtype)
+            outs = []
+            for c in (split, plain):
+                dC, dZ = empty16((M, N)), empty16((M, N))
+                if mode == "fwd":
+                    c.gemm_x16(dtype, layout, M, N, K, dev16(A), sa[1], dev16(B), sb[1], dC, N,
+                               bias=dev16(bias), act=act, Z=dZ, ldz=N)
+                else:
+                    c.gemm_bwd_x16(dtype, layout, M, N, K, dev16(A), sa[1], dev16(B), sb[1], dC,
+                                   N, act=act, Zs=dev16(Zs), ldzs=N)
+                c.sync()
+                outs.append((host16(dC)[rows], host16(dZ)[rows]))
+            if mode == "fwd":
+                refC, refZ = O.gemm_x16(dtype, layout, rows_a(A), B, bias=bias, act=act,
+                                        want_z=True)
+                refV = O.gemm_x16(dtype, layout, rows_a(A), B)
+            else:
+                refC = O.gemm_bwd_x16(dtype, layout, rows_a(A), B, act=act, Zs=Zs[rows])
+            for k, (gC, gZ) in enumerate(outs):
+                if exact:
+                    assert np.array_equal(gC, refC), ("split", "plain")[k]
+                    if mode == "fwd":
+                        assert np.array_equal(gZ, refZ), ("split", "plain")[k]
+                elif mode == "fwd":
+                    check_epilogue(dtype, None, gC, gZ, refV, refC, refZ, act,
+                                   sum_error_bound(dtype, layout, rows_a(A), B))
+                else:
+                    # dC = round(round(v) * gelu'(z)): within 1.2 (esum + ulp(v)) + ulp(dC)
+                    f = lambda b: O.to_f32(dtype, b).astype(np.float64)
+                    v = O.gemm_x16(dtype, layout, rows_a(A), B)
+                    t = 1.2 * (sum_error_bound(dtype, layout, rows_a(A), B) + ulp_of(v, dtype)) \
+                        + ulp_of(refC, dtype)
+                    assert np.all(np.abs(f(gC) - f(refC)) <= t)
+                    assert np.mean(gC != refC) < 0.01
+        # C += op(A).op(B), no epilogue, on exact operands (the summing
+        # kernel's accumulate path)
+        A, B = quarter_ints(rng, sa, dtype), quarter_ints(rng, sb, dtype)
+        C0 = quarter_ints(rng, (M, N), dtype)
+        dC = dev16(C0)
+        split.gemm_x16(dtype, layout, M, N, K, dev16(A), sa[1], dev16(B), sb[1], dC, N,
+                       accumulate=True)
+        split.sync()
+        ref = O.gemm_x16(dtype, layout, rows_a(A), B, C=C0[rows])
+        assert np.array_equal(host16(dC)[rows], ref)
+    finally:
+        split.close()
+        plain.close()
+
+
 def test_gemm_x16_rejects_fp32_dtype(gpu_ctx):
     import ferrograd_amd as fa
 
