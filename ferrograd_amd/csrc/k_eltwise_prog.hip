@@ -4,6 +4,8 @@
 // for the short programs the planner emits.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "fg_act.h"
 #include "fg_eltwise.h"
 #include "fg_half.h"
@@ -89,112 +91,190 @@ __device__ __forceinline__ f32x4 quad_map(f32x4 x, F f) {
     return r;
 }
 
+template <int N>
+using QIdx = std::integral_constant<int, N>;
+// f(QIdx<0>{}), ..., f(QIdx<Q-1>{}): per-quad code with a constant quad index.
+template <int Q, class F>
+__device__ __forceinline__ void for_quads(F &&f) {
+    static_assert(Q == 1 || Q == 2, "one or two quads per thread");
+    f(QIdx<0>{});
+    if constexpr (Q > 1) f(QIdx<1>{});
+}
+
+// Q: quads per thread and pass.  Every lane runs the same instruction
+// stream, so decoding an instruction, branching on its op and reading its
+// pointers is scalar work done once per wave and pass; the scalar unit is
+// shared by the CU's waves and is what bounds short programs (tanh(a*b + c):
+// ~500 scalar instructions per wave, 60 % of the kernel's cycles).  Thread t
+// of a workgroup takes quads base + q * kThreads + t (q < Q), so each load
+// and store of the pass stays coalesced.  The pass loop is uniform: a lane
+// past the end takes an empty quad (loads give 0, stores skip), so the
+// interpreter runs outside any divergent region.
+template <int Q>
 __global__ __launch_bounds__(kThreads) void eltwise_prog_kernel(const EltProgram p) {
     const uint64_t nq = (p.n + 3) / 4;
-    const uint64_t stride = (uint64_t)gridDim.x * kThreads;
-    for (uint64_t q = (uint64_t)blockIdx.x * kThreads + threadIdx.x; q < nq; q += stride) {
-        const uint64_t i0 = 4 * q;
-        const int nv = p.n - i0 >= 4 ? 4 : (int)(p.n - i0);
-        // The register file as four plain arrays, one per element of the
-        // quad, each indexed by the same uniform register number (a float4
-        // array indexed at run time would go to scratch memory).
-        float r0[kEltRegs], r1[kEltRegs], r2[kEltRegs], r3[kEltRegs];
-#pragma unroll
-        for (int k = 0; k < kEltRegs; ++k) r0[k] = r1[k] = r2[k] = r3[k] = 0.0f;
+    const uint64_t span = (uint64_t)kThreads * Q;
+    const uint64_t stride = (uint64_t)gridDim.x * span;
+    for (uint64_t base = (uint64_t)blockIdx.x * span; base < nq; base += stride) {
+        uint64_t i0[Q];
+        int nv[Q];  // elements of quad q (0 past the end: loads give 0, stores skip)
+        // The register file: an array per element of each quad, all indexed
+        // by the same uniform register number.  Every access names its array
+        // at compile time (the quad through get / set, the element by name),
+        // which keeps each array in VGPRs, read and written through indexed
+        // moves; a float4 array, or one indexed by a run-time quad, would go
+        // to scratch memory.
+        float a0[kEltRegs], a1[kEltRegs], a2[kEltRegs], a3[kEltRegs];  // quad 0
+        float b0[kEltRegs], b1[kEltRegs], b2[kEltRegs], b3[kEltRegs];  // quad 1 (Q = 2)
+        auto get = [&](auto qc, int k) {
+            k &= kEltRegs - 1;
+            if constexpr (decltype(qc)::value == 0) return f32x4{a0[k], a1[k], a2[k], a3[k]};
+            else return f32x4{b0[k], b1[k], b2[k], b3[k]};
+        };
+        auto set = [&](auto qc, int k, f32x4 v) {
+            k &= kEltRegs - 1;
+            if constexpr (decltype(qc)::value == 0) {
+                a0[k] = v[0];
+                a1[k] = v[1];
+                a2[k] = v[2];
+                a3[k] = v[3];
+            } else {
+                b0[k] = v[0];
+                b1[k] = v[1];
+                b2[k] = v[2];
+                b3[k] = v[3];
+            }
+        };
         // The prefetched sources' quads, all loads issued before the program
         // runs: a load's value must be present when it is written to the
         // register file (indexed at run time), so loads issued by the
         // program itself each wait for their data in turn.
-        const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-        f32x4 pre[kEltPre];
+        constexpr f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+        f32x4 pre[Q][kEltPre];
+        for_quads<Q>([&](auto qc) {
+            constexpr int q = decltype(qc)::value;
+            const uint64_t qi = base + (uint64_t)q * kThreads + threadIdx.x;
+            i0[q] = 4 * qi;
+            nv[q] = qi >= nq ? 0 : (p.n - i0[q] >= 4 ? 4 : (int)(p.n - i0[q]));
 #pragma unroll
-        for (int j = 0; j < kEltPre; ++j)
-            pre[j] = (j < p.n_pre && nv == 4)
-                         ? *reinterpret_cast<const f32x4 *>(p.src[p.pre_src[j]] + i0)
-                         : zero;
-        auto get = [&](int k) { return f32x4{r0[k & 15], r1[k & 15], r2[k & 15], r3[k & 15]}; };
+            for (int k = 0; k < kEltRegs; ++k) set(qc, k, zero);
+#pragma unroll
+            for (int j = 0; j < kEltPre; ++j)
+                pre[q][j] = (j < p.n_pre && nv[q] == 4)
+                                ? *reinterpret_cast<const f32x4 *>(p.src[p.pre_src[j]] + i0[q])
+                                : zero;
+        });
         for (int k = 0; k < p.n_instr; ++k) {
             const EltInstr in = p.ins[k];
-            const f32x4 x = get(in.a), y = get(in.b);
-            f32x4 o = x;
+            // One read site for the operands and one write site for the
+            // result (each indexed access costs scalar work to set up, and
+            // more sites hold more registers).
+            f32x4 x[Q], y[Q], o[Q];
+            for_quads<Q>([&](auto qc) {
+                constexpr int q = decltype(qc)::value;
+                x[q] = get(qc, in.a);
+                y[q] = get(qc, in.b);
+                o[q] = x[q];
+            });
             bool wr = true;  // the instruction writes register in.dst
+            auto unary = [&](auto f) {
+#pragma unroll
+                for (int q = 0; q < Q; ++q) o[q] = quad_map(x[q], f);
+            };
             switch (in.op) {
                 case kEltLoad:
-                    if (in.pre && nv == 4) {
-                        switch (in.pre) {  // a constant index into pre[]
-                            case 1: o = pre[0]; break;
-                            case 2: o = pre[1]; break;
-                            case 3: o = pre[2]; break;
-                            default: o = pre[3]; break;
+#pragma unroll
+                    for (int q = 0; q < Q; ++q) {
+                        if (in.pre && nv[q] == 4) {
+                            switch (in.pre) {  // a constant index into pre[q]
+                                case 1: o[q] = pre[q][0]; break;
+                                case 2: o[q] = pre[q][1]; break;
+                                case 3: o[q] = pre[q][2]; break;
+                                default: o[q] = pre[q][3]; break;
+                            }
+                        } else {
+                            o[q] = quad_load(p, in.a, in.c, in.b, i0[q], nv[q]);
                         }
-                    } else {
-                        o = quad_load(p, in.a, in.c, in.b, i0, nv);
                     }
                     break;
-                case kEltImm: o = f32x4{in.imm, in.imm, in.imm, in.imm}; break;
+                case kEltImm:
+#pragma unroll
+                    for (int q = 0; q < Q; ++q) o[q] = f32x4{in.imm, in.imm, in.imm, in.imm};
+                    break;
                 case kEltStore:
-                    quad_store(p, in.a, in.c, i0, nv, y, false);
-                    wr = false;
-                    break;
                 case kEltAccum:
-                    quad_store(p, in.a, in.c, i0, nv, y, true);
+#pragma unroll
+                    for (int q = 0; q < Q; ++q)
+                        quad_store(p, in.a, in.c, i0[q], nv[q], y[q], in.op == kEltAccum);
                     wr = false;
                     break;
-                case kEltRound: o = quad_map(x, [&](float v) { return round_to(in.c, v); }); break;
-                case kEltAdd: o = x + y; break;
-                case kEltSub: o = x - y; break;
-                case kEltMul: o = x * y; break;
-                case kEltDiv: o = x / y; break;
-                case kEltNeg: o = -x; break;
-                case kEltRelu: o = quad_map(x, [](float v) { return act_fwd(kActRelu, v); }); break;
-                case kEltGelu: o = quad_map(x, [](float v) { return act_fwd(kActGelu, v); }); break;
-                case kEltElu:
-                    o = quad_map(x, [](float v) { return v >= 0.0f ? v : expf(v) - 1.0f; });
+                case kEltRound: unary([&](float v) { return round_to(in.c, v); }); break;
+                case kEltAdd:
+#pragma unroll
+                    for (int q = 0; q < Q; ++q) o[q] = x[q] + y[q];
                     break;
-                case kEltTanh: o = quad_map(x, [](float v) { return tanhf(v); }); break;
-                case kEltExp: o = quad_map(x, [](float v) { return expf(v); }); break;
-                case kEltLog: o = quad_map(x, [](float v) { return logf(v); }); break;
-                case kEltAbs: o = quad_map(x, [](float v) { return fabsf(v); }); break;
-                case kEltReluD: o = quad_map(x, [](float v) { return act_grad(kActRelu, v); }); break;
-                case kEltGeluD: o = quad_map(x, [](float v) { return act_grad(kActGelu, v); }); break;
-                case kEltEluD:
-                    o = quad_map(x, [](float v) { return v >= 0.0f ? 1.0f : expf(v); });
+                case kEltSub:
+#pragma unroll
+                    for (int q = 0; q < Q; ++q) o[q] = x[q] - y[q];
                     break;
+                case kEltMul:
+#pragma unroll
+                    for (int q = 0; q < Q; ++q) o[q] = x[q] * y[q];
+                    break;
+                case kEltDiv:
+#pragma unroll
+                    for (int q = 0; q < Q; ++q) o[q] = x[q] / y[q];
+                    break;
+                case kEltNeg:
+#pragma unroll
+                    for (int q = 0; q < Q; ++q) o[q] = -x[q];
+                    break;
+                case kEltRelu: unary([](float v) { return act_fwd(kActRelu, v); }); break;
+                case kEltGelu: unary([](float v) { return act_fwd(kActGelu, v); }); break;
+                case kEltElu: unary([](float v) { return v >= 0.0f ? v : expf(v) - 1.0f; }); break;
+                case kEltTanh: unary([](float v) { return tanhf(v); }); break;
+                case kEltExp: unary([](float v) { return expf(v); }); break;
+                case kEltLog: unary([](float v) { return logf(v); }); break;
+                case kEltAbs: unary([](float v) { return fabsf(v); }); break;
+                case kEltReluD: unary([](float v) { return act_grad(kActRelu, v); }); break;
+                case kEltGeluD: unary([](float v) { return act_grad(kActGelu, v); }); break;
+                case kEltEluD: unary([](float v) { return v >= 0.0f ? 1.0f : expf(v); }); break;
                 case kEltSign:
-                    o = quad_map(x, [](float v) { return v > 0.0f ? 1.0f : (v < 0.0f ? -1.0f : 0.0f); });
+                    unary([](float v) { return v > 0.0f ? 1.0f : (v < 0.0f ? -1.0f : 0.0f); });
                     break;
-                case kEltLabelEq: {
-                    f32x4 t{0.f, 0.f, 0.f, 0.f};
-                    for (int e = 0; e < nv; ++e) {
-                        const uint64_t row = (i0 + e) / p.cols, col = (i0 + e) % p.cols;
-                        t[e] = (p.labels[row] == (uint32_t)col) ? 1.0f : 0.0f;
+                case kEltLabelEq:
+#pragma unroll
+                    for (int q = 0; q < Q; ++q) {
+                        f32x4 t{0.f, 0.f, 0.f, 0.f};
+                        for (int e = 0; e < nv[q]; ++e) {
+                            const uint64_t row = (i0[q] + e) / p.cols, col = (i0[q] + e) % p.cols;
+                            t[e] = (p.labels[row] == (uint32_t)col) ? 1.0f : 0.0f;
+                        }
+                        o[q] = t;
                     }
-                    o = t;
                     break;
-                }
-                case kEltSelect: {
-                    const f32x4 z = get(in.c);
-                    f32x4 t;
+                case kEltSelect:
+                    for_quads<Q>([&](auto qc) {
+                        constexpr int q = decltype(qc)::value;
+                        const f32x4 z = get(qc, in.c);
+                        f32x4 t;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) t[e] = x[e] != 0.0f ? y[e] : z[e];
-                    o = t;
+                        for (int e = 0; e < 4; ++e) t[e] = x[q][e] != 0.0f ? y[q][e] : z[e];
+                        o[q] = t;
+                    });
                     break;
-                }
-                case kEltMax: {
-                    f32x4 t;
+                case kEltMax:
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) t[e] = fmaxf(x[e], y[e]);
-                    o = t;
+                    for (int q = 0; q < Q; ++q) {
+                        f32x4 t;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) t[e] = fmaxf(x[q][e], y[q][e]);
+                        o[q] = t;
+                    }
                     break;
-                }
                 default: wr = false; break;
             }
-            if (wr) {
-                r0[in.dst & 15] = o[0];
-                r1[in.dst & 15] = o[1];
-                r2[in.dst & 15] = o[2];
-                r3[in.dst & 15] = o[3];
-            }
+            if (wr) for_quads<Q>([&](auto qc) { set(qc, in.dst, o[decltype(qc)::value]); });
         }
     }
 }
@@ -258,7 +338,12 @@ int launch_eltwise(fg_ctx *ctx, const EltProgram &p0) {
     // fraction of the rate); the kernel's loop covers anything beyond.
     uint64_t blocks = ((p.n + 3) / 4 + kThreads - 1) / kThreads;
     if (blocks > (1u << 30)) blocks = 1u << 30;
-    eltwise_prog_kernel<<<(unsigned)blocks, kThreads, 0, ctx->stream>>>(p);
+#ifndef FG_ELT_QUADS  // quads per thread and pass (a knob for measurement builds)
+#define FG_ELT_QUADS 1
+#endif
+    constexpr int kQ = FG_ELT_QUADS;
+    blocks = (blocks + kQ - 1) / kQ;
+    eltwise_prog_kernel<kQ><<<(unsigned)blocks, kThreads, 0, ctx->stream>>>(p);
     FG_LAUNCH_CHECK("eltwise_prog_kernel");
     return FG_OK;
 }

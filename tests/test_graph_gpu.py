@@ -917,6 +917,43 @@ def test_unary_forward_backward(ctx, op):
     assert normwise_rel(ctx.download(st.grad_tensors[0]).reshape(R, C), exp) < 1e-5
 
 
+@pytest.mark.parametrize("R,C", [(37, 1024), (37, 1025), (3, 341)],
+                         ids=["whole-blocks", "blocks+partial", "one-partial-block"])
+def test_eltwise_program_whole_and_partial_blocks(ctx, R, C):
+    """tanh(x * y + z) and its gradients through elementwise programs at
+    sizes on either side of a workgroup's 256 quads (1024 elements): 37 x
+    1024 fills whole workgroups, 37 x 1025 adds a partial one with a partial
+    last quad, 3 x 341 (1023 elements) is one partial workgroup.  Forward and
+    every gradient against float64 numpy."""
+    G = api()
+    graph, meta = new_graph(G.MEAN_SQUARED_ERROR)
+    r, c = meta.new_field(), meta.new_field()
+    with graph.define_ops() as ops:
+        x = ops.input([r, c])
+        y = ops.input([r, c])
+        z = ops.input([r, c])
+        ops.tanh(ops.add(ops.mul(x, y), z))
+    mb = [G.f32_bits(1e-3), R, C]
+    st = ctx.alloc_tensors(graph, graph.compute_saved_nodes(), mb)
+    rng = np.random.default_rng(R * C)
+    X, Y, Z = (rng.standard_normal((R, C)).astype(f32) for _ in range(3))
+    ins = [ctx.init_tensor_f32([R, C], v) for v in (X, Y, Z)]
+    sch = ctx.schedule(graph.lower(meta), mb, ins, st)
+    seed = rng.standard_normal((R, C)).astype(f32)
+    ctx.upload(st.seed, seed)
+    ctx.dispatch_forward(sch)
+    ctx.dispatch_backward(sch)
+    ctx.sync()
+    x, yv, zv, s = (v.astype(np.float64) for v in (X, Y, Z, seed))
+    t = np.tanh(x * yv + zv)
+    assert normwise_rel(ctx.download(st.forward_out).reshape(R, C), t) < 1e-6
+    g = {tt.node: ctx.download(tt) for tt in st.grad_tensors}
+    du = s * (1 - t * t)
+    assert normwise_rel(g[0].reshape(R, C), du * yv) < 1e-5
+    assert normwise_rel(g[1].reshape(R, C), du * x) < 1e-5
+    assert normwise_rel(g[2].reshape(R, C), du) < 1e-5
+
+
 @pytest.mark.parametrize("C", [300, 301])
 def test_binary_broadcast_and_div_backward(ctx, C):
     """(a / b) * c - bias (row-broadcast sub): forward and every gradient
