@@ -273,6 +273,7 @@ def test_linear_bwd_parity(gpu_ctx, case, mat):
     # (M, N, K, act, accumulate)
     (2048, 4096, 4096, O.ACT_GELU, False),  # hidden layer: the 8-wave tiles' pair
     (2048, 4096, 1024, O.ACT_NONE, False),  # first layer: the 128x64 tiles' pair
+    (2048, 1000, 4096, O.ACT_GELU, False),  # 1000-wide head (dX's last K tile partial): two launches
     (64, 256, 784, O.ACT_RELU, True),       # c1's first layer: the small kernels' pair
     (100, 33, 17, O.ACT_GELU, True),        # unaligned rows: two launches
 ], ids=lambda c: f"{c[0]}x{c[1]}x{c[2]}-act{c[3]}{'-acc' if c[4] else ''}")
