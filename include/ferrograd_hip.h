@@ -74,7 +74,10 @@ int fg_ctx_target(fg_ctx *ctx, char *arch, size_t arch_len, uint32_t *flags,
 /* The hipStream_t work is enqueued on. */
 int fg_ctx_stream(fg_ctx *ctx, void **stream);
 /* Pre-size the context's scratch workspace so later direct-kernel calls
- * (and graph capture) never allocate. */
+ * (and graph capture) never allocate.  A GEMM of few output tiles and a long
+ * K splits K into this workspace when it already holds the slices (fp32 or
+ * fp32 sums of a 16-bit GEMM, M x N floats per slice); it is never grown for
+ * that, so a larger workspace can change which GEMMs split. */
 int fg_ctx_reserve_workspace(fg_ctx *ctx, uint64_t bytes);
 /* GpuBackend::sync / is_ready (rocm/mod.rs:398-400). */
 int fg_sync(fg_ctx *ctx);
