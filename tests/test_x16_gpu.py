@@ -141,15 +141,18 @@ def test_gemm_x16_exact_bits(gpu_ctx, dtype, layout, shape):
                                   (O.TN, 4096, 4096, 48), (O.NN, 2050, 4000, 96),
                                   (O.NT, 4096, 4000, 96), (O.TN, 4000, 4096, 96),
                                   (O.NN, 2050, 4000, 128), (O.NT, 4096, 4000, 192),
-                                  (O.TN, 4000, 4096, 128)],
+                                  (O.TN, 4000, 4096, 128), (O.NT, 2048, 1024, 1000),
+                                  (O.NT, 2050, 1030, 1000), (O.NT, 2048, 1024, 40)],
                          ids=["NN-4096x2048x64", "NT-4096x4096x64", "TN-4096x4096x48",
                               "NN-2050x4000x96", "NT-4096x4000x96", "TN-4000x4096x96",
-                              "NN-2050x4000x128", "NT-4096x4000x192", "TN-4000x4096x128"])
+                              "NN-2050x4000x128", "NT-4096x4000x192", "TN-4000x4096x128",
+                              "NT-2048x1024x1000", "NT-2050x1030x1000", "NT-2048x1024x40"])
 def test_gemm_x16_exact_bits_large_tiles(gpu_ctx, dtype, case):
     """Shapes large enough for the 256-wide tile configurations the
     dispatcher picks for full-chip GEMMs (8-wave 256x256 and 256x128 at
     BK 64, 256x256 at BK 32, 128x128), on the pipelined path (K a
-    multiple of 32 or 64; edge tiles in M and N) and off it (K = 48)."""
+    multiple of 32 or 64; edge tiles in M and N) and off it (K = 48, and
+    NT with K = 1000 or 40 on the 256x128 tiles of the any-shape kernel)."""
     layout, M, N, K = case
     note(f"gemm_x16 exact large {DT_IDS[dtype]} layout={layout} {M}x{N}x{K}")
     rng = np.random.default_rng(M + K + layout)
@@ -161,6 +164,24 @@ def test_gemm_x16_exact_bits_large_tiles(gpu_ctx, dtype, case):
     gpu_ctx.gemm_x16(dtype, layout, M, N, K, dev16(A), sa[1], dev16(B), sb[1], dC, N,
                      bias=dev16(bias), act=O.ACT_RELU)
     assert np.array_equal(host16(dC), refC)
+
+
+@pytest.mark.parametrize("dtype", [F16, BF16], ids=lambda d: DT_IDS[d])
+def test_gemm_bwd_x16_head_shape_exact_bits(gpu_ctx, dtype):
+    """The data gradient of a 1000-wide head, NT 2048x4096x1000 with the
+    ReLU derivative (K not a multiple of the tile depth), on operands whose
+    sums are exact in fp32: bit for bit on a sample of rows."""
+    M, N, K = 2048, 4096, 1000
+    note(f"gemm_bwd_x16 head shape {DT_IDS[dtype]}")
+    rng = np.random.default_rng(1000 + dtype)
+    A, B = quarter_ints(rng, (M, K), dtype), quarter_ints(rng, (N, K), dtype)
+    Zs = quarter_ints(rng, (M, N), dtype)
+    rows = np.sort(rng.choice(M, size=64, replace=False))
+    ref = O.gemm_bwd_x16(dtype, O.NT, A[rows], B, act=O.ACT_RELU, Zs=Zs[rows])
+    dC = empty16((M, N))
+    gpu_ctx.gemm_bwd_x16(dtype, O.NT, M, N, K, dev16(A), K, dev16(B), K, dC, N,
+                         act=O.ACT_RELU, Zs=dev16(Zs), ldzs=N)
+    assert np.array_equal(host16(dC)[rows], ref)
 
 
 @pytest.mark.parametrize("dtype", [F16, BF16], ids=lambda d: DT_IDS[d])
