@@ -629,6 +629,30 @@ def only_c5_step_bf16(ctx, reps):
     only_c5_step(ctx, reps, dtype="bf16")
 
 
+def only_gemm_bf16_c5_hidden(ctx, reps):
+    """The c5 step's hidden-layer GEMMs with bf16 tensors (for counter
+    passes): forward NN 2048x4096x4096 + bias + GELU with Z stored, dX NT
+    2048x4096x4096 * GELU'(Z), dW TN 4096x4096x2048 with the fused dbias;
+    N(0,1) operands."""
+    import torch
+
+    import ferrograd_amd as fa
+
+    M, N, K, bf = 2048, 4096, 4096, fa.DTYPE_BF16
+    g = torch.Generator(device="cuda").manual_seed(4)
+
+    def rnd(*shape):
+        return torch.randn(shape, device="cuda", generator=g).to(torch.bfloat16)
+
+    X, W, dZ, Zs, b = rnd(M, K), rnd(K, N), rnd(M, N), rnd(M, K), rnd(N)
+    H, Z, dX, dW, db = (torch.empty(sh, device="cuda", dtype=torch.bfloat16)
+                        for sh in ((M, N), (M, N), (M, K), (K, N), (N,)))
+    for _ in range(reps):
+        ctx.gemm_x16(bf, fa.NN, M, N, K, X, K, W, N, H, N, bias=b, act=fa.ACT_GELU, Z=Z, ldz=N)
+        ctx.gemm_bwd_x16(bf, fa.NT, M, K, N, dZ, N, W, N, dX, K, act=fa.ACT_GELU, Zs=Zs, ldzs=K)
+        ctx.gemm_dw_x16(bf, K, N, M, X, K, dZ, N, dW, N, colsum=db)
+
+
 def only_gemm_bf16_c2(ctx, reps):
     """The c2-shaped 4096^3 bf16 GEMMs: forward (bias + ReLU), dA, dB."""
     import torch
@@ -682,6 +706,7 @@ ONLY = {
     "c5_step": only_c5_step,
     "c5_step_bf16": only_c5_step_bf16,
     "gemm_bf16_c2": only_gemm_bf16_c2,
+    "gemm_bf16_c5_hidden": only_gemm_bf16_c5_hidden,
     "gemm_c2": only_gemm_c2,
     "gemm_c5_hidden": only_gemm_c5_hidden,
     "gemm_c5_fwd": only_c5_gemm("gemm_c5_fwd"),
