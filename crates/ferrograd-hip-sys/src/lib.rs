@@ -252,6 +252,28 @@ extern "C" {
         d_dbias: *mut f32,
         accumulate: c_int,
     ) -> c_int;
+    pub fn fg_matmul_bwd_x16(
+        ctx: *mut fg_ctx,
+        dtype: c_int,
+        M: c_int,
+        N: c_int,
+        K: c_int,
+        d_X: *const c_void,
+        ldx: c_int,
+        d_W: *const c_void,
+        ldw: c_int,
+        d_dZ: *const c_void,
+        lddz: c_int,
+        act: c_int,
+        d_Zs: *const c_void,
+        ldzs: c_int,
+        d_dX: *mut c_void,
+        lddx: c_int,
+        d_dW: *mut c_void,
+        lddw: c_int,
+        d_dbias: *mut c_void,
+        accumulate: c_int,
+    ) -> c_int;
     pub fn fg_linear_bwd_f32(
         ctx: *mut fg_ctx,
         act: c_int,

@@ -138,6 +138,14 @@ class Context:
              lddz, act, _ptr(Zs), ldzs, _ptr(dX), lddx, _ptr(dW), lddw, _ptr(dbias),
              int(accumulate))
 
+    def matmul_bwd_x16(self, dtype: int, M: int, N: int, K: int, X, ldx: int, W, ldw: int, dZ,
+                       lddz: int, dX, lddx: int, dW, lddw: int, dbias=None, act: int = ACT_NONE,
+                       Zs=None, ldzs: int = 0, accumulate: bool = False) -> None:
+        """matmul_bwd with 16-bit tensors (dtype DTYPE_F16 / DTYPE_BF16)."""
+        call("fg_matmul_bwd_x16", self.handle, dtype, M, N, K, _ptr(X), ldx, _ptr(W), ldw,
+             _ptr(dZ), lddz, act, _ptr(Zs), ldzs, _ptr(dX), lddx, _ptr(dW), lddw, _ptr(dbias),
+             int(accumulate))
+
     def gemm_dw_x16(self, dtype: int, M: int, N: int, K: int, A, lda: int, B, ldb: int, C,
                     ldc: int, accumulate: bool = False, colsum=None,
                     colsum_accumulate: bool = False) -> None:

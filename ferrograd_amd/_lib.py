@@ -52,6 +52,8 @@ SIGNATURES = {
                                 i32, vp, i32, vp, i32, vp, i32]),
     "fg_matmul_bwd_f32": (i32, [vp, i32, i32, i32, vp, i32, vp, i32, vp, i32, i32, vp, i32, vp,
                                 i32, vp, i32, vp, i32]),
+    "fg_matmul_bwd_x16": (i32, [vp, i32, i32, i32, i32, vp, i32, vp, i32, vp, i32, i32, vp, i32,
+                                vp, i32, vp, i32, vp, i32]),
     "fg_gemm_dw_x16": (i32, [vp, i32, i32, i32, i32, vp, i32, vp, i32, vp, i32, i32, vp, i32]),
     "fg_bias_grad": (i32, [vp, i32, i32, i32, vp, i32, vp, i32]),
     "fg_bias_grad_noalloc": (i32, [vp, i32, i32, i32, vp, i32, vp, i32]),

@@ -522,8 +522,40 @@ struct ColSum16 {
     }
 };
 
-template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC, bool BF>
-__global__ __launch_bounds__(64 * WGM * WGN) void gemm16_pipe(Args p) {
+// LDS of the pipelined kernel, in 16-bit elements: its stages (staged
+// loads -- global -> registers -> ds_write -- for every tile but 256x256
+// with 4 waves (256 accumulator registers) or with BK 64 (eight 16-byte
+// loads per wave and tile, which with the 128 accumulators of 8 waves exceed
+// the registers): two; direct-to-LDS loads: up to four, as many as fit in
+// the 160 KiB of LDS) or the epilogue's fp32 staging, whichever is larger.
+template <int BM, int BN, int BK, int WGM, int WGN>
+struct Pipe16Lds {
+    static constexpr int kNW = WGM * WGN;
+    static constexpr int kStageSz = BM * BK + BN * BK;  // elements
+    static constexpr bool kStaged = !(BM == 256 && BN == 256 && (kNW == 4 || BK == 64));
+    static constexpr int kStages = kStaged                             ? 2
+                                   : 4 * kStageSz * 2 <= 160 * 1024   ? 4
+                                   : 3 * kStageSz * 2 <= 160 * 1024 ? 3
+                                                                     : 2;
+    static constexpr int kEpiBytes = kNW * 32 * (BN / WGN + 4) * 4;
+    static constexpr int kBytes =
+        (kStages * kStageSz * 2 > kEpiBytes) ? kStages * kStageSz * 2 : kEpiBytes;
+    static constexpr int elems = kBytes / 2;
+};
+
+// The kernel's LDS buffer of N 16-bit elements: one static array per N, so
+// bodies that ask for the same N in one launch share it.
+template <int N>
+__device__ __forceinline__ uint16_t (&lds16_buffer())[N] {
+    __shared__ __attribute__((aligned(16))) uint16_t buf[N];
+    return buf;
+}
+
+// The pipelined 16-bit GEMM for output tile bx (and K slice by when split).
+// LDSN: the LDS buffer's size in elements, at least Pipe16Lds::elems (0:
+// just that) -- a launch running several bodies gives them all the largest.
+template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC, bool BF, int LDSN = 0>
+__device__ __forceinline__ void gemm16_pipe_body(Args p, int bx, int by) {
     using E = T16<BF>;
     constexpr int NW = WGM * WGN;
     constexpr int WTM = BM / WGM, WTN = BN / WGN;
@@ -535,29 +567,21 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm16_pipe(Args p) {
     static_assert(kInstA % NW == 0 && kInstB % NW == 0, "loads divide among the waves");
     constexpr int kPerA = kInstA / NW, kPerB = kInstB / NW, kLoads = kPerA + kPerB;
     constexpr int kASz = BM * BK, kBSz = BN * BK, kStageSz = kASz + kBSz;  // elements
-    // Staged loads (global -> registers -> ds_write) for every tile but
-    // 256x256 with 4 waves (256 accumulator registers) or with BK 64 (eight
-    // 16-byte loads per wave and tile, which with the 128 accumulators of 8
-    // waves exceed the registers): those load straight into LDS, with up to
-    // four stages, as many as fit in the 160 KiB of LDS.
-    constexpr bool kStaged = !(BM == 256 && BN == 256 && (NW == 4 || BK == 64));
-    constexpr int kStages = kStaged                             ? 2
-                            : 4 * kStageSz * 2 <= 160 * 1024   ? 4
-                            : 3 * kStageSz * 2 <= 160 * 1024 ? 3
-                                                              : 2;
-    constexpr int kEpiBytes = NW * 32 * (WTN + 4) * 4;
-    constexpr int kBytes = (kStages * kStageSz * 2 > kEpiBytes) ? kStages * kStageSz * 2 : kEpiBytes;
-    __shared__ __attribute__((aligned(16))) uint16_t lds[kBytes / 2];
+    using PL = Pipe16Lds<BM, BN, BK, WGM, WGN>;
+    constexpr bool kStaged = PL::kStaged;
+    constexpr int kStages = PL::kStages;
+    static_assert(LDSN == 0 || LDSN >= PL::elems, "LDS buffer too small");
+    uint16_t(&lds)[LDSN ? LDSN : PL::elems] = lds16_buffer<LDSN ? LDSN : PL::elems>();
 
-    if (p.ksplit > 0) {  // K slice blockIdx.y: offset operands, its own slot
-        const int kb = blockIdx.y * p.ksplit;
+    if (p.ksplit > 0) {  // K slice by: offset operands, its own slot
+        const int kb = by * p.ksplit;
         p.A += AK ? (size_t)kb : (size_t)kb * p.lda;
         p.B += BNC ? (size_t)kb * p.ldb : (size_t)kb;
         p.K = min(p.ksplit, p.K - kb);
-        p.partial += (size_t)blockIdx.y * p.M * p.N;
+        p.partial += (size_t)by * p.M * p.N;
     }
     int tile_m, tile_n;
-    tile_of(blockIdx.x, p.tiles_m, p.tiles_n, tile_m, tile_n);
+    tile_of(bx, p.tiles_m, p.tiles_n, tile_m, tile_n);
     const int m0 = tile_m * BM, n0 = tile_n * BN;
     // The wave index, as a uniform (scalar) value: it selects LDS destinations
     // and operands per wave, which the compiler would otherwise treat as
@@ -805,6 +829,39 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm16_pipe(Args p) {
                                       wave, lane);
 }
 
+template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC, bool BF>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm16_pipe(Args p) {
+    gemm16_pipe_body<BM, BN, BK, WGM, WGN, AK, BNC, BF>(p, blockIdx.x, blockIdx.y);
+}
+
+// A large layer's weight gradient (TN, 256x256 tiles, 8 waves, BK 32:
+// workgroups below n1) and data gradient (NT, 256x128 tiles, 8 waves, BK
+// 64: the rest) in one launch, each body exactly as its own kernel, both on
+// one LDS buffer of the larger size: the dW tiles' output writes drain while
+// dX tiles compute, where two launches would leave the CUs idle through them.
+constexpr int kPair16Lds = Pipe16Lds<256, 256, 32, 2, 4>::elems > Pipe16Lds<256, 128, 64, 4, 2>::elems
+                               ? Pipe16Lds<256, 256, 32, 2, 4>::elems
+                               : Pipe16Lds<256, 128, 64, 4, 2>::elems;
+template <bool BF>
+__global__ __launch_bounds__(512) void gemm16_pair_big(Args a1, Args a2, int n1) {
+    const int w = blockIdx.x;
+    if (w < n1)
+        gemm16_pipe_body<256, 256, 32, 2, 4, false, true, BF, kPair16Lds>(a1, w, 0);
+    else
+        gemm16_pipe_body<256, 128, 64, 4, 2, true, false, BF, kPair16Lds>(a2, w - n1, 0);
+}
+template <bool BF>
+void launch_pair16(Args a1, Args a2, hipStream_t st) {
+    a1.tiles_m = (a1.M + 255) / 256;
+    a1.tiles_n = (a1.N + 255) / 256;
+    a2.tiles_m = (a2.M + 255) / 256;
+    a2.tiles_n = (a2.N + 127) / 128;
+    const int n1 = a1.tiles_m * a1.tiles_n, n2 = a2.tiles_m * a2.tiles_n;
+    gemm16_pair_big<BF><<<n1 + n2, 512, 0, st>>>(a1, a2, n1);
+}
+// The pair's configurations (see launch_layout): dW on cfg 1, dX on cfg 8.
+constexpr int kPair16CfgW = 1, kPair16CfgX = 8;
+
 // The slots of a K-split GEMM summed in slot order (fp32), then the GEMM's
 // epilogue applied to each sum exactly as the kernel applies it to its own
 // (epi16_x4 on four columns, epi16 on the last few of a row).  One thread
@@ -916,6 +973,10 @@ void launch_layout(const Args &a, bool vec, bool pipe, int cfg, hipStream_t st) 
 // Defined in k_gemm16_{bf16,f16}.hip.  layout: FG_NN / FG_NT / FG_TN.
 void launch_bf16(int layout, const Args &a, bool vec, bool pipe, int cfg, hipStream_t st);
 void launch_f16(int layout, const Args &a, bool vec, bool pipe, int cfg, hipStream_t st);
+// gemm16_pair_big: dW (TN, a1) and dX (NT, a2), both planned pipelined on
+// kPair16CfgW / kPair16CfgX without a K split.
+void launch_pair_bf16(const Args &a1, const Args &a2, hipStream_t st);
+void launch_pair_f16(const Args &a1, const Args &a2, hipStream_t st);
 
 }  // namespace gemm16
 }  // namespace fg

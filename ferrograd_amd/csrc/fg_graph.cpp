@@ -967,7 +967,7 @@ int lower_backward(fg_plan &P, bool fused, std::vector<Launch> &out) {
                     L.desc = "backward gemm NT " + dims_str(M, K, N) + " -> grad of node " +
                              std::to_string(a);
                 }
-                if (idx_db != kNone && a != b && L.dtype == FG_DTYPE_F32) {
+                if (idx_db != kNone && a != b) {
                     out[idx_db].pair_next = true;
                     out[idx_db].desc += " [with the next]";
                 }
@@ -1208,6 +1208,17 @@ int run(fg_plan &P, const std::vector<Launch> &list, bool step = false, bool def
                 (const float *)P.ptr(X.sB), X.ldb, (const float *)P.ptr(X.sBias), X.act,
                 (float *)P.ptr(X.sC), X.ldc, (float *)P.ptr(X.sZ), X.ldz, X.accumulate,
                 want_ce ? &ce : nullptr, want_ce ? ce_done : nullptr);
+            if (rc != FG_OK) return rc;
+            skip = 1;
+            continue;
+        }
+        if (L.pair_next && i + 1 < list.size() && L.dtype != FG_DTYPE_F32) {
+            const Launch &X = list[i + 1];  // the same layer's dX (NT, act'), 16-bit
+            rc = fg::gemm16_dw_dx(ctx, L.dtype, L.M, L.N, L.K, P.ptr(L.sA), L.lda, P.ptr(L.sB),
+                                  L.ldb, P.ptr(L.sC), L.ldc, L.accumulate, P.ptr(L.sExtra),
+                                  L.accumulate2, X.M, X.N, X.K, P.ptr(X.sA), X.lda, P.ptr(X.sB),
+                                  X.ldb, X.act, P.ptr(X.sZ), X.ldz, P.ptr(X.sC), X.ldc,
+                                  X.accumulate);
             if (rc != FG_OK) return rc;
             skip = 1;
             continue;
@@ -2178,6 +2189,13 @@ FG_API int fg_plan_describe(const fg_plan *p, char *buf, size_t len, size_t *nee
             if (L.chain_next && i + 1 < v.size()) {
                 n += chain_dispatches(L, v[i + 1]);
                 ++i;
+            } else if (L.pair_next && i + 1 < v.size() && L.dtype != FG_DTYPE_F32) {
+                const Launch &X = v[i + 1];
+                n += wc ? fg::gemm16_dw_dx_dispatches(wc, L.M, L.N, L.K, p->ptr(L.sA), L.lda,
+                                                      p->ptr(L.sB), L.ldb, X.M, X.N, X.K,
+                                                      p->ptr(X.sA), X.lda, p->ptr(X.sB), X.ldb)
+                        : gemm_dispatches(L) + gemm_dispatches(X);
+                ++i;
             } else if (L.pair_next && i + 1 < v.size()) {
                 const Launch &X = v[i + 1];
                 n += wc ? fg::gemm_dw_dx_dispatches(wc, L.M, L.N, L.K, p->ptr(L.sA), L.lda,
@@ -2233,7 +2251,11 @@ FG_API int fg_plan_describe(const fg_plan *p, char *buf, size_t len, size_t *nee
         const Launch &X = bwd.back();
         const Launch *L = bwd.size() >= 2 && bwd[bwd.size() - 2].pair_next ? &bwd[bwd.size() - 2]
                                                                            : nullptr;
-        const Launch *H = gemm_dispatches(X) > 1 ? &X : L && gemm_dispatches(*L) > 1 ? L : nullptr;
+        // (fp32 summing passes only: a 16-bit split sums within its own call)
+        auto held = [&](const Launch *G) {
+            return G && G->dtype == FG_DTYPE_F32 && gemm_dispatches(*G) > 1;
+        };
+        const Launch *H = held(&X) ? &X : held(L) ? L : nullptr;
         if (H) {
             auto slot_range = [&](int slot) {
                 const uintptr_t b0 = (uintptr_t)p->ptr(slot);

@@ -121,6 +121,16 @@ uint64_t gemm16_split_ws_bytes(int cus, int layout, int M, int N, int K);
 // gradient of fg_gemm_dw_x16 is asked).
 int gemm16_dispatches(fg_ctx *ctx, int layout, int M, int N, int K, const void *A, int lda,
                       const void *B, int ldb, bool colsum);
+// A layer's dW (TN, fused column sums) and dX (NT, act') with 16-bit tensors,
+// in one launch when their kernels pair; its dispatches (no launch).
+int gemm16_dw_dx(fg_ctx *ctx, int dtype, int M1, int N1, int K1, const void *A1, int lda1,
+                 const void *B1, int ldb1, void *C1, int ldc1, int acc1, void *colsum,
+                 int colsum_acc, int M2, int N2, int K2, const void *A2, int lda2,
+                 const void *B2, int ldb2, int act, const void *Zs, int ldzs, void *C2, int ldc2,
+                 int acc2);
+int gemm16_dw_dx_dispatches(fg_ctx *ctx, int M1, int N1, int K1, const void *A1, int lda1,
+                            const void *B1, int ldb1, int M2, int N2, int K2, const void *A2,
+                            int lda2, const void *B2, int ldb2);
 
 // Adam with device-resident step counter / bias-correction scalars
 // (k_optim.hip).  d_state points at adam_dev_state_bytes() zeroed bytes.

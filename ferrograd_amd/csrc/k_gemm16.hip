@@ -112,6 +112,28 @@ Plan16 plan16(const fg_ctx *ctx, int layout, const Args &a) {
     return q;
 }
 
+// Argument checks of one call with M, N > 0 (nothing launched).
+int gemm16_check(fg_ctx *ctx, int dtype, int layout, const Args &a, const char *who) {
+    FG_REQUIRE(ctx, FG_ERR_INVALID_ARGUMENT, "%s: ctx is NULL", who);
+    FG_REQUIRE(dtype == FG_DTYPE_F16 || dtype == FG_DTYPE_BF16, FG_ERR_UNSUPPORTED,
+               "%s: dtype %d is not a 16-bit type (use fg_gemm_f32 for fp32)", who, dtype);
+    FG_REQUIRE(a.M > 0 && a.N > 0 && a.K >= 0, FG_ERR_SHAPE, "%s: empty or negative shape", who);
+    FG_REQUIRE(a.act >= 0 && a.act <= 2, FG_ERR_INVALID_ARGUMENT, "%s: bad act %d", who, a.act);
+    FG_REQUIRE(a.A && a.B && a.C, FG_ERR_INVALID_ARGUMENT, "%s: NULL operand", who);
+    const int a_cols = layout == FG_TN ? a.M : a.K;
+    const int b_cols = layout == FG_NT ? a.K : a.N;
+    FG_REQUIRE(a.lda >= std::max(a_cols, 1) && a.ldb >= std::max(b_cols, 1) && a.ldc >= a.N,
+               FG_ERR_SHAPE, "%s: leading dimension too small", who);
+    return FG_OK;
+}
+
+// 8-byte epilogue I/O where C / Z / bias allow it.
+void set_vec_out(Args &a) {
+    auto al = [](const void *q, unsigned m) { return (((uintptr_t)q) & (m - 1)) == 0; };
+    a.vec_out = al(a.C, 8) && a.ldc % 4 == 0 && (!a.Z || (al(a.Z, 8) && a.ldz % 4 == 0)) &&
+                (!a.bias || al(a.bias, 8));
+}
+
 int gemm16_common(fg_ctx *ctx, int dtype, int layout, Args &a, const char *who) {
     FG_REQUIRE(ctx, FG_ERR_INVALID_ARGUMENT, "%s: ctx is NULL", who);
     FG_REQUIRE(dtype == FG_DTYPE_F16 || dtype == FG_DTYPE_BF16, FG_ERR_UNSUPPORTED,
@@ -137,9 +159,7 @@ int gemm16_common(fg_ctx *ctx, int dtype, int layout, Args &a, const char *who) 
     FG_HIP(hipSetDevice(ctx->device));
     uint16_t *colsum = a.colsum;  // the bias gradient of fg_gemm_dw_x16, if any
     if (a.K == 0) a.A = a.B;  // loads are all masked; K=0 yields the epilogue of zero
-    auto al = [](const void *q, unsigned m) { return (((uintptr_t)q) & (m - 1)) == 0; };
-    a.vec_out = al(a.C, 8) && a.ldc % 4 == 0 && (!a.Z || (al(a.Z, 8) && a.ldz % 4 == 0)) &&
-                (!a.bias || al(a.bias, 8));
+    set_vec_out(a);
     const Plan16 q = plan16(ctx, layout, a);
     // Only the pipelined kernel sums B's columns; elsewhere the separate
     // reduction runs after the GEMM (same result up to the order of the
@@ -157,12 +177,104 @@ int gemm16_common(fg_ctx *ctx, int dtype, int layout, Args &a, const char *who) 
     return FG_OK;
 }
 
+// A layer's dW (TN, with the fused column sums) and dX (NT, act' of Zs)
+// arguments, as fg_gemm_dw_x16 and fg_gemm_bwd_x16 take them.
+Args dw_args16(int M, int N, int K, const void *A, int lda, const void *B, int ldb, void *C,
+               int ldc, int acc, void *colsum, int colsum_acc) {
+    Args a{};
+    a.A = static_cast<const uint16_t *>(A);
+    a.B = static_cast<const uint16_t *>(B);
+    a.C = static_cast<uint16_t *>(C);
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.lda = lda;
+    a.ldb = ldb;
+    a.ldc = ldc;
+    a.act = FG_ACT_NONE;
+    a.mode = 0;
+    a.accumulate = acc ? 1 : 0;
+    a.colsum = static_cast<uint16_t *>(colsum);
+    a.colsum_accumulate = colsum_acc ? 1 : 0;
+    return a;
+}
+Args dx_args16(int M, int N, int K, const void *A, int lda, const void *B, int ldb, int act,
+               const void *Zs, int ldzs, void *C, int ldc, int acc) {
+    Args a{};
+    a.A = static_cast<const uint16_t *>(A);
+    a.B = static_cast<const uint16_t *>(B);
+    a.C = static_cast<uint16_t *>(C);
+    a.Zs = static_cast<const uint16_t *>(Zs);
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.lda = lda;
+    a.ldb = ldb;
+    a.ldc = ldc;
+    a.ldzs = ldzs;
+    a.act = act;
+    a.mode = 1;
+    a.accumulate = acc ? 1 : 0;
+    return a;
+}
+// Both pipelined on the pair's configurations, neither split.
+bool pairable16(fg_ctx *ctx, Args &w, Args &x) {
+    if (w.M <= 0 || w.N <= 0 || w.K <= 0 || x.M <= 0 || x.N <= 0 || x.K <= 0) return false;
+    set_vec_out(w);
+    set_vec_out(x);
+    const Plan16 qw = plan16(ctx, FG_TN, w), qx = plan16(ctx, FG_NT, x);
+    return qw.pipe && qx.pipe && qw.splits == 1 && qx.splits == 1 &&
+           qw.cfg == fg::gemm16::kPair16CfgW && qx.cfg == fg::gemm16::kPair16CfgX;
+}
+
 }  // namespace
 
 namespace fg {
-// Workspace bytes a 16-bit GEMM of this shape splits K into when the
-// workspace holds them (0: it does not split), for planners that size a
-// workspace ahead.  Assumes the pipelined kernel (aligned operands).
+// A layer's two gradient GEMMs with 16-bit tensors: one launch
+// (gemm16_pair_big) when both take the large tiles' pipelined kernels
+// unsplit, else fg_gemm_dw_x16 then fg_gemm_bwd_x16.  Each part runs
+// exactly as its own call.
+int gemm16_dw_dx(fg_ctx *ctx, int dtype, int M1, int N1, int K1, const void *A1, int lda1,
+                 const void *B1, int ldb1, void *C1, int ldc1, int acc1, void *colsum,
+                 int colsum_acc, int M2, int N2, int K2, const void *A2, int lda2,
+                 const void *B2, int ldb2, int act, const void *Zs, int ldzs, void *C2, int ldc2,
+                 int acc2) {
+    Args w = dw_args16(M1, N1, K1, A1, lda1, B1, ldb1, C1, ldc1, acc1, colsum, colsum_acc);
+    Args x = dx_args16(M2, N2, K2, A2, lda2, B2, ldb2, act, Zs, ldzs, C2, ldc2, acc2);
+    const bool checked = M1 > 0 && N1 > 0 && M2 > 0 && N2 > 0 &&
+                         gemm16_check(ctx, dtype, FG_TN, w, "fg_gemm_dw_x16") == FG_OK &&
+                         gemm16_check(ctx, dtype, FG_NT, x, "fg_gemm_bwd_x16") == FG_OK &&
+                         (act == FG_ACT_NONE || (Zs && ldzs >= N2));
+    if (!checked || !pairable16(ctx, w, x)) {
+        fg::clear_error();  // the calls below report any error themselves
+        const int rc = fg_gemm_dw_x16(ctx, dtype, M1, N1, K1, A1, lda1, B1, ldb1, C1, ldc1, acc1,
+                                      colsum, colsum_acc);
+        if (rc) return rc;
+        return fg_gemm_bwd_x16(ctx, dtype, FG_NT, M2, N2, K2, A2, lda2, B2, ldb2, act, Zs, ldzs,
+                               C2, ldc2, acc2);
+    }
+    FG_HIP(hipSetDevice(ctx->device));
+    if (dtype == FG_DTYPE_BF16)
+        fg::gemm16::launch_pair_bf16(w, x, ctx->stream);
+    else
+        fg::gemm16::launch_pair_f16(w, x, ctx->stream);
+    FG_LAUNCH_CHECK("gemm16_dw_dx");
+    return FG_OK;
+}
+
+// Dispatches of gemm16_dw_dx for these operands (no launch).
+int gemm16_dw_dx_dispatches(fg_ctx *ctx, int M1, int N1, int K1, const void *A1, int lda1,
+                            const void *B1, int ldb1, int M2, int N2, int K2, const void *A2,
+                            int lda2, const void *B2, int ldb2) {
+    const int sep = gemm16_dispatches(ctx, FG_TN, M1, N1, K1, A1, lda1, B1, ldb1, true) +
+                    gemm16_dispatches(ctx, FG_NT, M2, N2, K2, A2, lda2, B2, ldb2, false);
+    if (!ctx) return sep;
+    void *c = reinterpret_cast<void *>(256);  // only the operands' alignment enters the choice
+    Args w = dw_args16(M1, N1, K1, A1, lda1, B1, ldb1, c, N1, 0, c, 0);
+    Args x = dx_args16(M2, N2, K2, A2, lda2, B2, ldb2, FG_ACT_NONE, nullptr, 0, c, N2, 0);
+    return pairable16(ctx, w, x) ? 1 : sep;
+}
+
 // Dispatches of one 16-bit GEMM call with these operands (no launch): the
 // GEMM, its summing kernel when it splits K, the column-sum reduction's two
 // when colsum is asked off the pipelined kernel.
@@ -183,6 +295,9 @@ int gemm16_dispatches(fg_ctx *ctx, int layout, int M, int N, int K, const void *
     return q.splits > 1 ? 2 : 1;
 }
 
+// Workspace bytes a 16-bit GEMM of this shape splits K into when the
+// workspace holds them (0: it does not split), for planners that size a
+// workspace ahead.  Assumes the pipelined kernel (aligned operands).
 uint64_t gemm16_split_ws_bytes(int cus, int layout, int M, int N, int K) {
     if (M <= 0 || N <= 0 || K <= 0) return 0;
     cus = cus > 0 ? cus : 256;
@@ -261,4 +376,25 @@ FG_API int fg_gemm_bwd_x16(fg_ctx *ctx, int dtype, int layout, int M, int N, int
     FG_REQUIRE(act == FG_ACT_NONE || (d_Zs && ldzs >= N), FG_ERR_INVALID_ARGUMENT,
                "fg_gemm_bwd_x16: act %d needs Zs with ldzs >= N", act);
     return gemm16_common(ctx, dtype, layout, a, "fg_gemm_bwd_x16");
+}
+
+FG_API int fg_matmul_bwd_x16(fg_ctx *ctx, int dtype, int M, int N, int K, const void *d_X,
+                             int ldx, const void *d_W, int ldw, const void *d_dZ, int lddz,
+                             int act, const void *d_Zs, int ldzs, void *d_dX, int lddx,
+                             void *d_dW, int lddw, void *d_dbias, int accumulate) {
+    const char *who = "fg_matmul_bwd_x16";
+    FG_REQUIRE(ctx, FG_ERR_INVALID_ARGUMENT, "%s: ctx is NULL", who);
+    FG_REQUIRE(act >= FG_ACT_NONE && act <= FG_ACT_GELU, FG_ERR_INVALID_ARGUMENT,
+               "%s: bad act %d", who, act);
+    FG_REQUIRE(M >= 0 && N >= 0 && K >= 0, FG_ERR_SHAPE, "%s: negative dimension", who);
+    FG_REQUIRE(d_X && d_W && d_dZ && d_dX && d_dW, FG_ERR_INVALID_ARGUMENT,
+               "%s: NULL operand or output", who);
+    FG_REQUIRE(ldx >= K && ldw >= N && lddz >= N && lddx >= K && lddw >= N,
+               FG_ERR_INVALID_ARGUMENT, "%s: a leading dimension is below its row length", who);
+    FG_REQUIRE(act == FG_ACT_NONE || (d_Zs && ldzs >= K), FG_ERR_INVALID_ARGUMENT,
+               "%s: act %d needs Zs with ldzs >= K", who, act);
+    // dW: TN K x N over M; dX: NT M x K over N.
+    return fg::gemm16_dw_dx(ctx, dtype, K, N, M, d_X, ldx, d_dZ, lddz, d_dW, lddw, accumulate,
+                            d_dbias, accumulate, M, K, N, d_dZ, lddz, d_W, ldw, act, d_Zs, ldzs,
+                            d_dX, lddx, accumulate);
 }

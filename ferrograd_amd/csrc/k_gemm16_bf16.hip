@@ -15,5 +15,9 @@ void launch_bf16(int layout, const Args &a, bool vec, bool pipe, int cfg, hipStr
     }
 }
 
+void launch_pair_bf16(const Args &a1, const Args &a2, hipStream_t st) {
+    launch_pair16<true>(a1, a2, st);
+}
+
 }  // namespace gemm16
 }  // namespace fg

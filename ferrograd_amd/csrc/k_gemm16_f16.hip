@@ -15,5 +15,9 @@ void launch_f16(int layout, const Args &a, bool vec, bool pipe, int cfg, hipStre
     }
 }
 
+void launch_pair_f16(const Args &a1, const Args &a2, hipStream_t st) {
+    launch_pair16<false>(a1, a2, st);
+}
+
 }  // namespace gemm16
 }  // namespace fg

@@ -231,6 +231,18 @@ int fg_gemm_dw_x16(fg_ctx *ctx, int dtype, int M, int N, int K, const void *d_A,
                    const void *d_B, int ldb, void *d_C, int ldc, int accumulate,
                    void *d_colsum, int colsum_accumulate);
 
+/* fg_matmul_bwd_f32 for 16-bit tensors (dtype FG_DTYPE_F16 / FG_DTYPE_BF16
+ * for every operand and output; leading dimensions in elements): dW and
+ * dbias as fg_gemm_dw_x16, dX as fg_gemm_bwd_x16 in the NT layout, one
+ * launch when both take the large layers' pipelined kernels unsplit (the
+ * same bits as the two calls), else the two calls in turn.  Replaces the
+ * 16-bit instances of the matmul backward (op/matmul/mod.rs:75-94). */
+int fg_matmul_bwd_x16(fg_ctx *ctx, int dtype, int M, int N, int K,
+                      const void *d_X, int ldx, const void *d_W, int ldw,
+                      const void *d_dZ, int lddz, int act, const void *d_Zs, int ldzs,
+                      void *d_dX, int lddx, void *d_dW, int lddw, void *d_dbias,
+                      int accumulate);
+
 /* dbias[j] (=|+=) sum_i dZ[i][j]: the bias-add's backward (new broadcast
  * op; reference binary.rs:53-63 has none). Deterministic order. */
 int fg_bias_grad_f32(fg_ctx *ctx, int M, int N, const float *d_dZ, int ld,

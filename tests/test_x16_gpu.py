@@ -341,6 +341,48 @@ def test_gemm_x16_split_k(dtype, case):
         plain.close()
 
 
+@pytest.mark.parametrize("dtype", [F16, BF16], ids=lambda d: DT_IDS[d])
+@pytest.mark.parametrize("case", [
+    (2048, 4096, 4096, O.ACT_GELU, False),  # hidden layer: one launch (gemm16_pair_big)
+    (2048, 4096, 1024, O.ACT_NONE, True),   # 1024-wide layer: two launches
+    (300, 260, 100, O.ACT_RELU, False),     # small, unaligned tiles: two launches
+], ids=lambda c: f"{c[0]}x{c[1]}x{c[2]}-act{c[3]}{'-acc' if c[4] else ''}")
+def test_matmul_bwd_x16_matches_separate_calls(dtype, case):
+    """fg_matmul_bwd_x16 (dW + dbias and dX with act', one launch where the
+    two kernels pair) against fg_gemm_dw_x16 and fg_gemm_bwd_x16 on one
+    context and workspace: every output equal bit for bit."""
+    torch = _torch()
+    import ferrograd_amd as fa
+    M, N, K, act, acc = case
+    note(f"matmul_bwd_x16 {DT_IDS[dtype]} {case}")
+    rng = np.random.default_rng(M + 3 * N + 7 * K)
+    X, W = normal16(rng, (M, K), dtype), normal16(rng, (K, N), dtype, 1.0 / np.sqrt(K))
+    dZ, Zs = normal16(rng, (M, N), dtype), normal16(rng, (M, K), dtype)
+    dX0, dW0, db0 = (normal16(rng, sh, dtype) for sh in ((M, K), (K, N), (N,)))
+    own = fa.Context(0, torch.cuda.current_stream().cuda_stream)
+    try:
+        own.reserve_workspace(1 << 20)
+        gX, gW, gdZ, gZs = dev16(X), dev16(W), dev16(dZ), dev16(Zs)
+        outs = []
+        for fused in (True, False):
+            gx, gw, gb = dev16(dX0), dev16(dW0), dev16(db0)
+            if fused:
+                own.matmul_bwd_x16(dtype, M, N, K, gX, K, gW, N, gdZ, N, gx, K, gw, N, dbias=gb,
+                                   act=act, Zs=gZs, ldzs=K, accumulate=acc)
+            else:
+                own.gemm_dw_x16(dtype, K, N, M, gX, K, gdZ, N, gw, N, accumulate=acc, colsum=gb,
+                                colsum_accumulate=acc)
+                own.gemm_bwd_x16(dtype, O.NT, M, K, N, gdZ, N, gW, N, gx, K, act=act, Zs=gZs,
+                                 ldzs=K, accumulate=acc)
+            own.sync()
+            outs.append([host16(gx), host16(gw), host16(gb)])
+        for a, b in zip(*outs):
+            assert np.array_equal(a, b)
+    finally:
+        own.sync()
+        own.close()
+
+
 def test_gemm_x16_rejects_fp32_dtype(gpu_ctx):
     import ferrograd_amd as fa
 
