@@ -70,6 +70,10 @@ struct Args {
     // and applies the epilogue.  ksplit 0: no split.
     float *partial;
     int ksplit;
+    // With colsum and a K split: slot s of N fp32 column sums of the slice,
+    // added in slot order, rounded and written (or accumulated) by
+    // sum_slices16.
+    float *colsum_partial;
 };
 
 // Element conversion and the MFMA of one storage type.
@@ -515,6 +519,10 @@ struct ColSum16 {
             float t = 0.0f;
 #pragma unroll
             for (int k = 0; k < G; ++k) t += lds[k * BN + col];
+            if (p.ksplit > 0) {  // a K slice: its fp32 sums, finished by sum_slices16
+                p.colsum_partial[n0 + col] = t;
+                continue;
+            }
             uint16_t *dst = p.colsum + n0 + col;
             *dst = T16<BF>::from_f(p.colsum_accumulate ? T16<BF>::to_f(*dst) + t : t);
         }
@@ -579,6 +587,7 @@ __device__ __forceinline__ void gemm16_pipe_body(Args p, int bx, int by) {
         p.B += BNC ? (size_t)kb * p.ldb : (size_t)kb;
         p.K = min(p.ksplit, p.K - kb);
         p.partial += (size_t)by * p.M * p.N;
+        if (p.colsum) p.colsum_partial += (size_t)by * p.N;
     }
     int tile_m, tile_n;
     tile_of(bx, p.tiles_m, p.tiles_n, tile_m, tile_n);
@@ -874,6 +883,16 @@ __global__ __launch_bounds__(256) void sum_slices16(Args p, int splits) {
     if (q >= (int64_t)p.M * g4) return;
     const int row = (int)(q / g4), col = (int)(q % g4) * 4;
     const size_t slot = (size_t)p.M * p.N;
+    if (row == 0 && p.colsum) {  // the column sums' slots, in slot order
+#pragma unroll 1
+        for (int t = 0; t < 4 && col + t < p.N; ++t) {
+            float v = p.colsum_partial[col + t];
+#pragma unroll 1
+            for (int s = 1; s < splits; ++s) v += p.colsum_partial[(size_t)s * p.N + col + t];
+            uint16_t *dst = p.colsum + col + t;
+            *dst = E::from_f(p.colsum_accumulate ? E::to_f(*dst) + v : v);
+        }
+    }
     const float *src = p.partial + (size_t)row * p.N + col;
     if (p.vec_out && p.N % 4 == 0) {
         f32x4 v = *reinterpret_cast<const f32x4 *>(src);

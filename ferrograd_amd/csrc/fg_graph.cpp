@@ -1719,10 +1719,11 @@ FG_API int fg_plan_create(fg_ctx *ctx, const fg_graph *g, const uint32_t *meta, 
                     ws = std::max<uint64_t>(ws, fg::bias_grad_ws_bytes(cus, L.M, L.N));
         for (auto *list : {&P->fwd, &P->bwd_seed, &P->bwd_fused})
             for (const Launch &L : *list)
-                if ((L.kind == LK_GEMM || L.kind == LK_GEMM_BWD) && L.dtype != FG_DTYPE_F32 &&
-                    L.sExtra == kNone)
-                    ws = std::max<uint64_t>(
-                        ws, fg::gemm16_split_ws_bytes(cus, L.layout, L.M, L.N, L.K));
+                if ((L.kind == LK_GEMM || L.kind == LK_GEMM_BWD) && L.dtype != FG_DTYPE_F32) {
+                    const bool cs = L.kind == LK_GEMM && L.sExtra != kNone;  // dW + dbias (TN)
+                    ws = std::max<uint64_t>(ws, fg::gemm16_split_ws_bytes(
+                                                    cus, cs ? FG_TN : L.layout, L.M, L.N, L.K, cs));
+                }
         P->ws_bytes = ws;
         P->ws_slot = P->new_slot(ws / 4);
     }

@@ -115,8 +115,8 @@ int noalloc_init(int device);
 // with `cus` compute units (the partial sums of its row splits).
 uint64_t bias_grad_ws_bytes(int cus, int M, int N);
 // Workspace bytes of the K slices a 16-bit GEMM of this shape takes when the
-// workspace holds them (0: no split).
-uint64_t gemm16_split_ws_bytes(int cus, int layout, int M, int N, int K);
+// workspace holds them (0: no split); colsum: with the fused column sums.
+uint64_t gemm16_split_ws_bytes(int cus, int layout, int M, int N, int K, bool colsum);
 // Dispatches of one 16-bit GEMM call (no launch; colsum: the fused bias
 // gradient of fg_gemm_dw_x16 is asked).
 int gemm16_dispatches(fg_ctx *ctx, int layout, int M, int N, int K, const void *A, int lda,

@@ -100,11 +100,13 @@ Plan16 plan16(const fg_ctx *ctx, int layout, const Args &a) {
     // Few tiles and a long K: K slices into the context's workspace when
     // what is reserved holds them (it is never grown for this), summed by a
     // second kernel in slot order -- deterministic, within the GEMM
-    // tolerance of the unsplit sum.  Never with the fused column sums.
-    if (q.pipe && !a.colsum && ctx->ws) {
+    // tolerance of the unsplit sum.  With the fused column sums each slice
+    // also leaves N fp32 sums, after the output slots.
+    if (q.pipe && ctx->ws) {
         int ks;
         const int sl = split16(cus, a.M, a.N, a.K, q.cfg, ks);
-        if (sl > 1 && (uint64_t)sl * a.M * a.N * sizeof(float) <= ctx->ws_bytes) {
+        const uint64_t need = (uint64_t)sl * ((uint64_t)a.M * a.N + (a.colsum ? a.N : 0));
+        if (sl > 1 && need * sizeof(float) <= ctx->ws_bytes) {
             q.splits = sl;
             q.ks = ks;
         }
@@ -167,6 +169,8 @@ int gemm16_common(fg_ctx *ctx, int dtype, int layout, Args &a, const char *who) 
     if (colsum && !q.pipe) a.colsum = nullptr;
     a.partial = q.splits > 1 ? static_cast<float *>(ctx->ws) : nullptr;
     a.ksplit = q.splits > 1 ? q.ks : 0;
+    a.colsum_partial =
+        q.splits > 1 && a.colsum ? a.partial + (size_t)q.splits * a.M * a.N : nullptr;
     if (dtype == FG_DTYPE_BF16)
         fg::gemm16::launch_bf16(layout, a, q.vec, q.pipe, q.cfg, ctx->stream);
     else
@@ -298,14 +302,14 @@ int gemm16_dispatches(fg_ctx *ctx, int layout, int M, int N, int K, const void *
 // Workspace bytes a 16-bit GEMM of this shape splits K into when the
 // workspace holds them (0: it does not split), for planners that size a
 // workspace ahead.  Assumes the pipelined kernel (aligned operands).
-uint64_t gemm16_split_ws_bytes(int cus, int layout, int M, int N, int K) {
+uint64_t gemm16_split_ws_bytes(int cus, int layout, int M, int N, int K, bool colsum) {
     if (M <= 0 || N <= 0 || K <= 0) return 0;
     cus = cus > 0 ? cus : 256;
     const int cfg = pick_cfg16(layout, M, N, K, cus);
     if (cfg == 3 || K % fg::gemm16::cfg_bk16(cfg) != 0) return 0;
     int ks;
     const int sl = split16(cus, M, N, K, cfg, ks);
-    return sl > 1 ? (uint64_t)sl * M * N * sizeof(float) : 0;
+    return sl > 1 ? (uint64_t)sl * ((uint64_t)M * N + (colsum ? N : 0)) * sizeof(float) : 0;
 }
 }  // namespace fg
 

@@ -383,6 +383,43 @@ def test_matmul_bwd_x16_matches_separate_calls(dtype, case):
         own.close()
 
 
+@pytest.mark.parametrize("dtype", [F16, BF16], ids=lambda d: DT_IDS[d])
+@pytest.mark.parametrize("acc", [False, True], ids=["write", "accumulate"])
+def test_gemm_dw_x16_split_k_with_column_sums(dtype, acc):
+    """The weight gradient of a 1000-wide head, TN 4096x1000x2048 with the
+    fused bias gradient: its 128 tiles split K in two when the workspace
+    holds the slots and the slices' column sums (each slice's first tile row
+    leaves N fp32 sums, added in slot order by the summing kernel).  On
+    operands whose sums are exact in fp32 both dW and dbias equal the oracle
+    bit for bit, split (64 MiB workspace) and unsplit (none), written and
+    accumulated."""
+    torch = _torch()
+    import ferrograd_amd as fa
+    M, N, K = 4096, 1000, 2048
+    note(f"gemm_dw_x16 split-K colsum {DT_IDS[dtype]} acc={acc}")
+    rng = np.random.default_rng(77 + dtype + acc)
+    A, B = quarter_ints(rng, (K, M), dtype), quarter_ints(rng, (K, N), dtype)
+    C0, b0 = quarter_ints(rng, (M, N), dtype), quarter_ints(rng, (N,), dtype)
+    rows = np.sort(rng.choice(M, size=64, replace=False))
+    refC = O.gemm_x16(dtype, O.TN, A[:, rows], B, C=C0[rows] if acc else None)
+    colsum = O.to_f32(dtype, B).astype(np.float64).sum(0)
+    refb = O.from_f32(dtype, (colsum + (O.to_f32(dtype, b0) if acc else 0)).astype(np.float32))
+    split = fa.Context(0, torch.cuda.current_stream().cuda_stream)
+    plain = fa.Context(0, torch.cuda.current_stream().cuda_stream)
+    try:
+        split.reserve_workspace(64 << 20)
+        for c in (split, plain):
+            dC, db = (dev16(C0), dev16(b0)) if acc else (empty16((M, N)), empty16((N,)))
+            c.gemm_dw_x16(dtype, M, N, K, dev16(A), M, dev16(B), N, dC, N, accumulate=acc,
+                          colsum=db, colsum_accumulate=acc)
+            c.sync()
+            assert np.array_equal(host16(dC)[rows], refC)
+            assert np.array_equal(host16(db), refb)
+    finally:
+        split.close()
+        plain.close()
+
+
 def test_gemm_x16_rejects_fp32_dtype(gpu_ctx):
     import ferrograd_amd as fa
 
