@@ -90,6 +90,19 @@ def test_host_rng_distributions():
     assert w.min() >= -0.5 and w.max() < 0.5
 
 
+@pytest.mark.parametrize("fn", ["fg_matmul_bwd_f32", "fg_matmul_bwd_x16"])
+def test_matmul_bwd_rejects_null_context(fn):
+    """A matmul node's gradient entry points check their context before
+    anything else: INVALID_ARGUMENT and a message, no device touched."""
+    args = [None, 64, 32, 16, None, 16, None, 32, None, 32, 0, None, 0, None, 16, None, 32,
+            None, 0]
+    if fn.endswith("x16"):
+        args.insert(1, 2)  # dtype bf16
+    with pytest.raises(fa.FgError) as e:
+        _lib.call(fn, *args)
+    assert e.value.code == 1 and "ctx is NULL" in str(e.value)
+
+
 def test_context_without_gpu_reports_no_device():
     torch = pytest.importorskip("torch")
     if torch.cuda.is_available():

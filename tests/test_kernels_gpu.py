@@ -327,6 +327,27 @@ def test_matmul_bwd_matches_separate_calls(case):
         own.close()
 
 
+def test_matmul_bwd_rejects_bad_arguments(gpu_ctx):
+    """fg_matmul_bwd_f32 / _x16 report a missing operand, a leading
+    dimension below its row length and an activation without Zs as
+    INVALID_ARGUMENT, launching nothing."""
+    import ferrograd_amd as fa
+    M, N, K = 64, 32, 16
+    X, W, dZ, dX, dW = (empty(s) for s in ((M, K), (K, N), (M, N), (M, K), (K, N)))
+    for kw, bad in ((dict(ldx=K - 1), "ld"), (dict(X=None), "null"), (dict(act=O.ACT_GELU), "zs")):
+        a = dict(X=X, ldx=K, W=W, ldw=N, dZ=dZ, lddz=N, dX=dX, lddx=K, dW=dW, lddw=N, act=0)
+        a.update(kw)
+        with pytest.raises(fa.FgError) as e:
+            gpu_ctx.matmul_bwd(M, N, K, a["X"], a["ldx"], a["W"], a["ldw"], a["dZ"], a["lddz"],
+                               a["dX"], a["lddx"], a["dW"], a["lddw"], act=a["act"])
+        assert e.value.code == 1, bad
+        with pytest.raises(fa.FgError) as e:
+            gpu_ctx.matmul_bwd_x16(fa.DTYPE_BF16, M, N, K, a["X"], a["ldx"], a["W"], a["ldw"],
+                                   a["dZ"], a["lddz"], a["dX"], a["lddx"], a["dW"], a["lddw"],
+                                   act=a["act"])
+        assert e.value.code == 1, bad
+
+
 @pytest.mark.parametrize("mat", [False, True], ids=["prologue", "dZ"])
 def test_linear_bwd_relu_mask_from_output(gpu_ctx, mat):
     """For ReLU the forward output C = max(Z, 0) gives the same mask as Z,
