@@ -3,7 +3,10 @@
 The first test re-hosts the reference's own 16-bit test
 (crates/ferrograd/tests/nonf32.rs:11-99) with its exact expectations; the
 second runs a two-layer MLP step (bias + ReLU, softmax-CE, SGD) in each
-16-bit type against the oracle's 16-bit operations composed the same way.
+16-bit type against the oracle's 16-bit operations composed the same way,
+small and at a size whose GEMMs split K; the third checks a bf16 step whose
+plan pairs a 4096-wide layer's gradient GEMMs in one launch against the
+same step from single calls, bit for bit.
 """
 import math
 
@@ -150,3 +153,80 @@ def test_mlp_step_16bit_matches_oracle(ctx, kind, size):
         got = ctx.download(t)
         got = got.view(np.uint16) if kind == "f16" else got
         assert np.array_equal(got.reshape(-1), O.from_f32(dt, w)), k
+
+
+def test_bf16_step_with_pair_and_split_matches_single_calls(ctx):
+    """bf16 MLP (batch 2048, 256 -> 4096 -> 4096 -> 16, GELU, CE): the plan
+    runs the 4096-wide layer's dW and dX as one launch (gemm16_pair_big) and
+    splits the first layer's dW with its column sums into its workspace; the
+    same step from single calls, on a context whose workspace takes the same
+    K splits, gives every gradient bit for bit."""
+    torch = pytest.importorskip("torch")
+    import ferrograd_amd as fa
+    G = api()
+    kind, dt, bf = "bf16", O.BF16, fa.DTYPE_BF16
+    dims, B = [256, 4096, 4096, 16], 2048
+    graph, meta = G.Graph(G.CROSS_ENTROPY, G.Optim.sgd().lower), G.Metadata.new()
+    fb = meta.new_field()
+    fd = [meta.new_field() for _ in dims]
+    with graph.define_ops() as ops:
+        h = ops.input([fb, fd[0]], kind, trainable=False)
+        for l in range(3):
+            W = ops.input([fd[l], fd[l + 1]], kind)
+            b = ops.input([fd[l + 1]], kind)
+            z = ops.bias_add(ops.matmul(h, W), b)
+            h = ops.gelu(z) if l < 2 else z
+        ops.softmax(h)
+    mb = [G.f32_bits(0.01), B] + dims
+    st = ctx.alloc_tensors(graph, graph.compute_saved_nodes(), mb)
+    X16 = O.from_f32(dt, fa.rng_uniform(0, 0, (B, dims[0])))
+    y = fa.rng_int(0, 1, (B,), dims[-1])
+    Ws = [O.from_f32(dt, fa.rng_uniform(0, 10 + l, (dims[l], dims[l + 1]),
+                                        -math.sqrt(6 / dims[l]), math.sqrt(6 / dims[l])))
+          for l in range(3)]
+    bs = [O.from_f32(dt, 0.05 * fa.rng_normal(0, 20 + l, (dims[l + 1],))) for l in range(3)]
+    ins = [ctx.init_tensor_bf16(X16.shape, X16)]
+    for W, b in zip(Ws, bs):
+        ins += [ctx.init_tensor_bf16(W.shape, W), ctx.init_tensor_bf16(b.shape, b)]
+    tgt = ctx.new_onehot_init(y)
+    sch = ctx.schedule(graph.lower(meta), mb, ins, st)
+    ctx.dispatch_forward(sch)
+    ctx.dispatch_loss(sch, tgt)
+    ctx.dispatch_backward(sch)
+    ctx.sync()
+    grads = {t.node: np.asarray(ctx.download(t)).view(np.uint16).reshape(-1)
+             for t in st.grad_tensors}
+    in_nodes = [i for i, nd in enumerate(graph.nodes) if nd.op == 0]
+    own = fa.Context(0, ctx.ctx.stream)
+    try:
+        own.reserve_workspace(64 << 20)
+        x, w1, b1, w2, b2, w3, b3 = ins
+
+        def buf(*shape):
+            return torch.zeros(shape, dtype=torch.int16, device="cuda")
+        d0, d1, d2, d3 = dims
+        Z1, H1, Z2, H2, L = buf(B, d1), buf(B, d1), buf(B, d2), buf(B, d2), buf(B, d3)
+        own.gemm_x16(bf, fa.NN, B, d1, d0, x, d0, w1, d1, H1, d1, bias=b1, act=fa.ACT_GELU,
+                     Z=Z1, ldz=d1)
+        own.gemm_x16(bf, fa.NN, B, d2, d1, H1, d1, w2, d2, H2, d2, bias=b2, act=fa.ACT_GELU,
+                     Z=Z2, ldz=d2)
+        own.gemm_x16(bf, fa.NN, B, d3, d2, H2, d2, w3, d3, L, d3, bias=b3)
+        dl = buf(B, d3)
+        own.softmax_ce(L, d3, tgt, B, d3, 1.0, dlogits=dl, ldd=d3, dtype=bf)
+        dW3, db3, dZ2 = buf(d2, d3), buf(d3), buf(B, d2)
+        own.gemm_dw_x16(bf, d2, d3, B, H2, d2, dl, d3, dW3, d3, colsum=db3)
+        own.gemm_bwd_x16(bf, fa.NT, B, d2, d3, dl, d3, w3, d3, dZ2, d2, act=fa.ACT_GELU,
+                         Zs=Z2, ldzs=d2)
+        dW2, db2, dZ1 = buf(d1, d2), buf(d2), buf(B, d1)
+        own.gemm_dw_x16(bf, d1, d2, B, H1, d1, dZ2, d2, dW2, d2, colsum=db2)
+        own.gemm_bwd_x16(bf, fa.NT, B, d1, d2, dZ2, d2, w2, d2, dZ1, d1, act=fa.ACT_GELU,
+                         Zs=Z1, ldzs=d1)
+        dW1, db1, dX = buf(d0, d1), buf(d1), buf(B, d0)
+        own.gemm_dw_x16(bf, d0, d1, B, x, d0, dZ1, d1, dW1, d1, colsum=db1)
+        own.gemm_bwd_x16(bf, fa.NT, B, d0, d1, dZ1, d1, w1, d1, dX, d0)
+        own.sync()
+        ref = [dX, dW1, db1, dW2, db2, dW3, db3]
+        for node, r in zip(in_nodes, ref):
+            assert np.array_equal(grads[node], r.cpu().numpy().view(np.uint16).reshape(-1)), node
+    finally:
+        own.close()
