@@ -4,7 +4,7 @@ The first test re-hosts the reference's own 16-bit test
 (crates/ferrograd/tests/nonf32.rs:11-99) with its exact expectations; the
 second runs a two-layer MLP step (bias + ReLU, softmax-CE, SGD) in each
 16-bit type against the oracle's 16-bit operations composed the same way,
-small and at a size whose GEMMs split K; the third checks a bf16 step whose
+small and at a size whose GEMMs split K; the third checks a 16-bit step whose
 plan pairs a 4096-wide layer's gradient GEMMs in one launch against the
 same step from single calls, bit for bit.
 """
@@ -155,8 +155,9 @@ def test_mlp_step_16bit_matches_oracle(ctx, kind, size):
         assert np.array_equal(got.reshape(-1), O.from_f32(dt, w)), k
 
 
-def test_bf16_step_with_pair_and_split_matches_single_calls(ctx):
-    """bf16 MLP (batch 2048, 256 -> 4096 -> 4096 -> 16, GELU, CE): the plan
+@pytest.mark.parametrize("kind", ["f16", "bf16"])
+def test_step_with_pair_and_split_matches_single_calls(ctx, kind):
+    """16-bit MLP (batch 2048, 256 -> 4096 -> 4096 -> 16, GELU, CE): the plan
     runs the 4096-wide layer's dW and dX as one launch (gemm16_pair_big) and
     splits the first layer's dW with its column sums into its workspace; the
     same step from single calls, on a context whose workspace takes the same
@@ -164,7 +165,7 @@ def test_bf16_step_with_pair_and_split_matches_single_calls(ctx):
     torch = pytest.importorskip("torch")
     import ferrograd_amd as fa
     G = api()
-    kind, dt, bf = "bf16", O.BF16, fa.DTYPE_BF16
+    dt, bf = (O.F16, fa.DTYPE_F16) if kind == "f16" else (O.BF16, fa.DTYPE_BF16)
     dims, B = [256, 4096, 4096, 16], 2048
     graph, meta = G.Graph(G.CROSS_ENTROPY, G.Optim.sgd().lower), G.Metadata.new()
     fb = meta.new_field()
@@ -185,9 +186,14 @@ def test_bf16_step_with_pair_and_split_matches_single_calls(ctx):
                                         -math.sqrt(6 / dims[l]), math.sqrt(6 / dims[l])))
           for l in range(3)]
     bs = [O.from_f32(dt, 0.05 * fa.rng_normal(0, 20 + l, (dims[l + 1],))) for l in range(3)]
-    ins = [ctx.init_tensor_bf16(X16.shape, X16)]
+    def dev(bits):
+        if kind == "f16":
+            return ctx.init_tensor_f16(bits.shape, bits.view(np.float16))
+        return ctx.init_tensor_bf16(bits.shape, bits)
+
+    ins = [dev(X16)]
     for W, b in zip(Ws, bs):
-        ins += [ctx.init_tensor_bf16(W.shape, W), ctx.init_tensor_bf16(b.shape, b)]
+        ins += [dev(W), dev(b)]
     tgt = ctx.new_onehot_init(y)
     sch = ctx.schedule(graph.lower(meta), mb, ins, st)
     ctx.dispatch_forward(sch)
