@@ -95,7 +95,7 @@ class MLPStep:
         fd = [meta.new_field() for _ in dims]
         L = len(dims) - 1
         with graph.define_ops() as ops:
-            h = ops.input([fb, fd[0]], dtype, trainable=False)
+            self.x_node = h = ops.input([fb, fd[0]], dtype, trainable=False)
             self.w_nodes, self.b_nodes = [], []
             for l in range(L):
                 W = ops.input([fd[l], fd[l + 1]], dtype)
@@ -131,6 +131,7 @@ class MLPStep:
         gmap = {t.node: t for t in self.st.grad_tensors}
         self.dW = [gmap[n] for n in self.w_nodes]
         self.db = [gmap[n] for n in self.b_nodes]
+        self.dX = gmap[self.x_node]
         self.describe = self.sch.plan.describe()
 
     def launches_per_step(self) -> int:
@@ -775,7 +776,7 @@ def rel_err(a, b) -> float:
 
 def oracle_mlp_grads(X, y, W, b, act):
     """Forward, softmax-CE and backward (dX of the data included) of an MLP
-    with the CPU restatement: (mean loss, dW list, db list)."""
+    with the CPU restatement: (mean loss, dW list, db list, dX)."""
     import oracle as O
 
     L = len(W)
@@ -793,7 +794,7 @@ def oracle_mlp_grads(X, y, W, b, act):
         db[l] = O.bias_grad(dZ)
         up = O.gemm(O.NT, dZ, W[l])
         dZ = O.act_bwd(act, up, Zs[l - 1]) if l > 0 else up
-    return mean, dW, db
+    return mean, dW, db, dZ
 
 
 def cpu_c1(sample, threads):
@@ -808,7 +809,7 @@ def cpu_c1(sample, threads):
     b = [np.zeros(w.shape[1], np.float32) for w in W]
 
     def step():
-        mean, dW, db = oracle_mlp_grads(X, y, W, b, O.ACT_RELU)
+        mean, dW, db, _ = oracle_mlp_grads(X, y, W, b, O.ACT_RELU)
         for p, g in zip(W + b, dW + db):
             O.sgd_(p.copy().reshape(-1), g.copy().reshape(-1), np.float32(0.01), True)
         return mean, dW, db
@@ -837,32 +838,36 @@ def cpu_c1(sample, threads):
 
 def cpu_c2(sample, threads):
     """c2 on the CPU: forward ReLU(A.B + bias) and the masked backward (dA,
-    dB, dbias), timed once each on `threads` threads (412 GFLOP).  The CPU
-    backward takes the GPU forward's mask ([C_gpu > 0]; a sign that fp32
-    rounding decides differently would otherwise flip single terms), and the
-    flipped signs are counted."""
+    dB, dbias) on `threads` threads (412 GFLOP), each timed as the median of
+    5 runs after a warm-up run.  The CPU backward takes the GPU forward's
+    mask ([C_gpu > 0]; a sign that fp32 rounding decides differently would
+    otherwise flip single terms), and the flipped signs are counted."""
     import numpy as np
 
     import oracle as O
 
     O.set_num_threads(threads)
     A, B, bias, dC = sample["A"], sample["B"], sample["bias"], sample["dC"]
-    t0 = time.perf_counter()
-    _, C = O.bias_act(O.gemm(O.NN, A, B), bias, O.ACT_RELU)
-    t_f = time.perf_counter() - t0
     Cg = sample["C"]
-    t0 = time.perf_counter()
-    dZ = O.act_bwd(O.ACT_RELU, dC, Cg)
-    dA = O.gemm(O.NT, dZ, B)
-    dB = O.gemm(O.TN, A, dZ)
-    db = O.bias_grad(dZ)
-    t_b = time.perf_counter() - t0
+    out = {}
+
+    def fwd():
+        out["C"] = O.bias_act(O.gemm(O.NN, A, B), bias, O.ACT_RELU)[1]
+
+    def bwd():
+        dZ = O.act_bwd(O.ACT_RELU, dC, Cg)
+        out["dA"], out["dB"], out["db"] = O.gemm(O.NT, dZ, B), O.gemm(O.TN, A, dZ), O.bias_grad(dZ)
+
+    t_f = cpu_time_s(fwd, 5)
+    t_b = cpu_time_s(bwd, 5)
+    C, dA, dB, db = out["C"], out["dA"], out["dB"], out["db"]
     flops = 3 * 2.0 * A.shape[0] * A.shape[1] * B.shape[1]
     tol = 1e-5 * math.sqrt(A.shape[1])
     err = {"C": rel_err(Cg, C), "dA": rel_err(sample["dA"], dA), "dB": rel_err(sample["dB"], dB),
            "dbias": rel_err(sample["db"], db)}
     return {"cpu_ms": 1e3 * (t_f + t_b), "cpu_fwd_ms": 1e3 * t_f, "cpu_bwd_ms": 1e3 * t_b,
             "cpu_tflops": flops / (t_f + t_b) / 1e12, "cores": threads, "kind": "port",
+            "timing": "median of 5 after a warm-up run, forward and backward each",
             "mask_sign_flips": int(np.count_nonzero((Cg > 0) != (C > 0))),
             "max_rel_err": err, "tolerance": tol,
             "parity_ok": bool(max(err.values()) < tol)}
@@ -944,7 +949,8 @@ def adam_sample_run(ctx, nt: int = 8, steps: int = 10, threads: int = 1):
 def cpu_c5(host, first, dims, threads):
     """c5 on the CPU: one full training step (forward, CE, backward incl. dX,
     Adam) on the same initial inputs; parity of the GPU's first step (loss,
-    every dW / db) and Adam bit-exact on the GPU's own gradients."""
+    every dW / db, the data input's dX) and Adam bit-exact on the GPU's own
+    gradients."""
     import numpy as np
 
     import oracle as O
@@ -955,7 +961,7 @@ def cpu_c5(host, first, dims, threads):
     b = [np.zeros(dims[l + 1], np.float32) for l in range(L)]
     s, r = O.adam_scalars(np.float32(1e-3), np.float32(0.9), np.float32(0.999), 1)
     t0 = time.perf_counter()
-    mean, dW, db = oracle_mlp_grads(X, y, W, b, O.ACT_GELU)
+    mean, dW, db, dX = oracle_mlp_grads(X, y, W, b, O.ACT_GELU)
     for p0, g in zip(W + b, dW + db):
         p = p0.copy()
         O.adam_(p, g, np.zeros_like(p), np.zeros_like(p), np.float32(0.9), np.float32(0.999),
@@ -972,10 +978,12 @@ def cpu_c5(host, first, dims, threads):
     tol = 1e-5 * math.sqrt(4096)
     err = {"loss": abs(first["mean_loss"] - mean) / max(1.0, abs(mean)),
            "dW": max(rel_err(a, r_) for a, r_ in zip(first["dW"], dW)),
-           "db": max(rel_err(a, r_) for a, r_ in zip(first["db"], db))}
+           "db": max(rel_err(a, r_) for a, r_ in zip(first["db"], db)),
+           "dX": rel_err(first["dX"], dX)}
     return dt, {"max_rel_err": err, "tolerance_gemm": tol, "adam_bit_exact_on_gpu_grads":
                 adam_exact, "parity_ok": bool(err["loss"] < 1e-5 and err["dW"] < tol and
-                                              err["db"] < tol and adam_exact)}
+                                              err["db"] < tol and err["dX"] < tol and
+                                              adam_exact)}
 
 
 def main() -> int:
@@ -1024,6 +1032,7 @@ def main() -> int:
     first = {"mean_loss": tr.mean_loss(),
              "dW": [tr.download(t).reshape(w.shape) for t, w in zip(tr.dW, tr.W)],
              "db": [tr.download(t) for t in tr.db], "W": [w.cpu().numpy() for w in tr.W],
+             "dX": tr.download(tr.dX).reshape(tuple(tr.X.shape)),
              "b": [b.cpu().numpy() for b in tr.b]}
     for _ in range(max(0, args.warmup - 1)):
         tr.step_eager()

@@ -45,8 +45,12 @@ void *workspace(fg_ctx *ctx, uint64_t bytes) {
                   (unsigned long long)bytes, (unsigned long long)ctx->ws_bytes);
         return nullptr;
     }
-    // Round up to 1 MiB so repeated small growth does not thrash.
+    // Grow geometrically (at least double, rounded up to 1 MiB): every
+    // replaced buffer is kept until the context is destroyed (below), so
+    // the kept buffers total at most about twice the final size however the
+    // requests creep upward.
     uint64_t want = (bytes + (1u << 20) - 1) & ~uint64_t((1u << 20) - 1);
+    if (want < 2 * ctx->ws_bytes) want = 2 * ctx->ws_bytes;
     void *p = nullptr;
     hipError_t e = hipMalloc(&p, want);
     if (e != hipSuccess) {

@@ -16,6 +16,7 @@
 // every partial sum the second pass reads.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "fg_bias_grad.h"
@@ -30,7 +31,10 @@ constexpr uint64_t kScratchFloats = uint64_t(1) << 20;
 __device__ __align__(256) float scratch[kScratchFloats];
 
 constexpr int kMaxDevices = 64;
-float *g_scratch_ptr[kMaxDevices];  // device address of `scratch`, per device
+// Device address of `scratch`, per device.  Written once under the mutex by
+// noalloc_init; read without it by fg_bias_grad_noalloc on any host thread,
+// so each entry is atomic (release store, acquire load).
+std::atomic<float *> g_scratch_ptr[kMaxDevices];
 std::mutex g_scratch_mu;
 
 }  // namespace
@@ -44,13 +48,13 @@ int noalloc_init(int device) {
     FG_REQUIRE(device >= 0 && device < kMaxDevices, FG_ERR_UNSUPPORTED,
                "noalloc_init: device %d beyond the %d devices this library tracks", device,
                kMaxDevices);
-    if (g_scratch_ptr[device]) return FG_OK;
+    if (g_scratch_ptr[device].load(std::memory_order_acquire)) return FG_OK;
     void *ptr = nullptr;
     const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
     if (e != hipSuccess)
         return hip_fail(e, "hipGetSymbolAddress(scratch)", __FILE__, __LINE__);
     FG_REQUIRE(ptr, FG_ERR_INTERNAL, "noalloc_init: no device address for scratch");
-    g_scratch_ptr[device] = static_cast<float *>(ptr);
+    g_scratch_ptr[device].store(static_cast<float *>(ptr), std::memory_order_release);
     return FG_OK;
 }
 
@@ -73,10 +77,11 @@ FG_API int fg_bias_grad_noalloc(fg_ctx *ctx, int dtype, int M, int N, const void
                N, (unsigned long long)(sp.partial_floats(N) * sizeof(float)),
                (unsigned long long)(kScratchFloats * sizeof(float)),
                (unsigned long long)kScratchFloats);
-    FG_REQUIRE(ctx->device >= 0 && ctx->device < kMaxDevices && g_scratch_ptr[ctx->device],
-               FG_ERR_INTERNAL, "fg_bias_grad_noalloc: scratch of device %d not set up",
+    FG_REQUIRE(ctx->device >= 0 && ctx->device < kMaxDevices, FG_ERR_INTERNAL,
+               "fg_bias_grad_noalloc: device %d beyond the tracked devices", ctx->device);
+    float *partial = g_scratch_ptr[ctx->device].load(std::memory_order_acquire);
+    FG_REQUIRE(partial, FG_ERR_INTERNAL, "fg_bias_grad_noalloc: scratch of device %d not set up",
                ctx->device);
-    float *partial = g_scratch_ptr[ctx->device];
     FG_HIP(hipSetDevice(ctx->device));
     FG_HIP(fg::colsum::launch(ctx->stream, sp, dtype, M, N, d_dZ, ld, d_dbias, accumulate,
                               partial));

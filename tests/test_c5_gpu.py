@@ -5,10 +5,20 @@ optimiser through the C ABI, against the CPU oracle on the same inputs.
 
 Inputs follow the configuration (generator seed 4): X ~ N(0,1), labels
 U{0..999}, Kaiming-uniform weights U(-sqrt(6/fan_in), +sqrt(6/fan_in)),
-zero biases.  Checks: mean loss within 1e-5; every dW and db within
-1e-5*sqrt(4096) normwise; the Adam update bit for bit against the oracle's
+zero biases.  Checks: mean loss within 1e-5; every dW and db, and the data
+input's gradient dX (ferrograd gives every Input a gradient,
+crates/fused_gpu/src/dispatch/backend/kernel/backward.rs:93-106), within
+1e-5*sqrt(K) normwise; the Adam update bit for bit against the oracle's
 Adam applied to the GPU's own gradients (so any difference would be the
-update itself, not the gradient feeding it)."""
+update itself, not the gradient feeding it).
+
+The second test pins the path that bench.py times: the whole step captured
+as one hipGraph (fg_plan_capture_step) runs other kernels than eager steps
+do (the final softmax elided into the loss, the Adam step counter advanced
+on the device), so two steps of a captured plan are compared bit for bit with
+two eager steps of an identical plan: every parameter, every gradient
+(dX of the data input included), Adam m and v, the mean loss, the per-row
+losses and the probabilities."""
 import math
 
 import numpy as np
@@ -20,22 +30,23 @@ from conftest import normwise_rel
 pytestmark = pytest.mark.gpu
 
 f32 = np.float32
+DIMS, BATCH = [1024] + [4096] * 7 + [1000], 2048
 
 
-def test_c5_full_size_step_matches_oracle(gpu_ctx):
+def build_c5(gpu_ctx):
+    """The c5 graph, its plan and its bound inputs (host copies kept)."""
     import ferrograd_amd as fa
     from ferrograd_amd import graph as G
 
-    dims, B = [1024] + [4096] * 7 + [1000], 2048
+    dims, B = DIMS, BATCH
     L = len(dims) - 1
-    print(f"c5 full size: dims {dims}, batch {B}", flush=True)
     ctx = G.GpuContext(gpu_ctx)
     graph, meta = G.Graph(G.CROSS_ENTROPY, G.Optim.adam().lower), G.Metadata.new()
     fb = meta.new_field()
     fd = [meta.new_field() for _ in dims]
     w_nodes, b_nodes = [], []
     with graph.define_ops() as ops:
-        h = ops.input([fb, fd[0]], trainable=False)
+        x_node = h = ops.input([fb, fd[0]], trainable=False)
         for l in range(L):
             W = ops.input([fd[l], fd[l + 1]])
             b = ops.input([fd[l + 1]])
@@ -56,13 +67,31 @@ def test_c5_full_size_step_matches_oracle(gpu_ctx):
         ins += [ctx.init_tensor_f32(W.shape, W), ctx.init_tensor_f32(b.shape, b)]
     tgt = ctx.new_onehot_init(y)
     sch = ctx.schedule(graph.lower(meta), mb, ins, st)
+    return dict(ctx=ctx, st=st, sch=sch, ins=ins, tgt=tgt, X=X, y=y, Ws=Ws, bs=bs,
+                x_node=x_node, w_nodes=w_nodes, b_nodes=b_nodes)
+
+
+def free_c5(c):
+    c["st"].plan.close()
+    for t in c["ins"] + [c["tgt"]]:
+        t.free()
+
+
+def test_c5_full_size_step_matches_oracle(gpu_ctx):
+    L = len(DIMS) - 1
+    print(f"c5 full size: dims {DIMS}, batch {BATCH}", flush=True)
+    c = build_c5(gpu_ctx)
+    ctx, st, sch, ins = c["ctx"], c["st"], c["sch"], c["ins"]
+    X, y, Ws, bs = c["X"], c["y"], c["Ws"], c["bs"]
     ctx.dispatch_forward(sch)
-    ctx.dispatch_loss(sch, tgt)
+    ctx.dispatch_loss(sch, c["tgt"])
     ctx.dispatch_backward(sch)
     ctx.sync()
     gmap = {t.node: t for t in st.grad_tensors}
-    dW_gpu = [ctx.download(gmap[n]).reshape(W.shape) for n, W in zip(w_nodes, Ws)]
-    db_gpu = [ctx.download(gmap[n]) for n in b_nodes]
+    assert c["x_node"] in gmap, "the data input has no gradient tensor"
+    dX_gpu = ctx.download(gmap[c["x_node"]]).reshape(X.shape)
+    dW_gpu = [ctx.download(gmap[n]).reshape(W.shape) for n, W in zip(c["w_nodes"], Ws)]
+    db_gpu = [ctx.download(gmap[n]) for n in c["b_nodes"]]
     loss_gpu = float(ctx.download(st.mean_loss)[0])
     ctx.dispatch_optim(sch)
     ctx.sync()
@@ -84,8 +113,14 @@ def test_c5_full_size_step_matches_oracle(gpu_ctx):
         e_b = normwise_rel(db_gpu[l], O.bias_grad(dZ))
         print(f"layer {l}: dW {e_w:.2e} db {e_b:.2e}", flush=True)
         assert e_w < tol and e_b < tol, (l, e_w, e_b)
+        up = O.gemm(O.NT, dZ, Ws[l])
         if l > 0:
-            dZ = O.act_bwd(O.ACT_GELU, O.gemm(O.NT, dZ, Ws[l]), Zs[l - 1])
+            dZ = O.act_bwd(O.ACT_GELU, up, Zs[l - 1])
+        else:
+            # dX = dZ1 . W0^T: K = 4096 (the width of layer 0's output).
+            e_x = normwise_rel(dX_gpu, up)
+            print(f"data input: dX {e_x:.2e}", flush=True)
+            assert e_x < 1e-5 * math.sqrt(DIMS[1]), e_x
 
     # Adam step 1 on the GPU's own gradients: bit for bit.
     s, r = O.adam_scalars(f32(1e-3), f32(0.9), f32(0.999), 1)
@@ -95,4 +130,59 @@ def test_c5_full_size_step_matches_oracle(gpu_ctx):
         O.adam_(p, np.ascontiguousarray(g, f32).reshape(p.shape).copy(), np.zeros_like(p),
                 np.zeros_like(p), f32(0.9), f32(0.999), f32(1e-8), s, r)
         assert np.array_equal(ctx.download(ins[k + 1]).reshape(p.shape), p), k
-    st.plan.close()
+    # The data input is frozen: the optimiser leaves it as it was.
+    assert np.array_equal(ctx.download(ins[0]).reshape(X.shape), X)
+    free_c5(c)
+
+
+def test_c5_captured_step_matches_eager_bit_for_bit(gpu_ctx):
+    """Two c5 plans from identical inputs: one runs two eager steps (forward,
+    loss, backward, optimiser as separate calls), the other captures the
+    whole step once and replays it twice.  After each step every parameter,
+    gradient (dX included), Adam m and v, the mean loss, the per-row losses
+    and the probabilities agree bit for bit."""
+    from ferrograd_amd._lib import call
+
+    snaps = []
+    for captured in (False, True):
+        print(f"c5 {'captured' if captured else 'eager'} plan", flush=True)
+        c = build_c5(gpu_ctx)
+        ctx, st, sch = c["ctx"], c["st"], c["sch"]
+        if captured:
+            call("fg_plan_bind_target", sch.plan.handle, c["tgt"].data_ptr(), c["tgt"].nbytes)
+            call("fg_plan_capture_step", sch.plan.handle)
+        steps = []
+        for step in range(2):
+            if captured:
+                call("fg_plan_launch_step", sch.plan.handle)
+            else:
+                ctx.dispatch_forward(sch)
+                ctx.dispatch_loss(sch, c["tgt"])
+                ctx.dispatch_backward(sch)
+                ctx.dispatch_optim(sch)
+            ctx.sync()
+            snap = {"params": [ctx.download(t).copy() for t in c["ins"]],
+                    "grads": {t.node: ctx.download(t).copy() for t in st.grad_tensors},
+                    "state": [ctx.download(t).copy() for t in st.state],
+                    "mean": ctx.download(st.mean_loss).copy(),
+                    "row_loss": ctx.download(st.loss_t).copy(),
+                    "probs": ctx.download(st.forward_out).copy()}
+            print(f"  step {step + 1}: mean loss {float(snap['mean'][0]):.6f}", flush=True)
+            steps.append(snap)
+        snaps.append((steps, c["x_node"], len(st.state)))
+        free_c5(c)
+    (eager, x_node, n_state), (capt, _, _) = snaps
+    assert n_state == 2 * 2 * (len(DIMS) - 1)  # m and v for every W and b
+    for step, (e, g) in enumerate(zip(eager, capt)):
+        assert np.array_equal(e["mean"], g["mean"]), step
+        assert np.array_equal(e["row_loss"], g["row_loss"]), step
+        assert np.array_equal(e["probs"], g["probs"]), step
+        for k, (a, b) in enumerate(zip(e["params"], g["params"])):
+            assert np.array_equal(a, b), (step, "param", k)
+        assert e["grads"].keys() == g["grads"].keys() and x_node in e["grads"]
+        for node in e["grads"]:
+            assert np.array_equal(e["grads"][node], g["grads"][node]), (step, "grad", node)
+        for k, (a, b) in enumerate(zip(e["state"], g["state"])):
+            assert np.array_equal(a, b), (step, "adam state", k)
+    # The two steps did move the parameters (the comparison is not vacuous).
+    assert not np.array_equal(eager[0]["params"][1], eager[1]["params"][1])

@@ -62,3 +62,45 @@ def test_noalloc_bias_grad_rejects_too_many_columns(gpu_ctx):
         _call("fg_bias_grad_noalloc", gpu_ctx.handle, 0, 64, N, 256, N, 256, 0)
     assert e.value.code == 9  # FG_ERR_OUT_OF_BOUNDS
     assert "scratch" in str(e.value)
+
+
+def test_noalloc_bias_grad_under_graph_capture_on_fresh_context(gpu_ctx):
+    """The case the entry point is for: a context that has never allocated a
+    workspace calls fg_bias_grad_noalloc inside a hipGraph capture (global
+    capture mode, so any allocation or synchronising call in the capture
+    fails it).  The graph is replayed twice, with eager work and a
+    synchronisation between the replays, and each result is compared bit for
+    bit with fg_bias_grad run afterwards (which then grows the workspace)."""
+    import torch
+
+    import ferrograd_amd as fa
+
+    M, N = 2048, 4096
+    rng = np.random.default_rng(23)
+    dZ = torch.from_numpy(rng.standard_normal((M, N)).astype(f32)).cuda()
+    db = torch.empty(N, device="cuda")
+    s = torch.cuda.Stream()
+    fresh = fa.Context(0, s.cuda_stream)
+    try:
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        print("noalloc under capture: capturing", flush=True)
+        with torch.cuda.graph(g, stream=s, capture_error_mode="global"):
+            _call("fg_bias_grad_noalloc", fresh.handle, 0, M, N, dZ.data_ptr(), N,
+                  db.data_ptr(), 0)
+        ref = torch.empty(N, device="cuda")
+        for rep in range(2):
+            db.fill_(float("nan"))
+            g.replay()
+            torch.cuda.synchronize()
+            got = db.cpu().numpy().copy()
+            with torch.cuda.stream(s):
+                _call("fg_bias_grad", fresh.handle, 0, M, N, dZ.data_ptr(), N,
+                      ref.data_ptr(), 0)
+            torch.cuda.synchronize()
+            print(f"noalloc under capture: replay {rep} compared", flush=True)
+            assert np.array_equal(got, ref.cpu().numpy()), rep
+            dZ.mul_(-0.5)  # eager work between replays; the next replay reads it
+    finally:
+        fresh.sync()
+        fresh.close()
