@@ -384,24 +384,15 @@ def adam_component(ctx, reps: int):
                                "frac_hbm": nbytes / t / 1e6 / PEAK_HBM_GBS}}
 
 
-def hbm_kernels_component(ctx, reps: int):
-    """The other HBM-bound kernels of the path, in GB/s of algorithmic bytes
-    (each launch timed with HIP events after 200 ms of the same launches):
-    * eltwise: a fused elementwise program, the planner's forward of
-      y = tanh(a * b + c) over 8192 x 8192 fp32 -- one launch reading a, b,
-      c and writing the three node values the plan keeps (a * b, a * b + c
-      and y, its forward_saved tensors): 24 B per element;
-    * act_bwd: dZ = dH * GELU'(Z) over 2^28 elements (12 B per element);
-    * sgd: the multi-tensor SGD over c4's 64 x 4 Mi parameters, gradients
-      zeroed after the update (read p, g; write p, g: 16 B per parameter)."""
+def eltwise_tanh_plan(ctx, R: int, C: int):
+    """The planner's forward of y = tanh(a * b + c) over R x C fp32 inputs
+    a, b, c ~ N(0,1) (library generator, seed 7): one elementwise-program
+    launch.  Returns (tensors, schedule, context, inputs to keep alive)."""
     import numpy as np
     import torch
 
-    import ferrograd_amd as fa
     from ferrograd_amd import graph as G
 
-    out = {}
-    R = C = 8192
     gctx = G.GpuContext(ctx)
     graph, meta = G.Graph(G.MEAN_SQUARED_ERROR, G.Optim.sgd().lower), G.Metadata.new()
     fr, fc = meta.new_field(), meta.new_field()
@@ -416,12 +407,32 @@ def hbm_kernels_component(ctx, reps: int):
     ins = [G.Tensor(x.data_ptr(), x.numel() * 4, x.shape, np.float32, owner=x) for x in xs]
     sch = gctx.schedule(graph.lower(meta), mb, ins, st)
     assert "forward: 1 launches" in st.plan.describe()
+    return st, sch, gctx, (xs, ins)
+
+
+def hbm_kernels_component(ctx, reps: int):
+    """The other HBM-bound kernels of the path, in GB/s of algorithmic bytes
+    (each launch timed with HIP events after 200 ms of the same launches):
+    * eltwise: a fused elementwise program, the planner's forward of
+      y = tanh(a * b + c) over 8192 x 8192 fp32 -- one launch reading a, b,
+      c and writing the three node values the plan keeps (a * b, a * b + c
+      and y, its forward_saved tensors): 24 B per element;
+    * act_bwd: dZ = dH * GELU'(Z) over 2^28 elements (12 B per element);
+    * sgd: the multi-tensor SGD over c4's 64 x 4 Mi parameters, gradients
+      zeroed after the update (read p, g; write p, g: 16 B per parameter)."""
+    import torch
+
+    import ferrograd_amd as fa
+
+    out = {}
+    R = C = 8192
+    st, sch, gctx, keep = eltwise_tanh_plan(ctx, R, C)
     t = event_time_ms(lambda: gctx.dispatch_forward(sch), reps, warm_ms=200)
     nbytes = 24 * R * C
     out["eltwise_fwd_8192x8192"] = {"ms": t, "bytes": nbytes, "gbs": nbytes / t / 1e6,
                                     "frac_hbm": nbytes / t / 1e6 / PEAK_HBM_GBS}
     st.plan.close()
-    del xs, ins
+    del keep
 
     n = 1 << 28
     dH, Z, dZ = (torch.empty(n, device="cuda") for _ in range(3))
@@ -616,6 +627,15 @@ def only_copy_256mib(ctx, reps):
         b.copy_(a)
 
 
+def only_eltwise(ctx, reps):
+    """The elementwise program tanh(a * b + c) over 8192 x 8192 fp32."""
+    st, sch, gctx, keep = eltwise_tanh_plan(ctx, 8192, 8192)
+    for _ in range(reps):
+        gctx.dispatch_forward(sch)
+    gctx.sync()
+    st.plan.close()
+
+
 def only_c5_step(ctx, reps, dtype="f32"):
     """The c5 training step as a captured hipGraph, replayed (for kernel
     traces of the step alone)."""
@@ -717,6 +737,7 @@ ONLY = {
     "softmax_ce_c3": only_softmax_ce_c3,
     "adam_c4": only_adam_c4,
     "copy_256mib": only_copy_256mib,
+    "eltwise_8192": only_eltwise,
     "hbm_kernels": lambda ctx, reps: print(json.dumps(hbm_kernels_component(ctx, reps)),
                                            flush=True),
 }

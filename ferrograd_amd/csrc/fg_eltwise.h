@@ -9,6 +9,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <cstdio>
 
 namespace fg {
 
@@ -52,9 +53,11 @@ constexpr int kEltMaxDst = 8;
 constexpr int kEltRegs = 16;
 constexpr int kEltPre = 4;  // sources prefetched per quad (launch_eltwise)
 
-// pre: set by launch_eltwise on a load it prefetches, slot + 1 (0: none).
+// Register operands by op: a and b of binary ops and kEltMax, a of unary ops
+// and kEltRound, b of a store / accumulate, a, b and c of kEltSelect; dst of
+// every op but a store / accumulate.  Other fields are not registers.
 struct EltInstr {
-    uint8_t op, dst, a, b, c, pre, pad[2];
+    uint8_t op, dst, a, b, c, pad[3];
     float imm;
 };
 
@@ -78,9 +81,12 @@ struct EltProgram {
     int32_t n_instr;
     EltInstr ins[kEltMaxInstr];
     // Filled by launch_eltwise: the sources whose quads every thread loads
-    // before running the program (fp32, whole tensor, 16-byte aligned).
+    // into registers 0 .. n_pre-1 before running the program (whole-tensor
+    // sources of element type pre_dt[j], aligned for quad loads, disjoint
+    // from every destination), their loads taken out of the program.
     int32_t n_pre;
     int32_t pre_src[kEltPre];
+    int32_t pre_dt[kEltPre];
 };
 
 // The rule above, checked: every array the kernel indexes with a run-time
@@ -93,5 +99,144 @@ static_assert(sizeof(EltProgram::dst[0]) % 4 == 0 && offsetof(EltProgram, dst) %
 static_assert(sizeof(EltInstr) % 4 == 0 && alignof(EltInstr) >= 4 &&
                   offsetof(EltProgram, ins) % 4 == 0,
               "ins[] elements must be whole 4-byte words");
+
+// ---------------------------------------------------------------- host side
+// (plain C++: the launch code and the CPU tests of the allocation use it)
+
+// Which fields of an instruction are registers.
+struct EltRegUse {
+    bool a, b, c, w;
+    bool known;  // a valid op
+};
+
+inline EltRegUse elt_reg_use(const EltInstr &in) {
+    switch (in.op) {
+        case kEltLoad: case kEltImm: case kEltLabelEq: return {false, false, false, true, true};
+        case kEltStore: case kEltAccum: return {false, true, false, false, true};
+        case kEltRound: case kEltNeg: case kEltRelu: case kEltGelu: case kEltElu: case kEltTanh:
+        case kEltExp: case kEltLog: case kEltAbs: case kEltReluD: case kEltGeluD: case kEltEluD:
+        case kEltSign:
+            return {true, false, false, true, true};
+        case kEltAdd: case kEltSub: case kEltMul: case kEltDiv: case kEltMax:
+            return {true, true, false, true, true};
+        case kEltSelect: return {true, true, true, true, true};
+        default: return {false, false, false, false, false};
+    }
+}
+
+// Element size of a storage type code (0 fp32, 1 fp16, 2 bf16).
+inline uint64_t elt_esize(int dt) { return dt == 0 ? 4 : 2; }
+
+// Rewrites a validated program into the form the kernel runs:
+//  * prefetch (when `prefetch`): up to kEltPre sources loaded whole (mode
+//    kModeFull) from memory aligned for quad loads (16 bytes fp32, 8 bytes
+//    16-bit) and disjoint from every destination's bytes (so no store of the
+//    program can precede a load of the same memory) are bound to registers
+//    0 .. n_pre-1 (n_pre, pre_src, pre_dt) and their loads removed;
+//  * registers by liveness: each write starts a new value, and a register
+//    is free again once its value's last reader has run.  An instruction
+//    reads its operands before it writes, so its result may take the
+//    register of an operand it reads last.  For straight-line code this
+//    linear scan uses exactly as many registers as values live at once.
+// Returns the registers used (possibly above kEltRegs when prefetching
+// raised the pressure; the caller then allocates again without it), or -1
+// with `why` set when an instruction reads a register never written.
+inline int elt_allocate(EltProgram &p, bool prefetch, char *why, size_t why_len) {
+    const int n = p.n_instr;
+    int pre_of_src[kEltMaxSrc];
+    for (int s = 0; s < kEltMaxSrc; ++s) pre_of_src[s] = -1;
+    p.n_pre = 0;
+    if (prefetch) {
+        for (int k = 0; k < n; ++k) {
+            const EltInstr &in = p.ins[k];
+            if (in.op != kEltLoad || in.c != kModeFull || in.a >= kEltMaxSrc ||
+                pre_of_src[in.a] >= 0 || p.n_pre == kEltPre)
+                continue;
+            const uintptr_t lo = (uintptr_t)p.src[in.a];
+            if ((lo & (in.b == 0 ? 15u : 7u)) != 0) continue;
+            const uintptr_t hi = lo + p.n * elt_esize(in.b);
+            bool clash = false;
+            for (int j = 0; j < n && !clash; ++j) {
+                const EltInstr &st = p.ins[j];
+                if (st.op != kEltStore && st.op != kEltAccum) continue;
+                const uintptr_t dlo = (uintptr_t)p.dst[st.a];
+                const uintptr_t dhi = dlo + p.n * elt_esize(st.c);
+                clash = dlo < hi && lo < dhi;
+            }
+            if (clash) continue;
+            pre_of_src[in.a] = p.n_pre;
+            p.pre_src[p.n_pre] = in.a;
+            p.pre_dt[p.n_pre] = in.b;
+            ++p.n_pre;
+        }
+    }
+    // Values 0 .. n_pre-1 are the prefetched sources, then one per write;
+    // cur[r] = the value register r holds (-1: never written).
+    constexpr int kMaxVals = kEltPre + kEltMaxInstr;
+    int cur[kEltRegs];
+    for (int r = 0; r < kEltRegs; ++r) cur[r] = -1;
+    int nvals = p.n_pre;
+    int last_use[kMaxVals];
+    for (int v = 0; v < kMaxVals; ++v) last_use[v] = -1;
+    int rd[kEltMaxInstr][3], wv[kEltMaxInstr];
+    bool keep[kEltMaxInstr];
+    for (int k = 0; k < n; ++k) {
+        const EltInstr &in = p.ins[k];
+        const EltRegUse u = elt_reg_use(in);
+        const uint8_t f[3] = {in.a, in.b, in.c};
+        const bool use[3] = {u.a, u.b, u.c};
+        for (int i = 0; i < 3; ++i) {
+            rd[k][i] = -1;
+            if (!use[i]) continue;
+            const int v = f[i] < kEltRegs ? cur[f[i]] : -1;
+            if (v < 0) {
+                snprintf(why, why_len, "instruction %d reads register %d before any write", k,
+                         f[i]);
+                return -1;
+            }
+            rd[k][i] = v;
+            last_use[v] = k;
+        }
+        keep[k] = !(in.op == kEltLoad && in.c == kModeFull && in.a < kEltMaxSrc &&
+                    pre_of_src[in.a] >= 0 && p.pre_dt[pre_of_src[in.a]] == in.b);
+        wv[k] = -1;
+        if (u.w) {
+            if (in.dst >= kEltRegs) {
+                snprintf(why, why_len, "instruction %d writes register %d", k, in.dst);
+                return -1;
+            }
+            wv[k] = keep[k] ? nvals++ : pre_of_src[in.a];
+            cur[in.dst] = wv[k];
+        }
+    }
+    int phys[kMaxVals];
+    bool busy[kMaxVals] = {};  // at most kMaxVals values, so registers < kMaxVals
+    int used = p.n_pre;
+    for (int v = 0; v < p.n_pre; ++v) {
+        phys[v] = v;
+        busy[v] = last_use[v] >= 0;
+    }
+    int out = 0;
+    for (int k = 0; k < n; ++k) {
+        for (int i = 0; i < 3; ++i)  // operands whose last reader this is
+            if (rd[k][i] >= 0 && last_use[rd[k][i]] == k) busy[phys[rd[k][i]]] = false;
+        if (!keep[k]) continue;
+        EltInstr in = p.ins[k];
+        if (rd[k][0] >= 0) in.a = (uint8_t)phys[rd[k][0]];
+        if (rd[k][1] >= 0) in.b = (uint8_t)phys[rd[k][1]];
+        if (rd[k][2] >= 0) in.c = (uint8_t)phys[rd[k][2]];
+        if (wv[k] >= 0) {
+            int r = 0;
+            while (busy[r]) ++r;
+            phys[wv[k]] = r;
+            busy[r] = last_use[wv[k]] > k;  // a value nobody reads frees at once
+            if (r + 1 > used) used = r + 1;
+            in.dst = (uint8_t)r;
+        }
+        p.ins[out++] = in;
+    }
+    p.n_instr = out;
+    return used;
+}
 
 }  // namespace fg

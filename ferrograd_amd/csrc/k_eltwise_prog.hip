@@ -18,6 +18,7 @@ namespace {
 constexpr int kThreads = 256;
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // Each thread runs the program over a quad of 4 consecutive elements
 // (i0 .. i0+3, i0 % 4 == 0): registers are f32x4, and a load or store moves
@@ -31,25 +32,42 @@ __device__ __forceinline__ bool quad_aligned(const void *q, int dt) {
     return (((uintptr_t)q) & (dt == kF32 ? 15u : 7u)) == 0;
 }
 
+// NT: streaming (non-temporal) loads and stores, for tensors far larger than
+// the caches (the copy-like streams of such programs ran 6 % faster).
+template <bool NT>
 __device__ __forceinline__ f32x4 quad_get(const void *q, int dt, uint64_t j) {
-    if (dt == kF32) return *reinterpret_cast<const f32x4 *>(static_cast<const float *>(q) + j);
-    const uint2 w = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(q) + j);
+    if (dt == kF32) {
+        const f32x4 *a = reinterpret_cast<const f32x4 *>(static_cast<const float *>(q) + j);
+        return NT ? __builtin_nontemporal_load(a) : *a;
+    }
+    const u32x2 *a = reinterpret_cast<const u32x2 *>(static_cast<const uint16_t *>(q) + j);
+    const u32x2 w = NT ? __builtin_nontemporal_load(a) : *a;
     return f32x4{h16_to_f(dt, (uint16_t)(w.x & 0xffffu)), h16_to_f(dt, (uint16_t)(w.x >> 16)),
                  h16_to_f(dt, (uint16_t)(w.y & 0xffffu)), h16_to_f(dt, (uint16_t)(w.y >> 16))};
 }
 
+template <bool NT>
 __device__ __forceinline__ void quad_put(void *q, int dt, uint64_t j, f32x4 v) {
     if (dt == kF32) {
-        *reinterpret_cast<f32x4 *>(static_cast<float *>(q) + j) = v;
+        f32x4 *a = reinterpret_cast<f32x4 *>(static_cast<float *>(q) + j);
+        if (NT)
+            __builtin_nontemporal_store(v, a);
+        else
+            *a = v;
         return;
     }
-    uint2 w;
+    u32x2 w;
     w.x = (uint32_t)f_to_h16(dt, v[0]) | ((uint32_t)f_to_h16(dt, v[1]) << 16);
     w.y = (uint32_t)f_to_h16(dt, v[2]) | ((uint32_t)f_to_h16(dt, v[3]) << 16);
-    *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(q) + j) = w;
+    u32x2 *a = reinterpret_cast<u32x2 *>(static_cast<uint16_t *>(q) + j);
+    if (NT)
+        __builtin_nontemporal_store(w, a);
+    else
+        *a = w;
 }
 
 // Source s at elements i0 .. i0+nv-1 (missing lanes of a partial quad are 0).
+template <bool NT>
 __device__ __forceinline__ f32x4 quad_load(const EltProgram &p, int s, int mode, int dt,
                                            uint64_t i0, int nv) {
     const void *q = p.src[s];
@@ -58,25 +76,26 @@ __device__ __forceinline__ f32x4 quad_load(const EltProgram &p, int s, int mode,
         return f32x4{x, x, x, x};
     }
     if (mode == kModeFull) {
-        if (nv == 4 && quad_aligned(q, dt)) return quad_get(q, dt, i0);
+        if (nv == 4 && quad_aligned(q, dt)) return quad_get<NT>(q, dt, i0);
         f32x4 r{0.f, 0.f, 0.f, 0.f};
         for (int e = 0; e < nv; ++e) r[e] = load_as_f(q, dt, i0 + e);
         return r;
     }
     // Row broadcast: element i reads src[i % cols].
     const uint32_t c0 = (uint32_t)(i0 % p.cols);
-    if (nv == 4 && p.cols % 4 == 0 && quad_aligned(q, dt)) return quad_get(q, dt, c0);
+    if (nv == 4 && p.cols % 4 == 0 && quad_aligned(q, dt)) return quad_get<false>(q, dt, c0);
     f32x4 r{0.f, 0.f, 0.f, 0.f};
     for (int e = 0; e < nv; ++e) r[e] = load_as_f(q, dt, (c0 + (uint32_t)e) % p.cols);
     return r;
 }
 
+template <bool NT>
 __device__ __forceinline__ void quad_store(const EltProgram &p, int d, int dt, uint64_t i0, int nv,
                                            f32x4 v, bool accum) {
     void *q = p.dst[d];
     if (nv == 4 && quad_aligned(q, dt)) {
-        if (accum) v += quad_get(q, dt, i0);
-        quad_put(q, dt, i0, v);
+        if (accum) v += quad_get<NT>(q, dt, i0);
+        quad_put<NT>(q, dt, i0, v);
         return;
     }
     for (int e = 0; e < nv; ++e)
@@ -91,143 +110,115 @@ __device__ __forceinline__ f32x4 quad_map(f32x4 x, F f) {
     return r;
 }
 
-template <int N>
-using QIdx = std::integral_constant<int, N>;
-// f(QIdx<0>{}), ..., f(QIdx<Q-1>{}): per-quad code with a constant quad index.
-template <int Q, class F>
-__device__ __forceinline__ void for_quads(F &&f) {
-    static_assert(Q == 1 || Q == 2, "one or two quads per thread");
-    f(QIdx<0>{});
-    if constexpr (Q > 1) f(QIdx<1>{});
-}
-
-// Q: quads per thread and pass.  Every lane runs the same instruction
-// stream, so decoding an instruction, branching on its op and reading its
-// pointers is scalar work done once per wave and pass; the scalar unit is
-// shared by the CU's waves and is what bounds short programs (tanh(a*b + c):
-// ~500 scalar instructions per wave, 60 % of the kernel's cycles).  Thread t
-// of a workgroup takes quads base + q * kThreads + t (q < Q), so each load
-// and store of the pass stays coalesced.  The pass loop is uniform: a lane
-// past the end takes an empty quad (loads give 0, stores skip), so the
-// interpreter runs outside any divergent region.
-template <int Q>
+// The register file holds kEltRegs = R * U quads per thread: R program
+// registers for each of the U quads the thread runs the program over in one
+// pass.  Slot u * R + r holds register r of quad u, in four arrays (one per
+// element of a quad) of kEltRegs floats, all indexed by the same uniform
+// number.  Arrays of 16 are indexed through the GPU's relative register
+// addressing (one index setup serves every quad, since quad u only adds the
+// constant u * R), where smaller arrays turn into select chains.
+//
+// Every lane runs the same instruction stream, so decoding an instruction,
+// branching on its op and reading its pointers is scalar work done once per
+// wave and pass; the scalar unit is shared by the CU's waves and bounds
+// short programs.  U quads per pass spread that work over 4 * U elements per
+// lane: launch_eltwise allocates the program's registers by liveness and
+// takes the smallest file (R = 4, 8 or 16) that holds them.  Thread t of a
+// workgroup takes quads base + u * kThreads + t (u < U), so each load and
+// store of a pass stays coalesced.  The pass loop is uniform: a lane past the
+// end takes an empty quad (loads give 0, stores skip), so the interpreter
+// runs outside any divergent region.
+template <int R, int U, bool NT>
 __global__ __launch_bounds__(kThreads) void eltwise_prog_kernel(const EltProgram p) {
+    static_assert(R * U == kEltRegs, "the file holds kEltRegs quads per thread");
+    static_assert(kEltPre <= R, "prefetched sources occupy registers 0 .. n_pre-1");
     const uint64_t nq = (p.n + 3) / 4;
-    const uint64_t span = (uint64_t)kThreads * Q;
+    const uint64_t span = (uint64_t)kThreads * U;
     const uint64_t stride = (uint64_t)gridDim.x * span;
-    for (uint64_t base = (uint64_t)blockIdx.x * span; base < nq; base += stride) {
-        uint64_t i0[Q];
-        int nv[Q];  // elements of quad q (0 past the end: loads give 0, stores skip)
-        // The register file: an array per element of each quad, all indexed
-        // by the same uniform register number.  Every access names its array
-        // at compile time (the quad through get / set, the element by name),
-        // which keeps each array in VGPRs, read and written through indexed
-        // moves; a float4 array, or one indexed by a run-time quad, would go
-        // to scratch memory.
-        float a0[kEltRegs], a1[kEltRegs], a2[kEltRegs], a3[kEltRegs];  // quad 0
-        float b0[kEltRegs], b1[kEltRegs], b2[kEltRegs], b3[kEltRegs];  // quad 1 (Q = 2)
-        auto get = [&](auto qc, int k) {
-            k &= kEltRegs - 1;
-            if constexpr (decltype(qc)::value == 0) return f32x4{a0[k], a1[k], a2[k], a3[k]};
-            else return f32x4{b0[k], b1[k], b2[k], b3[k]};
-        };
-        auto set = [&](auto qc, int k, f32x4 v) {
-            k &= kEltRegs - 1;
-            if constexpr (decltype(qc)::value == 0) {
-                a0[k] = v[0];
-                a1[k] = v[1];
-                a2[k] = v[2];
-                a3[k] = v[3];
-            } else {
-                b0[k] = v[0];
-                b1[k] = v[1];
-                b2[k] = v[2];
-                b3[k] = v[3];
-            }
-        };
-        // The prefetched sources' quads, all loads issued before the program
-        // runs: a load's value must be present when it is written to the
-        // register file (indexed at run time), so loads issued by the
-        // program itself each wait for their data in turn.
-        constexpr f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-        f32x4 pre[Q][kEltPre];
-        for_quads<Q>([&](auto qc) {
-            constexpr int q = decltype(qc)::value;
-            const uint64_t qi = base + (uint64_t)q * kThreads + threadIdx.x;
-            i0[q] = 4 * qi;
-            nv[q] = qi >= nq ? 0 : (p.n - i0[q] >= 4 ? 4 : (int)(p.n - i0[q]));
+    float f0[kEltRegs], f1[kEltRegs], f2[kEltRegs], f3[kEltRegs];
 #pragma unroll
-            for (int k = 0; k < kEltRegs; ++k) set(qc, k, zero);
+    for (int k = 0; k < kEltRegs; ++k) f0[k] = f1[k] = f2[k] = f3[k] = 0.0f;
+    // u is a compile-time constant at every call (unrolled loops), r a
+    // uniform run-time register number kept inside the file by the mask.
+    auto get = [&](int u, int r) {
+        const int k = u * R + (r & (R - 1));
+        return f32x4{f0[k], f1[k], f2[k], f3[k]};
+    };
+    auto set = [&](int u, int r, f32x4 v) {
+        const int k = u * R + (r & (R - 1));
+        f0[k] = v[0];
+        f1[k] = v[1];
+        f2[k] = v[2];
+        f3[k] = v[3];
+    };
+    for (uint64_t base = (uint64_t)blockIdx.x * span; base < nq; base += stride) {
+        uint64_t i0[U];
+        int nv[U];  // elements of quad u (0 past the end: loads give 0, stores skip)
+        // The prefetched sources, every load issued before the program runs:
+        // a value must be present when the program first reads the file (a
+        // run-time index), so loads the program issues itself wait in turn.
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint64_t qi = base + (uint64_t)u * kThreads + threadIdx.x;
+            i0[u] = 4 * qi;
+            nv[u] = qi >= nq ? 0 : (p.n - i0[u] >= 4 ? 4 : (int)(p.n - i0[u]));
 #pragma unroll
             for (int j = 0; j < kEltPre; ++j)
-                pre[q][j] = (j < p.n_pre && nv[q] == 4)
-                                ? *reinterpret_cast<const f32x4 *>(p.src[p.pre_src[j]] + i0[q])
-                                : zero;
-        });
+                if (j < p.n_pre)
+                    set(u, j, quad_load<NT>(p, p.pre_src[j], kModeFull, p.pre_dt[j], i0[u], nv[u]));
+        }
         for (int k = 0; k < p.n_instr; ++k) {
             const EltInstr in = p.ins[k];
-            // One read site for the operands and one write site for the
-            // result (each indexed access costs scalar work to set up, and
-            // more sites hold more registers).
-            f32x4 x[Q], y[Q], o[Q];
-            for_quads<Q>([&](auto qc) {
-                constexpr int q = decltype(qc)::value;
-                x[q] = get(qc, in.a);
-                y[q] = get(qc, in.b);
-                o[q] = x[q];
-            });
+            // One read site per operand and one write site for the result
+            // (each indexed access costs scalar work to set up).
+            f32x4 x[U], y[U], o[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                x[u] = get(u, in.a);
+                y[u] = get(u, in.b);
+                o[u] = x[u];
+            }
             bool wr = true;  // the instruction writes register in.dst
             auto unary = [&](auto f) {
 #pragma unroll
-                for (int q = 0; q < Q; ++q) o[q] = quad_map(x[q], f);
+                for (int u = 0; u < U; ++u) o[u] = quad_map(x[u], f);
             };
             switch (in.op) {
                 case kEltLoad:
 #pragma unroll
-                    for (int q = 0; q < Q; ++q) {
-                        if (in.pre && nv[q] == 4) {
-                            switch (in.pre) {  // a constant index into pre[q]
-                                case 1: o[q] = pre[q][0]; break;
-                                case 2: o[q] = pre[q][1]; break;
-                                case 3: o[q] = pre[q][2]; break;
-                                default: o[q] = pre[q][3]; break;
-                            }
-                        } else {
-                            o[q] = quad_load(p, in.a, in.c, in.b, i0[q], nv[q]);
-                        }
-                    }
+                    for (int u = 0; u < U; ++u) o[u] = quad_load<NT>(p, in.a, in.c, in.b, i0[u], nv[u]);
                     break;
                 case kEltImm:
 #pragma unroll
-                    for (int q = 0; q < Q; ++q) o[q] = f32x4{in.imm, in.imm, in.imm, in.imm};
+                    for (int u = 0; u < U; ++u) o[u] = f32x4{in.imm, in.imm, in.imm, in.imm};
                     break;
                 case kEltStore:
                 case kEltAccum:
 #pragma unroll
-                    for (int q = 0; q < Q; ++q)
-                        quad_store(p, in.a, in.c, i0[q], nv[q], y[q], in.op == kEltAccum);
+                    for (int u = 0; u < U; ++u)
+                        quad_store<NT>(p, in.a, in.c, i0[u], nv[u], y[u], in.op == kEltAccum);
                     wr = false;
                     break;
                 case kEltRound: unary([&](float v) { return round_to(in.c, v); }); break;
                 case kEltAdd:
 #pragma unroll
-                    for (int q = 0; q < Q; ++q) o[q] = x[q] + y[q];
+                    for (int u = 0; u < U; ++u) o[u] = x[u] + y[u];
                     break;
                 case kEltSub:
 #pragma unroll
-                    for (int q = 0; q < Q; ++q) o[q] = x[q] - y[q];
+                    for (int u = 0; u < U; ++u) o[u] = x[u] - y[u];
                     break;
                 case kEltMul:
 #pragma unroll
-                    for (int q = 0; q < Q; ++q) o[q] = x[q] * y[q];
+                    for (int u = 0; u < U; ++u) o[u] = x[u] * y[u];
                     break;
                 case kEltDiv:
 #pragma unroll
-                    for (int q = 0; q < Q; ++q) o[q] = x[q] / y[q];
+                    for (int u = 0; u < U; ++u) o[u] = x[u] / y[u];
                     break;
                 case kEltNeg:
 #pragma unroll
-                    for (int q = 0; q < Q; ++q) o[q] = -x[q];
+                    for (int u = 0; u < U; ++u) o[u] = -x[u];
                     break;
                 case kEltRelu: unary([](float v) { return act_fwd(kActRelu, v); }); break;
                 case kEltGelu: unary([](float v) { return act_fwd(kActGelu, v); }); break;
@@ -244,73 +235,72 @@ __global__ __launch_bounds__(kThreads) void eltwise_prog_kernel(const EltProgram
                     break;
                 case kEltLabelEq:
 #pragma unroll
-                    for (int q = 0; q < Q; ++q) {
+                    for (int u = 0; u < U; ++u) {
                         f32x4 t{0.f, 0.f, 0.f, 0.f};
-                        for (int e = 0; e < nv[q]; ++e) {
-                            const uint64_t row = (i0[q] + e) / p.cols, col = (i0[q] + e) % p.cols;
+                        for (int e = 0; e < nv[u]; ++e) {
+                            const uint64_t row = (i0[u] + e) / p.cols, col = (i0[u] + e) % p.cols;
                             t[e] = (p.labels[row] == (uint32_t)col) ? 1.0f : 0.0f;
                         }
-                        o[q] = t;
+                        o[u] = t;
                     }
                     break;
                 case kEltSelect:
-                    for_quads<Q>([&](auto qc) {
-                        constexpr int q = decltype(qc)::value;
-                        const f32x4 z = get(qc, in.c);
+#pragma unroll
+                    for (int u = 0; u < U; ++u) {
+                        const f32x4 z = get(u, in.c);
                         f32x4 t;
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) t[e] = x[q][e] != 0.0f ? y[q][e] : z[e];
-                        o[q] = t;
-                    });
+                        for (int e = 0; e < 4; ++e) t[e] = x[u][e] != 0.0f ? y[u][e] : z[e];
+                        o[u] = t;
+                    }
                     break;
                 case kEltMax:
 #pragma unroll
-                    for (int q = 0; q < Q; ++q) {
+                    for (int u = 0; u < U; ++u) {
                         f32x4 t;
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) t[e] = fmaxf(x[q][e], y[q][e]);
-                        o[q] = t;
+                        for (int e = 0; e < 4; ++e) t[e] = fmaxf(x[u][e], y[u][e]);
+                        o[u] = t;
                     }
                     break;
                 default: wr = false; break;
             }
-            if (wr) for_quads<Q>([&](auto qc) { set(qc, in.dst, o[decltype(qc)::value]); });
+            if (wr) {
+#pragma unroll
+                for (int u = 0; u < U; ++u) set(u, in.dst, o[u]);
+            }
         }
     }
+}
+
+template <int R, int U, bool NT>
+int launch_file(fg_ctx *ctx, const EltProgram &p) {
+    // One pass per workgroup where the grid allows it; the launch keeps
+    // gridDim.x * blockDim.x within 32 bits and the pass loop covers the
+    // rest.
+    uint64_t blocks = ((p.n + 3) / 4 + (uint64_t)kThreads * U - 1) / ((uint64_t)kThreads * U);
+    constexpr uint64_t kMaxBlocks = (uint64_t(1) << 32) / kThreads / 2;
+    if (blocks > kMaxBlocks) blocks = kMaxBlocks;
+    eltwise_prog_kernel<R, U, NT><<<(unsigned)blocks, kThreads, 0, ctx->stream>>>(p);
+    FG_LAUNCH_CHECK("eltwise_prog_kernel");
+    return FG_OK;
 }
 
 }  // namespace
 
 // Validates the program's indices on the host (so the kernel never reads a
-// source or writes a destination that was not supplied) and launches it.
+// source or writes a destination that was not supplied), allocates its
+// registers and launches it on the smallest register file that holds them.
 int launch_eltwise(fg_ctx *ctx, const EltProgram &p0) {
     if (p0.n == 0) return FG_OK;
-    // Prefetch slots for up to kEltPre sources read whole as fp32 from
-    // 16-byte aligned memory (a source read by several loads takes one).
-    EltProgram p = p0;
-    p.n_pre = 0;
-    for (int k = 0; k < p.n_instr && k < kEltMaxInstr; ++k) {
-        EltInstr &in = p.ins[k];
-        in.pre = 0;
-        if (in.op != kEltLoad || in.c != kModeFull || in.b != kF32 || in.a >= kEltMaxSrc ||
-            !p.src[in.a] || (((uintptr_t)p.src[in.a]) & 15u) != 0)
-            continue;
-        int slot = -1;
-        for (int j = 0; j < p.n_pre; ++j)
-            if (p.pre_src[j] == in.a) slot = j;
-        if (slot < 0 && p.n_pre < kEltPre) {
-            slot = p.n_pre++;
-            p.pre_src[slot] = in.a;
-        }
-        if (slot >= 0) in.pre = (uint8_t)(slot + 1);
-    }
-    FG_REQUIRE(p.n_instr >= 0 && p.n_instr <= kEltMaxInstr, FG_ERR_INTERNAL,
-               "eltwise program: %d instructions (max %d)", p.n_instr, kEltMaxInstr);
+    FG_REQUIRE(p0.n_instr >= 0 && p0.n_instr <= kEltMaxInstr, FG_ERR_INTERNAL,
+               "eltwise program: %d instructions (max %d)", p0.n_instr, kEltMaxInstr);
     bool needs_cols = false;
-    for (int k = 0; k < p.n_instr; ++k) {
-        const EltInstr &in = p.ins[k];
+    for (int k = 0; k < p0.n_instr; ++k) {
+        const EltInstr &in = p0.ins[k];
+        FG_REQUIRE(elt_reg_use(in).known, FG_ERR_INTERNAL, "eltwise program: unknown op %d", in.op);
         if (in.op == kEltLoad) {
-            FG_REQUIRE(in.a < kEltMaxSrc && p.src[in.a], FG_ERR_INTERNAL,
+            FG_REQUIRE(in.a < kEltMaxSrc && p0.src[in.a], FG_ERR_INTERNAL,
                        "eltwise program: load of missing source %d", in.a);
             FG_REQUIRE(in.c <= kModeScalar, FG_ERR_INTERNAL,
                        "eltwise program: bad addressing mode %d", in.c);
@@ -319,7 +309,7 @@ int launch_eltwise(fg_ctx *ctx, const EltProgram &p0) {
             if (in.c == kModeRow) needs_cols = true;
         }
         if (in.op == kEltStore || in.op == kEltAccum) {
-            FG_REQUIRE(in.a < kEltMaxDst && p.dst[in.a], FG_ERR_INTERNAL,
+            FG_REQUIRE(in.a < kEltMaxDst && p0.dst[in.a], FG_ERR_INTERNAL,
                        "eltwise program: store to missing destination %d", in.a);
             FG_REQUIRE(in.c <= kBF16, FG_ERR_INTERNAL, "eltwise program: bad store type %d",
                        in.c);
@@ -328,24 +318,32 @@ int launch_eltwise(fg_ctx *ctx, const EltProgram &p0) {
             FG_REQUIRE(in.c <= kBF16, FG_ERR_INTERNAL, "eltwise program: bad round type %d",
                        in.c);
         if (in.op == kEltLabelEq) {
-            FG_REQUIRE(p.labels, FG_ERR_INTERNAL, "eltwise program: labels missing");
+            FG_REQUIRE(p0.labels, FG_ERR_INTERNAL, "eltwise program: labels missing");
             needs_cols = true;
         }
     }
-    FG_REQUIRE(!needs_cols || p.cols > 0, FG_ERR_INTERNAL, "eltwise program: cols is 0");
-    // One quad per thread and as many workgroups as that takes, up to the
-    // grid limit (a capped grid looping over the tensor streamed at a
-    // fraction of the rate); the kernel's loop covers anything beyond.
-    uint64_t blocks = ((p.n + 3) / 4 + kThreads - 1) / kThreads;
-    if (blocks > (1u << 30)) blocks = 1u << 30;
-#ifndef FG_ELT_QUADS  // quads per thread and pass (a knob for measurement builds)
-#define FG_ELT_QUADS 1
-#endif
-    constexpr int kQ = FG_ELT_QUADS;
-    blocks = (blocks + kQ - 1) / kQ;
-    eltwise_prog_kernel<kQ><<<(unsigned)blocks, kThreads, 0, ctx->stream>>>(p);
-    FG_LAUNCH_CHECK("eltwise_prog_kernel");
-    return FG_OK;
+    FG_REQUIRE(!needs_cols || p0.cols > 0, FG_ERR_INTERNAL, "eltwise program: cols is 0");
+    EltProgram p = p0;
+    char why[128] = "";
+    int regs = elt_allocate(p, true, why, sizeof why);
+    if (regs > kEltRegs) {  // prefetching raised the pressure: load in place
+        p = p0;
+        regs = elt_allocate(p, false, why, sizeof why);
+    }
+    FG_REQUIRE(regs >= 0, FG_ERR_INTERNAL, "eltwise program: %s", why);
+    FG_REQUIRE(regs <= kEltRegs, FG_ERR_INTERNAL, "eltwise program: %d registers (max %d)",
+               regs, kEltRegs);
+    // Streaming accesses once each tensor is well past the L2 caches (4 MiB
+    // per XCD), so small programs keep their outputs cached for the next
+    // launch.
+    if (p.n >= (uint64_t(1) << 22)) {
+        if (regs <= 4) return launch_file<4, 4, true>(ctx, p);
+        if (regs <= 8) return launch_file<8, 2, true>(ctx, p);
+        return launch_file<16, 1, true>(ctx, p);
+    }
+    if (regs <= 4) return launch_file<4, 4, false>(ctx, p);
+    if (regs <= 8) return launch_file<8, 2, false>(ctx, p);
+    return launch_file<16, 1, false>(ctx, p);
 }
 
 }  // namespace fg

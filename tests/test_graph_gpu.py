@@ -917,14 +917,18 @@ def test_unary_forward_backward(ctx, op):
     assert normwise_rel(ctx.download(st.grad_tensors[0]).reshape(R, C), exp) < 1e-5
 
 
-@pytest.mark.parametrize("R,C", [(37, 1024), (37, 1025), (3, 341)],
-                         ids=["whole-blocks", "blocks+partial", "one-partial-block"])
+@pytest.mark.parametrize("R,C", [(37, 1024), (37, 1025), (3, 341), (5, 4096), (5, 4097),
+                                 (3, 1365), (1031, 4099)],
+                         ids=["1k-whole", "1k-partial", "1k-one-partial", "4k-whole",
+                              "4k-partial", "4k-one-partial", "streaming-partial"])
 def test_eltwise_program_whole_and_partial_blocks(ctx, R, C):
     """tanh(x * y + z) and its gradients through elementwise programs at
-    sizes on either side of a workgroup's 256 quads (1024 elements): 37 x
-    1024 fills whole workgroups, 37 x 1025 adds a partial one with a partial
-    last quad, 3 x 341 (1023 elements) is one partial workgroup.  Forward and
-    every gradient against float64 numpy."""
+    sizes on either side of a workgroup's pass (256 threads x U quads:
+    1024 elements for the 16-register file, 4096 for the 4-register file the
+    forward program takes): whole workgroups, a partial last workgroup with
+    a partial last quad, and one partial workgroup; 1031 x 4099 (4.2 M
+    elements, a partial last quad) takes the streaming loads and stores of
+    large tensors.  Forward and every gradient against float64 numpy."""
     G = api()
     graph, meta = new_graph(G.MEAN_SQUARED_ERROR)
     r, c = meta.new_field(), meta.new_field()
