@@ -626,12 +626,12 @@ __device__ __forceinline__ void gemm16_pipe_body(Args p, int bx, int by) {
             const int li = wave * kPerA + q, pos = li * 64 + lane;
             const uint16_t *src = AK ? src_kc(p.A, p.lda, m0, p.M, k0, pos)
                                      : src_rc(p.A, p.lda, m0, p.M, k0, pos, BM);
-            __builtin_amdgcn_global_load_lds(src, sa + li * 512, 16, 0, 0);
+            lds_dma16(src, sa + li * 512);
         } else {
             const int li = wave * kPerB + (q - kPerA), pos = li * 64 + lane;
             const uint16_t *src = BNC ? src_rc(p.B, p.ldb, n0, p.N, k0, pos, BN)
                                       : src_kc(p.B, p.ldb, n0, p.N, k0, pos);
-            __builtin_amdgcn_global_load_lds(src, sa + kASz + li * 512, 16, 0, 0);
+            lds_dma16(src, sa + kASz + li * 512);
         }
     };
     auto issue = [&](int kt, int stage) {
@@ -843,19 +843,19 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm16_pipe(Args p) {
     gemm16_pipe_body<BM, BN, BK, WGM, WGN, AK, BNC, BF>(p, blockIdx.x, blockIdx.y);
 }
 
-// A large layer's weight gradient (TN, 256x256 tiles, 8 waves, BK 32:
-// workgroups below n1) and data gradient (NT, 256x128 tiles, 8 waves, BK
+// A large layer's weight gradient (TN, 256x256 tiles, 8 waves, BK 64, direct
+// loads: workgroups below n1) and data gradient (NT, 256x128 tiles, 8 waves, BK
 // 64: the rest) in one launch, each body exactly as its own kernel, both on
 // one LDS buffer of the larger size: the dW tiles' output writes drain while
 // dX tiles compute, where two launches would leave the CUs idle through them.
-constexpr int kPair16Lds = Pipe16Lds<256, 256, 32, 2, 4>::elems > Pipe16Lds<256, 128, 64, 4, 2>::elems
-                               ? Pipe16Lds<256, 256, 32, 2, 4>::elems
+constexpr int kPair16Lds = Pipe16Lds<256, 256, 64, 2, 4>::elems > Pipe16Lds<256, 128, 64, 4, 2>::elems
+                               ? Pipe16Lds<256, 256, 64, 2, 4>::elems
                                : Pipe16Lds<256, 128, 64, 4, 2>::elems;
 template <bool BF>
 __global__ __launch_bounds__(512) void gemm16_pair_big(Args a1, Args a2, int n1) {
     const int w = blockIdx.x;
     if (w < n1)
-        gemm16_pipe_body<256, 256, 32, 2, 4, false, true, BF, kPair16Lds>(a1, w, 0);
+        gemm16_pipe_body<256, 256, 64, 2, 4, false, true, BF, kPair16Lds>(a1, w, 0);
     else
         gemm16_pipe_body<256, 128, 64, 4, 2, true, false, BF, kPair16Lds>(a2, w - n1, 0);
 }
@@ -868,8 +868,8 @@ void launch_pair16(Args a1, Args a2, hipStream_t st) {
     const int n1 = a1.tiles_m * a1.tiles_n, n2 = a2.tiles_m * a2.tiles_n;
     gemm16_pair_big<BF><<<n1 + n2, 512, 0, st>>>(a1, a2, n1);
 }
-// The pair's configurations (see launch_layout): dW on cfg 1, dX on cfg 8.
-constexpr int kPair16CfgW = 1, kPair16CfgX = 8;
+// The pair's configurations (see launch_layout): dW on cfg 6, dX on cfg 8.
+constexpr int kPair16CfgW = 6, kPair16CfgX = 8;
 
 // The slots of a K-split GEMM summed in slot order (fp32), then the GEMM's
 // epilogue applied to each sum exactly as the kernel applies it to its own

@@ -23,13 +23,15 @@ int tiles(int M, int N, int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn 
 // Tile configuration (indices as in fg_gemm16_kernel.h), from a measured
 // sweep on MI355X of every configuration of the pipelined kernel (TFLOP/s,
 // bf16, N(0,1) operands; fp16 within a few percent):
-//  * squares that give >= one 256x256 tile per CU: NT (both operands
-//    k-contiguous) 256x256 with 8 waves and BK 64, direct loads (1178-1209
-//    at 4096^3, against 1049 for the staged BK 32 tile); NN and TN 256x256
-//    with 8 waves and BK 32, staged loads (1147 / 1073 at 4096^3, 1002 for
-//    the 4096x4096x2048 weight gradient, against 933 / 714 / 600 for the
-//    direct BK 64 tile: the compiler makes each transposing LDS read wait for
-//    every direct load in flight, as it cannot tell them apart);
+//  * squares that give >= one 256x256 tile per CU: 256x256 with 8 waves and
+//    BK 64, direct loads, every layout: 1134-1162 / 1141-1171 / 1117-1145
+//    (NN / NT / TN) at 4096^3 and 995-1003 for the 4096x4096x2048 weight
+//    gradient, against 1115-1145 / 1143-1171 / 1117-1151 and 938-947 for
+//    the staged BK 32 tile, and 1070-1098 / 1075-1105 / 1050-1080 and 839-846
+//    for 4 waves (one per SIMD: each wave's waits idle its matrix unit).
+//    The direct loads are issued as inline assembly (lds_dma16): as builtins
+//    the compiler made every transposing LDS read wait for all of them in
+//    flight (933 / 714 / 600 then);
 //  * else 256x128 with 8 waves and BK 64 down to a quarter tile per CU: 956
 //    for the 2048x4096x4096 forward, 799-855 for its NT data gradient, 302
 //    for the 1000-wide head, where every smaller tile measured lower;
@@ -39,7 +41,7 @@ int tiles(int M, int N, int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn 
 // gemm16_mfma, with 256x128 / 8 waves where it gives a quarter tile per CU.
 int pick_cfg16(int layout, int M, int N, int K, int cus) {
     if (K % 64 == 0) {
-        if (tiles(M, N, 256, 256) >= cus) return layout == FG_NT ? 6 : 1;
+        if (tiles(M, N, 256, 256) >= cus) return 6;
         if (tiles(M, N, 256, 128) >= cus / 4) return 8;
     } else if (K % 32 == 0) {
         if (tiles(M, N, 256, 256) >= cus) return 1;
