@@ -153,3 +153,97 @@ def test_gemm_x16_random_vs_float64(dtype):
     diff = np.abs(got.astype(np.int32) - want.astype(np.int32))
     assert diff.max() <= 1
     assert np.mean(diff != 0) < 0.01
+
+
+# GELU-tanh with the reference's constants (crates/ferrograd-nn/src/op/
+# unary.rs:493-494), evaluated independently of the C oracle: numpy float64
+# for the value, complex-step differentiation of the same float64 form for
+# the derivative (f'(x) = Im f(x + ih) / h, exact to float64 rounding for
+# tiny h, with no closed form of the derivative involved).
+_C0, _C1 = 0.7978846, 0.044715
+
+
+def _gelu64(x):
+    return 0.5 * x * (1.0 + np.tanh(_C0 * (x + _C1 * x * x * x)))
+
+
+def _gelu_grad64(x):
+    h = 1e-30
+    return np.imag(_gelu64(x.astype(np.complex128) + 1j * h)) / h
+
+
+def _sixty_fourths(rng, shape):
+    """Multiples of 1/64 in [-1/2, 1/2] (exact in both 16-bit types):
+    products are multiples of 1/4096, and sums over K = 64 stay exact in fp32
+    (at most 16 significant bits) yet need more bits than either 16-bit type
+    holds, and are of order one, where GELU curves."""
+    return rng.integers(-32, 33, size=shape).astype(np.float64) / 64.0
+
+
+def _round_f32(dtype, x64):
+    """A float64 value rounded to float32, then to the 16-bit type (the
+    oracle evaluates activations in double and stores them through float)."""
+    return _round_ref(dtype, x64.astype(np.float32).astype(np.float64))
+
+
+@pytest.mark.parametrize("dtype", [F16, BF16])
+def test_gemm_x16_gelu_rounds_each_node_once(dtype):
+    """Forward matmul -> bias add -> GELU on 16-bit tensors: exact-integer
+    operands fix the product, so the result is set by the rounding points:
+    the matmul node, the bias-add node (Z) and the GELU node are each rounded
+    once to the storage type.  The inputs are chosen so that GELU of an
+    unrounded pre-activation, or of a product whose rounding was dropped,
+    gives other bits on some elements (asserted), so either mistake fails."""
+    rng = np.random.default_rng(21 + dtype)
+    M, N, K = 37, 29, 64
+    a, b, bias = _sixty_fourths(rng, (M, K)), _sixty_fourths(rng, (K, N)), _sixty_fourths(rng, (N,))
+    A16, B16, b16 = _round_ref(dtype, a), _round_ref(dtype, b), _round_ref(dtype, bias)
+    exact = (np.rint(a * 64).astype(np.int64) @ np.rint(b * 64).astype(np.int64)) / 4096.0
+    v = _widen_ref(dtype, _round_ref(dtype, exact))
+    z16 = _round_ref(dtype, v + bias[None, :])
+    want = _round_f32(dtype, _gelu64(_widen_ref(dtype, z16)))
+    C, Z = oracle.gemm_x16(dtype, oracle.NN, A16, B16, bias=b16, act=oracle.ACT_GELU, want_z=True)
+    assert np.array_equal(Z, z16)
+    assert np.array_equal(C, want)
+    # The plausible mistakes differ on these inputs.
+    no_z_round = _round_f32(dtype, _gelu64(v + bias[None, :]))
+    no_v_round = _round_f32(dtype, _gelu64(_widen_ref(dtype, _round_ref(dtype, exact + bias))))
+    assert np.count_nonzero(no_z_round != want) > 0
+    assert np.count_nonzero(no_v_round != want) > 0
+
+
+@pytest.mark.parametrize("dtype", [F16, BF16])
+def test_gemm_bwd_x16_gelu_grad_rounds_once(dtype):
+    """Data gradient through GELU on 16-bit tensors: dX = round(round(dC.W^T)
+    * GELU'(Z)), the product in fp32 and one rounding of the result.  A
+    dropped rounding of the matmul node, or an extra rounding of GELU'(Z) to
+    the storage type before the multiply, gives other bits on some elements
+    of these inputs (asserted)."""
+    rng = np.random.default_rng(31 + dtype)
+    M, N, K = 24, 40, 64
+    a, w = _sixty_fourths(rng, (M, K)), _sixty_fourths(rng, (N, K))
+    Z16 = _round_ref(dtype, rng.normal(0.0, 2.0, (M, N)))
+    A16, W16 = _round_ref(dtype, a), _round_ref(dtype, w)
+    exact = (np.rint(a * 64).astype(np.int64) @ np.rint(w * 64).astype(np.int64).T) / 4096.0
+    v32 = _widen_ref(dtype, _round_ref(dtype, exact)).astype(np.float32)
+    g32 = _gelu_grad64(_widen_ref(dtype, Z16)).astype(np.float32)
+    want = _round_ref(dtype, (v32 * g32).astype(np.float64))
+    got = oracle.gemm_bwd_x16(dtype, oracle.NT, A16, W16, act=oracle.ACT_GELU, Zs=Z16)
+    assert np.array_equal(got, want)
+    no_v_round = _round_ref(dtype, (exact.astype(np.float32) * g32).astype(np.float64))
+    g16 = _widen_ref(dtype, _round_ref(dtype, g32.astype(np.float64))).astype(np.float32)
+    extra_g_round = _round_ref(dtype, (v32 * g16).astype(np.float64))
+    assert np.count_nonzero(no_v_round != want) > 0
+    assert np.count_nonzero(extra_g_round != want) > 0
+
+
+def test_gelu_reference_forms_agree_with_torch():
+    """The float64 forms above against torch's tanh GELU and its autograd
+    derivative (torch's constant sqrt(2/pi) differs from the reference's
+    0.7978846 by 5e-8 relative, hence the tolerance)."""
+    x = np.linspace(-8.0, 8.0, 4001)
+    t = torch.tensor(x, dtype=torch.float64, requires_grad=True)
+    y = torch.nn.functional.gelu(t, approximate="tanh")
+    y.sum().backward()
+    assert np.allclose(_gelu64(x), y.detach().numpy(), rtol=1e-6, atol=1e-7)
+    assert np.allclose(_gelu_grad64(x), t.grad.numpy(), rtol=1e-6, atol=1e-7)
