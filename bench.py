@@ -472,6 +472,50 @@ def copy_component(reps: int):
                               "frac_hbm": nbytes / t / 1e6 / PEAK_HBM_GBS}}
 
 
+def hbm_roof_component(reps: int):
+    """The practical HBM roof of the access patterns the bandwidth-bound
+    kernels use, from the measurement kernels of ferrograd_amd/csrc/probe/
+    k_hbm_roof.hip (16-byte non-temporal accesses, one 4 KiB chunk per block
+    pass): a read-only stream of 1 GiB, a 1 GiB copy, 3 streams read and 3
+    written (the elementwise program's count) and 4 read and 3 written
+    (Adam's) over 256 MiB each.  Bytes counted = bytes moved."""
+    import ctypes
+
+    import torch
+
+    from ferrograd_amd import _build
+
+    lib = ctypes.CDLL(_build.ROOF_LIB)
+    u64, vp = ctypes.c_uint64, ctypes.c_void_p
+    stream = vp(torch.cuda.current_stream().cuda_stream)
+    out = {}
+
+    def rec(key, fn, nbytes):
+        t = event_time_ms(fn, reps, warm_ms=200)
+        out[key] = {"ms": t, "bytes": nbytes, "gbs": nbytes / t / 1e6,
+                    "frac_hbm": nbytes / t / 1e6 / PEAK_HBM_GBS}
+
+    def check(rc):
+        if rc != 0:
+            raise RuntimeError("HBM roof kernel launch failed")
+
+    n = 256 * 1024 * 1024
+    a = torch.ones(n, device="cuda")
+    part = torch.empty(lib.fg_roof_blocks(u64(n)), device="cuda")
+    rec("read_1gib", lambda: check(lib.fg_roof_read(stream, vp(a.data_ptr()), u64(n),
+                                                   vp(part.data_ptr()))), 4 * n)
+    b = torch.empty_like(a)
+    rec("copy_1gib", lambda: check(lib.fg_roof_copy(stream, vp(a.data_ptr()), vp(b.data_ptr()),
+                                                   u64(n))), 8 * n)
+    del a, b, part
+    n = 64 * 1024 * 1024
+    x = [torch.full((n,), 0.5, device="cuda") for _ in range(6)]
+    p = [vp(t.data_ptr()) for t in x]
+    rec("s3r3w_256mib", lambda: check(lib.fg_roof_s3r3w(stream, *p, u64(n))), 24 * n)
+    rec("s4r3w_256mib", lambda: check(lib.fg_roof_s4r3w(stream, *p[:4], u64(n))), 28 * n)
+    return {"hbm_roof": out}
+
+
 def c5_bf16_component(ctx, steps: int = 10):
     """The c5 step with every tensor in bfloat16 (16-bit MFMA GEMMs, fp32
     sums and optimiser state): captured steps/s and effective TFLOP/s."""
@@ -738,6 +782,7 @@ ONLY = {
     "adam_c4": only_adam_c4,
     "copy_256mib": only_copy_256mib,
     "eltwise_8192": only_eltwise,
+    "hbm_roof": lambda ctx, reps: print(json.dumps(hbm_roof_component(reps)), flush=True),
     "hbm_kernels": lambda ctx, reps: print(json.dumps(hbm_kernels_component(ctx, reps)),
                                            flush=True),
 }
@@ -1127,6 +1172,7 @@ def main() -> int:
         comps.update(gemm_bf16_component(ctx, args.reps))
         comps.update(c5_bf16_component(ctx))
         comps.update(copy_component(args.reps))
+        comps.update(hbm_roof_component(args.reps))
     log("components: " + json.dumps(comps))
 
     cpu = None

@@ -106,5 +106,24 @@ def build(verbose: bool = True, lib: str = LIB, obj_dir: str = OBJ, defines=()) 
     return lib
 
 
+ROOF_SRC = os.path.join(CSRC, "probe", "k_hbm_roof.hip")
+ROOF_LIB = os.path.join(HERE, "libfg_hbm_roof.so")
+
+
+def build_roof(verbose: bool = True) -> str:
+    """The measurement kernels of bench.py's HBM-roof mode (their own
+    library; the product never loads it)."""
+    tmp = ROOF_LIB + ".tmp"
+    cmd = [HIPCC, *COMMON, *DEVICE, "-shared", "-x", "hip", ROOF_SRC, "-o", tmp]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {ROOF_SRC}:\n{' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, ROOF_LIB)
+    if verbose:
+        print(f"built {ROOF_LIB}")
+    return ROOF_LIB
+
+
 if __name__ == "__main__":
     build()
+    build_roof()
