@@ -137,6 +137,13 @@ int gemm16_dw_dx_dispatches(fg_ctx *ctx, int M1, int N1, int K1, const void *A1,
 uint64_t adam_dev_state_bytes();
 int mt_adam_dev(fg_ctx *ctx, fg_mt *mt, float lr, float b1, float b2, float eps, void *d_state,
                 int zero_grad);
+// The two halves of mt_adam_dev, for updates split over several launches
+// (and streams) within one step: one advance, then any number of updates.
+// max_blocks (0: one workgroup per chunk) caps the grid; each workgroup then
+// walks several chunks.
+int adam_dev_advance(fg_ctx *ctx, float lr, float b1, float b2, void *d_state);
+int mt_adam_dev_update(fg_mt *mt, hipStream_t stream, float b1, float b2, float eps,
+                       const void *d_state, int zero_grad, uint32_t max_blocks);
 
 // fg_softmax_ce with one more output: probs[r][c] = softmax(x_r)[c] (ld
 // ldp, element type dtype; NULL: none), so a fused loss launch can also

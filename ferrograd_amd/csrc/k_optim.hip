@@ -149,11 +149,12 @@ __global__ void adam_advance_kernel(AdamDevState *st, double lr, double b1, doub
     st->inv_sqrt_bc2 = (float)(1.0 / sqrt(bc2));
 }
 
-__global__ __launch_bounds__(kThreads) void adam_mt_dev_kernel(
-    const MTTensor *__restrict__ tensors, const MTChunk *__restrict__ chunks, float b1,
-    float b2, float eps, const AdamDevState *__restrict__ st, int zero_grad, int vec) {
-    const float step_size = st->step_size, inv_sqrt_bc2 = st->inv_sqrt_bc2;
-    const MTChunk c = chunks[blockIdx.x];
+// One chunk of the multi-tensor Adam update with the step's scalars.
+__device__ __forceinline__ void adam_dev_chunk(const MTTensor *__restrict__ tensors,
+                                               const MTChunk *__restrict__ chunks, uint32_t ci,
+                                               float b1, float b2, float eps, float step_size,
+                                               float inv_sqrt_bc2, int zero_grad, int vec) {
+    const MTChunk c = chunks[ci];
     const MTTensor t = tensors[c.tensor];
     const uint64_t end = (c.start + kChunk < t.n) ? c.start + kChunk : t.n;
     if (t.dtype != fg::kF32) {
@@ -214,6 +215,17 @@ __global__ __launch_bounds__(kThreads) void adam_mt_dev_kernel(
     }
 }
 
+
+// Workgroup w updates chunks w, w + gridDim.x, ...: one chunk each when the
+// grid covers the chunk table (a step's single update), several when a
+// smaller grid trickles an update beside other kernels.
+__global__ __launch_bounds__(kThreads) void adam_mt_dev_kernel(
+    const MTTensor *__restrict__ tensors, const MTChunk *__restrict__ chunks, uint32_t nchunks,
+    float b1, float b2, float eps, const AdamDevState *__restrict__ st, int zero_grad, int vec) {
+    const float step_size = st->step_size, inv_sqrt_bc2 = st->inv_sqrt_bc2;
+    for (uint32_t ci = blockIdx.x; ci < nchunks; ci += gridDim.x)
+        adam_dev_chunk(tensors, chunks, ci, b1, b2, eps, step_size, inv_sqrt_bc2, zero_grad, vec);
+}
 // basic_optim.rs:3-31: scaled = g*lr ; w = w - scaled ; g = 0 (fg_optim.h).
 __global__ __launch_bounds__(kThreads) void sgd_mt_kernel(const MTTensor *__restrict__ tensors,
                                                           const MTChunk *__restrict__ chunks,
@@ -326,19 +338,36 @@ namespace fg {
 uint64_t adam_dev_state_bytes() { return sizeof(AdamDevState); }
 
 // Advance the device step counter at d_state (zero-initialised
-// AdamDevState) and apply one Adam update with the derived scalars.
-int mt_adam_dev(fg_ctx *ctx, fg_mt *mt, float lr, float b1, float b2, float eps, void *d_state,
-                int zero_grad) {
-    FG_REQUIRE(ctx && mt && d_state, FG_ERR_INVALID_ARGUMENT, "mt_adam_dev: NULL argument");
-    FG_REQUIRE(mt->has_state, FG_ERR_INVALID_ARGUMENT,
-               "mt_adam_dev: tensor list was created without m/v state");
+// AdamDevState) and derive the step's bias-correction scalars.
+int adam_dev_advance(fg_ctx *ctx, float lr, float b1, float b2, void *d_state) {
+    FG_REQUIRE(ctx && d_state, FG_ERR_INVALID_ARGUMENT, "adam_dev_advance: NULL argument");
     AdamDevState *st = reinterpret_cast<AdamDevState *>(d_state);
     adam_advance_kernel<<<1, 64, 0, ctx->stream>>>(st, (double)lr, (double)b1, (double)b2);
     FG_LAUNCH_CHECK("adam_advance_kernel");
-    adam_mt_dev_kernel<<<mt->nchunks, kThreads, 0, ctx->stream>>>(
-        mt->d_tensors, mt->d_chunks, b1, b2, eps, st, zero_grad, mt->vec);
+    return FG_OK;
+}
+
+// One Adam update of mt's tensors on `stream` with the scalars at d_state
+// (advanced by adam_dev_advance before this runs).
+int mt_adam_dev_update(fg_mt *mt, hipStream_t stream, float b1, float b2, float eps,
+                       const void *d_state, int zero_grad, uint32_t max_blocks) {
+    FG_REQUIRE(mt && d_state, FG_ERR_INVALID_ARGUMENT, "mt_adam_dev_update: NULL argument");
+    FG_REQUIRE(mt->has_state, FG_ERR_INVALID_ARGUMENT,
+               "mt_adam_dev_update: tensor list was created without m/v state");
+    const uint32_t blocks = max_blocks && max_blocks < mt->nchunks ? max_blocks : mt->nchunks;
+    adam_mt_dev_kernel<<<blocks, kThreads, 0, stream>>>(
+        mt->d_tensors, mt->d_chunks, mt->nchunks, b1, b2, eps,
+        reinterpret_cast<const AdamDevState *>(d_state), zero_grad, mt->vec);
     FG_LAUNCH_CHECK("adam_mt_dev_kernel");
     return FG_OK;
+}
+
+// Advance the device step counter and apply one Adam update.
+int mt_adam_dev(fg_ctx *ctx, fg_mt *mt, float lr, float b1, float b2, float eps, void *d_state,
+                int zero_grad) {
+    FG_REQUIRE(ctx && mt && d_state, FG_ERR_INVALID_ARGUMENT, "mt_adam_dev: NULL argument");
+    if (int rc = adam_dev_advance(ctx, lr, b1, b2, d_state)) return rc;
+    return mt_adam_dev_update(mt, ctx->stream, b1, b2, eps, d_state, zero_grad, 0);
 }
 
 }  // namespace fg
