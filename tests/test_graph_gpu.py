@@ -774,6 +774,93 @@ def test_captured_step_survives_workspace_growth(ctx):
         own.close()
 
 
+# Shapes for the fused paths of captured SGD steps beyond c1's own: heads of
+# at most 16 classes on hidden widths of at most 256 (the skinny head GEMM
+# that finishes the loss and computes the head's data gradient, and the
+# triple launch that follows), first layers long enough in K to split
+# (the chained forward and the summing pass held for the SGD launch), odd
+# batches, widths off multiples of 16.
+FUSED_SGD_SHAPES = [([300, 128, 16], 32, "relu"), ([1000, 256, 3], 100, "gelu"),
+                    ([640, 200, 7], 48, "relu"), ([784, 256, 10], 128, "gelu"),
+                    ([96, 64, 12], 17, "relu")]
+
+
+@pytest.mark.parametrize("dims,B,act", FUSED_SGD_SHAPES,
+                         ids=["-".join(map(str, d)) + f"-b{b}" for d, b, _ in FUSED_SGD_SHAPES])
+def test_captured_sgd_fused_paths_at_other_shapes(ctx, dims, B, act):
+    """Captured SGD steps of two-layer MLPs at shapes other than c1's: three
+    replays of the captured step against three eager steps of an identical
+    plan, bit for bit (parameters, mean loss, probabilities, every gradient),
+    and the first step against the oracle (loss within 1e-5, gradients
+    within 1e-5 sqrt(K))."""
+    import ferrograd_amd as fa
+    from ferrograd_amd._lib import call
+    G = api()
+    print(f"fused SGD paths: dims {dims} batch {B} {act}", flush=True)
+    runs, plans = [], []
+    X = fa.rng_uniform(5, 0, (B, dims[0]))
+    y = fa.rng_int(5, 1, (B,), dims[-1])
+    Ws = [fa.rng_uniform(5, 10 + l, (dims[l], dims[l + 1]), -math.sqrt(6 / dims[l]),
+                         math.sqrt(6 / dims[l])) for l in range(2)]
+    bs = [fa.rng_uniform(5, 20 + l, (dims[l + 1],), -0.1, 0.1) for l in range(2)]
+    graphs = []
+    try:
+        for captured in (False, True):
+            graph, meta, mb, st = build_mlp(ctx, dims, B, act, G.Optim.sgd())
+            ins = [ctx.init_tensor_f32(X.shape, X)]
+            for W, b in zip(Ws, bs):
+                ins += [ctx.init_tensor_f32(W.shape, W), ctx.init_tensor_f32(b.shape, b)]
+            tgt = ctx.new_onehot_init(y)
+            sch = ctx.schedule(graph.lower(meta), [G.f32_bits(0.01)] + mb[1:], ins, st)
+            plans.append((sch, st, ins, tgt))
+            graphs.append(graph)
+        desc = plans[1][1].plan.describe()
+        fused = [k for k in ("the head GEMM finishes the loss", "the head's data gradient",
+                             "shares the SGD launch", "summed by the next launch")
+                 if k in desc]
+        print("  fused paths taken: " + (", ".join(fused) or "none"), flush=True)
+        sch, st, ins, tgt = plans[1]
+        call("fg_plan_bind_target", sch.plan.handle, tgt.data_ptr(), tgt.nbytes)
+        call("fg_plan_capture_step", sch.plan.handle)
+        first = None  # the eager plan's first-step gradients, before SGD zeroes them
+        for captured, (sch, st, ins, tgt) in zip((False, True), plans):
+            hist = []
+            for step in range(3):
+                if captured:
+                    call("fg_plan_launch_step", sch.plan.handle)
+                else:
+                    ctx.dispatch_forward(sch)
+                    ctx.dispatch_loss(sch, tgt)
+                    ctx.dispatch_backward(sch)
+                    if step == 0:
+                        ctx.sync()
+                        first = {t.node: ctx.download(t).copy() for t in st.grad_tensors}
+                    ctx.dispatch_optim(sch)
+                ctx.sync()
+                hist.append([ctx.download(t).copy() for t in ins[1:]] +
+                            [ctx.download(st.mean_loss).copy(),
+                             ctx.download(st.forward_out).copy()] +
+                            [ctx.download(t).copy() for t in st.grad_tensors])
+            runs.append(hist)
+        for step, (a, b) in enumerate(zip(*runs)):
+            for k, (x, y2) in enumerate(zip(a, b)):
+                assert np.array_equal(x, y2), (step, k)
+        # The first step against the oracle: loss, probabilities, and every
+        # gradient (dX of the data input included).
+        mean, _, dW, db, dX, probs = oracle_mlp_step(X, Ws, bs, y.astype(np.uint32),
+                                                     O.ACT_RELU if act == "relu" else O.ACT_GELU)
+        assert abs(float(runs[0][0][4][0]) - mean) < 1e-5 * max(1.0, abs(mean))
+        assert normwise_rel(runs[0][0][5].reshape(probs.shape), probs) < 1e-5
+        in_nodes = [i for i, nd in enumerate(graphs[0].nodes) if nd.op == 0]
+        exp = [dX] + [v for pair in zip(dW, db) for v in pair]
+        tol = 1e-5 * math.sqrt(max(dims[0], dims[1], B))
+        for node, ref in zip(in_nodes, exp):
+            assert normwise_rel(first[node].reshape(ref.shape), ref) < tol, node
+    finally:
+        for _, st, _, _ in plans:
+            st.plan.close()
+
+
 @pytest.mark.parametrize("act", ["relu", "gelu"])
 @pytest.mark.parametrize("seeded", [True, False], ids=["seed", "mse"])
 def test_linear_root_activation_backward(ctx, act, seeded):
