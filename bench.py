@@ -267,11 +267,12 @@ def gemm_components(ctx, reps: int, want_host: bool = False):
 
 
 def c5_gemm_kernels(ctx):
-    """The hidden-layer GEMMs of the c5 step on its shapes and epilogues
-    (random operands, library generator): key -> (description, launch
-    closure, algorithmic bytes per launch, GEMMs per launch, launches per
-    step).  The step runs the forward and the dW + dX pair
-    (fg_matmul_bwd_f32: one launch); dX and dW are also timed alone."""
+    """The GEMMs of the c5 step on its shapes and epilogues (random
+    operands, library generator): key -> (description, launch closure,
+    algorithmic bytes per launch, flops per launch, launches per step).  A
+    hidden layer runs the forward and the dW + dX pair (fg_matmul_bwd_f32:
+    one launch); dX and dW are also timed alone.  The first layer and the
+    head complete the step's 24 GEMMs."""
     import torch
 
     import ferrograd_amd as fa
@@ -284,42 +285,69 @@ def c5_gemm_kernels(ctx):
         ctx.rng_normal(4, 500 + i, 0.0, 1.0, t, t.numel())
     H, Z, dX, dW = (torch.empty(shape, device="cuda") for shape in
                     ((M, N), (M, N), (M, K), (K, N)))
+    F, C = 1024, 1000  # the first layer's input width, the head's classes
+    X0, W0, W7, b7, D7 = (torch.empty(shape, device="cuda") for shape in
+                          ((M, F), (F, N), (K, C), (C,), (M, C)))
+    for i, t in enumerate((X0, W0, W7, b7, D7)):
+        ctx.rng_normal(4, 520 + i, 0.0, 1.0, t, t.numel())
+    L7, dW7, db7, dX7, dX0, dW0 = (torch.empty(shape, device="cuda") for shape in
+                                   ((M, C), (K, C), (C,), (M, K), (M, F), (F, N)))
     dx_bytes = 4 * (M * N + K * N + 2 * M * K)
     dw_bytes = 4 * (M * K + M * N + K * N + N)
     return {
         "gemm_c5_fwd": ("NN 2048x4096x4096 + bias + GELU, Z stored (forward)",
                         lambda: ctx.gemm(fa.NN, M, N, K, X, K, W, N, H, N, bias=b,
                                          act=fa.ACT_GELU, Z=Z, ldz=N),
-                        4 * (M * K + K * N + N + 2 * M * N), 1, 6),
+                        4 * (M * K + K * N + N + 2 * M * N), 2 * M * N * K, 6),
         "gemm_c5_bwd_pair": ("TN 4096x4096x2048 + fused dbias and NT 2048x4096x4096 * GELU'(Z) "
                              "in one launch (dW, db and dX of a hidden layer)",
                              lambda: ctx.matmul_bwd(M, N, K, X, K, W, N, dZ, N, dX, K, dW, N,
                                                     dbias=db, act=fa.ACT_GELU, Zs=Zs, ldzs=K),
                              # dZ is read by both GEMMs
-                             dx_bytes + dw_bytes, 2, 6),
+                             dx_bytes + dw_bytes, 4 * M * N * K, 6),
         "gemm_c5_dx": ("NT 2048x4096x4096 * GELU'(Z) (dX of a hidden layer, alone)",
                        lambda: ctx.gemm_bwd(fa.NT, M, K, N, dZ, N, W, N, dX, K,
                                             act=fa.ACT_GELU, Zs=Zs, ldzs=K),
-                       dx_bytes, 1, 0),
+                       dx_bytes, 2 * M * N * K, 0),
         "gemm_c5_dw": ("TN 4096x4096x2048 + fused dbias (dW, db of a hidden layer, alone)",
                        lambda: ctx.gemm_dw(K, N, M, X, K, dZ, N, dW, N, colsum=db),
-                       dw_bytes, 1, 0),
+                       dw_bytes, 2 * M * N * K, 0),
+        # The step's other GEMMs: the 1024-wide first layer and the 1000-wide head.
+        "gemm_c5_fwd_first": ("NN 2048x4096x1024 + bias + GELU, Z stored (first layer)",
+                              lambda: ctx.gemm(fa.NN, M, N, F, X0, F, W0, N, H, N, bias=b,
+                                               act=fa.ACT_GELU, Z=Z, ldz=N),
+                              4 * (M * F + F * N + N + 2 * M * N), 2 * M * N * F, 1),
+        "gemm_c5_fwd_head": ("NN 2048x1000x4096 + bias (head)",
+                             lambda: ctx.gemm(fa.NN, M, C, K, X, K, W7, C, L7, C, bias=b7),
+                             4 * (M * K + K * C + C + M * C), 2 * M * C * K, 1),
+        "gemm_c5_dw_head": ("TN 4096x1000x2048 + fused dbias (head dW, db)",
+                            lambda: ctx.gemm_dw(K, C, M, X, K, D7, C, dW7, C, colsum=db7),
+                            4 * (M * K + M * C + K * C + C), 2 * M * C * K, 1),
+        "gemm_c5_dx_head": ("NT 2048x4096x1000 * GELU'(Z) (head dX, K tail)",
+                            lambda: ctx.gemm_bwd(fa.NT, M, K, C, D7, C, W7, C, dX7, K,
+                                                 act=fa.ACT_GELU, Zs=Zs, ldzs=K),
+                            4 * (M * C + K * C + 2 * M * K), 2 * M * C * K, 1),
+        "gemm_c5_pair_first": ("TN 1024x4096x2048 + fused dbias and NT 2048x1024x4096 in one "
+                               "launch (first layer's dW, db and the data input's dX)",
+                               lambda: ctx.matmul_bwd(M, N, F, X0, F, W0, N, dZ, N, dX0, F, dW0,
+                                                      N, dbias=db),
+                               4 * (2 * M * N + F * N + M * F) + 4 * (M * F + M * N + F * N + N),
+                               4 * M * N * F, 1),
     }
 
 
 def c5_gemm_shares(ctx, reps: int, step_ms: float):
-    """The hidden-layer GEMMs, 18 of the c5 step's 24 GEMMs, timed with HIP
-    events on the step's own shapes and epilogues: the forward NN
-    2048x4096x4096 + bias + GELU (+Z), 6 launches per step, and the
-    backward pair (dW TN 4096x4096x2048 with the fused dbias beside dX NT
-    2048x4096x4096 with the GELU derivative, one launch), 6 per step;
-    share = launches per step * time / step time.  dX and dW alone (share
-    None: the step does not launch them alone) for comparison."""
-    gemm = 2.0 * 2048 * 4096 * 4096
+    """The c5 step's GEMMs timed with HIP events on the step's own shapes
+    and epilogues: the hidden layers' forward NN 2048x4096x4096 + bias +
+    GELU (+Z), 6 launches per step, and backward pair (dW TN
+    4096x4096x2048 with the fused dbias beside dX NT 2048x4096x4096 with the
+    GELU derivative, one launch), 6 per step; the first layer's forward and
+    pair and the head's forward, dW and dX, one each; share = launches per
+    step * time / step time.  Hidden dX and dW alone (share None: the step
+    does not launch them alone) for comparison."""
     out = {}
-    for key, (what, fn, nbytes, gemms, per_step) in c5_gemm_kernels(ctx).items():
+    for key, (what, fn, nbytes, flops, per_step) in c5_gemm_kernels(ctx).items():
         t = event_time_ms(fn, reps, warm_ms=200)
-        flops = gemms * gemm
         out[key] = {"what": what, "ms": t, "tflops": flops / t / 1e9,
                     "frac": flops / t / 1e9 / PEAK_FP32_MFMA_TFLOPS, "per_step": per_step,
                     "step_share": per_step * t / step_ms if per_step else None,
@@ -778,6 +806,11 @@ ONLY = {
     "gemm_c5_bwd_pair": only_c5_gemm("gemm_c5_bwd_pair"),
     "gemm_c5_dx": only_c5_gemm("gemm_c5_dx"),
     "gemm_c5_dw": only_c5_gemm("gemm_c5_dw"),
+    "gemm_c5_fwd_first": only_c5_gemm("gemm_c5_fwd_first"),
+    "gemm_c5_fwd_head": only_c5_gemm("gemm_c5_fwd_head"),
+    "gemm_c5_dw_head": only_c5_gemm("gemm_c5_dw_head"),
+    "gemm_c5_dx_head": only_c5_gemm("gemm_c5_dx_head"),
+    "gemm_c5_pair_first": only_c5_gemm("gemm_c5_pair_first"),
     "softmax_ce_c3": only_softmax_ce_c3,
     "adam_c4": only_adam_c4,
     "copy_256mib": only_copy_256mib,
