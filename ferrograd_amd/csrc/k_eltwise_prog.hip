@@ -110,34 +110,38 @@ __device__ __forceinline__ f32x4 quad_map(f32x4 x, F f) {
     return r;
 }
 
-// The register file holds kEltRegs = R * U quads per thread: R program
-// registers for each of the U quads the thread runs the program over in one
-// pass.  Slot u * R + r holds register r of quad u, in four arrays (one per
-// element of a quad) of kEltRegs floats, all indexed by the same uniform
-// number.  Arrays of 16 are indexed through the GPU's relative register
-// addressing (one index setup serves every quad, since quad u only adds the
-// constant u * R), where smaller arrays turn into select chains.
+// The register file holds R * U <= kEltRegs quads per thread: R program
+// registers (a power of two) for each of the U quads the thread runs the
+// program over in one pass.  Slot u * R + r holds register r of quad u, in
+// four arrays (one per element of a quad) of R * U floats, all indexed by
+// the same uniform number: the compiler reads arrays of 12 or more through
+// the GPU's relative register addressing (one index setup serves every quad,
+// since quad u only adds the constant u * R), and smaller ones through
+// select chains.
 //
 // Every lane runs the same instruction stream, so decoding an instruction,
 // branching on its op and reading its pointers is scalar work done once per
 // wave and pass; the scalar unit is shared by the CU's waves and bounds
-// short programs.  U quads per pass spread that work over 4 * U elements per
-// lane: launch_eltwise allocates the program's registers by liveness and
-// takes the smallest file (R = 4, 8 or 16) that holds them.  Thread t of a
-// workgroup takes quads base + u * kThreads + t (u < U), so each load and
-// store of a pass stays coalesced.  The pass loop is uniform: a lane past the
-// end takes an empty quad (loads give 0, stores skip), so the interpreter
-// runs outside any divergent region.
+// short programs on one quad per thread.  U quads per pass spread that work
+// over 4 * U elements per lane, while the register file and the U quads'
+// operands set how many waves fit a SIMD, and with them the bytes in flight:
+// launch_eltwise allocates the program's registers by liveness and picks the
+// file from a measured sweep.  Thread t of a workgroup takes quads
+// base + u * kThreads + t (u < U), so each load and store of a pass stays
+// coalesced.  The pass loop is uniform: a lane past the end takes an empty
+// quad (loads give 0, stores skip), so the interpreter runs outside any
+// divergent region.
 template <int R, int U, bool NT>
 __global__ __launch_bounds__(kThreads) void eltwise_prog_kernel(const EltProgram p) {
-    static_assert(R * U == kEltRegs, "the file holds kEltRegs quads per thread");
+    static_assert(R * U <= kEltRegs && (R & (R - 1)) == 0, "the file holds R x U quads per thread");
     static_assert(kEltPre <= R, "prefetched sources occupy registers 0 .. n_pre-1");
+    constexpr int kFile = R * U;
     const uint64_t nq = (p.n + 3) / 4;
     const uint64_t span = (uint64_t)kThreads * U;
     const uint64_t stride = (uint64_t)gridDim.x * span;
-    float f0[kEltRegs], f1[kEltRegs], f2[kEltRegs], f3[kEltRegs];
+    float f0[kFile], f1[kFile], f2[kFile], f3[kFile];
 #pragma unroll
-    for (int k = 0; k < kEltRegs; ++k) f0[k] = f1[k] = f2[k] = f3[k] = 0.0f;
+    for (int k = 0; k < kFile; ++k) f0[k] = f1[k] = f2[k] = f3[k] = 0.0f;
     // u is a compile-time constant at every call (unrolled loops), r a
     // uniform run-time register number kept inside the file by the mask.
     auto get = [&](int u, int r) {
@@ -336,12 +340,19 @@ int launch_eltwise(fg_ctx *ctx, const EltProgram &p0) {
     // Streaming accesses once each tensor is well past the L2 caches (4 MiB
     // per XCD), so small programs keep their outputs cached for the next
     // launch.
+    // Register files, from a measured sweep on tanh(a*b + c) over 8192^2
+    // (3 registers): 4 registers x 3 quads 5.65 TB/s (127 VGPRs, 4 waves per
+    // SIMD), 8 x 2 5.18 (125 VGPRs), 4 x 4 4.84 (163 VGPRs, 3 waves), 16 x 1
+    // 4.32 (scalar-bound), 4 x 2 4.65-4.71 (an 8-entry file is indexed
+    // through select chains).  Streaming accesses once each tensor is well
+    // past the L2 caches (4 MiB per XCD), so small programs keep their outputs
+    // cached for the next launch.
     if (p.n >= (uint64_t(1) << 22)) {
-        if (regs <= 4) return launch_file<4, 4, true>(ctx, p);
+        if (regs <= 4) return launch_file<4, 3, true>(ctx, p);
         if (regs <= 8) return launch_file<8, 2, true>(ctx, p);
         return launch_file<16, 1, true>(ctx, p);
     }
-    if (regs <= 4) return launch_file<4, 4, false>(ctx, p);
+    if (regs <= 4) return launch_file<4, 3, false>(ctx, p);
     if (regs <= 8) return launch_file<8, 2, false>(ctx, p);
     return launch_file<16, 1, false>(ctx, p);
 }

@@ -1004,18 +1004,20 @@ def test_unary_forward_backward(ctx, op):
     assert normwise_rel(ctx.download(st.grad_tensors[0]).reshape(R, C), exp) < 1e-5
 
 
-@pytest.mark.parametrize("R,C", [(37, 1024), (37, 1025), (3, 341), (5, 4096), (5, 4097),
-                                 (3, 1365), (1031, 4099)],
-                         ids=["1k-whole", "1k-partial", "1k-one-partial", "4k-whole",
-                              "4k-partial", "4k-one-partial", "streaming-partial"])
+@pytest.mark.parametrize("R,C", [(37, 1024), (37, 1025), (3, 341), (6, 2048), (6, 2049),
+                                 (3, 1023), (5, 4097), (1031, 4099), (1024, 4096)],
+                         ids=["1k-whole", "1k-partial", "1k-one-partial", "3k-whole",
+                              "3k-partial", "3k-one-partial", "2k-and-4k-partial",
+                              "streaming-partial", "streaming-whole"])
 def test_eltwise_program_whole_and_partial_blocks(ctx, R, C):
     """tanh(x * y + z) and its gradients through elementwise programs at
-    sizes on either side of a workgroup's pass (256 threads x U quads:
-    1024 elements for the 16-register file, 4096 for the 4-register file the
-    forward program takes): whole workgroups, a partial last workgroup with
-    a partial last quad, and one partial workgroup; 1031 x 4099 (4.2 M
-    elements, a partial last quad) takes the streaming loads and stores of
-    large tensors.  Forward and every gradient against float64 numpy."""
+    sizes on either side of a workgroup's pass (256 threads x U quads: 1024
+    elements for the 16-register file, 2048 for the 8-register file, 3072
+    for the 4-register file the forward program takes): whole workgroups, a
+    partial last workgroup with a partial last quad, and one partial
+    workgroup; 1031 x 4099 (4.2 M elements, a partial last quad) and 1024 x
+    4096 take the streaming loads and stores of large tensors.  Forward and
+    every gradient against float64 numpy."""
     G = api()
     graph, meta = new_graph(G.MEAN_SQUARED_ERROR)
     r, c = meta.new_field(), meta.new_field()
