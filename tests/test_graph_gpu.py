@@ -1047,6 +1047,46 @@ def test_eltwise_program_whole_and_partial_blocks(ctx, R, C):
     assert normwise_rel(g[2].reshape(R, C), du) < 1e-5
 
 
+@pytest.mark.parametrize("R,C", [(9, 301), (1100, 4097)], ids=["small", "streaming"])
+def test_eltwise_program_wide_expression(ctx, R, C):
+    """((a*b + c*d) * (e - f)) / (g*g + 1) with seven inputs: forward and
+    every gradient against float64 numpy.  Its programs hold more values at
+    once than the tanh chain (more sources than are prefetched, the backward
+    reuses many intermediates), so they run on the larger register files;
+    1100 x 4097 takes the streaming accesses and a partial last quad."""
+    G = api()
+    graph, meta = new_graph(G.MEAN_SQUARED_ERROR)
+    r, c = meta.new_field(), meta.new_field()
+    with graph.define_ops() as ops:
+        a, b, cc, d, e, f, g = (ops.input([r, c]) for _ in range(7))
+        num = ops.mul(ops.add(ops.mul(a, b), ops.mul(cc, d)), ops.sub(e, f))
+        one = ops.constant_f32(1.0)
+        ops.div(num, ops.add(ops.mul(g, g), one))
+    mb = [G.f32_bits(1e-3), R, C]
+    st = ctx.alloc_tensors(graph, graph.compute_saved_nodes(), mb)
+    rng = np.random.default_rng(R + C)
+    V = [rng.standard_normal((R, C)).astype(f32) for _ in range(7)]
+    ins = [ctx.init_tensor_f32([R, C], v) for v in V]
+    sch = ctx.schedule(graph.lower(meta), mb, ins, st)
+    seed = rng.standard_normal((R, C)).astype(f32)
+    ctx.upload(st.seed, seed)
+    ctx.dispatch_forward(sch)
+    ctx.dispatch_backward(sch)
+    ctx.sync()
+    A, B, Cc, D, E, F, Gv, S = (v.astype(np.float64) for v in V + [seed])
+    p = A * B + Cc * D
+    q = E - F
+    den = Gv * Gv + 1.0
+    y = p * q / den
+    assert normwise_rel(ctx.download(st.forward_out).reshape(R, C), y) < 1e-6
+    g = {t.node: ctx.download(t).reshape(R, C) for t in st.grad_tensors}
+    u = S / den
+    exp = [u * q * B, u * q * A, u * q * D, u * q * Cc, u * p, -u * p,
+           -S * p * q / (den * den) * 2.0 * Gv]
+    for k, ref in enumerate(exp):
+        assert normwise_rel(g[k], ref) < 1e-5, k
+
+
 @pytest.mark.parametrize("C", [300, 301])
 def test_binary_broadcast_and_div_backward(ctx, C):
     """(a / b) * c - bias (row-broadcast sub): forward and every gradient
