@@ -1510,23 +1510,45 @@ int run_bwd_adam_overlapped(fg_plan &P, const std::vector<Launch> &bwd) {
     if (int rc = fg::adam_dev_advance(ctx, P.lr, P.b1, P.b2, P.ptr(P.adam_slot))) return rc;
     const size_t G = P.mt_groups.size();
     bool forked = false;  // the second stream has joined the capture
-    auto fork = [&](size_t g) -> int {
+    // The main stream records group g's event once it has run the launch
+    // group that releases g; the update itself is issued one launch group
+    // later, after the main stream's next launch.  The dependencies are the
+    // same either way, but a replayed graph runs a node's first-created child
+    // on the node's hardware queue: created first, the next GEMM keeps the
+    // backward on one queue, and the updates branch off onto another (created
+    // first, an update took the queue and a later GEMM queued behind one,
+    // ~120 us per c5 step).
+    std::vector<size_t> pending;
+    auto mark = [&](size_t g) -> int {
         FG_HIP(hipEventRecord(P.events[g], ctx->stream));
-        FG_HIP(hipStreamWaitEvent(P.side, P.events[g], 0));
-        forked = true;
-        return fg::mt_adam_dev_update(P.mt_groups[g], P.side, P.b1, P.b2, P.eps,
-                                      P.ptr(P.adam_slot), 0, kSideAdamBlocks);
+        pending.push_back(g);
+        return FG_OK;
+    };
+    auto issue = [&](bool last) -> int {
+        for (size_t g : pending) {
+            FG_HIP(hipStreamWaitEvent(P.side, P.events[g], 0));
+            forked = true;
+            // Nothing runs beside the backward's last updates: a full grid.
+            if (int r = fg::mt_adam_dev_update(P.mt_groups[g], P.side, P.b1, P.b2, P.eps,
+                                               P.ptr(P.adam_slot), 0,
+                                               last ? 0u : kSideAdamBlocks))
+                return r;
+        }
+        pending.clear();
+        return FG_OK;
     };
     int rc = FG_OK;
     for (size_t g = 0; g < G && rc == FG_OK; ++g)  // inputs the backward never touches
-        if (P.mt_group_after[g] < 0) rc = fork(g);
+        if (P.mt_group_after[g] < 0) rc = mark(g);
     const std::function<int(size_t)> after = [&](size_t last) -> int {
+        if (int r = issue(false)) return r;
         for (size_t g = 0; g < G; ++g)
             if (P.mt_group_after[g] == (int)last)
-                if (int r = fork(g)) return r;
+                if (int r = mark(g)) return r;
         return FG_OK;
     };
     if (rc == FG_OK) rc = run(P, bwd, false, false, nullptr, nullptr, nullptr, -1, &after);
+    if (rc == FG_OK) rc = issue(true);
     // Rejoin whatever happened, so the capture can end.
     if (forked) {
         const hipError_t e1 = hipEventRecord(P.events[G], P.side);
