@@ -427,15 +427,15 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm16_mfma(Args p) {
 // chunk of wave load li landing at element 512 li + 8 l of the operand's
 // stage area; the source of each chunk is chosen so that the stage ends up
 // in the swizzled layout below.  Two ways to move the chunks:
-//  * staged (every tile but 256x256 with 4 waves or BK 64): global loads
-//    into registers, two register sets alternating by tile parity, written
-//    to a two-stage LDS ring by ds_write_b128 one tile later;
-//  * direct (256x256 with 4 waves or BK 64, whose accumulators leave no room
-//    for two register sets): global_load_lds_dwordx4 straight into an LDS
-//    ring of up to four stages.  The compiler cannot tell a transposing LDS
-//    read from the direct loads in flight and waits for all of them before
-//    each such read, so the tile rule keeps these tiles to layouts without a
-//    row-contiguous operand.
+//  * staged (BK 32 tiles but 256x256 with 4 waves): global loads into
+//    registers, two register sets alternating by tile parity, written to a
+//    two-stage LDS ring by ds_write_b128 one tile later;
+//  * direct (BK 64 tiles, and 256x256 with 4 waves, whose accumulators leave
+//    no room for two register sets): global_load_lds_dwordx4 (inline
+//    assembly, lds_dma16) straight into an LDS ring of up to four stages,
+//    as many as fit -- three for 256x128 tiles, whose two tiles in flight
+//    ran their NT data gradient 917-922 -> 944-948 TF at 2048x4096x4096
+//    (bf16 c5 step 2.066-2.070 -> 2.037-2.042 ms).
 // A BK of 32 or 64 is only 1-2 thousand MFMA cycles per SIMD, so the barrier
 // is overlapped: the last k16 step of each tile is multiplied after it, from
 // registers.  No operand is transposed on its way in:
@@ -531,16 +531,15 @@ struct ColSum16 {
 };
 
 // LDS of the pipelined kernel, in 16-bit elements: its stages (staged
-// loads -- global -> registers -> ds_write -- for every tile but 256x256
-// with 4 waves (256 accumulator registers) or with BK 64 (eight 16-byte
-// loads per wave and tile, which with the 128 accumulators of 8 waves exceed
-// the registers): two; direct-to-LDS loads: up to four, as many as fit in
-// the 160 KiB of LDS) or the epilogue's fp32 staging, whichever is larger.
+// loads -- global -> registers -> ds_write -- for BK 32 tiles but 256x256
+// with 4 waves (256 accumulator registers): two; direct-to-LDS loads: up to
+// four, as many as fit in the 160 KiB of LDS) or the epilogue's fp32
+// staging, whichever is larger.
 template <int BM, int BN, int BK, int WGM, int WGN>
 struct Pipe16Lds {
     static constexpr int kNW = WGM * WGN;
     static constexpr int kStageSz = BM * BK + BN * BK;  // elements
-    static constexpr bool kStaged = !(BM == 256 && BN == 256 && (kNW == 4 || BK == 64));
+    static constexpr bool kStaged = BK == 32 && !(BM == 256 && BN == 256 && kNW == 4);
     static constexpr int kStages = kStaged                             ? 2
                                    : 4 * kStageSz * 2 <= 160 * 1024   ? 4
                                    : 3 * kStageSz * 2 <= 160 * 1024 ? 3
@@ -845,7 +844,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm16_pipe(Args p) {
 
 // A large layer's weight gradient (TN, 256x256 tiles, 8 waves, BK 64, direct
 // loads: workgroups below n1) and data gradient (NT, 256x128 tiles, 8 waves, BK
-// 64: the rest) in one launch, each body exactly as its own kernel, both on
+// 64, direct loads: the rest) in one launch, each body exactly as its own kernel, both on
 // one LDS buffer of the larger size: the dW tiles' output writes drain while
 // dX tiles compute, where two launches would leave the CUs idle through them.
 constexpr int kPair16Lds = Pipe16Lds<256, 256, 64, 2, 4>::elems > Pipe16Lds<256, 128, 64, 4, 2>::elems
