@@ -113,6 +113,10 @@ pub const FG_BPAT_V1M: c_int = 2;
 pub const FG_BPAT_V2_F16: c_int = 3;
 pub const FG_BPAT_V2_BF16: c_int = 4;
 pub const FG_BPAT_V2_F32: c_int = 5;
+// elementwise program modes (fg_eltwise_set_mode)
+pub const FG_ELTWISE_INTERPRET: c_int = 0;
+pub const FG_ELTWISE_COMPILE_LARGE: c_int = 1;
+pub const FG_ELTWISE_COMPILE_ALL: c_int = 2;
 // fg_loss (ferrograd-nn LossType constants)
 pub const FG_LOSS_MSE: c_int = 0;
 pub const FG_LOSS_BCE: c_int = 1;
@@ -564,6 +568,12 @@ extern "C" {
         index: c_int,
         d_dst: *mut c_void,
         dtype: c_int,
+    ) -> c_int;
+    pub fn fg_eltwise_set_mode(mode: c_int, previous: *mut c_int) -> c_int;
+    pub fn fg_eltwise_stats(
+        kernels_compiled: *mut u64,
+        compiled_launches: *mut u64,
+        interpreted_launches: *mut u64,
     ) -> c_int;
     pub fn fg_graph_create(loss: c_int, optim: c_int, out: *mut *mut fg_graph) -> c_int;
     pub fn fg_graph_destroy(g: *mut fg_graph) -> c_int;

@@ -28,10 +28,12 @@ from ._lib import FgError, call, load
 NN, NT, TN = 0, 1, 2
 ACT_NONE, ACT_RELU, ACT_GELU = 0, 1, 2
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
+ELTWISE_INTERPRET, ELTWISE_COMPILE_LARGE, ELTWISE_COMPILE_ALL = 0, 1, 2
 
 __all__ = [
     "NN", "NT", "TN", "ACT_NONE", "ACT_RELU", "ACT_GELU", "FgError", "Context",
     "MultiTensor", "load", "rng_uniform", "rng_normal", "rng_int", "torch_context",
+    "eltwise_mode", "eltwise_stats",
 ]
 
 
@@ -282,3 +284,21 @@ def rng_int(seed: int, tensor_id: int, shape, bound: int) -> np.ndarray:
     out = np.empty(shape, dtype=np.uint32)
     call("fg_rng_int_host", seed, tensor_id, bound, out.ctypes.data, out.size)
     return out
+
+
+# ------------------------------------------------ compiled elementwise kernels
+def eltwise_mode(mode: int) -> int:
+    """Sets how plans run elementwise programs (ELTWISE_INTERPRET,
+    ELTWISE_COMPILE_LARGE -- the default -- or ELTWISE_COMPILE_ALL), process-wide;
+    returns the previous mode."""
+    prev = ctypes.c_int32(0)
+    call("fg_eltwise_set_mode", mode, ctypes.byref(prev))
+    return prev.value
+
+
+def eltwise_stats() -> dict:
+    """Process-wide counts: kernels compiled, launches of compiled kernels,
+    launches of the interpreter."""
+    c, j, i = ctypes.c_uint64(0), ctypes.c_uint64(0), ctypes.c_uint64(0)
+    call("fg_eltwise_stats", ctypes.byref(c), ctypes.byref(j), ctypes.byref(i))
+    return {"compiled": c.value, "compiled_launches": j.value, "interpreted_launches": i.value}

@@ -39,7 +39,13 @@ SOURCES = [
     "fg_graph.cpp",
     "fg_bpat.cpp",
     "fg_telemetry.cpp",
+    "fg_elt_jit.cpp",
 ]
+
+# Device headers that kernels compiled at run time include (fg_elt_jit.cpp):
+# their text goes into the library, written into the build folder as
+# fg_jit_headers.inc before the compile.
+JIT_HEADERS = ["fg_half.h", "fg_act.h", "fg_elt_ops.h"]
 
 # Packed-fp32 VALU instructions are disabled for all device code: some of
 # their forms have produced silent wrong results on the target machines.
@@ -69,7 +75,8 @@ EXTRA = {
 def _compile(src: str, obj_dir: str = OBJ, defines=()) -> str:
     path = os.path.join(CSRC, src)
     obj = os.path.join(obj_dir, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *COMMON, *DEVICE, *EXTRA.get(src, []), *[f"-D{d}" for d in defines]]
+    cmd = [HIPCC, *COMMON, *DEVICE, *EXTRA.get(src, []), *[f"-D{d}" for d in defines],
+           f"-I{obj_dir}"]
     if src.endswith(".hip"):
         cmd += ["-x", "hip"]
     cmd += ["-c", path, "-o", obj]
@@ -85,10 +92,30 @@ def _compile(src: str, obj_dir: str = OBJ, defines=()) -> str:
     return obj
 
 
+def write_jit_headers(obj_dir: str) -> str:
+    """fg_jit_headers.inc: {name, text} of each JIT_HEADERS file, as raw
+    string literals."""
+    out = ["struct FgJitHeader { const char *name; const char *text; };",
+           "static const FgJitHeader kJitHeaders[] = {"]
+    for name in JIT_HEADERS:
+        text = open(os.path.join(CSRC, name)).read()
+        if ")FGJITH\"" in text:
+            raise RuntimeError(f"{name} holds the raw-string delimiter")
+        out.append(f'    {{"{name}", R"FGJITH({text})FGJITH"}},')
+    out.append("};")
+    path = os.path.join(obj_dir, "fg_jit_headers.inc")
+    tmp = path + ".tmp"
+    with open(tmp, "w") as f:
+        f.write("\n".join(out) + "\n")
+    os.replace(tmp, path)
+    return path
+
+
 def build(verbose: bool = True, lib: str = LIB, obj_dir: str = OBJ, defines=()) -> str:
     """Compile all sources and link the shared library; returns its path.
     `defines` (e.g. ["FG_GEMM_BK=32"]) builds a tuning variant into `lib`."""
     os.makedirs(obj_dir, exist_ok=True)
+    write_jit_headers(obj_dir)
     jobs = min(len(SOURCES), int(os.environ.get("MAX_JOBS", "8")))
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
         objs = list(ex.map(lambda s: _compile(s, obj_dir, defines), SOURCES))
@@ -96,7 +123,7 @@ def build(verbose: bool = True, lib: str = LIB, obj_dir: str = OBJ, defines=()) 
     # -z defs: an undefined symbol (e.g. a kernel launch stub that a
     # compilation pass failed to emit) fails the link, not the first load.
     cmd = [HIPCC, "-shared", f"--offload-arch={ARCH}", "-fPIC", "-Wl,-z,defs", "-o", tmp, *objs,
-           "-lpthread"]
+           "-L/opt/rocm/lib", "-lhiprtc", "-lpthread"]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{res.stdout}\n{res.stderr}")

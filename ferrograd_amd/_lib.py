@@ -93,6 +93,8 @@ SIGNATURES = {
     "fg_adam_step_scalars": (i32, [vp, vp, f32, f32, f32, f32, f32, i32]),
     "fg_memcpy_h2d": (i32, [vp, vp, vp, u64]),
     "fg_memcpy_d2h": (i32, [vp, vp, vp, u64]),
+    "fg_eltwise_set_mode": (i32, [i32, ctypes.POINTER(i32)]),
+    "fg_eltwise_stats": (i32, [ctypes.POINTER(u64), ctypes.POINTER(u64), ctypes.POINTER(u64)]),
     "fg_graph_create": (i32, [i32, i32, pvp]),
     "fg_graph_destroy": (i32, [vp]),
     "fg_graph_new_field": (i32, [vp, ctypes.POINTER(u32)]),

@@ -17,7 +17,9 @@
 //   dominated the activation epilogues.
 #pragma once
 
+#ifndef __HIPCC_RTC__  // hipRTC declares the runtime itself
 #include <hip/hip_runtime.h>
+#endif
 
 namespace fg {
 

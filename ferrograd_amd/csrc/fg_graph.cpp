@@ -32,6 +32,7 @@
 #include <cmath>
 #include <cstring>
 #include <functional>
+#include <initializer_list>
 #include <map>
 #include <memory>
 #include <set>
@@ -1161,6 +1162,40 @@ bool head_bwd_fusable(const fg_plan &P, const std::vector<Launch> &bwd, int hc) 
     return dw0 && dx0 && pair1;
 }
 
+// The elementwise program of an LK_ELT launch with the plan's pointers.
+int elt_program(const fg_plan &P, const Launch &L, fg::EltProgram *out) {
+    fg::EltProgram &p = *out;
+    p = L.prog;
+    for (int k = 0; k < fg::kEltMaxSrc; ++k)
+        if (L.src_slot[k] != kNone) {
+            p.src[k] = (const float *)P.ptr(L.src_slot[k]);
+            FG_REQUIRE(p.src[k], FG_ERR_INVALID_ARGUMENT, "plan: unbound input or target (%s)",
+                       L.desc.c_str());
+        }
+    for (int k = 0; k < fg::kEltMaxDst; ++k)
+        if (L.dst_slot[k] != kNone) p.dst[k] = (float *)P.ptr(L.dst_slot[k]);
+    if (L.label_slot != kNone) {
+        p.labels = (const uint32_t *)P.ptr(L.label_slot);
+        FG_REQUIRE(p.labels, FG_ERR_INVALID_ARGUMENT,
+                   "dispatch_loss: no target bound (fg_plan_bind_target)");
+    }
+    return FG_OK;
+}
+
+// Compiles, ahead of a stream capture, the elementwise kernels that the
+// lists' programs will take (a capture meeting one not compiled yet would
+// run it on the interpreter).
+int prepare_elt(fg_plan &P, std::initializer_list<const std::vector<Launch> *> lists) {
+    for (const std::vector<Launch> *list : lists)
+        for (const Launch &L : *list) {
+            if (L.kind != LK_ELT) continue;
+            fg::EltProgram p;
+            if (int rc = elt_program(P, L, &p)) return rc;
+            if (int rc = fg::prepare_eltwise(&P.wctx, p)) return rc;
+        }
+    return FG_OK;
+}
+
 // defer_last: the summing launch of a split GEMM in the list's last launch
 // (or the pair or chain ending it) is held in the plan's context view for the
 // optimiser launch that follows (captured steps, run_optim).  ce_loss: the
@@ -1318,21 +1353,9 @@ int run(fg_plan &P, const std::vector<Launch> &list, bool step = false, bool def
                                        step ? P.ptr(L.sProbs) : nullptr, L.N);
                 break;
             case LK_ELT: {
-                fg::EltProgram p = L.prog;
-                for (int k = 0; k < fg::kEltMaxSrc; ++k)
-                    if (L.src_slot[k] != kNone) {
-                        p.src[k] = (const float *)P.ptr(L.src_slot[k]);
-                        FG_REQUIRE(p.src[k], FG_ERR_INVALID_ARGUMENT,
-                                   "plan: unbound input or target (%s)", L.desc.c_str());
-                    }
-                for (int k = 0; k < fg::kEltMaxDst; ++k)
-                    if (L.dst_slot[k] != kNone) p.dst[k] = (float *)P.ptr(L.dst_slot[k]);
-                if (L.label_slot != kNone) {
-                    p.labels = (const uint32_t *)P.ptr(L.label_slot);
-                    FG_REQUIRE(p.labels, FG_ERR_INVALID_ARGUMENT,
-                               "dispatch_loss: no target bound (fg_plan_bind_target)");
-                }
-                rc = fg::launch_eltwise(ctx, p);
+                fg::EltProgram p;
+                rc = elt_program(P, L, &p);
+                if (rc == FG_OK) rc = fg::launch_eltwise(ctx, p);
                 break;
             }
             case LK_FILL0:
@@ -2163,6 +2186,8 @@ FG_API int fg_plan_capture_step(fg_plan *p) {
     FG_REQUIRE(p->ptr(p->target_slot), FG_ERR_INVALID_ARGUMENT,
                "fg_plan_capture_step: no target bound");
     int rc = ensure_mt(*p);  // allocates: must precede capture
+    if (rc) return rc;
+    rc = prepare_elt(*p, {&p->fwd, &p->loss, &p->bwd_fused, &p->bwd_seed});
     if (rc) return rc;
     drop_graph(*p);
     FG_HIP(hipStreamSynchronize(p->ctx->stream));

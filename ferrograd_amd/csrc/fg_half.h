@@ -8,9 +8,13 @@
 // (fp32 carries more than twice the 11-bit / 8-bit significands plus two).
 #pragma once
 
+// hipRTC (the compiled elementwise kernels, fg_elt_jit.cpp) declares the
+// runtime and the fixed-width integer types itself.
+#ifndef __HIPCC_RTC__
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#endif
 
 namespace fg {
 

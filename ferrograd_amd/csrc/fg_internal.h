@@ -158,9 +158,19 @@ int softmax_ce_dispatches(int R, int C, bool mean);
 // skinny head GEMM can run in a captured step.
 bool softmax_ce_row16_case(int R, int C);
 
-// Elementwise program launch (k_eltwise_prog.hip).
+// Elementwise program launch (k_eltwise_prog.hip): through its compiled
+// kernel or the interpreter; prepare_eltwise compiles the kernel a launch
+// would take, ahead of a stream capture.
 struct EltProgram;
 int launch_eltwise(fg_ctx *ctx, const EltProgram &p);
+int prepare_eltwise(fg_ctx *ctx, const EltProgram &p);
+// Compiled elementwise kernels (fg_elt_jit.cpp): whether the mode selects
+// one for p; the compile / launch of a validated program (`live`: values
+// kept at once; *launched false when the interpreter is to run it); the
+// interpreter's launch count.
+bool eltwise_jit_selected(const EltProgram &p);
+int eltwise_jit(fg_ctx *ctx, const EltProgram &p, int live, bool prepare_only, bool *launched);
+void eltwise_count_interpreted();
 // Kernel dispatches of one fp32 GEMM call with these operands (2 when K is
 // split: the slices, then the summing epilogue), for plan descriptions.
 int gemm_f32_dispatches(fg_ctx *ctx, int layout, int M, int N, int K, const void *A, int lda,

@@ -6,7 +6,7 @@
 
 #include <type_traits>
 
-#include "fg_act.h"
+#include "fg_elt_ops.h"
 #include "fg_eltwise.h"
 #include "fg_half.h"
 #include "fg_internal.h"
@@ -224,19 +224,17 @@ __global__ __launch_bounds__(kThreads) void eltwise_prog_kernel(const EltProgram
 #pragma unroll
                     for (int u = 0; u < U; ++u) o[u] = -x[u];
                     break;
-                case kEltRelu: unary([](float v) { return act_fwd(kActRelu, v); }); break;
-                case kEltGelu: unary([](float v) { return act_fwd(kActGelu, v); }); break;
-                case kEltElu: unary([](float v) { return v >= 0.0f ? v : expf(v) - 1.0f; }); break;
-                case kEltTanh: unary([](float v) { return tanhf(v); }); break;
-                case kEltExp: unary([](float v) { return expf(v); }); break;
-                case kEltLog: unary([](float v) { return logf(v); }); break;
-                case kEltAbs: unary([](float v) { return fabsf(v); }); break;
-                case kEltReluD: unary([](float v) { return act_grad(kActRelu, v); }); break;
-                case kEltGeluD: unary([](float v) { return act_grad(kActGelu, v); }); break;
-                case kEltEluD: unary([](float v) { return v >= 0.0f ? 1.0f : expf(v); }); break;
-                case kEltSign:
-                    unary([](float v) { return v > 0.0f ? 1.0f : (v < 0.0f ? -1.0f : 0.0f); });
-                    break;
+                case kEltRelu: unary([](float v) { return elt_relu(v); }); break;
+                case kEltGelu: unary([](float v) { return elt_gelu(v); }); break;
+                case kEltElu: unary([](float v) { return elt_elu(v); }); break;
+                case kEltTanh: unary([](float v) { return elt_tanh(v); }); break;
+                case kEltExp: unary([](float v) { return elt_exp(v); }); break;
+                case kEltLog: unary([](float v) { return elt_log(v); }); break;
+                case kEltAbs: unary([](float v) { return elt_abs(v); }); break;
+                case kEltReluD: unary([](float v) { return elt_relu_d(v); }); break;
+                case kEltGeluD: unary([](float v) { return elt_gelu_d(v); }); break;
+                case kEltEluD: unary([](float v) { return elt_elu_d(v); }); break;
+                case kEltSign: unary([](float v) { return elt_sign(v); }); break;
                 case kEltLabelEq:
 #pragma unroll
                     for (int u = 0; u < U; ++u) {
@@ -254,7 +252,7 @@ __global__ __launch_bounds__(kThreads) void eltwise_prog_kernel(const EltProgram
                         const f32x4 z = get(u, in.c);
                         f32x4 t;
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) t[e] = x[u][e] != 0.0f ? y[u][e] : z[e];
+                        for (int e = 0; e < 4; ++e) t[e] = elt_select(x[u][e], y[u][e], z[e]);
                         o[u] = t;
                     }
                     break;
@@ -263,7 +261,7 @@ __global__ __launch_bounds__(kThreads) void eltwise_prog_kernel(const EltProgram
                     for (int u = 0; u < U; ++u) {
                         f32x4 t;
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) t[e] = fmaxf(x[u][e], y[u][e]);
+                        for (int e = 0; e < 4; ++e) t[e] = elt_max(x[u][e], y[u][e]);
                         o[u] = t;
                     }
                     break;
@@ -290,13 +288,10 @@ int launch_file(fg_ctx *ctx, const EltProgram &p) {
     return FG_OK;
 }
 
-}  // namespace
-
-// Validates the program's indices on the host (so the kernel never reads a
-// source or writes a destination that was not supplied), allocates its
-// registers and launches it on the smallest register file that holds them.
-int launch_eltwise(fg_ctx *ctx, const EltProgram &p0) {
-    if (p0.n == 0) return FG_OK;
+// Validates the program's indices on the host (so no kernel reads a source
+// or writes a destination that was not supplied) and returns, in *live, the
+// values it keeps at most at once (its registers without prefetching).
+int check_program(const EltProgram &p0, int *live) {
     FG_REQUIRE(p0.n_instr >= 0 && p0.n_instr <= kEltMaxInstr, FG_ERR_INTERNAL,
                "eltwise program: %d instructions (max %d)", p0.n_instr, kEltMaxInstr);
     bool needs_cols = false;
@@ -329,17 +324,49 @@ int launch_eltwise(fg_ctx *ctx, const EltProgram &p0) {
     FG_REQUIRE(!needs_cols || p0.cols > 0, FG_ERR_INTERNAL, "eltwise program: cols is 0");
     EltProgram p = p0;
     char why[128] = "";
+    const int regs = elt_allocate(p, false, why, sizeof why);
+    FG_REQUIRE(regs >= 0, FG_ERR_INTERNAL, "eltwise program: %s", why);
+    FG_REQUIRE(regs <= kEltRegs, FG_ERR_INTERNAL, "eltwise program: %d registers (max %d)",
+               regs, kEltRegs);
+    *live = regs;
+    return FG_OK;
+}
+
+}  // namespace
+
+// Compiles (fg_elt_jit.cpp) the kernel a launch of this program will take,
+// when the mode selects one: for callers about to capture the launch.
+int prepare_eltwise(fg_ctx *ctx, const EltProgram &p0) {
+    if (p0.n == 0) return FG_OK;
+    int live = 0;
+    if (int rc = check_program(p0, &live)) return rc;
+    if (!eltwise_jit_selected(p0)) return FG_OK;
+    bool launched = false;
+    return eltwise_jit(ctx, p0, live, true, &launched);
+}
+
+// Runs the program through its compiled kernel when the mode selects one
+// (and it exists or can be built now), else through the interpreter: its
+// registers allocated by liveness, on the smallest register file that holds
+// them.
+int launch_eltwise(fg_ctx *ctx, const EltProgram &p0) {
+    if (p0.n == 0) return FG_OK;
+    int live = 0;
+    if (int rc = check_program(p0, &live)) return rc;
+    if (eltwise_jit_selected(p0)) {
+        bool launched = false;
+        if (int rc = eltwise_jit(ctx, p0, live, false, &launched)) return rc;
+        if (launched) return FG_OK;
+    }
+    eltwise_count_interpreted();
+    EltProgram p = p0;
+    char why[128] = "";
     int regs = elt_allocate(p, true, why, sizeof why);
     if (regs > kEltRegs) {  // prefetching raised the pressure: load in place
         p = p0;
         regs = elt_allocate(p, false, why, sizeof why);
     }
-    FG_REQUIRE(regs >= 0, FG_ERR_INTERNAL, "eltwise program: %s", why);
-    FG_REQUIRE(regs <= kEltRegs, FG_ERR_INTERNAL, "eltwise program: %d registers (max %d)",
-               regs, kEltRegs);
-    // Streaming accesses once each tensor is well past the L2 caches (4 MiB
-    // per XCD), so small programs keep their outputs cached for the next
-    // launch.
+    FG_REQUIRE(regs >= 0 && regs <= kEltRegs, FG_ERR_INTERNAL, "eltwise program: %s", why);
     // Register files, from a measured sweep on tanh(a*b + c) over 8192^2
     // (3 registers): 4 registers x 3 quads 5.65 TB/s (127 VGPRs, 4 waves per
     // SIMD), 8 x 2 5.18 (125 VGPRs), 4 x 4 4.84 (163 VGPRs, 3 waves), 16 x 1

@@ -389,6 +389,29 @@ int fg_bpat_read_f32(const fg_bpat *f, int index, float *dst);
 int fg_bpat_upload(fg_ctx *ctx, const fg_bpat *f, int index, void *d_dst, int dtype);
 
 /* --------------------------------------------------------------- graph */
+/* ----------------------------------------- compiled elementwise kernels */
+/* A plan runs each fused elementwise chain (forward, backward, losses) as one
+ * launch of an elementwise program: either a kernel generated for the
+ * program and compiled at run time with hipRTC -- as the reference compiles
+ * every fused kernel it generates (GpuBackend::compile,
+ * crates/fused_gpu/src/dispatch/mod.rs:210; rocm/mod.rs:140-170) -- or the
+ * library's precompiled interpreter of such programs.  Both give the same
+ * bits.  Compiled kernels are kept for the life of the process, one per
+ * device and program; a graph capture meeting a program not compiled yet
+ * uses the interpreter (fg_plan_capture_step compiles its programs before it
+ * captures).  The setting is process-wide; the environment variable
+ * FG_ELTWISE_MODE (0, 1 or 2) sets the initial mode, default
+ * FG_ELTWISE_COMPILE_LARGE.  No reference counterpart: its backend always
+ * compiles. */
+#define FG_ELTWISE_INTERPRET 0      /* every program on the interpreter         */
+#define FG_ELTWISE_COMPILE_LARGE 1  /* compile programs over >= 2^20 elements   */
+#define FG_ELTWISE_COMPILE_ALL 2    /* compile every program                    */
+int fg_eltwise_set_mode(int mode, int *previous);
+/* Process-wide counts: kernels compiled, launches of compiled kernels,
+ * launches of the interpreter (any pointer may be NULL). */
+int fg_eltwise_stats(uint64_t *kernels_compiled, uint64_t *compiled_launches,
+                     uint64_t *interpreted_launches);
+
 /* Graph IR: the mirror of fused_gpu's Graph / Node / GraphOp
  * (crates/fused_gpu/src/dispatch/backend/mod.rs:499-1316) with the
  * ferrograd-nn builders as a fixed operation enum.  Node ids are creation
