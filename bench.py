@@ -444,7 +444,10 @@ def hbm_kernels_component(ctx, reps: int):
     * eltwise: a fused elementwise program, the planner's forward of
       y = tanh(a * b + c) over 8192 x 8192 fp32 -- one launch reading a, b,
       c and writing the three node values the plan keeps (a * b, a * b + c
-      and y, its forward_saved tensors): 24 B per element;
+      and y, its forward_saved tensors): 24 B per element; the default path
+      runs the program's compiled kernel (fg_eltwise_set_mode: programs of
+      2^20 elements or more), eltwise_..._interp the same program on the
+      interpreter;
     * act_bwd: dZ = dH * GELU'(Z) over 2^28 elements (12 B per element);
     * sgd: the multi-tensor SGD over c4's 64 x 4 Mi parameters, gradients
       zeroed after the update (read p, g; write p, g: 16 B per parameter)."""
@@ -455,10 +458,16 @@ def hbm_kernels_component(ctx, reps: int):
     out = {}
     R = C = 8192
     st, sch, gctx, keep = eltwise_tanh_plan(ctx, R, C)
-    t = event_time_ms(lambda: gctx.dispatch_forward(sch), reps, warm_ms=200)
     nbytes = 24 * R * C
-    out["eltwise_fwd_8192x8192"] = {"ms": t, "bytes": nbytes, "gbs": nbytes / t / 1e6,
-                                    "frac_hbm": nbytes / t / 1e6 / PEAK_HBM_GBS}
+    for key, mode in (("eltwise_fwd_8192x8192", fa.ELTWISE_COMPILE_LARGE),
+                      ("eltwise_fwd_8192x8192_interp", fa.ELTWISE_INTERPRET)):
+        prev = fa.eltwise_mode(mode)
+        try:
+            t = event_time_ms(lambda: gctx.dispatch_forward(sch), reps, warm_ms=200)
+        finally:
+            fa.eltwise_mode(prev)
+        out[key] = {"ms": t, "bytes": nbytes, "gbs": nbytes / t / 1e6,
+                    "frac_hbm": nbytes / t / 1e6 / PEAK_HBM_GBS}
     st.plan.close()
     del keep
 
@@ -699,13 +708,20 @@ def only_copy_256mib(ctx, reps):
         b.copy_(a)
 
 
-def only_eltwise(ctx, reps):
-    """The elementwise program tanh(a * b + c) over 8192 x 8192 fp32."""
-    st, sch, gctx, keep = eltwise_tanh_plan(ctx, 8192, 8192)
-    for _ in range(reps):
-        gctx.dispatch_forward(sch)
-    gctx.sync()
-    st.plan.close()
+def only_eltwise(ctx, reps, mode=None):
+    """The elementwise program tanh(a * b + c) over 8192 x 8192 fp32 (its
+    compiled kernel, the default; or on the interpreter)."""
+    import ferrograd_amd as fa
+
+    prev = fa.eltwise_mode(fa.ELTWISE_COMPILE_LARGE if mode is None else mode)
+    try:
+        st, sch, gctx, keep = eltwise_tanh_plan(ctx, 8192, 8192)
+        for _ in range(reps):
+            gctx.dispatch_forward(sch)
+        gctx.sync()
+        st.plan.close()
+    finally:
+        fa.eltwise_mode(prev)
 
 
 def only_c5_step(ctx, reps, dtype="f32"):
@@ -815,6 +831,7 @@ ONLY = {
     "adam_c4": only_adam_c4,
     "copy_256mib": only_copy_256mib,
     "eltwise_8192": only_eltwise,
+    "eltwise_8192_interp": lambda ctx, reps: only_eltwise(ctx, reps, 0),
     "hbm_roof": lambda ctx, reps: print(json.dumps(hbm_roof_component(reps)), flush=True),
     "hbm_kernels": lambda ctx, reps: print(json.dumps(hbm_kernels_component(ctx, reps)),
                                            flush=True),

@@ -190,8 +190,14 @@ inline const char *elt_jit_unary_fn(int op) {
 
 // Quads per thread and pass for a program that keeps `live` values (its
 // register count after allocation): every value of every quad stays in
-// registers, so the quads multiply the registers a thread holds.
-inline int elt_jit_quads(int live) { return live <= 4 ? 4 : live <= 8 ? 2 : 1; }
+// registers, so the quads multiply the registers a thread holds, and fewer
+// registers let more waves keep loads in flight.  Measured (HIP events, one
+// process): tanh(a*b + c) over 8192^2 (3 values) 0.266 / 0.258 / 0.258 ms
+// with 4 / 2 / 1 quads (interpreter 0.289); the seven-input expression
+// ((a*b + c*d)(e - f)) / (g*g + 1) over 4096 x 8192, forward 0.389 / 0.382 /
+// 0.389 ms (interpreter 0.429), its backward's programs 0.742 / 0.726 /
+// 0.715 ms (interpreter 0.808).
+inline int elt_jit_quads(int live) { return live <= 4 ? 2 : 1; }
 
 // The kernel source of a validated program (launch_eltwise's checks: known
 // ops, sources, destinations and element types present, registers written
