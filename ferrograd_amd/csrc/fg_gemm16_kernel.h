@@ -695,7 +695,15 @@ __device__ __forceinline__ void gemm16_pipe_body(Args p, int bx, int by) {
     constexpr int kPieces = TM + TN;                     // operand fragments per step
     constexpr int kSlots = (NU - 1) * kMfma;             // MFMAs of a tile before its barrier
     static_assert(NU >= 2 && kLoads <= kSlots, "a tile's loads fit among its MFMAs");
-    constexpr int kStride = kSlots / kLoads;             // MFMAs per load
+    // MFMAs per load: staged, spread over the steps before the barrier;
+    // direct, one per MFMA from the tile's first step, which leaves them
+    // most of the tile to land (the two-stage ring of the 256x256 tiles
+    // waits for them at the tile's end): 4096^3 NN / NT / TN 1160-1167 /
+    // 1166-1178 / 1127-1149 -> 1202-1210 / 1215-1226 / 1186-1196 TF, the
+    // 256x128 tiles of the c5 shapes unchanged.  Issuing them a step
+    // earlier still, among the MFMAs right after the barrier that frees
+    // their stage, measured 1181 / 1191 / 1162.
+    constexpr int kStride = kStaged ? kSlots / kLoads : 1;
     constexpr int kAhead = kStages - 1;                  // direct: tiles in flight
     // One k16 step's MFMAs on (ca, cb) in a fixed order: after MFMA m, the
     // reads of operand fragment m of step un (A fragments, then B), and, when
