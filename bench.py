@@ -780,6 +780,41 @@ def only_gemm_bf16_c2(ctx, reps):
         ctx.gemm_x16(bf, fa.TN, n, n, n, A, n, dC, n, dB, n)
 
 
+def only_gemm_bf16_data(ctx, reps):
+    """The plain bf16 NN GEMM at 4096^3, ours and torch.mm's (hipBLASLt),
+    each 3 + `reps` times on N(0,1) operands and then on zero operands (for a counter pass of MFMA busy cycles and the clock: the
+    matrix units' power, and so the clock, depend on the data)."""
+    import torch
+
+    import ferrograd_amd as fa
+
+    n, bf = 4096, fa.DTYPE_BF16
+    g = torch.Generator(device="cuda").manual_seed(1)
+    C = torch.empty((n, n), device="cuda", dtype=torch.bfloat16)
+    flops = 2.0 * n * n * n
+    out = {}
+    for data in ("normal", "zeros"):
+        if data == "normal":
+            A, Bm = (torch.randn((n, n), device="cuda", generator=g).to(torch.bfloat16)
+                     for _ in range(2))
+        else:
+            A, Bm = (torch.zeros((n, n), device="cuda", dtype=torch.bfloat16) for _ in range(2))
+        for who, fn in (("ours", lambda: ctx.gemm_x16(bf, fa.NN, n, n, n, A, n, Bm, n, C, n)),
+                        ("torch_mm", lambda: torch.mm(A, Bm, out=C))):
+            for _ in range(3):  # untimed: library set-up, first-touch costs
+                fn()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                fn()
+            e1.record()
+            e1.synchronize()
+            ms = e0.elapsed_time(e1) / reps
+            out[f"{who}_{data}"] = {"ms": ms, "tflops": flops / ms / 1e9}
+    print(json.dumps({"gemm_bf16_4096_nn_by_data": out}), flush=True)
+
+
 def only_gemm_c2(ctx, reps):
     """The c2 GEMMs: forward (bias + ReLU) and the masked backward (dA, dB +
     dbias) through fg_linear_bwd_f32."""
@@ -816,6 +851,7 @@ ONLY = {
     "c5_step_bf16": only_c5_step_bf16,
     "gemm_bf16_c2": only_gemm_bf16_c2,
     "gemm_bf16_c5_hidden": only_gemm_bf16_c5_hidden,
+    "gemm_bf16_data": only_gemm_bf16_data,
     "gemm_c2": only_gemm_c2,
     "gemm_c5_hidden": only_gemm_c5_hidden,
     "gemm_c5_fwd": only_c5_gemm("gemm_c5_fwd"),
