@@ -15,6 +15,11 @@
 //   finite; beyond it s is 0 or 1 as the limits require).  This avoids the
 //   cancellation of 1 + tanh(u) near -1 and costs a fraction of tanhf, which
 //   dominated the activation epilogues.
+// Contraction is off in these functions: with multiply-adds left to the
+// compiler, it fused them differently where the same function was inlined
+// into different code (a GEMM's staged and register epilogues gave fp16
+// GELU values one unit apart), so every caller now evaluates the same
+// sequence of roundings.
 #pragma once
 
 #ifndef __HIPCC_RTC__  // hipRTC declares the runtime itself
@@ -30,18 +35,21 @@ constexpr float kGeluC1 = 0.044715f;
 
 // s = 0.5 (1 + tanh(u)) = 1 / (1 + exp(-2u)) for the GELU argument u of z.
 __device__ __forceinline__ float gelu_s(float z) {
+#pragma clang fp contract(off)
     constexpr float kM2Log2e = -2.0f * 1.4426950408889634f;  // -2 / ln 2
     const float u = kGeluC0 * (z + kGeluC1 * z * z * z);
     return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(kM2Log2e * u));
 }
 
 __device__ __forceinline__ float act_fwd(int act, float z) {
+#pragma clang fp contract(off)
     if (act == kActRelu) return z > 0.0f ? z : 0.0f;
     if (act == kActGelu) return z * gelu_s(z);
     return z;
 }
 
 __device__ __forceinline__ float act_grad(int act, float z) {
+#pragma clang fp contract(off)
     if (act == kActRelu) return z > 0.0f ? 1.0f : 0.0f;
     if (act == kActGelu) {
         const float s = gelu_s(z);

@@ -76,13 +76,22 @@ struct Args {
     float *colsum_partial;
 };
 
-// Element conversion and the MFMA of one storage type.
+// Element conversion and the MFMA of one storage type.  from_f rounds the
+// fp32 value it is given: an empty asm statement keeps the compiler from
+// folding the operation that produced it into the conversion (fp16 has
+// v_fma_mix*, which computed GELU's z * s as fma(s, z, +0) and so returned
+// +0 where the product is -0), so every epilogue rounds the same fp32
+// value.
 template <bool BF>
 struct T16;
+__device__ __forceinline__ float opaque(float f) {
+    asm volatile("" : "+v"(f));
+    return f;
+}
 template <>
 struct T16<true> {
     static __device__ __forceinline__ float to_f(uint16_t h) { return bf16_to_f(h); }
-    static __device__ __forceinline__ uint16_t from_f(float f) { return f_to_bf16(f); }
+    static __device__ __forceinline__ uint16_t from_f(float f) { return f_to_bf16(opaque(f)); }
     static __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
@@ -91,7 +100,7 @@ struct T16<true> {
 template <>
 struct T16<false> {
     static __device__ __forceinline__ float to_f(uint16_t h) { return f16_to_f(h); }
-    static __device__ __forceinline__ uint16_t from_f(float f) { return f_to_f16(f); }
+    static __device__ __forceinline__ uint16_t from_f(float f) { return f_to_f16(opaque(f)); }
     static __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                      __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
@@ -340,6 +349,174 @@ __device__ __forceinline__ void store_tile16(const Args &p, const f32x16 (&acc)[
             }
         }
         __syncthreads();
+    }
+}
+
+// ------------------------------------------------ register epilogue
+// The pipelined kernels' epilogue when the workgroup's whole tile is in
+// bounds (and rows are 8-byte aligned): no LDS and no workgroup barrier.
+// Accumulator registers 4k .. 4k+3 of lane (h, l32) hold rows 8k + 4h + 0..3
+// of column l32 of a 32x32 block; within each quad of lanes (l32 = 4a + e)
+// a 4x4 transpose by two DPP exchanges leaves lane e with row 8k + 4h + e,
+// columns 4a .. 4a+3, which it finishes and stores as 8 bytes (16 for the
+// fp32 sums of a K slice).  The kind of epilogue (mode, bias, activation) is
+// a template parameter, so the per-element code branches on none of them;
+// the operations per element are epi16_x4's, so the bits are those of the
+// staged epilogue (store_tile16), which stays for partial tiles.  The
+// staged epilogue cost 13 us of a 4096x4096 launch (its LDS round trip,
+// barriers and a pass loop branching on every epilogue choice); against it
+// (bf16, A/B in one process): c5 hidden forward / dX / dW 75.4 / 72.6 /
+// 71.2 -> 73.2 / 70.3 / 67.0 us, their dW + dX pair 140.8 -> 134.3 us,
+// 4096^3 NN 116.0 -> 112.9 us, 4096x4096x1024 with bias + GELU + Z 53.4 ->
+// 46.7 us.
+
+template <int CTRL>
+__device__ __forceinline__ float dpp16(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
+// Lane e of each quad holds x[q] = M[q][e] of a 4x4 block; returns M[e][0..3]:
+// first an exchange with lane e^1 (quad_perm [1,0,3,2]) that moves the 2x2
+// off-diagonal blocks' elements, then one with lane e^2 ([2,3,0,1]).
+__device__ __forceinline__ f32x4 quad_transpose4(f32x4 x, int e) {
+    constexpr int kSwap1 = 0xB1, kSwap2 = 0x4E;
+    const bool odd = (e & 1) != 0, high = (e & 2) != 0;
+    f32x4 y, z;
+    const float u0 = dpp16<kSwap1>(odd ? x[0] : x[1]);
+    const float u1 = dpp16<kSwap1>(odd ? x[2] : x[3]);
+    y[0] = odd ? u0 : x[0];
+    y[1] = odd ? x[1] : u0;
+    y[2] = odd ? u1 : x[2];
+    y[3] = odd ? x[3] : u1;
+    const float w0 = dpp16<kSwap2>(high ? y[0] : y[2]);
+    const float w1 = dpp16<kSwap2>(high ? y[1] : y[3]);
+    z[0] = high ? w0 : y[0];
+    z[1] = high ? w1 : y[1];
+    z[2] = high ? y[2] : w0;
+    z[3] = high ? y[3] : w1;
+    return z;
+}
+
+// epi16_x4 with the mode (0 forward, 1 act-derivative), the bias and the
+// activation fixed; z: the four saved pre-activations (MODE 1 with an
+// activation), loaded by the caller.
+template <bool BF, int MODE, bool BIAS, int ACT>
+__device__ __forceinline__ void epi16_x4_k(const Args &p, f32x4 v, f32x4 bv, f32x4 z, int row,
+                                           int col) {
+    using E = T16<BF>;
+    auto rnd = [](f32x4 x) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) x[t] = E::to_f(E::from_f(x[t]));
+        return x;
+    };
+    auto st4 = [](uint16_t *q, f32x4 x) {
+        *reinterpret_cast<u32x2 *>(q) = u32x2{pack2(E::from_f(x[0]), E::from_f(x[1])),
+                                              pack2(E::from_f(x[2]), E::from_f(x[3]))};
+    };
+    v = rnd(v);
+    if constexpr (MODE == 0) {
+        if constexpr (BIAS) v = rnd(v + bv);
+        if (p.Z) st4(p.Z + (size_t)row * p.ldz + col, v);
+        if constexpr (ACT != kActNone) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) v[t] = act_fwd(ACT, v[t]);
+            v = rnd(v);
+        }
+    } else if constexpr (ACT == kActRelu) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) v[t] = z[t] > 0.0f ? v[t] : 0.0f;
+    } else if constexpr (ACT != kActNone) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) v[t] = v[t] * act_grad(ACT, z[t]);
+        v = rnd(v);
+    }
+    uint16_t *c = p.C + (size_t)row * p.ldc + col;
+    if (p.accumulate) {
+        const u32x2 w = *reinterpret_cast<const u32x2 *>(c);
+        v += f32x4{E::to_f((uint16_t)w[0]), E::to_f((uint16_t)(w[0] >> 16)),
+                   E::to_f((uint16_t)w[1]), E::to_f((uint16_t)(w[1] >> 16))};
+    }
+    st4(c, v);
+}
+
+// MODE 2: the raw fp32 sums of a K slice into its slot.  Blocks (i, j) are
+// unrolled; the four row groups k of a block run as a loop that picks its
+// registers by k, which keeps the code (fetched cold, once per CU and
+// launch) short.  MODE 1 with an activation loads a block's 16 saved
+// pre-activations before its loop.
+template <bool BF, int TM, int TN, int MODE, bool BIAS, int ACT>
+__device__ __forceinline__ void store_direct16_k(const Args &p, const f32x16 (&acc)[TM][TN],
+                                                 int r0, int c0, int lane) {
+    using E = T16<BF>;
+    const int l32 = lane & 31, e = lane & 3, a4 = l32 & ~3;
+    const int rl = 4 * (lane >> 5) + e;  // row within each group of 8
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int col = c0 + 32 * j + a4;
+        f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (MODE == 0 && BIAS) {
+            const u32x2 w = *reinterpret_cast<const u32x2 *>(p.bias + col);
+            bv = f32x4{E::to_f((uint16_t)w[0]), E::to_f((uint16_t)(w[0] >> 16)),
+                       E::to_f((uint16_t)w[1]), E::to_f((uint16_t)(w[1] >> 16))};
+        }
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const f32x16 &a = acc[i][j];
+            const int rowb = r0 + 32 * i + rl;
+            constexpr bool kZs = MODE == 1 && ACT != kActNone;
+            u32x2 zr[4];
+            if constexpr (kZs) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    zr[k] = *reinterpret_cast<const u32x2 *>(p.Zs + (size_t)(rowb + 8 * k) * p.ldzs +
+                                                             col);
+            }
+#pragma unroll 1
+            for (int k = 0; k < 4; ++k) {
+                f32x4 x;
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    x[q] = k == 0 ? a[q] : k == 1 ? a[4 + q] : k == 2 ? a[8 + q] : a[12 + q];
+                const f32x4 y = quad_transpose4(x, e);
+                const int row = rowb + 8 * k;
+                if constexpr (MODE == 2) {
+                    *reinterpret_cast<f32x4 *>(p.partial + (size_t)row * p.N + col) = y;
+                } else {
+                    f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                    if constexpr (kZs) {
+                        const u32x2 w = k == 0 ? zr[0] : k == 1 ? zr[1] : k == 2 ? zr[2] : zr[3];
+                        z = f32x4{E::to_f((uint16_t)w[0]), E::to_f((uint16_t)(w[0] >> 16)),
+                                  E::to_f((uint16_t)w[1]), E::to_f((uint16_t)(w[1] >> 16))};
+                    }
+                    epi16_x4_k<BF, MODE, BIAS, ACT>(p, y, bv, z, row, col);
+                }
+            }
+        }
+    }
+}
+
+// Picks the register epilogue's kind; an activation code outside ReLU / GELU
+// takes the kind without one (the staged epilogue's act_fwd / act_grad are
+// the identity for it, so the bits agree).
+template <bool BF, int TM, int TN>
+__device__ __forceinline__ void store_direct16(const Args &p, const f32x16 (&acc)[TM][TN], int r0,
+                                               int c0, int lane) {
+    if (p.ksplit > 0) {
+        store_direct16_k<BF, TM, TN, 2, false, kActNone>(p, acc, r0, c0, lane);
+    } else if (p.mode == 0) {
+        if (p.bias) {
+            if (p.act == kActRelu) store_direct16_k<BF, TM, TN, 0, true, kActRelu>(p, acc, r0, c0, lane);
+            else if (p.act == kActGelu) store_direct16_k<BF, TM, TN, 0, true, kActGelu>(p, acc, r0, c0, lane);
+            else store_direct16_k<BF, TM, TN, 0, true, kActNone>(p, acc, r0, c0, lane);
+        } else {
+            if (p.act == kActRelu) store_direct16_k<BF, TM, TN, 0, false, kActRelu>(p, acc, r0, c0, lane);
+            else if (p.act == kActGelu) store_direct16_k<BF, TM, TN, 0, false, kActGelu>(p, acc, r0, c0, lane);
+            else store_direct16_k<BF, TM, TN, 0, false, kActNone>(p, acc, r0, c0, lane);
+        }
+    } else {
+        if (p.act == kActRelu) store_direct16_k<BF, TM, TN, 1, false, kActRelu>(p, acc, r0, c0, lane);
+        else if (p.act == kActGelu) store_direct16_k<BF, TM, TN, 1, false, kActGelu>(p, acc, r0, c0, lane);
+        else store_direct16_k<BF, TM, TN, 1, false, kActNone>(p, acc, r0, c0, lane);
     }
 }
 
@@ -841,8 +1018,13 @@ __device__ __forceinline__ void gemm16_pipe_body(Args p, int bx, int by) {
     __syncthreads();
     if constexpr (kTN)
         if (do_cs) cs.finish(p, reinterpret_cast<float *>(lds), n0);
-    store_tile16<BF, TM, TN, WTN, NW>(p, acc, reinterpret_cast<float *>(lds), m0 + wm0, n0 + wn0,
-                                      wave, lane);
+    // The whole tile in bounds: the register epilogue (uniform across the
+    // workgroup, as the staged one has workgroup barriers).
+    if (p.vec_out && m0 + BM <= p.M && n0 + BN <= p.N && (p.ksplit == 0 || p.N % 4 == 0))
+        store_direct16<BF, TM, TN>(p, acc, m0 + wm0, n0 + wn0, lane);
+    else
+        store_tile16<BF, TM, TN, WTN, NW>(p, acc, reinterpret_cast<float *>(lds), m0 + wm0,
+                                          n0 + wn0, wave, lane);
 }
 
 template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC, bool BF>
