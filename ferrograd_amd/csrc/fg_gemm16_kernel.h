@@ -370,33 +370,6 @@ __device__ __forceinline__ void store_tile16(const Args &p, const f32x16 (&acc)[
 // 4096^3 NN 116.0 -> 112.9 us, 4096x4096x1024 with bias + GELU + Z 53.4 ->
 // 46.7 us.
 
-template <int CTRL>
-__device__ __forceinline__ float dpp16(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
-}
-
-// Lane e of each quad holds x[q] = M[q][e] of a 4x4 block; returns M[e][0..3]:
-// first an exchange with lane e^1 (quad_perm [1,0,3,2]) that moves the 2x2
-// off-diagonal blocks' elements, then one with lane e^2 ([2,3,0,1]).
-__device__ __forceinline__ f32x4 quad_transpose4(f32x4 x, int e) {
-    constexpr int kSwap1 = 0xB1, kSwap2 = 0x4E;
-    const bool odd = (e & 1) != 0, high = (e & 2) != 0;
-    f32x4 y, z;
-    const float u0 = dpp16<kSwap1>(odd ? x[0] : x[1]);
-    const float u1 = dpp16<kSwap1>(odd ? x[2] : x[3]);
-    y[0] = odd ? u0 : x[0];
-    y[1] = odd ? x[1] : u0;
-    y[2] = odd ? u1 : x[2];
-    y[3] = odd ? x[3] : u1;
-    const float w0 = dpp16<kSwap2>(high ? y[0] : y[2]);
-    const float w1 = dpp16<kSwap2>(high ? y[1] : y[3]);
-    z[0] = high ? w0 : y[0];
-    z[1] = high ? w1 : y[1];
-    z[2] = high ? y[2] : w0;
-    z[3] = high ? y[3] : w1;
-    return z;
-}
-
 // epi16_x4 with the mode (0 forward, 1 act-derivative), the bias and the
 // activation fixed; z: the four saved pre-activations (MODE 1 with an
 // activation), loaded by the caller.

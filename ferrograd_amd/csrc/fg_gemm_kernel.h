@@ -302,6 +302,7 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int &
 // One output element of the epilogue.
 __device__ __forceinline__ float epi_value(const GemmArgs &p, float v, float bv, int row, int col,
                                            float *zout) {
+#pragma clang fp contract(off)
     if (p.mode == 0) {
         v += bv;
         *zout = v;
@@ -323,7 +324,7 @@ __device__ __forceinline__ void split_sum_store(const GemmArgs &p, int splits, i
     float o = epi_value(p, v, b, row, col, &z);
     if (p.mode == 0 && p.Z) p.Z[(size_t)row * p.ldz + col] = z;
     float *c = p.C + (size_t)row * p.ldc + col;
-    if (p.accumulate) o += *c;
+    if (p.accumulate) o += *c;  // (in its own statement: no contraction with o)
     *c = o;
 }
 
@@ -341,6 +342,7 @@ __device__ __forceinline__ void split_sum_blocks(const GemmArgs &p, int splits, 
 // (mode, activation, Z, accumulate) taken once per four.  Returns the four
 // values stored to C.
 __device__ __forceinline__ f32x4 epi_x4(const GemmArgs &p, f32x4 v, f32x4 bv, int row, int col) {
+#pragma clang fp contract(off)
     if (p.mode == 0) {
         v += bv;
         if (p.Z) *reinterpret_cast<f32x4 *>(p.Z + (size_t)row * p.ldz + col) = v;
@@ -423,6 +425,134 @@ __device__ __forceinline__ void store_tile(const GemmArgs &p, const f32x16 (&acc
         }
         __syncthreads();
     }
+}
+
+// ------------------------------------------------ register epilogue
+// The pipelined kernels' epilogue when the workgroup's whole tile is in
+// bounds and rows are 16-byte aligned: no LDS, no workgroup barrier.
+// Accumulator registers 4k .. 4k+3 of lane (h, l32) hold rows x = 8k + 4h +
+// 0..3 of a block's column; the block's rows and columns in C follow
+// store_tile's mapping (interleaved or not).  Without column interleave, a
+// 4x4 transpose within each quad of lanes (quad_transpose4) leaves lane e of
+// quad a with row x = 8k + 4h + e and columns 4a .. 4a+3, finished and
+// stored as 16 bytes; with it (IB = TN, the TN layout's weight gradients) a
+// lane already holds TN consecutive columns of each row and stores them as
+// they are, for the plain product only (the kinds with a bias, an
+// activation or Z take store_tile there).  The kind of epilogue is a
+// template parameter, so the per-element code branches on none of it; the
+// operations per element are epi_x4's (a plain product still adds the zero
+// bias, as epi_x4 does, which turns -0 into +0), so the bits are
+// store_tile's.  Four row groups k of a block run as a loop that picks its
+// registers by k, which keeps the code (fetched cold, once per CU and
+// launch) short.  The staged epilogue cost 5-23 us per launch on the c5
+// shapes (its LDS round trip, barriers and a pass loop branching on every
+// epilogue choice; the activation-derivative kinds also waited for each
+// saved pre-activation load in turn).
+template <int MODE, int ACT>
+__device__ __forceinline__ void epi_x4_k(const GemmArgs &p, f32x4 v, f32x4 bv, f32x4 z, int row,
+                                         int col) {
+#pragma clang fp contract(off)
+    if constexpr (MODE == 0) {
+        v += bv;
+        if (p.Z) *reinterpret_cast<f32x4 *>(p.Z + (size_t)row * p.ldz + col) = v;
+        if constexpr (ACT != kActNone) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) v[t] = act_fwd(ACT, v[t]);
+        }
+    } else if constexpr (ACT != kActNone) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) v[t] *= act_grad(ACT, z[t]);
+    }
+    float *c = p.C + (size_t)row * p.ldc + col;
+    if (p.accumulate) v += *reinterpret_cast<const f32x4 *>(c);
+    *reinterpret_cast<f32x4 *>(c) = v;
+}
+
+template <int TM, int TN, int IA, int IB, int MODE, int ACT>
+__device__ __forceinline__ void store_direct_k(const GemmArgs &p, const f32x16 (&acc)[TM][TN],
+                                               int r0, int c0, int lane) {
+#pragma clang fp contract(off)
+    const int l32 = lane & 31, h = lane >> 5, e = lane & 3;
+    // Row of C of block row i and block-row index x (0..31).
+    auto crow = [&](int i, int x) { return IA > 1 ? r0 + TM * x + i : r0 + 32 * i + x; };
+    if constexpr (IB == 1) {
+        const int a4 = l32 & ~3;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int col = c0 + 32 * j + a4;
+            f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+            if (MODE == 0 && p.bias) bv = *reinterpret_cast<const f32x4 *>(p.bias + col);
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                const f32x16 &a = acc[i][j];
+                constexpr bool kZs = MODE == 1 && ACT != kActNone;
+                f32x4 zr[4];
+                if constexpr (kZs) {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        zr[k] = *reinterpret_cast<const f32x4 *>(
+                            p.Zs + (size_t)crow(i, 8 * k + 4 * h + e) * p.ldzs + col);
+                }
+#pragma unroll 1
+                for (int k = 0; k < 4; ++k) {
+                    f32x4 x;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        x[q] = k == 0 ? a[q] : k == 1 ? a[4 + q] : k == 2 ? a[8 + q] : a[12 + q];
+                    const f32x4 y = quad_transpose4(x, e);
+                    f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                    if constexpr (kZs) z = k == 0 ? zr[0] : k == 1 ? zr[1] : k == 2 ? zr[2] : zr[3];
+                    epi_x4_k<MODE, ACT>(p, y, bv, z, crow(i, 8 * k + 4 * h + e), col);
+                }
+            }
+        }
+    } else {
+        typedef float vec_t __attribute__((ext_vector_type(IB)));
+        const int col = c0 + TN * l32;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll 1
+            for (int k = 0; k < 4; ++k)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    vec_t v;
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) {
+                        const f32x16 &a = acc[i][j];
+                        v[j] = (k == 0 ? a[q] : k == 1 ? a[4 + q] : k == 2 ? a[8 + q] : a[12 + q]) +
+                               0.0f;
+                    }
+                    float *c = p.C + (size_t)crow(i, 8 * k + 4 * h + q) * p.ldc + col;
+                    if (p.accumulate) v += *reinterpret_cast<const vec_t *>(c);
+                    *reinterpret_cast<vec_t *>(c) = v;
+                }
+    }
+}
+
+// Runs the register epilogue's kind for p; false (nothing stored) for a
+// kind it does not take, which then goes to store_tile.  An activation code
+// outside ReLU / GELU takes the kind without one (act_fwd / act_grad are
+// the identity for it, so the bits agree).  Waves holding 256 accumulator
+// registers (the 4-wave 256x256 tile) keep store_tile: with every register
+// taken, the register epilogue's temporaries spill.
+template <int TM, int TN, int IA, int IB>
+__device__ __forceinline__ bool store_direct(const GemmArgs &p, const f32x16 (&acc)[TM][TN],
+                                             int r0, int c0, int lane) {
+    if constexpr (TM * TN > 8) {
+        return false;
+    } else if constexpr (IB > 1) {
+        if (p.mode != 0 || p.bias || p.Z || p.act == kActRelu || p.act == kActGelu) return false;
+        store_direct_k<TM, TN, IA, IB, 0, kActNone>(p, acc, r0, c0, lane);
+    } else if (p.mode == 0) {
+        if (p.act == kActRelu) store_direct_k<TM, TN, IA, IB, 0, kActRelu>(p, acc, r0, c0, lane);
+        else if (p.act == kActGelu) store_direct_k<TM, TN, IA, IB, 0, kActGelu>(p, acc, r0, c0, lane);
+        else store_direct_k<TM, TN, IA, IB, 0, kActNone>(p, acc, r0, c0, lane);
+    } else {
+        if (p.act == kActRelu) store_direct_k<TM, TN, IA, IB, 1, kActRelu>(p, acc, r0, c0, lane);
+        else if (p.act == kActGelu) store_direct_k<TM, TN, IA, IB, 1, kActGelu>(p, acc, r0, c0, lane);
+        else store_direct_k<TM, TN, IA, IB, 1, kActNone>(p, acc, r0, c0, lane);
+    }
+    return true;
 }
 
 // The kernel bodies take their workgroup's coordinates (bx: output tile,
@@ -1024,7 +1154,11 @@ __device__ __forceinline__ void gemm_f32_pipe_body(GemmArgs p, int bx, int by) {
     __syncthreads();  // every wave past its last tile read before the stage reuse
     if constexpr (kTN)
         if (do_cs) cs.finish(p, lds, n0);
-    store_tile<TM, TN, WTN, NW, IA, IB>(p, acc, lds, m0 + wm0, n0 + wn0, wave, lane);
+    // The whole tile in bounds: the register epilogue (the choice is uniform
+    // across the workgroup, as store_tile has workgroup barriers).
+    if (!(p.vec_out && m0 + BM <= p.M && n0 + BN <= p.N &&
+          store_direct<TM, TN, IA, IB>(p, acc, m0 + wm0, n0 + wn0, lane)))
+        store_tile<TM, TN, WTN, NW, IA, IB>(p, acc, lds, m0 + wm0, n0 + wn0, wave, lane);
 }
 
 template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC, int PRO, bool KT>

@@ -32,4 +32,36 @@ __device__ __forceinline__ void lds_dma16(const void *src, const void *lds_dst) 
                  : "memory");
 }
 
+// 4x4 transpose within each quad of lanes, for the GEMMs' register
+// epilogues: lane e (of its quad) holds x[q] = M[q][e]; returns M[e][0..3].
+// First an exchange with lane e^1 (DPP quad_perm [1,0,3,2]) that swaps the
+// off-diagonal elements of each 2x2 block, then one with lane e^2
+// ([2,3,0,1]) that swaps the off-diagonal 2x2 blocks.  Moves and selects
+// only: every value keeps its bits.
+typedef float qt_f32x4 __attribute__((ext_vector_type(4)));
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
+__device__ __forceinline__ qt_f32x4 quad_transpose4(qt_f32x4 x, int e) {
+    constexpr int kSwap1 = 0xB1, kSwap2 = 0x4E;
+    const bool odd = (e & 1) != 0, high = (e & 2) != 0;
+    qt_f32x4 y, z;
+    const float u0 = dpp_mov_f32<kSwap1>(odd ? x[0] : x[1]);
+    const float u1 = dpp_mov_f32<kSwap1>(odd ? x[2] : x[3]);
+    y[0] = odd ? u0 : x[0];
+    y[1] = odd ? x[1] : u0;
+    y[2] = odd ? u1 : x[2];
+    y[3] = odd ? x[3] : u1;
+    const float w0 = dpp_mov_f32<kSwap2>(high ? y[0] : y[2]);
+    const float w1 = dpp_mov_f32<kSwap2>(high ? y[1] : y[3]);
+    z[0] = high ? w0 : y[0];
+    z[1] = high ? w1 : y[1];
+    z[2] = high ? y[2] : w0;
+    z[3] = high ? y[3] : w1;
+    return z;
+}
+
 }  // namespace fg
