@@ -371,25 +371,26 @@ __device__ __forceinline__ void store_tile16(const Args &p, const f32x16 (&acc)[
 // 46.7 us.
 
 // epi16_x4 with the mode (0 forward, 1 act-derivative), the bias and the
-// activation fixed; z: the four saved pre-activations (MODE 1 with an
-// activation), loaded by the caller.
+// activation fixed, without the stores: returns the four C values and (MODE
+// 0 with Z) the four Z values, packed; z: the four saved pre-activations
+// (MODE 1 with an activation); c_old: C's current four values when
+// accumulating.
 template <bool BF, int MODE, bool BIAS, int ACT>
-__device__ __forceinline__ void epi16_x4_k(const Args &p, f32x4 v, f32x4 bv, f32x4 z, int row,
-                                           int col) {
+__device__ __forceinline__ u32x2 epi16_x4_k(const Args &p, f32x4 v, f32x4 bv, f32x4 z,
+                                            f32x4 c_old, u32x2 *zpack) {
     using E = T16<BF>;
     auto rnd = [](f32x4 x) {
 #pragma unroll
         for (int t = 0; t < 4; ++t) x[t] = E::to_f(E::from_f(x[t]));
         return x;
     };
-    auto st4 = [](uint16_t *q, f32x4 x) {
-        *reinterpret_cast<u32x2 *>(q) = u32x2{pack2(E::from_f(x[0]), E::from_f(x[1])),
-                                              pack2(E::from_f(x[2]), E::from_f(x[3]))};
+    auto pk = [](f32x4 x) {
+        return u32x2{pack2(E::from_f(x[0]), E::from_f(x[1])), pack2(E::from_f(x[2]), E::from_f(x[3]))};
     };
     v = rnd(v);
     if constexpr (MODE == 0) {
         if constexpr (BIAS) v = rnd(v + bv);
-        if (p.Z) st4(p.Z + (size_t)row * p.ldz + col, v);
+        *zpack = pk(v);
         if constexpr (ACT != kActNone) {
 #pragma unroll
             for (int t = 0; t < 4; ++t) v[t] = act_fwd(ACT, v[t]);
@@ -403,65 +404,99 @@ __device__ __forceinline__ void epi16_x4_k(const Args &p, f32x4 v, f32x4 bv, f32
         for (int t = 0; t < 4; ++t) v[t] = v[t] * act_grad(ACT, z[t]);
         v = rnd(v);
     }
-    uint16_t *c = p.C + (size_t)row * p.ldc + col;
-    if (p.accumulate) {
-        const u32x2 w = *reinterpret_cast<const u32x2 *>(c);
-        v += f32x4{E::to_f((uint16_t)w[0]), E::to_f((uint16_t)(w[0] >> 16)),
-                   E::to_f((uint16_t)w[1]), E::to_f((uint16_t)(w[1] >> 16))};
-    }
-    st4(c, v);
+    if (p.accumulate) v += c_old;
+    return pk(v);
 }
 
-// MODE 2: the raw fp32 sums of a K slice into its slot.  Blocks (i, j) are
-// unrolled; the four row groups k of a block run as a loop that picks its
-// registers by k, which keeps the code (fetched cold, once per CU and
-// launch) short.  MODE 1 with an activation loads a block's 16 saved
-// pre-activations before its loop.
+__device__ __forceinline__ f32x4 unpack4(bool bf, u32x2 w) {
+    return bf ? f32x4{bf16_to_f((uint16_t)w[0]), bf16_to_f((uint16_t)(w[0] >> 16)),
+                      bf16_to_f((uint16_t)w[1]), bf16_to_f((uint16_t)(w[1] >> 16))}
+              : f32x4{f16_to_f((uint16_t)w[0]), f16_to_f((uint16_t)(w[0] >> 16)),
+                      f16_to_f((uint16_t)w[1]), f16_to_f((uint16_t)(w[1] >> 16))};
+}
+
+// The register epilogue over block pairs (j, j+1), whose columns make
+// 128-byte rows of C: after the quad transposes, lane (h, a, e) holds row
+// 8k + 4h + e of both blocks (8 bytes each); half h sends the other half
+// the block it does not store (__shfl_xor by 32), so that lanes of half h
+// store block j + h of rows 8k + e and 8k + 4 + e -- every store
+// instruction then writes whole 128-byte lines (4 rows).  Storing 64-byte
+// halves of lines from different instructions made the bf16 c5 step's Adam
+// update that follows the backward 379 -> 414 us.  MODE 2: the raw fp32
+// sums of a K slice into its slot, 16 bytes a row per block (whole 128-byte
+// lines already).  Blocks (i, pair) are unrolled; the four row groups k of a
+// block run as a loop that picks its registers by k, which keeps the code
+// (fetched cold, once per CU and launch) short.  MODE 1 with an activation
+// loads a block pair's saved pre-activations before its loop.
 template <bool BF, int TM, int TN, int MODE, bool BIAS, int ACT>
 __device__ __forceinline__ void store_direct16_k(const Args &p, const f32x16 (&acc)[TM][TN],
                                                  int r0, int c0, int lane) {
     using E = T16<BF>;
-    const int l32 = lane & 31, e = lane & 3, a4 = l32 & ~3;
-    const int rl = 4 * (lane >> 5) + e;  // row within each group of 8
+    static_assert(TN % 2 == 0, "block pairs");
+    const int l32 = lane & 31, e = lane & 3, a4 = l32 & ~3, h = lane >> 5;
+    const int rl = 4 * h + e;  // row within each group of 8, before the exchange
+    auto pick = [](const f32x16 &a, int k) {
+        f32x4 x;
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-        const int col = c0 + 32 * j + a4;
-        f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+        for (int q = 0; q < 4; ++q)
+            x[q] = k == 0 ? a[q] : k == 1 ? a[4 + q] : k == 2 ? a[8 + q] : a[12 + q];
+        return x;
+    };
+#pragma unroll
+    for (int jp = 0; jp < TN; jp += 2) {
+        const int col0 = c0 + 32 * jp + a4, col1 = col0 + 32;
+        const int colh = col0 + 32 * h;  // the block this lane stores
+        f32x4 bv0 = {0.f, 0.f, 0.f, 0.f}, bv1 = bv0;
         if constexpr (MODE == 0 && BIAS) {
-            const u32x2 w = *reinterpret_cast<const u32x2 *>(p.bias + col);
-            bv = f32x4{E::to_f((uint16_t)w[0]), E::to_f((uint16_t)(w[0] >> 16)),
-                       E::to_f((uint16_t)w[1]), E::to_f((uint16_t)(w[1] >> 16))};
+            bv0 = unpack4(BF, *reinterpret_cast<const u32x2 *>(p.bias + col0));
+            bv1 = unpack4(BF, *reinterpret_cast<const u32x2 *>(p.bias + col1));
         }
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
-            const f32x16 &a = acc[i][j];
+            const f32x16 &a0 = acc[i][jp], &a1 = acc[i][jp + 1];
             const int rowb = r0 + 32 * i + rl;
             constexpr bool kZs = MODE == 1 && ACT != kActNone;
-            u32x2 zr[4];
+            u32x2 zr0[4], zr1[4];
             if constexpr (kZs) {
 #pragma unroll
-                for (int k = 0; k < 4; ++k)
-                    zr[k] = *reinterpret_cast<const u32x2 *>(p.Zs + (size_t)(rowb + 8 * k) * p.ldzs +
-                                                             col);
+                for (int k = 0; k < 4; ++k) {
+                    const uint16_t *zq = p.Zs + (size_t)(rowb + 8 * k) * p.ldzs;
+                    zr0[k] = *reinterpret_cast<const u32x2 *>(zq + col0);
+                    zr1[k] = *reinterpret_cast<const u32x2 *>(zq + col1);
+                }
             }
 #pragma unroll 1
             for (int k = 0; k < 4; ++k) {
-                f32x4 x;
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    x[q] = k == 0 ? a[q] : k == 1 ? a[4 + q] : k == 2 ? a[8 + q] : a[12 + q];
-                const f32x4 y = quad_transpose4(x, e);
-                const int row = rowb + 8 * k;
+                const f32x4 y0 = quad_transpose4(pick(a0, k), e);
+                const f32x4 y1 = quad_transpose4(pick(a1, k), e);
+                const int row = rowb + 8 * k;                     // this lane's row now
+                const int rowA = r0 + 32 * i + 8 * k + e, rowB = rowA + 4;
                 if constexpr (MODE == 2) {
-                    *reinterpret_cast<f32x4 *>(p.partial + (size_t)row * p.N + col) = y;
+                    *reinterpret_cast<f32x4 *>(p.partial + (size_t)row * p.N + col0) = y0;
+                    *reinterpret_cast<f32x4 *>(p.partial + (size_t)row * p.N + col1) = y1;
                 } else {
-                    f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                    f32x4 z0 = {0.f, 0.f, 0.f, 0.f}, z1 = z0, o0 = z0, o1 = z0;
                     if constexpr (kZs) {
-                        const u32x2 w = k == 0 ? zr[0] : k == 1 ? zr[1] : k == 2 ? zr[2] : zr[3];
-                        z = f32x4{E::to_f((uint16_t)w[0]), E::to_f((uint16_t)(w[0] >> 16)),
-                                  E::to_f((uint16_t)w[1]), E::to_f((uint16_t)(w[1] >> 16))};
+                        z0 = unpack4(BF, k == 0 ? zr0[0] : k == 1 ? zr0[1] : k == 2 ? zr0[2] : zr0[3]);
+                        z1 = unpack4(BF, k == 0 ? zr1[0] : k == 1 ? zr1[1] : k == 2 ? zr1[2] : zr1[3]);
                     }
-                    epi16_x4_k<BF, MODE, BIAS, ACT>(p, y, bv, z, row, col);
+                    if (p.accumulate) {
+                        const uint16_t *cq = p.C + (size_t)row * p.ldc;
+                        o0 = unpack4(BF, *reinterpret_cast<const u32x2 *>(cq + col0));
+                        o1 = unpack4(BF, *reinterpret_cast<const u32x2 *>(cq + col1));
+                    }
+                    u32x2 zp0, zp1;
+                    const u32x2 c0v = epi16_x4_k<BF, MODE, BIAS, ACT>(p, y0, bv0, z0, o0, &zp0);
+                    const u32x2 c1v = epi16_x4_k<BF, MODE, BIAS, ACT>(p, y1, bv1, z1, o1, &zp1);
+                    auto xch = [&](u32x2 w0, u32x2 w1, uint16_t *base, int ld) {
+                        const u32x2 send = h ? w0 : w1;
+                        const u32x2 recv = {(uint32_t)__shfl_xor((int)send[0], 32),
+                                            (uint32_t)__shfl_xor((int)send[1], 32)};
+                        *reinterpret_cast<u32x2 *>(base + (size_t)rowA * ld + colh) = h ? recv : w0;
+                        *reinterpret_cast<u32x2 *>(base + (size_t)rowB * ld + colh) = h ? w1 : recv;
+                    };
+                    if (MODE == 0 && p.Z) xch(zp0, zp1, p.Z, p.ldz);
+                    xch(c0v, c1v, p.C, p.ldc);
                 }
             }
         }
@@ -993,11 +1028,20 @@ __device__ __forceinline__ void gemm16_pipe_body(Args p, int bx, int by) {
         if (do_cs) cs.finish(p, reinterpret_cast<float *>(lds), n0);
     // The whole tile in bounds: the register epilogue (uniform across the
     // workgroup, as the staged one has workgroup barriers).
-    if (p.vec_out && m0 + BM <= p.M && n0 + BN <= p.N && (p.ksplit == 0 || p.N % 4 == 0))
-        store_direct16<BF, TM, TN>(p, acc, m0 + wm0, n0 + wn0, lane);
-    else
+    // It pairs blocks, so it needs an even TN (the 64x64 tile keeps the
+    // staged one); waves holding 256 accumulator registers (the 4-wave
+    // 256x256 tiles) keep it too, as the register epilogue's temporaries
+    // would spill there.
+    constexpr bool kDirect = TN % 2 == 0 && TM * TN <= 8;
+    bool direct = false;
+    if constexpr (kDirect)
+        direct = p.vec_out && m0 + BM <= p.M && n0 + BN <= p.N && (p.ksplit == 0 || p.N % 4 == 0);
+    if (direct) {
+        if constexpr (kDirect) store_direct16<BF, TM, TN>(p, acc, m0 + wm0, n0 + wn0, lane);
+    } else {
         store_tile16<BF, TM, TN, WTN, NW>(p, acc, reinterpret_cast<float *>(lds), m0 + wm0,
                                           n0 + wn0, wave, lane);
+    }
 }
 
 template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC, bool BF>
