@@ -10,21 +10,30 @@
 // second time (defect).
 //
 // Here one workgroup owns one row.  The fast path keeps the whole row in
-// registers (NV float4 per thread; 256 threads, or 512 for rows of more
+// registers (NV float4 per thread; 256 threads, or 1024 for rows of more
 // than 16384 columns: up to 32768 columns), so the logits are read from HBM
 // exactly once and dlogits written exactly once: 8*C bytes per row, the
 // minimum.  Reductions are wavefront shuffles (64 lanes) followed by one LDS
 // exchange across the waves.  Rows too long for registers, or not 16-byte
 // aligned, use a two-pass streaming kernel with an online max/sum.
 //
-// Long rows: 512 threads with 16 float4 each, read and written with buffer
-// instructions, take 363.5 us on the 8192 x 32000 CE (5.77 TB/s) against
-// 372.5 us for 256 threads with 32 float4 and plain global accesses.
-// Measured and dropped: rotating each row's chunk order by the row index
-// (366.9 us), holding the 512-thread kernel to 80 VGPRs for a sixth wave per
-// SIMD (it then spills: 381 us), 256 threads with buffer instructions
-// (377 us).  For scale, a flat copy of the same bytes reaches 6.6 TB/s, and a
-// copy kernel with this kernel's row structure 5.6-5.9 TB/s.
+// Long rows (up to 32768 columns): 1024 threads with 8 float4 each, held
+// to 64 VGPRs so that two workgroups share a CU, read and written with
+// buffer instructions: the 8192 x 32000 CE at 5.76-5.84 TB/s (median of 30)
+// against 5.70-5.75 for 512 threads with 16 float4 (two or three
+// workgroups per CU) and 4.5-4.8 for 1024 threads at 4 waves per SIMD (one
+// workgroup per CU: its reductions and exponentials leave the CU's memory
+// idle).  Earlier, on the 512-thread kernel: 363.5 us (5.77 TB/s) against
+// 372.5 us for 256 threads with 32 float4 and plain global accesses; measured
+// and dropped: rotating each row's chunk order by the row index (366.9 us),
+// holding the 512-thread kernel to 80 VGPRs for a sixth wave per SIMD (it
+// then spills: 381 us), 256 threads with buffer instructions (377 us).  For
+// scale: a flat copy of the same bytes reaches 6.5-6.6 TB/s, and copy kernels
+// with this kernel's row structure (one workgroup reads a 128 KB row into
+// registers, reduces it, writes it) 5.8 TB/s with 512 threads and 6.0 with
+// 1024; capping each wave's loads in flight at 4, 8 or 12 of 16, walking the
+// rows in another order, or a persistent workgroup that loads the next row
+// while it finishes one leave them within 1-3 %.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -139,8 +148,12 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kBufWord3 = 0x00020000;  // buffer descriptor word 3 for gfx9 targets
 constexpr int kBufNT = 2;              // cache-policy bits: non-temporal
 
+// A 1024-thread workgroup is held to 64 VGPRs (8 waves per SIMD), so that
+// two rows share a CU and one's reductions and exponentials overlap the
+// other's memory traffic.
 template <int NV, int NT>
-__global__ __launch_bounds__(NT) void softmax_rows_v4(const float *__restrict__ x, int ldx,
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(NT >= 1024 ? 8 : 1)))
+void softmax_rows_v4(const float *__restrict__ x, int ldx,
                                                       const uint32_t *__restrict__ labels, int C,
                                                       float scale, float *__restrict__ row_loss,
                                                       float *__restrict__ out, int ldo,
@@ -589,8 +602,8 @@ int launch_rows(fg_ctx *ctx, int dt, const void *x, int ldx, const uint32_t *lab
             FG_SM_LAUNCH(8, kNT);
         else if (aligned && C4 <= kNT * 16)
             FG_SM_LAUNCH(16, kNT);
-        else if (aligned && C4 <= 2 * kNT * 16)
-            FG_SM_LAUNCH(16, 2 * kNT);
+        else if (aligned && C4 <= 4 * kNT * 8)
+            FG_SM_LAUNCH(8, 4 * kNT);
         else
             softmax_rows_stream<<<grid, block, 0, st>>>(x, ldx, labels, C, scale, row_loss, out,
                                                         ldo, argmax, dt, probs, ldp);
