@@ -515,7 +515,9 @@ def hbm_roof_component(reps: int):
     k_hbm_roof.hip (16-byte non-temporal accesses, one 4 KiB chunk per block
     pass): a read-only stream of 1 GiB, a 1 GiB copy, 3 streams read and 3
     written (the elementwise program's count) and 4 read and 3 written
-    (Adam's) over 256 MiB each.  Bytes counted = bytes moved."""
+    (Adam's) over 256 MiB each, and the softmax + CE kernel's row structure
+    on c3's 8192 x 32000 (one workgroup per 128 KB row: read it all, reduce,
+    write it all).  Bytes counted = bytes moved."""
     import ctypes
 
     import torch
@@ -550,6 +552,14 @@ def hbm_roof_component(reps: int):
     p = [vp(t.data_ptr()) for t in x]
     rec("s3r3w_256mib", lambda: check(lib.fg_roof_s3r3w(stream, *p, u64(n))), 24 * n)
     rec("s4r3w_256mib", lambda: check(lib.fg_roof_s4r3w(stream, *p[:4], u64(n))), 28 * n)
+    del x, p
+    # The softmax + CE row structure on c3's shape (a read and a write per
+    # element): 512 and 1024 threads per 128 KB row.
+    R, C = 8192, 32000
+    xs, ys = torch.ones((R, C), device="cuda"), torch.empty((R, C), device="cuda")
+    for wide, key in ((0, "rows512_8192x32000"), (1, "rows1024_8192x32000")):
+        rec(key, lambda: check(lib.fg_roof_rows(stream, vp(xs.data_ptr()), vp(ys.data_ptr()),
+                                                R, C, wide)), 8 * R * C)
     return {"hbm_roof": out}
 
 

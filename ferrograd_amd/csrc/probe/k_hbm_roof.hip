@@ -12,8 +12,15 @@
 //           count of the elementwise program tanh(a * b + c))
 //   s4r3w:  p, m, v updated from p, g, m, v with multiply-adds (4 read,
 //           3 write: the stream count of Adam)
+//   rows:   y = x - rowmax(x) over rows of C <= 32768 floats, with the row
+//           structure of the softmax + CE kernel: one workgroup reads its
+//           whole row into registers (16-byte buffer loads), reduces it
+//           across the workgroup, then writes it -- 512 threads x 16 float4,
+//           or 1024 threads x 8 float4 held to 64 VGPRs (two workgroups per
+//           CU) as the softmax kernel runs rows of more than 16384 columns
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdint>
 
 namespace {
@@ -69,6 +76,51 @@ __global__ __launch_bounds__(kThreads) void s4r3w_k(f32x4 *p, const f32x4 *g, f3
     }
 }
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kBufWord3 = 0x00020000;  // buffer descriptor word 3 for gfx9 targets
+constexpr int kBufNT = 2;              // cache-policy bits: non-temporal
+
+// Chunk k (NT float4) of a row: a descriptor whose range ends at the row's
+// end, so lanes past it read zero and have their stores dropped.
+template <int NT>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const float *row, int C, int k) {
+    const int skip = k * NT * 16;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(row) + skip / 4, (short)0,
+                                             max(C * 4 - skip, 0), kBufWord3);
+}
+
+template <int NV, int NT>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(NT >= 1024 ? 8 : 1)))
+void rows_k(const float *x, float *y, int C) {
+    constexpr int NW = NT / 64;
+    __shared__ float sm[NW];
+    const float *xr = x + (size_t)blockIdx.x * C;
+    float *yr = y + (size_t)blockIdx.x * C;
+    const int off = (int)threadIdx.x * 16;
+    f32x4 v[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+        v[i] = __builtin_bit_cast(
+            f32x4, __builtin_amdgcn_raw_buffer_load_b128(row_rsrc<NT>(xr, C, i), off, 0, kBufNT));
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const bool in = (int)threadIdx.x + NT * i < C / 4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) m = in ? fmaxf(m, v[i][e]) : m;
+    }
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if ((threadIdx.x & 63) == 0) sm[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = sm[0];
+#pragma unroll
+    for (int k = 1; k < NW; ++k) m = fmaxf(m, sm[k]);
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[i] - m),
+                                               row_rsrc<NT>(yr, C, i), off, 0, kBufNT);
+}
+
 // One block per 4 KiB chunk up to the 32-bit work-item limit; the loops
 // cover the rest.
 unsigned blocks_for(uint64_t nq) {
@@ -114,5 +166,17 @@ extern "C" __attribute__((visibility("default"))) int fg_roof_s4r3w(void *stream
     s4r3w_k<<<blocks_for(n / 4), kThreads, 0, (hipStream_t)stream>>>(
         reinterpret_cast<f32x4 *>(p), reinterpret_cast<const f32x4 *>(g),
         reinterpret_cast<f32x4 *>(m), reinterpret_cast<f32x4 *>(v), n / 4);
+    return status();
+}
+// R rows of C floats (C % 4 == 0, 0 < C <= 32768, rows 16-byte aligned and
+// contiguous); wide: the 1024-thread form.
+extern "C" __attribute__((visibility("default"))) int fg_roof_rows(void *stream, const float *x,
+                                                                   float *y, int R, int C,
+                                                                   int wide) {
+    if (R <= 0 || C <= 0 || C % 4 != 0 || C > 32768) return 1;
+    if (wide)
+        rows_k<8, 1024><<<R, 1024, 0, (hipStream_t)stream>>>(x, y, C);
+    else
+        rows_k<16, 512><<<R, 512, 0, (hipStream_t)stream>>>(x, y, C);
     return status();
 }
