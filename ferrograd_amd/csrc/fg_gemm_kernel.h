@@ -709,9 +709,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_f32_mfma(GemmArgs p) {
     gemm_f32_mfma_body<BM, BN, BK, WGM, WGN, AK, BNC, VEC, PRO>(p, blockIdx.x, blockIdx.y);
 }
 
-// KT: K need not be a multiple of BK (staged tiles, no prologue): the last
-// tile's chunks past K are loaded from a clamped address and zeroed before
-// their LDS write, so they add nothing to any output.
+// KT: K need not be a multiple of BK (staged tiles, no prologue): the tile
+// loop runs over the whole tiles only, and the K % BK values of k past them
+// are multiplied into the accumulators straight from global memory at the
+// end (see the K tail below), so the loop keeps the whole-tile addressing.
 // LDS of the pipelined kernel, in floats: its stages (staged tiles: two;
 // direct: three when they fit in the 160 KiB of LDS, else two) or the
 // epilogue's staging, whichever is larger.
@@ -777,34 +778,18 @@ __device__ __forceinline__ void gemm_f32_pipe_body(GemmArgs p, int bx, int by) {
     // Source address of this lane's chunk for wave load `li` of an operand:
     // the chunk's position in the stage fixes (row, physical chunk); the
     // swizzle gives the logical chunk to fetch.
-    // (KT: a chunk past K is fetched from the last valid k; staged_value
-    // zeroes it.)
     auto src_kc = [&](const float *base, int ld, int r0, int rmax, int k0, int pos) {
         const int row = pos / (BK / 4), pc = pos % (BK / 4);
         const int c = pc ^ swz_k<BK>(row);
         const float *rp = base + (size_t)min(r0 + row, rmax - 1) * ld;
         // Whole tiles: the per-lane part (row, chunk) stays loop-invariant
         // and k0 is added as a uniform offset.
-        if constexpr (KT) return rp + min(k0 + 4 * c, p.K - 4);
         return rp + 4 * c + k0;
     };
     auto src_rc = [&](const float *base, int ld, int r0, int rmax, int k0, int pos, int R) {
         const int k = pos / (R / 4), pc = pos % (R / 4);
         const int c = pc ^ swz_r(k);
-        int kk = k0 + k;
-        if constexpr (KT) kk = min(kk, p.K - 1);
-        return base + (size_t)kk * ld + min(r0 + 4 * c, rmax - 4);
-    };
-    // The tile-local k of this lane's chunk of wave load q.
-    auto koff_of = [&](int q) -> int {
-        if (q < kPerA) {
-            const int pos = (wave * kPerA + q) * 64 + lane;
-            if constexpr (AK) return 4 * ((pos % (BK / 4)) ^ swz_k<BK>(pos / (BK / 4)));
-            return pos / (BM / 4);
-        }
-        const int pos = (wave * kPerB + (q - kPerA)) * 64 + lane;
-        if constexpr (BNC) return pos / (BN / 4);
-        return 4 * ((pos % (BK / 4)) ^ swz_k<BK>(pos / (BK / 4)));
+        return base + (size_t)(k0 + k) * ld + min(r0 + 4 * c, rmax - 4);
     };
     // Wave load q (0 .. kLoads-1) of a tile: this wave's share of A first,
     // then of B.  Source of this lane's chunk, and its place in a stage.
@@ -866,16 +851,14 @@ __device__ __forceinline__ void gemm_f32_pipe_body(GemmArgs p, int bx, int by) {
         }
         return *reinterpret_cast<const f32x4 *>(src);
     };
-    // Chunk q of register set (R, Z), holding tile kst, as it goes to LDS.
-    auto staged_value = [&](const f32x4 *R, const f32x4 *Zr, int q, int kst) -> f32x4 {
+    // Chunk q of register set (R, Z) as it goes to LDS.
+    auto staged_value = [&](const f32x4 *R, const f32x4 *Zr, int q, int) -> f32x4 {
         if constexpr (PRO != kProNone)
             if (is_pro(q)) return pro_scale<pro_act(PRO)>(R[q], Zr[q - kProFirst]);
-        if constexpr (KT)
-            if (kst * BK + koff_of(q) >= p.K) return f32x4{0.f, 0.f, 0.f, 0.f};
         return R[q];
     };
 
-    const int nk = KT ? (p.K + BK - 1) / BK : p.K / BK;
+    const int nk = p.K / BK;  // whole tiles (KT: the rest is the K tail)
     constexpr bool kTN = !AK && BNC;
     ColSum<BN, BK, 64 * NW> cs;
     const bool do_cs = kTN && p.colsum && tile_m == 0;
@@ -1149,6 +1132,72 @@ __device__ __forceinline__ void gemm_f32_pipe_body(GemmArgs p, int bx, int by) {
                 tile(kt, min(kt + kAhead, nk - 1), (kt + kAhead) % kStages, nullptr, nullptr,
                      nullptr, nullptr);
             wait_vmcnt<0>();  // the reloads past the last tile, before the LDS reuse
+        }
+    }
+    // K tail (KT): k = kb .. K-1 past the whole tiles, multiplied straight
+    // from global memory in the order the tile loop takes a tile (MFMA step
+    // s of group g, blocks i then j; lane half h supplies k = kb + k_of(g) +
+    // s), as from a last tile zero-filled past K: a group whose k are all
+    // past K is skipped, and a lane supplies zeros for its k past K.  A lane
+    // takes the four k of a group from a k-contiguous operand with one
+    // 16-byte load (K % 4 == 0 there), from a row-contiguous one with four
+    // loads that are coalesced across the lanes; every address is clamped
+    // into the operand, and all loads go out before the first MFMA.  The
+    // column sums (TN) take the same k, after the tiles'.
+    if constexpr (KT) {
+        const int kb = nk * BK;
+        if (kb < p.K) {
+            int arow[TM], bcol[TN];
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+                arow[i] = min(m0 + wm0 + (IA > 1 ? TM * l32 + i : 32 * i + l32), p.M - 1);
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                bcol[j] = min(n0 + wn0 + (IB > 1 ? TN * l32 + j : 32 * j + l32), p.N - 1);
+            // Four k from k4 of row r of a k-contiguous operand, or of
+            // column r of a row-contiguous one; zeros past K.
+            auto four = [&](const float *base, int ld, bool kc, int r, int k4) {
+                f32x4 v;
+                if (kc) {
+                    v = *reinterpret_cast<const f32x4 *>(base + (size_t)r * ld + min(k4, p.K - 4));
+                    if (k4 >= p.K) v = f32x4{0.f, 0.f, 0.f, 0.f};
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float x = base[(size_t)min(k4 + e, p.K - 1) * ld + r];
+                        v[e] = k4 + e < p.K ? x : 0.0f;
+                    }
+                }
+                return v;
+            };
+            f32x4 ta[NG][TM], tb[NG][TN];
+#pragma unroll
+            for (int g = 0; g < NG; ++g) {
+                if (kb + (g >> 1) * 16 + 4 * (g & 1) >= p.K) continue;  // uniform
+                const int k4 = kb + k_of(g);
+#pragma unroll
+                for (int i = 0; i < TM; ++i) ta[g][i] = four(p.A, p.lda, AK, arow[i], k4);
+#pragma unroll
+                for (int j = 0; j < TN; ++j) tb[g][j] = four(p.B, p.ldb, !BNC, bcol[j], k4);
+            }
+#pragma unroll
+            for (int g = 0; g < NG; ++g) {
+                if (kb + (g >> 1) * 16 + 4 * (g & 1) >= p.K) continue;
+#pragma unroll
+                for (int st = 0; st < 4; ++st)
+#pragma unroll
+                    for (int i = 0; i < TM; ++i)
+#pragma unroll
+                        for (int j = 0; j < TN; ++j)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                                ta[g][i][st], tb[g][j][st], acc[i][j], 0, 0, 0);
+            }
+            if constexpr (kTN)
+                if (do_cs)
+                    cs.add([&](int k, int c) {
+                        const int kk = kb + k;
+                        return kk < p.K ? p.B[(size_t)kk * p.ldb + min(n0 + c, p.N - 1)] : 0.0f;
+                    });
         }
     }
     __syncthreads();  // every wave past its last tile read before the stage reuse

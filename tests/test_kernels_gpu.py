@@ -385,8 +385,12 @@ def test_linear_bwd_relu_mask_from_output(gpu_ctx, mat):
     (O.TN, 4096, 4096, 16, "fwd"),     # one K tile (256x128, 4 waves, BK 16)
     # K % BK != 0: the register-staged kernel with the same tiles
     (O.NT, 2048, 4096, 1000, "bwd"),   # 256x128, 8 waves (c5 head dA)
+    (O.NT, 2048, 4096, 1020, "bwd"),   # a 28-deep tail: every MFMA group of the tail tile
     (O.TN, 1024, 4096, 1000, "fwd"),   # 128x64, row-contiguous operands
+    (O.TN, 1024, 4096, 1001, "fwd"),   # odd K: a lane half past K in the last tail step
+    (O.TN, 4096, 4096, 2020, "bwd"),   # 256x128, 8 waves, interleaved TN fragments
     (O.NN, 2048, 4096, 20, "fwd"),     # K below one tile
+    (O.NT, 2048, 4096, 12, "bwd"),     # K below one tile, NT
 ], ids=lambda c: f"{['NN', 'NT', 'TN'][c[0]]}-{c[1]}x{c[2]}x{c[3]}-{c[4]}")
 def test_gemm_pipe_configs_sampled(gpu_ctx, case):
     """The large tile configurations at full size (and the same tiles for K
@@ -552,13 +556,16 @@ def test_bias_grad_parity(gpu_ctx, shape):
 
 
 @pytest.mark.parametrize("shape", [(256, 4096, 2048), (1024, 4096, 2048), (96, 128, 64),
-                                   (784, 256, 64), (37, 29, 300), (130, 200, 33), (4096, 1000, 2048)],
+                                   (784, 256, 64), (37, 29, 300), (130, 200, 33), (4096, 1000, 2048),
+                                   (1024, 4096, 1000), (256, 512, 999)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_gemm_dw_fused_bias_grad(gpu_ctx, shape):
     """dW = A^T.dZ and dbias = column sums of dZ in one launch (TN layout):
     dW to the GEMM tolerance, dbias to 1e-5 of the float64 column sums, both
     with and without accumulation.  The shapes cover the pipelined path
-    (K a multiple of 32) and the other kernel (K = 300, 33)."""
+    (K a multiple of 32, and K = 1000, 999 with the K tail's rows added to
+    the column sums after the whole tiles') and the other kernel (K = 300,
+    33, whose M is not a multiple of 4)."""
     M, N, K = shape  # dW is M x N; the reduction runs over K rows
     note(f"gemm_dw M={M} N={N} K={K}")
     rng = np.random.default_rng(M + 3 * N + K)
