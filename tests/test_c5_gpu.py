@@ -33,8 +33,10 @@ f32 = np.float32
 DIMS, BATCH = [1024] + [4096] * 7 + [1000], 2048
 
 
-def build_c5(gpu_ctx):
-    """The c5 graph, its plan and its bound inputs (host copies kept)."""
+def build_c5(gpu_ctx, kind="f32"):
+    """The c5 graph, its plan and its bound inputs (host copies kept); kind
+    "bf16" builds every tensor in bfloat16 (inputs rounded once from the
+    same fp32 draws)."""
     import ferrograd_amd as fa
     from ferrograd_amd import graph as G
 
@@ -46,10 +48,10 @@ def build_c5(gpu_ctx):
     fd = [meta.new_field() for _ in dims]
     w_nodes, b_nodes = [], []
     with graph.define_ops() as ops:
-        x_node = h = ops.input([fb, fd[0]], trainable=False)
+        x_node = h = ops.input([fb, fd[0]], kind, trainable=False)
         for l in range(L):
-            W = ops.input([fd[l], fd[l + 1]])
-            b = ops.input([fd[l + 1]])
+            W = ops.input([fd[l], fd[l + 1]], kind)
+            b = ops.input([fd[l + 1]], kind)
             w_nodes.append(W)
             b_nodes.append(b)
             z = ops.bias_add(ops.matmul(h, W), b)
@@ -62,9 +64,14 @@ def build_c5(gpu_ctx):
     Ws = [fa.rng_uniform(4, 10 + l, (dims[l], dims[l + 1]), -math.sqrt(6 / dims[l]),
                          math.sqrt(6 / dims[l])) for l in range(L)]
     bs = [np.zeros(d, f32) for d in dims[1:]]
-    ins = [ctx.init_tensor_f32(X.shape, X)]
+    def dev(a):
+        if kind == "bf16":
+            return ctx.init_tensor_bf16(a.shape, O.from_f32(O.BF16, a))
+        return ctx.init_tensor_f32(a.shape, a)
+
+    ins = [dev(X)]
     for W, b in zip(Ws, bs):
-        ins += [ctx.init_tensor_f32(W.shape, W), ctx.init_tensor_f32(b.shape, b)]
+        ins += [dev(W), dev(b)]
     tgt = ctx.new_onehot_init(y)
     sch = ctx.schedule(graph.lower(meta), mb, ins, st)
     return dict(ctx=ctx, st=st, sch=sch, ins=ins, tgt=tgt, X=X, y=y, Ws=Ws, bs=bs,
@@ -135,18 +142,22 @@ def test_c5_full_size_step_matches_oracle(gpu_ctx):
     free_c5(c)
 
 
-def test_c5_captured_step_matches_eager_bit_for_bit(gpu_ctx):
+@pytest.mark.parametrize("kind", ["f32", "bf16"])
+def test_c5_captured_step_matches_eager_bit_for_bit(gpu_ctx, kind):
     """Two c5 plans from identical inputs: one runs two eager steps (forward,
     loss, backward, optimiser as separate calls), the other captures the
     whole step once and replays it twice.  After each step every parameter,
     gradient (dX included), Adam m and v, the mean loss, the per-row losses
-    and the probabilities agree bit for bit."""
+    and the probabilities agree bit for bit.  With bf16 tensors (the step
+    bench.py times beside the fp32 one) the step runs other kernels: the
+    16-bit dW + dX pairs, K-split GEMMs with their summing kernels, Adam as
+    one launch after the backward."""
     from ferrograd_amd._lib import call
 
     snaps = []
     for captured in (False, True):
-        print(f"c5 {'captured' if captured else 'eager'} plan", flush=True)
-        c = build_c5(gpu_ctx)
+        print(f"c5 {kind} {'captured' if captured else 'eager'} plan", flush=True)
+        c = build_c5(gpu_ctx, kind)
         ctx, st, sch = c["ctx"], c["st"], c["sch"]
         if captured:
             call("fg_plan_bind_target", sch.plan.handle, c["tgt"].data_ptr(), c["tgt"].nbytes)
