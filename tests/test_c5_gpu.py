@@ -18,7 +18,10 @@ do (the final softmax elided into the loss, the Adam step counter advanced
 on the device), so two steps of a captured plan are compared bit for bit with
 two eager steps of an identical plan: every parameter, every gradient
 (dX of the data input included), Adam m and v, the mean loss, the per-row
-losses and the probabilities."""
+losses and the probabilities -- for fp32 and for bf16 tensors.
+
+The last test runs the step with bf16 tensors against the oracle's 16-bit
+composition at the same full size."""
 import math
 
 import numpy as np
@@ -197,3 +200,86 @@ def test_c5_captured_step_matches_eager_bit_for_bit(gpu_ctx, kind):
             assert np.array_equal(a, b), (step, "adam state", k)
     # The two steps did move the parameters (the comparison is not vacuous).
     assert not np.array_equal(eager[0]["params"][1], eager[1]["params"][1])
+
+
+def test_c5_bf16_full_size_step_matches_oracle(gpu_ctx):
+    """The c5 step with every tensor in bfloat16 (the step bench.py times
+    beside the fp32 one), at its real size, against the oracle's 16-bit
+    composition in the same node order: each GEMM sums in fp32 and rounds
+    once, bias-add and GELU nodes are each rounded (forward), the loss takes
+    the widened logits and dlogits are rounded, act' is applied to the
+    rounded data gradient and rounded again, column sums are rounded once.
+    The GPU sums in another order, so a value that falls on a rounding
+    boundary may land one unit in the last place (ulp, 2^-7 relative) away
+    and carry that into later layers: every gradient must agree within two
+    ulps normwise, as the 2-layer 16-bit step does (the composition through
+    eight layers measured at most 1.3 ulps, at the first layer's dW and the
+    data input's dX), the mean loss within two ulps; Adam step 1 on the
+    GPU's own gradients (fp32 update, the parameter rounded once) bit for
+    bit."""
+    from ferrograd_amd import graph as G
+
+    L = len(DIMS) - 1
+    dt = O.BF16
+    ulp = 2.0 ** -7
+    print(f"c5 bf16 full size: dims {DIMS}, batch {BATCH}", flush=True)
+    c = build_c5(gpu_ctx, "bf16")
+    ctx, st, sch, ins = c["ctx"], c["st"], c["sch"], c["ins"]
+    X16 = O.from_f32(dt, c["X"])
+    W16 = [O.from_f32(dt, W) for W in c["Ws"]]
+    b16 = [O.from_f32(dt, b) for b in c["bs"]]
+    y = c["y"]
+    ctx.dispatch_forward(sch)
+    ctx.dispatch_loss(sch, c["tgt"])
+    ctx.dispatch_backward(sch)
+    ctx.sync()
+    gmap = {t.node: t for t in st.grad_tensors}
+
+    def f(t):
+        return G.bf16_to_f32(ctx.download(t))
+
+    dX_gpu = f(gmap[c["x_node"]]).reshape(X16.shape)
+    dW_gpu = [f(gmap[n]).reshape(W.shape) for n, W in zip(c["w_nodes"], W16)]
+    db_gpu = [f(gmap[n]) for n in c["b_nodes"]]
+    loss_gpu = float(ctx.download(st.mean_loss)[0])
+    ctx.dispatch_optim(sch)
+    ctx.sync()
+    print("c5 bf16 full size: GPU step done; oracle step", flush=True)
+
+    Zs, Hs, inp = [], [], X16
+    for l in range(L):
+        if l < L - 1:
+            H, Z = O.gemm_x16(dt, O.NN, inp, W16[l], bias=b16[l], act=O.ACT_GELU, want_z=True)
+        else:
+            Z = O.gemm_x16(dt, O.NN, inp, W16[l], bias=b16[l])
+            H = Z
+        Zs.append(Z)
+        Hs.append(H)
+        inp = H
+    _, d, _, mean = O.softmax_ce(O.to_f32(dt, Zs[-1]), y)
+    dZ = O.from_f32(dt, d)
+    print(f"loss: gpu {loss_gpu:.6f} oracle {mean:.6f}", flush=True)
+    assert abs(loss_gpu - mean) <= 2 * ulp * max(1.0, abs(mean)), (loss_gpu, mean)
+    for l in range(L - 1, -1, -1):
+        prev = Hs[l - 1] if l > 0 else X16
+        dW = O.to_f32(dt, O.gemm_x16(dt, O.TN, prev, dZ))
+        db = O.to_f32(dt, O.from_f32(dt, O.to_f32(dt, dZ).astype(np.float64).sum(0).astype(f32)))
+        e_w, e_b = normwise_rel(dW_gpu[l], dW), normwise_rel(db_gpu[l], db)
+        print(f"layer {l}: dW {e_w / ulp:.2f} ulp, db {e_b / ulp:.2f} ulp", flush=True)
+        assert e_w <= 2 * ulp and e_b <= 2 * ulp, (l, e_w, e_b)
+        if l > 0:
+            dZ = O.gemm_bwd_x16(dt, O.NT, dZ, W16[l], act=O.ACT_GELU, Zs=Zs[l - 1])
+        else:
+            e_x = normwise_rel(dX_gpu, O.to_f32(dt, O.gemm_bwd_x16(dt, O.NT, dZ, W16[0])))
+            print(f"data input: dX {e_x / ulp:.2f} ulp", flush=True)
+            assert e_x <= 2 * ulp, e_x
+
+    s, r = O.adam_scalars(f32(1e-3), f32(0.9), f32(0.999), 1)
+    for k, (p16, g) in enumerate(zip([w for pair in zip(W16, b16) for w in pair],
+                                     [g for pair in zip(dW_gpu, db_gpu) for g in pair])):
+        p = O.to_f32(dt, p16).reshape(-1).copy()
+        O.adam_(p, np.ascontiguousarray(g, f32).reshape(-1).copy(), np.zeros_like(p),
+                np.zeros_like(p), f32(0.9), f32(0.999), f32(1e-8), s, r)
+        got = ctx.download(ins[k + 1]).reshape(-1)
+        assert np.array_equal(got, O.from_f32(dt, p)), k
+    free_c5(c)
