@@ -391,6 +391,8 @@ def test_linear_bwd_relu_mask_from_output(gpu_ctx, mat):
     (O.TN, 4096, 4096, 2020, "bwd"),   # 256x128, 8 waves, interleaved TN fragments
     (O.NN, 2048, 4096, 20, "fwd"),     # K below one tile
     (O.NT, 2048, 4096, 12, "bwd"),     # K below one tile, NT
+    (O.NN, 2000, 4000, 1000, "fwd"),   # K tail on partial M and N edge tiles
+    (O.NT, 1000, 1000, 996, "bwd"),    # 64x64 tiles, BK 16, a 4-deep tail, partial tiles
 ], ids=lambda c: f"{['NN', 'NT', 'TN'][c[0]]}-{c[1]}x{c[2]}x{c[3]}-{c[4]}")
 def test_gemm_pipe_configs_sampled(gpu_ctx, case):
     """The large tile configurations at full size (and the same tiles for K
