@@ -1526,8 +1526,10 @@ int ensure_mt(fg_plan &P) {
 // ahead of them.  c5 fp32 step: 10.02-10.03 ms with the single update at
 // the end; 9.86-9.90 with 256 or 512 workgroups per group; 9.98-10.01 with
 // 1024; 10.2 / 11.0 / 13.0 ms with 128 / 64 / 32 (too slow to finish
-// within the backward).
+// within the backward).  The update beside the final launch is the
+// exception (kSideAdamFinalBlocks, below).
 constexpr uint32_t kSideAdamBlocks = 256;
+constexpr uint32_t kSideAdamFinalBlocks = 1024;
 int run_bwd_adam_overlapped(fg_plan &P, const std::vector<Launch> &bwd) {
     fg_ctx *ctx = &P.wctx;
     if (int rc = fg::adam_dev_advance(ctx, P.lr, P.b1, P.b2, P.ptr(P.adam_slot))) return rc;
@@ -1547,14 +1549,21 @@ int run_bwd_adam_overlapped(fg_plan &P, const std::vector<Launch> &bwd) {
         pending.push_back(g);
         return FG_OK;
     };
-    auto issue = [&](bool last) -> int {
+    // The update issued beside the backward's final launch has the least
+    // time to finish before the step ends (the forward of the next step waits
+    // for it), and the pair launches raise their waves' priority over it: it
+    // takes a 1024-workgroup grid (c5 step -31..-36 us against 256, three
+    // passes on one box; a full grid -31 us).
+    auto issue = [&](bool last, bool beside_final = false) -> int {
         for (size_t g : pending) {
             FG_HIP(hipStreamWaitEvent(P.side, P.events[g], 0));
             forked = true;
             // Nothing runs beside the backward's last updates: a full grid.
             if (int r = fg::mt_adam_dev_update(P.mt_groups[g], P.side, P.b1, P.b2, P.eps,
                                                P.ptr(P.adam_slot), 0,
-                                               last ? 0u : kSideAdamBlocks))
+                                               last           ? 0u
+                                               : beside_final ? kSideAdamFinalBlocks
+                                                              : kSideAdamBlocks))
                 return r;
         }
         pending.clear();
@@ -1564,7 +1573,11 @@ int run_bwd_adam_overlapped(fg_plan &P, const std::vector<Launch> &bwd) {
     for (size_t g = 0; g < G && rc == FG_OK; ++g)  // inputs the backward never touches
         if (P.mt_group_after[g] < 0) rc = mark(g);
     const std::function<int(size_t)> after = [&](size_t last) -> int {
-        if (int r = issue(false)) return r;
+        // The group about to run starts at launch last + 1; a pair or chain
+        // spans two launches.  (Only the grid size depends on this.)
+        const size_t nx = last + 1;
+        const bool two = nx < bwd.size() && (bwd[nx].pair_next || bwd[nx].chain_next);
+        if (int r = issue(false, nx + (two ? 1 : 0) + 1 >= bwd.size())) return r;
         for (size_t g = 0; g < G; ++g)
             if (P.mt_group_after[g] == (int)last)
                 if (int r = mark(g)) return r;
