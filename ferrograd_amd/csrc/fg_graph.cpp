@@ -1526,10 +1526,20 @@ int ensure_mt(fg_plan &P) {
 // ahead of them.  c5 fp32 step: 10.02-10.03 ms with the single update at
 // the end; 9.86-9.90 with 256 or 512 workgroups per group; 9.98-10.01 with
 // 1024; 10.2 / 11.0 / 13.0 ms with 128 / 64 / 32 (too slow to finish
-// within the backward).  The update beside the final launch is the
-// exception (kSideAdamFinalBlocks, below).
-constexpr uint32_t kSideAdamBlocks = 256;
-constexpr uint32_t kSideAdamFinalBlocks = 1024;
+// within the backward).  Since the pair launches raise their waves' issue
+// priority over the update (k_gemm_pair.hip), larger grids finish the
+// updates sooner at less cost to the pairs: 512 workgroups per group, and
+// 1024 for the update beside the final launch, whose end the step waits for:
+// 9.607 ms per c5 step, against 9.624 with 512 for every group and 9.650
+// with 256 (1024 beside the last two launches), three passes on one box.
+#ifndef FG_SIDE_ADAM_BLOCKS  // knobs for measurement builds
+#define FG_SIDE_ADAM_BLOCKS 512
+#endif
+#ifndef FG_SIDE_ADAM_FINAL_BLOCKS
+#define FG_SIDE_ADAM_FINAL_BLOCKS 1024
+#endif
+constexpr uint32_t kSideAdamBlocks = FG_SIDE_ADAM_BLOCKS;
+constexpr uint32_t kSideAdamFinalBlocks = FG_SIDE_ADAM_FINAL_BLOCKS;
 int run_bwd_adam_overlapped(fg_plan &P, const std::vector<Launch> &bwd) {
     fg_ctx *ctx = &P.wctx;
     if (int rc = fg::adam_dev_advance(ctx, P.lr, P.b1, P.b2, P.ptr(P.adam_slot))) return rc;
@@ -1549,11 +1559,6 @@ int run_bwd_adam_overlapped(fg_plan &P, const std::vector<Launch> &bwd) {
         pending.push_back(g);
         return FG_OK;
     };
-    // The update issued beside the backward's final launch has the least
-    // time to finish before the step ends (the forward of the next step waits
-    // for it), and the pair launches raise their waves' priority over it: it
-    // takes a 1024-workgroup grid (c5 step -31..-36 us against 256, three
-    // passes on one box; a full grid -31 us).
     auto issue = [&](bool last, bool beside_final = false) -> int {
         for (size_t g : pending) {
             FG_HIP(hipStreamWaitEvent(P.side, P.events[g], 0));
@@ -1573,11 +1578,9 @@ int run_bwd_adam_overlapped(fg_plan &P, const std::vector<Launch> &bwd) {
     for (size_t g = 0; g < G && rc == FG_OK; ++g)  // inputs the backward never touches
         if (P.mt_group_after[g] < 0) rc = mark(g);
     const std::function<int(size_t)> after = [&](size_t last) -> int {
-        // The group about to run starts at launch last + 1; a pair or chain
-        // spans two launches.  (Only the grid size depends on this.)
-        const size_t nx = last + 1;
-        const bool two = nx < bwd.size() && (bwd[nx].pair_next || bwd[nx].chain_next);
-        if (int r = issue(false, nx + (two ? 1 : 0) + 1 >= bwd.size())) return r;
+        // Called after the final launch group too (last = bwd.size() - 1):
+        // the updates issued then run beside that final launch.
+        if (int r = issue(false, last + 1 >= bwd.size())) return r;
         for (size_t g = 0; g < G; ++g)
             if (P.mt_group_after[g] == (int)last)
                 if (int r = mark(g)) return r;
