@@ -109,8 +109,9 @@ constexpr int kBigLds = PipeLds<256, 256, 32, 2, 4>::floats > PipeLds<256, 128, 
 // Captured Adam steps run the optimiser's update beside these launches; the
 // pair's waves take a raised issue priority (s_setprio 1) so that a CU's
 // arbiter serves their MFMAs ahead of the update's waves: c5 fp32 step
-// 9.649-9.690 -> 9.638-9.684 ms (two passes, A/B on one box; priority 3 the
-// same as 1).
+// 9.649-9.690 -> 9.638-9.684 ms with 256-workgroup updates (two passes, A/B
+// on one box); with the 512-workgroup updates the planner now issues,
+// priority 0, 1 and 3 measure within noise (9.562-9.572 ms).
 #ifndef FG_PAIR_PRIO  // a knob for measurement builds
 #define FG_PAIR_PRIO 1
 #endif
