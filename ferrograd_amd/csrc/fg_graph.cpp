@@ -313,7 +313,8 @@ struct fg_plan {
     std::vector<fg_mt *> mt_groups;
     std::vector<int> mt_group_after;
     hipStream_t side = nullptr;        // that second stream (default priority)
-    std::vector<hipEvent_t> events;    // one per group, then the join
+    std::vector<hipEvent_t> events;    // one per group, then the join, then the fork
+    bool hold_mean = false;            // capture: the loss leaves its mean to the side stream
     bool mt_dirty = true;
     float lr = 1e-3f, b1 = 0.9f, b2 = 0.999f, eps = 1e-8f;
     // The plan's own view of its context: same device and stream, with a
@@ -1343,15 +1344,24 @@ int run(fg_plan &P, const std::vector<Launch> &list, bool step = false, bool def
                 rc = fg_softmax_bwd(ctx, L.dtype, P.ptr(L.sA), P.ptr(L.sB), L.M, L.N, P.ptr(L.sC),
                                     L.accumulate);
                 break;
-            case LK_SMCE:
+            case LK_SMCE: {
                 FG_REQUIRE(P.ptr(L.sZ), FG_ERR_INVALID_ARGUMENT,
                            "dispatch_loss: no target bound (fg_plan_bind_target)");
+                // A captured Adam step leaves the mean loss, a launch of its
+                // own here, to its second stream (run_bwd_adam_overlapped).
+                const bool hold = P.hold_mean && fg::softmax_ce_dispatches(L.M, L.N, true) == 2;
+                float *mean = (float *)P.ptr(L.sBias);
                 rc = fg::softmax_ce_ex(ctx, L.dtype, P.ptr(L.sA), L.N,
                                        (const uint32_t *)P.ptr(L.sZ), L.M, L.N, 1.0f,
-                                       (float *)P.ptr(L.sB), (float *)P.ptr(L.sBias),
-                                       P.ptr(L.sC), L.N, nullptr,
-                                       step ? P.ptr(L.sProbs) : nullptr, L.N);
+                                       (float *)P.ptr(L.sB), hold ? nullptr : mean, P.ptr(L.sC),
+                                       L.N, nullptr, step ? P.ptr(L.sProbs) : nullptr, L.N);
+                if (rc == FG_OK && hold) {
+                    ctx->mean_src = (const float *)P.ptr(L.sB);
+                    ctx->mean_rows = L.M;
+                    ctx->mean_dst = mean;
+                }
                 break;
+            }
             case LK_ELT: {
                 fg::EltProgram p;
                 rc = elt_program(P, L, &p);
@@ -1542,9 +1552,15 @@ constexpr uint32_t kSideAdamBlocks = FG_SIDE_ADAM_BLOCKS;
 constexpr uint32_t kSideAdamFinalBlocks = FG_SIDE_ADAM_FINAL_BLOCKS;
 int run_bwd_adam_overlapped(fg_plan &P, const std::vector<Launch> &bwd) {
     fg_ctx *ctx = &P.wctx;
-    if (int rc = fg::adam_dev_advance(ctx, P.lr, P.b1, P.b2, P.ptr(P.adam_slot))) return rc;
     const size_t G = P.mt_groups.size();
     bool forked = false;  // the second stream has joined the capture
+    // The second stream starts from the loss: it runs the mean loss the loss
+    // launch held (ctx->mean_dst) and the step counter's advance, both off
+    // the backward's path, before the first group's update (c5 step 9.608 ->
+    // 9.600 ms, three passes on one box).  Its first node is created after
+    // the backward's first launch, which so keeps the main stream's queue.
+    FG_HIP(hipEventRecord(P.events[G + 1], ctx->stream));
+    bool side_head = true;  // that first work not issued yet
     // The main stream records group g's event once it has run the launch
     // group that releases g; the update itself is issued one launch group
     // later, after the main stream's next launch.  The dependencies are the
@@ -1560,6 +1576,19 @@ int run_bwd_adam_overlapped(fg_plan &P, const std::vector<Launch> &bwd) {
         return FG_OK;
     };
     auto issue = [&](bool last, bool beside_final = false) -> int {
+        if (side_head) {
+            side_head = false;
+            FG_HIP(hipStreamWaitEvent(P.side, P.events[G + 1], 0));
+            forked = true;
+            if (ctx->mean_dst) {
+                if (int r = fg::launch_mean_loss(P.side, ctx->mean_src, ctx->mean_rows,
+                                                 ctx->mean_dst))
+                    return r;
+                ctx->mean_dst = nullptr;
+            }
+            if (int r = fg::adam_dev_advance_on(P.side, P.lr, P.b1, P.b2, P.ptr(P.adam_slot)))
+                return r;
+        }
         for (size_t g : pending) {
             FG_HIP(hipStreamWaitEvent(P.side, P.events[g], 0));
             forked = true;
@@ -2211,6 +2240,8 @@ FG_API int fg_plan_capture_step(fg_plan *p) {
     // With SGD the head GEMM may finish the loss (its mean then runs in the
     // SGD launch).
     const int hc = head_loss_chain(*p);
+    const bool overlap = p->g.optim == FG_OPTIM_ADAM && !p->mt_groups.empty();
+    p->hold_mean = overlap;
     const std::vector<Launch> &bwd = p->ce_fused_possible ? p->bwd_fused : p->bwd_seed;
     const bool hb = head_bwd_fusable(*p, bwd, hc);
     bool ce_done = false;
@@ -2227,7 +2258,6 @@ FG_API int fg_plan_capture_step(fg_plan *p) {
     // The backward's last summing launch may share the SGD launch; with the
     // head's dX computed in the forward, the head's dW runs beside the next
     // pair.
-    const bool overlap = p->g.optim == FG_OPTIM_ADAM && !p->mt_groups.empty();
     if (rc == FG_OK && overlap) {
         rc = run_bwd_adam_overlapped(*p, bwd);
     } else {
@@ -2237,6 +2267,7 @@ FG_API int fg_plan_capture_step(fg_plan *p) {
         if (rc == FG_OK) rc = run_optim(*p, p->mt_all);
     }
     p->wctx.defer_reduce = false;
+    p->hold_mean = false;
     if (rc != FG_OK) {
         p->wctx.pending_splits = 0;
         p->wctx.mean_dst = nullptr;

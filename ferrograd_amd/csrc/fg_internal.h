@@ -142,6 +142,7 @@ int mt_adam_dev(fg_ctx *ctx, fg_mt *mt, float lr, float b1, float b2, float eps,
 // max_blocks (0: one workgroup per chunk) caps the grid; each workgroup then
 // walks several chunks.
 int adam_dev_advance(fg_ctx *ctx, float lr, float b1, float b2, void *d_state);
+int adam_dev_advance_on(hipStream_t stream, float lr, float b1, float b2, void *d_state);
 int mt_adam_dev_update(fg_mt *mt, hipStream_t stream, float b1, float b2, float eps,
                        const void *d_state, int zero_grad, uint32_t max_blocks);
 
@@ -151,6 +152,10 @@ int mt_adam_dev_update(fg_mt *mt, hipStream_t stream, float b1, float b2, float 
 int softmax_ce_ex(fg_ctx *ctx, int dtype, const void *d_logits, int ldx, const uint32_t *d_labels,
                   int R, int C, float grad_scale, float *d_row_loss, float *d_mean_loss,
                   void *d_dlogits, int ldd, uint32_t *d_argmax, void *d_probs, int ldp);
+
+// The mean loss of R per-row losses, on `stream`, by the kernel softmax_ce_ex
+// launches for it (same operations, so the same bits).
+int launch_mean_loss(hipStream_t stream, const float *d_row_loss, int R, float *d_mean_loss);
 
 // Kernel dispatches of softmax_ce_ex for R x C (with or without the mean).
 int softmax_ce_dispatches(int R, int C, bool mean);

@@ -339,12 +339,17 @@ uint64_t adam_dev_state_bytes() { return sizeof(AdamDevState); }
 
 // Advance the device step counter at d_state (zero-initialised
 // AdamDevState) and derive the step's bias-correction scalars.
-int adam_dev_advance(fg_ctx *ctx, float lr, float b1, float b2, void *d_state) {
-    FG_REQUIRE(ctx && d_state, FG_ERR_INVALID_ARGUMENT, "adam_dev_advance: NULL argument");
+int adam_dev_advance_on(hipStream_t stream, float lr, float b1, float b2, void *d_state) {
+    FG_REQUIRE(d_state, FG_ERR_INVALID_ARGUMENT, "adam_dev_advance: NULL state");
     AdamDevState *st = reinterpret_cast<AdamDevState *>(d_state);
-    adam_advance_kernel<<<1, 64, 0, ctx->stream>>>(st, (double)lr, (double)b1, (double)b2);
+    adam_advance_kernel<<<1, 64, 0, stream>>>(st, (double)lr, (double)b1, (double)b2);
     FG_LAUNCH_CHECK("adam_advance_kernel");
     return FG_OK;
+}
+
+int adam_dev_advance(fg_ctx *ctx, float lr, float b1, float b2, void *d_state) {
+    FG_REQUIRE(ctx, FG_ERR_INVALID_ARGUMENT, "adam_dev_advance: NULL context");
+    return adam_dev_advance_on(ctx->stream, lr, b1, b2, d_state);
 }
 
 // One Adam update of mt's tensors on `stream` with the scalars at d_state

@@ -634,6 +634,14 @@ int launch_rows(fg_ctx *ctx, int dt, const void *x, int ldx, const uint32_t *lab
 }  // namespace
 
 namespace fg {
+int launch_mean_loss(hipStream_t stream, const float *d_row_loss, int R, float *d_mean_loss) {
+    FG_REQUIRE(d_row_loss && d_mean_loss && R >= 0, FG_ERR_INVALID_ARGUMENT,
+               "launch_mean_loss: NULL buffer or negative row count");
+    mean_kernel<<<1, 1024, 0, stream>>>(d_row_loss, R, d_mean_loss);
+    FG_LAUNCH_CHECK("mean_kernel");
+    return FG_OK;
+}
+
 int softmax_ce_dispatches(int R, int C, bool mean) {
     const bool small = small_case(R, C);
     return (mean && !small) ? 2 : 1;
