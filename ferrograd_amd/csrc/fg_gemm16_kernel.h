@@ -692,6 +692,21 @@ struct ColSum16 {
                 s[e] += T16<BF>::to_f((uint16_t)(w[e >> 1] >> (16 * (e & 1))));
         }
     }
+    // The rows k0 .. K-1 past the whole tiles (fewer than BK), from global
+    // memory in the same thread-to-(column, k-row) assignment, after the
+    // tiles' rows.
+    __device__ __forceinline__ void add_tail(const uint16_t *B, int ldb, int k0, int K, int n0,
+                                             int N) {
+        const int c = threadIdx.x % kChunks, g = threadIdx.x / kChunks;
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const int k = k0 + g * KPT + i;
+            if (k >= K) continue;
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                s[e] += T16<BF>::to_f(B[(size_t)k * ldb + min(n0 + c * 8 + e, N - 1)]);
+        }
+    }
     // Combines the k-groups through lds (G * BN floats, free) and writes the
     // tile's columns.  Called by every thread of the workgroup.
     __device__ __forceinline__ void finish(const Args &p, float *lds, int n0) const {
@@ -746,7 +761,11 @@ __device__ __forceinline__ uint16_t (&lds16_buffer())[N] {
 // The pipelined 16-bit GEMM for output tile bx (and K slice by when split).
 // LDSN: the LDS buffer's size in elements, at least Pipe16Lds::elems (0:
 // just that) -- a launch running several bodies gives them all the largest.
-template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC, bool BF, int LDSN = 0>
+// KT: K need not be a multiple of BK (K % 8 == 0 where an operand is
+// k-contiguous): the tile loop runs the whole tiles, and the k past them go
+// into the accumulators from global memory at the end (the K tail below).
+template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC, bool BF, int LDSN = 0,
+          bool KT = false>
 __device__ __forceinline__ void gemm16_pipe_body(Args p, int bx, int by) {
     using E = T16<BF>;
     constexpr int NW = WGM * WGN;
@@ -1023,6 +1042,62 @@ __device__ __forceinline__ void gemm16_pipe_body(Args p, int bx, int by) {
             wait_vmcnt<0>();  // the reloads past the last tile, before the LDS reuse
         }
     }
+    // K tail (KT): k = kb .. K-1 past the whole tiles, in k16 steps as a tile
+    // takes them (lane half h supplies k = kb + 16 s + 8 h .. + 7 of its row /
+    // column), zeros for a lane's k past K and the steps entirely past K
+    // skipped.  A lane takes its eight k of a k-contiguous operand with one
+    // 16-byte load (K % 8 == 0 there), of a row-contiguous one with eight
+    // loads coalesced across the lanes; every address is clamped into the
+    // operand, and all loads go out before the first MFMA.  The column sums
+    // (TN) add the same k after the tiles'.
+    if constexpr (KT) {
+        const int kb = nk * BK;
+        if (kb < p.K) {
+            constexpr int NS = BK / 16;
+            int arow[TM], bcol[TN];
+#pragma unroll
+            for (int i = 0; i < TM; ++i) arow[i] = min(m0 + wm0 + 32 * i + l32, p.M - 1);
+#pragma unroll
+            for (int j = 0; j < TN; ++j) bcol[j] = min(n0 + wn0 + 32 * j + l32, p.N - 1);
+            auto eight = [&](const uint16_t *base, int ld, bool kc, int r, int k8) {
+                u32x4 v;
+                if (kc) {
+                    v = *reinterpret_cast<const u32x4 *>(base + (size_t)r * ld + min(k8, p.K - 8));
+                    if (k8 >= p.K) v = u32x4{0u, 0u, 0u, 0u};
+                } else {
+                    uint16_t e[8];
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) {
+                        const uint16_t x = base[(size_t)min(k8 + t, p.K - 1) * ld + r];
+                        e[t] = k8 + t < p.K ? x : (uint16_t)0;
+                    }
+                    v = u32x4{pack2(e[0], e[1]), pack2(e[2], e[3]), pack2(e[4], e[5]),
+                              pack2(e[6], e[7])};
+                }
+                return v;
+            };
+            u32x4 ta[NS][TM], tb[NS][TN];
+#pragma unroll
+            for (int st = 0; st < NS; ++st) {
+                if (kb + 16 * st >= p.K) continue;  // uniform
+                const int k8 = kb + 16 * st + 8 * h;
+#pragma unroll
+                for (int i = 0; i < TM; ++i) ta[st][i] = eight(p.A, p.lda, AK, arow[i], k8);
+#pragma unroll
+                for (int j = 0; j < TN; ++j) tb[st][j] = eight(p.B, p.ldb, !BNC, bcol[j], k8);
+            }
+#pragma unroll
+            for (int st = 0; st < NS; ++st) {
+                if (kb + 16 * st >= p.K) continue;
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) acc[i][j] = E::mfma(ta[st][i], tb[st][j], acc[i][j]);
+            }
+            if constexpr (kTN)
+                if (do_cs) cs.add_tail(p.B, p.ldb, kb, p.K, n0, p.N);
+        }
+    }
     __syncthreads();
     if constexpr (kTN)
         if (do_cs) cs.finish(p, reinterpret_cast<float *>(lds), n0);
@@ -1044,9 +1119,9 @@ __device__ __forceinline__ void gemm16_pipe_body(Args p, int bx, int by) {
     }
 }
 
-template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC, bool BF>
+template <int BM, int BN, int BK, int WGM, int WGN, bool AK, bool BNC, bool BF, bool KT = false>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm16_pipe(Args p) {
-    gemm16_pipe_body<BM, BN, BK, WGM, WGN, AK, BNC, BF>(p, blockIdx.x, blockIdx.y);
+    gemm16_pipe_body<BM, BN, BK, WGM, WGN, AK, BNC, BF, 0, KT>(p, blockIdx.x, blockIdx.y);
 }
 
 // A large layer's weight gradient (TN, 256x256 tiles, 8 waves, BK 64, direct
@@ -1128,13 +1203,13 @@ __global__ __launch_bounds__(256) void sum_slices16(Args p, int splits) {
     }
 }
 
-template <int BM, int BN, int WGM, int WGN, int BK, bool AK, bool BNC, bool BF>
+template <int BM, int BN, int WGM, int WGN, int BK, bool AK, bool BNC, bool BF, bool KT = false>
 void launch_pipe16(const Args &a0, hipStream_t st) {
     Args a = a0;
     a.tiles_m = (a.M + BM - 1) / BM;
     a.tiles_n = (a.N + BN - 1) / BN;
     const int splits = a.ksplit > 0 ? (a.K + a.ksplit - 1) / a.ksplit : 1;
-    gemm16_pipe<BM, BN, BK, WGM, WGN, AK, BNC, BF>
+    gemm16_pipe<BM, BN, BK, WGM, WGN, AK, BNC, BF, KT>
         <<<dim3(a.tiles_m * a.tiles_n, splits), 64 * WGM * WGN, 0, st>>>(a);
     if (splits > 1) {
         const int64_t threads = (int64_t)a.M * ((a.N + 3) / 4);
@@ -1156,9 +1231,10 @@ void launch_one(const Args &a0, hipStream_t st) {
 //   2: 128x128, 4 waves, BK 32     3:  64x64,  4 waves, BK 32
 //   4: 256x128, 4 waves, BK 32     5: 256x256, 4 waves, BK 64
 //   6: 256x256, 8 waves, BK 64     7: 256x128, 4 waves, BK 64
-//   8: 256x128, 8 waves, BK 64
+//   8: 256x128, 8 waves, BK 64      9: 8's tiles with a K tail (K % 64 != 0)
 // 64x64 is also the only element-load variant, for unaligned operands.
-constexpr int kNumCfgs = 9;
+constexpr int kNumCfgs = 10;
+constexpr int kCfgKTail16 = 9;
 
 // K depth of a configuration.
 inline int cfg_bk16(int cfg) { return cfg >= 5 ? 64 : 32; }
@@ -1178,6 +1254,7 @@ void launch_layout(const Args &a, bool vec, bool pipe, int cfg, hipStream_t st) 
             case 5: launch_pipe16<256, 256, 2, 2, 64, AK, BNC, BF>(a, st); break;
             case 6: launch_pipe16<256, 256, 2, 4, 64, AK, BNC, BF>(a, st); break;
             case 7: launch_pipe16<256, 128, 2, 2, 64, AK, BNC, BF>(a, st); break;
+            case kCfgKTail16: launch_pipe16<256, 128, 4, 2, 64, AK, BNC, BF, true>(a, st); break;
             default: launch_pipe16<256, 128, 4, 2, 64, AK, BNC, BF>(a, st); break;
         }
         return;
@@ -1190,7 +1267,8 @@ void launch_layout(const Args &a, bool vec, bool pipe, int cfg, hipStream_t st) 
         case 5: launch_one<256, 256, 2, 2, 64, AK, BNC, true, BF>(a, st); break;
         case 6: launch_one<256, 256, 2, 4, 64, AK, BNC, true, BF>(a, st); break;
         case 7: launch_one<256, 128, 2, 2, 64, AK, BNC, true, BF>(a, st); break;
-        case 8: launch_one<256, 128, 4, 2, 64, AK, BNC, true, BF>(a, st); break;
+        case 8:
+        case kCfgKTail16: launch_one<256, 128, 4, 2, 64, AK, BNC, true, BF>(a, st); break;
         default: launch_one<64, 64, 2, 2, 32, AK, BNC, true, BF>(a, st); break;
     }
 }

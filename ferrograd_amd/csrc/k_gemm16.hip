@@ -38,7 +38,8 @@ int tiles(int M, int N, int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn 
 //  * else 128x128, else 64x64.
 // The BK 64 tiles need K % 64 == 0; when only K % 32 == 0 holds, 256x256
 // with 8 waves and BK 32 or 128x128 keep the pipelined kernel.  Other K take
-// gemm16_mfma, with 256x128 / 8 waves where it gives a quarter tile per CU.
+// the 256x128 8-wave tiles where they give a quarter tile per CU: pipelined
+// with a K tail (plan16), or gemm16_mfma where the operands do not allow it.
 int pick_cfg16(int layout, int M, int N, int K, int cus) {
     if (K % 64 == 0) {
         if (tiles(M, N, 256, 256) >= cus) return 6;
@@ -99,6 +100,15 @@ Plan16 plan16(const fg_ctx *ctx, int layout, const Args &a) {
     const bool rc_ok = (layout == FG_NT || a.N % 8 == 0) && (layout != FG_TN || a.M % 8 == 0);
     q.pipe = kPipe16 && q.vec && rc_ok && a.K > 0 && a.K % fg::gemm16::cfg_bk16(q.cfg) == 0 &&
              a.M >= 8 && a.N >= 8 && q.cfg != 3;
+    // K not a multiple of 32 on the 256x128 8-wave tiles (the 1000-deep data
+    // gradient of a 1000-wide head): the pipelined kernel over the whole
+    // tiles with the K tail from global memory, where each k-contiguous
+    // operand's rows hold whole 8-element chunks of k (K % 8 == 0).
+    if (!q.pipe && q.cfg == 8 && kPipe16 && q.vec && rc_ok && a.K > 0 && a.M >= 8 && a.N >= 8 &&
+        (layout == FG_TN || a.K % 8 == 0)) {
+        q.pipe = true;
+        q.cfg = fg::gemm16::kCfgKTail16;
+    }
     // Few tiles and a long K: K slices into the context's workspace when
     // what is reserved holds them (it is never grown for this), summed by a
     // second kernel in slot order -- deterministic, within the GEMM

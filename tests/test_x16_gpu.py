@@ -142,11 +142,13 @@ def test_gemm_x16_exact_bits(gpu_ctx, dtype, layout, shape):
                                   (O.NT, 4096, 4000, 96), (O.TN, 4000, 4096, 96),
                                   (O.NN, 2050, 4000, 128), (O.NT, 4096, 4000, 192),
                                   (O.TN, 4000, 4096, 128), (O.NT, 2048, 1024, 1000),
-                                  (O.NT, 2050, 1030, 1000), (O.NT, 2048, 1024, 40)],
+                                  (O.NT, 2050, 1030, 1000), (O.NT, 2048, 1024, 40),
+                                  (O.NN, 2048, 4096, 1000), (O.TN, 4096, 4096, 1001)],
                          ids=["NN-4096x2048x64", "NT-4096x4096x64", "TN-4096x4096x48",
                               "NN-2050x4000x96", "NT-4096x4000x96", "TN-4000x4096x96",
                               "NN-2050x4000x128", "NT-4096x4000x192", "TN-4000x4096x128",
-                              "NT-2048x1024x1000", "NT-2050x1030x1000", "NT-2048x1024x40"])
+                              "NT-2048x1024x1000", "NT-2050x1030x1000", "NT-2048x1024x40",
+                              "NN-2048x4096x1000", "TN-4096x4096x1001"])
 def test_gemm_x16_exact_bits_large_tiles(gpu_ctx, dtype, case):
     """Shapes large enough for the 256-wide tile configurations the
     dispatcher picks for full-chip GEMMs (8-wave 256x256 and 256x128 at
@@ -509,7 +511,8 @@ def test_bias_grad_x16_exact(gpu_ctx, dtype, shape):
 @pytest.mark.parametrize("dtype", [F16, BF16], ids=lambda d: DT_IDS[d])
 @pytest.mark.parametrize("shape", [(4096, 4096, 64), (1024, 4096, 192), (4000, 1000, 128),
                                    (1024, 1024, 32), (512, 512, 96), (37, 29, 300),
-                                   (64, 10, 256), (0, 64, 128), (64, 64, 0)],
+                                   (64, 10, 256), (0, 64, 128), (64, 64, 0),
+                                   (1024, 4096, 1000), (1024, 4096, 999)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_gemm_dw_x16_fused_bias_grad(gpu_ctx, dtype, shape):
     """dW = A^T.dZ and dbias = column sums of dZ in one call (TN layout): on
@@ -517,8 +520,9 @@ def test_gemm_dw_x16_fused_bias_grad(gpu_ctx, dtype, shape):
     equal the oracle's bit for bit, with and without accumulation.  The
     shapes take the pipelined kernels that sum the columns in the GEMM
     (8-wave 256x256 and 256x128 tiles at BK 64 with edge tiles, 4-wave
-    128x128 at BK 32) and the fallback of GEMM + separate reduction (K off
-    the tile depth, unaligned, N = 10, no rows, K = 0)."""
+    128x128 at BK 32, 8-wave 256x128 with a K tail of 40 or 39 rows) and
+    the fallback of GEMM + separate reduction (unaligned, N = 10, no rows,
+    K = 0)."""
     M, N, K = shape  # dW is M x N; the reduction runs over K rows
     note(f"gemm_dw_x16 {DT_IDS[dtype]} M={M} N={N} K={K}")
     rng = np.random.default_rng(7 + M + 3 * N + K)
